@@ -1,0 +1,99 @@
+"""Builds the native parts in-tree (quipullm_amd/lib/):
+
+* quipu_kernels.hsaco -- the gfx950 kernels (hipcc --genco), loaded at run time with hipModuleLoad;
+* libquipu.so         -- the C ABI of include/quipu.h (HIP runtime, op table);
+* quipu_napi.node     -- the Node.js (N-API) addon over libquipu.so, for the JavaScript host.
+
+Every call recompiles (it is the "does it build" check); nothing is downloaded.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "lib")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+NODE_INC = "/usr/include/node"
+
+HSACO = os.path.join(LIB, "quipu_kernels.hsaco")
+SO = os.path.join(LIB, "libquipu.so")
+NAPI = os.path.join(LIB, "quipu_napi.node")
+
+# hipcc flags for device code: gfx950 only; packed-fp32 instructions disabled.
+HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+             "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]
+
+
+def _run(cmd, what):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError(f"build of {what} failed: {' '.join(cmd)}")
+    return r
+
+
+def _atomic(out, build):
+    """Builds into a temporary name and renames, so a half-written file is never loaded."""
+    tmp = out + ".tmp%d" % os.getpid()
+    try:
+        build(tmp)
+        os.replace(tmp, out)
+    finally:
+        if os.path.exists(tmp):
+            os.remove(tmp)
+
+
+def build_kernels():
+    src = os.path.join(CSRC, "kernels", "qp_kernels.hip")
+    _atomic(HSACO, lambda o: _run([HIPCC, "--genco", *HIP_FLAGS, "-o", o, src], "kernels"))
+    return HSACO
+
+
+def build_lib():
+    src = os.path.join(CSRC, "quipu.cpp")
+    cmd = lambda o: ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-parameter",
+                     "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", "-o", o, src, f"-L{ROCM}/lib", "-lamdhip64",
+                     f"-Wl,-rpath,{ROCM}/lib", "-Wl,-soname,libquipu.so"]
+    _atomic(SO, lambda o: _run(cmd(o), "libquipu"))
+    return SO
+
+
+def build_napi():
+    if not os.path.isdir(NODE_INC):
+        return None
+    src = os.path.join(CSRC, "napi", "quipu_napi.cpp")
+    cmd = lambda o: ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-parameter",
+                     f"-I{NODE_INC}", f"-I{os.path.join(ROOT, 'include')}", "-o", o, src, f"-L{LIB}", "-lquipu",
+                     "-Wl,-rpath,$ORIGIN"]
+    _atomic(NAPI, lambda o: _run(cmd(o), "N-API addon"))
+    return NAPI
+
+
+def build_oracle():
+    """The CPU checker (test infrastructure; not part of the product)."""
+    _run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], "oracle")
+
+
+def build_all(oracle=True):
+    os.makedirs(LIB, exist_ok=True)
+    if not shutil.which(HIPCC) and not os.path.exists(HIPCC):
+        raise RuntimeError("hipcc not found")
+    out = [build_kernels(), build_lib(), build_napi()]
+    if oracle:
+        build_oracle()
+    return [o for o in out if o]
+
+
+def built() -> bool:
+    return all(os.path.exists(p) for p in (HSACO, SO))
+
+
+if __name__ == "__main__":
+    for p in build_all():
+        print(p)

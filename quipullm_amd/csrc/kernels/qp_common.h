@@ -1,0 +1,200 @@
+// Device helpers shared by the gfx950 kernels (64-lane wavefronts).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "../qp_args.h"
+
+#define QP_DEV __device__ __forceinline__
+
+QP_DEV float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+QP_DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+template <class T>
+QP_DEV const T* cptr(uint64_t a) { return reinterpret_cast<const T*>(a); }
+template <class T>
+QP_DEV T* mptr(uint64_t a) { return reinterpret_cast<T*>(a); }
+
+// Loads through a global-address-space pointer.  Addresses that reach a kernel inside an argument block are
+// generic to the compiler, which would otherwise emit flat loads; a flat load counts against both the vector-
+// memory and the LDS wait counters, so every LDS read would also wait for all in-flight weight loads.
+#define QP_GLOBAL __attribute__((address_space(1)))
+// (The integer address is converted straight to a global pointer: a cast from a generic pointer stays flat.)
+template <class T>
+QP_DEV T gload(uint64_t addr) {
+    return *(const QP_GLOBAL T*)addr;
+}
+template <class T>
+QP_DEV void gstore(uint64_t addr, T v) {
+    *(QP_GLOBAL T*)addr = v;
+}
+
+QP_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+QP_DEV float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+// reductions over aligned groups of 32 lanes (half a wavefront)
+QP_DEV float half_sum(float v) {
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+QP_DEV float half_max(float v) {
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+// Paso in device memory: {T, pos0, a, b}
+QP_DEV uint32_t paso_T(uint64_t p) { return cptr<uint32_t>(p)[0]; }
+QP_DEV uint32_t paso_pos(uint64_t p) { return cptr<uint32_t>(p)[1]; }
+
+// ------------------------------------------------------------------ scalar dequant (bit-exact formulas)
+// These follow the reference's element formulas (kquants.js:166-175, gpu.js:601-603) with every product and
+// difference rounded separately; fp-contract is switched off inside them.
+QP_DEV void q4k_scmin_bytes(const uint8_t* s, uint32_t j, uint32_t& sc, uint32_t& mn) {
+    if (j < 4) {
+        sc = s[j] & 63u;
+        mn = s[j + 4] & 63u;
+    } else {
+        sc = (s[j + 4] & 15u) | ((uint32_t)(s[j - 4] >> 6) << 4);
+        mn = (s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
+    }
+}
+
+QP_DEV float deq_q4k(const uint8_t* blk, uint32_t e) {
+#pragma clang fp contract(off)
+    const uint32_t j = e >> 5, l = e & 31;
+    uint32_t sc, mn;
+    q4k_scmin_bytes(blk + 4, j, sc, mn);
+    const float d = h2f(blk[0] | (blk[1] << 8)), dmin = h2f(blk[2] | (blk[3] << 8));
+    const float fd = d * (float)sc;
+    const float fm = dmin * (float)mn;
+    const uint32_t q = (blk[16 + (j >> 1) * 32 + l] >> ((j & 1) * 4)) & 15u;
+    const float a = fd * (float)q;
+    return a - fm;
+}
+
+// Q6_K element from the planar layout: block index gb of NB blocks at base.
+QP_DEV float deq_q6k_planar(const uint8_t* base, uint64_t NB, uint64_t gb, uint32_t e) {
+#pragma clang fp contract(off)
+    const uint32_t s = e >> 4, h = e >> 7, r = e & 127, qd = r >> 5, l = r & 31;
+    const uint8_t* ql = base + gb * 128;
+    const uint8_t* qh = base + NB * 128 + gb * 64;
+    const int8_t* sc = reinterpret_cast<const int8_t*>(base + NB * 192 + gb * 16);
+    const uint8_t* dp = base + NB * 208 + gb * 2;
+    const uint32_t lo = (ql[h * 64 + (qd & 1) * 32 + l] >> ((qd >> 1) * 4)) & 15u;
+    const uint32_t hi = (qh[h * 32 + l] >> (qd * 2)) & 3u;
+    const float d = h2f(dp[0] | (dp[1] << 8));
+    const float fd = d * (float)sc[s];
+    const float q = (float)(lo | (hi << 4)) - 32.0f;
+    return fd * q;
+}
+
+QP_DEV float deq_q8_planar(const uint8_t* base, uint64_t NB, uint64_t gb, uint32_t e) {
+#pragma clang fp contract(off)
+    const int8_t q = reinterpret_cast<const int8_t*>(base)[gb * 32 + e];
+    const uint8_t* dp = base + NB * 32 + gb * 2;
+    return (float)q * h2f(dp[0] | (dp[1] << 8));
+}
+
+// Element k of row `row` of a K-wide matrix in device layout fmt (NB = total blocks of the tensor).
+QP_DEV float deq_elem(uint32_t fmt, const uint8_t* base, uint64_t NB, uint64_t row, uint32_t K, uint32_t k) {
+    if (fmt == QP_Q4_K) return deq_q4k(base + (row * (K >> 8) + (k >> 8)) * 144, k & 255);
+    if (fmt == QP_Q6_K) return deq_q6k_planar(base, NB, row * (K >> 8) + (k >> 8), k & 255);
+    if (fmt == QP_Q8_0) return deq_q8_planar(base, NB, row * (K >> 5) + (k >> 5), k & 31);
+    return reinterpret_cast<const float*>(base)[row * K + k];
+}
+
+QP_DEV uint64_t total_blocks(uint32_t fmt, uint64_t nrows, uint32_t K) {
+    if (fmt == QP_Q4_K || fmt == QP_Q6_K) return nrows * (K >> 8);
+    if (fmt == QP_Q8_0) return nrows * (K >> 5);
+    return nrows * K;
+}
+
+// ------------------------------------------------------------------ sin/cos (reference gpu.js:13-25)
+// Cody-Waite reduction by pi/2 in three parts and the Cephes single-precision minimax polynomials.
+QP_DEV void sincos2(float x, float& sn_out, float& cs_out) {
+#pragma clang fp contract(off)
+    const float kx = x * 0.6366197723675814f;
+    const int k = (int)__builtin_rintf(kx);
+    const float kf = (float)k;
+    const float r = ((x - kf * 1.5703125f) - kf * 4.837512969970703125e-4f) - kf * 7.549789948768648e-8f;
+    const float r2 = r * r;
+    const float sn = r + (r * r2) * (-1.6666654611e-1f + r2 * (8.3321608736e-3f + r2 * -1.9515295891e-4f));
+    const float cs = (1.0f - 0.5f * r2) +
+                     (r2 * r2) * (4.166664568298827e-2f + r2 * (-1.388731625493765e-3f + r2 * 2.443315711809948e-5f));
+    const uint32_t q = (uint32_t)k & 3u;
+    if (q == 0) { sn_out = sn; cs_out = cs; }
+    else if (q == 1) { sn_out = cs; cs_out = -sn; }
+    else if (q == 2) { sn_out = -sn; cs_out = -cs; }
+    else { sn_out = -cs; cs_out = sn; }
+}
+
+// RoPE of element i of a head vector v (shared memory), reference norm_rope (gpu.js:424-441).
+QP_DEV float rope_elem(const float* v, uint32_t i, uint32_t nrot, bool neox, float pos_esc, float base) {
+    float r = v[i];
+    if (i < nrot) {
+        const uint32_t mitad = nrot / 2;
+        uint32_t j;
+        float a, b;
+        bool primero;
+        if (neox) {
+            j = i % mitad;
+            if (i < mitad) { a = v[i]; b = v[i + mitad]; } else { a = v[i - mitad]; b = v[i]; }
+            primero = i < mitad;
+        } else {
+            j = i / 2;
+            const uint32_t i0 = i - (i % 2);
+            a = v[i0]; b = v[i0 + 1];
+            primero = (i % 2) == 0;
+        }
+        const float ex = (-2.0f * (float)j) / (float)nrot;
+        const float theta = pos_esc * powf(base, ex);
+        float sn, c;
+        sincos2(theta, sn, c);
+        r = primero ? (a * c - b * sn) : (a * sn + b * c);
+    }
+    return r;
+}
+
+// Optional per-head RMSNorm then RoPE of one head vector held in shared memory (hd <= 256), done by one
+// wavefront; `lane` in 0..63.
+QP_DEV void wave_norm_rope(float* v, const float* w, uint32_t hd, bool use_norm, float eps, float pos_esc,
+                           float base, uint32_t nrot, bool neox, int lane) {
+    float vals[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t i = lane + 64 * c;
+        vals[c] = i < hd ? v[i] : 0.0f;
+        ss += vals[c] * vals[c];
+    }
+    ss = wave_sum(ss);
+    if (use_norm) {
+        const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t i = lane + 64 * c;
+            if (i < hd) v[i] = (vals[c] * inv) * w[i];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t i = lane + 64 * c;
+        if (i < hd) vals[c] = rope_elem(v, i, nrot, neox, pos_esc, base);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t i = lane + 64 * c;
+        if (i < hd) v[i] = vals[c];
+    }
+    __builtin_amdgcn_wave_barrier();
+}

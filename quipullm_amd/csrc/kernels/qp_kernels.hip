@@ -1,0 +1,1128 @@
+// gfx950 kernels of the quipu token loop.  One translation unit, compiled to a code object that the
+// runtime loads with hipModuleLoad and launches with hipModuleLaunchKernel.  Every kernel takes one
+// argument block from qp_args.h by value.
+//
+// Semantics follow the reference's WGSL kernels (citations per kernel); the launch shapes, data layouts
+// and reduction orders are this build's own (64-lane wavefronts, 16-byte loads, LDS-staged activations).
+#include "qp_common.h"
+
+#define KERNEL extern "C" __global__
+
+// ====================================================================================== load-time ops
+// Q6_K: GGUF 210-byte blocks -> planar ql | qh | scales | d (one thread per block).
+KERNEL __launch_bounds__(256) void qp_repack_q6k(QpRepackArgs a) {
+    const uint64_t NB = a.nblocks;
+    for (uint64_t b = blockIdx.x * 256ull + threadIdx.x; b < NB; b += (uint64_t)gridDim.x * 256ull) {
+        const uint8_t* s = cptr<uint8_t>(a.src) + b * 210;
+        uint8_t* d = mptr<uint8_t>(a.dst);
+        for (int i = 0; i < 128; i++) d[b * 128 + i] = s[i];
+        for (int i = 0; i < 64; i++) d[NB * 128 + b * 64 + i] = s[128 + i];
+        for (int i = 0; i < 16; i++) d[NB * 192 + b * 16 + i] = s[192 + i];
+        d[NB * 208 + b * 2] = s[208];
+        d[NB * 208 + b * 2 + 1] = s[209];
+    }
+}
+
+// Q8_0: GGUF 34-byte blocks -> planar qs | d (reference keeps qs + f32 ds, gpu.js:1150-1162).
+KERNEL __launch_bounds__(256) void qp_repack_q8(QpRepackArgs a) {
+    const uint64_t NB = a.nblocks;
+    for (uint64_t b = blockIdx.x * 256ull + threadIdx.x; b < NB; b += (uint64_t)gridDim.x * 256ull) {
+        const uint8_t* s = cptr<uint8_t>(a.src) + b * 34;
+        uint8_t* d = mptr<uint8_t>(a.dst);
+        for (int i = 0; i < 32; i++) d[b * 32 + i] = s[2 + i];
+        d[NB * 32 + b * 2] = s[0];
+        d[NB * 32 + b * 2 + 1] = s[1];
+    }
+}
+
+KERNEL __launch_bounds__(256) void qp_fill_u32(QpFillArgs a) {
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < a.count; i += (uint64_t)gridDim.x * 256ull)
+        mptr<uint32_t>(a.dst)[i] = a.value;
+}
+
+// Whole-tensor dequant to f32 in element order (reference's scalar formula; used for checks).
+KERNEL __launch_bounds__(256) void qp_dequant(QpDequantArgs a) {
+    const uint32_t epb = a.fmt == QP_Q8_0 ? 32 : (a.fmt == QP_F32 ? 1 : 256);
+    const uint64_t NB = a.nelem / epb;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < a.nelem; i += (uint64_t)gridDim.x * 256ull) {
+        // treat the tensor as one row of nelem elements split into blocks
+        const uint64_t blk = i / epb;
+        const uint32_t e = (uint32_t)(i % epb);
+        float v;
+        if (a.fmt == QP_Q4_K) v = deq_q4k(cptr<uint8_t>(a.w) + blk * 144, e);
+        else if (a.fmt == QP_Q6_K) v = deq_q6k_planar(cptr<uint8_t>(a.w), NB, blk, e);
+        else if (a.fmt == QP_Q8_0) v = deq_q8_planar(cptr<uint8_t>(a.w), NB, blk, e);
+        else v = cptr<float>(a.w)[i];
+        mptr<float>(a.y)[i] = v;
+    }
+}
+
+// ====================================================================================== embeddings
+// Reference embed_q4k/q6k (kquants.js:481-504), embed_q8 (gpu.js:585-604), embed_f32 (gpu.js:605-618):
+// y[t][k] = deq(W[ids[t]][k]).  a.rows (the tensor's row count) sizes the planar sub-arrays.
+KERNEL __launch_bounds__(256) void qp_embed(QpEmbedArgs a) {
+    const uint32_t T = paso_T(a.paso), D = a.d;
+    const uint64_t nrows = a.rows;
+    const uint64_t NB = total_blocks(a.fmt, nrows, D);
+    const uint64_t n = (uint64_t)T * D;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull) {
+        const uint32_t t = (uint32_t)(i / D), k = (uint32_t)(i % D);
+        uint32_t id = cptr<uint32_t>(a.ids)[t];
+        if (id >= a.rows) id = a.rows - 1;  // the host validates ids; a stray one never reads outside the table
+        mptr<float>(a.y)[i] = deq_elem(a.fmt, cptr<uint8_t>(a.w), NB, id, D, k);
+    }
+}
+
+// ====================================================================================== GEMV (one token)
+// A wavefront computes R weight rows at once.  Lanes stride over "pieces" of each row; the input vector is
+// staged once per workgroup in LDS (optionally RMS-normalized on the way in), with per-group sums of x, and each
+// piece's x values are read from LDS once for all R rows.  Q4_K piece: one 32-byte quant group = 64 weights
+// (low nibbles: sub-block 2g, high nibbles: sub-block 2g+1) plus the block header.  Q6_K piece: 64 weights
+// (ql 2x16 B, qh 16 B, 4 scales).  Q8_0 piece: one 32-weight block.  F32 piece: 16 floats.
+// Semantics: reference matmul_*_1 (kquants.js:188-251, gpu.js:123-198): y = W.x with the per-sub-block
+// factoring a += d*sc*sum(q x) - dmin*m*sum(x).
+
+// Dot of the 4 bytes of w (each a small unsigned integer) with x.  The empty asm makes w opaque to the
+// optimizer, so the byte selects stay (w >> 8k) & 0xff and become single v_cvt_f32_ubyte{k} instructions
+// instead of a bit-field extract plus a convert.
+QP_DEV float nib4_dot(uint32_t w, const float4 x) {
+    asm("" : "+v"(w));
+    return (float)(w & 0xffu) * x.x + (float)((w >> 8) & 0xffu) * x.y + (float)((w >> 16) & 0xffu) * x.z +
+           (float)(w >> 24) * x.w;
+}
+// acc + dot(bytes of w, x) as one chain of fused multiply-adds (one instruction per weight after the convert).
+QP_DEV float nib4_fma(uint32_t w, const float4 x, float acc) {
+    asm("" : "+v"(w));
+    acc = fmaf((float)(w & 0xffu), x.x, acc);
+    acc = fmaf((float)((w >> 8) & 0xffu), x.y, acc);
+    acc = fmaf((float)((w >> 16) & 0xffu), x.z, acc);
+    return fmaf((float)(w >> 24), x.w, acc);
+}
+QP_DEV float sum4(const float4 x) { return (x.x + x.y) + (x.z + x.w); }
+
+QP_DEV void q4k_sm(uint32_t s03, uint32_t s47, uint32_t s811, uint32_t j, uint32_t& sc, uint32_t& mn) {
+    // 6-bit scale/min unpack of sub-block j (reference scmin, kquants.js:65-76)
+    const uint32_t jj = (j & 3) * 8;
+    const uint32_t a = (s03 >> jj) & 0xffu, b = (s47 >> jj) & 0xffu, c = (s811 >> jj) & 0xffu;
+    if (j < 4) {
+        sc = a & 63u;
+        mn = b & 63u;
+    } else {
+        sc = (c & 15u) | ((a >> 6) << 4);
+        mn = (c >> 4) | ((b >> 6) << 4);
+    }
+}
+
+struct RowRef {
+    uint64_t base;  // tensor base address (device layout)
+    uint64_t row;   // weight row index within the tensor
+};
+
+// Per-format piece registers for R rows: load() issues the global loads of piece p, compute() consumes them
+// with the piece's x values (xs, piece-major) and x-group sums (xsum[p*S + i]) from LDS.  Splitting the two
+// lets the row loop keep the next piece's loads in flight while the current piece is being multiplied.
+template <int FMT, int R>
+struct Piece;
+
+template <int R>
+struct Piece<QP_Q4_K, R> {
+    uint4 hd[R], q0[R], q1[R];
+    static constexpr uint32_t J = 16;  // float4s of x per piece: 8 for sub-block 2g, 8 for sub-block 2g+1
+    static constexpr uint32_t S = 2;   // x sums per piece: sub-block 2g, sub-block 2g+1
+    static QP_DEV uint32_t count(uint32_t K) { return K >> 6; }
+    static QP_DEV uint32_t x_src(uint32_t p, uint32_t j) {
+        const uint32_t b = p >> 2, g = p & 3;
+        return (b * 256 + g * 64 + (j >> 3) * 32) / 4 + (j & 7);
+    }
+    QP_DEV void load(const RowRef (&rr)[R], uint64_t, uint32_t K, uint32_t p) {
+        const uint32_t nb = K >> 8, b = p >> 2, g = p & 3;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint64_t blk = rr[r].base + (rr[r].row * nb + b) * 144;
+            hd[r] = gload<uint4>(blk);
+            q0[r] = gload<uint4>(blk + 16 + g * 32);
+            q1[r] = gload<uint4>(blk + 32 + g * 32);
+        }
+    }
+    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, const float* __restrict__ xsum, uint32_t p,
+                        float (&acc)[R]) const {
+        const uint32_t g = p & 3;
+        float4 xl[8], xh[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            xl[i] = xs[i * npc + p];
+            xh[i] = xs[(8 + i) * npc + p];
+        }
+        const float2 sx = *reinterpret_cast<const float2*>(xsum + 2 * p);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            uint32_t sc0, m0, sc1, m1;
+            q4k_sm(hd[r].y, hd[r].z, hd[r].w, 2 * g, sc0, m0);
+            q4k_sm(hd[r].y, hd[r].z, hd[r].w, 2 * g + 1, sc1, m1);
+            const float d = h2f(hd[r].x & 0xffffu), dm = h2f(hd[r].x >> 16);
+            const uint32_t ws[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+            float dl[2] = {0.0f, 0.0f}, dh[2] = {0.0f, 0.0f};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                dl[i & 1] = nib4_fma(ws[i] & 0x0f0f0f0fu, xl[i], dl[i & 1]);
+                dh[i & 1] = nib4_fma((ws[i] >> 4) & 0x0f0f0f0fu, xh[i], dh[i & 1]);
+            }
+            acc[r] += ((d * (float)sc0) * (dl[0] + dl[1]) - (dm * (float)m0) * sx.x) +
+                      ((d * (float)sc1) * (dh[0] + dh[1]) - (dm * (float)m1) * sx.y);
+        }
+    }
+};
+
+template <int R>
+struct Piece<QP_Q6_K, R> {
+    uint4 ql0[R], ql1[R], qh[R];
+    uint2 sc8[R];
+    uint32_t dd[R];
+    static constexpr uint32_t J = 16;  // 4 groups (qd) of 16 consecutive x values
+    static constexpr uint32_t S = 4;   // one x sum per group (for the -32 offset of the quants)
+    static QP_DEV uint32_t count(uint32_t K) { return K >> 6; }
+    static QP_DEV uint32_t x_src(uint32_t p, uint32_t j) {
+        const uint32_t b = p >> 2, h = (p >> 1) & 1, l0 = (p & 1) * 16;
+        return (b * 256 + h * 128 + (j >> 2) * 32 + l0) / 4 + (j & 3);
+    }
+    QP_DEV void load(const RowRef (&rr)[R], uint64_t NB, uint32_t K, uint32_t p) {
+        const uint32_t nb = K >> 8, b = p >> 2, h = (p >> 1) & 1, l0 = (p & 1) * 16;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint64_t gb = rr[r].row * nb + b;
+            const uint64_t base = rr[r].base;
+            ql0[r] = gload<uint4>(base + gb * 128 + h * 64 + l0);
+            ql1[r] = gload<uint4>(base + gb * 128 + h * 64 + 32 + l0);
+            qh[r] = gload<uint4>(base + NB * 128 + gb * 64 + h * 32 + l0);
+            sc8[r] = gload<uint2>(base + NB * 192 + gb * 16 + h * 8);
+            dd[r] = gload<uint16_t>(base + NB * 208 + gb * 2);
+        }
+    }
+    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, const float* __restrict__ xsum, uint32_t p,
+                        float (&acc)[R]) const {
+        const uint32_t odd = p & 1;
+        float4 xv[4][4];
+#pragma unroll
+        for (int qd = 0; qd < 4; qd++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) xv[qd][i] = xs[(qd * 4 + i) * npc + p];
+        const float4 sx4 = *reinterpret_cast<const float4*>(xsum + 4 * p);
+        const float sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float d = h2f(dd[r]);
+            float a = 0.0f;
+#pragma unroll
+            for (int qd = 0; qd < 4; qd++) {
+                const uint4 lo = (qd & 1) ? ql1[r] : ql0[r];
+                const uint32_t nsh = (qd >> 1) * 4, hsh = qd * 2;
+                const uint32_t w0 = ((lo.x >> nsh) & 0x0f0f0f0fu) | (((qh[r].x >> hsh) & 0x03030303u) << 4);
+                const uint32_t w1 = ((lo.y >> nsh) & 0x0f0f0f0fu) | (((qh[r].y >> hsh) & 0x03030303u) << 4);
+                const uint32_t w2 = ((lo.z >> nsh) & 0x0f0f0f0fu) | (((qh[r].z >> hsh) & 0x03030303u) << 4);
+                const uint32_t w3 = ((lo.w >> nsh) & 0x0f0f0f0fu) | (((qh[r].w >> hsh) & 0x03030303u) << 4);
+                const float sq = nib4_fma(w1, xv[qd][1], nib4_fma(w0, xv[qd][0], 0.0f)) +
+                                 nib4_fma(w3, xv[qd][3], nib4_fma(w2, xv[qd][2], 0.0f));
+                const uint32_t si = qd * 2 + odd;  // scale byte within the 8 loaded
+                const uint32_t sw = si < 4 ? sc8[r].x : sc8[r].y;
+                const float scf = (float)(int8_t)((sw >> ((si & 3) * 8)) & 0xffu);
+                a += (d * scf) * (sq - 32.0f * sx[qd]);
+            }
+            acc[r] += a;
+        }
+    }
+};
+
+template <int R>
+struct Piece<QP_Q8_0, R> {
+    uint4 q0[R], q1[R];
+    uint32_t dd[R];
+    static constexpr uint32_t J = 8;
+    static constexpr uint32_t S = 0;
+    static QP_DEV uint32_t count(uint32_t K) { return K >> 5; }
+    static QP_DEV uint32_t x_src(uint32_t p, uint32_t j) { return p * 8 + j; }
+    QP_DEV void load(const RowRef (&rr)[R], uint64_t NB, uint32_t K, uint32_t p) {
+        const uint32_t nb = K >> 5;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint64_t gb = rr[r].row * nb + p;
+            q0[r] = gload<uint4>(rr[r].base + gb * 32);
+            q1[r] = gload<uint4>(rr[r].base + gb * 32 + 16);
+            dd[r] = gload<uint16_t>(rr[r].base + NB * 32 + gb * 2);
+        }
+    }
+    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, const float*, uint32_t p,
+                        float (&acc)[R]) const {
+        float4 xv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) xv[i] = xs[i * npc + p];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t ws[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t w = ws[i];
+                s += (float)(int8_t)(w & 0xffu) * xv[i].x + (float)(int8_t)((w >> 8) & 0xffu) * xv[i].y +
+                     (float)(int8_t)((w >> 16) & 0xffu) * xv[i].z + (float)(int8_t)(w >> 24) * xv[i].w;
+            }
+            acc[r] += h2f(dd[r]) * s;
+        }
+    }
+};
+
+template <int R>
+struct Piece<QP_F32, R> {
+    float4 w[R][4];
+    static constexpr uint32_t J = 4;
+    static constexpr uint32_t S = 0;
+    static QP_DEV uint32_t count(uint32_t K) { return K >> 4; }
+    static QP_DEV uint32_t x_src(uint32_t p, uint32_t j) { return p * 4 + j; }
+    QP_DEV void load(const RowRef (&rr)[R], uint64_t, uint32_t K, uint32_t p) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint64_t wp = rr[r].base + (rr[r].row * (K >> 2) + p * 4) * 16;
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[r][i] = gload<float4>(wp + 16 * i);
+        }
+    }
+    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, const float*, uint32_t p,
+                        float (&acc)[R]) const {
+        float4 xv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) xv[i] = xs[i * npc + p];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                s += w[r][i].x * xv[i].x + w[r][i].y * xv[i].y + w[r][i].z * xv[i].z + w[r][i].w * xv[i].w;
+            acc[r] += s;
+        }
+    }
+};
+
+// Software-pipelined row dot products: `cur` already holds piece `lane` (when lane < count); each step issues
+// the loads of the lane's next piece before multiplying the current one.
+template <int FMT, int R>
+QP_DEV void dot_rows_pipelined(Piece<FMT, R>& cur, const RowRef (&rr)[R], uint64_t NB, uint32_t K, const float4* xs,
+                               const float* xsum, uint32_t lane, float (&acc)[R]) {
+    const uint32_t npc = Piece<FMT, R>::count(K);
+    for (uint32_t p = lane; p < npc; p += 64) {
+        Piece<FMT, R> nxt;
+        const bool more = p + 64 < npc;
+        if (more) nxt.load(rr, NB, K, p + 64);
+        cur.compute(npc, xs, xsum, p, acc);
+        if (more) cur = nxt;
+    }
+}
+
+// Stage the input vector into LDS in the piece-major layout of FMT: float4 j of piece p at xs[j*npc + p], so that
+// in each LDS read the 64 lanes (consecutive pieces) touch consecutive 16-byte words (no bank conflicts).  With a
+// norm weight, x*w is stored and the RMSNorm scale 1/sqrt(mean(x^2)+eps) is returned (applied to the dot
+// products afterwards).
+template <int FMT>
+QP_DEV float stage_x(float4* xs, float* xsum, uint64_t x4, uint64_t nw, uint32_t K, float eps, float* red) {
+    const uint32_t tid = threadIdx.x;
+    const uint64_t w4 = nw;
+    const uint32_t npc = Piece<FMT, 1>::count(K);
+    float ss = 0.0f;
+    for (uint32_t q = tid; q < (K >> 2); q += blockDim.x) {
+        const uint32_t j = q / npc, p = q - j * npc;
+        const uint32_t src = Piece<FMT, 1>::x_src(p, j);
+        float4 v = gload<float4>(x4 + 16ull * src);
+        if (nw) {
+            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+            const float4 w = gload<float4>(w4 + 16ull * src);
+            v.x *= w.x; v.y *= w.y; v.z *= w.z; v.w *= w.w;
+        }
+        xs[q] = v;
+    }
+    float inv = 1.0f;
+    if (nw) {
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+    }
+    __syncthreads();
+    constexpr uint32_t S = Piece<FMT, 1>::S;
+    if constexpr (S > 0) {
+        constexpr uint32_t per = Piece<FMT, 1>::J / S;  // float4s per summed group
+        for (uint32_t p = tid; p < npc; p += blockDim.x)
+#pragma unroll
+            for (uint32_t i = 0; i < S; i++) {
+                float t = 0.0f;
+#pragma unroll
+                for (uint32_t j = 0; j < per; j++) t += sum4(xs[(i * per + j) * npc + p]);
+                xsum[p * S + i] = t;
+            }
+        __syncthreads();
+    }
+    if (nw) {
+        float t = 0.0f;
+        for (uint32_t i = 0; i < (blockDim.x >> 6); i++) t += red[i];
+        inv = 1.0f / sqrtf(t / (float)K + eps);
+    }
+    return inv;
+}
+
+QP_DEV uint64_t amax_key(float v, uint32_t idx) {
+    if (v != v) return 0ull;  // NaN is never chosen (reference compares with '>')
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - idx);
+}
+
+// Segment of workgroup wg: the last segment whose first workgroup is <= wg (segments are in order).
+QP_DEV uint32_t seg_of(const QpGemvArgs& a, uint32_t wg) {
+    uint32_t s = 0;
+    for (uint32_t i = 1; i < a.nseg; i++) s = wg >= a.seg[i].wg0 ? i : s;
+    return s;
+}
+
+// Rows of one pass (one row group of one segment) for this wavefront.
+template <int R>
+struct Pass {
+    uint32_t si, mode, n, r0;
+    bool pair;
+    uint64_t NB;
+    RowRef rr[R];
+};
+
+template <int FMT, int R>
+QP_DEV void pass_setup(const QpGemvArgs& a, uint32_t wg, uint32_t wave, Pass<R>& P) {
+    P.si = seg_of(a, wg);
+    P.mode = a.seg[P.si].mode;
+    P.n = a.seg[P.si].n;
+    P.pair = P.mode == QP_GEMV_SWIGLU;
+    const uint32_t outs = P.pair ? R / 2 : R;  // output rows per wave
+    P.r0 = (wg - a.seg[P.si].wg0) * 4 * outs + wave * outs;
+    P.NB = total_blocks(FMT, (uint64_t)a.seg[P.si].rows_total, a.k);
+    const uint64_t w1 = a.seg[P.si].w;
+    const uint64_t w2 = a.seg[P.si].w2;
+    const uint32_t rb = a.seg[P.si].row_base;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t o = (P.pair && R > 1) ? (uint32_t)(r % (R / 2 > 0 ? R / 2 : 1)) : (uint32_t)r;
+        P.rr[r].base = (P.pair && r >= R / 2) ? w2 : w1;
+        P.rr[r].row = min(P.r0 + o, P.n - 1) + rb;
+    }
+}
+
+// All segments of one launch share the format FMT; a wavefront computes R weight rows per pass.  The grid is
+// sized to the resident capacity and each workgroup streams its passes (wg, wg + grid, ...).  The work of a
+// wavefront is one sequence of items (pass k, piece slot j < ppl); two register sets A and B alternate so that the
+// loads of item n+1 are in flight while item n is multiplied, across pass boundaries too.  Loads are issued for
+// every lane (the piece index is clamped), which keeps the wait counters exact; lanes past the row's last piece
+// skip the arithmetic.  The first item's loads are issued before the input vector is staged.
+template <int FMT, int R>
+QP_DEV void gemv_seg_body(const QpGemvArgs& a) {
+    extern __shared__ float4 xs[];
+    float* xsum = reinterpret_cast<float*>(xs + (a.k >> 2));  // after the K floats of x
+    __shared__ float red[4];
+    __shared__ uint64_t wbest[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t K = a.k;
+    const uint32_t npc = Piece<FMT, R>::count(K);
+    const uint32_t ppl = (npc + 63) >> 6;  // piece slots per pass (wave-uniform)
+    const uint32_t G = gridDim.x;
+    const uint32_t mine = blockIdx.x < a.total_wg ? (a.total_wg - 1 - blockIdx.x) / G + 1 : 0;
+    const uint32_t n_total = mine * ppl;
+    Pass<R> PL, PC;
+    Piece<FMT, R> A, B;
+    auto load_item = [&](Piece<FMT, R>& X, uint32_t n) {
+        const uint32_t k = n / ppl, j = n - k * ppl;
+        if (j == 0) pass_setup<FMT, R>(a, blockIdx.x + k * G, wave, PL);
+        X.load(PL.rr, PL.NB, K, min(lane + 64 * j, npc - 1));
+    };
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    uint64_t best = 0;
+    float inv = 1.0f;
+    auto compute_item = [&](const Piece<FMT, R>& X, uint32_t n) {
+        const uint32_t k = n / ppl, j = n - k * ppl;
+        if (j == 0) pass_setup<FMT, R>(a, blockIdx.x + k * G, wave, PC);
+        const uint32_t p = lane + 64 * j;
+        if (p < npc) X.compute(npc, xs, xsum, p, acc);
+        if (j + 1 < ppl) return;
+        // end of pass: reduce across the wavefront and write the R rows
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]) * inv;
+        float* y = mptr<float>(a.seg[PC.si].y);
+        if (PC.pair) {
+#pragma unroll
+            for (int r = 0; r < R / 2; r++) {
+                const uint32_t row = PC.r0 + r;
+                if (lane == (uint32_t)r && row < PC.n) {
+                    const float g = acc[r], u = acc[r + R / 2];
+                    y[row] = (g / (1.0f + expf(-g))) * u;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t row = PC.r0 + r;
+                if (lane == (uint32_t)r && row < PC.n) {
+                    if (PC.mode == QP_GEMV_ACC) y[row] = y[row] + acc[r];
+                    else y[row] = acc[r];
+                }
+                if (PC.mode == QP_GEMV_ARGMAX && row < PC.n) {
+                    const uint64_t key = amax_key(acc[r], row);
+                    best = key > best ? key : best;
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    };
+    if (n_total) load_item(A, 0);
+    const uint32_t xrow = a.last_row ? paso_T(a.paso) - 1 : 0;
+    inv = stage_x<FMT>(xs, xsum, a.x + 4ull * xrow * K, a.norm_w, K, a.eps, red);
+    for (uint32_t n = 0; n < n_total; n += 2) {
+        if (n + 1 < n_total) load_item(B, n + 1);
+        compute_item(A, n);
+        if (n + 1 < n_total) {
+            if (n + 2 < n_total) load_item(A, n + 2);
+            compute_item(B, n + 1);
+        }
+    }
+    if (a.amax) {
+        if (lane == 0) wbest[wave] = best;
+        __syncthreads();
+        if (tid == 0) {
+            uint64_t b = wbest[0];
+            for (int i = 1; i < 4; i++) b = wbest[i] > b ? wbest[i] : b;
+            mptr<uint64_t>(a.amax)[blockIdx.x] = b;
+        }
+    }
+}
+
+#define GEMV_KERNELS(NAME, FMT)                                                                          \
+    KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r1(QpGemvArgs a) { gemv_seg_body<FMT, 1>(a); } \
+    KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r2(QpGemvArgs a) { gemv_seg_body<FMT, 2>(a); } \
+    KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r4(QpGemvArgs a) { gemv_seg_body<FMT, 4>(a); }
+#define GEMV_KERNEL_R8(NAME, FMT) \
+    KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r8(QpGemvArgs a) { gemv_seg_body<FMT, 8>(a); }
+GEMV_KERNELS(q4k, QP_Q4_K)
+GEMV_KERNELS(q6k, QP_Q6_K)  // Q6_K holds more registers per row; R = 8 would spill
+GEMV_KERNELS(q8, QP_Q8_0)
+GEMV_KERNELS(f32, QP_F32)
+GEMV_KERNEL_R8(q4k, QP_Q4_K)
+GEMV_KERNEL_R8(q8, QP_Q8_0)
+GEMV_KERNEL_R8(f32, QP_F32)
+
+// Gathered expert GEMV (reference matmul_*_e, kquants.js:256-304 and kds.js:110-186).
+// grid.x: row groups of 4*R rows (R/2 output rows per wave in SWIGLU mode), grid.y: job.
+template <int FMT, int R>
+QP_DEV void gemv_exp_body(const QpGemvExpArgs& a) {
+    extern __shared__ float4 xs[];
+    float* xsum = reinterpret_cast<float*>(xs + (a.k >> 2));  // after the K floats of x
+    __shared__ float red[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t njobs = a.njobs_fixed ? a.njobs_fixed : paso_T(a.paso) * a.kused;
+    const uint32_t job = blockIdx.y;
+    if (job >= njobs) return;
+    const uint32_t K = a.k;
+    uint32_t ex = cptr<uint32_t>(a.sel)[job];
+    if (ex >= a.n_exp) ex = a.n_exp - 1;  // routing only produces valid experts; never read outside the tensor
+    const bool pair = a.mode == QP_GEMV_SWIGLU;
+    const uint32_t outs = pair ? R / 2 : R;
+    const uint32_t r0 = blockIdx.x * 4 * outs + wave * outs;
+    RowRef rr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t o = (pair && R > 1) ? (uint32_t)(r % (R / 2 > 0 ? R / 2 : 1)) : (uint32_t)r;
+        rr[r].base = (pair && r >= R / 2) ? a.w2 : a.w;
+        rr[r].row = (uint64_t)ex * a.n + min(r0 + o, a.n - 1);
+    }
+    const uint64_t NB = total_blocks(FMT, (uint64_t)a.n_exp * a.n, K);
+    const uint32_t npc = Piece<FMT, R>::count(K);
+    Piece<FMT, R> cur;
+    if (lane < npc) cur.load(rr, NB, K, lane);
+    stage_x<FMT>(xs, xsum, a.x + 4ull * (job / a.tfijo) * K, 0, K, 0.0f, red);
+    if (r0 >= a.n) return;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    dot_rows_pipelined<FMT, R>(cur, rr, NB, K, xs, xsum, lane, acc);
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    float* y = mptr<float>(a.y) + (uint64_t)job * a.n;
+    if (pair) {
+#pragma unroll
+        for (int r = 0; r < R / 2; r++)
+            if (lane == (uint32_t)r && r0 + r < a.n) {
+                const float g = acc[r], u = acc[r + R / 2];
+                y[r0 + r] = (g / (1.0f + expf(-g))) * u;
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (lane == (uint32_t)r && r0 + r < a.n) y[r0 + r] = acc[r];
+    }
+}
+
+#define GEMV_EXP_KERNELS(NAME, FMT)                                                                              \
+    KERNEL __launch_bounds__(256) void qp_gemv_exp_##NAME##_r2(QpGemvExpArgs a) { gemv_exp_body<FMT, 2>(a); } \
+    KERNEL __launch_bounds__(256) void qp_gemv_exp_##NAME##_r4(QpGemvExpArgs a) { gemv_exp_body<FMT, 4>(a); }
+GEMV_EXP_KERNELS(q4k, QP_Q4_K)
+GEMV_EXP_KERNELS(q6k, QP_Q6_K)
+GEMV_EXP_KERNELS(q8, QP_Q8_0)
+GEMV_EXP_KERNELS(f32, QP_F32)
+
+// ====================================================================================== multi-token GEMM
+// Prefill y[t][r] (+)= W[r].x[t] for T tokens (reference matmul_*_4 and the tiled matmul_*_t,
+// kquants.js:309-386): a 64-row x 64-token tile per workgroup, K in steps of 32; the weight tile is
+// dequantized to f32 in LDS with the reference's element formula, then each thread accumulates a 4x4
+// register tile.
+KERNEL __launch_bounds__(256) void qp_gemm_mt(QpGemmArgs a) {
+    __shared__ float wt[32][64 + 4];
+    __shared__ float xt[32][64 + 4];
+    const uint32_t T = a.tfix ? a.tfix : paso_T(a.paso);
+    const uint32_t N = a.n, K = a.k;
+    const uint32_t r0 = blockIdx.x * 64, t0 = blockIdx.y * 64;
+    if (t0 >= T) return;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t ty = tid >> 4, tx = tid & 15;  // rows ty*4.., tokens tx*4..
+    const uint8_t* W = cptr<uint8_t>(a.w);
+    const float* X = cptr<float>(a.x);
+    const uint64_t NB = total_blocks(a.fmt, N, K);
+    float c[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) c[i][j] = 0.0f;
+    // loader roles: weight row lr (0..63), 8 consecutive k at lk*8; x token lt, same k split
+    const uint32_t lr = tid >> 2, lk = (tid & 3) * 8;
+    const uint32_t wrow = min(r0 + lr, N - 1);
+    const uint32_t xtok = min(t0 + lr, T - 1);
+    for (uint32_t k0 = 0; k0 < K; k0 += 32) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t k = k0 + lk + i;
+            wt[lk + i][lr] = k < K ? deq_elem(a.fmt, W, NB, wrow, K, k) : 0.0f;
+            xt[lk + i][lr] = k < K ? X[(uint64_t)xtok * K + k] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int kk = 0; kk < 32; kk++) {
+            const float4 wv = *reinterpret_cast<const float4*>(&wt[kk][ty * 4]);
+            const float4 xv = *reinterpret_cast<const float4*>(&xt[kk][tx * 4]);
+            const float w4[4] = {wv.x, wv.y, wv.z, wv.w}, x4[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) c[i][j] += w4[i] * x4[j];
+        }
+        __syncthreads();
+    }
+    float* Y = mptr<float>(a.y);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t r = r0 + ty * 4 + i;
+        if (r >= N) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t t = t0 + tx * 4 + j;
+            if (t >= T) continue;
+            float* o = Y + (uint64_t)t * N + r;
+            *o = a.acc ? *o + c[i][j] : c[i][j];
+        }
+    }
+}
+
+// ====================================================================================== RMSNorm
+// Reference rmsnorm (gpu.js:332-356), same reduction order: 256 threads stride the row, LDS tree 128..1,
+// y = (x * inv) * w.  ultima = 1: only row T-1, written to row 0.
+KERNEL __launch_bounds__(256) void qp_rmsnorm(QpRmsArgs a) {
+    __shared__ float red[256];
+    const uint32_t T = a.rows_fixed ? a.rows_fixed : paso_T(a.paso);
+    const uint32_t li = threadIdx.x, D = a.d;
+    uint32_t fila = blockIdx.x, out = blockIdx.x;
+    if (a.ultima) { fila = T - 1; out = 0; }
+    else if (fila >= T) return;
+    const float* x = cptr<float>(a.x) + (uint64_t)fila * D;
+    float s = 0.0f;
+    for (uint32_t i = li; i < D; i += 256) { const float v = x[i]; s = s + v * v; }
+    red[li] = s;
+    __syncthreads();
+    for (uint32_t k = 128; k > 0; k >>= 1) {
+        if (li < k) red[li] = red[li] + red[li + k];
+        __syncthreads();
+    }
+    const float inv = 1.0f / sqrtf(red[0] / (float)D + a.eps);
+    const float* w = cptr<float>(a.w);
+    float* y = mptr<float>(a.y) + (uint64_t)out * D;
+    for (uint32_t i = li; i < D; i += 256) y[i] = (x[i] * inv) * w[i];
+}
+
+// ====================================================================================== norm + RoPE
+// Reference norm_rope (gpu.js:394-444): grid (heads, T), one wavefront per head vector.
+KERNEL __launch_bounds__(64) void qp_norm_rope(QpRopeArgs a) {
+    __shared__ float v[256];
+    const uint32_t h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    if (t >= paso_T(a.paso)) return;
+    float* row = mptr<float>(a.v) + ((uint64_t)t * a.nh + h) * a.hd;
+    for (uint32_t i = lane; i < a.hd; i += 64) v[i] = row[i];
+    __builtin_amdgcn_wave_barrier();
+    const float pos = (float)(paso_pos(a.paso) + t);
+    wave_norm_rope(v, a.w ? cptr<float>(a.w) : nullptr, a.hd, a.use_norm != 0, a.eps, pos * a.esc, a.base, a.nrot,
+                   a.neox != 0, (int)lane);
+    for (uint32_t i = lane; i < a.hd; i += 64) row[i] = v[i];
+}
+
+// ====================================================================================== KV write
+// Reference kv_write (gpu.js:447-466): slot = pos0 + t (mod cap); f32 cache, or f16 (round to nearest even).
+KERNEL __launch_bounds__(256) void qp_kv_write(QpKvArgs a) {
+    const uint32_t T = paso_T(a.paso), pos0 = paso_pos(a.paso);
+    const uint64_t n = (uint64_t)T * a.kvd;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull) {
+        const uint32_t t = (uint32_t)(i / a.kvd), c = (uint32_t)(i % a.kvd);
+        uint32_t slot = pos0 + t;
+        if (a.cap) slot %= a.cap;
+        if (slot >= a.rows) continue;
+        const uint64_t o = (uint64_t)slot * a.kvd + c;
+        if (a.f16) {
+            mptr<uint16_t>(a.kc)[o] = f2h(cptr<float>(a.k)[i]);
+            mptr<uint16_t>(a.vc)[o] = f2h(cptr<float>(a.v)[i]);
+        } else {
+            mptr<float>(a.kc)[o] = cptr<float>(a.k)[i];
+            mptr<float>(a.vc)[o] = cptr<float>(a.v)[i];
+        }
+    }
+}
+
+// ====================================================================================== SwiGLU
+// Reference swiglu (gpu.js:570-582): g = g / (1 + exp(-g)) * u over T*F.
+KERNEL __launch_bounds__(256) void qp_swiglu(QpSwigluArgs a) {
+    const uint64_t n = (uint64_t)paso_T(a.paso) * a.f;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull) {
+        const float g = cptr<float>(a.g)[i];
+        mptr<float>(a.g)[i] = (g / (1.0f + expf(-g))) * cptr<float>(a.u)[i];
+    }
+}
+
+// ====================================================================================== MoE routing
+// Reference moe_topk (kds.js:191-221): softmax over E router logits, k rounds of strict argmax (ties to the
+// lower index), weights = probs * scale (/ max(sum, 2^-14) when norm).  One workgroup per token.
+KERNEL __launch_bounds__(256) void qp_moe_topk(QpTopkArgs a) {
+    __shared__ float pr[1024];
+    __shared__ float rv[4];
+    __shared__ uint32_t ri[4];
+    __shared__ float tot_s;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (t >= paso_T(a.paso)) return;
+    const uint32_t E = a.e;
+    const float* lg = cptr<float>(a.lg) + (uint64_t)t * E;
+    float m = -3.0e38f;
+    for (uint32_t e = tid; e < E; e += 256) { pr[e] = lg[e]; m = fmaxf(m, pr[e]); }
+    m = wave_max(m);
+    if (lane == 0) rv[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(rv[0], rv[1]), fmaxf(rv[2], rv[3]));
+    __syncthreads();
+    float s = 0.0f;
+    for (uint32_t e = tid; e < E; e += 256) { const float v = expf(pr[e] - m); pr[e] = v; s += v; }
+    s = wave_sum(s);
+    if (lane == 0) rv[wave] = s;
+    __syncthreads();
+    s = (rv[0] + rv[1]) + (rv[2] + rv[3]);
+    for (uint32_t e = tid; e < E; e += 256) pr[e] = pr[e] / s;
+    if (tid == 0) tot_s = 0.0f;
+    __syncthreads();
+    for (uint32_t i = 0; i < a.k; i++) {
+        float bv = -1.0f;
+        uint32_t bi = 0xffffffffu;
+        for (uint32_t e = tid; e < E; e += 256)
+            if (pr[e] > bv) { bv = pr[e]; bi = e; }
+#pragma unroll
+        for (int msk = 32; msk >= 1; msk >>= 1) {
+            const float ov = __shfl_xor(bv, msk, 64);
+            const uint32_t oi = __shfl_xor(bi, msk, 64);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (lane == 0) { rv[wave] = bv; ri[wave] = bi; }
+        __syncthreads();
+        if (tid == 0) {
+            float b = rv[0];
+            uint32_t bix = ri[0];
+            for (int w = 1; w < 4; w++)
+                if (rv[w] > b || (rv[w] == b && ri[w] < bix)) { b = rv[w]; bix = ri[w]; }
+            if (bix == 0xffffffffu) bix = 0;
+            mptr<uint32_t>(a.sel)[t * a.k + i] = bix;
+            mptr<float>(a.wts)[t * a.k + i] = b;
+            tot_s = tot_s + b;
+            pr[bix] = -2.0f;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        float f = a.scale;
+        if (a.norm) f = f / fmaxf(tot_s, 6.103515625e-5f);
+        for (uint32_t i = 0; i < a.k; i++) mptr<float>(a.wts)[t * a.k + i] = mptr<float>(a.wts)[t * a.k + i] * f;
+    }
+}
+
+// Reference moe_comb (kds.js:224-240): x[t][i] += sum_s wts[t*k+s] * de[(t*k+s)*D + i].
+KERNEL __launch_bounds__(256) void qp_moe_comb(QpCombArgs a) {
+    const uint64_t n = (uint64_t)paso_T(a.paso) * a.d;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull) {
+        const uint32_t t = (uint32_t)(i / a.d), c = (uint32_t)(i % a.d);
+        float acc = 0.0f;
+        for (uint32_t s = 0; s < a.k; s++)
+            acc = acc + cptr<float>(a.wts)[t * a.k + s] * cptr<float>(a.de)[((uint64_t)t * a.k + s) * a.d + c];
+        mptr<float>(a.x)[i] = mptr<float>(a.x)[i] + acc;
+    }
+}
+
+// ====================================================================================== attention
+// Causal GQA attention over the cache for any T (reference atencion, gpu.js:467-539): a workgroup takes one
+// KV head and a block of queries for all the query heads that share it; keys and values are staged in LDS
+// in tiles of 32 and an online softmax runs per (head, query) row.  32 rows per workgroup.
+template <int HD>
+QP_DEV float kv_load(uint64_t base, uint32_t f16, uint64_t idx) {
+    return f16 ? h2f(cptr<uint16_t>(base)[idx]) : cptr<float>(base)[idx];
+}
+
+template <int HD>
+QP_DEV void attn_gen_body(const QpAttnArgs& a) {
+    constexpr int ROWS = 32, TK = 32;
+    constexpr int RPT = ROWS * HD / 256;  // P.V rows per thread
+    extern __shared__ float4 smem4[];
+    float* qs = reinterpret_cast<float*>(smem4);  // [ROWS][HD]
+    float* ks = qs + ROWS * HD;                   // [TK][HD+1]
+    float* vs = ks + TK * (HD + 1);               // [TK][HD]
+    float* ps = vs + TK * HD;                     // [ROWS][TK+1]
+    float* mr = ps + ROWS * (TK + 1);             // [ROWS]
+    float* lr = mr + ROWS;
+    float* cr = lr + ROWS;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t T = paso_T(a.paso), pos0 = paso_pos(a.paso);
+    const uint32_t G = a.nh / a.nkv, kvh = blockIdx.x;
+    const uint32_t QB = ROWS / G;
+    const uint32_t t0 = blockIdx.y * QB;
+    if (t0 >= T) return;
+    const uint32_t kvd = a.nkv * HD;
+    const uint32_t nrows = G * QB;
+    // rows: r = g*QB + qi
+    for (uint32_t i = tid; i < ROWS * HD; i += 256) {
+        const uint32_t r = i / HD, d = i % HD;
+        const uint32_t g = r / QB, qi = r % QB;
+        const uint32_t t = min(t0 + qi, T - 1);
+        qs[i] = (r < nrows) ? cptr<float>(a.q)[((uint64_t)t * a.nh + kvh * G + g) * HD + d] : 0.0f;
+    }
+    if (tid < ROWS) { mr[tid] = -3.0e38f; lr[tid] = 0.0f; }
+    const uint32_t tlast = min(t0 + QB, T) - 1;
+    const uint32_t kend = a.cap ? pos0 + tlast + 1 : min(pos0 + tlast + 1, a.rows);
+    uint32_t kbeg = 0;
+    if (a.swa) {
+        const uint32_t nk0 = pos0 + t0 + 1;
+        kbeg = nk0 > a.swa ? nk0 - a.swa : 0;
+    }
+    // score roles: key j, rows rg*4..+4
+    const uint32_t j = tid & 31, rg = tid >> 5;
+    // P.V roles: column d, rows pv*RPT..
+    const uint32_t d = tid % HD, pv = tid / HD;
+    float acc[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) acc[i] = 0.0f;
+    __syncthreads();
+    for (uint32_t kt = kbeg - (kbeg % TK); kt < kend; kt += TK) {
+        for (uint32_t i = tid; i < TK * HD; i += 256) {
+            const uint32_t jj = i / HD, dd = i % HD;
+            const uint32_t key = kt + jj;
+            float kv = 0.0f, vv = 0.0f;
+            if (key < kend) {
+                const uint32_t sl = a.cap ? key % a.cap : key;
+                const uint64_t idx = (uint64_t)sl * kvd + kvh * HD + dd;
+                kv = kv_load<HD>(a.kc, a.f16, idx);
+                vv = kv_load<HD>(a.vc, a.f16, idx);
+            }
+            ks[jj * (HD + 1) + dd] = kv;
+            vs[jj * HD + dd] = vv;
+        }
+        __syncthreads();
+        const uint32_t key = kt + j;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t r = rg * 4 + i;
+            const uint32_t qi = r % QB;
+            const uint32_t t = t0 + qi;
+            const uint32_t nk = pos0 + t + 1;
+            uint32_t ini = 0;
+            if (a.swa && nk > a.swa) ini = nk - a.swa;
+            const bool valid = r < nrows && t < T && key < nk && key >= ini;
+            float s = -3.0e38f;
+            if (valid) {
+                float dot = 0.0f;
+                const float* qr = qs + r * HD;
+                const float* kr = ks + j * (HD + 1);
+#pragma unroll 8
+                for (int q = 0; q < HD; q++) dot += qr[q] * kr[q];
+                s = dot * a.scale;
+            }
+            const float mold = mr[r];
+            const float mt = fmaxf(mold, half_max(s));
+            const float p = valid ? expf(s - mt) : 0.0f;
+            const float sum = half_sum(p);
+            ps[r * (TK + 1) + j] = p;
+            if (j == 0) {
+                const float corr = expf(mold - mt);
+                cr[r] = corr;
+                lr[r] = lr[r] * corr + sum;
+                mr[r] = mt;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const uint32_t r = pv * RPT + i;
+            float v = acc[i] * cr[r];
+            const float* pr = ps + r * (TK + 1);
+#pragma unroll 8
+            for (int jj = 0; jj < TK; jj++) v += pr[jj] * vs[jj * HD + d];
+            acc[i] = v;
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const uint32_t r = pv * RPT + i;
+        const uint32_t g = r / QB, qi = r % QB, t = t0 + qi;
+        if (r < nrows && t < T)
+            mptr<float>(a.o)[((uint64_t)t * a.nh + kvh * G + g) * HD + d] = acc[i] / lr[r];
+    }
+}
+
+KERNEL __launch_bounds__(256) void qp_attn_hd64(QpAttnArgs a) { attn_gen_body<64>(a); }
+KERNEL __launch_bounds__(256) void qp_attn_hd128(QpAttnArgs a) { attn_gen_body<128>(a); }
+
+// Split-K decode attention for one token, with the per-head q/k RMSNorm, RoPE and the KV append fused in.
+// grid (nkv, nsplit).  Each workgroup takes a contiguous key range of one KV head for all G query heads of the
+// group and writes an unnormalized partial (m, l, acc) per head; qp_dec_attn_comb merges the splits.
+template <int HD>
+QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
+    constexpr int TK = 32;
+    extern __shared__ float4 smem4[];
+    const uint32_t G = a.nh / a.nkv;
+    float* qs = reinterpret_cast<float*>(smem4);  // [G][HD]
+    float* ks = qs + G * HD;                      // [TK][HD+1]
+    float* vs = ks + TK * (HD + 1);               // [TK][HD]
+    float* ps = vs + TK * HD;                     // [G][TK]
+    float* kn = ps + G * TK;                      // [HD] new key (roped)
+    float* vn = kn + HD;                          // [HD] new value
+    float* cr = vn + HD;                          // [G]
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t kvh = blockIdx.x, sp = blockIdx.y;
+    const uint32_t pos0 = paso_pos(a.paso);
+    const bool fits = pos0 < a.rows;          // a position past the cache writes nothing and reads nothing
+    const uint32_t nk = fits ? pos0 + 1 : 0;
+    uint32_t per = (nk + a.nsplit - 1) / a.nsplit;
+    per = (per + TK - 1) / TK * TK;
+    const uint32_t k0 = sp * per, k1 = min(nk, k0 + per);
+    const uint32_t kvd = a.nkv * HD;
+    const float pos_esc = (float)pos0 * a.esc;
+    // queries of the group, normalized and rotated
+    for (uint32_t i = tid; i < G * HD; i += 256) qs[i] = cptr<float>(a.q)[(uint64_t)kvh * G * HD + i];
+    const bool has_new = k0 < k1 && k1 == nk;
+    if (has_new)
+        for (uint32_t i = tid; i < HD; i += 256) {
+            kn[i] = cptr<float>(a.k)[(uint64_t)kvh * HD + i];
+            vn[i] = cptr<float>(a.v)[(uint64_t)kvh * HD + i];
+        }
+    __syncthreads();
+    for (uint32_t g = wave; g < G + (has_new ? 1u : 0u); g += 4) {
+        if (g < G)
+            wave_norm_rope(qs + g * HD, a.qnorm ? cptr<float>(a.qnorm) : nullptr, HD, a.qnorm != 0, a.eps, pos_esc,
+                           a.base, a.nrot, a.neox != 0, (int)lane);
+        else
+            wave_norm_rope(kn, a.knorm ? cptr<float>(a.knorm) : nullptr, HD, a.knorm != 0, a.eps, pos_esc, a.base,
+                           a.nrot, a.neox != 0, (int)lane);
+    }
+    __syncthreads();
+    if (has_new) {
+        // append to the cache at slot pos0; in f16 mode the LDS copy is rounded the same way
+        const uint64_t o = (uint64_t)pos0 * kvd + kvh * HD;
+        for (uint32_t i = tid; i < HD; i += 256) {
+            if (a.f16) {
+                const uint16_t hk = f2h(kn[i]), hv = f2h(vn[i]);
+                mptr<uint16_t>(a.kc)[o + i] = hk;
+                mptr<uint16_t>(a.vc)[o + i] = hv;
+                kn[i] = h2f(hk);
+                vn[i] = h2f(hv);
+            } else {
+                mptr<float>(a.kc)[o + i] = kn[i];
+                mptr<float>(a.vc)[o + i] = vn[i];
+            }
+        }
+    }
+    // score roles: head g = tid / 32 (< G), key j = tid % 32;  P.V roles: output o = tid + 256*c
+    const uint32_t sg = tid >> 5, j = tid & 31;
+    constexpr int MAXC = 8 * HD / 256 > 0 ? 8 * HD / 256 : 1;  // up to G = 8
+    float acc[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) acc[c] = 0.0f;
+    float m = -3.0e38f, l = 0.0f;
+    __syncthreads();
+    for (uint32_t kt = k0; kt < k1; kt += TK) {
+        for (uint32_t i = tid; i < TK * HD; i += 256) {
+            const uint32_t jj = i / HD, dd = i % HD;
+            const uint32_t key = kt + jj;
+            float kv = 0.0f, vv = 0.0f;
+            if (key < k1) {
+                if (key == pos0) { kv = kn[dd]; vv = vn[dd]; }
+                else {
+                    const uint64_t idx = (uint64_t)key * kvd + kvh * HD + dd;
+                    kv = kv_load<HD>(a.kc, a.f16, idx);
+                    vv = kv_load<HD>(a.vc, a.f16, idx);
+                }
+            }
+            ks[jj * (HD + 1) + dd] = kv;
+            vs[jj * HD + dd] = vv;
+        }
+        __syncthreads();
+        if (sg < G) {
+            const uint32_t key = kt + j;
+            const bool valid = key < k1;
+            float s = -3.0e38f;
+            if (valid) {
+                float dot = 0.0f;
+                const float* qr = qs + sg * HD;
+                const float* kr = ks + j * (HD + 1);
+#pragma unroll 8
+                for (int q = 0; q < HD; q++) dot += qr[q] * kr[q];
+                s = dot * a.scale;
+            }
+            const float mt = fmaxf(m, half_max(s));
+            const float p = valid ? expf(s - mt) : 0.0f;
+            const float sum = half_sum(p);
+            const float corr = expf(m - mt);
+            l = l * corr + sum;
+            m = mt;
+            ps[sg * TK + j] = p;
+            if (j == 0) cr[sg] = corr;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < MAXC; c++) {
+            const uint32_t o = tid + 256 * c;
+            if (o < G * HD) {
+                const uint32_t g = o / HD, dd = o % HD;
+                float v = acc[c] * cr[g];
+                const float* pr = ps + g * TK;
+#pragma unroll 8
+                for (int jj = 0; jj < TK; jj++) v += pr[jj] * vs[jj * HD + dd];
+                acc[c] = v;
+            }
+        }
+        __syncthreads();
+    }
+    const uint32_t h0 = kvh * G;
+    if (sg < G && j == 0) {
+        float* ml = mptr<float>(a.part_ml) + ((uint64_t)(h0 + sg) * a.nsplit + sp) * 2;
+        ml[0] = m;
+        ml[1] = l;
+    }
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) {
+        const uint32_t o = tid + 256 * c;
+        if (o < G * HD) {
+            const uint32_t g = o / HD, dd = o % HD;
+            mptr<float>(a.part_o)[((uint64_t)(h0 + g) * a.nsplit + sp) * HD + dd] = acc[c];
+        }
+    }
+}
+
+KERNEL __launch_bounds__(256) void qp_dec_attn_hd64(QpDecAttnArgs a) { attn_dec_body<64>(a); }
+KERNEL __launch_bounds__(256) void qp_dec_attn_hd128(QpDecAttnArgs a) { attn_dec_body<128>(a); }
+
+// Merge of the split partials: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).  grid nh.
+KERNEL __launch_bounds__(256) void qp_dec_attn_comb(QpDecCombArgs a) {
+    const uint32_t h = blockIdx.x, d = threadIdx.x;
+    const float* ml = cptr<float>(a.part_ml) + (uint64_t)h * a.nsplit * 2;
+    float M = -3.0e38f;
+    for (uint32_t s = 0; s < a.nsplit; s++) M = fmaxf(M, ml[2 * s + 1] > 0.0f ? ml[2 * s] : -3.0e38f);
+    float L = 0.0f, o = 0.0f;
+    const float* po = cptr<float>(a.part_o) + (uint64_t)h * a.nsplit * a.hd;
+    for (uint32_t s = 0; s < a.nsplit; s++) {
+        const float l = ml[2 * s + 1];
+        if (l > 0.0f) {
+            const float e = expf(ml[2 * s] - M);
+            L += l * e;
+            if (d < a.hd) o += po[(uint64_t)s * a.hd + d] * e;
+        }
+    }
+    if (d < a.hd) mptr<float>(a.o)[(uint64_t)h * a.hd + d] = o / L;
+}
+
+// ====================================================================================== argmax
+// Greedy (reference sampling.js:38-42): strict '>' from -Infinity, so ties go to the lowest index and NaN is
+// never chosen.  Single workgroup.
+KERNEL __launch_bounds__(1024) void qp_argmax(QpArgmaxArgs a) {
+    __shared__ uint64_t wb[16];
+    const uint32_t tid = threadIdx.x;
+    uint64_t best = 0;
+    for (uint32_t i = tid; i < a.n; i += 1024) {
+        const uint64_t k = amax_key(cptr<float>(a.v)[i], i);
+        best = k > best ? k : best;
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = __shfl_xor(best, m, 64);
+        best = o > best ? o : best;
+    }
+    if ((tid & 63) == 0) wb[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t b = 0;
+        for (int i = 0; i < 16; i++) b = wb[i] > b ? wb[i] : b;
+        mptr<uint32_t>(a.out)[0] = b ? 0xffffffffu - (uint32_t)(b & 0xffffffffu) : 0u;
+    }
+}
+
+// Finish of the fused output GEMV's partial maxima: ids[0] = token, tokens[step] = token, step++, pos0 += T.
+KERNEL __launch_bounds__(256) void qp_argmax_fin(QpArgmaxFinArgs a) {
+    __shared__ uint64_t wb[4];
+    const uint32_t tid = threadIdx.x;
+    uint64_t best = 0;
+    for (uint32_t i = tid; i < a.count; i += 256) {
+        const uint64_t k = cptr<uint64_t>(a.amax)[i];
+        best = k > best ? k : best;
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = __shfl_xor(best, m, 64);
+        best = o > best ? o : best;
+    }
+    if ((tid & 63) == 0) wb[tid >> 6] = best;
+    __syncthreads();
+    // the partials are cleared once read, so a later launch with fewer producing workgroups sees no stale entry
+    for (uint32_t i = tid; i < a.count; i += 256) mptr<uint64_t>(a.amax)[i] = 0ull;
+    if (tid == 0) {
+        uint64_t b = wb[0];
+        for (int i = 1; i < 4; i++) b = wb[i] > b ? wb[i] : b;
+        const uint32_t tok = b ? 0xffffffffu - (uint32_t)(b & 0xffffffffu) : 0u;
+        mptr<uint32_t>(a.ids)[0] = tok;
+        uint32_t* st = mptr<uint32_t>(a.step);
+        if (a.tokens && st[0] < a.cap) mptr<uint32_t>(a.tokens)[st[0]] = tok;
+        st[0] = st[0] + 1;
+        if (a.advance) {
+            uint32_t* p = mptr<uint32_t>(a.paso);
+            p[1] = p[1] + p[0];
+        }
+    }
+}
+
+// ====================================================================================== calibration
+// Plain streaming kernels of known traffic: copy n float4s (reads and writes 16n bytes each) and a read-only
+// sum of n float4s (one float written per thread).  Used to calibrate HBM traffic counters and bandwidth.
+KERNEL __launch_bounds__(256) void qp_copy_f4(QpRepackArgs a) {
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < a.nblocks; i += (uint64_t)gridDim.x * 256ull)
+        gstore<float4>(a.dst + 16 * i, gload<float4>(a.src + 16 * i));
+}
+
+KERNEL __launch_bounds__(256) void qp_read_f4(QpRepackArgs a) {
+    float s = 0.0f;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < a.nblocks; i += (uint64_t)gridDim.x * 256ull) {
+        const float4 v = gload<float4>(a.src + 16 * i);
+        s += (v.x + v.y) + (v.z + v.w);
+    }
+    gstore<float>(a.dst + 4 * (blockIdx.x * 256ull + threadIdx.x), s);
+}

@@ -1,0 +1,127 @@
+// Kernel argument blocks, shared by the host op table (quipu.cpp) and the gfx950 kernels.
+// Every kernel takes exactly one of these structs by value.  Device addresses travel as uint64_t so the
+// header stays plain C on both sides.
+#pragma once
+#include <stdint.h>
+
+// ---------------------------------------------------------------- weight formats (ggml type ids)
+#define QP_F32 0
+#define QP_Q8_0 8
+#define QP_Q4_K 12
+#define QP_Q6_K 14
+
+// Device layouts (private to the ops that read them; produced at load time by the repack ops):
+//  F32  : [N][K] floats.
+//  Q4_K : the GGUF blocks unchanged, [N][K/256][144 B]; 144 = 9*16 so every block is 16-byte aligned.
+//  Q6_K : planar over the NB = N*K/256 blocks: ql [NB][128] | qh [NB][64] | scales [NB][16] | d [NB] f16.
+//  Q8_0 : planar over NB = N*K/32 blocks: qs [NB][32] int8 | d [NB] f16.
+// Planar sub-arrays start at multiples of 16 bytes, so every lane load is a 16-byte vector load.
+
+// Paso (per-forward step record, reference gpu.js:9): {T, pos0, a, b}, in device memory.
+// The decode graph advances pos0 on the device.
+
+// ---------------------------------------------------------------- GEMV (one token)
+#define QP_GEMV_STORE 0   // y[r] = v
+#define QP_GEMV_ACC 1     // y[r] += v   (residual add, reference acc=1)
+#define QP_GEMV_SWIGLU 2  // segment pairs gate rows with the same rows of w2 (up): y[r] = silu(g)*u
+#define QP_GEMV_ARGMAX 3  // y[r] = v, and a packed (value, index) max per row group into amax
+#define QP_MAX_SEG 4
+
+typedef struct {
+    uint64_t w;     // weights (device layout of fmt)
+    uint64_t w2;    // second matrix (QP_GEMV_SWIGLU: the up projection; same fmt and shape)
+    uint64_t y;     // output floats
+    uint32_t fmt;   // QP_F32 / QP_Q8_0 / QP_Q4_K / QP_Q6_K
+    uint32_t n;     // output rows of this segment
+    uint32_t wg0;   // first workgroup of this segment
+    uint32_t mode;  // QP_GEMV_*
+    uint32_t row_base;    // rows of this segment start at weight row row_base of the tensor
+    uint32_t rows_total;  // rows of the whole tensor (sizes the planar sub-arrays)
+    uint32_t pad[2];
+} QpGemvSeg;
+
+typedef struct {
+    QpGemvSeg seg[QP_MAX_SEG];
+    uint64_t x;       // input floats [K] (row xrow of a [T][K] activation)
+    uint64_t norm_w;  // 0, or RMSNorm weight [K]: the input is rmsnorm(x) * norm_w (fused prologue)
+    uint64_t paso;    // device Paso (for xrow = T-1 when last_row)
+    uint64_t amax;    // QP_GEMV_ARGMAX target: one uint64 (packed value/index), max-reduced
+    uint32_t nseg;
+    uint32_t k;
+    float eps;
+    uint32_t last_row;  // 1: read x row T-1 (the reference's rmsnorm "ultima" mode)
+    uint32_t rows_per_wg;  // weight rows per workgroup pass (4 waves x R)
+    uint32_t total_wg;     // workgroups covering all segments (grid-stride over them)
+    uint32_t pad[2];
+} QpGemvArgs;
+
+// Gathered expert GEMV (reference matmul_*_e, kquants.js:256-304): job z uses expert sel[z].
+typedef struct {
+    uint64_t w, x, y, sel, paso;
+    uint32_t fmt, n, k, tfijo;   // n rows per expert; input row = job / tfijo
+    uint32_t njobs_fixed;        // 0: njobs = T * kused from paso; else fixed
+    uint32_t kused;
+    uint32_t mode;               // 0 store; QP_GEMV_SWIGLU: w2 = up, y = silu(gate.x) * up.x
+    uint32_t n_exp;              // experts in the stacked tensor (rows = n_exp * n)
+    uint64_t w2;
+} QpGemvExpArgs;
+
+// Multi-token GEMV for prefill (reference matmul_*_4 / matmul_*_t semantics): y[t][r] (+)= W[r].x[t].
+typedef struct {
+    uint64_t w, x, y, paso;
+    uint32_t fmt, n, k, acc;
+    uint32_t tfix;   // 0: T from paso
+    uint32_t pad[3];
+} QpGemmArgs;
+
+// ---------------------------------------------------------------- elementwise / small ops
+typedef struct { uint64_t w, ids, y, paso; uint32_t fmt, d, rows, pad; } QpEmbedArgs;  // rows: tensor rows
+typedef struct { uint64_t x, w, y, paso; uint32_t d, ultima; float eps; uint32_t rows_fixed; } QpRmsArgs;
+typedef struct {
+    uint64_t v, w, paso;
+    uint32_t hd, nh, use_norm, neox;
+    float eps, base;
+    uint32_t nrot;
+    float esc;
+} QpRopeArgs;
+// rows: slots of the cache (writes at or past it are dropped, never out of bounds)
+typedef struct { uint64_t k, v, kc, vc, paso; uint32_t kvd, cap, f16, rows; } QpKvArgs;
+typedef struct { uint64_t g, u, paso; uint32_t f, pad; } QpSwigluArgs;
+typedef struct { uint64_t lg, sel, wts, paso; uint32_t e, k, norm; float scale; } QpTopkArgs;
+typedef struct { uint64_t x, de, wts, paso; uint32_t d, k, pad0, pad1; } QpCombArgs;
+
+// Causal GQA attention over the cache (reference atencion, gpu.js:467-539), any T.
+typedef struct {
+    uint64_t q, kc, vc, o, paso;
+    uint32_t hd, nh, nkv, swa;
+    float scale;
+    uint32_t cap, f16, qb;   // qb: queries per workgroup
+    uint32_t rows, pad[3];   // rows: slots of the cache; keys at or past it are not read
+} QpAttnArgs;
+
+// Split-K decode attention with fused q/k norm + RoPE + KV append (one token).
+typedef struct {
+    uint64_t q, k, v, kc, vc, paso;
+    uint64_t qnorm, knorm;      // 0 when absent
+    uint64_t part_o, part_ml;   // [nh][nsplit][hd], [nh][nsplit][2]
+    uint32_t hd, nh, nkv, nsplit;
+    float scale, eps, base, esc;
+    uint32_t nrot, neox, f16, rows;  // rows: slots of the cache; a position at or past it writes an empty result
+} QpDecAttnArgs;
+
+typedef struct {
+    uint64_t part_o, part_ml, o, paso;
+    uint32_t hd, nh, nsplit, pad;
+} QpDecCombArgs;
+
+// Greedy argmax finish: reads the packed max, writes ids[0] and tokens[step], clears the max, advances
+// paso.pos0 by T and the step counter.
+// cap: entries of `tokens`; steps at or past it are not recorded
+typedef struct { uint64_t amax, ids, tokens, step, paso; uint32_t count, advance, cap, pad; } QpArgmaxFinArgs;
+// Plain argmax over n floats (lowest index wins ties; NaN never chosen) -> out[0].
+typedef struct { uint64_t v, out; uint32_t n, pad; } QpArgmaxArgs;
+
+// Load-time repacks from the GGUF block layout to the device layout.
+typedef struct { uint64_t src, dst; uint64_t nblocks; } QpRepackArgs;
+typedef struct { uint64_t dst; uint64_t count; uint32_t value, pad; } QpFillArgs;
+typedef struct { uint64_t w, y; uint32_t fmt, pad; uint64_t nelem; } QpDequantArgs;

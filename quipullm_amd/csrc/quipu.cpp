@@ -1,0 +1,892 @@
+// libquipu: HIP runtime, code-object loader and the named-op table behind include/quipu.h.
+//
+// The op table maps quipullm's per-op dispatch interface (op name + uniform struct P + binding list, as
+// web/js/gpu.js's grupo()/despachar() build it) onto this backend's gfx950 kernels.  Each handler validates
+// the bindings, builds the kernel's argument block (qp_args.h) and launches it with hipModuleLaunchKernel on
+// the library's stream.  Launch shapes are chosen here, not taken from the reference's dispatch sizes.
+#include "../../include/quipu.h"
+
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "qp_args.h"
+
+namespace {
+
+thread_local std::string g_err;
+bool g_init = false;
+std::atomic<int> g_lost{0};
+int g_device = 0;
+hipStream_t g_stream = nullptr;
+hipModule_t g_mod = nullptr;
+std::mutex g_mu;
+std::unordered_map<uint64_t, uint64_t> g_allocs;  // address -> bytes
+uint64_t g_bytes = 0;
+bool g_capturing = false;
+long g_fail_alloc = -1, g_fail_launch = -1;  // QP_FAIL_ALLOC / QP_FAIL_LAUNCH: fail the Nth call (1-based)
+long g_n_alloc = 0, g_n_launch = 0;
+std::string g_summary, g_arch;
+int g_cus = 0;
+uint64_t g_hbm = 0;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    if (e == hipErrorIllegalAddress || e == hipErrorLaunchFailure || e == hipErrorECCNotCorrectable ||
+        e == hipErrorAssert)
+        g_lost = 1;
+    return fail((int)e, "HIP %s: %s (%s)", what, hipGetErrorName(e), hipGetErrorString(e));
+}
+
+#define HIPCHK(expr, what)                               \
+    do {                                                 \
+        hipError_t e_ = (expr);                          \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+#define NEED_INIT()                                                             \
+    do {                                                                        \
+        if (!g_init) return fail(QP_E_NOT_INIT, "qp_init has not succeeded"); \
+        if (g_lost) return fail(QP_E_NOT_INIT, "device lost");                 \
+    } while (0)
+
+// ------------------------------------------------------------------------------------------------ kernels
+enum Kid {
+#define K(name) K_##name,
+#include "qp_kernel_list.inc"
+#undef K
+    K_COUNT
+};
+const char* kNames[] = {
+#define K(name) "qp_" #name,
+#include "qp_kernel_list.inc"
+#undef K
+};
+hipFunction_t g_fn[K_COUNT];
+
+template <class A>
+int launch(Kid k, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block, uint32_t lds, const A& args) {
+    if (g_fail_launch > 0 && ++g_n_launch == g_fail_launch)
+        return fail(QP_E_INJECTED, "injected launch failure (QP_FAIL_LAUNCH=%ld)", g_fail_launch);
+    if (gx == 0 || gy == 0 || gz == 0) return 0;
+    void* params[] = {(void*)&args};
+    HIPCHK(hipModuleLaunchKernel(g_fn[k], gx, gy, gz, block, 1, 1, lds, g_stream, params, nullptr), kNames[k]);
+    return 0;
+}
+
+uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+uint32_t grid_cap(uint64_t n_threads) {
+    uint64_t g = (n_threads + 255) / 256;
+    if (g > 4096) g = 4096;
+    return g ? (uint32_t)g : 1u;
+}
+
+// ------------------------------------------------------------------------------------------------ op context
+struct Ctx {
+    const uint8_t* u;
+    uint32_t usize;
+    const uint64_t* b;
+    uint32_t nb;
+    uint32_t gx, gy, gz;
+    uint32_t U(int i) const {
+        if ((uint32_t)(i * 4 + 4) > usize) return 0;
+        uint32_t v;
+        memcpy(&v, u + i * 4, 4);
+        return v;
+    }
+    float F(int i) const {
+        uint32_t v = U(i);
+        float f;
+        memcpy(&f, &v, 4);
+        return f;
+    }
+    uint64_t U64(int lo) const { return (uint64_t)U(lo) | ((uint64_t)U(lo + 1) << 32); }
+    uint64_t B(uint32_t i) const { return i < nb ? b[i] : 0; }
+};
+
+int need_bufs(const Ctx& c, uint32_t n, const char* op) {
+    if (c.nb < n) return fail(QP_E_ARG, "%s: %u bindings after the uniform expected, got %u", op, n, c.nb);
+    return 0;
+}
+
+int fmt_of(const char* s) {
+    if (!strcmp(s, "q4k")) return QP_Q4_K;
+    if (!strcmp(s, "q6k")) return QP_Q6_K;
+    if (!strcmp(s, "q8")) return QP_Q8_0;
+    if (!strcmp(s, "f32")) return QP_F32;
+    return -1;
+}
+
+int check_k(int fmt, uint32_t K, const char* op) {
+    if ((fmt == QP_Q4_K || fmt == QP_Q6_K) && K % 256)
+        return fail(QP_E_ARG, "%s: K=%u is not a multiple of 256", op, K);
+    if (fmt == QP_Q8_0 && K % 32) return fail(QP_E_ARG, "%s: K=%u is not a multiple of 32", op, K);
+    if (fmt == QP_F32 && K % 16) return fail(QP_E_ARG, "%s: K=%u is not a multiple of 16", op, K);
+    if (K == 0 || K > 15360) return fail(QP_E_ARG, "%s: K=%u outside 1..15360", op, K);
+    return 0;
+}
+
+// Q8_0 bindings (qs, ds) must be the two planes of one device tensor: ds == qs + NB*32.
+int q8_planes(uint64_t qs, uint64_t ds, uint64_t nb, const char* op) {
+    if (ds != qs + nb * 32) return fail(QP_E_ARG, "%s: ds binding is not the scale plane of qs", op);
+    return 0;
+}
+
+int default_r(int fmt) {
+    static int env = -2;
+    if (env == -2) {
+        const char* e = getenv("QP_GEMV_R");
+        env = e ? atoi(e) : -1;
+    }
+    if (env == 1 || env == 2 || env == 4 || env == 8) return env;
+    return fmt == QP_Q6_K ? 2 : 4;
+}
+
+Kid gemv_kid(int fmt, int R) {
+    int f = fmt == QP_Q4_K ? 0 : fmt == QP_Q6_K ? 1 : fmt == QP_Q8_0 ? 2 : 3;
+    int r = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : 3;
+    static const Kid t[4][4] = {{K_gemv_q4k_r1, K_gemv_q4k_r2, K_gemv_q4k_r4, K_gemv_q4k_r8},
+                                {K_gemv_q6k_r1, K_gemv_q6k_r2, K_gemv_q6k_r4, K_gemv_q6k_r4},
+                                {K_gemv_q8_r1, K_gemv_q8_r2, K_gemv_q8_r4, K_gemv_q8_r8},
+                                {K_gemv_f32_r1, K_gemv_f32_r2, K_gemv_f32_r4, K_gemv_f32_r8}};
+    return t[f][r];
+}
+
+// LDS of the GEMV kernels: the K input floats plus up to K/64 * 4 group sums.
+uint32_t gemv_lds(uint32_t K) { return K * 4 + K / 4; }
+
+// Workgroups of kernel k that fit on the whole device at once (occupancy x CUs), cached per (kernel, LDS).
+uint32_t resident_wgs(Kid k, uint32_t block, uint32_t lds) {
+    static std::unordered_map<uint64_t, uint32_t> cache;
+    const uint64_t key = ((uint64_t)k << 40) | ((uint64_t)block << 24) | lds;
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, g_fn[k], (int)block, lds) != hipSuccess ||
+        per_cu <= 0)
+        per_cu = 1;
+    const uint32_t n = (uint32_t)per_cu * (uint32_t)(g_cus > 0 ? g_cus : 1);
+    cache[key] = n;
+    return n;
+}
+
+// Lays out the segments' workgroups and launches the GEMV kernel of `fmt`.  max_wg caps the grid (the
+// kernel grid-strides over the remaining row groups); 0 = one workgroup per row group.
+int run_gemv(int fmt, QpGemvArgs& a, int R, uint32_t max_wg, uint32_t* grid_out) {
+    if (int e = check_k(fmt, a.k, "gemv")) return e;
+    if (fmt == QP_Q6_K && R > 4) R = 4;  // no Q6_K kernel with R = 8 (it would spill)
+    uint32_t total = 0;
+    for (uint32_t i = 0; i < a.nseg; i++) {
+        QpGemvSeg& s = a.seg[i];
+        if (s.n == 0) return fail(QP_E_ARG, "gemv: empty segment %u", i);
+        if (s.mode == QP_GEMV_SWIGLU && R < 2) return fail(QP_E_ARG, "gemv: SwiGLU pairs need R >= 2");
+        if (s.rows_total == 0) s.rows_total = s.row_base + s.n;
+        const uint32_t outs = (s.mode == QP_GEMV_SWIGLU ? R / 2 : R) * 4;
+        s.wg0 = total;
+        total += cdiv(s.n, outs);
+    }
+    a.rows_per_wg = 4 * R;
+    a.total_wg = total;
+    const Kid kid = gemv_kid(fmt, R);
+    const uint32_t lds = gemv_lds(a.k);
+    if (!max_wg) max_wg = resident_wgs(kid, 256, lds);  // persistent: one wave of resident workgroups
+    uint32_t grid = max_wg && max_wg < total ? max_wg : total;
+    if (grid_out) *grid_out = grid;
+    return launch(kid, grid, 1, 1, 256, lds, a);
+}
+
+// ------------------------------------------------------------------------------------------------ reference ops
+// matmul_<fmt>_1 (kquants.js:188-251, gpu.js:123-198): P{N,K,acc,tfijo}; [paso, w, x, y] (q8: [paso,qs,ds,x,y]).
+int op_matmul_1(const Ctx& c, int fmt, const char* name) {
+    const bool q8 = fmt == QP_Q8_0;
+    if (int e = need_bufs(c, q8 ? 5 : 4, name)) return e;
+    const uint32_t N = c.U(0), K = c.U(1), acc = c.U(2);
+    if (int e = check_k(fmt, K, name)) return e;
+    const uint64_t w = c.B(1);
+    if (q8)
+        if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)N * K / 32, name)) return e;
+    QpGemvArgs a = {};
+    a.nseg = 1;
+    a.k = K;
+    a.paso = c.B(0);
+    a.x = c.B(q8 ? 3 : 2);
+    a.seg[0].w = w;
+    a.seg[0].y = c.B(q8 ? 4 : 3);
+    a.seg[0].fmt = fmt;
+    a.seg[0].n = N;
+    a.seg[0].mode = acc ? QP_GEMV_ACC : QP_GEMV_STORE;
+    a.seg[0].rows_total = N;
+    return run_gemv(fmt, a, default_r(fmt), 0, nullptr);
+}
+
+// matmul_<fmt>_4 / matmul_<fmt>_t (prefill, kquants.js:188-251 nt=4 and 309-386): T tokens from paso.
+int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z) {
+    const bool q8 = fmt == QP_Q8_0;
+    if (int e = need_bufs(c, q8 ? 5 : 4, name)) return e;
+    const uint32_t N = c.U(0), K = c.U(1), acc = c.U(2);
+    if (int e = check_k(fmt, K, name)) return e;
+    if (q8)
+        if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)N * K / 32, name)) return e;
+    QpGemmArgs a = {};
+    a.w = c.B(1);
+    a.x = c.B(q8 ? 3 : 2);
+    a.y = c.B(q8 ? 4 : 3);
+    a.paso = c.B(0);
+    a.fmt = fmt;
+    a.n = N;
+    a.k = K;
+    a.acc = acc;
+    const uint32_t tmax = c.gz * tokens_per_z;
+    return launch(K_gemm_mt, cdiv(N, 64), cdiv(tmax ? tmax : 1, 64), 1, 256, 0, a);
+}
+
+// matmul_<fmt>_e (kquants.js:256-304, kds.js:110-186): P{N,K,acc,tfijo,E}; [paso, w, x, y, sel]
+// (q8: [paso, qs, ds, x, y, sel]); jobs = gz.  E (the 5th word) sizes the planar formats' sub-arrays.
+int op_matmul_e(const Ctx& c, int fmt, const char* name, bool swiglu) {
+    const bool q8 = fmt == QP_Q8_0;
+    const uint32_t nb = (q8 ? 6 : 5) + (swiglu ? 1 : 0);
+    if (int e = need_bufs(c, nb, name)) return e;
+    const uint32_t N = c.U(0), K = c.U(1), tfijo = c.U(3), E = c.U(4);
+    if (int e = check_k(fmt, K, name)) return e;
+    if ((fmt == QP_Q6_K || fmt == QP_Q8_0) && E == 0) return fail(QP_E_ARG, "%s: P.E (expert count) is 0", name);
+    if (tfijo == 0) return fail(QP_E_ARG, "%s: tfijo is 0", name);
+    if (q8)
+        if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)E * N * K / 32, name)) return e;
+    QpGemvExpArgs a = {};
+    uint32_t i = 1;
+    a.w = c.B(i++);
+    if (q8) i++;
+    if (swiglu) a.w2 = c.B(i++);
+    a.x = c.B(i++);
+    a.y = c.B(i++);
+    a.sel = c.B(i++);
+    a.paso = c.B(0);
+    a.fmt = fmt;
+    a.n = N;
+    a.k = K;
+    a.tfijo = tfijo;
+    a.njobs_fixed = c.gz;
+    a.mode = swiglu ? QP_GEMV_SWIGLU : QP_GEMV_STORE;
+    a.n_exp = E;
+    const int R = 4;
+    const uint32_t outs = (swiglu ? R / 2 : R) * 4;
+    Kid k;
+    if (fmt == QP_Q4_K) k = K_gemv_exp_q4k_r4;
+    else if (fmt == QP_Q6_K) k = K_gemv_exp_q6k_r4;
+    else if (fmt == QP_Q8_0) k = K_gemv_exp_q8_r4;
+    else k = K_gemv_exp_f32_r4;
+    return launch(k, cdiv(N, outs), c.gz, 1, 256, gemv_lds(K), a);
+}
+
+// embed_<fmt> (kquants.js:481-504, gpu.js:585-618): P{D, rows}; [paso, w, ids, y] (q8: [paso,qs,ds,ids,y]).
+int op_embed(const Ctx& c, int fmt, const char* name) {
+    const bool q8 = fmt == QP_Q8_0;
+    if (int e = need_bufs(c, q8 ? 5 : 4, name)) return e;
+    QpEmbedArgs a = {};
+    a.fmt = fmt;
+    a.d = c.U(0);
+    a.rows = c.U(1);
+    if ((fmt == QP_Q6_K || fmt == QP_Q8_0) && a.rows == 0) return fail(QP_E_ARG, "%s: P.rows is 0", name);
+    if (q8)
+        if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)a.rows * a.d / 32, name)) return e;
+    a.w = c.B(1);
+    a.ids = c.B(q8 ? 3 : 2);
+    a.y = c.B(q8 ? 4 : 3);
+    a.paso = c.B(0);
+    return launch(K_embed, c.gx ? (c.gx > 4096 ? 4096 : c.gx) : 1, 1, 1, 256, 0, a);
+}
+
+// rmsnorm (gpu.js:332-356): P{D, ultima, eps, z}; [paso, x, w, y]; gx rows.
+int op_rmsnorm(const Ctx& c) {
+    if (int e = need_bufs(c, 4, "rmsnorm")) return e;
+    QpRmsArgs a = {};
+    a.d = c.U(0);
+    a.ultima = c.U(1);
+    a.eps = c.F(2);
+    a.paso = c.B(0);
+    a.x = c.B(1);
+    a.w = c.B(2);
+    a.y = c.B(3);
+    return launch(K_rmsnorm, a.ultima ? 1 : c.gx, 1, 1, 256, 0, a);
+}
+
+// norm_rope (gpu.js:394-444): P{hd, nh, usaNorm, neox, eps, base, nrot, z=esc bits}; [paso, v, w]; (nh, T).
+int op_norm_rope(const Ctx& c) {
+    if (int e = need_bufs(c, 3, "norm_rope")) return e;
+    QpRopeArgs a = {};
+    a.hd = c.U(0);
+    a.nh = c.U(1);
+    a.use_norm = c.U(2);
+    a.neox = c.U(3);
+    a.eps = c.F(4);
+    a.base = c.F(5);
+    a.nrot = c.U(6);
+    a.esc = c.U(7) ? c.F(7) : 1.0f;
+    if (a.hd > 256 || a.nrot > a.hd) return fail(QP_E_ARG, "norm_rope: hd=%u nrot=%u", a.hd, a.nrot);
+    a.paso = c.B(0);
+    a.v = c.B(1);
+    a.w = c.B(2);
+    return launch(K_norm_rope, a.nh, c.gy, 1, 64, 0, a);
+}
+
+// kv_write (gpu.js:447-466): P{kvd, cap, f16, rows}; [paso, k, v, kc, vc].  rows = cache slots (required).
+int op_kv_write(const Ctx& c) {
+    if (int e = need_bufs(c, 5, "kv_write")) return e;
+    QpKvArgs a = {};
+    a.kvd = c.U(0);
+    a.cap = c.U(1);
+    a.f16 = c.U(2);
+    a.rows = c.U(3);
+    if (!a.rows) return fail(QP_E_ARG, "kv_write: P.rows (cache slots) is 0");
+    a.paso = c.B(0);
+    a.k = c.B(1);
+    a.v = c.B(2);
+    a.kc = c.B(3);
+    a.vc = c.B(4);
+    return launch(K_kv_write, c.gx ? (c.gx > 4096 ? 4096 : c.gx) : 1, 1, 1, 256, 0, a);
+}
+
+uint32_t attn_lds(uint32_t hd) {
+    const uint32_t rows = 32, tk = 32;
+    return 4 * (rows * hd + tk * (hd + 1) + tk * hd + rows * (tk + 1) + 3 * rows);
+}
+
+// atencion (gpu.js:467-539): P{hd, nh, nkv, swa, escala, cap, z1, z2, f16, rows}; [paso, q, kc, vc, o]; (nh, T).
+// rows = cache slots (required).
+int op_atencion(const Ctx& c) {
+    if (int e = need_bufs(c, 5, "atencion")) return e;
+    QpAttnArgs a = {};
+    a.hd = c.U(0);
+    a.nh = c.U(1);
+    a.nkv = c.U(2);
+    a.swa = c.U(3);
+    a.scale = c.F(4);
+    a.cap = c.U(5);
+    if (c.U(6) || c.U(7)) return fail(QP_E_ARG, "atencion: bidirectional / non-causal modes are not supported");
+    a.f16 = c.U(8);
+    a.rows = c.U(9);
+    if (!a.rows) return fail(QP_E_ARG, "atencion: P.rows (cache slots) is 0");
+    if (a.hd != 64 && a.hd != 128) return fail(QP_E_ARG, "atencion: head_dim %u (64 or 128 supported)", a.hd);
+    if (!a.nkv || a.nh % a.nkv || a.nh / a.nkv > 32)
+        return fail(QP_E_ARG, "atencion: nh=%u nkv=%u", a.nh, a.nkv);
+    a.paso = c.B(0);
+    a.q = c.B(1);
+    a.kc = c.B(2);
+    a.vc = c.B(3);
+    a.o = c.B(4);
+    const uint32_t qb = 32 / (a.nh / a.nkv);
+    a.qb = qb;
+    return launch(a.hd == 64 ? K_attn_hd64 : K_attn_hd128, a.nkv, cdiv(c.gy ? c.gy : 1, qb), 1, 256, attn_lds(a.hd),
+                  a);
+}
+
+// swiglu (gpu.js:570-582): P{F}; [paso, g, u].
+int op_swiglu(const Ctx& c) {
+    if (int e = need_bufs(c, 3, "swiglu")) return e;
+    QpSwigluArgs a = {};
+    a.f = c.U(0);
+    a.paso = c.B(0);
+    a.g = c.B(1);
+    a.u = c.B(2);
+    return launch(K_swiglu, c.gx ? (c.gx > 4096 ? 4096 : c.gx) : 1, 1, 1, 256, 0, a);
+}
+
+// moe_topk (kds.js:191-221): P{E, k, norm, escala}; [paso, lg, sel, wts]; ceil(T/64) groups.
+int op_moe_topk(const Ctx& c) {
+    if (int e = need_bufs(c, 4, "moe_topk")) return e;
+    QpTopkArgs a = {};
+    a.e = c.U(0);
+    a.k = c.U(1);
+    a.norm = c.U(2);
+    a.scale = c.F(3);
+    if (a.e == 0 || a.e > 1024 || a.k == 0 || a.k > a.e) return fail(QP_E_ARG, "moe_topk: E=%u k=%u", a.e, a.k);
+    a.paso = c.B(0);
+    a.lg = c.B(1);
+    a.sel = c.B(2);
+    a.wts = c.B(3);
+    return launch(K_moe_topk, (c.gx ? c.gx : 1) * 64, 1, 1, 256, 0, a);
+}
+
+// moe_comb (kds.js:224-240): P{D, k}; [paso, x, de, wts].
+int op_moe_comb(const Ctx& c) {
+    if (int e = need_bufs(c, 4, "moe_comb")) return e;
+    QpCombArgs a = {};
+    a.d = c.U(0);
+    a.k = c.U(1);
+    a.paso = c.B(0);
+    a.x = c.B(1);
+    a.de = c.B(2);
+    a.wts = c.B(3);
+    return launch(K_moe_comb, c.gx ? (c.gx > 4096 ? 4096 : c.gx) : 1, 1, 1, 256, 0, a);
+}
+
+// ------------------------------------------------------------------------------------------------ backend ops
+// gemv: fused one-token GEMV over up to 4 same-format segments.
+// P{nseg, K, eps, last_row, R, max_wg, fmt, 0, then per segment {mode, n, row_base, rows_total}};
+// [paso, x, norm_w|0, amax|0, then per segment w, w2|0, y].
+int op_gemv(const Ctx& c) {
+    const uint32_t nseg = c.U(0);
+    if (nseg == 0 || nseg > QP_MAX_SEG) return fail(QP_E_ARG, "gemv: nseg=%u", nseg);
+    if (int e = need_bufs(c, 4 + 3 * nseg, "gemv")) return e;
+    QpGemvArgs a = {};
+    a.nseg = nseg;
+    a.k = c.U(1);
+    a.eps = c.F(2);
+    a.last_row = c.U(3);
+    int R = (int)c.U(4);
+    if (R == 0) R = default_r((int)c.U(6));
+    if (R != 1 && R != 2 && R != 4 && R != 8) return fail(QP_E_ARG, "gemv: R=%d", R);
+    const uint32_t max_wg = c.U(5);
+    const int fmt = (int)c.U(6);
+    a.paso = c.B(0);
+    a.x = c.B(1);
+    a.norm_w = c.B(2);
+    a.amax = c.B(3);
+    for (uint32_t i = 0; i < nseg; i++) {
+        QpGemvSeg& s = a.seg[i];
+        s.mode = c.U(8 + 4 * i);
+        s.n = c.U(9 + 4 * i);
+        s.row_base = c.U(10 + 4 * i);
+        s.rows_total = c.U(11 + 4 * i);
+        s.fmt = fmt;
+        s.w = c.B(4 + 3 * i);
+        s.w2 = c.B(5 + 3 * i);
+        s.y = c.B(6 + 3 * i);
+        if (s.mode > QP_GEMV_ARGMAX) return fail(QP_E_ARG, "gemv: mode %u", s.mode);
+        if (s.mode == QP_GEMV_SWIGLU && !s.w2) return fail(QP_E_ARG, "gemv: SwiGLU segment without w2");
+        if (s.mode == QP_GEMV_ARGMAX && !a.amax) return fail(QP_E_ARG, "gemv: argmax segment without amax");
+    }
+    return run_gemv(fmt, a, R, max_wg, nullptr);
+}
+
+// dec_attn: split-K decode attention with fused q/k norm, RoPE and KV append.
+// P{hd, nh, nkv, nsplit, scale, eps, base, esc, nrot, neox, f16, rows}; [paso, q, k, v, kc, vc, qnorm|0,
+// knorm|0, part_o, part_ml].  rows = cache slots (required).
+int op_dec_attn(const Ctx& c) {
+    if (int e = need_bufs(c, 10, "dec_attn")) return e;
+    QpDecAttnArgs a = {};
+    a.hd = c.U(0);
+    a.nh = c.U(1);
+    a.nkv = c.U(2);
+    a.nsplit = c.U(3);
+    a.scale = c.F(4);
+    a.eps = c.F(5);
+    a.base = c.F(6);
+    a.esc = c.U(7) ? c.F(7) : 1.0f;
+    a.nrot = c.U(8);
+    a.neox = c.U(9);
+    a.f16 = c.U(10);
+    a.rows = c.U(11);
+    if (!a.rows) return fail(QP_E_ARG, "dec_attn: P.rows (cache slots) is 0");
+    if (a.hd != 64 && a.hd != 128) return fail(QP_E_ARG, "dec_attn: head_dim %u", a.hd);
+    if (!a.nkv || a.nh % a.nkv || a.nh / a.nkv > 8) return fail(QP_E_ARG, "dec_attn: nh=%u nkv=%u", a.nh, a.nkv);
+    if (!a.nsplit || a.nsplit > 1024) return fail(QP_E_ARG, "dec_attn: nsplit=%u", a.nsplit);
+    a.paso = c.B(0);
+    a.q = c.B(1);
+    a.k = c.B(2);
+    a.v = c.B(3);
+    a.kc = c.B(4);
+    a.vc = c.B(5);
+    a.qnorm = c.B(6);
+    a.knorm = c.B(7);
+    a.part_o = c.B(8);
+    a.part_ml = c.B(9);
+    const uint32_t G = a.nh / a.nkv, tk = 32;
+    const uint32_t lds = 4 * (G * a.hd + tk * (a.hd + 1) + tk * a.hd + G * tk + 2 * a.hd + G);
+    return launch(a.hd == 64 ? K_dec_attn_hd64 : K_dec_attn_hd128, a.nkv, a.nsplit, 1, 256, lds, a);
+}
+
+// dec_attn_comb: P{hd, nh, nsplit}; [paso, part_o, part_ml, o].
+int op_dec_attn_comb(const Ctx& c) {
+    if (int e = need_bufs(c, 4, "dec_attn_comb")) return e;
+    QpDecCombArgs a = {};
+    a.hd = c.U(0);
+    a.nh = c.U(1);
+    a.nsplit = c.U(2);
+    a.paso = c.B(0);
+    a.part_o = c.B(1);
+    a.part_ml = c.B(2);
+    a.o = c.B(3);
+    if (a.hd > 256) return fail(QP_E_ARG, "dec_attn_comb: hd=%u", a.hd);
+    return launch(K_dec_attn_comb, a.nh, 1, 1, 256, 0, a);
+}
+
+// argmax: P{n}; [paso, v, out] (greedy, sampling.js:38-42).
+int op_argmax(const Ctx& c) {
+    if (int e = need_bufs(c, 3, "argmax")) return e;
+    QpArgmaxArgs a = {};
+    a.n = c.U(0);
+    a.v = c.B(1);
+    a.out = c.B(2);
+    return launch(K_argmax, 1, 1, 1, 1024, 0, a);
+}
+
+// argmax_fin: P{count, advance, cap}; [paso, amax, ids, tokens|0, step].  cap = entries of tokens.
+int op_argmax_fin(const Ctx& c) {
+    if (int e = need_bufs(c, 5, "argmax_fin")) return e;
+    QpArgmaxFinArgs a = {};
+    a.count = c.U(0);
+    a.advance = c.U(1);
+    a.cap = c.U(2);
+    a.paso = c.B(0);
+    a.amax = c.B(1);
+    a.ids = c.B(2);
+    a.tokens = c.B(3);
+    a.step = c.B(4);
+    return launch(K_argmax_fin, 1, 1, 1, 256, 0, a);
+}
+
+// repack_q6k / repack_q8: P{nblocks lo, hi}; [paso|0, src, dst].
+int op_repack(const Ctx& c, Kid k, const char* name) {
+    if (int e = need_bufs(c, 3, name)) return e;
+    QpRepackArgs a = {};
+    a.nblocks = c.U64(0);
+    a.src = c.B(1);
+    a.dst = c.B(2);
+    return launch(k, grid_cap(a.nblocks), 1, 1, 256, 0, a);
+}
+
+// fill_u32: P{value, count lo, hi}; [paso|0, dst].  A kernel, so it may be captured in a graph.
+int op_fill(const Ctx& c) {
+    if (int e = need_bufs(c, 2, "fill_u32")) return e;
+    QpFillArgs a = {};
+    a.value = c.U(0);
+    a.count = c.U64(1);
+    a.dst = c.B(1);
+    return launch(K_fill_u32, grid_cap(a.count), 1, 1, 256, 0, a);
+}
+
+// copy_f4 / read_f4: P{n float4s lo, hi, grid}; [paso|0, src, dst] -- plain streaming kernels of known traffic
+// (read_f4 writes one float per thread of the grid into dst).
+int op_stream(const Ctx& c, Kid k, const char* name) {
+    if (int e = need_bufs(c, 3, name)) return e;
+    QpRepackArgs a = {};
+    a.nblocks = c.U64(0);
+    a.src = c.B(1);
+    a.dst = c.B(2);
+    uint32_t grid = c.U(2) ? c.U(2) : resident_wgs(k, 256, 0);
+    return launch(k, grid, 1, 1, 256, 0, a);
+}
+
+// dequant: P{fmt, n lo, hi}; [paso|0, w, y]: whole tensor to f32.
+int op_dequant(const Ctx& c) {
+    if (int e = need_bufs(c, 3, "dequant")) return e;
+    QpDequantArgs a = {};
+    a.fmt = c.U(0);
+    a.nelem = c.U64(1);
+    a.w = c.B(1);
+    a.y = c.B(2);
+    return launch(K_dequant, grid_cap(a.nelem), 1, 1, 256, 0, a);
+}
+
+// ------------------------------------------------------------------------------------------------ registry
+typedef int (*OpFn)(const Ctx&);
+struct Op {
+    std::string name;
+    std::function<int(const Ctx&)> fn;
+};
+std::vector<Op>& ops() {
+    static std::vector<Op> v;
+    return v;
+}
+
+void register_ops() {
+    auto& v = ops();
+    if (!v.empty()) return;
+    for (const char* f : {"q4k", "q6k", "q8", "f32"}) {
+        const int fmt = fmt_of(f);
+        std::string s(f);
+        std::string n1 = "matmul_" + s + "_1", n4 = "matmul_" + s + "_4", nt = "matmul_" + s + "_t";
+        std::string ne = "matmul_" + s + "_e", nes = "matmul_" + s + "_e_swiglu", nem = "embed_" + s;
+        v.push_back({n1, [fmt, n1](const Ctx& c) { return op_matmul_1(c, fmt, n1.c_str()); }});
+        v.push_back({n4, [fmt, n4](const Ctx& c) { return op_matmul_mt(c, fmt, n4.c_str(), 4); }});
+        v.push_back({nt, [fmt, nt](const Ctx& c) { return op_matmul_mt(c, fmt, nt.c_str(), 32); }});
+        v.push_back({ne, [fmt, ne](const Ctx& c) { return op_matmul_e(c, fmt, ne.c_str(), false); }});
+        v.push_back({nes, [fmt, nes](const Ctx& c) { return op_matmul_e(c, fmt, nes.c_str(), true); }});
+        v.push_back({nem, [fmt, nem](const Ctx& c) { return op_embed(c, fmt, nem.c_str()); }});
+    }
+    v.push_back({"rmsnorm", op_rmsnorm});
+    v.push_back({"norm_rope", op_norm_rope});
+    v.push_back({"kv_write", op_kv_write});
+    v.push_back({"atencion", op_atencion});
+    v.push_back({"swiglu", op_swiglu});
+    v.push_back({"moe_topk", op_moe_topk});
+    v.push_back({"moe_comb", op_moe_comb});
+    v.push_back({"gemv", op_gemv});
+    v.push_back({"dec_attn", op_dec_attn});
+    v.push_back({"dec_attn_comb", op_dec_attn_comb});
+    v.push_back({"argmax", op_argmax});
+    v.push_back({"argmax_fin", op_argmax_fin});
+    v.push_back({"repack_q6k", [](const Ctx& c) { return op_repack(c, K_repack_q6k, "repack_q6k"); }});
+    v.push_back({"repack_q8", [](const Ctx& c) { return op_repack(c, K_repack_q8, "repack_q8"); }});
+    v.push_back({"fill_u32", op_fill});
+    v.push_back({"dequant", op_dequant});
+    v.push_back({"copy_f4", [](const Ctx& c) { return op_stream(c, K_copy_f4, "copy_f4"); }});
+    v.push_back({"read_f4", [](const Ctx& c) { return op_stream(c, K_read_f4, "read_f4"); }});
+}
+
+std::string self_dir() {
+    Dl_info info;
+    if (dladdr((void*)&self_dir, &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t s = p.rfind('/');
+        if (s != std::string::npos) return p.substr(0, s);
+    }
+    return ".";
+}
+
+}  // namespace
+
+// ================================================================================================ C ABI
+extern "C" {
+
+int qp_init(int device) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_init) {
+        if (device != g_device) return fail(QP_E_ARG, "already initialized on device %d", g_device);
+        return 0;
+    }
+    register_ops();
+    if (const char* e = getenv("QP_FAIL_ALLOC")) g_fail_alloc = atol(e);
+    if (const char* e = getenv("QP_FAIL_LAUNCH")) g_fail_launch = atol(e);
+    int n = 0;
+    HIPCHK(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    if (device < 0 || device >= n) return fail(QP_E_ARG, "device %d of %d", device, n);
+    HIPCHK(hipSetDevice(device), "hipSetDevice");
+    hipDeviceProp_t p;
+    HIPCHK(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties");
+    g_summary = p.name;
+    g_arch = p.gcnArchName;
+    g_cus = p.multiProcessorCount;
+    g_hbm = p.totalGlobalMem;
+    if (g_arch.rfind("gfx950", 0) != 0)
+        return fail(QP_E_ARG, "device %d is %s; this backend is built for gfx950 only", device, g_arch.c_str());
+    HIPCHK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreate");
+    std::string path;
+    if (const char* e = getenv("QP_KERNELS")) path = e;
+    else path = self_dir() + "/quipu_kernels.hsaco";
+    HIPCHK(hipModuleLoad(&g_mod, path.c_str()), ("hipModuleLoad " + path).c_str());
+    for (int k = 0; k < K_COUNT; k++)
+        HIPCHK(hipModuleGetFunction(&g_fn[k], g_mod, kNames[k]), kNames[k]);
+    g_device = device;
+    g_init = true;
+    return 0;
+}
+
+int qp_info(char* json, size_t cap) {
+    NEED_INIT();
+    char buf[512];
+    snprintf(buf, sizeof buf,
+             "{\"summary\":\"%s\",\"arch\":\"%s\",\"cus\":%d,\"hbm_bytes\":%llu,\"max_buffer\":%llu,"
+             "\"bytes_used\":%llu}",
+             g_summary.c_str(), g_arch.c_str(), g_cus, (unsigned long long)g_hbm, (unsigned long long)g_hbm,
+             (unsigned long long)g_bytes);
+    if (!json || cap <= strlen(buf)) return fail(QP_E_ARG, "qp_info: buffer too small");
+    strcpy(json, buf);
+    return 0;
+}
+
+int qp_last_error(char* buf, size_t cap) {
+    if (!buf || !cap) return QP_E_ARG;
+    snprintf(buf, cap, "%s", g_err.c_str());
+    return 0;
+}
+
+uint64_t qp_bytes_used(void) { return g_bytes; }
+int qp_lost(void) { return g_lost.load(); }
+
+int qp_alloc(uint64_t bytes, uint64_t* dev) {
+    NEED_INIT();
+    if (!dev) return fail(QP_E_ARG, "qp_alloc: null out");
+    if (g_capturing) return fail(QP_E_CAPTURE, "qp_alloc during graph capture");
+    if (g_fail_alloc > 0 && ++g_n_alloc == g_fail_alloc)
+        return fail(QP_E_INJECTED, "injected allocation failure (QP_FAIL_ALLOC=%ld)", g_fail_alloc);
+    uint64_t tam = bytes < 16 ? 16 : (bytes + 3) / 4 * 4;
+    if (tam > g_hbm) return fail(QP_E_ARG, "buffer of %llu bytes exceeds the device", (unsigned long long)tam);
+    void* p = nullptr;
+    HIPCHK(hipMalloc(&p, tam), "hipMalloc");
+    *dev = (uint64_t)p;
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_allocs[*dev] = tam;
+    g_bytes += tam;
+    return 0;
+}
+
+int qp_free(uint64_t dev) {
+    NEED_INIT();
+    if (!dev) return 0;
+    if (g_capturing) return fail(QP_E_CAPTURE, "qp_free during graph capture");
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_allocs.find(dev);
+        if (it == g_allocs.end()) return fail(QP_E_ARG, "qp_free: 0x%llx is not a live buffer", (unsigned long long)dev);
+        g_bytes -= it->second;
+        g_allocs.erase(it);
+    }
+    HIPCHK(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+    HIPCHK(hipFree((void*)dev), "hipFree");
+    return 0;
+}
+
+int qp_upload(uint64_t dst, uint64_t off, const void* src, uint64_t n) {
+    NEED_INIT();
+    if (g_capturing) return fail(QP_E_CAPTURE, "qp_upload during graph capture");
+    if (!n) return 0;
+    HIPCHK(hipMemcpyAsync((void*)(dst + off), src, n, hipMemcpyHostToDevice, g_stream), "upload");
+    HIPCHK(hipStreamSynchronize(g_stream), "upload sync");  // the host buffer may be reused at once
+    return 0;
+}
+
+int qp_download(void* dst, uint64_t src, uint64_t off, uint64_t n) {
+    NEED_INIT();
+    if (g_capturing) return fail(QP_E_CAPTURE, "qp_download during graph capture");
+    if (!n) return 0;
+    HIPCHK(hipMemcpyAsync(dst, (const void*)(src + off), n, hipMemcpyDeviceToHost, g_stream), "download");
+    HIPCHK(hipStreamSynchronize(g_stream), "download sync");
+    return 0;
+}
+
+int qp_copy(uint64_t dst, uint64_t doff, uint64_t src, uint64_t soff, uint64_t n) {
+    NEED_INIT();
+    if (!n) return 0;
+    HIPCHK(hipMemcpyAsync((void*)(dst + doff), (const void*)(src + soff), n, hipMemcpyDeviceToDevice, g_stream),
+           "copy");
+    return 0;
+}
+
+int qp_sync(void) {
+    NEED_INIT();
+    HIPCHK(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+    return 0;
+}
+
+int qp_op_id(const char* name) {
+    register_ops();
+    if (!name) return -1;
+    auto& v = ops();
+    for (size_t i = 0; i < v.size(); i++)
+        if (v[i].name == name) return (int)i;
+    return -1;
+}
+
+int qp_dispatch(int op, const void* uniform, uint32_t usize, const uint64_t* bufs, uint32_t nbuf, uint32_t gx,
+                uint32_t gy, uint32_t gz) {
+    NEED_INIT();
+    auto& v = ops();
+    if (op < 0 || (size_t)op >= v.size()) return fail(QP_E_ARG, "qp_dispatch: unknown op %d", op);
+    if (usize && !uniform) return fail(QP_E_ARG, "%s: null uniform", v[op].name.c_str());
+    Ctx c{(const uint8_t*)uniform, usize, bufs, nbuf, gx, gy, gz};
+    return v[op].fn(c);
+}
+
+int qp_module_load(const char* path, uint64_t* module) {
+    NEED_INIT();
+    hipModule_t m;
+    HIPCHK(hipModuleLoad(&m, path), "hipModuleLoad");
+    *module = (uint64_t)m;
+    return 0;
+}
+
+int qp_kernel(uint64_t module, const char* name, uint64_t* fn) {
+    NEED_INIT();
+    hipFunction_t f;
+    HIPCHK(hipModuleGetFunction(&f, (hipModule_t)module, name), name);
+    *fn = (uint64_t)f;
+    return 0;
+}
+
+int qp_launch(uint64_t fn, const uint32_t grid[3], const uint32_t block[3], uint32_t lds, const void* args,
+              uint64_t args_size) {
+    NEED_INIT();
+    if (g_fail_launch > 0 && ++g_n_launch == g_fail_launch)
+        return fail(QP_E_INJECTED, "injected launch failure (QP_FAIL_LAUNCH=%ld)", g_fail_launch);
+    size_t sz = (size_t)args_size;
+    void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, (void*)args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                     HIP_LAUNCH_PARAM_END};
+    HIPCHK(hipModuleLaunchKernel((hipFunction_t)fn, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds,
+                                 g_stream, nullptr, extra),
+           "qp_launch");
+    return 0;
+}
+
+int qp_graph_begin(void) {
+    NEED_INIT();
+    if (g_capturing) return fail(QP_E_CAPTURE, "capture already open");
+    HIPCHK(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    g_capturing = true;
+    return 0;
+}
+
+int qp_graph_end(uint64_t* graph) {
+    NEED_INIT();
+    if (!g_capturing) return fail(QP_E_CAPTURE, "no capture open");
+    g_capturing = false;
+    hipGraph_t g;
+    HIPCHK(hipStreamEndCapture(g_stream, &g), "hipStreamEndCapture");
+    hipGraphExec_t ex;
+    hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *graph = (uint64_t)ex;
+    return 0;
+}
+
+int qp_graph_launch(uint64_t graph) {
+    NEED_INIT();
+    HIPCHK(hipGraphLaunch((hipGraphExec_t)graph, g_stream), "hipGraphLaunch");
+    return 0;
+}
+
+int qp_graph_free(uint64_t graph) {
+    NEED_INIT();
+    HIPCHK(hipGraphExecDestroy((hipGraphExec_t)graph), "hipGraphExecDestroy");
+    return 0;
+}
+
+int qp_event_create(uint64_t* ev) {
+    NEED_INIT();
+    hipEvent_t e;
+    HIPCHK(hipEventCreate(&e), "hipEventCreate");
+    *ev = (uint64_t)e;
+    return 0;
+}
+
+int qp_event_record(uint64_t ev) {
+    NEED_INIT();
+    HIPCHK(hipEventRecord((hipEvent_t)ev, g_stream), "hipEventRecord");
+    return 0;
+}
+
+int qp_event_elapsed(uint64_t ev0, uint64_t ev1, float* ms) {
+    NEED_INIT();
+    HIPCHK(hipEventSynchronize((hipEvent_t)ev1), "hipEventSynchronize");
+    HIPCHK(hipEventElapsedTime(ms, (hipEvent_t)ev0, (hipEvent_t)ev1), "hipEventElapsedTime");
+    return 0;
+}
+
+int qp_event_free(uint64_t ev) {
+    NEED_INIT();
+    HIPCHK(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,115 @@
+'use strict';
+// Command-line driver of the engine, for tests and the benchmark.
+//
+//   node cli.js generate --model M.gguf --prompt-file ids.json --n 128 [--mode fast|ref] [--kv f16|f32]
+//                        [--ctx N] [--batch N] [--no-tiled] [--logits-out file.f32]
+//   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
+//                        [--warmup W]
+//
+// generate prints one JSON line {ids, prompt_ms, decode_ms, tps}; with --logits-out the logits each token was
+// chosen from are appended to the file as float32 (vocab floats per token).  mode "ref" runs the reference op
+// sequence with a host argmax per token; "fast" runs the captured one-token graph with the device argmax.
+// bench prefills the prompt, then times n decode steps (device events around the graph replays, and the wall
+// clock) and prints {decode_tok_s, ms_per_token, ...}.
+const fs = require('fs');
+const engine = require('./engine');
+const { argmax } = require('./sampling');
+
+function args(argv) {
+  const o = { _: [] };
+  for (let i = 0; i < argv.length; i++) {
+    const a = argv[i];
+    if (a.startsWith('--')) {
+      const k = a.slice(2);
+      if (i + 1 < argv.length && !argv[i + 1].startsWith('--')) o[k] = argv[++i]; else o[k] = true;
+    } else o._.push(a);
+  }
+  return o;
+}
+
+async function cargar(o) {
+  const options = { tiled_prefill: !o['no-tiled'], kv_f16: o.kv === 'f16' };
+  if (o.batch) options.batch = parseInt(o.batch, 10);
+  if (o['max-gen']) options.max_gen = parseInt(o['max-gen'], 10);
+  return engine.cargarModelo(o.model, { ctx: o.ctx ? parseInt(o.ctx, 10) : undefined, options: options });
+}
+
+async function generate(o) {
+  const modelo = await cargar(o);
+  const ids = JSON.parse(fs.readFileSync(o['prompt-file'], 'utf8'));
+  const n = parseInt(o.n || '16', 10);
+  const out = o['logits-out'] ? fs.openSync(o['logits-out'], 'w') : null;
+  const escribe = function (lg) { if (out !== null) fs.writeSync(out, Buffer.from(lg.buffer, lg.byteOffset, lg.byteLength)); };
+  const t0 = Date.now();
+  const logits = await engine.prefill(modelo, ids);
+  const tPrompt = Date.now();
+  const toks = [];
+  if (o.mode === 'ref') {
+    let lg = logits;
+    while (toks.length < n) {
+      escribe(lg);
+      const t = argmax(lg);
+      toks.push(t);
+      if (toks.length >= n) break;
+      lg = await modelo.forward([t], true);
+    }
+  } else {
+    escribe(logits);
+    toks.push(argmax(logits));
+    if (n > 1) {
+      const nuevos = modelo.decodificarVoraz(toks[0], n - 1, out !== null ? { porPaso: function (i, t, lg) { if (i < n - 1) escribe(lg); } } : {});
+      for (const t of nuevos) toks.push(t);
+    }
+  }
+  const tEnd = Date.now();
+  if (out !== null) fs.closeSync(out);
+  const r = { ids: toks, prompt_ms: tPrompt - t0, decode_ms: tEnd - tPrompt, pos: modelo.pos };
+  modelo.free();
+  process.stdout.write(JSON.stringify(r) + '\n');
+}
+
+async function bench(o) {
+  const tLoad = Date.now();
+  const modelo = await cargar(o);
+  const loadMs = Date.now() - tLoad;
+  const ids = JSON.parse(fs.readFileSync(o['prompt-file'], 'utf8'));
+  const n = parseInt(o.n || '256', 10);
+  const warm = parseInt(o.warmup || '8', 10);
+  const gpu = modelo.gpu;
+  const tp0 = Date.now();
+  const logits = await engine.prefill(modelo, ids);
+  gpu.sincronizar();
+  const prefillMs = Date.now() - tp0;
+  const primero = argmax(logits);
+  const pos0 = modelo.pos;
+  // warm-up steps (then rewind the position: the KV slots they wrote are overwritten by the timed run)
+  if (warm > 0) {
+    modelo.decodificarVoraz(primero, warm);
+    gpu.sincronizar();
+    modelo.pos = pos0;
+  }
+  const tiempos = {};
+  const tw0 = process.hrtime.bigint();
+  const toks = modelo.decodificarVoraz(primero, n, { tiempos: tiempos });
+  const wallMs = Number(process.hrtime.bigint() - tw0) / 1e6;
+  const r = {
+    decode_tok_s: n / (tiempos.ms / 1000), ms_per_token: tiempos.ms / n, device_ms: tiempos.ms, wall_ms: wallMs,
+    wall_tok_s: n / (wallMs / 1000), n: n, prompt_tokens: ids.length, prefill_ms: prefillMs,
+    prefill_tok_s: ids.length / (prefillMs / 1000), load_ms: loadMs, first_ids: toks.slice(0, 8),
+    ctx: modelo.ctx, nsplit: modelo.nsplit, kv_f16: modelo.kvF16, bytes_on_gpu: gpu.bytesUsados,
+  };
+  modelo.free();
+  process.stdout.write(JSON.stringify(r) + '\n');
+}
+
+const o = args(process.argv.slice(2));
+const cmd = o._[0];
+const fn = { generate: generate, bench: bench }[cmd];
+if (!fn) {
+  process.stderr.write('usage: node cli.js generate|bench --model M.gguf --prompt-file ids.json ...\n');
+  process.exit(2);
+}
+fn(o).catch(function (e) {
+  process.stderr.write('error: ' + (e && e.stack ? e.stack : e) + '\n');
+  process.exit(1);
+});

@@ -1,0 +1,114 @@
+'use strict';
+// Token loop of the engine on the gfx950 backend.
+//
+// Architecture registry: manifests in ./arch/*.json map general.architecture to a base model class, as
+// quipullm's web/arch manifests do (engine.js:14-34, server.py:64-101).  generar() is the reference's
+// generation loop (engine.js:226-322) without the HTTP job protocol: the prompt is processed in chunks of
+// modelo.batch tokens (only the last chunk asks for logits), then tokens are chosen until max_tokens.  With
+// greedy parameters the decode runs on the device (one captured graph per token, argmax on the device);
+// otherwise each step reads the logits back and the host sampler chooses.
+const fs = require('fs');
+const path = require('path');
+const { GPU } = require('./gpu');
+const { metaDe } = require('./gguf');
+const { ModeloTransformer } = require('./transformer');
+const { Muestreador, argmax } = require('./sampling');
+
+const BASES = { transformer: ModeloTransformer };
+const DIR_ARCH = path.join(__dirname, 'arch');
+
+function cargarRegistro() {
+  const reg = {};
+  for (const f of fs.readdirSync(DIR_ARCH).sort()) {
+    if (!f.endsWith('.json')) continue;
+    const man = JSON.parse(fs.readFileSync(path.join(DIR_ARCH, f), 'utf8'));
+    if (!man.id || !Array.isArray(man.arch) || !man.arch.length) throw new Error('invalid manifest ' + f);
+    if (!!man.base === !!man.module) throw new Error(f + ": define exactly one of 'base' or 'module'");
+    const Clase = man.base ? BASES[man.base] : require(path.join(DIR_ARCH, man.module));
+    if (typeof Clase !== 'function') throw new Error(f + ': unknown base ' + man.base);
+    for (const a of man.arch) reg[a] = { Clase: Clase, manifiesto: man };
+  }
+  return reg;
+}
+
+let gpuGlobal = null;
+async function gpu() {
+  if (!gpuGlobal) gpuGlobal = await GPU.crear(null);
+  return gpuGlobal;
+}
+
+// Loads a GGUF model: reads the header, picks the class from the registry, uploads the weights.
+async function cargarModelo(ruta, opciones) {
+  opciones = opciones || {};
+  const reg = cargarRegistro();
+  const cab = metaDe(ruta, {});
+  const a = cab.kv['general.architecture'];
+  if (!reg[a]) throw new Error("architecture '" + a + "' is not supported by this engine (see quipullm_amd/js/arch)");
+  const meta = metaDe(ruta, { manifiesto: reg[a].manifiesto, ctx: opciones.ctx, options: opciones.options });
+  const modelo = new reg[a].Clase(await gpu(), meta);
+  await modelo.load(ruta, opciones.progreso);
+  return modelo;
+}
+
+// Prompt processing in chunks of modelo.batch (reference engine.js:253-288); returns the last logits.
+async function prefill(modelo, ids) {
+  modelo.reset();
+  const TL = modelo.batch;
+  let logits = null;
+  for (let i = 0; i < ids.length; i += TL) {
+    const fin = Math.min(i + TL, ids.length);
+    logits = await modelo.forward(ids.slice(i, fin), fin >= ids.length);
+  }
+  return logits;
+}
+
+// Generation (reference engine.js:226-322).  Returns {ids, prompt_ms, decode_ms, tps}; tps is computed as the
+// reference does (generated / (t_end - t_after_prompt), engine.js:315-316).
+async function generar(modelo, ids, params) {
+  params = params || {};
+  if (!ids.length) throw new Error('the prompt is empty');
+  const ctx = modelo.ctx;
+  if (ids.length >= ctx) throw new Error('the prompt has ' + ids.length + ' tokens and the model context is ' + ctx);
+  const maxTok = params.max_tokens > 0 ? Math.min(params.max_tokens, ctx - ids.length) : ctx - ids.length;
+  const esFin = params.esFin || function () { return false; };
+  const porToken = params.onToken || function () {};
+  const mu = new Muestreador(params);
+  const t0 = Date.now();
+  let logits = await prefill(modelo, ids);
+  const tPrompt = Date.now();
+  const hist = ids.slice();
+  const out = [];
+  if (mu.esVoraz() && modelo.decodificarVoraz && !params.host_loop) {
+    const primero = argmax(logits);
+    if (!esFin(primero)) {
+      out.push(primero); porToken(primero);
+      const resto = maxTok - 1;
+      const bloque = params.bloque || resto;   // tokens per device run between host readbacks
+      let hechos = 0;
+      while (hechos < resto) {
+        const n = Math.min(bloque, resto - hechos);
+        const nuevos = modelo.decodificarVoraz(out[out.length - 1], n);
+        let parar = false;
+        for (const t of nuevos) {
+          if (esFin(t)) { parar = true; break; }
+          out.push(t); porToken(t);
+        }
+        hechos += n;
+        if (parar) break;
+      }
+    }
+  } else {
+    while (out.length < maxTok) {
+      const id = mu.elegir(logits, hist);
+      if (esFin(id)) break;
+      hist.push(id); out.push(id); porToken(id);
+      if (out.length >= maxTok) break;
+      logits = await modelo.forward([id], true);
+    }
+  }
+  const tEnd = Date.now();
+  const seg = (tEnd - tPrompt) / 1000;
+  return { ids: out, prompt_ms: tPrompt - t0, decode_ms: tEnd - tPrompt, tps: out.length && seg > 0 ? out.length / seg : null };
+}
+
+module.exports = { cargarRegistro: cargarRegistro, cargarModelo: cargarModelo, prefill: prefill, generar: generar, gpu: gpu };

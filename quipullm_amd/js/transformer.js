@@ -1,0 +1,442 @@
+'use strict';
+// Llama-style decoder on the gfx950 backend: the dense architectures (llama, qwen3) and the GQA
+// mixture-of-experts variant (qwen3moe).
+//
+// Plugin interface of quipullm's model classes (docs/ARCH_GUIDE.md:52-65, used by engine.js:104-125 and
+// 265-312): new Clase(gpu, meta); load(path, progress); reset(); forward(ids, wantLogits) -> Float32Array |
+// null; free(); properties nLayers, D, ctx, batch, vocab.  forward() issues the reference's op sequence
+// (transformer.js:252-336; the MoE FFN of deepseek2.js:374-386 without shared experts) through the named-op
+// facade.  decodificarVoraz() is this backend's fast path for greedy decoding: the whole one-token step is
+// captured once in a HIP graph with fused kernels (norm folded into the GEMVs, split-K attention with RoPE and
+// the KV append, SwiGLU folded into the gate/up GEMV, residual adds in the epilogues) and the argmax stays on
+// the device, feeding the next step's token id.
+const { despachar, dim2, vista } = require('./gpu');
+const { CargadorPesos } = require('./weights');
+
+const ROPE_NEOX = new Set(['qwen2', 'qwen3', 'qwen3moe', 'phi3', 'gemma', 'gemma2', 'gemma3', 'stablelm', 'olmo2']);
+const KQ = new Set(['q4k', 'q6k']);
+const FMT_ID = { f32: 0, q8: 8, q4k: 12, q6k: 14 };
+// gemv segment modes (qp_args.h)
+const STORE = 0, ACC = 1, SWIGLU = 2, ARGMAX = 3;
+const AMAX_WG = 512;   // workgroups of the fused output GEMV = partial maxima for the device argmax
+
+class ModeloTransformer {
+  constructor(gpu, meta) {
+    this.gpu = gpu;
+    this.meta = meta;
+    const kv = meta.kv, a = kv['general.architecture'];
+    this.arch = a;
+    const g = function (k, d) { return kv[a + '.' + k] !== undefined ? kv[a + '.' + k] : d; };
+    this.nLayers = g('block_count');
+    this.D = g('embedding_length');
+    this.nh = g('attention.head_count');
+    const hkv = g('attention.head_count_kv', this.nh);
+    if (Array.isArray(hkv)) throw new Error('per-layer KV head counts are not supported by this backend');
+    this.nkv = hkv;
+    this.hd = g('attention.key_length', this.D / this.nh);
+    this.eps = g('attention.layer_norm_rms_epsilon', 1e-5);
+    this.base = g('rope.freq_base', 10000);
+    this.nrot = g('rope.dimension_count', this.hd);
+    const oa = meta.arch_options || {};
+    this.neox = oa.rope ? (oa.rope === 'neox' ? 1 : 0) : (ROPE_NEOX.has(a) ? 1 : 0);
+    this.escAtt = g('attention.scale', 0) || 1 / Math.sqrt(this.hd);
+    if (g('embedding_scale', 0) || g('residual_scale', 0) || g('logit_scale', 0) || g('attention.sliding_window', 0))
+      throw new Error(a + ': embedding/residual/logit scales and sliding windows are not supported by this backend');
+    this.ctx = meta.ctx || 4096;
+    this.vocab = kv['tokenizer.ggml.tokens'].length;
+    this.nExp = g('expert_count', 0);
+    this.nUsados = g('expert_used_count', 0);
+    this.ffe = g('expert_feed_forward_length', 0);
+    this.normExp = !!g('expert_weights_norm', false);
+    this.escExp = g('expert_weights_scale', 1) || 1;
+    if (this.nExp > 1024 || this.nUsados > this.nExp) throw new Error(a + ': expert count not supported');
+    if (this.hd !== 64 && this.hd !== 128) throw new Error('head_dim ' + this.hd + ' not supported (64 or 128)');
+    if (this.nh % this.nkv || this.nh / this.nkv > 8) throw new Error('GQA group ' + this.nh + '/' + this.nkv + ' not supported');
+    const op = meta.options || {};
+    this.batch = op.batch || 32;                 // tokens per prefill pass (reference transformer.js:10 uses 32)
+    this.kvF16 = !!op.kv_f16;                    // f16 KV cache (the reference keeps it in f32)
+    this.baldosa = op.tiled_prefill !== false;   // config.json "tiled_prefill"
+    this.bufs = [];
+    this.pos = 0;
+    this.grafo = null;
+  }
+
+  load(ruta, progreso) {
+    const gpu = this.gpu, c = new CargadorPesos(gpu, this.meta, ruta, progreso);
+    this.cargador = c;
+    try {
+      if (c.existe('rope_freqs.weight')) throw new Error('this model uses rope_freqs.weight (scaled RoPE), which is not supported');
+      this.emb = c.matriz('token_embd.weight');
+      this.vocab = this.emb.N;
+      this.salida = c.existe('output.weight') ? c.matriz('output.weight') : this.emb;
+      this.normFinal = c.f32('output_norm.weight');
+      this.capas = [];
+      let F = 0;
+      for (let i = 0; i < this.nLayers; i++) {
+        const p = 'blk.' + i + '.';
+        for (const n of ['attn_q.bias', 'attn_k.bias', 'attn_v.bias', 'attn_output.bias', 'post_attention_norm.weight', 'post_ffw_norm.weight'])
+          if (c.existe(p + n)) throw new Error(p + n + ': biases and post-norms are not supported by this backend');
+        const capa = {};
+        capa.attnNorm = c.f32(p + 'attn_norm.weight');
+        capa.wq = c.matriz(p + 'attn_q.weight');
+        capa.wk = c.matriz(p + 'attn_k.weight');
+        capa.wv = c.matriz(p + 'attn_v.weight');
+        capa.wo = c.matriz(p + 'attn_output.weight');
+        capa.qNorm = c.existe(p + 'attn_q_norm.weight') ? c.f32(p + 'attn_q_norm.weight') : null;
+        capa.kNorm = c.existe(p + 'attn_k_norm.weight') ? c.f32(p + 'attn_k_norm.weight') : null;
+        capa.ffnNorm = c.f32(p + 'ffn_norm.weight');
+        if (this.nExp) {
+          capa.router = c.matriz(p + 'ffn_gate_inp.weight');
+          capa.eg = c.matriz(p + 'ffn_gate_exps.weight');
+          capa.eu = c.matriz(p + 'ffn_up_exps.weight');
+          capa.ed = c.matriz(p + 'ffn_down_exps.weight');
+          if (capa.eg.N !== this.nExp * this.ffe || capa.ed.N !== this.nExp * this.D)
+            throw new Error('layer ' + i + ': unexpected expert dimensions');
+        } else {
+          capa.gate = c.matriz(p + 'ffn_gate.weight');
+          capa.up = c.matriz(p + 'ffn_up.weight');
+          capa.down = c.matriz(p + 'ffn_down.weight');
+          F = Math.max(F, capa.gate.N);
+        }
+        const kvd = this.nkv * this.hd, eb = this.kvF16 ? 2 : 4;
+        capa.kc = gpu.buffer(this.ctx * kvd * eb, undefined, 'kcache' + i);
+        capa.vc = gpu.buffer(this.ctx * kvd * eb, undefined, 'vcache' + i);
+        this.bufs.push(capa.kc, capa.vc);
+        this.capas.push(capa);
+      }
+      this.F = F;
+    } finally {
+      c.cerrar();
+    }
+    const B = (n, l) => { const b = gpu.buffer(n, undefined, l); this.bufs.push(b); return b; };
+    const TB = this.batch, D = this.D, qd = this.nh * this.hd, kvd = this.nkv * this.hd;
+    const FF = this.nExp ? this.nUsados * this.ffe : this.F;
+    this.bPaso = B(16, 'paso');
+    this.bIds = B(4 * TB, 'ids');
+    gpu.escribir(this.bIds, 0, new Uint32Array(TB));   // device memory starts undefined; ids index the embeddings
+    this.x = B(4 * TB * D, 'x');
+    this.xn = B(4 * TB * D, 'xn');
+    this.q = B(4 * TB * qd, 'q');
+    this.k = B(4 * TB * kvd, 'k');
+    this.v = B(4 * TB * kvd, 'v');
+    this.att = B(4 * TB * qd, 'att');
+    this.g = B(4 * TB * FF, 'g');
+    this.u = B(4 * TB * FF, 'u');
+    if (this.nExp) {
+      this.rl = B(4 * TB * this.nExp, 'router_logits');
+      this.sel = B(4 * TB * this.nUsados, 'sel');
+      this.wts = B(4 * TB * this.nUsados, 'wts');
+      this.de = B(4 * TB * this.nUsados * D, 'de');
+    }
+    this.xl = B(4 * D, 'xlast');
+    this.logits = B(4 * this.vocab, 'logits');
+    // decode fast path
+    this.nsplit = Math.max(1, Math.min(Math.ceil(512 / this.nkv), Math.ceil(this.ctx / 32)));
+    this.partO = B(4 * this.nh * this.nsplit * this.hd, 'attn_part_o');
+    this.partML = B(8 * this.nh * this.nsplit, 'attn_part_ml');
+    this.amax = B(8 * AMAX_WG, 'argmax_partials');
+    gpu.escribir(this.amax, 0, new Uint8Array(8 * AMAX_WG));
+    this.maxGen = op_max_gen(this.meta);
+    this.tokens = B(4 * this.maxGen, 'tokens');
+    this.contador = B(16, 'step_counter');
+    this._armarGrupos();
+    this.prepararDecode();
+    this.reset();
+    return Promise.resolve();
+  }
+
+  // ---------------------------------------------------------------- reference op sequence
+  // matmul of the reference facade: one token -> matmul_<t>_1; T >= 8 with a K-quant and tiling -> _t; else _4
+  // (transformer.js:268-284).
+  _mm(W, x, y, acc) {
+    const gpu = this.gpu;
+    const u = gpu.uniforme([['u', W.N], ['u', W.K], ['u', acc ? 1 : 0], ['u', 0]]);
+    const wb = W.tipo === 'q8' ? [W.qs, W.ds] : [W.w];
+    const b = [u, this.bPaso].concat(wb, [x, y]);
+    return {
+      uno: gpu.grupo('matmul_' + W.tipo + '_1', b), lote: gpu.grupo('matmul_' + W.tipo + '_4', b),
+      baldosa: this.baldosa && KQ.has(W.tipo) ? gpu.grupo('matmul_' + W.tipo + '_t', b) : null, filas: W.N,
+    };
+  }
+
+  _mmE(W, x, y, tfijo) {
+    const gpu = this.gpu;
+    const u = gpu.uniforme([['u', W.N / this.nExp], ['u', W.K], ['u', 0], ['u', tfijo], ['u', this.nExp]]);
+    const wb = W.tipo === 'q8' ? [W.qs, W.ds] : [W.w];
+    return { g: gpu.grupo('matmul_' + W.tipo + '_e', [u, this.bPaso].concat(wb, [x, y, this.sel])), filas: W.N / this.nExp };
+  }
+
+  _embedGrupo(ids, y) {
+    const gpu = this.gpu, E = this.emb;
+    const u = gpu.uniforme([['u', this.D], ['u', E.N]]);
+    const wb = E.tipo === 'q8' ? [E.qs, E.ds] : [E.w];
+    return gpu.grupo('embed_' + E.tipo, [u, this.bPaso].concat(wb, [ids, y]));
+  }
+
+  _armarGrupos() {
+    const gpu = this.gpu, D = this.D, P = this.bPaso;
+    const G = {};
+    G.embed = this._embedGrupo(this.bIds, this.x);
+    const uNorm = gpu.uniforme([['u', D], ['u', 0], ['f', this.eps], ['u', 0]]);
+    const dummy = this.normFinal;
+    const f16 = this.kvF16 ? 1 : 0;
+    const kvd = this.nkv * this.hd;
+    G.capas = this.capas.map((c) => {
+      const ur = (nh, norm) => gpu.uniforme([['u', this.hd], ['u', nh], ['u', norm ? 1 : 0], ['u', this.neox],
+        ['f', this.eps], ['f', this.base], ['u', this.nrot], ['u', 0]]);
+      const gc = {
+        attnNorm: gpu.grupo('rmsnorm', [uNorm, P, this.x, c.attnNorm, this.xn]),
+        ffnNorm: gpu.grupo('rmsnorm', [uNorm, P, this.x, c.ffnNorm, this.xn]),
+        wq: this._mm(c.wq, this.xn, this.q, 0), wk: this._mm(c.wk, this.xn, this.k, 0), wv: this._mm(c.wv, this.xn, this.v, 0),
+        ropeQ: gpu.grupo('norm_rope', [ur(this.nh, !!c.qNorm), P, this.q, c.qNorm || dummy]),
+        ropeK: gpu.grupo('norm_rope', [ur(this.nkv, !!c.kNorm), P, this.k, c.kNorm || dummy]),
+        kvw: gpu.grupo('kv_write', [gpu.uniforme([['u', kvd], ['u', 0], ['u', f16], ['u', this.ctx]]), P, this.k, this.v, c.kc, c.vc]),
+        att: gpu.grupo('atencion', [gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', 0],
+          ['f', this.escAtt], ['u', 0], ['u', 0], ['u', 0], ['u', f16], ['u', this.ctx]]), P, this.q, c.kc, c.vc, this.att]),
+        wo: this._mm(c.wo, this.att, this.x, 1),
+      };
+      if (this.nExp) {
+        const K = this.nUsados;
+        gc.router = this._mm(c.router, this.xn, this.rl, 0);
+        gc.topk = gpu.grupo('moe_topk', [gpu.uniforme([['u', this.nExp], ['u', K], ['u', this.normExp ? 1 : 0],
+          ['f', this.escExp]]), P, this.rl, this.sel, this.wts]);
+        gc.eg = this._mmE(c.eg, this.xn, this.g, K);
+        gc.eu = this._mmE(c.eu, this.xn, this.u, K);
+        gc.eact = gpu.grupo('swiglu', [gpu.uniforme([['u', K * this.ffe]]), P, this.g, this.u]);
+        gc.ed = this._mmE(c.ed, this.g, this.de, 1);
+        gc.comb = gpu.grupo('moe_comb', [gpu.uniforme([['u', D], ['u', K]]), P, this.x, this.de, this.wts]);
+      } else {
+        gc.gate = this._mm(c.gate, this.xn, this.g, 0);
+        gc.up = this._mm(c.up, this.xn, this.u, 0);
+        gc.swiglu = gpu.grupo('swiglu', [gpu.uniforme([['u', c.gate.N]]), P, this.g, this.u]);
+        gc.F = c.gate.N;
+        gc.down = this._mm(c.down, this.g, this.x, 1);
+      }
+      return gc;
+    });
+    G.normFinal = gpu.grupo('rmsnorm', [gpu.uniforme([['u', D], ['u', 1], ['f', this.eps], ['u', 0]]), P, this.x, this.normFinal, this.xl]);
+    G.salida = this._mm(this.salida, this.xl, this.logits, 0);
+    G.argmax = gpu.grupo('argmax', [gpu.uniforme([['u', this.vocab]]), P, this.logits, this.bIds]);
+    this.G = G;
+  }
+
+  reset() {
+    this.pos = 0;   // the KV cache is overwritten by position (reference transformer.js:243-245)
+  }
+
+  _despacharCapas(T) {
+    const G = this.G, self = this;
+    const mm = function (g, uno) {
+      if (uno === undefined) uno = T === 1;
+      if (!uno && g.baldosa && T >= 8) { despachar(null, g.baldosa, Math.ceil(g.filas / 64), 1, Math.ceil(T / 32)); return; }
+      const xy = dim2(Math.ceil(g.filas / 8));
+      despachar(null, uno ? g.uno : g.lote, xy[0], xy[1], uno ? 1 : Math.ceil(T / 4));
+    };
+    const filas = function (n) { return Math.ceil(T * n / 256); };
+    despachar(null, G.embed, filas(this.D));
+    for (const gc of G.capas) {
+      despachar(null, gc.attnNorm, T);
+      mm(gc.wq); mm(gc.wk); mm(gc.wv);
+      despachar(null, gc.ropeQ, this.nh, T);
+      despachar(null, gc.ropeK, this.nkv, T);
+      despachar(null, gc.kvw, Math.ceil(T * this.nkv * this.hd / 256));
+      despachar(null, gc.att, this.nh, T);
+      mm(gc.wo);
+      despachar(null, gc.ffnNorm, T);
+      if (this.nExp) {
+        mm(gc.router);
+        despachar(null, gc.topk, Math.ceil(T / 64));
+        const e = function (m) { const xy = dim2(Math.ceil(m.filas / 8)); despachar(null, m.g, xy[0], xy[1], T * self.nUsados); };
+        e(gc.eg); e(gc.eu);
+        despachar(null, gc.eact, filas(this.nUsados * this.ffe));
+        e(gc.ed);
+        despachar(null, gc.comb, filas(this.D));
+      } else {
+        mm(gc.gate); mm(gc.up);
+        despachar(null, gc.swiglu, filas(gc.F));
+        mm(gc.down);
+      }
+    }
+    return mm;
+  }
+
+  // Processes up to `batch` tokens from the current position; with conLogits returns the logits of the last
+  // one (reference transformer.js:252-336).
+  forward(ids, conLogits) {
+    const T = ids.length;
+    if (T < 1 || T > this.batch) return Promise.reject(new Error('invalid batch'));
+    if (this.pos + T > this.ctx) return Promise.reject(new Error('context exceeded (' + this.ctx + ' tokens)'));
+    for (const id of ids) if (!(id >= 0 && id < this.vocab)) return Promise.reject(new Error('token id ' + id + ' outside the vocabulary'));
+    const gpu = this.gpu;
+    gpu.escribir(this.bPaso, 0, new Uint32Array([T, this.pos, 0, 0]));
+    gpu.escribir(this.bIds, 0, new Uint32Array(ids));
+    const mm = this._despacharCapas(T);
+    if (conLogits) {
+      despachar(null, this.G.normFinal, 1);
+      mm(this.G.salida, true);
+    }
+    this.pos += T;
+    if (!conLogits) return Promise.resolve(null);
+    const out = new Float32Array(this.vocab);
+    gpu.leer(this.logits, 0, out);
+    return Promise.resolve(out);
+  }
+
+  // ---------------------------------------------------------------- fused greedy decode
+  _gemv(segs, x, norm, K, opts) {
+    opts = opts || {};
+    const gpu = this.gpu;
+    const fmt = FMT_ID[segs[0].W.tipo];
+    const u = [['u', segs.length], ['u', K], ['f', this.eps], ['u', opts.last ? 1 : 0], ['u', opts.R || 0],
+      ['u', opts.maxWg || 0], ['u', fmt], ['u', 0]];
+    const b = [this.bPaso, x, norm || null, opts.amax || null];
+    for (const s of segs) {
+      if (FMT_ID[s.W.tipo] !== fmt) throw new Error('gemv segments must share one format');
+      u.push(['u', s.mode], ['u', s.W.N], ['u', 0], ['u', s.W.N]);
+      b.push(s.W.w, s.W2 ? s.W2.w : null, s.y);
+    }
+    return gpu.grupo('gemv', [gpu.uniforme(u)].concat(b));
+  }
+
+  // GEMV segments grouped by format (one launch per format present).
+  _gemvPorFormato(segs, x, norm, K) {
+    const porFmt = new Map();
+    for (const s of segs) {
+      if (!porFmt.has(s.W.tipo)) porFmt.set(s.W.tipo, []);
+      porFmt.get(s.W.tipo).push(s);
+    }
+    const out = [];
+    for (const lista of porFmt.values()) out.push(this._gemv(lista, x, norm, K));
+    return out;
+  }
+
+  _armarDecode() {
+    const gpu = this.gpu, P = this.bPaso, D = this.D, qd = this.nh * this.hd;
+    const plan = [];
+    plan.push([this._embedGrupo(this.bIds, this.x), Math.ceil(D / 256)]);
+    const uAtt = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', this.nsplit], ['f', this.escAtt],
+      ['f', this.eps], ['f', this.base], ['u', 0], ['u', this.nrot], ['u', this.neox], ['u', this.kvF16 ? 1 : 0], ['u', this.ctx]]);
+    const uComb = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nsplit]]);
+    for (let i = 0; i < this.capas.length; i++) {
+      const c = this.capas[i], gc = this.G.capas[i];
+      for (const g of this._gemvPorFormato([{ W: c.wq, mode: STORE, y: this.q }, { W: c.wk, mode: STORE, y: this.k },
+        { W: c.wv, mode: STORE, y: this.v }], this.x, c.attnNorm, D)) plan.push([g, 1]);
+      plan.push([gpu.grupo('dec_attn', [uAtt, P, this.q, this.k, this.v, c.kc, c.vc, c.qNorm, c.kNorm, this.partO, this.partML]), 1]);
+      plan.push([gpu.grupo('dec_attn_comb', [uComb, P, this.partO, this.partML, this.att]), 1]);
+      plan.push([this._gemv([{ W: c.wo, mode: ACC, y: this.x }], this.att, null, qd), 1]);
+      if (this.nExp) {
+        plan.push([gc.ffnNorm, 1]);
+        plan.push([this._gemv([{ W: c.router, mode: STORE, y: this.rl }], this.xn, null, D), 1]);
+        plan.push([gc.topk, 1]);
+        const K = this.nUsados, E = this.nExp;
+        const eg = c.eg, eu = c.eu, ed = c.ed;
+        if (eg.tipo === eu.tipo) {
+          const wb = eg.tipo === 'q8' ? [eg.qs, eg.ds] : [eg.w];
+          plan.push([gpu.grupo('matmul_' + eg.tipo + '_e_swiglu', [gpu.uniforme([['u', this.ffe], ['u', D], ['u', 0], ['u', K], ['u', E]]),
+            P].concat(wb, [eu.w, this.xn, this.g, this.sel])), [1, 1, K]]);
+        } else {
+          plan.push([gc.eg.g, [1, 1, K]]); plan.push([gc.eu.g, [1, 1, K]]); plan.push([gc.eact, Math.ceil(K * this.ffe / 256)]);
+        }
+        plan.push([gc.ed.g, [1, 1, K]]);
+        plan.push([gc.comb, Math.ceil(D / 256)]);
+      } else if (c.gate.tipo === c.up.tipo) {
+        plan.push([this._gemv([{ W: c.gate, W2: c.up, mode: SWIGLU, y: this.g }], this.x, c.ffnNorm, D), 1]);
+        plan.push([this._gemv([{ W: c.down, mode: ACC, y: this.x }], this.g, null, this.F), 1]);
+      } else {
+        for (const g of this._gemvPorFormato([{ W: c.gate, mode: STORE, y: this.g }, { W: c.up, mode: STORE, y: this.u }], this.x, c.ffnNorm, D)) plan.push([g, 1]);
+        plan.push([gc.swiglu, Math.ceil(this.F / 256)]);
+        plan.push([this._gemv([{ W: c.down, mode: ACC, y: this.x }], this.g, null, this.F), 1]);
+      }
+    }
+    const S = this.salida;
+    const rOut = S.tipo === 'q6k' ? 2 : 4;
+    this.amaxWg = Math.min(AMAX_WG, Math.ceil(this.vocab / (4 * rOut)));
+    plan.push([this._gemv([{ W: S, mode: ARGMAX, y: this.logits }], this.x, this.normFinal, D,
+      { R: rOut, maxWg: this.amaxWg, amax: this.amax }), 1]);
+    plan.push([gpu.grupo('argmax_fin', [gpu.uniforme([['u', this.amaxWg], ['u', 1], ['u', this.maxGen]]), P, this.amax, this.bIds,
+      this.tokens, this.contador]), 1]);
+    return plan;
+  }
+
+  _ejecutar(plan) {
+    for (const it of plan) {
+      const d = Array.isArray(it[1]) ? it[1] : [it[1], 1, 1];
+      despachar(null, it[0], d[0], d[1], d[2]);
+    }
+  }
+
+  // Builds and captures the fused one-token step.  Called from load(): the eager validation run writes KV slot 0
+  // of every layer, which the first prefill overwrites.
+  prepararDecode() {
+    if (this.grafo) return;
+    this.planDecode = this._armarDecode();
+    const self = this;
+    // one eager run validates every op's bindings before capture (a failed op inside a capture is harder to read)
+    this.gpu.escribir(this.bPaso, 0, new Uint32Array([1, 0, 0, 0]));
+    this.gpu.escribir(this.bIds, 0, new Uint32Array([0]));
+    this.gpu.escribir(this.contador, 0, new Uint32Array([0, 0, 0, 0]));
+    this._ejecutar(this.planDecode);
+    this.gpu.sincronizar();
+    this.grafo = this.gpu.capturar(function () { self._ejecutar(self.planDecode); });
+  }
+
+  // Greedy continuation on the device: `primero` is the token chosen from the last logits; runs `n` one-token
+  // steps (each consumes the previous token and picks the next with the reference's argmax: strict '>', lowest
+  // index on ties) and returns the n new token ids.  Positions advance by n.  With porPaso, each step's logits
+  // are passed to porPaso(i, token, logits) (one readback per step, for checks).
+  decodificarVoraz(primero, n, opciones) {
+    opciones = opciones || {};
+    if (n < 1) return [];
+    if (n > this.maxGen) throw new Error('at most ' + this.maxGen + ' tokens per call');
+    if (this.pos + n > this.ctx) throw new Error('context exceeded (' + this.ctx + ' tokens)');
+    if (!(primero >= 0 && primero < this.vocab)) throw new Error('token id ' + primero + ' outside the vocabulary');
+    this.prepararDecode();
+    const gpu = this.gpu;
+    gpu.escribir(this.bPaso, 0, new Uint32Array([1, this.pos, 0, 0]));
+    gpu.escribir(this.bIds, 0, new Uint32Array([primero]));
+    gpu.escribir(this.contador, 0, new Uint32Array([0, 0, 0, 0]));
+    if (opciones.porPaso) {
+      const lg = new Float32Array(this.vocab), t = new Uint32Array(1);
+      for (let i = 0; i < n; i++) {
+        gpu.reproducir(this.grafo, 1);
+        gpu.leer(this.logits, 0, lg);
+        gpu.leer(this.bIds, 0, t);
+        opciones.porPaso(i, t[0], lg);
+      }
+    } else if (opciones.tiempos) {
+      const e0 = gpu.evento(), e1 = gpu.evento();
+      gpu.marcar(e0);
+      gpu.reproducir(this.grafo, n);
+      gpu.marcar(e1);
+      opciones.tiempos.ms = gpu.msEntre(e0, e1);
+    } else {
+      gpu.reproducir(this.grafo, n);
+    }
+    const out = new Uint32Array(n);
+    gpu.leer(this.tokens, 0, out);
+    this.pos += n;
+    return Array.from(out);
+  }
+
+  // Greedy argmax of the current logits buffer on the device (same tie rule as the reference).
+  argmaxDispositivo() {
+    despachar(null, this.G.argmax, 1);
+    const t = new Uint32Array(1);
+    this.gpu.leer(this.bIds, 0, t);
+    return t[0];
+  }
+
+  free() {
+    if (this.grafo) { this.gpu.liberarGrafo(this.grafo); this.grafo = null; }
+    const todos = this.bufs.concat(this.cargador ? this.cargador.buffers : []);
+    this.gpu.liberar(todos);
+    this.bufs = [];
+  }
+}
+
+function op_max_gen(meta) {
+  const op = meta.options || {};
+  return op.max_gen || 4096;
+}
+
+module.exports = { ModeloTransformer: ModeloTransformer };
