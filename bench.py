@@ -1,0 +1,215 @@
+"""Benchmark of the MI355X token loop: decode tok/s of the 8B-shape Q4_K_M model, plus the Q4_K GEMV roofline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A "step" is one greedy decode token of the Llama-3-8B-shaped Q4_K_M model (32 layers, hidden 4096, GQA 32/8,
+head_dim 128, FFN 14336, vocab 128256; random weights written to a seeded synthetic GGUF), batch 1, f16 KV.
+The KV cache is first filled by prefilling 4096 uniform-random prompt ids (the headline figure) and, in a
+second measurement, 512.  Weights and activations are resident in HBM when the timed region starts; the
+timed region is K back-to-back replays of the captured one-token step, bracketed by HIP events on the
+backend's stream, with the greedy argmax on the device.
+
+Also measured live: the dominant kernel, the Q4_K GEMV (14336 x 4096, batch 1), over back-to-back launches that
+rotate through >= 512 MB of weight copies (so the 256 MB last-level cache cannot hold them), timed with HIP
+events on the backend's stream.  The CPU baseline is the C restatement of the reference semantics (the test
+oracle) timed on this host's cores on a bounded sample of the same decode.
+
+Process layout: this process loads the CPU checker first, runs the GPU decode in a child Node.js process
+(the product host) and only then opens the GPU itself (ctypes) for the GEMV measurement, so no program is
+started from a process that has initialised the GPU.  One JSON line is printed.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+from quipullm_amd import synth  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+MODEL = "llama8b_q4km"
+METRIC = "decode tok/s @8B-shape Q4_K ctx 4096; Q4_K GEMV HBM GB/s vs peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def model_dir():
+    d = os.environ.get("QP_MODEL_DIR") or os.path.join(os.environ.get("TMPDIR", "/tmp"), "quipu_models")
+    os.makedirs(d, exist_ok=True)
+    return d
+
+
+def ensure_built():
+    from quipullm_amd import build
+    if not build.built() or not os.path.exists(build.NAPI):
+        log("bench: native parts missing, building")
+        build.build_all(oracle=True)
+
+
+def decode_bytes_per_token(path, P, n):
+    """Algorithmic HBM bytes of one decode token, averaged over the n timed steps after a P-token prefill:
+    every weight tensor read once (embedding: one row), plus the f16 K and V rows of every cached position."""
+    from oracle.oracle import GGUF  # header reader only
+    g = GGUF(path)
+    c = synth.CONFIGS[MODEL]
+    w = 0
+    for name, t in g.tensors.items():
+        if name == "token_embd.weight":
+            w += t["bytes"] // c.vocab
+        else:
+            w += t["bytes"]
+    kv_per_pos = c.n_layers * 2 * c.nkv * c.hd * 2
+    mean_pos = P + (n + 1) / 2.0
+    return w, w + kv_per_pos * mean_pos
+
+
+def cpu_baseline(path, seconds=20.0):
+    """The oracle on this host: greedy decode steps of the same model after a 1-token prompt, as many as fit in
+    about `seconds` (at least 2)."""
+    from oracle import oracle as O
+    threads = O.lib().or_num_threads()
+    m = O.Model(path, ctx=64)
+    lg = m.forward([1], True)  # also pages the weights in
+    t0 = time.time()
+    steps = 0
+    while steps < 2 or (time.time() - t0 < seconds and steps < 40):
+        lg = m.forward([O.argmax(lg)], True)
+        steps += 1
+    dt = time.time() - t0
+    m.close()
+    return {"value": steps / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} greedy decode steps of the same 8B Q4_K_M model after a 1-token prompt "
+                      f"(KV length <= {steps + 1}, f32 KV) in {dt:.1f} s on {threads} OpenMP threads; "
+                      f"C restatement of the reference WGSL semantics"}
+
+
+def run_decode(path, steps, warmup, prefills):
+    c = synth.CONFIGS[MODEL]
+    ctx = max(prefills) + steps + warmup + 8
+    ids = synth.random_prompt(c.vocab, max(prefills), 7)
+    pf = os.path.join(model_dir(), f"{MODEL}.bench_prompt.json")
+    with open(pf, "w") as f:
+        json.dump(ids, f)
+    cmd = ["node", os.path.join(ROOT, "quipullm_amd", "js", "cli.js"), "bench", "--model", path, "--prompt-file", pf,
+           "--n", str(steps), "--warmup", str(warmup), "--kv", "f16", "--ctx", str(ctx), "--batch", "512",
+           "--max-gen", str(max(steps, warmup) + 8), "--prefill", ",".join(str(p) for p in prefills)]
+    log("bench: " + " ".join(cmd))
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    if r.returncode != 0:
+        raise RuntimeError("decode benchmark failed:\n" + r.stderr[-3000:])
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def gemv_microbench(shapes, iters=200, rotate_bytes=640 << 20):
+    """Average launch duration (HIP events over back-to-back launches) of the fused GEMV op, per shape."""
+    from quipullm_amd import capi
+    q = capi.Quipu(0)
+    out = []
+    paso = q.paso(1, 0)
+    for fmt, N, K in shapes:
+        nbytes = capi.device_bytes(fmt, N, K)
+        ncopy = max(2, rotate_bytes // nbytes + 1)
+        raw = np.frombuffer(synth.gen_blocks(np.random.default_rng([3, N, K]), fmt, N * K), np.uint8)
+        hs = [q.upload_matrix(fmt, raw, N, K) for _ in range(ncopy)]
+        xb = q.buffer_from(np.random.default_rng(4).standard_normal(K).astype(np.float32))
+        yb = q.alloc(N * 4)
+        u = capi.gemv_uniform(1, K, fmt=fmt, segs=[(capi.STORE, N, 0, N)])
+        for i in range(10):
+            q.dispatch("gemv", u, [paso, xb, 0, 0, hs[i % ncopy], 0, yb])
+        q.sync()
+        e0, e1 = q.event(), q.event()
+        q.record(e0)
+        for i in range(iters):
+            q.dispatch("gemv", u, [paso, xb, 0, 0, hs[i % ncopy], 0, yb])
+        q.record(e1)
+        us = q.elapsed_ms(e0, e1) * 1000.0 / iters
+        alg = nbytes + 4 * K + 4 * N
+        out.append({"format": capi.FMT_NAME[fmt], "N": N, "K": K, "bytes": alg, "us_per_launch": us,
+                    "GBs": alg / (us * 1e-6) / 1e9})
+        for h in hs:
+            q.free(h)
+        q.free(xb)
+        q.free(yb)
+        q.event_free(e0)
+        q.event_free(e1)
+    return out
+
+
+def committed_traffic():
+    """HBM bytes per launch of the Q4_K GEMV from the committed rocprofv3 counter summary, if present."""
+    p = os.path.join(ROOT, "profiles", "gemv_q4k_14336x4096_traffic.md")
+    if not os.path.exists(p):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.e+]+)", open(p).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); the multi-GPU sharding of the "
+              f"token loop is a design note, not a measured path", file=sys.stderr)
+        sys.exit(2)
+    if "RANK" in os.environ and os.environ.get("WORLD_SIZE", "1") != "1":
+        print("bench.py: one GPU only", file=sys.stderr)
+        sys.exit(2)
+    ensure_built()
+    t0 = time.time()
+    path = synth.ensure_model(MODEL, model_dir())
+    log(f"bench: model {path} ready in {time.time() - t0:.1f}s")
+    cpu = cpu_baseline(path, a.cpu_seconds)
+    log(f"bench: cpu baseline {cpu['value']:.3f} tok/s")
+    prefills = [4096, 512]
+    dec = run_decode(path, a.steps, a.warmup, prefills)
+    runs = {r["prompt_tokens"]: r for r in dec["runs"]}
+    log("bench: decode " + json.dumps(dec))
+    from quipullm_amd import capi
+    gem = gemv_microbench([(capi.Q4_K, 14336, 4096), (capi.Q4_K, 4096, 4096), (capi.Q4_K, 4096, 14336),
+                           (capi.Q6_K, 4096, 4096), (capi.Q6_K, 14336, 4096), (capi.Q6_K, 4096, 14336)])
+    dom = gem[0]
+    main_run = runs[4096]
+    wbytes, bpt = decode_bytes_per_token(path, 4096, a.steps)
+    _, bpt512 = decode_bytes_per_token(path, 512, a.steps)
+    tok_s = main_run["decode_tok_s"]
+    result = {
+        "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(main_run["ms_per_token"], 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "Llama-3-8B-shape Q4_K_M (Q6_K attn_v/ffn_down/output) greedy decode, batch 1, "
+                               "KV prefilled with 4096 random prompt ids, f16 KV, 256 timed tokens",
+                   "ctx": 4096, "kv": "f16", "batch": 1, "prefill_tokens": 4096,
+                   "decode_tok_s_ctx512": round(runs[512]["decode_tok_s"], 3),
+                   "decode_hbm_GBs_ctx4096": round(bpt * tok_s / 1e9, 1),
+                   "decode_roofline_frac_ctx4096": round(bpt * tok_s / 1e9 / PEAK_HBM_GBS, 4),
+                   "decode_roofline_frac_ctx512": round(bpt512 * runs[512]["decode_tok_s"] / 1e9 / PEAK_HBM_GBS, 4),
+                   "bytes_per_token_ctx4096": int(bpt), "weight_bytes_per_token": int(wbytes),
+                   "wall_tok_s_ctx4096": round(main_run["wall_tok_s"], 3),
+                   "prefill_tok_s_4096": round(main_run["prefill_tok_s"], 1),
+                   "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()} for g in gem]},
+        "roofline": {"bound": "hbm", "kernel": "qp_gemv_q4k (Q4_K GEMV 14336x4096, batch 1)",
+                     "achieved": round(dom["GBs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(dom["GBs"] / PEAK_HBM_GBS, 4), "traffic": committed_traffic(),
+                     "bytes_per_launch": dom["bytes"], "us_per_launch": round(dom["us_per_launch"], 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -898,17 +898,82 @@ KERNEL __launch_bounds__(256) void qp_attn_hd128(QpAttnArgs a) { attn_gen_body<1
 
 // Split-K decode attention for one token, with the per-head q/k RMSNorm, RoPE and the KV append fused in.
 // grid (nkv, nsplit).  Each workgroup takes a contiguous key range of one KV head for all G query heads of the
-// group and writes an unnormalized partial (m, l, acc) per head; qp_dec_attn_comb merges the splits.
+// group (G in 1, 2, 4, 8) and writes an unnormalized partial (m, l, acc) per head; qp_dec_attn_comb merges them.
+// Keys and values move in tiles of 32 with 16-byte loads; the next tile is loading while the current one is
+// scored.  Scores are float4 dot products from LDS; the online softmax runs per head within one wavefront.
+template <int HD>
+struct KvTile {
+    static constexpr int TK = 32;
+    static constexpr int MAXC = HD * 4 * TK / 16 / 256;  // 16-byte chunks per thread (f32 cache, the larger)
+    uint4 k[MAXC], v[MAXC];
+};
+
+template <int HD>
+QP_DEV void kv_tile_load(KvTile<HD>& t, const QpDecAttnArgs& a, uint32_t kvh, uint32_t kt, uint32_t k1) {
+    constexpr int TK = KvTile<HD>::TK;
+    const uint32_t eb = a.f16 ? 2 : 4;
+    const uint32_t cpk = HD * eb / 16;  // 16-byte chunks per key
+    const uint32_t kvd = a.nkv * HD;
+#pragma unroll
+    for (int c = 0; c < KvTile<HD>::MAXC; c++) {
+        const uint32_t q = threadIdx.x + 256 * c;
+        if (q < TK * cpk) {
+            const uint32_t key = min(kt + q / cpk, k1 - 1);  // clamped: rows past the range are loaded, not used
+            const uint64_t off = ((uint64_t)key * kvd + kvh * HD) * eb + (q % cpk) * 16;
+            t.k[c] = gload<uint4>(a.kc + off);
+            t.v[c] = gload<uint4>(a.vc + off);
+        }
+    }
+}
+
+template <int HD>
+QP_DEV void kv_tile_store(const KvTile<HD>& t, const QpDecAttnArgs& a, uint32_t kt, uint32_t k1, uint32_t pos0,
+                          float* ks, float* vs, const float* kn, const float* vn) {
+    constexpr int TK = KvTile<HD>::TK;
+    constexpr int KS = HD + 4;  // K row stride in LDS (16-byte aligned rows, shifted banks)
+    const uint32_t eb = a.f16 ? 2 : 4;
+    const uint32_t cpk = HD * eb / 16, epc = 16 / eb;  // chunks per key, elements per chunk
+#pragma unroll
+    for (int c = 0; c < KvTile<HD>::MAXC; c++) {
+        const uint32_t q = threadIdx.x + 256 * c;
+        if (q < TK * cpk) {
+            const uint32_t jj = q / cpk, d0 = (q % cpk) * epc, key = kt + jj;
+            float kf[8], vf[8];
+            if (a.f16) {
+                const uint32_t kw[4] = {t.k[c].x, t.k[c].y, t.k[c].z, t.k[c].w};
+                const uint32_t vw[4] = {t.v[c].x, t.v[c].y, t.v[c].z, t.v[c].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    kf[2 * i] = h2f(kw[i] & 0xffffu); kf[2 * i + 1] = h2f(kw[i] >> 16);
+                    vf[2 * i] = h2f(vw[i] & 0xffffu); vf[2 * i + 1] = h2f(vw[i] >> 16);
+                }
+            } else {
+                kf[0] = __uint_as_float(t.k[c].x); kf[1] = __uint_as_float(t.k[c].y);
+                kf[2] = __uint_as_float(t.k[c].z); kf[3] = __uint_as_float(t.k[c].w);
+                vf[0] = __uint_as_float(t.v[c].x); vf[1] = __uint_as_float(t.v[c].y);
+                vf[2] = __uint_as_float(t.v[c].z); vf[3] = __uint_as_float(t.v[c].w);
+            }
+            for (uint32_t e = 0; e < epc; e++) {
+                float kv = kf[e], vv = vf[e];
+                if (key == pos0) { kv = kn[d0 + e]; vv = vn[d0 + e]; }  // the new key: this workgroup's own copy
+                else if (key >= k1) { kv = 0.0f; vv = 0.0f; }
+                ks[jj * KS + d0 + e] = kv;
+                vs[jj * HD + d0 + e] = vv;
+            }
+        }
+    }
+}
+
 template <int HD>
 QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
-    constexpr int TK = 32;
+    constexpr int TK = KvTile<HD>::TK, KS = HD + 4;
     extern __shared__ float4 smem4[];
     const uint32_t G = a.nh / a.nkv;
     float* qs = reinterpret_cast<float*>(smem4);  // [G][HD]
-    float* ks = qs + G * HD;                      // [TK][HD+1]
-    float* vs = ks + TK * (HD + 1);               // [TK][HD]
+    float* ks = qs + 8 * HD;                      // [TK][KS]
+    float* vs = ks + TK * KS;                     // [TK][HD]
     float* ps = vs + TK * HD;                     // [G][TK]
-    float* kn = ps + G * TK;                      // [HD] new key (roped)
+    float* kn = ps + 8 * TK;                      // [HD] new key (normalized, rotated)
     float* vn = kn + HD;                          // [HD] new value
     float* cr = vn + HD;                          // [G]
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -921,13 +986,14 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
     const uint32_t k0 = sp * per, k1 = min(nk, k0 + per);
     const uint32_t kvd = a.nkv * HD;
     const float pos_esc = (float)pos0 * a.esc;
-    // queries of the group, normalized and rotated
-    for (uint32_t i = tid; i < G * HD; i += 256) qs[i] = cptr<float>(a.q)[(uint64_t)kvh * G * HD + i];
+    KvTile<HD> tile;
+    if (k0 < k1) kv_tile_load<HD>(tile, a, kvh, k0, k1);  // first tile in flight during the q/k preparation
+    for (uint32_t i = tid; i < G * HD; i += 256) qs[i] = gload<float>(a.q + 4ull * ((uint64_t)kvh * G * HD + i));
     const bool has_new = k0 < k1 && k1 == nk;
     if (has_new)
         for (uint32_t i = tid; i < HD; i += 256) {
-            kn[i] = cptr<float>(a.k)[(uint64_t)kvh * HD + i];
-            vn[i] = cptr<float>(a.v)[(uint64_t)kvh * HD + i];
+            kn[i] = gload<float>(a.k + 4ull * ((uint64_t)kvh * HD + i));
+            vn[i] = gload<float>(a.v + 4ull * ((uint64_t)kvh * HD + i));
         }
     __syncthreads();
     for (uint32_t g = wave; g < G + (has_new ? 1u : 0u); g += 4) {
@@ -945,89 +1011,82 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
         for (uint32_t i = tid; i < HD; i += 256) {
             if (a.f16) {
                 const uint16_t hk = f2h(kn[i]), hv = f2h(vn[i]);
-                mptr<uint16_t>(a.kc)[o + i] = hk;
-                mptr<uint16_t>(a.vc)[o + i] = hv;
+                gstore<uint16_t>(a.kc + 2 * (o + i), hk);
+                gstore<uint16_t>(a.vc + 2 * (o + i), hv);
                 kn[i] = h2f(hk);
                 vn[i] = h2f(hv);
             } else {
-                mptr<float>(a.kc)[o + i] = kn[i];
-                mptr<float>(a.vc)[o + i] = vn[i];
+                gstore<float>(a.kc + 4 * (o + i), kn[i]);
+                gstore<float>(a.vc + 4 * (o + i), vn[i]);
             }
         }
     }
-    // score roles: head g = tid / 32 (< G), key j = tid % 32;  P.V roles: output o = tid + 256*c
-    const uint32_t sg = tid >> 5, j = tid & 31;
-    constexpr int MAXC = 8 * HD / 256 > 0 ? 8 * HD / 256 : 1;  // up to G = 8
-    float acc[MAXC];
+    // score roles: pair (g, j) handled by tpp adjacent threads, each over HD / tpp dims
+    const uint32_t tpp = G * TK * 2 <= 256 ? 2 : 1;
+    const uint32_t pair = tid / tpp, part = tid % tpp;
+    const uint32_t sg = pair / TK, j = pair % TK;
+    const bool scorer = sg < G;
+    constexpr int MAXO = 8 * HD / 256 > 0 ? 8 * HD / 256 : 1;  // P.V outputs per thread (G <= 8)
+    float acc[MAXO];
 #pragma unroll
-    for (int c = 0; c < MAXC; c++) acc[c] = 0.0f;
+    for (int c = 0; c < MAXO; c++) acc[c] = 0.0f;
     float m = -3.0e38f, l = 0.0f;
-    __syncthreads();
     for (uint32_t kt = k0; kt < k1; kt += TK) {
-        for (uint32_t i = tid; i < TK * HD; i += 256) {
-            const uint32_t jj = i / HD, dd = i % HD;
-            const uint32_t key = kt + jj;
-            float kv = 0.0f, vv = 0.0f;
-            if (key < k1) {
-                if (key == pos0) { kv = kn[dd]; vv = vn[dd]; }
-                else {
-                    const uint64_t idx = (uint64_t)key * kvd + kvh * HD + dd;
-                    kv = kv_load<HD>(a.kc, a.f16, idx);
-                    vv = kv_load<HD>(a.vc, a.f16, idx);
-                }
-            }
-            ks[jj * (HD + 1) + dd] = kv;
-            vs[jj * HD + dd] = vv;
-        }
+        __syncthreads();  // the previous tile's LDS is free; kn/vn are final
+        kv_tile_store<HD>(tile, a, kt, k1, pos0, ks, vs, kn, vn);
         __syncthreads();
-        if (sg < G) {
+        if (kt + TK < k1) kv_tile_load<HD>(tile, a, kvh, kt + TK, k1);  // next tile loads during this one
+        if (scorer) {
             const uint32_t key = kt + j;
             const bool valid = key < k1;
-            float s = -3.0e38f;
-            if (valid) {
-                float dot = 0.0f;
-                const float* qr = qs + sg * HD;
-                const float* kr = ks + j * (HD + 1);
-#pragma unroll 8
-                for (int q = 0; q < HD; q++) dot += qr[q] * kr[q];
-                s = dot * a.scale;
+            const float4* qr = reinterpret_cast<const float4*>(qs + sg * HD + part * (HD / tpp));
+            const float4* kr = reinterpret_cast<const float4*>(ks + j * KS + part * (HD / tpp));
+            float dot = 0.0f;
+            for (uint32_t i = 0; i < HD / tpp / 4; i++) {
+                const float4 qv = qr[i], kv = kr[i];
+                dot = fmaf(qv.x, kv.x, dot); dot = fmaf(qv.y, kv.y, dot);
+                dot = fmaf(qv.z, kv.z, dot); dot = fmaf(qv.w, kv.w, dot);
             }
-            const float mt = fmaxf(m, half_max(s));
+            if (tpp == 2) dot += __shfl_xor(dot, 1, 64);
+            const float s = valid ? dot * a.scale : -3.0e38f;
+            float mx = s;
+            for (uint32_t msk = tpp; msk < 32 * tpp; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+            const float mt = fmaxf(m, mx);
             const float p = valid ? expf(s - mt) : 0.0f;
-            const float sum = half_sum(p);
+            float sum = part == 0 ? p : 0.0f;
+            for (uint32_t msk = 1; msk < 32 * tpp; msk <<= 1) sum += __shfl_xor(sum, msk, 64);
             const float corr = expf(m - mt);
             l = l * corr + sum;
             m = mt;
-            ps[sg * TK + j] = p;
-            if (j == 0) cr[sg] = corr;
+            if (part == 0) ps[sg * TK + j] = p;
+            if (part == 0 && j == 0) cr[sg] = corr;
         }
         __syncthreads();
 #pragma unroll
-        for (int c = 0; c < MAXC; c++) {
+        for (int c = 0; c < MAXO; c++) {
             const uint32_t o = tid + 256 * c;
             if (o < G * HD) {
                 const uint32_t g = o / HD, dd = o % HD;
                 float v = acc[c] * cr[g];
                 const float* pr = ps + g * TK;
 #pragma unroll 8
-                for (int jj = 0; jj < TK; jj++) v += pr[jj] * vs[jj * HD + dd];
+                for (int jj = 0; jj < TK; jj++) v = fmaf(pr[jj], vs[jj * HD + dd], v);
                 acc[c] = v;
             }
         }
-        __syncthreads();
     }
     const uint32_t h0 = kvh * G;
-    if (sg < G && j == 0) {
-        float* ml = mptr<float>(a.part_ml) + ((uint64_t)(h0 + sg) * a.nsplit + sp) * 2;
-        ml[0] = m;
-        ml[1] = l;
+    if (scorer && part == 0 && j == 0) {
+        const uint64_t i = (uint64_t)(h0 + sg) * a.nsplit + sp;
+        gstore<float>(a.part_ml + 8 * i, m);
+        gstore<float>(a.part_ml + 8 * i + 4, l);
     }
 #pragma unroll
-    for (int c = 0; c < MAXC; c++) {
+    for (int c = 0; c < MAXO; c++) {
         const uint32_t o = tid + 256 * c;
         if (o < G * HD) {
             const uint32_t g = o / HD, dd = o % HD;
-            mptr<float>(a.part_o)[((uint64_t)(h0 + g) * a.nsplit + sp) * HD + dd] = acc[c];
+            gstore<float>(a.part_o + 4 * (((uint64_t)(h0 + g) * a.nsplit + sp) * HD + dd), acc[c]);
         }
     }
 }
@@ -1035,23 +1094,50 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
 KERNEL __launch_bounds__(256) void qp_dec_attn_hd64(QpDecAttnArgs a) { attn_dec_body<64>(a); }
 KERNEL __launch_bounds__(256) void qp_dec_attn_hd128(QpDecAttnArgs a) { attn_dec_body<128>(a); }
 
-// Merge of the split partials: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).  grid nh.
+// Merge of the split partials: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), splits with l = 0 skipped.
+// grid nh; the per-split weights are computed in parallel, then each output element sums its splits with
+// independent loads.
 KERNEL __launch_bounds__(256) void qp_dec_attn_comb(QpDecCombArgs a) {
-    const uint32_t h = blockIdx.x, d = threadIdx.x;
-    const float* ml = cptr<float>(a.part_ml) + (uint64_t)h * a.nsplit * 2;
-    float M = -3.0e38f;
-    for (uint32_t s = 0; s < a.nsplit; s++) M = fmaxf(M, ml[2 * s + 1] > 0.0f ? ml[2 * s] : -3.0e38f);
-    float L = 0.0f, o = 0.0f;
-    const float* po = cptr<float>(a.part_o) + (uint64_t)h * a.nsplit * a.hd;
-    for (uint32_t s = 0; s < a.nsplit; s++) {
-        const float l = ml[2 * s + 1];
-        if (l > 0.0f) {
-            const float e = expf(ml[2 * s] - M);
-            L += l * e;
-            if (d < a.hd) o += po[(uint64_t)s * a.hd + d] * e;
-        }
+    __shared__ float ws[1024];
+    __shared__ float red[4];
+    __shared__ float part[256];
+    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t ml = a.part_ml + 8ull * h * a.nsplit;
+    float mx = -3.0e38f;
+    for (uint32_t s = tid; s < a.nsplit; s += 256) {
+        const float2 v = gload<float2>(ml + 8ull * s);
+        if (v.y > 0.0f) mx = fmaxf(mx, v.x);
     }
-    if (d < a.hd) mptr<float>(a.o)[(uint64_t)h * a.hd + d] = o / L;
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float ls = 0.0f;
+    for (uint32_t s = tid; s < a.nsplit; s += 256) {
+        const float2 v = gload<float2>(ml + 8ull * s);
+        const float e = v.y > 0.0f ? expf(v.x - M) : 0.0f;
+        ws[s] = e;
+        ls += v.y * e;
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) red[wave] = ls;
+    __syncthreads();
+    const float L = (red[0] + red[1]) + (red[2] + red[3]);
+    const uint32_t P = 256 / a.hd, d = tid % a.hd, pt = tid / a.hd;
+    float o = 0.0f;
+    const uint64_t po = a.part_o + 4ull * h * a.nsplit * a.hd;
+    if (pt < P) {
+#pragma unroll 8
+        for (uint32_t s = pt; s < a.nsplit; s += P) o = fmaf(ws[s], gload<float>(po + 4ull * ((uint64_t)s * a.hd + d)), o);
+    }
+    part[tid] = o;
+    __syncthreads();
+    if (tid < a.hd) {
+        float t = 0.0f;
+        for (uint32_t i = 0; i < P; i++) t += part[i * a.hd + tid];
+        gstore<float>(a.o + 4ull * ((uint64_t)h * a.hd + tid), t / L);
+    }
 }
 
 // ====================================================================================== argmax

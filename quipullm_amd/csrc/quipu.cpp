@@ -158,7 +158,7 @@ int default_r(int fmt) {
         env = e ? atoi(e) : -1;
     }
     if (env == 1 || env == 2 || env == 4 || env == 8) return env;
-    return fmt == QP_Q6_K ? 2 : 4;
+    return 2;
 }
 
 Kid gemv_kid(int fmt, int R) {
@@ -498,7 +498,9 @@ int op_dec_attn(const Ctx& c) {
     a.rows = c.U(11);
     if (!a.rows) return fail(QP_E_ARG, "dec_attn: P.rows (cache slots) is 0");
     if (a.hd != 64 && a.hd != 128) return fail(QP_E_ARG, "dec_attn: head_dim %u", a.hd);
-    if (!a.nkv || a.nh % a.nkv || a.nh / a.nkv > 8) return fail(QP_E_ARG, "dec_attn: nh=%u nkv=%u", a.nh, a.nkv);
+    const uint32_t G0 = a.nkv ? a.nh / a.nkv : 0;
+    if (!a.nkv || a.nh % a.nkv || (G0 != 1 && G0 != 2 && G0 != 4 && G0 != 8))
+        return fail(QP_E_ARG, "dec_attn: nh=%u nkv=%u (group of 1, 2, 4 or 8 query heads)", a.nh, a.nkv);
     if (!a.nsplit || a.nsplit > 1024) return fail(QP_E_ARG, "dec_attn: nsplit=%u", a.nsplit);
     a.paso = c.B(0);
     a.q = c.B(1);
@@ -510,8 +512,8 @@ int op_dec_attn(const Ctx& c) {
     a.knorm = c.B(7);
     a.part_o = c.B(8);
     a.part_ml = c.B(9);
-    const uint32_t G = a.nh / a.nkv, tk = 32;
-    const uint32_t lds = 4 * (G * a.hd + tk * (a.hd + 1) + tk * a.hd + G * tk + 2 * a.hd + G);
+    const uint32_t tk = 32;  // LDS: q [8][hd] | K tile [32][hd+4] | V tile [32][hd] | p [8][32] | k, v [hd] | corr [8]
+    const uint32_t lds = 4 * (8 * a.hd + tk * (a.hd + 4) + tk * a.hd + 8 * tk + 2 * a.hd + 8);
     return launch(a.hd == 64 ? K_dec_attn_hd64 : K_dec_attn_hd128, a.nkv, a.nsplit, 1, 256, lds, a);
 }
 
@@ -526,7 +528,8 @@ int op_dec_attn_comb(const Ctx& c) {
     a.part_o = c.B(1);
     a.part_ml = c.B(2);
     a.o = c.B(3);
-    if (a.hd > 256) return fail(QP_E_ARG, "dec_attn_comb: hd=%u", a.hd);
+    if (a.hd != 64 && a.hd != 128) return fail(QP_E_ARG, "dec_attn_comb: hd=%u", a.hd);
+    if (a.nsplit == 0 || a.nsplit > 1024) return fail(QP_E_ARG, "dec_attn_comb: nsplit=%u", a.nsplit);
     return launch(K_dec_attn_comb, a.nh, 1, 1, 256, 0, a);
 }
 

@@ -68,21 +68,16 @@ async function generate(o) {
   process.stdout.write(JSON.stringify(r) + '\n');
 }
 
-async function bench(o) {
-  const tLoad = Date.now();
-  const modelo = await cargar(o);
-  const loadMs = Date.now() - tLoad;
-  const ids = JSON.parse(fs.readFileSync(o['prompt-file'], 'utf8'));
-  const n = parseInt(o.n || '256', 10);
-  const warm = parseInt(o.warmup || '8', 10);
+// One decode measurement after prefilling the first P ids: warm-up steps (then the position is rewound; the KV
+// slots they wrote are overwritten by the timed run), then n timed steps.
+async function medir(modelo, ids, P, n, warm, eager) {
   const gpu = modelo.gpu;
   const tp0 = Date.now();
-  const logits = await engine.prefill(modelo, ids);
+  const logits = await engine.prefill(modelo, ids.slice(0, P));
   gpu.sincronizar();
   const prefillMs = Date.now() - tp0;
   const primero = argmax(logits);
   const pos0 = modelo.pos;
-  // warm-up steps (then rewind the position: the KV slots they wrote are overwritten by the timed run)
   if (warm > 0) {
     modelo.decodificarVoraz(primero, warm);
     gpu.sincronizar();
@@ -90,14 +85,30 @@ async function bench(o) {
   }
   const tiempos = {};
   const tw0 = process.hrtime.bigint();
-  const toks = modelo.decodificarVoraz(primero, n, { tiempos: tiempos });
+  const toks = modelo.decodificarVoraz(primero, n, { tiempos: tiempos, eager: eager });
   const wallMs = Number(process.hrtime.bigint() - tw0) / 1e6;
-  const r = {
-    decode_tok_s: n / (tiempos.ms / 1000), ms_per_token: tiempos.ms / n, device_ms: tiempos.ms, wall_ms: wallMs,
-    wall_tok_s: n / (wallMs / 1000), n: n, prompt_tokens: ids.length, prefill_ms: prefillMs,
-    prefill_tok_s: ids.length / (prefillMs / 1000), load_ms: loadMs, first_ids: toks.slice(0, 8),
-    ctx: modelo.ctx, nsplit: modelo.nsplit, kv_f16: modelo.kvF16, bytes_on_gpu: gpu.bytesUsados,
+  return {
+    prompt_tokens: P, n: n, decode_tok_s: n / (tiempos.ms / 1000), ms_per_token: tiempos.ms / n,
+    device_ms: tiempos.ms, wall_ms: wallMs, wall_tok_s: n / (wallMs / 1000), prefill_ms: prefillMs,
+    prefill_tok_s: P / (prefillMs / 1000), first_ids: [primero].concat(toks.slice(0, 7)),
   };
+}
+
+async function bench(o) {
+  const tLoad = Date.now();
+  const modelo = await cargar(o);
+  const loadMs = Date.now() - tLoad;
+  const ids = JSON.parse(fs.readFileSync(o['prompt-file'], 'utf8'));
+  const n = parseInt(o.n || '256', 10);
+  const warm = parseInt(o.warmup || '8', 10);
+  const prefills = (o.prefill ? String(o.prefill) : String(ids.length)).split(',').map(function (x) { return parseInt(x, 10); });
+  const runs = [];
+  for (const P of prefills) {
+    if (P > ids.length) throw new Error('prompt file has ' + ids.length + ' ids, ' + P + ' requested');
+    runs.push(await medir(modelo, ids, P, n, warm, !!o.eager));
+  }
+  const r = { runs: runs, load_ms: loadMs, ctx: modelo.ctx, nsplit: modelo.nsplit, kv_f16: modelo.kvF16,
+    batch: modelo.batch, bytes_on_gpu: modelo.gpu.bytesUsados };
   modelo.free();
   process.stdout.write(JSON.stringify(r) + '\n');
 }

@@ -406,7 +406,8 @@ class ModeloTransformer {
     } else if (opciones.tiempos) {
       const e0 = gpu.evento(), e1 = gpu.evento();
       gpu.marcar(e0);
-      gpu.reproducir(this.grafo, n);
+      if (opciones.eager) for (let i = 0; i < n; i++) this._ejecutar(this.planDecode);   // same ops, no graph
+      else gpu.reproducir(this.grafo, n);
       gpu.marcar(e1);
       opciones.tiempos.ms = gpu.msEntre(e0, e1);
     } else {
