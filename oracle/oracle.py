@@ -41,6 +41,8 @@ def lib():
         vp, i, f = C.c_void_p, C.c_int, C.c_float
         L.or_f16.restype = f
         L.or_f16.argtypes = [C.c_uint16]
+        L.or_f16_from.restype = C.c_uint16
+        L.or_f16_from.argtypes = [f]
         L.or_dequant.argtypes = [i, vp, C.c_int64, vp]
         L.or_matmul.argtypes = [i, vp, i, i, vp, i, vp, i, i]
         L.or_matmul_e.argtypes = [i, vp, i, i, vp, vp, i, i, vp, i]
@@ -81,6 +83,10 @@ def _f32(a):
 # ------------------------------------------------------------------------------------------------ ops
 def f16(h: int) -> float:
     return lib().or_f16(h)
+
+
+def f16_from(x: float) -> int:
+    return lib().or_f16_from(x)
 
 
 def dequant(fmt, raw, nelem):
@@ -266,7 +272,7 @@ class _Model(C.Structure):
                [(n, C.c_float) for n in ("eps", "base", "escala", "moe_scale")] + \
                [("tok_embd", C.c_void_p), ("output", C.c_void_p), ("output_norm", C.c_void_p),
                 ("f_embd", C.c_int), ("f_output", C.c_int), ("layers", C.POINTER(_Layer)), ("pos", C.c_int),
-                ("kc", C.c_void_p), ("vc", C.c_void_p)]
+                ("kc", C.c_void_p), ("vc", C.c_void_p), ("kv_f16", C.c_int)]
 
 
 ROPE_NEOX = {"qwen2", "qwen3", "qwen3moe", "phi3", "gemma", "gemma2", "gemma3", "stablelm", "olmo2"}
@@ -276,7 +282,7 @@ class Model:
     """The reference's model forward (transformer.js:252-336; MoE FFN of deepseek2.js:374-386) on the CPU,
     over a GGUF file.  Hyper-parameters are read with the reference's defaults (transformer.js:16-61)."""
 
-    def __init__(self, path, ctx=None, tiled=True, rope=None):
+    def __init__(self, path, ctx=None, tiled=True, rope=None, kv_f16=False):
         L = lib()
         assert L.or_model_sizeof() == C.sizeof(_Model) and L.or_layer_sizeof() == C.sizeof(_Layer)
         self.g = g = GGUF(path)
@@ -301,6 +307,7 @@ class Model:
         m.n_layers, m.D, m.nh, m.nkv, m.hd = self.n_layers, self.D, self.nh, self.nkv, self.hd
         m.vocab, m.nrot, m.neox, m.ctx, m.tiled = self.vocab, self.nrot, int(self.neox), self.ctx, int(tiled)
         m.eps, m.base = self.eps, self.base
+        m.kv_f16 = int(kv_f16)
         m.escala = float(np.float32(1.0 / np.sqrt(self.hd)))
         m.n_exp = self.n_exp
         m.n_used = get("expert_used_count", 0)

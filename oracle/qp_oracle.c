@@ -36,6 +36,33 @@ float or_f16(uint16_t h) {
     return s ? -v : v;
 }
 
+/* f32 -> f16, IEEE 754 round to nearest, ties to even (overflow to infinity, NaN kept quiet).  Used for the
+ * f16 KV-cache option of this backend (the reference keeps its cache in f32). */
+uint16_t or_f16_from(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds past 65504 */
+    uint32_t q, rem, half;
+    if (ax < 0x38800000u) {                                   /* below 2^-14: a multiple of 2^-24 */
+        if (ax < 0x33000000u) return (uint16_t)sign;          /* below 2^-25 */
+        const uint32_t e = ax >> 23, m = (ax & 0x7fffffu) | 0x800000u, sh = 126 - e;
+        q = m >> sh;
+        rem = m & ((1u << sh) - 1);
+        half = 1u << (sh - 1);
+    } else {
+        const uint32_t r = ax - 0x38000000u;                  /* exponent rebiased from 127 to 15 */
+        q = r >> 13;
+        rem = r & 0x1fffu;
+        half = 0x1000u;
+    }
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
+
+static inline float f16_round(float f) { return or_f16(or_f16_from(f)); }
+
 static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 static inline uint32_t rd32(const uint8_t* p) {
     return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
@@ -535,6 +562,7 @@ typedef struct {
     /* state */
     int pos;
     float *kc, *vc; /* [L][ctx][kvd] */
+    int kv_f16;     /* option of this backend: cache rows rounded to f16 when written (reference: f32 only) */
 } OrModel;
 
 OrModel* or_model_new(void) { return (OrModel*)calloc(1, sizeof(OrModel)); }
@@ -600,6 +628,11 @@ int or_model_forward(OrModel* m, const uint32_t* ids, int T, float* logits) {
         or_norm_rope(k, (const float*)L->k_norm, T, nkv, hd, L->k_norm != NULL, m->neox, m->eps, m->base, m->nrot,
                      1.0f, m->pos);
         or_kv_write(k, v, kc, vc, T, kvd, m->pos, 0);
+        if (m->kv_f16)
+            for (size_t i = (size_t)m->pos * kvd; i < (size_t)(m->pos + T) * kvd; i++) {
+                kc[i] = f16_round(kc[i]);
+                vc[i] = f16_round(vc[i]);
+            }
         or_attention(q, kc, vc, att, T, m->pos, nh, nkv, hd, m->escala, 0, 0);
         mm(m, L->fo, L->wo, D, qd, att, T, x, 1);
         or_rmsnorm(x, (const float*)L->ffn_norm, xn, T, D, m->eps, 0);

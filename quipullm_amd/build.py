@@ -77,7 +77,7 @@ def build_napi():
 
 def build_oracle():
     """The CPU checker (test infrastructure; not part of the product)."""
-    _run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], "oracle")
+    _run(["make", "-s", "-B", "-C", os.path.join(ROOT, "oracle")], "oracle")
 
 
 def build_all(oracle=True):

@@ -1094,7 +1094,8 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
 KERNEL __launch_bounds__(256) void qp_dec_attn_hd64(QpDecAttnArgs a) { attn_dec_body<64>(a); }
 KERNEL __launch_bounds__(256) void qp_dec_attn_hd128(QpDecAttnArgs a) { attn_dec_body<128>(a); }
 
-// Merge of the split partials: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), splits with l = 0 skipped.
+// Merge of the split partials: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), splits with l = 0 skipped
+// (all of them empty, for a position past the cache: o = 0).
 // grid nh; the per-split weights are computed in parallel, then each output element sums its splits with
 // independent loads.
 KERNEL __launch_bounds__(256) void qp_dec_attn_comb(QpDecCombArgs a) {
@@ -1136,7 +1137,7 @@ KERNEL __launch_bounds__(256) void qp_dec_attn_comb(QpDecCombArgs a) {
     if (tid < a.hd) {
         float t = 0.0f;
         for (uint32_t i = 0; i < P; i++) t += part[i * a.hd + tid];
-        gstore<float>(a.o + 4ull * ((uint64_t)h * a.hd + tid), t / L);
+        gstore<float>(a.o + 4ull * ((uint64_t)h * a.hd + tid), L > 0.0f ? t / L : 0.0f);  // no key: zeros
     }
 }
 

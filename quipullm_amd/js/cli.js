@@ -1,14 +1,16 @@
 'use strict';
 // Command-line driver of the engine, for tests and the benchmark.
 //
-//   node cli.js generate --model M.gguf --prompt-file ids.json --n 128 [--mode fast|ref] [--kv f16|f32]
+//   node cli.js generate --model M.gguf --prompt-file ids.json --n 128 [--mode fast|ref|engine] [--kv f16|f32]
 //                        [--ctx N] [--batch N] [--no-tiled] [--logits-out file.f32]
+//                        [--repeat-penalty R] [--frequency-penalty F] [--presence-penalty P] [--host-loop]
 //   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
 //                        [--warmup W]
 //
 // generate prints one JSON line {ids, prompt_ms, decode_ms, tps}; with --logits-out the logits each token was
 // chosen from are appended to the file as float32 (vocab floats per token).  mode "ref" runs the reference op
-// sequence with a host argmax per token; "fast" runs the captured one-token graph with the device argmax.
+// sequence with a host argmax per token; "fast" runs the captured one-token graph with the device argmax;
+// "engine" runs engine.generar with the given sampler parameters (no logits file).
 // bench prefills the prompt, then times n decode steps (device events around the graph replays, and the wall
 // clock) and prints {decode_tok_s, ms_per_token, ...}.
 const fs = require('fs');
@@ -44,7 +46,16 @@ async function generate(o) {
   const logits = await engine.prefill(modelo, ids);
   const tPrompt = Date.now();
   const toks = [];
-  if (o.mode === 'ref') {
+  if (o.mode === 'engine') {
+    // the engine's generation loop with sampler parameters (penalties -> host loop, greedy -> device loop)
+    const params = { temperature: 0, max_tokens: n, host_loop: !!o['host-loop'] };
+    for (const k of ['repeat_penalty', 'frequency_penalty', 'presence_penalty']) {
+      const v = o[k.replace(/_/g, '-')];
+      if (v !== undefined) params[k] = parseFloat(v);
+    }
+    const r = await engine.generar(modelo, ids, params);
+    for (const t of r.ids) toks.push(t);
+  } else if (o.mode === 'ref') {
     let lg = logits;
     while (toks.length < n) {
       escribe(lg);

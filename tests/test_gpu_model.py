@@ -1,0 +1,142 @@
+"""End-to-end parity of the token loop on the GPU: the JavaScript engine (Node.js over the N-API addon) generates
+greedily from seeded synthetic GGUF files and is compared with the CPU oracle on the same files.
+
+Bars: the greedy ids are identical for every generated token, and the logits each token was chosen from
+agree within 1e-3 relative (max |a - b| / max |b|).  Modes: "ref" is the reference op sequence (one op per
+reference shader, host argmax), "fast" the captured one-token graph with fused kernels and the device argmax,
+"engine" the engine's generation loop.  KV cache in f32 (the reference's) and f16 (checked against the oracle
+with the same f16 rounding of the cache).
+
+Node is started through the spawner of conftest.py, never from this (GPU-using) process.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, run
+from quipullm_amd import build, synth
+
+pytestmark = pytest.mark.gpu
+
+CLI = os.path.join(ROOT, "quipullm_amd", "js", "cli.js")
+
+MINI = ["mini_llama_q4km_c", "mini_llama_q8_c", "mini_qwen3_q4km_c", "mini_qwen3moe_q4k_c", "mini_llama_q4km",
+        "mini_qwen3moe_q4k"]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def native():
+    if not build.built() or not os.path.exists(build.NAPI):
+        pytest.fail("native parts not built: run __graft_entry__.build() first")
+
+
+def rel(a, b):
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def generate(path, prompt, n, mode, kv, tmp, extra=()):
+    pf = os.path.join(tmp, "prompt.json")
+    lf = os.path.join(tmp, "logits.f32")
+    with open(pf, "w") as f:
+        json.dump([int(t) for t in prompt], f)
+    if os.path.exists(lf):
+        os.remove(lf)
+    cmd = ["timeout", "-k", "5", "110", "node", CLI, "generate", "--model", path, "--prompt-file", pf, "--n", str(n),
+           "--mode", mode, "--kv", kv, "--ctx", "256"] + (["--logits-out", lf] if mode != "engine" else []) + \
+        list(extra)
+    print("node generate", os.path.basename(path), mode, kv, flush=True)
+    rc, out, err = run(cmd, timeout=120)
+    assert rc == 0, err[-3000:]
+    r = json.loads(out.strip().splitlines()[-1])
+    lg = np.fromfile(lf, np.float32) if mode != "engine" else None
+    return r, lg
+
+
+def oracle_run(oracle, path, prompt, n, kv_f16):
+    m = oracle.Model(path, ctx=256, kv_f16=kv_f16)
+    ids, lgs = m.generate(prompt, n)
+    m.close()
+    return ids, lgs
+
+
+@pytest.mark.parametrize("name", MINI)
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_greedy_matches_oracle(oracle, models_dir, tmp_path, name, kv):
+    path = synth.ensure_model(name, models_dir)
+    vocab = oracle.GGUF(path).tensors["token_embd.weight"]["dims"][1]
+    prompt = synth.random_prompt(vocab, 40, 1)
+    n = 24
+    want_ids, want_lg = oracle_run(oracle, path, prompt, n, kv == "f16")
+    for mode in ("ref", "fast"):
+        r, lg = generate(path, prompt, n, mode, kv, str(tmp_path))
+        lg = lg.reshape(-1, vocab)
+        assert len(lg) == n
+        errs = [rel(a, b) for a, b in zip(lg, want_lg)]
+        assert r["ids"] == want_ids, (mode, r["ids"], want_ids, errs)
+        assert max(errs) < 1e-3, (mode, errs)
+        assert r["pos"] == len(prompt) + n - 1
+
+
+def test_tiny_q8_config(oracle, models_dir, tmp_path):
+    """The reference's CPU-runnable case: 8 layers, hidden 1024, 16 x 64 MHA, FFN 2816, vocab 32000, Q8_0; a
+    32-token random prompt, then 128 greedy tokens, batch 1."""
+    path = synth.ensure_model("tiny_q8", models_dir)
+    prompt = synth.random_prompt(32000, 32, 2)
+    want_ids, want_lg = oracle_run(oracle, path, prompt, 128, False)
+    r, lg = generate(path, prompt, 128, "fast", "f32", str(tmp_path))
+    lg = lg.reshape(-1, 32000)
+    errs = [rel(a, b) for a, b in zip(lg, want_lg)]
+    assert r["ids"] == want_ids
+    assert max(errs) < 1e-3, max(errs)
+
+
+def test_engine_loop_greedy_and_penalties(oracle, models_dir, tmp_path):
+    """engine.generar: greedy on the device loop and on the host loop give the oracle's ids; with a repetition
+    penalty the host sampler (penalties over the last 64 tokens of prompt + output) is followed."""
+    path = synth.ensure_model("mini_llama_q4km_c", models_dir)
+    vocab = oracle.GGUF(path).tensors["token_embd.weight"]["dims"][1]
+    prompt = synth.random_prompt(vocab, 20, 5)
+    n = 16
+    want_ids, _ = oracle_run(oracle, path, prompt, n, False)
+    for extra in ((), ("--host-loop",)):
+        r, _ = generate(path, prompt, n, "engine", "f32", str(tmp_path), extra)
+        assert r["ids"] == want_ids, extra
+    # penalties: restated on the oracle's logits (sampling.js:25-42 of the reference)
+    rp, fp, pp = 1.3, 0.2, 0.1
+    m = oracle.Model(path, ctx=256)
+    hist = list(prompt)
+    lg = None
+    for i in range(0, len(prompt), 32):
+        lg = m.forward(prompt[i:i + 32], i + 32 >= len(prompt))
+    out = []
+    while len(out) < n:
+        lg = lg.copy()
+        counts = {}
+        for t in hist[-64:]:
+            counts[t] = counts.get(t, 0) + 1
+        for t, c in counts.items():
+            v = lg[t]
+            v = v / rp if v > 0 else v * rp
+            lg[t] = v - (c * fp + pp)
+        t = oracle.argmax(lg)
+        out.append(t)
+        hist.append(t)
+        if len(out) < n:
+            lg = m.forward([t], True)
+    m.close()
+    r, _ = generate(path, prompt, n, "engine", "f32", str(tmp_path),
+                    ("--repeat-penalty", str(rp), "--frequency-penalty", str(fp), "--presence-penalty", str(pp)))
+    assert r["ids"] == out
+
+
+def test_engine_rejects_bad_input(models_dir, tmp_path):
+    path = synth.ensure_model("mini_llama_q8", models_dir)
+    pf = os.path.join(str(tmp_path), "bad.json")
+    for ids in ([800], [], [5] * 300):  # id outside the vocabulary (800), empty prompt, beyond the context (256)
+        with open(pf, "w") as f:
+            json.dump(ids, f)
+        rc, out, err = run(["timeout", "-k", "5", "110", "node", CLI, "generate", "--model", path, "--prompt-file",
+                            pf, "--n", "4", "--mode", "engine", "--ctx", "256"], timeout=120)
+        assert rc == 1 and "error" in err, (ids, rc, err[-500:])

@@ -1,0 +1,527 @@
+"""Op-level parity of the gfx950 kernels against the CPU oracle, through the C ABI (ctypes).
+
+Bars: dequantization, embedding rows, KV appends and argmax are bit-exact; the dot products follow their own
+summation order on the GPU, so they are held to an absolute bound proportional to sum |x_k w_k| (float32
+rounding of a K-term sum in any order); the other float kernels to small relative bounds stated per test.
+
+Every dispatch here uses buffers sized exactly as the kernel indexes them (shapes are checked by the op table
+on the host before any launch).
+"""
+import numpy as np
+import pytest
+
+import refs
+from quipullm_amd import capi, synth
+
+pytestmark = pytest.mark.gpu
+
+FMTS = [capi.Q4_K, capi.Q6_K, capi.Q8_0, capi.F32]
+
+
+def raw_matrix(fmt, N, K, seed, centered=False):
+    if fmt == capi.F32:
+        return np.random.default_rng(seed).standard_normal(N * K).astype(np.float32).view(np.uint8)
+    return np.frombuffer(synth.gen_blocks(np.random.default_rng(seed), fmt, N * K, "w", centered), np.uint8)
+
+
+def dot_bound(W, x, rel=2e-5):
+    """Absolute error allowed for y = W x in float32: rel * sum_k |w_k x_k| per row."""
+    return rel * (np.abs(W.astype(np.float64)) @ np.abs(np.asarray(x, np.float64))) + 1e-30
+
+
+class Dev:
+    """Tracks device buffers of one test and frees them."""
+
+    def __init__(self, q):
+        self.q, self.hs = q, []
+
+    def buf(self, arr):
+        h = self.q.buffer_from(np.ascontiguousarray(arr))
+        self.hs.append(h)
+        return h
+
+    def zeros(self, nbytes):
+        h = self.q.alloc(nbytes)
+        self.q.upload(h, np.zeros(nbytes, np.uint8))
+        self.hs.append(h)
+        return h
+
+    def matrix(self, fmt, raw, N, K):
+        h = self.q.upload_matrix(fmt, raw, N, K)
+        self.hs.append(h)
+        return h
+
+    def paso(self, T, pos0):
+        return self.buf(np.array([T, pos0, 0, 0], np.uint32))
+
+    def get(self, h, shape, dtype=np.float32):
+        self.q.sync()
+        return self.q.download(h, shape, dtype)
+
+    def close(self):
+        for h in self.hs:
+            self.q.free(h)
+
+
+@pytest.fixture
+def dev(quipu):
+    d = Dev(quipu)
+    yield d
+    d.close()
+
+
+def test_info(quipu):
+    i = quipu.info()
+    assert i["arch"].startswith("gfx950") and i["cus"] >= 200
+
+
+# ------------------------------------------------------------------------------------------------ dequant / embed
+@pytest.mark.parametrize("fmt", [capi.Q4_K, capi.Q6_K, capi.Q8_0])
+@pytest.mark.parametrize("centered", [False, True])
+def test_dequant_bit_exact(quipu, dev, oracle, fmt, centered):
+    N, K = 96, 1024
+    raw = raw_matrix(fmt, N, K, 11, centered)
+    h = dev.matrix(fmt, raw, N, K)
+    got = quipu.dequant(fmt, h, N * K)
+    want = oracle.dequant(fmt, raw, N * K)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_embed_rows_bit_exact(quipu, dev, oracle, fmt):
+    V, D = 300, 512
+    raw = raw_matrix(fmt, V, D, 12)
+    w = dev.matrix(fmt, raw, V, D)
+    ids = np.array([0, 299, 17, 17, 150], np.uint32)
+    T = len(ids)
+    y = dev.zeros(T * D * 4)
+    nm = "embed_" + capi.FMT_NAME[fmt]
+    wb = [w, w + V * D] if fmt == capi.Q8_0 else [w]
+    quipu.dispatch(nm, [("u", D), ("u", V)], [dev.paso(T, 0)] + wb + [dev.buf(ids), y], ((T * D + 255) // 256,))
+    got = dev.get(y, (T, D))
+    np.testing.assert_array_equal(got.view(np.uint32), oracle.embed(fmt, raw, D, ids).view(np.uint32))
+
+
+# ------------------------------------------------------------------------------------------------ GEMV
+@pytest.mark.parametrize("fmt,N,K", [(capi.Q4_K, 1000, 4096), (capi.Q6_K, 513, 2048), (capi.Q8_0, 700, 1536),
+                                     (capi.F32, 130, 1024), (capi.Q4_K, 64, 14336), (capi.Q6_K, 40, 14336)])
+def test_matmul_1_reference_op(quipu, dev, oracle, fmt, N, K):
+    raw = raw_matrix(fmt, N, K, 13)
+    w = dev.matrix(fmt, raw, N, K)
+    x = np.random.default_rng(1).standard_normal(K).astype(np.float32)
+    y0 = np.random.default_rng(2).standard_normal(N).astype(np.float32)
+    W = oracle.dequant(fmt, raw, N * K).reshape(N, K) if fmt != capi.F32 else raw.view(np.float32).reshape(N, K)
+    wb = [w, w + N * K] if fmt == capi.Q8_0 else [w]
+    for acc in (0, 1):
+        y = dev.buf(y0)
+        quipu.dispatch("matmul_%s_1" % capi.FMT_NAME[fmt], [("u", N), ("u", K), ("u", acc), ("u", 0)],
+                       [dev.paso(1, 0)] + wb + [dev.buf(x), y], capi.dim2((N + 7) // 8))
+        got = dev.get(y, (N,))
+        want = oracle.matmul(fmt, raw, N, K, x, y=y0 if acc else None, acc=bool(acc))[0]
+        assert np.all(np.abs(got - want) <= dot_bound(W, x) + (2e-7 * np.abs(y0) if acc else 0)), acc
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("R", [1, 2, 4, 8])
+def test_gemv_segments_norm_and_persistent_grid(quipu, dev, oracle, fmt, R):
+    """Three segments (like Q, K, V) over one RMS-normalized input, the middle one a row window of a larger
+    matrix; the grid capped at 5 workgroups so each strides over many row groups."""
+    K = 2048
+    shapes = [(260, 0, 260), (72, 40, 150), (33, 0, 33)]  # (n, row_base, rows_total)
+    x = (np.random.default_rng(3).standard_normal(K) * 2).astype(np.float32)
+    nw = (1 + 0.2 * np.random.default_rng(4).standard_normal(K)).astype(np.float32)
+    eps = 1e-5
+    xn = oracle.rmsnorm(x[None], nw, eps)[0]
+    segs, bufs, want, bounds, outs = [], [], [], [], []
+    for i, (n, rb, rt) in enumerate(shapes):
+        raw = raw_matrix(fmt, rt, K, 20 + i)
+        W = (oracle.dequant(fmt, raw, rt * K) if fmt != capi.F32 else raw.view(np.float32)).reshape(rt, K)
+        h = dev.matrix(fmt, raw, rt, K)
+        y = dev.zeros(n * 4)
+        segs.append((capi.STORE, n, rb, rt))
+        bufs += [h, 0, y]
+        want.append(oracle.matmul(fmt, raw, rt, K, xn)[0][rb:rb + n])
+        bounds.append(dot_bound(W[rb:rb + n], xn, 3e-5))
+        outs.append((y, n))
+    u = capi.gemv_uniform(3, K, eps=eps, R=R, max_wg=5, fmt=fmt, segs=segs)
+    quipu.dispatch("gemv", u, [dev.paso(1, 0), dev.buf(x), dev.buf(nw), 0] + bufs)
+    for (y, n), w_, b in zip(outs, want, bounds):
+        got = dev.get(y, (n,))
+        assert np.all(np.abs(got - w_) <= b)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_gemv_acc_last_row(quipu, dev, oracle, fmt):
+    """ACC mode (the residual add of wo / ffn_down) reading the last of T = 3 input rows."""
+    N, K, T = 300, 1024, 3
+    raw = raw_matrix(fmt, N, K, 30)
+    W = (oracle.dequant(fmt, raw, N * K) if fmt != capi.F32 else raw.view(np.float32)).reshape(N, K)
+    x = np.random.default_rng(5).standard_normal((T, K)).astype(np.float32)
+    y0 = np.random.default_rng(6).standard_normal(N).astype(np.float32)
+    y = dev.buf(y0)
+    u = capi.gemv_uniform(1, K, last_row=1, fmt=fmt, segs=[(capi.ACC, N, 0, N)])
+    quipu.dispatch("gemv", u, [dev.paso(T, 0), dev.buf(x), 0, 0, dev.matrix(fmt, raw, N, K), 0, y])
+    got = dev.get(y, (N,))
+    want = oracle.matmul(fmt, raw, N, K, x[-1], y=y0, acc=True)[0]
+    assert np.all(np.abs(got - want) <= dot_bound(W, x[-1]) + 2e-7 * np.abs(y0))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("R", [2, 4, 8])
+def test_gemv_swiglu_pairs(quipu, dev, oracle, fmt, R):
+    N, K = 333, 1024
+    rg, ru = raw_matrix(fmt, N, K, 40), raw_matrix(fmt, N, K, 41)
+    Wg = (oracle.dequant(fmt, rg, N * K) if fmt != capi.F32 else rg.view(np.float32)).reshape(N, K)
+    Wu = (oracle.dequant(fmt, ru, N * K) if fmt != capi.F32 else ru.view(np.float32)).reshape(N, K)
+    x = np.random.default_rng(7).standard_normal(K).astype(np.float32)
+    y = dev.zeros(N * 4)
+    u = capi.gemv_uniform(1, K, R=R, fmt=fmt, segs=[(capi.SWIGLU, N, 0, N)])
+    quipu.dispatch("gemv", u, [dev.paso(1, 0), dev.buf(x), 0, 0, dev.matrix(fmt, rg, N, K),
+                               dev.matrix(fmt, ru, N, K), y])
+    got = dev.get(y, (N,))
+    g, uu = oracle.matmul(fmt, rg, N, K, x)[0], oracle.matmul(fmt, ru, N, K, x)[0]
+    want = oracle.swiglu(g, uu)
+    silu = np.abs(g / (1 + np.exp(-g.astype(np.float64))))
+    bound = 1.1 * np.abs(uu) * dot_bound(Wg, x) + silu * dot_bound(Wu, x) + 1e-6 * np.abs(want)
+    assert np.all(np.abs(got - want) <= bound)
+
+
+@pytest.mark.parametrize("fmt", [capi.Q6_K, capi.Q4_K, capi.Q8_0])
+def test_gemv_argmax_fused(quipu, dev, oracle, fmt):
+    """Output GEMV with the fused device argmax: partial maxima per workgroup, then argmax_fin.  Rows 7 and 900
+    are copies of the largest row, so the greedy choice is the lowest index holding that value (strict '>'
+    scan)."""
+    V, K, maxwg = 1200, 1024, 37
+    raw = bytearray(raw_matrix(fmt, V, K, 50).tobytes())
+    x = np.random.default_rng(8).standard_normal(K).astype(np.float32)
+    W = oracle.dequant(fmt, bytes(raw), V * K).reshape(V, K)
+    best = int(np.argmax(W @ x))
+    rb = capi.device_bytes(fmt, 1, K)
+    for dst in (7, 900):
+        raw[dst * rb:(dst + 1) * rb] = raw[best * rb:(best + 1) * rb]
+    raw = np.frombuffer(bytes(raw), np.uint8)
+    W = oracle.dequant(fmt, raw, V * K).reshape(V, K)
+    y = dev.zeros(V * 4)
+    amax = dev.zeros(8 * maxwg)
+    ids = dev.zeros(16)
+    toks = dev.zeros(4 * 8)
+    step = dev.zeros(16)
+    paso = dev.paso(1, 5)
+    u = capi.gemv_uniform(1, K, R=2, max_wg=maxwg, fmt=fmt, segs=[(capi.ARGMAX, V, 0, V)])
+    fin = [("u", maxwg), ("u", 1), ("u", 8)]
+    quipu.dispatch("gemv", u, [paso, dev.buf(x), 0, amax, dev.matrix(fmt, raw, V, K), 0, y])
+    quipu.dispatch("argmax_fin", fin, [paso, amax, ids, toks, step])
+    logits = dev.get(y, (V,))
+    top = min(best, 7)
+    assert int(dev.get(ids, (1,), np.uint32)[0]) == top == oracle.argmax(logits)
+    assert dev.get(amax, (maxwg,), np.uint64).sum() == 0  # partials cleared for the next launch
+    assert list(dev.get(step, (1,), np.uint32)) == [1] and list(dev.get(paso, (2,), np.uint32)) == [1, 6]
+    assert dev.get(toks, (1,), np.uint32)[0] == top
+    want = oracle.matmul(fmt, raw, V, K, x)[0]
+    assert np.all(np.abs(logits - want) <= dot_bound(W, x))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T,op", [(3, "4"), (9, "4"), (40, "t"), (70, "t")])
+def test_matmul_multi_token(quipu, dev, oracle, fmt, T, op):
+    """Prefill matmuls (matmul_<fmt>_4 and the tiled _t), acc on, T rows of x."""
+    N, K = 200, 1024
+    raw = raw_matrix(fmt, N, K, 60)
+    W = (oracle.dequant(fmt, raw, N * K) if fmt != capi.F32 else raw.view(np.float32)).reshape(N, K)
+    x = np.random.default_rng(9).standard_normal((T, K)).astype(np.float32)
+    y0 = np.random.default_rng(10).standard_normal((T, N)).astype(np.float32)
+    y = dev.buf(y0)
+    wb = [dev.matrix(fmt, raw, N, K)]
+    if fmt == capi.Q8_0:
+        wb.append(wb[0] + N * K)
+    grid = ((N + 63) // 64, 1, (T + 31) // 32) if op == "t" else capi.dim2((N + 7) // 8) + ((T + 3) // 4,)
+    quipu.dispatch("matmul_%s_%s" % (capi.FMT_NAME[fmt], op), [("u", N), ("u", K), ("u", 1), ("u", 0)],
+                   [dev.paso(T, 0)] + wb + [dev.buf(x), y], grid)
+    got = dev.get(y, (T, N))
+    want = oracle.matmul(fmt, raw, N, K, x, T, y=y0, acc=True, mode=1)
+    for t in range(T):
+        assert np.all(np.abs(got[t] - want[t]) <= dot_bound(W, x[t]) + 2e-7 * np.abs(y0[t])), t
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_matmul_expert_jobs(quipu, dev, oracle, fmt):
+    """matmul_<fmt>_e (one job per selected expert) and the fused gate/up _e_swiglu; tfijo = k routes job z to
+    input row z / k."""
+    E, N, K, k, T = 6, 96, 512, 2, 2
+    rg, ru = raw_matrix(fmt, E * N, K, 70), raw_matrix(fmt, E * N, K, 71)
+    Wg = (oracle.dequant(fmt, rg, E * N * K) if fmt != capi.F32 else rg.view(np.float32)).reshape(E, N, K)
+    x = np.random.default_rng(11).standard_normal((T, K)).astype(np.float32)
+    sel = np.array([4, 1, 0, 5], np.uint32)
+    hg, hu = dev.matrix(fmt, rg, E * N, K), dev.matrix(fmt, ru, E * N, K)
+    y = dev.zeros(T * k * N * 4)
+    u = [("u", N), ("u", K), ("u", 0), ("u", k), ("u", E)]
+    wb = [hg, hg + E * N * K] if fmt == capi.Q8_0 else [hg]
+    xb, sb, pb = dev.buf(x), dev.buf(sel), dev.paso(T, 0)
+    quipu.dispatch("matmul_%s_e" % capi.FMT_NAME[fmt], u, [pb] + wb + [xb, y, sb], (1, 1, T * k))
+    got = dev.get(y, (T * k, N))
+    want = oracle.matmul_e(fmt, rg, N, K, x, sel, k)
+    for z in range(T * k):
+        assert np.all(np.abs(got[z] - want[z]) <= dot_bound(Wg[sel[z]], x[z // k])), z
+    y2 = dev.zeros(T * k * N * 4)
+    quipu.dispatch("matmul_%s_e_swiglu" % capi.FMT_NAME[fmt], u, [pb] + wb + [hu, xb, y2, sb], (1, 1, T * k))
+    got2 = dev.get(y2, (T * k, N))
+    want2 = oracle.swiglu(want, oracle.matmul_e(fmt, ru, N, K, x, sel, k))
+    np.testing.assert_allclose(got2, want2, rtol=1e-4, atol=1e-4 * np.abs(want2).max())
+
+
+# ------------------------------------------------------------------------------------------------ elementwise
+def test_rmsnorm(quipu, dev, oracle):
+    T, D = 5, 4096
+    x = (np.random.default_rng(12).standard_normal((T, D)) * 3).astype(np.float32)
+    w = np.random.default_rng(13).standard_normal(D).astype(np.float32)
+    for ultima in (0, 1):
+        y = dev.zeros(T * D * 4)
+        quipu.dispatch("rmsnorm", [("u", D), ("u", ultima), ("f", 1e-5), ("u", 0)],
+                       [dev.paso(T, 0), dev.buf(x), dev.buf(w), y], (T,))
+        got = dev.get(y, (1 if ultima else T, D))
+        np.testing.assert_allclose(got, oracle.rmsnorm(x, w, 1e-5, ultima=bool(ultima)), rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("hd,neox,use_norm", [(128, 0, 0), (128, 1, 1), (64, 1, 0), (64, 0, 1)])
+def test_norm_rope(quipu, dev, oracle, hd, neox, use_norm):
+    nh, T, pos0 = 8, 3, 1000
+    v = np.random.default_rng(14).standard_normal((T, nh, hd)).astype(np.float32)
+    w = (1 + 0.1 * np.random.default_rng(15).standard_normal(hd)).astype(np.float32)
+    vb = dev.buf(v)
+    quipu.dispatch("norm_rope", [("u", hd), ("u", nh), ("u", use_norm), ("u", neox), ("f", 1e-6), ("f", 5e5),
+                                 ("u", hd), ("u", 0)], [dev.paso(T, pos0), vb, dev.buf(w)], (nh, T))
+    got = dev.get(vb, (T * nh * hd,))
+    want = oracle.norm_rope(v, w, nh, hd, use_norm, neox, 1e-6, 5e5, hd, pos0)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("f16", [0, 1])
+def test_kv_write(quipu, dev, oracle, f16):
+    kvd, rows, T, pos0 = 256, 20, 4, 15
+    k = np.random.default_rng(16).standard_normal((T, kvd)).astype(np.float32)
+    v = np.random.default_rng(17).standard_normal((T, kvd)).astype(np.float32)
+    es = 2 if f16 else 4
+    kc, vc = dev.zeros(rows * kvd * es), dev.zeros(rows * kvd * es)
+    quipu.dispatch("kv_write", [("u", kvd), ("u", 0), ("u", f16), ("u", rows)],
+                   [dev.paso(T, pos0), dev.buf(k), dev.buf(v), kc, vc], ((T * kvd + 255) // 256,))
+    dt = np.float16 if f16 else np.float32
+    gk, gv = dev.get(kc, (rows, kvd), dt), dev.get(vc, (rows, kvd), dt)
+    # rows 15..18 written (f16: round to nearest even), everything else untouched
+    np.testing.assert_array_equal(gk[pos0:pos0 + T], k.astype(dt))
+    np.testing.assert_array_equal(gv[pos0:pos0 + T], v.astype(dt))
+    assert not gk[:pos0].any() and not gk[pos0 + T:].any()
+
+
+def test_kv_write_past_the_cache_writes_nothing(quipu, dev):
+    kvd, rows = 64, 4
+    kc, vc = dev.zeros(rows * kvd * 4), dev.zeros(rows * kvd * 4)
+    k = np.ones((2, kvd), np.float32)
+    quipu.dispatch("kv_write", [("u", kvd), ("u", 0), ("u", 0), ("u", rows)],
+                   [dev.paso(2, 3), dev.buf(k), dev.buf(k), kc, vc], (1,))
+    gk = dev.get(kc, (rows, kvd))
+    assert gk[3].all() and not gk[:3].any()  # slot 4 is past the cache: skipped
+
+
+def test_swiglu_moe_ops(quipu, dev, oracle):
+    rng = np.random.default_rng(18)
+    T, F = 2, 3000
+    g = (rng.standard_normal(T * F) * 4).astype(np.float32)
+    uu = rng.standard_normal(T * F).astype(np.float32)
+    gb = dev.buf(g)
+    quipu.dispatch("swiglu", [("u", F)], [dev.paso(T, 0), gb, dev.buf(uu)], ((T * F + 255) // 256,))
+    np.testing.assert_allclose(dev.get(gb, (T * F,)), oracle.swiglu(g, uu), rtol=2e-6, atol=1e-7)
+    # routing: E = 128, k = 8, with normalization and an exact tie at the top of token 1
+    E, k = 128, 8
+    lg = rng.standard_normal((3, E)).astype(np.float32)
+    lg[1, 9] = lg[1, 100] = 5.0
+    for norm, scale in ((1, 1.0), (0, 2.5)):
+        sel, wts = dev.zeros(3 * k * 4), dev.zeros(3 * k * 4)
+        quipu.dispatch("moe_topk", [("u", E), ("u", k), ("u", norm), ("f", scale)],
+                       [dev.paso(3, 0), dev.buf(lg), sel, wts], (1,))
+        s_want, w_want = oracle.moe_topk(lg, E, k, norm, scale)
+        np.testing.assert_array_equal(dev.get(sel, (3 * k,), np.uint32), s_want)
+        np.testing.assert_allclose(dev.get(wts, (3 * k,)), w_want, rtol=2e-6, atol=1e-7)
+        assert list(s_want[k:k + 2]) == [9, 100]
+    D = 1000
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    de = rng.standard_normal((T * k, D)).astype(np.float32)
+    wts = rng.random(T * k).astype(np.float32)
+    xb = dev.buf(x)
+    quipu.dispatch("moe_comb", [("u", D), ("u", k)], [dev.paso(T, 0), xb, dev.buf(de), dev.buf(wts)],
+                   ((T * D + 255) // 256,))
+    np.testing.assert_allclose(dev.get(xb, (T, D)), oracle.moe_comb(x, de, wts, D, k).reshape(T, D),
+                               rtol=1e-6, atol=1e-6)
+
+
+def test_argmax_ties_nan_negative(quipu, dev, oracle):
+    for v in (np.array([1, 3, 3, 2], np.float32), np.array([np.nan, 0.5, np.nan, 0.25], np.float32),
+              np.array([-5, -1, -3], np.float32), np.random.default_rng(19).standard_normal(128256).astype(np.float32)):
+        out = dev.zeros(16)
+        quipu.dispatch("argmax", [("u", v.size)], [0, dev.buf(v), out])
+        assert int(dev.get(out, (1,), np.uint32)[0]) == oracle.argmax(v)
+
+
+# ------------------------------------------------------------------------------------------------ attention
+def f16r(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("hd,nh,nkv,T,pos0,f16", [(128, 32, 8, 1, 0, 0), (128, 32, 8, 9, 100, 0),
+                                                  (64, 8, 2, 33, 40, 1), (128, 16, 16, 5, 300, 1),
+                                                  (64, 16, 1, 3, 7, 0)])
+def test_atencion_prefill(quipu, dev, oracle, hd, nh, nkv, T, pos0, f16):
+    rows = 512
+    kvd = nkv * hd
+    rng = np.random.default_rng(20)
+    q = rng.standard_normal((T, nh * hd)).astype(np.float32)
+    kc = rng.standard_normal((rows, kvd)).astype(np.float32)
+    vc = rng.standard_normal((rows, kvd)).astype(np.float32)
+    if f16:
+        kc, vc = f16r(kc), f16r(vc)
+    dt = np.float16 if f16 else np.float32
+    o = dev.zeros(T * nh * hd * 4)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    quipu.dispatch("atencion", [("u", hd), ("u", nh), ("u", nkv), ("u", 0), ("f", scale), ("u", 0), ("u", 0), ("u", 0),
+                                ("u", f16), ("u", rows)],
+                   [dev.paso(T, pos0), dev.buf(q), dev.buf(kc.astype(dt)), dev.buf(vc.astype(dt)), o], (nh, T))
+    got = dev.get(o, (T, nh * hd))
+    want = oracle.attention(q, kc, vc, T, pos0, nh, nkv, hd, scale)
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
+
+
+@pytest.mark.parametrize("hd,nh,nkv,pos0,nsplit,f16,neox,qk_norm",
+                         [(128, 32, 8, 0, 4, 0, 0, 0), (128, 32, 8, 4095, 64, 1, 0, 0), (128, 32, 8, 777, 7, 0, 1, 1),
+                          (64, 16, 16, 100, 3, 1, 1, 0), (64, 8, 1, 31, 1, 0, 0, 1), (128, 16, 8, 33, 200, 0, 0, 0),
+                          (64, 32, 4, 2000, 16, 1, 0, 1)])
+def test_dec_attn_fused(quipu, dev, oracle, hd, nh, nkv, pos0, nsplit, f16, neox, qk_norm):
+    """One-token attention with the fused q/k norm + RoPE + KV append, split over the keys and merged; the
+    expected result is the reference op sequence norm_rope(q), norm_rope(k), kv_write, atencion."""
+    rows = 4100
+    kvd = nkv * hd
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(kvd).astype(np.float32)
+    v = rng.standard_normal(kvd).astype(np.float32)
+    kc = rng.standard_normal((rows, kvd)).astype(np.float32)
+    vc = rng.standard_normal((rows, kvd)).astype(np.float32)
+    if f16:
+        kc, vc = f16r(kc), f16r(vc)
+    qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    eps, base = 1e-6, 1e6
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    dt = np.float16 if f16 else np.float32
+    kcb, vcb = dev.buf(kc.astype(dt)), dev.buf(vc.astype(dt))
+    po, pml, o = dev.zeros(nh * nsplit * hd * 4), dev.zeros(nh * nsplit * 8), dev.zeros(nh * hd * 4)
+    paso = dev.paso(1, pos0)
+    u = [("u", hd), ("u", nh), ("u", nkv), ("u", nsplit), ("f", scale), ("f", eps), ("f", base), ("u", 0),
+         ("u", hd), ("u", neox), ("u", f16), ("u", rows)]
+    quipu.dispatch("dec_attn", u, [paso, dev.buf(q), dev.buf(k), dev.buf(v), kcb, vcb,
+                                   dev.buf(qn) if qk_norm else 0, dev.buf(kn) if qk_norm else 0, po, pml])
+    quipu.dispatch("dec_attn_comb", [("u", hd), ("u", nh), ("u", nsplit)], [paso, po, pml, o])
+    got = dev.get(o, (nh * hd,))
+    qr = oracle.norm_rope(q, qn, nh, hd, qk_norm, neox, eps, base, hd, pos0)
+    kr = oracle.norm_rope(k, kn, nkv, hd, qk_norm, neox, eps, base, hd, pos0)
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[pos0] = f16r(kr) if f16 else kr
+    vc2[pos0] = f16r(v) if f16 else v
+    want = oracle.attention(qr, kc2, vc2, 1, pos0, nh, nkv, hd, scale)[0]
+    np.testing.assert_allclose(got, want, rtol=5e-5, atol=5e-5)
+    # the appended cache row: RoPE'd key (to within the rotation's rounding), value copied (rounded if f16)
+    gk, gv = dev.get(kcb, (rows, kvd), dt), dev.get(vcb, (rows, kvd), dt)
+    np.testing.assert_allclose(gk[pos0].astype(np.float32), kc2[pos0], rtol=1e-5, atol=2e-3 if f16 else 1e-5)
+    np.testing.assert_array_equal(gv[pos0].astype(np.float32), vc2[pos0])
+    np.testing.assert_array_equal(gv[pos0 + 1:].astype(np.float32), vc[pos0 + 1:])
+
+
+def test_dec_attn_past_the_cache_reads_and_writes_nothing(quipu, dev):
+    hd, nh, nkv, rows, nsplit = 64, 4, 2, 16, 2
+    kvd = nkv * hd
+    kc = dev.zeros(rows * kvd * 4)
+    po, pml, o = dev.zeros(nh * nsplit * hd * 4), dev.zeros(nh * nsplit * 8), dev.zeros(nh * hd * 4)
+    one = dev.buf(np.ones(nh * hd, np.float32))
+    paso = dev.paso(1, rows)
+    quipu.dispatch("dec_attn", [("u", hd), ("u", nh), ("u", nkv), ("u", nsplit), ("f", 0.125), ("f", 1e-6),
+                                ("f", 1e4), ("u", 0), ("u", hd), ("u", 0), ("u", 0), ("u", rows)],
+                   [paso, one, one, one, kc, kc, 0, 0, po, pml])
+    quipu.dispatch("dec_attn_comb", [("u", hd), ("u", nh), ("u", nsplit)], [paso, po, pml, o])
+    assert not dev.get(kc, (rows * kvd,)).any()
+    assert not dev.get(o, (nh * hd,)).any()
+
+
+# ------------------------------------------------------------------------------------------------ graphs
+def test_graph_replay_matches_eager(quipu, dev, oracle):
+    """A captured decode-like step (fused-norm GEMV + argmax with position advance) replayed 5 times with host
+    reads between the replays; each replay must reproduce the eager result and advance the position."""
+    V, K, maxwg = 800, 1024, 64
+    raw = raw_matrix(capi.Q4_K, V, K, 80)
+    x = np.random.default_rng(22).standard_normal(K).astype(np.float32)
+    nw = np.ones(K, np.float32)
+    w = dev.matrix(capi.Q4_K, raw, V, K)
+    y, amax, ids, step = dev.zeros(V * 4), dev.zeros(8 * maxwg), dev.zeros(16), dev.zeros(16)
+    toks = dev.zeros(4 * 16)
+    paso = dev.paso(1, 0)
+    xb, nb = dev.buf(x), dev.buf(nw)
+    u = capi.gemv_uniform(1, K, eps=1e-5, R=4, max_wg=maxwg, fmt=capi.Q4_K, segs=[(capi.ARGMAX, V, 0, V)])
+
+    def step_ops():
+        quipu.dispatch("gemv", u, [paso, xb, nb, amax, w, 0, y])
+        quipu.dispatch("argmax_fin", [("u", maxwg), ("u", 1), ("u", 16)], [paso, amax, ids, toks, step])
+
+    step_ops()
+    eager_y = dev.get(y, (V,)).copy()
+    eager_id = int(dev.get(ids, (1,), np.uint32)[0])
+    assert eager_id == oracle.argmax(eager_y)
+    quipu.sync()
+    quipu.graph_begin()
+    step_ops()
+    g = quipu.graph_end()
+    try:
+        for r in range(5):
+            quipu.upload(y, np.zeros(V, np.float32))
+            quipu.graph_launch(g)
+            np.testing.assert_array_equal(dev.get(y, (V,)), eager_y)
+            assert int(dev.get(ids, (1,), np.uint32)[0]) == eager_id
+            assert list(dev.get(paso, (2,), np.uint32)) == [1, 2 + r]
+        assert list(dev.get(toks, (6,), np.uint32)) == [eager_id] * 6
+    finally:
+        quipu.graph_free(g)
+
+
+# ------------------------------------------------------------------------------------------------ errors
+def test_host_checks_reject_bad_dispatches(quipu, dev):
+    """Shapes and bindings the kernels cannot take are refused on the host, before any launch."""
+    x = dev.zeros(4096 * 4)
+    y = dev.zeros(4096 * 4)
+    w = dev.zeros(144 * 16)
+    p = dev.paso(1, 0)
+    bad = [
+        ("gemv", capi.gemv_uniform(0, 256, segs=[]), [p, x, 0, 0]),
+        ("gemv", capi.gemv_uniform(1, 256, R=3, segs=[(capi.STORE, 16, 0, 16)]), [p, x, 0, 0, w, 0, y]),
+        ("gemv", capi.gemv_uniform(1, 300, segs=[(capi.STORE, 16, 0, 16)]), [p, x, 0, 0, w, 0, y]),
+        ("gemv", capi.gemv_uniform(1, 256, segs=[(capi.SWIGLU, 16, 0, 16)]), [p, x, 0, 0, w, 0, y]),
+        ("gemv", capi.gemv_uniform(1, 256, segs=[(capi.ARGMAX, 16, 0, 16)]), [p, x, 0, 0, w, 0, y]),
+        ("gemv", capi.gemv_uniform(1, 256, segs=[(capi.STORE, 16, 0, 16)]), [p, x, 0, 0, w]),
+        ("gemv", capi.gemv_uniform(1, 256 * 61, segs=[(capi.STORE, 1, 0, 1)]), [p, x, 0, 0, w, 0, y]),
+        ("kv_write", [("u", 64), ("u", 0), ("u", 0), ("u", 0)], [p, x, x, y, y]),
+        ("atencion", [("u", 96), ("u", 4), ("u", 2), ("u", 0), ("f", 1), ("u", 0), ("u", 0), ("u", 0), ("u", 0),
+                      ("u", 8)], [p, x, y, y, x]),
+        ("dec_attn", [("u", 128), ("u", 12), ("u", 4), ("u", 1), ("f", 1), ("f", 0), ("f", 1), ("u", 0), ("u", 128),
+                      ("u", 0), ("u", 0), ("u", 8)], [p, x, x, x, y, y, 0, 0, y, y]),
+        ("moe_topk", [("u", 2000), ("u", 8), ("u", 1), ("f", 1)], [p, x, y, y]),
+        ("matmul_q8_1", [("u", 16), ("u", 256), ("u", 0), ("u", 0)], [p, w, w + 8, x, y]),
+    ]
+    for name, u, b in bad:
+        with pytest.raises(capi.QuipuError):
+            quipu.dispatch(name, u, b)
+    quipu.sync()  # nothing was launched, the stream is healthy
+    with pytest.raises(capi.QuipuError):
+        quipu.free(12345)
+
+
+def test_allocation_accounting(quipu):
+    before = quipu.bytes_used()
+    h = quipu.alloc(1 << 20)
+    assert quipu.bytes_used() >= before + (1 << 20)
+    quipu.free(h)
+    assert quipu.bytes_used() == before

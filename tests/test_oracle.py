@@ -1,0 +1,286 @@
+"""Pins the CPU oracle (oracle/qp_oracle.c) -- the checker every GPU parity test relies on.
+
+The reference path (WGSL on WebGPU) cannot run here and commits no golden vectors for it, so each oracle function is
+checked against what fixes it independently: exact library conversions, the ggml-spec dequantizers of refs.py,
+float64 textbook formulas, closed forms and invariants.  Each check is chosen so that a plausible mistake (a dropped
+min term, a swapped nibble, a wrong RoPE pairing, a GQA off-by-one, an exp sign) fails it.
+"""
+import numpy as np
+import pytest
+
+import refs
+from quipullm_amd import synth
+
+
+def blocks(fmt, n_elem, seed=0, centered=False):
+    return np.frombuffer(synth.gen_blocks(np.random.default_rng(seed), fmt, n_elem, "w", centered), np.uint8)
+
+
+# ------------------------------------------------------------------------------------------------ formats
+def test_f16_all_values_exact(oracle):
+    h = np.arange(65536, dtype=np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    got = np.array([oracle.f16(int(x)) for x in h[::7]], np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32)[~np.isnan(got)],
+                                  ref[::7].view(np.uint32)[~np.isnan(ref[::7])])
+    assert np.array_equal(np.isnan(got), np.isnan(ref[::7]))
+
+
+def test_f16_rounding_matches_numpy(oracle):
+    # every finite f16, the midpoints between neighbours (ties to even), random floats over the whole range,
+    # the subnormal range and the overflow threshold 65520
+    h = np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = (h[:-1] + h[1:]) / 2
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([h, mids, -mids, rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 6, 20000),
+                         np.array([65504, 65519.99, 65520, 1e6, -1e9, 2.0 ** -25, 2.0 ** -24 * 1.5, 0.0, -0.0])]
+                        ).astype(np.float32)
+    got = np.array([oracle.f16_from(float(x)) for x in xs], np.uint16)
+    np.testing.assert_array_equal(got, xs.astype(np.float16).view(np.uint16))
+    assert oracle.f16_from(float("nan")) & 0x7c00 == 0x7c00 and oracle.f16_from(float("nan")) & 0x3ff
+
+
+@pytest.mark.parametrize("fmt,n", [(refs.Q4_K, 256 * 300), (refs.Q6_K, 256 * 300), (refs.Q8_0, 32 * 500)])
+@pytest.mark.parametrize("centered", [False, True])
+def test_dequant_bit_exact_vs_ggml_spec(oracle, fmt, n, centered):
+    raw = blocks(fmt, n, 1, centered)
+    got = oracle.dequant(fmt, raw, n)
+    ref = refs.dequant(fmt, raw)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_q4k_known_answer(oracle):
+    # d = 1, dmin = 0.5, scale/min of sub-block j = (j + 1, j), quant q at element e: q = e % 16
+    sc = np.arange(1, 9, dtype=np.uint8)[None]
+    mn = np.arange(0, 8, dtype=np.uint8)[None]
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.array([1.0], np.float16).view(np.uint8)
+    b[2:4] = np.array([0.5], np.float16).view(np.uint8)
+    b[4:16] = synth.pack_q4k_scales(sc, mn)[0]
+    q = np.arange(256) % 16
+    for g in range(4):  # low nibble -> sub-block 2g, high nibble -> 2g+1
+        lo, hi = q[g * 64:g * 64 + 32], q[g * 64 + 32:g * 64 + 64]
+        b[16 + g * 32:16 + g * 32 + 32] = (lo | (hi << 4)).astype(np.uint8)
+    got = oracle.dequant(refs.Q4_K, b, 256)
+    j = np.arange(256) // 32
+    np.testing.assert_array_equal(got, (j + 1) * q - 0.5 * j)
+
+
+def test_q6k_known_answer(oracle):
+    # d = 1, all scales 1: value = q - 32 with q the 6-bit quant (low 4 bits in ql, high 2 in qh)
+    q = (np.arange(256) * 7) % 64
+    b = np.zeros(210, np.uint8)
+    for n in range(2):
+        for k in range(4):
+            for l in range(32):
+                v = int(q[n * 128 + k * 32 + l])
+                lo, hi = v & 15, v >> 4
+                qli = n * 64 + (k & 1) * 32 + l
+                b[qli] |= lo << (4 * (k >> 1))
+                b[128 + n * 32 + l] |= hi << (2 * k)
+    b[192:208] = 1
+    b[208:210] = np.array([1.0], np.float16).view(np.uint8)
+    np.testing.assert_array_equal(oracle.dequant(refs.Q6_K, b, 256), q - 32.0)
+
+
+def test_q8_known_answer(oracle):
+    b = np.zeros(34, np.uint8)
+    b[0:2] = np.array([0.25], np.float16).view(np.uint8)
+    b[2:] = np.arange(-16, 16, dtype=np.int8).view(np.uint8)
+    np.testing.assert_array_equal(oracle.dequant(refs.Q8_0, b, 32), np.arange(-16, 16) * 0.25)
+
+
+# ------------------------------------------------------------------------------------------------ matmul
+@pytest.mark.parametrize("fmt,N,K", [(refs.Q4_K, 33, 512), (refs.Q6_K, 17, 768), (refs.Q8_0, 19, 320),
+                                     (refs.F32, 9, 96)])
+@pytest.mark.parametrize("T,mode", [(1, 0), (3, 0), (9, 1)])
+def test_matmul_vs_float64(oracle, fmt, N, K, T, mode):
+    rng = np.random.default_rng(5)
+    raw = blocks(fmt, N * K, 2) if fmt != refs.F32 else rng.standard_normal(N * K).astype(np.float32).view(np.uint8)
+    W = refs.dequant(fmt, raw).reshape(N, K).astype(np.float64)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    got = oracle.matmul(fmt, raw, N, K, x, T, mode=mode)
+    ref = x.astype(np.float64) @ W.T
+    bound = 2e-6 * (np.abs(x.astype(np.float64)) @ np.abs(W).T) + 1e-30
+    assert np.all(np.abs(got - ref) <= bound)
+
+
+def test_matmul_acc_onehot_zero(oracle):
+    N, K = 8, 256
+    raw = blocks(refs.Q4_K, N * K, 3)
+    W = refs.dequant(refs.Q4_K, raw).reshape(N, K)
+    e = np.zeros(K, np.float32)
+    e[37] = 1.0
+    np.testing.assert_array_equal(oracle.matmul(refs.Q4_K, raw, N, K, e)[0], W[:, 37])
+    y0 = np.arange(N, dtype=np.float32)
+    got = oracle.matmul(refs.Q4_K, raw, N, K, e, y=y0, acc=True)[0]
+    np.testing.assert_array_equal(got, y0 + W[:, 37])
+    zero = np.zeros(N * 144, np.uint8)
+    assert not np.any(oracle.matmul(refs.Q4_K, zero, N, K, np.ones(K, np.float32)))
+
+
+def test_matmul_e_selects_expert_rows(oracle):
+    E, N, K, k = 6, 8, 256, 2
+    raw = blocks(refs.Q4_K, E * N * K, 4)
+    W = refs.dequant(refs.Q4_K, raw).reshape(E, N, K).astype(np.float64)
+    x = np.random.default_rng(1).standard_normal((1, K)).astype(np.float32)
+    sel = np.array([4, 1], np.uint32)
+    got = oracle.matmul_e(refs.Q4_K, raw, N, K, x, sel, tfijo=k)
+    for z in range(k):
+        np.testing.assert_allclose(got[z], W[sel[z]] @ x[0], rtol=2e-6, atol=1e-6 * np.abs(W[sel[z]]).sum())
+
+
+# ------------------------------------------------------------------------------------------------ elementwise
+def test_rmsnorm(oracle):
+    x = np.random.default_rng(2).standard_normal((5, 1000)).astype(np.float32) * 3
+    w = np.random.default_rng(3).standard_normal(1000).astype(np.float32)
+    np.testing.assert_allclose(oracle.rmsnorm(x, w, 1e-5), refs.rmsnorm64(x, w, 1e-5), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(oracle.rmsnorm(x, w, 1e-5, ultima=True)[0], refs.rmsnorm64(x[-1], w, 1e-5),
+                               rtol=1e-6, atol=1e-6)
+
+
+def test_sincos_cody_waite_cephes(oracle):
+    for x in np.concatenate([np.linspace(-10, 10, 2001), np.linspace(-4500, 4500, 1001)]):
+        s, c = oracle.sincos2(float(np.float32(x)))
+        xf = float(np.float32(x))
+        assert abs(s - np.sin(xf)) < 2e-6 * max(1.0, abs(xf) / 1000) and abs(c - np.cos(xf)) < 2e-6 * max(1.0, abs(xf) / 1000)
+
+
+@pytest.mark.parametrize("neox", [0, 1])
+@pytest.mark.parametrize("use_norm", [0, 1])
+def test_norm_rope(oracle, neox, use_norm):
+    nh, hd, T, pos0 = 3, 64, 4, 37
+    v = np.random.default_rng(4).standard_normal((T, nh, hd)).astype(np.float32)
+    w = (1 + 0.1 * np.random.default_rng(5).standard_normal(hd)).astype(np.float32)
+    got = oracle.norm_rope(v, w, nh, hd, use_norm, neox, 1e-6, 10000.0, hd, pos0).reshape(T, nh, hd)
+    for t in range(T):
+        src = refs.rmsnorm64(v[t], w, 1e-6) if use_norm else v[t]
+        np.testing.assert_allclose(got[t], refs.rope64(src, pos0 + t, 10000.0, hd, neox), rtol=2e-5, atol=2e-5)
+    # position 0 without the norm is the identity; the rotation preserves each pair's norm
+    np.testing.assert_array_equal(oracle.norm_rope(v[:1], w, nh, hd, 0, neox, 1e-6, 1e4, hd, 0).reshape(-1),
+                                  v[:1].reshape(-1))
+    r = oracle.norm_rope(v, w, nh, hd, 0, neox, 1e-6, 1e4, hd, 123).reshape(T, nh, hd)
+    np.testing.assert_allclose(np.linalg.norm(r, axis=-1), np.linalg.norm(v, axis=-1), rtol=1e-5)
+
+
+@pytest.mark.parametrize("nh,nkv,T,pos0", [(4, 1, 1, 0), (4, 2, 1, 70), (8, 2, 5, 130), (2, 2, 3, 64)])
+def test_attention(oracle, nh, nkv, T, pos0):
+    hd, ctx = 64, 256
+    rng = np.random.default_rng(6)
+    q = rng.standard_normal((T, nh * hd)).astype(np.float32)
+    kc = rng.standard_normal((ctx, nkv * hd)).astype(np.float32)
+    vc = rng.standard_normal((ctx, nkv * hd)).astype(np.float32)
+    got = oracle.attention(q, kc, vc, T, pos0, nh, nkv, hd, 0.125)
+    np.testing.assert_allclose(got, refs.attention64(q, kc, vc, pos0, nh, nkv, hd, 0.125), rtol=1e-5, atol=1e-5)
+
+
+def test_attention_closed_forms(oracle):
+    hd, nh = 64, 2
+    rng = np.random.default_rng(7)
+    kc = rng.standard_normal((8, nh * hd)).astype(np.float32)
+    vc = rng.standard_normal((8, nh * hd)).astype(np.float32)
+    q = rng.standard_normal((1, nh * hd)).astype(np.float32)
+    np.testing.assert_allclose(oracle.attention(q, kc, vc, 1, 0, nh, nh, hd, 1.0), vc[:1], rtol=1e-6)  # one key
+    z = np.zeros((1, nh * hd), np.float32)
+    np.testing.assert_allclose(oracle.attention(z, kc, vc, 1, 7, nh, nh, hd, 1.0)[0], vc.mean(0), rtol=1e-5,
+                               atol=1e-6)  # uniform scores
+
+
+def test_swiglu(oracle):
+    g = np.linspace(-30, 30, 301).astype(np.float32)
+    u = np.linspace(1, 2, 301).astype(np.float32)
+    np.testing.assert_allclose(oracle.swiglu(g, u), refs.silu64(g) * u, rtol=1e-6, atol=1e-30)
+
+
+def test_moe_topk(oracle):
+    lg = np.array([[0.5, 2.0, 2.0, -1.0, 1.0, 2.0]], np.float32)
+    sel, wts = oracle.moe_topk(lg, 6, 3, 1, 2.5)
+    assert list(sel) == [1, 2, 5]  # ties go to the lower index
+    np.testing.assert_allclose(wts.sum(), 2.5, rtol=1e-6)
+    sel, wts = oracle.moe_topk(lg, 6, 2, 0, 1.0)
+    r_sel, r_w = refs.topk64(lg[0].astype(np.float64), 2, False, 1.0)
+    assert list(sel) == list(r_sel)
+    np.testing.assert_allclose(wts, r_w, rtol=1e-6)
+    rng = np.random.default_rng(8)
+    for _ in range(20):
+        lg = rng.standard_normal((1, 128)).astype(np.float32)
+        sel, wts = oracle.moe_topk(lg, 128, 8, 1, 1.0)
+        r_sel, r_w = refs.topk64(lg[0].astype(np.float64), 8, True, 1.0)
+        assert list(sel) == list(r_sel)
+        np.testing.assert_allclose(wts, r_w, rtol=1e-5)
+
+
+def test_moe_comb(oracle):
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((2, 16)).astype(np.float32)
+    de = rng.standard_normal((2 * 3, 16)).astype(np.float32)
+    w = rng.random(6).astype(np.float32)
+    ref = x.astype(np.float64) + np.einsum("tk,tkd->td", w.reshape(2, 3).astype(np.float64),
+                                           de.reshape(2, 3, 16).astype(np.float64))
+    np.testing.assert_allclose(oracle.moe_comb(x, de, w, 16, 3), ref, rtol=1e-6, atol=1e-6)
+
+
+def test_argmax_ties_nan(oracle):
+    assert oracle.argmax([1, 3, 3, 2]) == 1
+    assert oracle.argmax([np.nan, 1, np.nan, 1]) == 1
+    assert oracle.argmax([np.nan, np.nan]) == 0
+    assert oracle.argmax([-np.inf, -np.inf]) == 0
+
+
+# ------------------------------------------------------------------------------------------------ model
+@pytest.mark.parametrize("name,neox", [("mini_llama_q4km_c", 0), ("mini_qwen3_q4km_c", 1), ("mini_qwen3moe_q4k_c", 1),
+                                       ("mini_llama_q8_c", 0)])
+def test_model_forward_vs_float64(oracle, models_dir, name, neox):
+    # float32 rounding, amplified by near-ties of the large activations of the centered models, stays below these
+    # bounds; a semantic slip (RoPE pairing, norm placement, GQA head map, missing residual) is O(0.1)
+    path = synth.ensure_model(name, models_dir)
+    m = oracle.Model(path, ctx=64)
+    prompt = synth.random_prompt(m.vocab, 12, 3)
+    ref = refs.Model64(m.g, neox)
+    lg = m.forward(prompt[:9], True)  # T = 9: the tiled (serial) prefill order
+    for t in prompt[:9]:
+        lr = ref.step(t)
+    assert refs.rel_err(lg, lr) < 2e-3
+    m2 = oracle.Model(path, ctx=64)
+    ref2 = refs.Model64(m2.g, neox)
+    for t in prompt:  # T = 1: the lane order
+        assert refs.rel_err(m2.forward([t], True), ref2.step(t)) < 2e-4
+
+
+@pytest.mark.parametrize("name,neox", [("mini_llama_q4km_c", 0), ("mini_qwen3moe_q4k_c", 1)])
+def test_model_kv_f16_vs_float64(oracle, models_dir, name, neox):
+    """The f16 KV-cache option: cache rows rounded to half precision when written."""
+    path = synth.ensure_model(name, models_dir)
+    m = oracle.Model(path, ctx=64, kv_f16=True)
+    ref = refs.Model64(m.g, neox, kv_f16=True)
+    ref32 = refs.Model64(m.g, neox)
+    prompt = synth.random_prompt(m.vocab, 8, 4)
+    differs = False
+    for t in prompt:
+        lg, lr, l32 = m.forward([t], True), ref.step(t), ref32.step(t)
+        assert refs.rel_err(lg, lr) < 2e-4
+        differs |= refs.rel_err(lg, l32) > 1e-5  # the rounding is really applied
+    assert differs
+
+
+def test_model_context_overflow(oracle, models_dir):
+    m = oracle.Model(synth.ensure_model("mini_llama_q8", models_dir), ctx=8)
+    m.forward(list(range(8)), False)
+    with pytest.raises(RuntimeError):
+        m.forward([1], True)
+
+
+# ------------------------------------------------------------------------------------------------ GGUF
+def test_gguf_roundtrip(oracle, models_dir):
+    c = synth.CONFIGS["mini_qwen3moe_q4k"]
+    g = oracle.GGUF(synth.ensure_model("mini_qwen3moe_q4k", models_dir))
+    plan = synth.tensor_plan(c)
+    assert g.order == [p[0] for p in plan]
+    for name, dims, gtype, _ in plan:
+        t = g.tensors[name]
+        assert t["dims"] == dims and t["tipo"] == gtype
+        assert t["bytes"] == synth.tensor_nbytes(dims, gtype)
+        assert t["abs"] % 32 == 0
+    assert g.kv["general.architecture"] == "qwen3moe"
+    assert g.kv["qwen3moe.expert_count"] == 16 and g.kv["qwen3moe.expert_weights_norm"] is True
+    assert len(g.kv["tokenizer.ggml.tokens"]) == c.vocab
