@@ -409,7 +409,9 @@ void or_norm_rope(float* v, const float* w, int T, int nh, int hd, int usaNorm, 
                         primero = (i % 2) == 0;
                     }
                     float ex = (-2.0f * (float)j) / (float)nrot;
-                    float theta = (pos * esc) * powf(base, ex);
+                    /* base^ex rounded once to float (evaluated in double), so the frequency does not depend
+                     * on the accuracy of a library powf */
+                    float theta = (pos * esc) * (float)pow((double)base, (double)ex);
                     float sn, c;
                     or_sincos2(theta, &sn, &c);
                     r = primero ? (a * c - b * sn) : (a * sn + b * c);

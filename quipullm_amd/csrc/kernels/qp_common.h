@@ -155,7 +155,8 @@ QP_DEV float rope_elem(const float* v, uint32_t i, uint32_t nrot, bool neox, flo
             primero = (i % 2) == 0;
         }
         const float ex = (-2.0f * (float)j) / (float)nrot;
-        const float theta = pos_esc * powf(base, ex);
+        // base^ex rounded once to float (evaluated in double): the frequency does not depend on a powf's accuracy
+        const float theta = pos_esc * (float)pow((double)base, (double)ex);
         float sn, c;
         sincos2(theta, sn, c);
         r = primero ? (a * c - b * sn) : (a * sn + b * c);

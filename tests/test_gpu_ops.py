@@ -291,7 +291,7 @@ def test_norm_rope(quipu, dev, oracle, hd, neox, use_norm):
     quipu.dispatch("norm_rope", [("u", hd), ("u", nh), ("u", use_norm), ("u", neox), ("f", 1e-6), ("f", 5e5),
                                  ("u", hd), ("u", 0)], [dev.paso(T, pos0), vb, dev.buf(w)], (nh, T))
     got = dev.get(vb, (T * nh * hd,))
-    want = oracle.norm_rope(v, w, nh, hd, use_norm, neox, 1e-6, 5e5, hd, pos0)
+    want = oracle.norm_rope(v, w, nh, hd, use_norm, neox, 1e-6, 5e5, hd, pos0).reshape(-1)
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
 
 
