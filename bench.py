@@ -12,7 +12,9 @@ backend's stream, with the greedy argmax on the device.
 Also measured live: the dominant kernel, the Q4_K GEMV (14336 x 4096, batch 1), over back-to-back launches that
 rotate through >= 512 MB of weight copies (so the 256 MB last-level cache cannot hold them), timed with HIP
 events on the backend's stream.  The CPU baseline is the C restatement of the reference semantics (the test
-oracle) timed on this host's cores on a bounded sample of the same decode.
+oracle) timed on this host's cores on a bounded sample of the same decode; the greedy ids and logits of that
+sample are also the parity check of the GPU run, which generates from the same prompt on the fused path before
+its timed runs (config.parity_vs_oracle: ids identical, max relative logit error).
 
 Process layout: this process loads the CPU checker first, runs the GPU decode in a child Node.js process
 (the product host) and only then opens the GPU itself (ctypes) for the GEMV measurement, so no program is
@@ -74,76 +76,70 @@ def decode_bytes_per_token(path, P, n):
     return w, w + kv_per_pos * mean_pos
 
 
+CHECK_PROMPT = [1, 128000, 9906, 1917]
+
+
 def cpu_baseline(path, seconds=20.0):
-    """The oracle on this host: greedy decode steps of the same model after a 1-token prompt, as many as fit in
-    about `seconds` (at least 2)."""
+    """The oracle on this host: greedy decode steps of the same model (f16 KV, as the GPU run) after a short
+    prompt, as many as fit in about `seconds` (at least 2).  Also returns the greedy ids and the logits each
+    was chosen from, for the parity check of the GPU run."""
     from oracle import oracle as O
     threads = O.lib().or_num_threads()
-    m = O.Model(path, ctx=64)
-    lg = m.forward([1], True)  # also pages the weights in
+    m = O.Model(path, ctx=64, kv_f16=True)
+    lg = m.forward(CHECK_PROMPT, True)  # also pages the weights in
+    ids, lgs = [O.argmax(lg)], [lg]
     t0 = time.time()
     steps = 0
     while steps < 2 or (time.time() - t0 < seconds and steps < 40):
-        lg = m.forward([O.argmax(lg)], True)
+        lg = m.forward([ids[-1]], True)
+        ids.append(O.argmax(lg))
+        lgs.append(lg)
         steps += 1
     dt = time.time() - t0
     m.close()
     return {"value": steps / dt, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} greedy decode steps of the same 8B Q4_K_M model after a 1-token prompt "
-                      f"(KV length <= {steps + 1}, f32 KV) in {dt:.1f} s on {threads} OpenMP threads; "
-                      f"C restatement of the reference WGSL semantics"}
+            "sample": f"{steps} greedy decode steps of the same 8B Q4_K_M model after a {len(CHECK_PROMPT)}-token "
+                      f"prompt (KV length <= {steps + len(CHECK_PROMPT)}, f16 KV) in {dt:.1f} s on {threads} "
+                      f"OpenMP threads; C restatement of the reference WGSL semantics"}, ids, lgs
 
 
-def run_decode(path, steps, warmup, prefills):
+def run_decode(path, steps, warmup, prefills, check_n, eager=False):
     c = synth.CONFIGS[MODEL]
     ctx = max(prefills) + steps + warmup + 8
     ids = synth.random_prompt(c.vocab, max(prefills), 7)
     pf = os.path.join(model_dir(), f"{MODEL}.bench_prompt.json")
+    cf = os.path.join(model_dir(), f"{MODEL}.check_prompt.json")
+    lf = os.path.join(model_dir(), f"{MODEL}.check_logits.f32")
     with open(pf, "w") as f:
         json.dump(ids, f)
+    with open(cf, "w") as f:
+        json.dump(CHECK_PROMPT, f)
     cmd = ["node", os.path.join(ROOT, "quipullm_amd", "js", "cli.js"), "bench", "--model", path, "--prompt-file", pf,
            "--n", str(steps), "--warmup", str(warmup), "--kv", "f16", "--ctx", str(ctx), "--batch", "512",
-           "--max-gen", str(max(steps, warmup) + 8), "--prefill", ",".join(str(p) for p in prefills)]
+           "--max-gen", str(max(steps, warmup, check_n) + 8), "--prefill", ",".join(str(p) for p in prefills),
+           "--check-prompt-file", cf, "--check-n", str(check_n), "--check-logits", lf] + (["--eager"] if eager else [])
     log("bench: " + " ".join(cmd))
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         raise RuntimeError("decode benchmark failed:\n" + r.stderr[-3000:])
-    return json.loads(r.stdout.strip().splitlines()[-1])
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    out["check_logits"] = np.fromfile(lf, np.float32).reshape(-1, c.vocab)
+    return out
+
+
+def parity(gpu_ids, gpu_lg, cpu_ids, cpu_lg):
+    """Greedy ids and logits of the GPU run against the oracle's on the same prompt (f16 KV on both)."""
+    n = min(len(gpu_ids), len(cpu_ids))
+    rel = [float(np.max(np.abs(a - b)) / np.max(np.abs(b))) for a, b in zip(gpu_lg[:n], cpu_lg[:n])]
+    return {"tokens": n, "ids_identical": gpu_ids[:n] == cpu_ids[:n], "max_rel_logits": max(rel),
+            "prompt": CHECK_PROMPT}
 
 
 def gemv_microbench(shapes, iters=200, rotate_bytes=640 << 20):
     """Average launch duration (HIP events over back-to-back launches) of the fused GEMV op, per shape."""
-    from quipullm_amd import capi
+    from quipullm_amd import capi, gemv_bench
     q = capi.Quipu(0)
-    out = []
-    paso = q.paso(1, 0)
-    for fmt, N, K in shapes:
-        nbytes = capi.device_bytes(fmt, N, K)
-        ncopy = max(2, rotate_bytes // nbytes + 1)
-        raw = np.frombuffer(synth.gen_blocks(np.random.default_rng([3, N, K]), fmt, N * K), np.uint8)
-        hs = [q.upload_matrix(fmt, raw, N, K) for _ in range(ncopy)]
-        xb = q.buffer_from(np.random.default_rng(4).standard_normal(K).astype(np.float32))
-        yb = q.alloc(N * 4)
-        u = capi.gemv_uniform(1, K, fmt=fmt, segs=[(capi.STORE, N, 0, N)])
-        for i in range(10):
-            q.dispatch("gemv", u, [paso, xb, 0, 0, hs[i % ncopy], 0, yb])
-        q.sync()
-        e0, e1 = q.event(), q.event()
-        q.record(e0)
-        for i in range(iters):
-            q.dispatch("gemv", u, [paso, xb, 0, 0, hs[i % ncopy], 0, yb])
-        q.record(e1)
-        us = q.elapsed_ms(e0, e1) * 1000.0 / iters
-        alg = nbytes + 4 * K + 4 * N
-        out.append({"format": capi.FMT_NAME[fmt], "N": N, "K": K, "bytes": alg, "us_per_launch": us,
-                    "GBs": alg / (us * 1e-6) / 1e9})
-        for h in hs:
-            q.free(h)
-        q.free(xb)
-        q.free(yb)
-        q.event_free(e0)
-        q.event_free(e1)
-    return out
+    return [gemv_bench.time_gemv(q, fmt, N, K, iters, rotate_bytes) for fmt, N, K in shapes]
 
 
 def committed_traffic():
@@ -161,6 +157,9 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--decode-launch", choices=["graph", "eager"], default="graph",
+                    help="the one-token step as a captured HIP graph (default) or dispatched op by op (same kernels; "
+                         "for profilers that cannot follow graph launches)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); the multi-GPU sharding of the "
@@ -173,12 +172,14 @@ def main():
     t0 = time.time()
     path = synth.ensure_model(MODEL, model_dir())
     log(f"bench: model {path} ready in {time.time() - t0:.1f}s")
-    cpu = cpu_baseline(path, a.cpu_seconds)
+    cpu, cpu_ids, cpu_lg = cpu_baseline(path, a.cpu_seconds)
     log(f"bench: cpu baseline {cpu['value']:.3f} tok/s")
     prefills = [4096, 512]
-    dec = run_decode(path, a.steps, a.warmup, prefills)
+    dec = run_decode(path, a.steps, a.warmup, prefills, len(cpu_ids), a.decode_launch == "eager")
+    check = parity(dec["check_ids"], dec.pop("check_logits"), cpu_ids, cpu_lg)
     runs = {r["prompt_tokens"]: r for r in dec["runs"]}
     log("bench: decode " + json.dumps(dec))
+    log("bench: parity " + json.dumps(check))
     from quipullm_amd import capi
     gem = gemv_microbench([(capi.Q4_K, 14336, 4096), (capi.Q4_K, 4096, 4096), (capi.Q4_K, 4096, 14336),
                            (capi.Q6_K, 4096, 4096), (capi.Q6_K, 14336, 4096), (capi.Q6_K, 4096, 14336)])
@@ -193,7 +194,7 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "Llama-3-8B-shape Q4_K_M (Q6_K attn_v/ffn_down/output) greedy decode, batch 1, "
                                "KV prefilled with 4096 random prompt ids, f16 KV, 256 timed tokens",
-                   "ctx": 4096, "kv": "f16", "batch": 1, "prefill_tokens": 4096,
+                   "ctx": 4096, "kv": "f16", "batch": 1, "prefill_tokens": 4096, "decode_launch": a.decode_launch,
                    "decode_tok_s_ctx512": round(runs[512]["decode_tok_s"], 3),
                    "decode_hbm_GBs_ctx4096": round(bpt * tok_s / 1e9, 1),
                    "decode_roofline_frac_ctx4096": round(bpt * tok_s / 1e9 / PEAK_HBM_GBS, 4),
@@ -201,7 +202,8 @@ def main():
                    "bytes_per_token_ctx4096": int(bpt), "weight_bytes_per_token": int(wbytes),
                    "wall_tok_s_ctx4096": round(main_run["wall_tok_s"], 3),
                    "prefill_tok_s_4096": round(main_run["prefill_tok_s"], 1),
-                   "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()} for g in gem]},
+                   "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()} for g in gem],
+                   "parity_vs_oracle": check},
         "roofline": {"bound": "hbm", "kernel": "qp_gemv_q4k (Q4_K GEMV 14336x4096, batch 1)",
                      "achieved": round(dom["GBs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(dom["GBs"] / PEAK_HBM_GBS, 4), "traffic": committed_traffic(),

@@ -5,14 +5,17 @@
 //                        [--ctx N] [--batch N] [--no-tiled] [--logits-out file.f32]
 //                        [--repeat-penalty R] [--frequency-penalty F] [--presence-penalty P] [--host-loop]
 //   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
-//                        [--warmup W]
+//                        [--warmup W] [--prefill P1,P2] [--eager]
+//                        [--check-prompt-file ids.json --check-n N --check-logits file.f32]
 //
 // generate prints one JSON line {ids, prompt_ms, decode_ms, tps}; with --logits-out the logits each token was
 // chosen from are appended to the file as float32 (vocab floats per token).  mode "ref" runs the reference op
 // sequence with a host argmax per token; "fast" runs the captured one-token graph with the device argmax;
 // "engine" runs engine.generar with the given sampler parameters (no logits file).
 // bench prefills the prompt, then times n decode steps (device events around the graph replays, and the wall
-// clock) and prints {decode_tok_s, ms_per_token, ...}.
+// clock) and prints {decode_tok_s, ms_per_token, ...}; with --check-prompt-file it first generates --check-n
+// greedy tokens from that prompt on the fused path (ids in check_ids, logits to --check-logits) for a parity
+// check by the caller.
 const fs = require('fs');
 const engine = require('./engine');
 const { argmax } = require('./sampling');
@@ -33,6 +36,7 @@ async function cargar(o) {
   const options = { tiled_prefill: !o['no-tiled'], kv_f16: o.kv === 'f16' };
   if (o.batch) options.batch = parseInt(o.batch, 10);
   if (o['max-gen']) options.max_gen = parseInt(o['max-gen'], 10);
+  if (o.eager) options.eager_decode = true;
   return engine.cargarModelo(o.model, { ctx: o.ctx ? parseInt(o.ctx, 10) : undefined, options: options });
 }
 
@@ -105,10 +109,31 @@ async function medir(modelo, ids, P, n, warm, eager) {
   };
 }
 
+// Greedy generation of n tokens from `ids` on the fused path, with the logits each token was chosen from
+// written to `archivo` (float32, vocab per token).  Returns the ids.
+async function chequeo(modelo, ids, n, archivo) {
+  const out = fs.openSync(archivo, 'w');
+  const escribe = function (lg) { fs.writeSync(out, Buffer.from(lg.buffer, lg.byteOffset, lg.byteLength)); };
+  const logits = await engine.prefill(modelo, ids);
+  escribe(logits);
+  const toks = [argmax(logits)];
+  if (n > 1) {
+    const nuevos = modelo.decodificarVoraz(toks[0], n - 1, { porPaso: function (i, t, lg) { escribe(lg); } });
+    for (const t of nuevos) toks.push(t);
+  }
+  fs.closeSync(out);
+  return toks;
+}
+
 async function bench(o) {
   const tLoad = Date.now();
   const modelo = await cargar(o);
   const loadMs = Date.now() - tLoad;
+  let check = null;
+  if (o['check-prompt-file']) {
+    const cids = JSON.parse(fs.readFileSync(o['check-prompt-file'], 'utf8'));
+    check = await chequeo(modelo, cids, parseInt(o['check-n'] || '8', 10), o['check-logits']);
+  }
   const ids = JSON.parse(fs.readFileSync(o['prompt-file'], 'utf8'));
   const n = parseInt(o.n || '256', 10);
   const warm = parseInt(o.warmup || '8', 10);
@@ -119,7 +144,7 @@ async function bench(o) {
     runs.push(await medir(modelo, ids, P, n, warm, !!o.eager));
   }
   const r = { runs: runs, load_ms: loadMs, ctx: modelo.ctx, nsplit: modelo.nsplit, kv_f16: modelo.kvF16,
-    batch: modelo.batch, bytes_on_gpu: modelo.gpu.bytesUsados };
+    batch: modelo.batch, bytes_on_gpu: modelo.gpu.bytesUsados, check_ids: check };
   modelo.free();
   process.stdout.write(JSON.stringify(r) + '\n');
 }

@@ -55,6 +55,7 @@ class ModeloTransformer {
     const op = meta.options || {};
     this.batch = op.batch || 32;                 // tokens per prefill pass (reference transformer.js:10 uses 32)
     this.kvF16 = !!op.kv_f16;                    // f16 KV cache (the reference keeps it in f32)
+    this.eagerDecode = !!op.eager_decode;        // fused step dispatched op by op instead of a captured graph
     this.baldosa = op.tiled_prefill !== false;   // config.json "tiled_prefill"
     this.bufs = [];
     this.pos = 0;
@@ -368,7 +369,7 @@ class ModeloTransformer {
   // Builds and captures the fused one-token step.  Called from load(): the eager validation run writes KV slot 0
   // of every layer, which the first prefill overwrites.
   prepararDecode() {
-    if (this.grafo) return;
+    if (this.planDecode && (this.grafo || this.eagerDecode)) return;
     this.planDecode = this._armarDecode();
     const self = this;
     // one eager run validates every op's bindings before capture (a failed op inside a capture is harder to read)
@@ -377,7 +378,13 @@ class ModeloTransformer {
     this.gpu.escribir(this.contador, 0, new Uint32Array([0, 0, 0, 0]));
     this._ejecutar(this.planDecode);
     this.gpu.sincronizar();
-    this.grafo = this.gpu.capturar(function () { self._ejecutar(self.planDecode); });
+    if (!this.eagerDecode) this.grafo = this.gpu.capturar(function () { self._ejecutar(self.planDecode); });
+  }
+
+  // k one-token steps of the fused plan: graph replays, or the same ops dispatched one by one (eager_decode).
+  _pasos(k) {
+    if (this.eagerDecode) for (let i = 0; i < k; i++) this._ejecutar(this.planDecode);
+    else this.gpu.reproducir(this.grafo, k);
   }
 
   // Greedy continuation on the device: `primero` is the token chosen from the last logits; runs `n` one-token
@@ -398,7 +405,7 @@ class ModeloTransformer {
     if (opciones.porPaso) {
       const lg = new Float32Array(this.vocab), t = new Uint32Array(1);
       for (let i = 0; i < n; i++) {
-        gpu.reproducir(this.grafo, 1);
+        this._pasos(1);
         gpu.leer(this.logits, 0, lg);
         gpu.leer(this.bIds, 0, t);
         opciones.porPaso(i, t[0], lg);
@@ -407,11 +414,11 @@ class ModeloTransformer {
       const e0 = gpu.evento(), e1 = gpu.evento();
       gpu.marcar(e0);
       if (opciones.eager) for (let i = 0; i < n; i++) this._ejecutar(this.planDecode);   // same ops, no graph
-      else gpu.reproducir(this.grafo, n);
+      else this._pasos(n);
       gpu.marcar(e1);
       opciones.tiempos.ms = gpu.msEntre(e0, e1);
     } else {
-      gpu.reproducir(this.grafo, n);
+      this._pasos(n);
     }
     const out = new Uint32Array(n);
     gpu.leer(this.tokens, 0, out);
