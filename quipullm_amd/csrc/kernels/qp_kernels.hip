@@ -897,240 +897,426 @@ KERNEL __launch_bounds__(256) void qp_attn_hd64(QpAttnArgs a) { attn_gen_body<64
 KERNEL __launch_bounds__(256) void qp_attn_hd128(QpAttnArgs a) { attn_gen_body<128>(a); }
 
 // Split-K decode attention for one token, with the per-head q/k RMSNorm, RoPE and the KV append fused in.
-// grid (nkv, nsplit).  Each workgroup takes a contiguous key range of one KV head for all G query heads of the
-// group (G in 1, 2, 4, 8) and writes an unnormalized partial (m, l, acc) per head; qp_dec_attn_comb merges them.
-// Keys and values move in tiles of 32 with 16-byte loads; the next tile is loading while the current one is
-// scored.  Scores are float4 dot products from LDS; the online softmax runs per head within one wavefront.
-template <int HD>
-struct KvTile {
-    static constexpr int TK = 32;
-    static constexpr int MAXC = HD * 4 * TK / 16 / 256;  // 16-byte chunks per thread (f32 cache, the larger)
-    uint4 k[MAXC], v[MAXC];
+// grid (nkv, nsplit); a workgroup covers a contiguous key range of one KV head for the G query heads of its
+// group, split again over its 4 wavefronts.  Each wavefront streams its keys straight from HBM into registers:
+// a key row is spread over LPK lanes (16 bytes each), KPI keys per load instruction, U instructions per step,
+// with the next step's loads in flight while the current one is consumed.  Scores are per-lane partial dot
+// products reduced over the key's lanes with DPP; every lane group keeps its own online-softmax state
+// (m, l, acc over its dims), merged across groups by shuffles and across wavefronts in LDS into one partial
+// per (head, workgroup), which qp_dec_attn_comb merges.  The q/k/v loads are issued first, then the first
+// step's K/V loads, so the q/k preparation runs while those are in flight (vector-memory waits are in order).
+template <int CTRL>
+QP_DEV float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// Sum over aligned groups of L lanes (L = 8, 16, 32 or 64); every lane of a group ends with the same bits.
+template <int L>
+QP_DEV float group_sum(float v) {
+    if (L >= 16) v += dpp_mov<0x140>(v);  // row_mirror: lane i + lane 15-i
+    v += dpp_mov<0x141>(v);               // row_half_mirror: lane i + lane 7-i
+    v += dpp_mov<0x4E>(v);                // quad_perm [2,3,0,1]
+    v += dpp_mov<0xB1>(v);                // quad_perm [1,0,3,2]
+    if (L >= 32) v += __shfl_xor(v, 16, 64);
+    if (L >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// RoPE of element i with the frequency table freq[j] = base^(-2j/nrot) (rounded once to float).
+QP_DEV float rope_elem_f(const float* v, uint32_t i, uint32_t nrot, bool neox, float pos_esc, const float* freq) {
+    float r = v[i];
+    if (i < nrot) {
+        const uint32_t mitad = nrot / 2;
+        uint32_t j;
+        float a, b;
+        bool primero;
+        if (neox) {
+            j = i % mitad;
+            if (i < mitad) { a = v[i]; b = v[i + mitad]; } else { a = v[i - mitad]; b = v[i]; }
+            primero = i < mitad;
+        } else {
+            j = i / 2;
+            const uint32_t i0 = i - (i % 2);
+            a = v[i0]; b = v[i0 + 1];
+            primero = (i % 2) == 0;
+        }
+        const float theta = pos_esc * freq[j];
+        float sn, c;
+        sincos2(theta, sn, c);
+        r = primero ? (a * c - b * sn) : (a * sn + b * c);
+    }
+    return r;
+}
+
+// wave_norm_rope with a frequency table in LDS (same values as rope_elem computes per element).
+QP_DEV void wave_norm_rope_f(float* v, const float* w, uint32_t hd, bool use_norm, float eps, float pos_esc,
+                             const float* freq, uint32_t nrot, bool neox, int lane) {
+    float vals[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t i = lane + 64 * c;
+        vals[c] = i < hd ? v[i] : 0.0f;
+        ss += vals[c] * vals[c];
+    }
+    ss = wave_sum(ss);
+    if (use_norm) {
+        const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t i = lane + 64 * c;
+            if (i < hd) v[i] = (vals[c] * inv) * w[i];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t i = lane + 64 * c;
+        if (i < hd) vals[c] = rope_elem_f(v, i, nrot, neox, pos_esc, freq);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t i = lane + 64 * c;
+        if (i < hd) v[i] = vals[c];
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+template <int HD, bool F16>
+struct DecCfg {
+    static constexpr int E = F16 ? 8 : 4;   // cache elements per 16-byte chunk
+    static constexpr int LPK = HD / E;      // lanes per key row
+    static constexpr int KPI = 64 / LPK;    // keys per load instruction
+    static constexpr int U = 4;             // load instructions per step
+    static constexpr int KS = U * KPI;      // keys per step
 };
 
-template <int HD>
-QP_DEV void kv_tile_load(KvTile<HD>& t, const QpDecAttnArgs& a, uint32_t kvh, uint32_t kt, uint32_t k1) {
-    constexpr int TK = KvTile<HD>::TK;
-    const uint32_t eb = a.f16 ? 2 : 4;
-    const uint32_t cpk = HD * eb / 16;  // 16-byte chunks per key
-    const uint32_t kvd = a.nkv * HD;
+struct DecBuf {
+    uint4 k[4], v[4];
+};
+
+template <int HD, bool F16>
+QP_DEV void dec_load(DecBuf& b, const QpDecAttnArgs& a, uint32_t kvh, uint32_t kb, uint32_t klast, uint32_t kq,
+                     uint32_t dsub) {
+    using C = DecCfg<HD, F16>;
+    const uint64_t kvd = (uint64_t)a.nkv * HD, eb = F16 ? 2 : 4;
 #pragma unroll
-    for (int c = 0; c < KvTile<HD>::MAXC; c++) {
-        const uint32_t q = threadIdx.x + 256 * c;
-        if (q < TK * cpk) {
-            const uint32_t key = min(kt + q / cpk, k1 - 1);  // clamped: rows past the range are loaded, not used
-            const uint64_t off = ((uint64_t)key * kvd + kvh * HD) * eb + (q % cpk) * 16;
-            t.k[c] = gload<uint4>(a.kc + off);
-            t.v[c] = gload<uint4>(a.vc + off);
+    for (int u = 0; u < C::U; u++) {
+        const uint32_t key = min(kb + u * C::KPI + kq, klast);  // clamped: keys past the range are loaded, unused
+        const uint64_t off = ((uint64_t)key * kvd + (uint64_t)kvh * HD) * eb + dsub * 16;
+        b.k[u] = gload<uint4>(a.kc + off);
+        b.v[u] = gload<uint4>(a.vc + off);
+    }
+}
+
+template <bool F16>
+QP_DEV void dec_unpack(const uint4 w, float (&f)[F16 ? 8 : 4]) {
+    if constexpr (F16) {
+        const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            f[2 * i] = h2f(x[i] & 0xffffu);
+            f[2 * i + 1] = h2f(x[i] >> 16);
+        }
+    } else {
+        f[0] = __uint_as_float(w.x); f[1] = __uint_as_float(w.y);
+        f[2] = __uint_as_float(w.z); f[3] = __uint_as_float(w.w);
+    }
+}
+
+constexpr float QP_LOG2E = 1.4426950408889634f;
+
+// One step of KS keys starting at kb: scores for the G heads, then the online-softmax update of this lane
+// group's state.  Keys at or past kend are masked; the key pos0 (this token's) comes from kn / vn.
+template <int HD, bool F16, int G>
+QP_DEV void dec_consume(const DecBuf& b, uint32_t kb, uint32_t kend, uint32_t pos0, const float* kn,
+                        const float* vn, uint32_t kq, uint32_t dsub, const float (&qr)[G][DecCfg<HD, F16>::E],
+                        float scale, float (&m)[G], float (&l)[G], float (&acc)[G][DecCfg<HD, F16>::E]) {
+    using C = DecCfg<HD, F16>;
+    constexpr int E = C::E;
+    const bool has_new = kb <= pos0 && pos0 < kb + C::KS;  // wave-uniform
+    float s[C::U][G];
+#pragma unroll
+    for (int u = 0; u < C::U; u++) {
+        float kf[E];
+        dec_unpack<F16>(b.k[u], kf);
+        if (has_new && kb + u * C::KPI + kq == pos0) {
+#pragma unroll
+            for (int e = 0; e < E; e++) kf[e] = kn[dsub * E + e];
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; e++) d = fmaf(qr[g][e], kf[e], d);
+            s[u][g] = group_sum<C::LPK>(d) * scale;
+        }
+    }
+    float mn[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float mx = m[g];
+#pragma unroll
+        for (int u = 0; u < C::U; u++)
+            if (kb + u * C::KPI + kq < kend) mx = fmaxf(mx, s[u][g]);
+        const float c = __builtin_amdgcn_exp2f((m[g] - mx) * QP_LOG2E);
+        l[g] *= c;
+#pragma unroll
+        for (int e = 0; e < E; e++) acc[g][e] *= c;
+        mn[g] = mx;
+        m[g] = mx;
+    }
+#pragma unroll
+    for (int u = 0; u < C::U; u++) {
+        const uint32_t key = kb + u * C::KPI + kq;
+        if (key < kend) {
+            float vf[E];
+            dec_unpack<F16>(b.v[u], vf);
+            if (has_new && key == pos0) {
+#pragma unroll
+                for (int e = 0; e < E; e++) vf[e] = vn[dsub * E + e];
+            }
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float p = __builtin_amdgcn_exp2f((s[u][g] - mn[g]) * QP_LOG2E);
+                l[g] += p;
+#pragma unroll
+                for (int e = 0; e < E; e++) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+            }
         }
     }
 }
 
-template <int HD>
-QP_DEV void kv_tile_store(const KvTile<HD>& t, const QpDecAttnArgs& a, uint32_t kt, uint32_t k1, uint32_t pos0,
-                          float* ks, float* vs, const float* kn, const float* vn) {
-    constexpr int TK = KvTile<HD>::TK;
-    constexpr int KS = HD + 4;  // K row stride in LDS (16-byte aligned rows, shifted banks)
-    const uint32_t eb = a.f16 ? 2 : 4;
-    const uint32_t cpk = HD * eb / 16, epc = 16 / eb;  // chunks per key, elements per chunk
-#pragma unroll
-    for (int c = 0; c < KvTile<HD>::MAXC; c++) {
-        const uint32_t q = threadIdx.x + 256 * c;
-        if (q < TK * cpk) {
-            const uint32_t jj = q / cpk, d0 = (q % cpk) * epc, key = kt + jj;
-            float kf[8], vf[8];
-            if (a.f16) {
-                const uint32_t kw[4] = {t.k[c].x, t.k[c].y, t.k[c].z, t.k[c].w};
-                const uint32_t vw[4] = {t.v[c].x, t.v[c].y, t.v[c].z, t.v[c].w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    kf[2 * i] = h2f(kw[i] & 0xffffu); kf[2 * i + 1] = h2f(kw[i] >> 16);
-                    vf[2 * i] = h2f(vw[i] & 0xffffu); vf[2 * i + 1] = h2f(vw[i] >> 16);
-                }
-            } else {
-                kf[0] = __uint_as_float(t.k[c].x); kf[1] = __uint_as_float(t.k[c].y);
-                kf[2] = __uint_as_float(t.k[c].z); kf[3] = __uint_as_float(t.k[c].w);
-                vf[0] = __uint_as_float(t.v[c].x); vf[1] = __uint_as_float(t.v[c].y);
-                vf[2] = __uint_as_float(t.v[c].z); vf[3] = __uint_as_float(t.v[c].w);
-            }
-            for (uint32_t e = 0; e < epc; e++) {
-                float kv = kf[e], vv = vf[e];
-                if (key == pos0) { kv = kn[d0 + e]; vv = vn[d0 + e]; }  // the new key: this workgroup's own copy
-                else if (key >= k1) { kv = 0.0f; vv = 0.0f; }
-                ks[jj * KS + d0 + e] = kv;
-                vs[jj * HD + d0 + e] = vv;
-            }
-        }
-    }
-}
-
-template <int HD>
+// LDS (floats): kn [HD] | vn [HD] | freq [HD/2] | q-norm, k-norm weights [HD] each | region R: q [G][HD]
+// during the preparation, then the wavefront partials wacc [4][G][HD], wm [4][8], wl [4][8].
+template <int HD, bool F16, int G>
 QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
-    constexpr int TK = KvTile<HD>::TK, KS = HD + 4;
+    using C = DecCfg<HD, F16>;
+    constexpr int E = C::E, LPK = C::LPK, KS = C::KS;
+    constexpr int QN = (G * HD + 255) / 256;  // q floats per thread
     extern __shared__ float4 smem4[];
-    const uint32_t G = a.nh / a.nkv;
-    float* qs = reinterpret_cast<float*>(smem4);  // [G][HD]
-    float* ks = qs + 8 * HD;                      // [TK][KS]
-    float* vs = ks + TK * KS;                     // [TK][HD]
-    float* ps = vs + TK * HD;                     // [G][TK]
-    float* kn = ps + 8 * TK;                      // [HD] new key (normalized, rotated)
-    float* vn = kn + HD;                          // [HD] new value
-    float* cr = vn + HD;                          // [G]
+    float* kn = reinterpret_cast<float*>(smem4);
+    float* vn = kn + HD;
+    float* freq = vn + HD;
+    float* qw = freq + HD / 2;
+    float* kw = qw + HD;
+    float* R = kw + HD;
+    float* qs = R;
+    float* wacc = R;
+    float* wm = R + 4 * G * HD;
+    float* wl = wm + 32;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t kvh = blockIdx.x, sp = blockIdx.y;
+    const uint32_t kvh = blockIdx.x, wg = blockIdx.y, h0 = kvh * G;
+    const uint32_t kq = lane / LPK, dsub = lane % LPK;
     const uint32_t pos0 = paso_pos(a.paso);
-    const bool fits = pos0 < a.rows;          // a position past the cache writes nothing and reads nothing
-    const uint32_t nk = fits ? pos0 + 1 : 0;
-    uint32_t per = (nk + a.nsplit - 1) / a.nsplit;
-    per = (per + TK - 1) / TK * TK;
-    const uint32_t k0 = sp * per, k1 = min(nk, k0 + per);
-    const uint32_t kvd = a.nkv * HD;
+    const uint32_t nk = pos0 < a.rows ? pos0 + 1 : 0;  // a position past the cache reads and writes nothing
+    const uint32_t W = 4 * a.nsplit;
+    const uint32_t per = (nk + W - 1) / W;
+    const uint32_t kw0 = min(nk, (wg * 4 + wave) * per), kw1 = min(nk, kw0 + per);
+    const uint32_t g0 = min(nk, wg * 4 * per), g1 = min(nk, g0 + 4 * per);
+    const bool wg_new = g0 <= pos0 && pos0 < g1;  // this workgroup holds the new key: it appends it
+    // 1. q (and the new k, v, and the frequency table) into registers, then the first K/V step
+    float qt[QN], knt = 0.0f, vnt = 0.0f, ft = 0.0f, qwt = 0.0f, kwt = 0.0f;
+#pragma unroll
+    for (int c = 0; c < QN; c++) {
+        const uint32_t i = tid + 256 * c;
+        qt[c] = i < G * HD ? gload<float>(a.q + 4ull * ((uint64_t)h0 * HD + i)) : 0.0f;
+    }
+    if (wg_new && tid < HD) {
+        knt = gload<float>(a.k + 4ull * ((uint64_t)kvh * HD + tid));
+        vnt = gload<float>(a.v + 4ull * ((uint64_t)kvh * HD + tid));
+    }
+    if (a.freq && tid < a.nrot / 2) ft = gload<float>(a.freq + 4ull * tid);
+    if (a.qnorm && tid < HD) qwt = gload<float>(a.qnorm + 4ull * tid);
+    if (a.knorm && wg_new && tid < HD) kwt = gload<float>(a.knorm + 4ull * tid);
+    // unconditional (a wavefront with no keys loads row 0, which always exists), so the waits below can count
+    // these loads as still in flight
+    const uint32_t klast = kw1 > kw0 ? kw1 - 1 : 0;
+    DecBuf A, B;
+    dec_load<HD, F16>(A, a, kvh, kw0, klast, kq, dsub);
+    dec_load<HD, F16>(B, a, kvh, kw0 + KS, klast, kq, dsub);
+    // 2. the preparation (waits for the loads of 1 only)
+    if (tid < a.nrot / 2)
+        freq[tid] = a.freq ? ft : (float)pow((double)a.base, (double)((-2.0f * (float)tid) / (float)a.nrot));
+#pragma unroll
+    for (int c = 0; c < QN; c++) {
+        const uint32_t i = tid + 256 * c;
+        if (i < G * HD) qs[i] = qt[c];
+    }
+    if (wg_new && tid < HD) {
+        kn[tid] = knt;
+        vn[tid] = vnt;
+    }
+    if (tid < HD) {
+        qw[tid] = qwt;
+        kw[tid] = kwt;
+    }
+    __syncthreads();
     const float pos_esc = (float)pos0 * a.esc;
-    KvTile<HD> tile;
-    if (k0 < k1) kv_tile_load<HD>(tile, a, kvh, k0, k1);  // first tile in flight during the q/k preparation
-    for (uint32_t i = tid; i < G * HD; i += 256) qs[i] = gload<float>(a.q + 4ull * ((uint64_t)kvh * G * HD + i));
-    const bool has_new = k0 < k1 && k1 == nk;
-    if (has_new)
-        for (uint32_t i = tid; i < HD; i += 256) {
-            kn[i] = gload<float>(a.k + 4ull * ((uint64_t)kvh * HD + i));
-            vn[i] = gload<float>(a.v + 4ull * ((uint64_t)kvh * HD + i));
-        }
-    __syncthreads();
-    for (uint32_t g = wave; g < G + (has_new ? 1u : 0u); g += 4) {
+    for (uint32_t g = wave; g < G + (wg_new ? 1u : 0u); g += 4) {
         if (g < G)
-            wave_norm_rope(qs + g * HD, a.qnorm ? cptr<float>(a.qnorm) : nullptr, HD, a.qnorm != 0, a.eps, pos_esc,
-                           a.base, a.nrot, a.neox != 0, (int)lane);
+            wave_norm_rope_f(qs + g * HD, qw, HD, a.qnorm != 0, a.eps, pos_esc, freq, a.nrot, a.neox != 0,
+                             (int)lane);
         else
-            wave_norm_rope(kn, a.knorm ? cptr<float>(a.knorm) : nullptr, HD, a.knorm != 0, a.eps, pos_esc, a.base,
-                           a.nrot, a.neox != 0, (int)lane);
+            wave_norm_rope_f(kn, kw, HD, a.knorm != 0, a.eps, pos_esc, freq, a.nrot, a.neox != 0, (int)lane);
     }
     __syncthreads();
-    if (has_new) {
+    if (wg_new && tid < HD) {
         // append to the cache at slot pos0; in f16 mode the LDS copy is rounded the same way
-        const uint64_t o = (uint64_t)pos0 * kvd + kvh * HD;
-        for (uint32_t i = tid; i < HD; i += 256) {
-            if (a.f16) {
-                const uint16_t hk = f2h(kn[i]), hv = f2h(vn[i]);
-                gstore<uint16_t>(a.kc + 2 * (o + i), hk);
-                gstore<uint16_t>(a.vc + 2 * (o + i), hv);
-                kn[i] = h2f(hk);
-                vn[i] = h2f(hv);
-            } else {
-                gstore<float>(a.kc + 4 * (o + i), kn[i]);
-                gstore<float>(a.vc + 4 * (o + i), vn[i]);
+        const uint64_t o = (uint64_t)pos0 * a.nkv * HD + (uint64_t)kvh * HD + tid;
+        if (F16) {
+            const uint16_t hk = f2h(kn[tid]), hv = f2h(vn[tid]);
+            gstore<uint16_t>(a.kc + 2 * o, hk);
+            gstore<uint16_t>(a.vc + 2 * o, hv);
+            kn[tid] = h2f(hk);
+            vn[tid] = h2f(hv);
+        } else {
+            gstore<float>(a.kc + 4 * o, kn[tid]);
+            gstore<float>(a.vc + 4 * o, vn[tid]);
+        }
+    }
+    __syncthreads();
+    float qr[G][E];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < E; e++) qr[g][e] = qs[g * HD + dsub * E + e];
+    __syncthreads();  // every wavefront holds its q before region R is reused
+    float m[G], l[G], acc[G][E];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -3.0e38f;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; e++) acc[g][e] = 0.0f;
+    }
+    // 3. the key stream: two steps in flight from the start, loads issued unconditionally (clamped to the last
+    // key, so the steps past the end re-read cached rows) and keys past kw1 masked
+    if (kw0 < kw1) {
+        const uint32_t nsteps = (kw1 - kw0 + KS - 1) / KS;
+        for (uint32_t s = 0; s < nsteps; s += 2) {
+            dec_consume<HD, F16, G>(A, kw0 + s * KS, kw1, pos0, kn, vn, kq, dsub, qr, a.scale, m, l, acc);
+            dec_load<HD, F16>(A, a, kvh, kw0 + (s + 2) * KS, klast, kq, dsub);
+            dec_consume<HD, F16, G>(B, kw0 + (s + 1) * KS, kw1, pos0, kn, vn, kq, dsub, qr, a.scale, m, l, acc);
+            dec_load<HD, F16>(B, a, kvh, kw0 + (s + 3) * KS, klast, kq, dsub);
+        }
+    }
+    // 4. merge the lane groups of this wavefront (groups hold different keys, the same dims)
+#pragma unroll
+    for (int off = LPK; off < 64; off *= 2) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float mo = __shfl_xor(m[g], off, 64), lo = __shfl_xor(l[g], off, 64);
+            const float M = fmaxf(m[g], mo);
+            const float fa = __builtin_amdgcn_exp2f((m[g] - M) * QP_LOG2E);
+            const float fb = __builtin_amdgcn_exp2f((mo - M) * QP_LOG2E);
+            l[g] = l[g] * fa + lo * fb;
+#pragma unroll
+            for (int e = 0; e < E; e++) {
+                const float ao = __shfl_xor(acc[g][e], off, 64);
+                acc[g][e] = acc[g][e] * fa + ao * fb;
+            }
+            m[g] = M;
+        }
+    }
+    if (lane < LPK) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+#pragma unroll
+            for (int e = 0; e < E; e++) wacc[(wave * G + g) * HD + lane * E + e] = acc[g][e];
+            if (lane == 0) {
+                wm[wave * 8 + g] = m[g];
+                wl[wave * 8 + g] = l[g];
             }
         }
     }
-    // score roles: pair (g, j) handled by tpp adjacent threads, each over HD / tpp dims
-    const uint32_t tpp = G * TK * 2 <= 256 ? 2 : 1;
-    const uint32_t pair = tid / tpp, part = tid % tpp;
-    const uint32_t sg = pair / TK, j = pair % TK;
-    const bool scorer = sg < G;
-    constexpr int MAXO = 8 * HD / 256 > 0 ? 8 * HD / 256 : 1;  // P.V outputs per thread (G <= 8)
-    float acc[MAXO];
-#pragma unroll
-    for (int c = 0; c < MAXO; c++) acc[c] = 0.0f;
-    float m = -3.0e38f, l = 0.0f;
-    for (uint32_t kt = k0; kt < k1; kt += TK) {
-        __syncthreads();  // the previous tile's LDS is free; kn/vn are final
-        kv_tile_store<HD>(tile, a, kt, k1, pos0, ks, vs, kn, vn);
-        __syncthreads();
-        if (kt + TK < k1) kv_tile_load<HD>(tile, a, kvh, kt + TK, k1);  // next tile loads during this one
-        if (scorer) {
-            const uint32_t key = kt + j;
-            const bool valid = key < k1;
-            const float4* qr = reinterpret_cast<const float4*>(qs + sg * HD + part * (HD / tpp));
-            const float4* kr = reinterpret_cast<const float4*>(ks + j * KS + part * (HD / tpp));
-            float dot = 0.0f;
-            for (uint32_t i = 0; i < HD / tpp / 4; i++) {
-                const float4 qv = qr[i], kv = kr[i];
-                dot = fmaf(qv.x, kv.x, dot); dot = fmaf(qv.y, kv.y, dot);
-                dot = fmaf(qv.z, kv.z, dot); dot = fmaf(qv.w, kv.w, dot);
+    __syncthreads();
+    // 5. this workgroup's partial per head: merge of its 4 wavefronts (those with no key have l = 0)
+    for (uint32_t t = tid; t < G * HD; t += 256) {
+        const uint32_t g = t / HD, d = t % HD;
+        float M = -3.0e38f;
+        for (int w = 0; w < 4; w++)
+            if (wl[w * 8 + g] > 0.0f) M = fmaxf(M, wm[w * 8 + g]);
+        float o = 0.0f, L = 0.0f;
+        for (int w = 0; w < 4; w++)
+            if (wl[w * 8 + g] > 0.0f) {
+                const float f = __builtin_amdgcn_exp2f((wm[w * 8 + g] - M) * QP_LOG2E);
+                o = fmaf(f, wacc[(w * G + g) * HD + d], o);
+                L = fmaf(f, wl[w * 8 + g], L);
             }
-            if (tpp == 2) dot += __shfl_xor(dot, 1, 64);
-            const float s = valid ? dot * a.scale : -3.0e38f;
-            float mx = s;
-            for (uint32_t msk = tpp; msk < 32 * tpp; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
-            const float mt = fmaxf(m, mx);
-            const float p = valid ? expf(s - mt) : 0.0f;
-            float sum = part == 0 ? p : 0.0f;
-            for (uint32_t msk = 1; msk < 32 * tpp; msk <<= 1) sum += __shfl_xor(sum, msk, 64);
-            const float corr = expf(m - mt);
-            l = l * corr + sum;
-            m = mt;
-            if (part == 0) ps[sg * TK + j] = p;
-            if (part == 0 && j == 0) cr[sg] = corr;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int c = 0; c < MAXO; c++) {
-            const uint32_t o = tid + 256 * c;
-            if (o < G * HD) {
-                const uint32_t g = o / HD, dd = o % HD;
-                float v = acc[c] * cr[g];
-                const float* pr = ps + g * TK;
-#pragma unroll 8
-                for (int jj = 0; jj < TK; jj++) v = fmaf(pr[jj], vs[jj * HD + dd], v);
-                acc[c] = v;
-            }
-        }
-    }
-    const uint32_t h0 = kvh * G;
-    if (scorer && part == 0 && j == 0) {
-        const uint64_t i = (uint64_t)(h0 + sg) * a.nsplit + sp;
-        gstore<float>(a.part_ml + 8 * i, m);
-        gstore<float>(a.part_ml + 8 * i + 4, l);
-    }
-#pragma unroll
-    for (int c = 0; c < MAXO; c++) {
-        const uint32_t o = tid + 256 * c;
-        if (o < G * HD) {
-            const uint32_t g = o / HD, dd = o % HD;
-            gstore<float>(a.part_o + 4 * (((uint64_t)(h0 + g) * a.nsplit + sp) * HD + dd), acc[c]);
+        const uint64_t i = (uint64_t)(h0 + g) * a.nsplit + wg;
+        gstore<float>(a.part_o + 4 * (i * HD + d), o);
+        if (d == 0) {
+            gstore<float>(a.part_ml + 8 * i, M);
+            gstore<float>(a.part_ml + 8 * i + 4, L);
         }
     }
 }
 
-KERNEL __launch_bounds__(256) void qp_dec_attn_hd64(QpDecAttnArgs a) { attn_dec_body<64>(a); }
-KERNEL __launch_bounds__(256) void qp_dec_attn_hd128(QpDecAttnArgs a) { attn_dec_body<128>(a); }
+#define DEC_ATTN_KERNEL(HD, KV, F16, G) \
+    KERNEL __launch_bounds__(256) void qp_dec_attn_h##HD##_##KV##_g##G(QpDecAttnArgs a) { attn_dec_body<HD, F16, G>(a); }
+#define DEC_ATTN_KERNELS(HD, KV, F16) \
+    DEC_ATTN_KERNEL(HD, KV, F16, 1) DEC_ATTN_KERNEL(HD, KV, F16, 2) DEC_ATTN_KERNEL(HD, KV, F16, 4) DEC_ATTN_KERNEL(HD, KV, F16, 8)
+DEC_ATTN_KERNELS(64, f16, true)
+DEC_ATTN_KERNELS(64, f32, false)
+DEC_ATTN_KERNELS(128, f16, true)
+DEC_ATTN_KERNELS(128, f32, false)
 
 // Merge of the split partials: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), splits with l = 0 skipped
 // (all of them empty, for a position past the cache: o = 0).
-// grid nh; the per-split weights are computed in parallel, then each output element sums its splits with
-// independent loads.
+// grid nh; every load of the first batch of splits (up to 16 per thread) and of the (m, l) pairs is issued
+// before any of them is used, so the kernel waits for one memory round trip.
 KERNEL __launch_bounds__(256) void qp_dec_attn_comb(QpDecCombArgs a) {
+    constexpr int CB = 16;
     __shared__ float ws[1024];
     __shared__ float red[4];
     __shared__ float part[256];
     const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint64_t ml = a.part_ml + 8ull * h * a.nsplit;
-    float mx = -3.0e38f;
-    for (uint32_t s = tid; s < a.nsplit; s += 256) {
-        const float2 v = gload<float2>(ml + 8ull * s);
-        if (v.y > 0.0f) mx = fmaxf(mx, v.x);
+    const uint32_t ns = a.nsplit, P = 256 / a.hd, d = tid % a.hd, pt = tid / a.hd;
+    const uint64_t ml = a.part_ml + 8ull * h * ns;
+    const uint64_t po = a.part_o + 4ull * h * ns * a.hd;
+    float pv[CB];
+#pragma unroll
+    for (int i = 0; i < CB; i++) {
+        const uint32_t sp = pt + P * i;
+        pv[i] = pt < P && sp < ns ? gload<float>(po + 4ull * ((uint64_t)sp * a.hd + d)) : 0.0f;
     }
+    float2 mv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t sp = tid + 256 * i;
+        mv[i] = sp < ns ? gload<float2>(ml + 8ull * sp) : make_float2(-3.0e38f, 0.0f);
+    }
+    float mx = -3.0e38f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (mv[i].y > 0.0f) mx = fmaxf(mx, mv[i].x);
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     float ls = 0.0f;
-    for (uint32_t s = tid; s < a.nsplit; s += 256) {
-        const float2 v = gload<float2>(ml + 8ull * s);
-        const float e = v.y > 0.0f ? expf(v.x - M) : 0.0f;
-        ws[s] = e;
-        ls += v.y * e;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t sp = tid + 256 * i;
+        const float e = mv[i].y > 0.0f ? expf(mv[i].x - M) : 0.0f;
+        if (sp < ns) ws[sp] = e;
+        ls += mv[i].y * e;
     }
     ls = wave_sum(ls);
     if (lane == 0) red[wave] = ls;
     __syncthreads();
     const float L = (red[0] + red[1]) + (red[2] + red[3]);
-    const uint32_t P = 256 / a.hd, d = tid % a.hd, pt = tid / a.hd;
     float o = 0.0f;
-    const uint64_t po = a.part_o + 4ull * h * a.nsplit * a.hd;
     if (pt < P) {
-#pragma unroll 8
-        for (uint32_t s = pt; s < a.nsplit; s += P) o = fmaf(ws[s], gload<float>(po + 4ull * ((uint64_t)s * a.hd + d)), o);
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            const uint32_t sp = pt + P * i;
+            if (sp < ns) o = fmaf(ws[sp], pv[i], o);
+        }
+        for (uint32_t sp = pt + P * CB; sp < ns; sp += P)  // more than CB splits per thread: the rest in turn
+            o = fmaf(ws[sp], gload<float>(po + 4ull * ((uint64_t)sp * a.hd + d)), o);
     }
     part[tid] = o;
     __syncthreads();

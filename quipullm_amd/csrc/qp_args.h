@@ -104,6 +104,7 @@ typedef struct {
     uint64_t q, k, v, kc, vc, paso;
     uint64_t qnorm, knorm;      // 0 when absent
     uint64_t part_o, part_ml;   // [nh][nsplit][hd], [nh][nsplit][2]
+    uint64_t freq;              // RoPE frequencies base^(-2j/nrot) as floats [nrot/2], or 0: computed in the kernel
     uint32_t hd, nh, nkv, nsplit;
     float scale, eps, base, esc;
     uint32_t nrot, neox, f16, rows;  // rows: slots of the cache; a position at or past it writes an empty result

@@ -9,6 +9,7 @@
 #include <dlfcn.h>
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -478,9 +479,10 @@ int op_gemv(const Ctx& c) {
     return run_gemv(fmt, a, R, max_wg, nullptr);
 }
 
-// dec_attn: split-K decode attention with fused q/k norm, RoPE and KV append.
+// dec_attn: split-K decode attention with fused q/k norm, RoPE and KV append; partials merged by dec_attn_comb.
 // P{hd, nh, nkv, nsplit, scale, eps, base, esc, nrot, neox, f16, rows}; [paso, q, k, v, kc, vc, qnorm|0,
-// knorm|0, part_o, part_ml].  rows = cache slots (required).
+// knorm|0, part_o, part_ml (, freq)].  rows = cache slots (required); freq = the RoPE frequency table
+// base^(-2j/nrot) rounded to float, [nrot/2] (optional: computed in the kernel when absent).
 int op_dec_attn(const Ctx& c) {
     if (int e = need_bufs(c, 10, "dec_attn")) return e;
     QpDecAttnArgs a = {};
@@ -498,10 +500,11 @@ int op_dec_attn(const Ctx& c) {
     a.rows = c.U(11);
     if (!a.rows) return fail(QP_E_ARG, "dec_attn: P.rows (cache slots) is 0");
     if (a.hd != 64 && a.hd != 128) return fail(QP_E_ARG, "dec_attn: head_dim %u", a.hd);
-    const uint32_t G0 = a.nkv ? a.nh / a.nkv : 0;
-    if (!a.nkv || a.nh % a.nkv || (G0 != 1 && G0 != 2 && G0 != 4 && G0 != 8))
+    if (a.nrot > a.hd || a.nrot % 2) return fail(QP_E_ARG, "dec_attn: nrot=%u", a.nrot);
+    const uint32_t G = a.nkv ? a.nh / a.nkv : 0;
+    if (!a.nkv || a.nh % a.nkv || (G != 1 && G != 2 && G != 4 && G != 8))
         return fail(QP_E_ARG, "dec_attn: nh=%u nkv=%u (group of 1, 2, 4 or 8 query heads)", a.nh, a.nkv);
-    if (!a.nsplit || a.nsplit > 1024) return fail(QP_E_ARG, "dec_attn: nsplit=%u", a.nsplit);
+    if (!a.nsplit || a.nsplit > 1024) return fail(QP_E_ARG, "dec_attn: nsplit=%u (1..1024)", a.nsplit);
     a.paso = c.B(0);
     a.q = c.B(1);
     a.k = c.B(2);
@@ -512,9 +515,18 @@ int op_dec_attn(const Ctx& c) {
     a.knorm = c.B(7);
     a.part_o = c.B(8);
     a.part_ml = c.B(9);
-    const uint32_t tk = 32;  // LDS: q [8][hd] | K tile [32][hd+4] | V tile [32][hd] | p [8][32] | k, v [hd] | corr [8]
-    const uint32_t lds = 4 * (8 * a.hd + tk * (a.hd + 4) + tk * a.hd + 8 * tk + 2 * a.hd + 8);
-    return launch(a.hd == 64 ? K_dec_attn_hd64 : K_dec_attn_hd128, a.nkv, a.nsplit, 1, 256, lds, a);
+    a.freq = c.B(10);
+    const uint32_t gi = G == 1 ? 0 : G == 2 ? 1 : G == 4 ? 2 : 3;
+    static const Kid kt[2][2][4] = {
+        {{K_dec_attn_h64_f32_g1, K_dec_attn_h64_f32_g2, K_dec_attn_h64_f32_g4, K_dec_attn_h64_f32_g8},
+         {K_dec_attn_h64_f16_g1, K_dec_attn_h64_f16_g2, K_dec_attn_h64_f16_g4, K_dec_attn_h64_f16_g8}},
+        {{K_dec_attn_h128_f32_g1, K_dec_attn_h128_f32_g2, K_dec_attn_h128_f32_g4, K_dec_attn_h128_f32_g8},
+         {K_dec_attn_h128_f16_g1, K_dec_attn_h128_f16_g2, K_dec_attn_h128_f16_g4, K_dec_attn_h128_f16_g8}}};
+    const Kid k = kt[a.hd == 128][a.f16 ? 1 : 0][gi];
+    // LDS floats: kn, vn [hd] | freq [hd/2] | q/k norm weights [hd] each | wavefront partials 4*G*hd + 64 (also
+    // holds q [G][hd] before)
+    const uint32_t lds = 4 * (a.hd * 9 / 2 + 4 * G * a.hd + 64);
+    return launch(k, a.nkv, a.nsplit, 1, 256, lds, a);
 }
 
 // dec_attn_comb: P{hd, nh, nsplit}; [paso, part_o, part_ml, o].

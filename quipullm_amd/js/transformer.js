@@ -56,6 +56,7 @@ class ModeloTransformer {
     this.batch = op.batch || 32;                 // tokens per prefill pass (reference transformer.js:10 uses 32)
     this.kvF16 = !!op.kv_f16;                    // f16 KV cache (the reference keeps it in f32)
     this.eagerDecode = !!op.eager_decode;        // fused step dispatched op by op instead of a captured graph
+    this.attnPorSplit = op.attn_keys_per_split || 128;   // decode attention: keys per workgroup at full context
     this.baldosa = op.tiled_prefill !== false;   // config.json "tiled_prefill"
     this.bufs = [];
     this.pos = 0;
@@ -132,9 +133,12 @@ class ModeloTransformer {
     this.xl = B(4 * D, 'xlast');
     this.logits = B(4 * this.vocab, 'logits');
     // decode fast path
-    this.nsplit = Math.max(1, Math.min(Math.ceil(512 / this.nkv), Math.ceil(this.ctx / 32)));
+    // split-K decode attention: workgroups per KV head (each covers ctx / nsplit keys at the longest context)
+    this.nsplit = Math.max(1, Math.min(256, Math.ceil(this.ctx / this.attnPorSplit)));
     this.partO = B(4 * this.nh * this.nsplit * this.hd, 'attn_part_o');
     this.partML = B(8 * this.nh * this.nsplit, 'attn_part_ml');
+    this.ropeFreq = B(4 * Math.max(1, this.nrot / 2), 'rope_freq');
+    gpu.escribir(this.ropeFreq, 0, tablaRope(this.base, this.nrot));
     this.amax = B(8 * AMAX_WG, 'argmax_partials');
     gpu.escribir(this.amax, 0, new Uint8Array(8 * AMAX_WG));
     this.maxGen = op_max_gen(this.meta);
@@ -322,7 +326,8 @@ class ModeloTransformer {
       const c = this.capas[i], gc = this.G.capas[i];
       for (const g of this._gemvPorFormato([{ W: c.wq, mode: STORE, y: this.q }, { W: c.wk, mode: STORE, y: this.k },
         { W: c.wv, mode: STORE, y: this.v }], this.x, c.attnNorm, D)) plan.push([g, 1]);
-      plan.push([gpu.grupo('dec_attn', [uAtt, P, this.q, this.k, this.v, c.kc, c.vc, c.qNorm, c.kNorm, this.partO, this.partML]), 1]);
+      plan.push([gpu.grupo('dec_attn', [uAtt, P, this.q, this.k, this.v, c.kc, c.vc, c.qNorm, c.kNorm, this.partO, this.partML,
+        this.ropeFreq]), 1]);
       plan.push([gpu.grupo('dec_attn_comb', [uComb, P, this.partO, this.partML, this.att]), 1]);
       plan.push([this._gemv([{ W: c.wo, mode: ACC, y: this.x }], this.att, null, qd), 1]);
       if (this.nExp) {
@@ -442,9 +447,17 @@ class ModeloTransformer {
   }
 }
 
+// RoPE frequencies base^(-2j/nrot) for j < nrot/2, each rounded once to float: the exponent is the float
+// quotient of the reference's formula (gpu.js:436), the power is evaluated in double.
+function tablaRope(base, nrot) {
+  const t = new Float32Array(Math.max(1, nrot / 2));
+  for (let j = 0; j < nrot / 2; j++) t[j] = Math.fround(Math.pow(base, Math.fround((-2 * j) / nrot)));
+  return t;
+}
+
 function op_max_gen(meta) {
   const op = meta.options || {};
   return op.max_gen || 4096;
 }
 
-module.exports = { ModeloTransformer: ModeloTransformer };
+module.exports = { ModeloTransformer: ModeloTransformer, tablaRope: tablaRope };

@@ -362,6 +362,12 @@ def test_argmax_ties_nan_negative(quipu, dev, oracle):
 
 
 # ------------------------------------------------------------------------------------------------ attention
+def rope_table(base, nrot):
+    """base^(-2j/nrot) rounded once to float, with the exponent the float quotient (as the JS host builds it)."""
+    ex = (np.float32(-2.0) * np.arange(nrot // 2, dtype=np.float32)) / np.float32(nrot)
+    return np.power(np.float64(np.float32(base)), ex.astype(np.float64)).astype(np.float32)
+
+
 def f16r(a):
     return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
 
@@ -389,13 +395,15 @@ def test_atencion_prefill(quipu, dev, oracle, hd, nh, nkv, T, pos0, f16):
     np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
 
 
+@pytest.mark.parametrize("table", [0, 1])
 @pytest.mark.parametrize("hd,nh,nkv,pos0,nsplit,f16,neox,qk_norm",
                          [(128, 32, 8, 0, 4, 0, 0, 0), (128, 32, 8, 4095, 64, 1, 0, 0), (128, 32, 8, 777, 7, 0, 1, 1),
                           (64, 16, 16, 100, 3, 1, 1, 0), (64, 8, 1, 31, 1, 0, 0, 1), (128, 16, 8, 33, 200, 0, 0, 0),
-                          (64, 32, 4, 2000, 16, 1, 0, 1)])
-def test_dec_attn_fused(quipu, dev, oracle, hd, nh, nkv, pos0, nsplit, f16, neox, qk_norm):
-    """One-token attention with the fused q/k norm + RoPE + KV append, split over the keys and merged; the
-    expected result is the reference op sequence norm_rope(q), norm_rope(k), kv_write, atencion."""
+                          (64, 32, 4, 2000, 16, 1, 0, 1), (128, 32, 4, 1500, 33, 1, 1, 1), (128, 8, 8, 5, 256, 0, 0, 0)])
+def test_dec_attn_fused(quipu, dev, oracle, hd, nh, nkv, pos0, nsplit, f16, neox, qk_norm, table):
+    """One-token attention with the fused q/k norm + RoPE + KV append, split over the keys and merged by
+    dec_attn_comb, with the RoPE frequency table bound or computed in the kernel; the expected result is the
+    reference op sequence norm_rope(q), norm_rope(k), kv_write, atencion."""
     rows = 4100
     kvd = nkv * hd
     rng = np.random.default_rng(21)
@@ -416,8 +424,11 @@ def test_dec_attn_fused(quipu, dev, oracle, hd, nh, nkv, pos0, nsplit, f16, neox
     paso = dev.paso(1, pos0)
     u = [("u", hd), ("u", nh), ("u", nkv), ("u", nsplit), ("f", scale), ("f", eps), ("f", base), ("u", 0),
          ("u", hd), ("u", neox), ("u", f16), ("u", rows)]
-    quipu.dispatch("dec_attn", u, [paso, dev.buf(q), dev.buf(k), dev.buf(v), kcb, vcb,
-                                   dev.buf(qn) if qk_norm else 0, dev.buf(kn) if qk_norm else 0, po, pml])
+    b = [paso, dev.buf(q), dev.buf(k), dev.buf(v), kcb, vcb, dev.buf(qn) if qk_norm else 0,
+         dev.buf(kn) if qk_norm else 0, po, pml]
+    if table:
+        b.append(dev.buf(rope_table(base, hd)))
+    quipu.dispatch("dec_attn", u, b)
     quipu.dispatch("dec_attn_comb", [("u", hd), ("u", nh), ("u", nsplit)], [paso, po, pml, o])
     got = dev.get(o, (nh * hd,))
     qr = oracle.norm_rope(q, qn, nh, hd, qk_norm, neox, eps, base, hd, pos0)
@@ -438,15 +449,44 @@ def test_dec_attn_past_the_cache_reads_and_writes_nothing(quipu, dev):
     hd, nh, nkv, rows, nsplit = 64, 4, 2, 16, 2
     kvd = nkv * hd
     kc = dev.zeros(rows * kvd * 4)
-    po, pml, o = dev.zeros(nh * nsplit * hd * 4), dev.zeros(nh * nsplit * 8), dev.zeros(nh * hd * 4)
+    po, pml = dev.zeros(nh * nsplit * hd * 4), dev.zeros(nh * nsplit * 8)
+    o = dev.buf(np.ones(nh * hd, np.float32))
     one = dev.buf(np.ones(nh * hd, np.float32))
     paso = dev.paso(1, rows)
-    quipu.dispatch("dec_attn", [("u", hd), ("u", nh), ("u", nkv), ("u", nsplit), ("f", 0.125), ("f", 1e-6),
-                                ("f", 1e4), ("u", 0), ("u", hd), ("u", 0), ("u", 0), ("u", rows)],
-                   [paso, one, one, one, kc, kc, 0, 0, po, pml])
+    u = [("u", hd), ("u", nh), ("u", nkv), ("u", nsplit), ("f", 0.125), ("f", 1e-6), ("f", 1e4), ("u", 0), ("u", hd),
+         ("u", 0), ("u", 0), ("u", rows)]
+    quipu.dispatch("dec_attn", u, [paso, one, one, one, kc, kc, 0, 0, po, pml])
     quipu.dispatch("dec_attn_comb", [("u", hd), ("u", nh), ("u", nsplit)], [paso, po, pml, o])
     assert not dev.get(kc, (rows * kvd,)).any()
     assert not dev.get(o, (nh * hd,)).any()
+
+
+def test_dec_attn_consecutive_tokens(quipu, dev, oracle):
+    """Three tokens in a row, each appending its key and attending over everything before it; checked against
+    the reference op sequence."""
+    hd, nh, nkv, nsplit, rows = 128, 32, 8, 16, 64
+    kvd = nkv * hd
+    rng = np.random.default_rng(23)
+    kc = rng.standard_normal((rows, kvd)).astype(np.float32)
+    vc = rng.standard_normal((rows, kvd)).astype(np.float32)
+    kcb, vcb = dev.buf(kc), dev.buf(vc)
+    o = dev.zeros(nh * hd * 4)
+    po, pml = dev.zeros(nh * nsplit * hd * 4), dev.zeros(nh * nsplit * 8)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    u = [("u", hd), ("u", nh), ("u", nkv), ("u", nsplit), ("f", scale), ("f", 1e-5), ("f", 1e4), ("u", 0), ("u", hd),
+         ("u", 0), ("u", 0), ("u", rows)]
+    for pos0 in (40, 41, 42):
+        q = rng.standard_normal(nh * hd).astype(np.float32)
+        k = rng.standard_normal(kvd).astype(np.float32)
+        v = rng.standard_normal(kvd).astype(np.float32)
+        paso = dev.paso(1, pos0)
+        quipu.dispatch("dec_attn", u, [paso, dev.buf(q), dev.buf(k), dev.buf(v), kcb, vcb, 0, 0, po, pml])
+        quipu.dispatch("dec_attn_comb", [("u", hd), ("u", nh), ("u", nsplit)], [paso, po, pml, o])
+        kc[pos0] = oracle.norm_rope(k, None, nkv, hd, 0, 0, 1e-5, 1e4, hd, pos0)
+        vc[pos0] = v
+        want = oracle.attention(oracle.norm_rope(q, None, nh, hd, 0, 0, 1e-5, 1e4, hd, pos0), kc, vc, 1, pos0, nh,
+                                nkv, hd, scale)[0]
+        np.testing.assert_allclose(dev.get(o, (nh * hd,)), want, rtol=5e-5, atol=5e-5)
 
 
 # ------------------------------------------------------------------------------------------------ graphs

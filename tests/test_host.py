@@ -186,6 +186,17 @@ console.log(JSON.stringify(out));
     assert r["greedy"] and not r["notGreedy"] and r["threw"]
 
 
+def test_js_rope_table_matches_double_power():
+    r = node("const t = require(%r); const o = {};"
+             "for (const b of [10000, 500000, 1000000]) for (const n of [64, 128]) o[b + ':' + n] = Array.from(t.tablaRope(b, n));"
+             "console.log(JSON.stringify(o));" % os.path.join(JS, "transformer.js"))
+    for key, vals in r.items():
+        base, nrot = (int(x) for x in key.split(":"))
+        ex = (np.float32(-2.0) * np.arange(nrot // 2, dtype=np.float32)) / np.float32(nrot)
+        want = np.power(np.float64(base), ex.astype(np.float64)).astype(np.float32)
+        np.testing.assert_array_equal(np.array(vals, np.float32), want)
+
+
 def test_js_registry():
     r = node("""
 const e = require(%r);
