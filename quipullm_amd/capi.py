@@ -173,25 +173,26 @@ class Quipu:
 
     # -------------------------------------------------------------- weights (device layout)
     def upload_matrix(self, fmt, raw, N, K):
-        """GGUF blocks of an N x K matrix -> device tensor in this backend's layout (Q6_K and Q8_0 are repacked
-        to planar on the device).  Returns the handle."""
+        """GGUF blocks of an N x K matrix -> device tensor in this backend's layout (repacked on the device: Q4_K
+        and Q6_K to row chunk planes, Q8_0 to planar qs | d).  Returns the handle."""
         raw = np.ascontiguousarray(np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray)) else raw)
         nbytes = device_bytes(fmt, N, K)
         assert raw.nbytes == nbytes, (raw.nbytes, nbytes)
-        if fmt in (F32, Q4_K):
+        if fmt == F32:
             return self.buffer_from(raw)
         staging = self.buffer_from(raw)
         dst = self.alloc(nbytes)
         nb = N * K // BLOCK[fmt][0]
-        self.dispatch("repack_q6k" if fmt == Q6_K else "repack_q8", [("u", nb & 0xFFFFFFFF), ("u", nb >> 32)],
-                      [0, staging, dst])
+        op = {Q4_K: "repack_q4k", Q6_K: "repack_q6k", Q8_0: "repack_q8"}[fmt]
+        self.dispatch(op, [("u", nb & 0xFFFFFFFF), ("u", nb >> 32), ("u", K)], [0, staging, dst])
         self.sync()
         self.free(staging)
         return dst
 
-    def dequant(self, fmt, h, nelem):
+    def dequant(self, fmt, h, nelem, K):
+        """The device tensor h (rows of K elements) dequantized to f32, in element order."""
         y = self.alloc(nelem * 4)
-        self.dispatch("dequant", [("u", fmt), ("u", nelem & 0xFFFFFFFF), ("u", nelem >> 32)], [0, h, y])
+        self.dispatch("dequant", [("u", fmt), ("u", nelem & 0xFFFFFFFF), ("u", nelem >> 32), ("u", K)], [0, h, y])
         out = self.download(y, (nelem,))
         self.free(y)
         return out

@@ -67,31 +67,43 @@ QP_DEV void q4k_scmin_bytes(const uint8_t* s, uint32_t j, uint32_t& sc, uint32_t
     }
 }
 
-QP_DEV float deq_q4k(const uint8_t* blk, uint32_t e) {
+// Q4_K and Q6_K device layout (written by the repack ops at load time).  Row r of a tensor with nb = K/256
+// blocks per row occupies nb*RB bytes starting at r*nb*RB (RB = 144 for Q4_K, 208 for Q6_K).  Inside a row the
+// blocks are stored as 16-byte chunk planes: chunk c (bytes 16c..16c+15 of the GGUF block) of block b sits at
+// c*nb*16 + b*16.  A wavefront lane that owns block b of a row therefore loads its chunk c with one 16-byte
+// load, and the lanes owning consecutive blocks read one contiguous run per plane.  Q6_K keeps its 13 chunks
+// (ql 0..7, qh 8..11, scales 12) in the row; the f16 d of every block goes to a plane [rows][nb] after all rows.
+template <int RB>
+QP_DEV uint8_t kq_byte(const uint8_t* base, uint32_t nb, uint64_t row, uint32_t b, uint32_t i) {
+    return base[row * nb * RB + (i >> 4) * nb * 16 + b * 16 + (i & 15)];
+}
+
+QP_DEV float deq_q4k_dev(const uint8_t* base, uint32_t nb, uint64_t row, uint32_t b, uint32_t e) {
 #pragma clang fp contract(off)
     const uint32_t j = e >> 5, l = e & 31;
+    uint8_t s[12];
+    for (int i = 0; i < 12; i++) s[i] = kq_byte<144>(base, nb, row, b, 4 + i);
     uint32_t sc, mn;
-    q4k_scmin_bytes(blk + 4, j, sc, mn);
-    const float d = h2f(blk[0] | (blk[1] << 8)), dmin = h2f(blk[2] | (blk[3] << 8));
+    q4k_scmin_bytes(s, j, sc, mn);
+    const float d = h2f(kq_byte<144>(base, nb, row, b, 0) | (kq_byte<144>(base, nb, row, b, 1) << 8));
+    const float dmin = h2f(kq_byte<144>(base, nb, row, b, 2) | (kq_byte<144>(base, nb, row, b, 3) << 8));
     const float fd = d * (float)sc;
     const float fm = dmin * (float)mn;
-    const uint32_t q = (blk[16 + (j >> 1) * 32 + l] >> ((j & 1) * 4)) & 15u;
+    const uint32_t q = (kq_byte<144>(base, nb, row, b, 16 + (j >> 1) * 32 + l) >> ((j & 1) * 4)) & 15u;
     const float a = fd * (float)q;
     return a - fm;
 }
 
-// Q6_K element from the planar layout: block index gb of NB blocks at base.
-QP_DEV float deq_q6k_planar(const uint8_t* base, uint64_t NB, uint64_t gb, uint32_t e) {
+// NB = blocks of the whole tensor (rows * nb): the d plane starts at NB*208.
+QP_DEV float deq_q6k_dev(const uint8_t* base, uint32_t nb, uint64_t NB, uint64_t row, uint32_t b, uint32_t e) {
 #pragma clang fp contract(off)
     const uint32_t s = e >> 4, h = e >> 7, r = e & 127, qd = r >> 5, l = r & 31;
-    const uint8_t* ql = base + gb * 128;
-    const uint8_t* qh = base + NB * 128 + gb * 64;
-    const int8_t* sc = reinterpret_cast<const int8_t*>(base + NB * 192 + gb * 16);
-    const uint8_t* dp = base + NB * 208 + gb * 2;
-    const uint32_t lo = (ql[h * 64 + (qd & 1) * 32 + l] >> ((qd >> 1) * 4)) & 15u;
-    const uint32_t hi = (qh[h * 32 + l] >> (qd * 2)) & 3u;
+    const uint32_t lo = (kq_byte<208>(base, nb, row, b, h * 64 + (qd & 1) * 32 + l) >> ((qd >> 1) * 4)) & 15u;
+    const uint32_t hi = (kq_byte<208>(base, nb, row, b, 128 + h * 32 + l) >> (qd * 2)) & 3u;
+    const int8_t sc = (int8_t)kq_byte<208>(base, nb, row, b, 192 + s);
+    const uint8_t* dp = base + NB * 208 + (row * nb + b) * 2;
     const float d = h2f(dp[0] | (dp[1] << 8));
-    const float fd = d * (float)sc[s];
+    const float fd = d * (float)sc;
     const float q = (float)(lo | (hi << 4)) - 32.0f;
     return fd * q;
 }
@@ -105,8 +117,8 @@ QP_DEV float deq_q8_planar(const uint8_t* base, uint64_t NB, uint64_t gb, uint32
 
 // Element k of row `row` of a K-wide matrix in device layout fmt (NB = total blocks of the tensor).
 QP_DEV float deq_elem(uint32_t fmt, const uint8_t* base, uint64_t NB, uint64_t row, uint32_t K, uint32_t k) {
-    if (fmt == QP_Q4_K) return deq_q4k(base + (row * (K >> 8) + (k >> 8)) * 144, k & 255);
-    if (fmt == QP_Q6_K) return deq_q6k_planar(base, NB, row * (K >> 8) + (k >> 8), k & 255);
+    if (fmt == QP_Q4_K) return deq_q4k_dev(base, K >> 8, row, k >> 8, k & 255);
+    if (fmt == QP_Q6_K) return deq_q6k_dev(base, K >> 8, NB, row, k >> 8, k & 255);
     if (fmt == QP_Q8_0) return deq_q8_planar(base, NB, row * (K >> 5) + (k >> 5), k & 31);
     return reinterpret_cast<const float*>(base)[row * K + k];
 }

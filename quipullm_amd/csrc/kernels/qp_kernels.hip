@@ -9,17 +9,35 @@
 #define KERNEL extern "C" __global__
 
 // ====================================================================================== load-time ops
-// Q6_K: GGUF 210-byte blocks -> planar ql | qh | scales | d (one thread per block).
+// GGUF blocks -> the row chunk-plane layout of Q4_K / Q6_K (qp_args.h).  One thread per 16-byte chunk; a.k is
+// the row length (nb = K/256 blocks per row).
+KERNEL __launch_bounds__(256) void qp_repack_q4k(QpRepackArgs a) {
+    const uint64_t NB = a.nblocks, nchunk = NB * 9;
+    const uint32_t nb = a.k >> 8;
+    for (uint64_t t = blockIdx.x * 256ull + threadIdx.x; t < nchunk; t += (uint64_t)gridDim.x * 256ull) {
+        const uint64_t blk = t / 9, row = blk / nb;
+        const uint32_t c = (uint32_t)(t - blk * 9), b = (uint32_t)(blk - row * nb);
+        const uint4 v = cptr<uint4>(a.src)[t];  // GGUF offset blk*144 + c*16
+        mptr<uint4>(a.dst + row * nb * 144 + (uint64_t)c * nb * 16 + b * 16)[0] = v;
+    }
+}
+
 KERNEL __launch_bounds__(256) void qp_repack_q6k(QpRepackArgs a) {
-    const uint64_t NB = a.nblocks;
-    for (uint64_t b = blockIdx.x * 256ull + threadIdx.x; b < NB; b += (uint64_t)gridDim.x * 256ull) {
-        const uint8_t* s = cptr<uint8_t>(a.src) + b * 210;
-        uint8_t* d = mptr<uint8_t>(a.dst);
-        for (int i = 0; i < 128; i++) d[b * 128 + i] = s[i];
-        for (int i = 0; i < 64; i++) d[NB * 128 + b * 64 + i] = s[128 + i];
-        for (int i = 0; i < 16; i++) d[NB * 192 + b * 16 + i] = s[192 + i];
-        d[NB * 208 + b * 2] = s[208];
-        d[NB * 208 + b * 2 + 1] = s[209];
+    const uint64_t NB = a.nblocks, nchunk = NB * 14;
+    const uint32_t nb = a.k >> 8;
+    for (uint64_t t = blockIdx.x * 256ull + threadIdx.x; t < nchunk; t += (uint64_t)gridDim.x * 256ull) {
+        const uint64_t blk = t / 14, row = blk / nb;
+        const uint32_t c = (uint32_t)(t - blk * 14), b = (uint32_t)(blk - row * nb);
+        const uint8_t* src = cptr<uint8_t>(a.src) + blk * 210;  // 210-byte blocks: only 2-byte aligned
+        uint8_t* dst = mptr<uint8_t>(a.dst);
+        if (c < 13) {
+            uint8_t* o = dst + row * nb * 208 + (uint64_t)c * nb * 16 + b * 16;
+            for (int i = 0; i < 16; i++) o[i] = src[c * 16 + i];
+        } else {
+            uint8_t* o = dst + NB * 208 + blk * 2;
+            o[0] = src[208];
+            o[1] = src[209];
+        }
     }
 }
 
@@ -40,20 +58,13 @@ KERNEL __launch_bounds__(256) void qp_fill_u32(QpFillArgs a) {
         mptr<uint32_t>(a.dst)[i] = a.value;
 }
 
-// Whole-tensor dequant to f32 in element order (reference's scalar formula; used for checks).
+// Whole-tensor dequant to f32 in element order, rows of a.k elements (reference's scalar formula; for checks).
 KERNEL __launch_bounds__(256) void qp_dequant(QpDequantArgs a) {
-    const uint32_t epb = a.fmt == QP_Q8_0 ? 32 : (a.fmt == QP_F32 ? 1 : 256);
-    const uint64_t NB = a.nelem / epb;
+    const uint32_t K = a.k;
+    const uint64_t NB = total_blocks(a.fmt, a.nelem / K, K);
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < a.nelem; i += (uint64_t)gridDim.x * 256ull) {
-        // treat the tensor as one row of nelem elements split into blocks
-        const uint64_t blk = i / epb;
-        const uint32_t e = (uint32_t)(i % epb);
-        float v;
-        if (a.fmt == QP_Q4_K) v = deq_q4k(cptr<uint8_t>(a.w) + blk * 144, e);
-        else if (a.fmt == QP_Q6_K) v = deq_q6k_planar(cptr<uint8_t>(a.w), NB, blk, e);
-        else if (a.fmt == QP_Q8_0) v = deq_q8_planar(cptr<uint8_t>(a.w), NB, blk, e);
-        else v = cptr<float>(a.w)[i];
-        mptr<float>(a.y)[i] = v;
+        const uint64_t row = i / K;
+        mptr<float>(a.y)[i] = deq_elem(a.fmt, cptr<uint8_t>(a.w), NB, row, K, (uint32_t)(i - row * K));
     }
 }
 
@@ -123,114 +134,6 @@ struct RowRef {
 // lets the row loop keep the next piece's loads in flight while the current piece is being multiplied.
 template <int FMT, int R>
 struct Piece;
-
-template <int R>
-struct Piece<QP_Q4_K, R> {
-    uint4 hd[R], q0[R], q1[R];
-    static constexpr uint32_t J = 16;  // float4s of x per piece: 8 for sub-block 2g, 8 for sub-block 2g+1
-    static constexpr uint32_t S = 2;   // x sums per piece: sub-block 2g, sub-block 2g+1
-    static QP_DEV uint32_t count(uint32_t K) { return K >> 6; }
-    static QP_DEV uint32_t x_src(uint32_t p, uint32_t j) {
-        const uint32_t b = p >> 2, g = p & 3;
-        return (b * 256 + g * 64 + (j >> 3) * 32) / 4 + (j & 7);
-    }
-    QP_DEV void load(const RowRef (&rr)[R], uint64_t, uint32_t K, uint32_t p) {
-        const uint32_t nb = K >> 8, b = p >> 2, g = p & 3;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint64_t blk = rr[r].base + (rr[r].row * nb + b) * 144;
-            hd[r] = gload<uint4>(blk);
-            q0[r] = gload<uint4>(blk + 16 + g * 32);
-            q1[r] = gload<uint4>(blk + 32 + g * 32);
-        }
-    }
-    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, const float* __restrict__ xsum, uint32_t p,
-                        float (&acc)[R]) const {
-        const uint32_t g = p & 3;
-        float4 xl[8], xh[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            xl[i] = xs[i * npc + p];
-            xh[i] = xs[(8 + i) * npc + p];
-        }
-        const float2 sx = *reinterpret_cast<const float2*>(xsum + 2 * p);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            uint32_t sc0, m0, sc1, m1;
-            q4k_sm(hd[r].y, hd[r].z, hd[r].w, 2 * g, sc0, m0);
-            q4k_sm(hd[r].y, hd[r].z, hd[r].w, 2 * g + 1, sc1, m1);
-            const float d = h2f(hd[r].x & 0xffffu), dm = h2f(hd[r].x >> 16);
-            const uint32_t ws[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
-            float dl[2] = {0.0f, 0.0f}, dh[2] = {0.0f, 0.0f};
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                dl[i & 1] = nib4_fma(ws[i] & 0x0f0f0f0fu, xl[i], dl[i & 1]);
-                dh[i & 1] = nib4_fma((ws[i] >> 4) & 0x0f0f0f0fu, xh[i], dh[i & 1]);
-            }
-            acc[r] += ((d * (float)sc0) * (dl[0] + dl[1]) - (dm * (float)m0) * sx.x) +
-                      ((d * (float)sc1) * (dh[0] + dh[1]) - (dm * (float)m1) * sx.y);
-        }
-    }
-};
-
-template <int R>
-struct Piece<QP_Q6_K, R> {
-    uint4 ql0[R], ql1[R], qh[R];
-    uint2 sc8[R];
-    uint32_t dd[R];
-    static constexpr uint32_t J = 16;  // 4 groups (qd) of 16 consecutive x values
-    static constexpr uint32_t S = 4;   // one x sum per group (for the -32 offset of the quants)
-    static QP_DEV uint32_t count(uint32_t K) { return K >> 6; }
-    static QP_DEV uint32_t x_src(uint32_t p, uint32_t j) {
-        const uint32_t b = p >> 2, h = (p >> 1) & 1, l0 = (p & 1) * 16;
-        return (b * 256 + h * 128 + (j >> 2) * 32 + l0) / 4 + (j & 3);
-    }
-    QP_DEV void load(const RowRef (&rr)[R], uint64_t NB, uint32_t K, uint32_t p) {
-        const uint32_t nb = K >> 8, b = p >> 2, h = (p >> 1) & 1, l0 = (p & 1) * 16;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint64_t gb = rr[r].row * nb + b;
-            const uint64_t base = rr[r].base;
-            ql0[r] = gload<uint4>(base + gb * 128 + h * 64 + l0);
-            ql1[r] = gload<uint4>(base + gb * 128 + h * 64 + 32 + l0);
-            qh[r] = gload<uint4>(base + NB * 128 + gb * 64 + h * 32 + l0);
-            sc8[r] = gload<uint2>(base + NB * 192 + gb * 16 + h * 8);
-            dd[r] = gload<uint16_t>(base + NB * 208 + gb * 2);
-        }
-    }
-    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, const float* __restrict__ xsum, uint32_t p,
-                        float (&acc)[R]) const {
-        const uint32_t odd = p & 1;
-        float4 xv[4][4];
-#pragma unroll
-        for (int qd = 0; qd < 4; qd++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) xv[qd][i] = xs[(qd * 4 + i) * npc + p];
-        const float4 sx4 = *reinterpret_cast<const float4*>(xsum + 4 * p);
-        const float sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const float d = h2f(dd[r]);
-            float a = 0.0f;
-#pragma unroll
-            for (int qd = 0; qd < 4; qd++) {
-                const uint4 lo = (qd & 1) ? ql1[r] : ql0[r];
-                const uint32_t nsh = (qd >> 1) * 4, hsh = qd * 2;
-                const uint32_t w0 = ((lo.x >> nsh) & 0x0f0f0f0fu) | (((qh[r].x >> hsh) & 0x03030303u) << 4);
-                const uint32_t w1 = ((lo.y >> nsh) & 0x0f0f0f0fu) | (((qh[r].y >> hsh) & 0x03030303u) << 4);
-                const uint32_t w2 = ((lo.z >> nsh) & 0x0f0f0f0fu) | (((qh[r].z >> hsh) & 0x03030303u) << 4);
-                const uint32_t w3 = ((lo.w >> nsh) & 0x0f0f0f0fu) | (((qh[r].w >> hsh) & 0x03030303u) << 4);
-                const float sq = nib4_fma(w1, xv[qd][1], nib4_fma(w0, xv[qd][0], 0.0f)) +
-                                 nib4_fma(w3, xv[qd][3], nib4_fma(w2, xv[qd][2], 0.0f));
-                const uint32_t si = qd * 2 + odd;  // scale byte within the 8 loaded
-                const uint32_t sw = si < 4 ? sc8[r].x : sc8[r].y;
-                const float scf = (float)(int8_t)((sw >> ((si & 3) * 8)) & 0xffu);
-                a += (d * scf) * (sq - 32.0f * sx[qd]);
-            }
-            acc[r] += a;
-        }
-    }
-};
 
 template <int R>
 struct Piece<QP_Q8_0, R> {
@@ -502,11 +405,8 @@ QP_DEV void gemv_seg_body(const QpGemvArgs& a) {
     KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r4(QpGemvArgs a) { gemv_seg_body<FMT, 4>(a); }
 #define GEMV_KERNEL_R8(NAME, FMT) \
     KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r8(QpGemvArgs a) { gemv_seg_body<FMT, 8>(a); }
-GEMV_KERNELS(q4k, QP_Q4_K)
-GEMV_KERNELS(q6k, QP_Q6_K)  // Q6_K holds more registers per row; R = 8 would spill
 GEMV_KERNELS(q8, QP_Q8_0)
 GEMV_KERNELS(f32, QP_F32)
-GEMV_KERNEL_R8(q4k, QP_Q4_K)
 GEMV_KERNEL_R8(q8, QP_Q8_0)
 GEMV_KERNEL_R8(f32, QP_F32)
 
@@ -564,10 +464,445 @@ QP_DEV void gemv_exp_body(const QpGemvExpArgs& a) {
 #define GEMV_EXP_KERNELS(NAME, FMT)                                                                              \
     KERNEL __launch_bounds__(256) void qp_gemv_exp_##NAME##_r2(QpGemvExpArgs a) { gemv_exp_body<FMT, 2>(a); } \
     KERNEL __launch_bounds__(256) void qp_gemv_exp_##NAME##_r4(QpGemvExpArgs a) { gemv_exp_body<FMT, 4>(a); }
-GEMV_EXP_KERNELS(q4k, QP_Q4_K)
-GEMV_EXP_KERNELS(q6k, QP_Q6_K)
 GEMV_EXP_KERNELS(q8, QP_Q8_0)
 GEMV_EXP_KERNELS(f32, QP_F32)
+
+// ====================================================================================== K-quant GEMV (one token)
+// Q4_K / Q6_K y = W.x for one token: the fused `gemv` op and the reference's matmul_q4k_1 / matmul_q6k_1
+// (kquants.js:188-251) and gathered-expert matmul_q4k_e / matmul_q6k_e (kquants.js:256-304).
+//
+// One lane owns one super-block (256 weights) of a row.  With the row chunk-plane layout (qp_args.h) the lane's
+// 9 (Q4_K) or 13 + 1 (Q6_K) loads are 16-byte loads whose lanes read contiguous runs, and the block header needs
+// no exchange between lanes.  A load instruction covers S = 64/nbp rows (nbp = nb rounded up to a power of two;
+// lanes past nb idle); a "unit" is the R rows per lane that share one pass over the staged input.  Weights are
+// read through a buffer resource so that a lane without a row (past the segment) passes an offset past the end
+// and costs no memory traffic.  The input vector is staged once per workgroup in LDS (block b's 64 float4 at
+// b*65: the one-float4 pad spreads the lanes' 16-byte reads over the banks) with per-group sums of x; its global
+// loads are issued before the first unit's weight loads and awaited on their own.  The dot products use the f16
+// form of a nibble: (w & 0x000f000f) holds two f16 subnormals q*2^-24, which v_fma_mix multiplies exactly by
+// the f32 x; the power of two is taken out of each sub-block sum.  Results are written after the unit loop: a
+// store in flight would make every later load wait for it.
+//
+// Semantics per row follow the reference's factoring: y = sum over sub-blocks of (d*sc)*sum(q*x) - (dmin*m)*sum(x)
+// (Q4_K) and (d*sc)*(sum(q*x) - 32*sum(x)) over 16-element groups (Q6_K); the summation order is this kernel's.
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <int FMT>
+struct KQ;
+template <>
+struct KQ<QP_Q4_K> {
+    static constexpr int CPB = 9, RB = 144, LOADS = 9, GROUP = 32;  // GROUP: elements per x sum
+};
+template <>
+struct KQ<QP_Q6_K> {
+    static constexpr int CPB = 13, RB = 208, LOADS = 14, GROUP = 16;
+};
+
+template <int FMT, int R>
+struct KUnit {
+    u32x4 c[R][KQ<FMT>::CPB];
+    uint32_t d[R];  // Q6_K: the block's f16 d
+};
+
+// acc + (f16 half SEL of m) * x, in one v_fma_mix_f32 (the f16 operand may be subnormal).
+template <int SEL>
+QP_DEV float fmix(uint32_t m, float x, float acc) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 h = __builtin_bit_cast(h2, m);
+    return fmaf((float)(SEL ? h.y : h.x), x, acc);
+}
+
+// v is produced before this point and no memory access moves across it: keeps the compiler from hoisting every
+// LDS read of the input above the arithmetic that consumes the previous ones (the reads are loop-invariant).
+QP_DEV void kq_fence(float& v) { asm volatile("" : "+v"(v)::"memory"); }
+
+QP_DEV __amdgpu_buffer_rsrc_t kq_rsrc(uint64_t base, uint64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+
+// Bytes of LDS the K-quant GEMV uses for a K-wide input (staged x + group sums + reduction slots).
+QP_DEV uint32_t kq_lds_offset_sum(uint32_t K) { return (K >> 8) * 65 * 16; }
+
+// One segment as the unit loop sees it (wave-uniform).
+struct KSeg {
+    uint64_t w, w2, y;
+    uint32_t n, row_base, rows_total, mode, u0;
+};
+
+template <int FMT, int R>
+QP_DEV void kq_dot_q4k(const KUnit<FMT, R>& B, const float4* xb4, const float* xsb, float (&tot)[R]) {
+    const float4 sa = *reinterpret_cast<const float4*>(xsb);
+    const float4 sb = *reinterpret_cast<const float4*>(xsb + 4);
+    const float sxs[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+#pragma unroll
+    for (int p = 0; p < 4; p++) {  // sub-block pair: quant bytes p*32..p*32+31, chunks 1+2p, 2+2p
+        float alo[R], ahi[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) alo[r] = ahi[r] = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {  // elements l = 16h..16h+15 of sub-blocks 2p (low nibbles), 2p+1 (high)
+            float4 x0[4], x1[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                x0[i] = xb4[(2 * p) * 8 + 4 * h + i];
+                x1[i] = xb4[(2 * p + 1) * 8 + 4 * h + i];
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const u32x4 qq = B.c[r][1 + 2 * p + h];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t wv = qq[i];  // bytes l, l+1, l+2, l+3
+                    const uint32_t m0 = wv & 0x000f000fu, m1 = wv & 0x00f000f0u;
+                    const uint32_t tw = wv >> 8;
+                    const uint32_t m2 = tw & 0x000f000fu, m3 = tw & 0x00f000f0u;
+                    alo[r] = fmix<0>(m0, x0[i].x, alo[r]);
+                    alo[r] = fmix<0>(m2, x0[i].y, alo[r]);
+                    alo[r] = fmix<1>(m0, x0[i].z, alo[r]);
+                    alo[r] = fmix<1>(m2, x0[i].w, alo[r]);
+                    ahi[r] = fmix<0>(m1, x1[i].x, ahi[r]);
+                    ahi[r] = fmix<0>(m3, x1[i].y, ahi[r]);
+                    ahi[r] = fmix<1>(m1, x1[i].z, ahi[r]);
+                    ahi[r] = fmix<1>(m3, x1[i].w, ahi[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                kq_fence(alo[r]);
+                kq_fence(ahi[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const u32x4 hd = B.c[r][0];
+            const float d = h2f(hd[0] & 0xffffu), dm = h2f(hd[0] >> 16);
+            uint32_t sc0, mn0, sc1, mn1;
+            q4k_sm(hd[1], hd[2], hd[3], 2 * p, sc0, mn0);
+            q4k_sm(hd[1], hd[2], hd[3], 2 * p + 1, sc1, mn1);
+            // low nibbles were summed as q*2^-24, high nibbles as 16q*2^-24
+            tot[r] += (d * (float)sc0) * (alo[r] * 16777216.0f) - (dm * (float)mn0) * sxs[2 * p];
+            tot[r] += (d * (float)sc1) * (ahi[r] * 1048576.0f) - (dm * (float)mn1) * sxs[2 * p + 1];
+        }
+    }
+}
+
+template <int FMT, int R>
+QP_DEV void kq_dot_q6k(const KUnit<FMT, R>& B, const float4* xb4, const float* xsb, float (&tot)[R]) {
+    // element (h, qd, l): ql chunk h*4 + (qd&1)*2 + l/16, nibble qd>>1; qh chunk 8 + h*2 + l/16, bits 2qd;
+    // scale s = h*8 + qd*2 + l/16 (chunk 12)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int lh = 0; lh < 2; lh++) {
+            float aq[R][4];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int qd = 0; qd < 4; qd++) aq[r][qd] = 0.0f;
+#pragma unroll
+            for (int qd = 0; qd < 4; qd++) {
+                float4 xv[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) xv[c] = xb4[(h * 128 + qd * 32 + lh * 16) / 4 + c];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const u32x4 lo = B.c[r][h * 4 + (qd & 1) * 2 + lh];
+                    const u32x4 hi = B.c[r][8 + h * 2 + lh];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const uint32_t q = ((lo[c] >> ((qd >> 1) * 4)) & 0x0f0f0f0fu) |
+                                           (((hi[c] >> (qd * 2)) & 0x03030303u) << 4);
+                        const uint32_t e = __builtin_amdgcn_perm(0u, q, 0x0c020c00u);  // bytes 0, 2 as f16 halves
+                        const uint32_t o = __builtin_amdgcn_perm(0u, q, 0x0c030c01u);  // bytes 1, 3
+                        aq[r][qd] = fmix<0>(e, xv[c].x, aq[r][qd]);
+                        aq[r][qd] = fmix<0>(o, xv[c].y, aq[r][qd]);
+                        aq[r][qd] = fmix<1>(e, xv[c].z, aq[r][qd]);
+                        aq[r][qd] = fmix<1>(o, xv[c].w, aq[r][qd]);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < R; r++) kq_fence(aq[r][qd]);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const u32x4 scw = B.c[r][12];
+                const float dd = h2f(B.d[r]);
+#pragma unroll
+                for (int qd = 0; qd < 4; qd++) {
+                    const int si = h * 8 + qd * 2 + lh;
+                    const int sc = (int)(int8_t)((scw[si >> 2] >> ((si & 3) * 8)) & 0xffu);
+                    const float sx = xsb[(h * 128 + qd * 32 + lh * 16) / 16];
+                    tot[r] += (dd * (float)sc) * (aq[r][qd] * 16777216.0f - 32.0f * sx);
+                }
+            }
+        }
+    }
+}
+
+// The unit loop.  seg_at(i) returns segment i (i < nseg); the wave's units are w, w + W, ... < total_units,
+// segment i owning units [u0_i, u0_{i+1}).  XS: x sub-blocks of 32 per thread for staging (K <= XS * 8192).
+template <int FMT, int R, int XS, class SegAt>
+QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t x, uint64_t norm_w, float eps,
+                    uint32_t K, uint64_t amax) {
+    extern __shared__ float4 xs[];
+    float* xsum = reinterpret_cast<float*>(xs + (K >> 8) * 65);
+    __shared__ float red[4];
+    __shared__ uint64_t wbest[4];
+    constexpr int RBT = FMT == QP_Q4_K ? 144 : 210;  // bytes per block of the whole tensor
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    constexpr uint32_t nwv = 4;  // launched with 256 threads
+    const uint32_t nb = K >> 8;
+    uint32_t nbp = 1;
+    while (nbp < nb) nbp <<= 1;
+    const uint32_t S = 64 / nbp, s = lane / nbp, b = lane % nbp;
+    const bool lane_on = b < nb;
+    const uint32_t W = gridDim.x * nwv, w = blockIdx.x * nwv + wave;
+    const uint32_t nmine = w < total_units ? (total_units - 1 - w) / W + 1 : 0;
+    const uint32_t ngrp = K / KQ<FMT>::GROUP;
+
+    // 1. this thread's share of x (and of the norm weight): sub-blocks q = tid + 256 i
+    float4 xr[XS][8], nr[XS][8];
+#pragma unroll
+    for (int i = 0; i < XS; i++) {
+        uint32_t q = tid + 256 * i;
+        q = q < (K >> 5) ? q : 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) xr[i][j] = gload<float4>(x + 128ull * q + 16ull * j);
+        if (norm_w) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) nr[i][j] = gload<float4>(norm_w + 128ull * q + 16ull * j);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. the first unit's weights
+    auto seg_of = [&](uint32_t g) __attribute__((always_inline)) {
+        uint32_t si = 0;
+        for (uint32_t i = 1; i < nseg; i++) si = g >= seg_at(i).u0 ? i : si;
+        return si;
+    };
+    KUnit<FMT, R> buf;
+    auto issue = [&](KUnit<FMT, R>& B, uint32_t n) __attribute__((always_inline)) {
+        const uint32_t g = w + n * W;
+        const bool uv = n < nmine;
+        const KSeg sg = seg_at(seg_of(uv ? g : w));
+        const uint32_t u = (uv ? g : w) - sg.u0;
+        const bool pair = sg.mode == QP_GEMV_SWIGLU;
+        const uint64_t tbytes = (uint64_t)sg.rows_total * nb * RBT;
+        const __amdgpu_buffer_rsrc_t rs0 = kq_rsrc(sg.w, tbytes);
+        const __amdgpu_buffer_rsrc_t rs1 = kq_rsrc(pair ? sg.w2 : sg.w, tbytes);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t lr = pair ? u * S + s : (u * R + r) * S + s;
+            const bool on = uv && lane_on && lr < sg.n;
+            const uint32_t row = sg.row_base + lr;
+            const uint32_t vo = on ? row * nb * KQ<FMT>::RB + b * 16 : 0x80000000u;
+            const __amdgpu_buffer_rsrc_t rs = (pair && r == 1) ? rs1 : rs0;
+#pragma unroll
+            for (int c = 0; c < KQ<FMT>::CPB; c++)
+                B.c[r][c] = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, c * nb * 16, 0);
+            if constexpr (FMT == QP_Q6_K)
+                B.d[r] = __builtin_amdgcn_raw_buffer_load_b16(
+                    rs, on ? sg.rows_total * nb * 208 + (row * nb + b) * 2 : 0x80000000u, 0, 0);
+        }
+    };
+    issue(buf, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        // the x loads are the oldest in flight: wait for them alone
+        constexpr int n = R * KQ<FMT>::LOADS > 63 ? 63 : R * KQ<FMT>::LOADS;
+        __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+    }
+
+    // 3. stage x (times the norm weight) in LDS with the group sums; sum of squares for the norm
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XS; i++) {
+        const uint32_t q = tid + 256 * i;
+        if (q < (K >> 5)) {
+            const uint32_t bb = q >> 3, j = q & 7;
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                float4 v = xr[i][t];
+                if (norm_w) {
+                    ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+                    const float4 nw4 = nr[i][t];
+                    v.x *= nw4.x;
+                    v.y *= nw4.y;
+                    v.z *= nw4.z;
+                    v.w *= nw4.w;
+                }
+                xs[bb * 65 + j * 8 + t] = v;
+                if (t < 4) s0 += (v.x + v.y) + (v.z + v.w);
+                else s1 += (v.x + v.y) + (v.z + v.w);
+            }
+            if constexpr (FMT == QP_Q4_K) {
+                xsum[q] = s0 + s1;
+            } else {
+                xsum[2 * q] = s0;
+                xsum[2 * q + 1] = s1;
+            }
+        }
+    }
+    if (norm_w) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+    }
+    __syncthreads();
+    float inv = 1.0f;
+    if (norm_w) {
+        float t = 0.0f;
+        for (uint32_t i = 0; i < nwv; i++) t += red[i];
+        inv = 1.0f / sqrtf(t / (float)K + eps);
+    }
+    (void)ngrp;
+
+    // 4. units
+    constexpr int NO = 2;  // deferred outputs: lane L of register k holds output L + 64k of this wave
+    float outv[NO];
+    uint32_t outk[NO];     // segment << 28 | row within the segment
+#pragma unroll
+    for (int k = 0; k < NO; k++) {
+        outv[k] = 0.0f;
+        outk[k] = 0;
+    }
+    uint32_t nout = 0;
+    uint64_t best = 0;
+    auto flush = [&](bool wait) __attribute__((always_inline)) {
+        for (uint32_t si = 0; si < nseg; si++) {
+            const KSeg sg = seg_at(si);
+#pragma unroll
+            for (int k = 0; k < NO; k++) {
+                if (lane + 64 * k < nout && outk[k] != 0xffffffffu && (outk[k] >> 28) == si) {
+                    QP_GLOBAL float* y = reinterpret_cast<QP_GLOBAL float*>(sg.y) + (outk[k] & 0x0fffffffu);
+                    *y = sg.mode == QP_GEMV_ACC ? *y + outv[k] : outv[k];
+                }
+            }
+        }
+        nout = 0;
+        // a store in flight makes the compiler wait for every later load; drain it here (rare)
+        if (wait) __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xf << 8));
+    };
+    const uint32_t sb = lane_on ? b : 0;
+    const float4* xb4 = xs + sb * 65;
+    const float* xsb = xsum + sb * (256 / KQ<FMT>::GROUP);
+    for (uint32_t n = 0; n < nmine; n++) {
+        asm volatile("" ::: "memory");
+        float tot[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) tot[r] = 0.0f;
+        if constexpr (FMT == QP_Q4_K) kq_dot_q4k<FMT, R>(buf, xb4, xsb, tot);
+        else kq_dot_q6k<FMT, R>(buf, xb4, xsb, tot);
+        const uint32_t g = w + n * W;
+        const uint32_t si = seg_of(g);
+        const KSeg sg = seg_at(si);
+        const uint32_t u = g - sg.u0;
+        const bool pair = sg.mode == QP_GEMV_SWIGLU;
+        issue(buf, n + 1);
+        // reduce over the nbp lanes of each slot, then hand each output to its deferred lane
+        float v[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float t = lane_on ? tot[r] : 0.0f;
+            for (uint32_t m = nbp >> 1; m >= 1; m >>= 1) t += __shfl_xor(t, m, 64);
+            v[r] = t * inv;
+        }
+        const uint32_t nper = pair ? 1 : R;
+        if (nout + nper * S > 64 * NO) flush(true);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if (pair && r > 0) break;
+            const float val = pair ? (v[0] / (1.0f + expf(-v[0]))) * v[R - 1] : v[r];
+            const uint32_t lr0 = pair ? u * S : (u * R + r) * S;
+            const int base = (int)(nout + r * S);
+#pragma unroll
+            for (int k = 0; k < NO; k++) {
+                const int rel = (int)lane + 64 * k - base;
+                const bool slot = rel >= 0 && rel < (int)S;
+                const bool take = slot && lr0 + rel < sg.n;
+                const float vv = __shfl(val, (take ? rel : 0) * (int)nbp, 64);
+                if (take) {
+                    outv[k] = vv;
+                    outk[k] = (si << 28) | (lr0 + rel);
+                    if (sg.mode == QP_GEMV_ARGMAX) {
+                        const uint64_t key = amax_key(vv, lr0 + rel);
+                        best = key > best ? key : best;
+                    }
+                } else if (slot) {
+                    outk[k] = 0xffffffffu;  // a row past the segment: nothing to write
+                }
+            }
+        }
+        nout += nper * S;
+    }
+    flush(false);
+    if (amax) {
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(best >> 32), m, 64) << 32) |
+                               (uint32_t)__shfl_xor((int)(uint32_t)best, m, 64);
+            best = o > best ? o : best;
+        }
+        if (lane == 0) wbest[wave] = best;
+        __syncthreads();
+        if (tid == 0) {
+            uint64_t bb = wbest[0];
+            for (uint32_t i = 1; i < nwv; i++) bb = wbest[i] > bb ? wbest[i] : bb;
+            mptr<uint64_t>(amax)[blockIdx.x] = bb;
+        }
+    }
+}
+
+template <int FMT, int R, int XS>
+QP_DEV void kq_gemv_seg(const QpGemvArgs& a) {
+    auto seg_at = [&](uint32_t i) __attribute__((always_inline)) {
+        const QpGemvSeg& q = a.seg[i];
+        return KSeg{q.w, q.w2, q.y, q.n, q.row_base, q.rows_total, q.mode, q.wg0};
+    };
+    const uint32_t xrow = a.last_row ? paso_T(a.paso) - 1 : 0;
+    kq_gemv<FMT, R, XS>(seg_at, a.nseg, a.total_wg, a.x + 4ull * xrow * a.k, a.norm_w, a.eps, a.k, a.amax);
+}
+
+// Gathered expert GEMV: grid.y = job, job z uses expert sel[z] and input row z / tfijo.
+template <int FMT, int R, int XS>
+QP_DEV void kq_gemv_exp(const QpGemvExpArgs& a) {
+    const uint32_t njobs = a.njobs_fixed ? a.njobs_fixed : paso_T(a.paso) * a.kused;
+    const uint32_t job = blockIdx.y;
+    if (job >= njobs) return;
+    uint32_t ex = cptr<uint32_t>(a.sel)[job];
+    if (ex >= a.n_exp) ex = a.n_exp - 1;  // routing only produces valid experts; never read outside the tensor
+    const bool pair = a.mode == QP_GEMV_SWIGLU;
+    const KSeg one{a.w, a.w2, a.y + 4ull * job * a.n, a.n, ex * a.n, a.n_exp * a.n,
+                   pair ? (uint32_t)QP_GEMV_SWIGLU : (uint32_t)QP_GEMV_STORE, 0};
+    uint32_t nbp = 1;
+    while (nbp < (a.k >> 8)) nbp <<= 1;
+    const uint32_t rpu = (pair ? 1 : R) * (64 / nbp);
+    const uint32_t units = (a.n + rpu - 1) / rpu;
+    kq_gemv<FMT, R, XS>([&](uint32_t) __attribute__((always_inline)) { return one; }, 1, units,
+                        a.x + 4ull * (job / a.tfijo) * a.k, 0, 0.0f, a.k, 0);
+}
+
+#define KQ_KERNELS(NAME, FMT)                                                                                     \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void qp_gemv_##NAME##_r1(           \
+        QpGemvArgs a) { kq_gemv_seg<FMT, 1, 1>(a); }                                                              \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_gemv_##NAME##_r2(           \
+        QpGemvArgs a) { kq_gemv_seg<FMT, 2, 1>(a); }                                                              \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_gemv_##NAME##_r1x2(         \
+        QpGemvArgs a) { kq_gemv_seg<FMT, 1, 2>(a); }                                                              \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_gemv_##NAME##_r2x2(         \
+        QpGemvArgs a) { kq_gemv_seg<FMT, 2, 2>(a); }                                                              \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void qp_gemv_exp_##NAME##_r1(       \
+        QpGemvExpArgs a) { kq_gemv_exp<FMT, 1, 1>(a); }                                                           \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_gemv_exp_##NAME##_r2(       \
+        QpGemvExpArgs a) { kq_gemv_exp<FMT, 2, 1>(a); }                                                           \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_gemv_exp_##NAME##_r1x2(     \
+        QpGemvExpArgs a) { kq_gemv_exp<FMT, 1, 2>(a); }                                                           \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_gemv_exp_##NAME##_r2x2(     \
+        QpGemvExpArgs a) { kq_gemv_exp<FMT, 2, 2>(a); }
+KQ_KERNELS(q4k, QP_Q4_K)
+KQ_KERNELS(q6k, QP_Q6_K)
 
 // ====================================================================================== multi-token GEMM
 // Prefill y[t][r] (+)= W[r].x[t] for T tokens (reference matmul_*_4 and the tiled matmul_*_t,

@@ -12,8 +12,10 @@
 
 // Device layouts (private to the ops that read them; produced at load time by the repack ops):
 //  F32  : [N][K] floats.
-//  Q4_K : the GGUF blocks unchanged, [N][K/256][144 B]; 144 = 9*16 so every block is 16-byte aligned.
-//  Q6_K : planar over the NB = N*K/256 blocks: ql [NB][128] | qh [NB][64] | scales [NB][16] | d [NB] f16.
+//  Q4_K : per row of nb = K/256 blocks, 9 planes of 16-byte chunks: chunk c of block b at row*nb*144 + c*nb*16 +
+//         b*16 (chunk 0 = d, dmin, 12 scale bytes; chunks 1..8 = the 128 quant bytes).
+//  Q6_K : per row, 13 chunk planes (ql 0..7, qh 8..11, scales 12) at row*nb*208 + c*nb*16 + b*16, then after all
+//         rows a plane of the f16 d values [rows][nb].
 //  Q8_0 : planar over NB = N*K/32 blocks: qs [NB][32] int8 | d [NB] f16.
 // Planar sub-arrays start at multiples of 16 bytes, so every lane load is a 16-byte vector load.
 
@@ -122,7 +124,7 @@ typedef struct { uint64_t amax, ids, tokens, step, paso; uint32_t count, advance
 // Plain argmax over n floats (lowest index wins ties; NaN never chosen) -> out[0].
 typedef struct { uint64_t v, out; uint32_t n, pad; } QpArgmaxArgs;
 
-// Load-time repacks from the GGUF block layout to the device layout.
-typedef struct { uint64_t src, dst; uint64_t nblocks; } QpRepackArgs;
+// Load-time repacks from the GGUF block layout to the device layout (k: row length, for Q4_K / Q6_K).
+typedef struct { uint64_t src, dst; uint64_t nblocks; uint32_t k, pad; } QpRepackArgs;
 typedef struct { uint64_t dst; uint64_t count; uint32_t value, pad; } QpFillArgs;
-typedef struct { uint64_t w, y; uint32_t fmt, pad; uint64_t nelem; } QpDequantArgs;
+typedef struct { uint64_t w, y; uint32_t fmt, k; uint64_t nelem; } QpDequantArgs;  // k: row length

@@ -162,12 +162,10 @@ int default_r(int fmt) {
     return 2;
 }
 
-Kid gemv_kid(int fmt, int R) {
-    int f = fmt == QP_Q4_K ? 0 : fmt == QP_Q6_K ? 1 : fmt == QP_Q8_0 ? 2 : 3;
+Kid gemv_kid(int fmt, int R) {  // the generic kernels (Q8_0, F32)
+    int f = fmt == QP_Q8_0 ? 0 : 1;
     int r = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : 3;
-    static const Kid t[4][4] = {{K_gemv_q4k_r1, K_gemv_q4k_r2, K_gemv_q4k_r4, K_gemv_q4k_r8},
-                                {K_gemv_q6k_r1, K_gemv_q6k_r2, K_gemv_q6k_r4, K_gemv_q6k_r4},
-                                {K_gemv_q8_r1, K_gemv_q8_r2, K_gemv_q8_r4, K_gemv_q8_r8},
+    static const Kid t[2][4] = {{K_gemv_q8_r1, K_gemv_q8_r2, K_gemv_q8_r4, K_gemv_q8_r8},
                                 {K_gemv_f32_r1, K_gemv_f32_r2, K_gemv_f32_r4, K_gemv_f32_r8}};
     return t[f][r];
 }
@@ -190,11 +188,60 @@ uint32_t resident_wgs(Kid k, uint32_t block, uint32_t lds) {
     return n;
 }
 
+// ---- K-quant GEMV (Q4_K / Q6_K): one lane per super-block; a unit is R rows per lane times S = 64/nbp rows per
+// load (nbp = blocks per row rounded up to a power of two).
+uint32_t kq_nbp(uint32_t K) {
+    uint32_t p = 1;
+    while (p < K / 256) p <<= 1;
+    return p;
+}
+uint32_t kq_lds(uint32_t K) { return (K / 256) * 65 * 16 + (K / 16) * 4; }
+uint64_t kq_tensor_bytes(int fmt, uint64_t rows, uint32_t K) { return rows * (K / 256) * (fmt == QP_Q4_K ? 144 : 210); }
+
+Kid kq_kid(int fmt, int R, bool x2, bool expert) {
+    static const Kid t[2][2][2][2] = {
+        {{{K_gemv_q4k_r1, K_gemv_q4k_r1x2}, {K_gemv_q4k_r2, K_gemv_q4k_r2x2}},
+         {{K_gemv_q6k_r1, K_gemv_q6k_r1x2}, {K_gemv_q6k_r2, K_gemv_q6k_r2x2}}},
+        {{{K_gemv_exp_q4k_r1, K_gemv_exp_q4k_r1x2}, {K_gemv_exp_q4k_r2, K_gemv_exp_q4k_r2x2}},
+         {{K_gemv_exp_q6k_r1, K_gemv_exp_q6k_r1x2}, {K_gemv_exp_q6k_r2, K_gemv_exp_q6k_r2x2}}}};
+    return t[expert ? 1 : 0][fmt == QP_Q6_K ? 1 : 0][R == 2 ? 1 : 0][x2 ? 1 : 0];
+}
+
+// Units per segment, then the grid: one unit per wavefront, at most two workgroups per CU (the kernel strides
+// over further units); max_wg caps it (the ARGMAX partials hold one entry per workgroup).
+int run_gemv_kq(int fmt, QpGemvArgs& a, uint32_t max_wg, uint32_t* grid_out) {
+    int R = 1;
+    for (uint32_t i = 0; i < a.nseg; i++)
+        if (a.seg[i].mode == QP_GEMV_SWIGLU) R = 2;
+    const uint32_t S = 64 / kq_nbp(a.k);
+    uint32_t total = 0;
+    for (uint32_t i = 0; i < a.nseg; i++) {
+        QpGemvSeg& s = a.seg[i];
+        if (s.n == 0) return fail(QP_E_ARG, "gemv: empty segment %u", i);
+        if (s.rows_total == 0) s.rows_total = s.row_base + s.n;
+        if ((uint64_t)s.row_base + s.n > s.rows_total)
+            return fail(QP_E_ARG, "gemv: segment %u rows %u..%u past the tensor's %u", i, s.row_base, s.row_base + s.n,
+                        s.rows_total);
+        if (kq_tensor_bytes(fmt, s.rows_total, a.k) >= (1ull << 31))
+            return fail(QP_E_ARG, "gemv: tensor of segment %u is 2 GiB or larger", i);
+        s.wg0 = total;  // first unit of the segment
+        total += cdiv(s.n, (s.mode == QP_GEMV_SWIGLU ? 1 : R) * S);
+    }
+    a.total_wg = total;
+    a.rows_per_wg = R * S;
+    uint32_t grid = cdiv(total, 4);
+    if (grid > 2 * (uint32_t)g_cus) grid = 2 * (uint32_t)g_cus;
+    if (max_wg && grid > max_wg) grid = max_wg;
+    if (grid == 0) grid = 1;
+    if (grid_out) *grid_out = grid;
+    return launch(kq_kid(fmt, R, a.k > 8192, false), grid, 1, 1, 256, kq_lds(a.k), a);
+}
+
 // Lays out the segments' workgroups and launches the GEMV kernel of `fmt`.  max_wg caps the grid (the
 // kernel grid-strides over the remaining row groups); 0 = one workgroup per row group.
 int run_gemv(int fmt, QpGemvArgs& a, int R, uint32_t max_wg, uint32_t* grid_out) {
     if (int e = check_k(fmt, a.k, "gemv")) return e;
-    if (fmt == QP_Q6_K && R > 4) R = 4;  // no Q6_K kernel with R = 8 (it would spill)
+    if (fmt == QP_Q4_K || fmt == QP_Q6_K) return run_gemv_kq(fmt, a, max_wg, grid_out);
     uint32_t total = 0;
     for (uint32_t i = 0; i < a.nseg; i++) {
         QpGemvSeg& s = a.seg[i];
@@ -268,7 +315,7 @@ int op_matmul_e(const Ctx& c, int fmt, const char* name, bool swiglu) {
     if (int e = need_bufs(c, nb, name)) return e;
     const uint32_t N = c.U(0), K = c.U(1), tfijo = c.U(3), E = c.U(4);
     if (int e = check_k(fmt, K, name)) return e;
-    if ((fmt == QP_Q6_K || fmt == QP_Q8_0) && E == 0) return fail(QP_E_ARG, "%s: P.E (expert count) is 0", name);
+    if (fmt == QP_Q8_0 && E == 0) return fail(QP_E_ARG, "%s: P.E (expert count) is 0", name);
     if (tfijo == 0) return fail(QP_E_ARG, "%s: tfijo is 0", name);
     if (q8)
         if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)E * N * K / 32, name)) return e;
@@ -288,13 +335,17 @@ int op_matmul_e(const Ctx& c, int fmt, const char* name, bool swiglu) {
     a.njobs_fixed = c.gz;
     a.mode = swiglu ? QP_GEMV_SWIGLU : QP_GEMV_STORE;
     a.n_exp = E;
+    if (fmt == QP_Q4_K || fmt == QP_Q6_K) {
+        if (E == 0) return fail(QP_E_ARG, "%s: P.E (expert count) is 0", name);
+        if (kq_tensor_bytes(fmt, (uint64_t)E * N, K) >= (1ull << 31))
+            return fail(QP_E_ARG, "%s: expert tensor is 2 GiB or larger", name);
+        const int R = swiglu ? 2 : 1;
+        const uint32_t units = cdiv(N, (swiglu ? 1 : R) * (64 / kq_nbp(K)));
+        return launch(kq_kid(fmt, R, K > 8192, true), cdiv(units, 4), c.gz, 1, 256, kq_lds(K), a);
+    }
     const int R = 4;
     const uint32_t outs = (swiglu ? R / 2 : R) * 4;
-    Kid k;
-    if (fmt == QP_Q4_K) k = K_gemv_exp_q4k_r4;
-    else if (fmt == QP_Q6_K) k = K_gemv_exp_q6k_r4;
-    else if (fmt == QP_Q8_0) k = K_gemv_exp_q8_r4;
-    else k = K_gemv_exp_f32_r4;
+    const Kid k = fmt == QP_Q8_0 ? K_gemv_exp_q8_r4 : K_gemv_exp_f32_r4;
     return launch(k, cdiv(N, outs), c.gz, 1, 256, gemv_lds(K), a);
 }
 
@@ -570,14 +621,23 @@ int op_argmax_fin(const Ctx& c) {
     return launch(K_argmax_fin, 1, 1, 1, 256, 0, a);
 }
 
-// repack_q6k / repack_q8: P{nblocks lo, hi}; [paso|0, src, dst].
+// repack_q4k / repack_q6k: P{nblocks lo, hi, K}; repack_q8: P{nblocks lo, hi}; [paso|0, src, dst].  K (the row
+// length) places the blocks in the row chunk-plane layout of Q4_K / Q6_K.
 int op_repack(const Ctx& c, Kid k, const char* name) {
     if (int e = need_bufs(c, 3, name)) return e;
     QpRepackArgs a = {};
     a.nblocks = c.U64(0);
+    a.k = c.U(2);
     a.src = c.B(1);
     a.dst = c.B(2);
-    return launch(k, grid_cap(a.nblocks), 1, 1, 256, 0, a);
+    uint64_t threads = a.nblocks;
+    if (k == K_repack_q4k || k == K_repack_q6k) {
+        if (a.k == 0 || a.k % 256 || a.k > 15360) return fail(QP_E_ARG, "%s: K=%u must be a multiple of 256 <= 15360", name, a.k);
+        if (a.nblocks % (a.k / 256)) return fail(QP_E_ARG, "%s: %llu blocks are not whole rows of K=%u", name,
+                                                 (unsigned long long)a.nblocks, a.k);
+        threads = a.nblocks * (k == K_repack_q4k ? 9 : 14);
+    }
+    return launch(k, grid_cap(threads), 1, 1, 256, 0, a);
 }
 
 // fill_u32: P{value, count lo, hi}; [paso|0, dst].  A kernel, so it may be captured in a graph.
@@ -608,8 +668,13 @@ int op_dequant(const Ctx& c) {
     QpDequantArgs a = {};
     a.fmt = c.U(0);
     a.nelem = c.U64(1);
+    a.k = c.U(3);
     a.w = c.B(1);
     a.y = c.B(2);
+    if (a.k == 0) a.k = (a.fmt == QP_Q8_0) ? 32 : (a.fmt == QP_F32 ? 1 : 256);  // one row per block
+    if (int e = check_k((int)a.fmt, a.k, "dequant")) return e;
+    if (a.nelem % a.k) return fail(QP_E_ARG, "dequant: %llu elements are not whole rows of K=%u",
+                                   (unsigned long long)a.nelem, a.k);
     return launch(K_dequant, grid_cap(a.nelem), 1, 1, 256, 0, a);
 }
 
@@ -651,6 +716,7 @@ void register_ops() {
     v.push_back({"dec_attn_comb", op_dec_attn_comb});
     v.push_back({"argmax", op_argmax});
     v.push_back({"argmax_fin", op_argmax_fin});
+    v.push_back({"repack_q4k", [](const Ctx& c) { return op_repack(c, K_repack_q4k, "repack_q4k"); }});
     v.push_back({"repack_q6k", [](const Ctx& c) { return op_repack(c, K_repack_q6k, "repack_q6k"); }});
     v.push_back({"repack_q8", [](const Ctx& c) { return op_repack(c, K_repack_q8, "repack_q8"); }});
     v.push_back({"fill_u32", op_fill});

@@ -87,13 +87,13 @@ class CargadorPesos {
     return b;
   }
 
-  // Raw blocks -> device layout, repacked on the device for the planar formats.
-  _subirRepack(u8, op, nblocks, etiqueta) {
+  // Raw blocks -> device layout, repacked on the device (Q4_K / Q6_K row chunk planes, Q8_0 planar).
+  _subirRepack(u8, op, nblocks, K, etiqueta) {
     const gpu = this.gpu;
     const staging = gpu.subir(u8, etiqueta + '.raw');
     const dst = gpu.buffer(u8.length, undefined, etiqueta);
     const lo = nblocks % 4294967296, hi = Math.floor(nblocks / 4294967296);
-    despachar(null, gpu.grupo(op, [gpu.uniforme([['u', lo], ['u', hi]]), null, staging, dst]), 1);
+    despachar(null, gpu.grupo(op, [gpu.uniforme([['u', lo], ['u', hi], ['u', K]]), null, staging, dst]), 1);
     gpu.liberar([staging]);
     return dst;
   }
@@ -106,14 +106,14 @@ class CargadorPesos {
       const info = K_QUANTS[t.tipo];
       if (K % 256) throw new Error(nombre + ': K=' + K + ' is not a multiple of 256 (' + info.nombre + ')');
       const u8 = this.bytes(t);
-      const w = info.nombre === 'q6k' ? this._subirRepack(u8, 'repack_q6k', N * K / 256, nombre) : this.gpu.subir(u8, nombre);
+      const w = this._subirRepack(u8, 'repack_' + info.nombre, N * K / 256, K, nombre);
       this.buffers.push(w);
       return { tipo: info.nombre, N: N, K: K, w: w };
     }
     if (t.tipo === 8) {
       if (K % 32) throw new Error(nombre + ': K=' + K + ' is not a multiple of 32');
       const u8 = this.bytes(t);
-      const w = this._subirRepack(u8, 'repack_q8', N * K / 32, nombre);
+      const w = this._subirRepack(u8, 'repack_q8', N * K / 32, K, nombre);
       this.buffers.push(w);
       return { tipo: 'q8', N: N, K: K, w: w, qs: w, ds: vista(w, N * K) };
     }

@@ -82,7 +82,7 @@ def test_dequant_bit_exact(quipu, dev, oracle, fmt, centered):
     N, K = 96, 1024
     raw = raw_matrix(fmt, N, K, 11, centered)
     h = dev.matrix(fmt, raw, N, K)
-    got = quipu.dequant(fmt, h, N * K)
+    got = quipu.dequant(fmt, h, N * K, K)
     want = oracle.dequant(fmt, raw, N * K)
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
