@@ -965,6 +965,248 @@ KERNEL __launch_bounds__(256) void qp_gemm_mt(QpGemmArgs a) {
     }
 }
 
+// ====================================================================================== prefill GEMM on MFMA
+// Y[t][n] (+)= sum_k X[t][k] * W[n][k] for T >= 64 tokens (the reference's tiled matmul_<fmt>_t and
+// matmul_<fmt>_4, kquants.js:309-386 and gpu.js:203-266, when a prefill chunk is large enough for matrix cores).
+//
+// A workgroup computes a 128-token x 128-row tile with v_mfma_f32_32x32x16_bf16: 4 wavefronts in 2 x 2, each
+// 64 x 64 (2 x 2 MFMA blocks).  Per K step of 64 every thread dequantizes 32 weights of one row with the
+// reference's element formula (exact f32) and converts 32 inputs of one token; each value v goes to LDS as
+// bf16 hi = bf16(v) and lo = bf16(v - hi), and the tile accumulates hi*hi + hi*lo + lo*hi in f32, so the
+// products keep about 16 significant bits instead of bf16's 8 (the dropped lo*lo term is 2^-18 relative).  The
+// global loads of step k+1 are issued before the matrix instructions of step k.  Tiles are numbered so that
+// each XCD (workgroup id mod 8) takes a contiguous range of weight tiles with all their token tiles: a weight
+// tile is dequantized from one L2.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+namespace mm {
+constexpr int TM = 128, TN = 128, TK = 64, LDK = 72;  // LDS rows padded to 72 bf16 (144 B)
+}
+
+QP_DEV void split_store(float v, __bf16* hi, __bf16* lo) {
+    const __bf16 h = (__bf16)v;
+    *hi = h;
+    *lo = (__bf16)(v - (float)h);
+}
+
+// Source registers of one thread's 32 weights for one K step (row `row`, k = k0 + koff .. ).
+struct MmW {
+    uint4 a, b, c, d, e;
+    uint32_t f;
+};
+
+template <int FMT>
+QP_DEV void mm_wload(MmW& r, const QpGemmArgs& g, uint32_t row, bool on, uint32_t k0, uint32_t part) {
+    const uint32_t K = g.k;
+    if (!on) row = 0;
+    if constexpr (FMT == QP_Q4_K) {
+        // chunk 1 + 2p + part: bytes 16*part.. of sub-block pair p (16 elements of sub-blocks 2p and 2p+1)
+        const uint32_t nb = K >> 8, b = k0 >> 8, p = (k0 & 255) >> 6;
+        const uint64_t base = g.w + (uint64_t)row * nb * 144 + b * 16;
+        r.a = gload<uint4>(base + (uint64_t)(1 + 2 * p + part) * nb * 16);
+        r.b = gload<uint4>(base);  // header chunk
+    } else if constexpr (FMT == QP_Q6_K) {
+        // qd = 2*kk + part with kk = (k0 & 127) >> 6, h = (k0 & 255) >> 7: 32 elements l = 0..31
+        const uint32_t nb = K >> 8, b = k0 >> 8, h = (k0 & 255) >> 7, qd = 2 * ((k0 & 127) >> 6) + part;
+        const uint64_t base = g.w + (uint64_t)row * nb * 208 + b * 16;
+        const uint32_t cl = h * 4 + (qd & 1) * 2, ch = 8 + h * 2;
+        r.a = gload<uint4>(base + (uint64_t)cl * nb * 16);
+        r.b = gload<uint4>(base + (uint64_t)(cl + 1) * nb * 16);
+        r.c = gload<uint4>(base + (uint64_t)ch * nb * 16);
+        r.d = gload<uint4>(base + (uint64_t)(ch + 1) * nb * 16);
+        r.e = gload<uint4>(base + (uint64_t)12 * nb * 16);
+        const uint64_t NB = (uint64_t)g.n * nb;
+        r.f = gload<uint16_t>(g.w + NB * 208 + ((uint64_t)row * nb + b) * 2);
+    } else if constexpr (FMT == QP_Q8_0) {
+        const uint64_t NB = (uint64_t)g.n * (K >> 5);
+        const uint64_t blk = (uint64_t)row * (K >> 5) + (k0 >> 5) + part;
+        const bool in = k0 + 32 * part < K;
+        const uint64_t bb = in ? blk : (uint64_t)row * (K >> 5);
+        r.a = gload<uint4>(g.w + bb * 32);
+        r.b = gload<uint4>(g.w + bb * 32 + 16);
+        r.f = gload<uint16_t>(g.w + NB * 32 + bb * 2);
+    }
+}
+
+// 32 weights in k order from the loaded registers (F32 reads its row directly).
+template <int FMT>
+QP_DEV void mm_wdeq(const MmW& r, const QpGemmArgs& g, uint32_t row, bool on, uint32_t k0, uint32_t part,
+                    float (&w)[32]) {
+#pragma clang fp contract(off)
+    if constexpr (FMT == QP_Q4_K) {
+        // element order: w[0..15] = sub-block 2p, l = 16*part..; w[16..31] = sub-block 2p+1, same l
+        const uint32_t p = (k0 & 255) >> 6;
+        uint32_t sc0, mn0, sc1, mn1;
+        q4k_sm(r.b.y, r.b.z, r.b.w, 2 * p, sc0, mn0);
+        q4k_sm(r.b.y, r.b.z, r.b.w, 2 * p + 1, sc1, mn1);
+        const float d = h2f(r.b.x & 0xffffu), dm = h2f(r.b.x >> 16);
+        const float fd0 = d * (float)sc0, fm0 = dm * (float)mn0, fd1 = d * (float)sc1, fm1 = dm * (float)mn1;
+        const uint32_t q4[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t byte = (q4[i >> 2] >> ((i & 3) * 8)) & 0xffu;
+            const float a0 = fd0 * (float)(byte & 15u), a1 = fd1 * (float)(byte >> 4);
+            w[i] = a0 - fm0;
+            w[16 + i] = a1 - fm1;
+        }
+    } else if constexpr (FMT == QP_Q6_K) {
+        const uint32_t h = (k0 & 255) >> 7, qd = 2 * ((k0 & 127) >> 6) + part;
+        const uint32_t lo[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+        const uint32_t hi[8] = {r.c.x, r.c.y, r.c.z, r.c.w, r.d.x, r.d.y, r.d.z, r.d.w};
+        const uint32_t scw[4] = {r.e.x, r.e.y, r.e.z, r.e.w};
+        const float d = h2f(r.f);
+        const uint32_t s0 = h * 8 + qd * 2;  // scale of l < 16; s0 + 1 for l >= 16
+        const float fd0 = d * (float)(int8_t)((scw[s0 >> 2] >> ((s0 & 3) * 8)) & 0xffu);
+        const float fd1 = d * (float)(int8_t)((scw[(s0 + 1) >> 2] >> (((s0 + 1) & 3) * 8)) & 0xffu);
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            const uint32_t lb = (lo[l >> 2] >> ((l & 3) * 8 + (qd >> 1) * 4)) & 15u;
+            const uint32_t hb = (hi[l >> 2] >> ((l & 3) * 8 + qd * 2)) & 3u;
+            const float q = (float)(lb | (hb << 4)) - 32.0f;
+            w[l] = (l < 16 ? fd0 : fd1) * q;
+        }
+    } else if constexpr (FMT == QP_Q8_0) {
+        const float d = h2f(r.f);
+        const uint32_t q8[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+        const bool in = k0 + 32 * part < g.k;
+#pragma unroll
+        for (int i = 0; i < 32; i++)
+            w[i] = in ? (float)(int8_t)((q8[i >> 2] >> ((i & 3) * 8)) & 0xffu) * d : 0.0f;
+    } else {
+        const uint32_t kb = k0 + 32 * part;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t k = kb + i;
+            w[i] = (on && k < g.k) ? cptr<float>(g.w)[(uint64_t)row * g.k + k] : 0.0f;
+        }
+    }
+}
+
+template <int FMT>
+QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
+    using namespace mm;
+    __shared__ __bf16 xh[TM * LDK], xl[TM * LDK], wh[TN * LDK], wl[TN * LDK];
+    const uint32_t T = g.tfix ? g.tfix : paso_T(g.paso);
+    const uint32_t N = g.n, K = g.k;
+    // XCD-aware tile order: workgroup i runs on XCD i % 8, as the j-th workgroup of that XCD; XCD x holds
+    // base + (x < rem) of the workgroups, so it takes the contiguous logical tiles starting at x*base + min(x, rem)
+    const uint32_t mt = (uint32_t)gridDim.y, ntl = (uint32_t)gridDim.x;
+    const uint32_t total = mt * ntl, id = blockIdx.y * ntl + blockIdx.x;
+    const uint32_t base = total >> 3, rem = total & 7, xcd = id & 7, j = id >> 3;
+    const uint32_t L = xcd * base + (xcd < rem ? xcd : rem) + j;
+    const uint32_t n_tile = L / mt, m_tile = L - n_tile * mt;
+    const uint32_t t0 = m_tile * TM, n0 = n_tile * TN;
+    if (t0 >= T) return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    // loader roles: token / row = tid >> 1, 32-element part = tid & 1
+    const uint32_t lr = tid >> 1, part = tid & 1;
+    const uint32_t xt = t0 + lr, wr = n0 + lr;
+    const bool xon = xt < T, won = wr < N;
+    const uint64_t xrow = g.x + 4ull * (uint64_t)(xon ? xt : 0) * K;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
+
+    float4 xr[8];
+    MmW wrg;
+    auto load = [&](uint32_t k0) __attribute__((always_inline)) {
+        const uint32_t kb = k0 + 32 * part;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t k = kb + 4 * i;
+            xr[i] = (k < K) ? gload<float4>(xrow + 4ull * k) : float4{0.f, 0.f, 0.f, 0.f};
+        }
+        mm_wload<FMT>(wrg, g, wr, won, k0, part);
+    };
+    const uint32_t nsteps = (K + TK - 1) / TK;
+    load(0);
+    for (uint32_t s = 0; s < nsteps; s++) {
+        const uint32_t k0 = s * TK;
+        // registers -> LDS (bf16 hi / lo)
+        {
+            __bf16* xh_r = xh + lr * LDK + 32 * part;
+            __bf16* xl_r = xl + lr * LDK + 32 * part;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 v = xon ? xr[i] : float4{0.f, 0.f, 0.f, 0.f};
+                split_store(v.x, xh_r + 4 * i + 0, xl_r + 4 * i + 0);
+                split_store(v.y, xh_r + 4 * i + 1, xl_r + 4 * i + 1);
+                split_store(v.z, xh_r + 4 * i + 2, xl_r + 4 * i + 2);
+                split_store(v.w, xh_r + 4 * i + 3, xl_r + 4 * i + 3);
+            }
+            float w[32];
+            mm_wdeq<FMT>(wrg, g, wr, won, k0, part, w);
+            __bf16* wh_r = wh + lr * LDK;
+            __bf16* wl_r = wl + lr * LDK;
+            if constexpr (FMT == QP_Q4_K) {
+                // w[0..15] -> k = 16*part + i (sub-block 2p), w[16..31] -> k = 32 + 16*part + i (sub-block 2p+1)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    split_store(won ? w[i] : 0.f, wh_r + 16 * part + i, wl_r + 16 * part + i);
+                    split_store(won ? w[16 + i] : 0.f, wh_r + 32 + 16 * part + i, wl_r + 32 + 16 * part + i);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 32; i++) split_store(won ? w[i] : 0.f, wh_r + 32 * part + i, wl_r + 32 * part + i);
+            }
+        }
+        __syncthreads();
+        if (s + 1 < nsteps) load(k0 + TK);
+        // 4 k slices of 16: A = x (tokens x k), B = w^T (k x rows)
+#pragma unroll
+        for (int ks = 0; ks < TK / 16; ks++) {
+            const uint32_t kk = ks * 16 + 8 * (lane >> 5);
+            bf16x8 ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+            for (int a = 0; a < 2; a++) {
+                const uint32_t tr = wm * 64 + a * 32 + (lane & 31);
+                ah[a] = *reinterpret_cast<const bf16x8*>(xh + tr * LDK + kk);
+                al[a] = *reinterpret_cast<const bf16x8*>(xl + tr * LDK + kk);
+                const uint32_t nr = wn * 64 + a * 32 + (lane & 31);
+                bh[a] = *reinterpret_cast<const bf16x8*>(wh + nr * LDK + kk);
+                bl[a] = *reinterpret_cast<const bf16x8*>(wl + nr * LDK + kk);
+            }
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[a], bh[b], acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[a], bl[b], acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[a], bh[b], acc[a][b], 0, 0, 0);
+                }
+        }
+        __syncthreads();
+    }
+    // D layout (32 x 32 block): lane holds column lane & 31, rows 8*(v/4) + 4*(lane/32) + v%4
+    float* Y = mptr<float>(g.y);
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const uint32_t n = n0 + wn * 64 + b * 32 + (lane & 31);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const uint32_t t = t0 + wm * 64 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (t < T && n < N) {
+                    float* o = Y + (uint64_t)t * N + n;
+                    *o = g.acc ? *o + acc[a][b][v] : acc[a][b][v];
+                }
+            }
+        }
+}
+
+KERNEL __launch_bounds__(256) void qp_gemm_mfma_q4k(QpGemmArgs a) { gemm_mfma_body<QP_Q4_K>(a); }
+KERNEL __launch_bounds__(256) void qp_gemm_mfma_q6k(QpGemmArgs a) { gemm_mfma_body<QP_Q6_K>(a); }
+KERNEL __launch_bounds__(256) void qp_gemm_mfma_q8(QpGemmArgs a) { gemm_mfma_body<QP_Q8_0>(a); }
+KERNEL __launch_bounds__(256) void qp_gemm_mfma_f32(QpGemmArgs a) { gemm_mfma_body<QP_F32>(a); }
+
 // ====================================================================================== RMSNorm
 // Reference rmsnorm (gpu.js:332-356), same reduction order: 256 threads stride the row, LDS tree 128..1,
 // y = (x * inv) * w.  ultima = 1: only row T-1, written to row 0.

@@ -152,6 +152,11 @@ int q8_planes(uint64_t qs, uint64_t ds, uint64_t nb, const char* op) {
     return 0;
 }
 
+bool getenv_flag(const char* name) {
+    const char* e = getenv(name);
+    return e && *e && strcmp(e, "0") != 0;
+}
+
 int default_r(int fmt) {
     static int env = -2;
     if (env == -2) {
@@ -304,6 +309,12 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
     a.k = K;
     a.acc = acc;
     const uint32_t tmax = c.gz * tokens_per_z;
+    if (tmax >= 64 && !getenv_flag("QP_NO_MFMA")) {
+        // matrix cores: 128 x 128 tiles (the kernel reads T from paso; tiles past it exit)
+        const Kid k = fmt == QP_Q4_K ? K_gemm_mfma_q4k : fmt == QP_Q6_K ? K_gemm_mfma_q6k
+                    : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
+        return launch(k, cdiv(N, 128), cdiv(tmax, 128), 1, 256, 0, a);
+    }
     return launch(K_gemm_mt, cdiv(N, 64), cdiv(tmax ? tmax : 1, 64), 1, 256, 0, a);
 }
 

@@ -61,6 +61,22 @@ def oracle_run(oracle, path, prompt, n, kv_f16):
     return ids, lgs
 
 
+@pytest.mark.parametrize("name", ["mini_llama_q4km_c", "mini_llama_q8_c", "mini_qwen3_q4km_c", "mini_qwen3moe_q4k_c"])
+def test_long_prefill_on_matrix_cores_matches_oracle(oracle, models_dir, tmp_path, name):
+    """A 150-token prompt in one chunk runs the prefill matmuls on MFMA (bf16 hi/lo products); the logits of the
+    prompt's last token and the greedy continuation must still match the oracle."""
+    path = synth.ensure_model(name, models_dir)
+    vocab = oracle.GGUF(path).tensors["token_embd.weight"]["dims"][1]
+    prompt = synth.random_prompt(vocab, 150, 2)
+    n = 8
+    want_ids, want_lg = oracle_run(oracle, path, prompt, n, False)
+    r, lg = generate(path, prompt, n, "fast", "f32", str(tmp_path), ["--batch", "160"])
+    lg = lg.reshape(-1, vocab)
+    errs = [rel(a, b) for a, b in zip(lg, want_lg)]
+    assert r["ids"] == want_ids, (r["ids"], want_ids, errs)
+    assert max(errs) < 1e-3, errs
+
+
 @pytest.mark.parametrize("name", MINI)
 @pytest.mark.parametrize("kv", ["f32", "f16"])
 def test_greedy_matches_oracle(oracle, models_dir, tmp_path, name, kv):

@@ -244,6 +244,30 @@ def test_matmul_multi_token(quipu, dev, oracle, fmt, T, op):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T,N,K,acc", [(200, 300, 2048, 1), (128, 256, 1024, 0), (64, 77, 512, 0),
+                                        (300, 500, 256, 1)])
+def test_matmul_prefill_mfma(quipu, dev, oracle, fmt, T, N, K, acc):
+    """The matrix-core prefill path (T >= 64): bf16 hi/lo products stay within the float32 dot bound, with
+    partial token and row tiles, and tile counts that are not a multiple of the 8 XCDs (3 x 4 = 12 tiles)."""
+    if fmt == capi.Q8_0 and K % 64:
+        K += 32
+    raw = raw_matrix(fmt, N, K, 61)
+    W = (oracle.dequant(fmt, raw, N * K) if fmt != capi.F32 else raw.view(np.float32)).reshape(N, K)
+    x = (np.random.default_rng(12).standard_normal((T, K)) * 3).astype(np.float32)
+    y0 = np.random.default_rng(13).standard_normal((T, N)).astype(np.float32)
+    y = dev.buf(y0)
+    wb = [dev.matrix(fmt, raw, N, K)]
+    if fmt == capi.Q8_0:
+        wb.append(wb[0] + N * K)
+    quipu.dispatch("matmul_%s_t" % capi.FMT_NAME[fmt], [("u", N), ("u", K), ("u", acc), ("u", 0)],
+                   [dev.paso(T, 0)] + wb + [dev.buf(x), y], ((N + 63) // 64, 1, (T + 31) // 32))
+    got = dev.get(y, (T, N))
+    want = (W.astype(np.float64) @ x.astype(np.float64).T).T + (y0 if acc else 0)
+    bound = (np.abs(W.astype(np.float64)) @ np.abs(x.astype(np.float64)).T).T * 2e-5 + 2e-7 * np.abs(y0) + 1e-30
+    assert np.all(np.abs(got - want) <= bound)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 def test_matmul_expert_jobs(quipu, dev, oracle, fmt):
     """matmul_<fmt>_e (one job per selected expert) and the fused gate/up _e_swiglu; tfijo = k routes job z to
     input row z / k."""
