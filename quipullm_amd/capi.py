@@ -235,8 +235,11 @@ class Quipu:
 
 
 def gemv_uniform(nseg, K, eps=0.0, last_row=0, R=0, max_wg=0, fmt=Q4_K, segs=()):
-    """P of the fused `gemv` op: segs = [(mode, n, row_base, rows_total), ...]."""
+    """P of the fused `gemv` op: segs = [(mode, n, row_base, rows_total[, seg_fmt]), ...]; a segment's own format
+    (Q4_K / Q6_K mixed in one launch) rides in bits 8..15 of its mode word."""
     u = [("u", nseg), ("u", K), ("f", eps), ("u", last_row), ("u", R), ("u", max_wg), ("u", fmt), ("u", 0)]
-    for mode, n, rb, rt in segs:
-        u += [("u", mode), ("u", n), ("u", rb), ("u", rt)]
+    for sg in segs:
+        mode, n, rb, rt = sg[:4]
+        sf = sg[4] if len(sg) > 4 else 0
+        u += [("u", mode | (sf << 8)), ("u", n), ("u", rb), ("u", rt)]
     return u

@@ -497,6 +497,13 @@ template <>
 struct KQ<QP_Q6_K> {
     static constexpr int CPB = 13, RB = 208, LOADS = 14, GROUP = 16;
 };
+// Segments of either format in one launch (each unit takes its segment's path; a Q4_K unit issues the Q6_K
+// number of loads, the extra ones past the end, so the wait counts do not depend on the format).
+#define QP_KQ_MIX 255
+template <>
+struct KQ<QP_KQ_MIX> {
+    static constexpr int CPB = 13, RB = 0, LOADS = 14, GROUP = 16;
+};
 
 template <int FMT, int R>
 struct KUnit {
@@ -526,14 +533,27 @@ QP_DEV uint32_t kq_lds_offset_sum(uint32_t K) { return (K >> 8) * 65 * 16; }
 // One segment as the unit loop sees it (wave-uniform).
 struct KSeg {
     uint64_t w, w2, y;
-    uint32_t n, row_base, rows_total, mode, u0;
+    uint32_t n, row_base, rows_total, mode, u0, fmt;
 };
 
-template <int FMT, int R>
-QP_DEV void kq_dot_q4k(const KUnit<FMT, R>& B, const float4* xb4, const float* xsb, float (&tot)[R]) {
-    const float4 sa = *reinterpret_cast<const float4*>(xsb);
-    const float4 sb = *reinterpret_cast<const float4*>(xsb + 4);
-    const float sxs[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+// G16: the x sums are per 16 elements (the mixed launch's layout): a sub-block's sum is the sum of its two halves,
+// the same value the 32-element staging computes.
+template <class U, int R, bool G16 = false>
+QP_DEV void kq_dot_q4k(const U& B, const float4* xb4, const float* xsb, float (&tot)[R]) {
+    float sxs[8];
+    if constexpr (G16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 t = *reinterpret_cast<const float4*>(xsb + 4 * i);
+            sxs[2 * i] = t.x + t.y;
+            sxs[2 * i + 1] = t.z + t.w;
+        }
+    } else {
+        const float4 sa = *reinterpret_cast<const float4*>(xsb);
+        const float4 sb = *reinterpret_cast<const float4*>(xsb + 4);
+        sxs[0] = sa.x; sxs[1] = sa.y; sxs[2] = sa.z; sxs[3] = sa.w;
+        sxs[4] = sb.x; sxs[5] = sb.y; sxs[6] = sb.z; sxs[7] = sb.w;
+    }
 #pragma unroll
     for (int p = 0; p < 4; p++) {  // sub-block pair: quant bytes p*32..p*32+31, chunks 1+2p, 2+2p
         float alo[R], ahi[R];
@@ -586,8 +606,8 @@ QP_DEV void kq_dot_q4k(const KUnit<FMT, R>& B, const float4* xb4, const float* x
     }
 }
 
-template <int FMT, int R>
-QP_DEV void kq_dot_q6k(const KUnit<FMT, R>& B, const float4* xb4, const float* xsb, float (&tot)[R]) {
+template <class U, int R>
+QP_DEV void kq_dot_q6k(const U& B, const float4* xb4, const float* xsb, float (&tot)[R]) {
     // element (h, qd, l): ql chunk h*4 + (qd&1)*2 + l/16, nibble qd>>1; qh chunk 8 + h*2 + l/16, bits 2qd;
     // scale s = h*8 + qd*2 + l/16 (chunk 12)
 #pragma unroll
@@ -648,7 +668,6 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     float* xsum = reinterpret_cast<float*>(xs + (K >> 8) * 65);
     __shared__ float red[4];
     __shared__ uint64_t wbest[4];
-    constexpr int RBT = FMT == QP_Q4_K ? 144 : 210;  // bytes per block of the whole tensor
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     constexpr uint32_t nwv = 4;  // launched with 256 threads
@@ -689,7 +708,9 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         const KSeg sg = seg_at(seg_of(uv ? g : w));
         const uint32_t u = (uv ? g : w) - sg.u0;
         const bool pair = sg.mode == QP_GEMV_SWIGLU;
-        const uint64_t tbytes = (uint64_t)sg.rows_total * nb * RBT;
+        const bool q6 = FMT == QP_KQ_MIX ? sg.fmt == QP_Q6_K : FMT == QP_Q6_K;
+        const uint32_t rb = q6 ? 208 : 144;
+        const uint64_t tbytes = (uint64_t)sg.rows_total * nb * (q6 ? 210 : 144);
         const __amdgpu_buffer_rsrc_t rs0 = kq_rsrc(sg.w, tbytes);
         const __amdgpu_buffer_rsrc_t rs1 = kq_rsrc(pair ? sg.w2 : sg.w, tbytes);
 #pragma unroll
@@ -697,14 +718,15 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
             const uint32_t lr = pair ? u * S + s : (u * R + r) * S + s;
             const bool on = uv && lane_on && lr < sg.n;
             const uint32_t row = sg.row_base + lr;
-            const uint32_t vo = on ? row * nb * KQ<FMT>::RB + b * 16 : 0x80000000u;
+            const uint32_t vo = on ? row * nb * rb + b * 16 : 0x80000000u;
             const __amdgpu_buffer_rsrc_t rs = (pair && r == 1) ? rs1 : rs0;
 #pragma unroll
             for (int c = 0; c < KQ<FMT>::CPB; c++)
-                B.c[r][c] = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, c * nb * 16, 0);
-            if constexpr (FMT == QP_Q6_K)
+                B.c[r][c] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rs, (FMT != QP_KQ_MIX || c < 9 || q6) ? vo : 0x80000000u, c * nb * 16, 0);
+            if constexpr (FMT != QP_Q4_K)
                 B.d[r] = __builtin_amdgcn_raw_buffer_load_b16(
-                    rs, on ? sg.rows_total * nb * 208 + (row * nb + b) * 2 : 0x80000000u, 0, 0);
+                    rs, (on && q6) ? sg.rows_total * nb * 208 + (row * nb + b) * 2 : 0x80000000u, 0, 0);
         }
     };
     issue(buf, 0);
@@ -793,11 +815,17 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         float tot[R];
 #pragma unroll
         for (int r = 0; r < R; r++) tot[r] = 0.0f;
-        if constexpr (FMT == QP_Q4_K) kq_dot_q4k<FMT, R>(buf, xb4, xsb, tot);
-        else kq_dot_q6k<FMT, R>(buf, xb4, xsb, tot);
         const uint32_t g = w + n * W;
         const uint32_t si = seg_of(g);
         const KSeg sg = seg_at(si);
+        if constexpr (FMT == QP_Q4_K) {
+            kq_dot_q4k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
+        } else if constexpr (FMT == QP_Q6_K) {
+            kq_dot_q6k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
+        } else {
+            if (sg.fmt == QP_Q6_K) kq_dot_q6k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
+            else kq_dot_q4k<KUnit<FMT, R>, R, true>(buf, xb4, xsb, tot);
+        }
         const uint32_t u = g - sg.u0;
         const bool pair = sg.mode == QP_GEMV_SWIGLU;
         issue(buf, n + 1);
@@ -859,7 +887,7 @@ template <int FMT, int R, int XS>
 QP_DEV void kq_gemv_seg(const QpGemvArgs& a) {
     auto seg_at = [&](uint32_t i) __attribute__((always_inline)) {
         const QpGemvSeg& q = a.seg[i];
-        return KSeg{q.w, q.w2, q.y, q.n, q.row_base, q.rows_total, q.mode, q.wg0};
+        return KSeg{q.w, q.w2, q.y, q.n, q.row_base, q.rows_total, q.mode, q.wg0, q.fmt};
     };
     const uint32_t xrow = a.last_row ? paso_T(a.paso) - 1 : 0;
     kq_gemv<FMT, R, XS>(seg_at, a.nseg, a.total_wg, a.x + 4ull * xrow * a.k, a.norm_w, a.eps, a.k, a.amax);
@@ -875,7 +903,7 @@ QP_DEV void kq_gemv_exp(const QpGemvExpArgs& a) {
     if (ex >= a.n_exp) ex = a.n_exp - 1;  // routing only produces valid experts; never read outside the tensor
     const bool pair = a.mode == QP_GEMV_SWIGLU;
     const KSeg one{a.w, a.w2, a.y + 4ull * job * a.n, a.n, ex * a.n, a.n_exp * a.n,
-                   pair ? (uint32_t)QP_GEMV_SWIGLU : (uint32_t)QP_GEMV_STORE, 0};
+                   pair ? (uint32_t)QP_GEMV_SWIGLU : (uint32_t)QP_GEMV_STORE, 0, (uint32_t)FMT};
     uint32_t nbp = 1;
     while (nbp < (a.k >> 8)) nbp <<= 1;
     const uint32_t rpu = (pair ? 1 : R) * (64 / nbp);
@@ -903,6 +931,18 @@ QP_DEV void kq_gemv_exp(const QpGemvExpArgs& a) {
         QpGemvExpArgs a) { kq_gemv_exp<FMT, 2, 2>(a); }
 KQ_KERNELS(q4k, QP_Q4_K)
 KQ_KERNELS(q6k, QP_Q6_K)
+KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void qp_gemv_mix_r1(QpGemvArgs a) {
+    kq_gemv_seg<QP_KQ_MIX, 1, 1>(a);
+}
+KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_gemv_mix_r2(QpGemvArgs a) {
+    kq_gemv_seg<QP_KQ_MIX, 2, 1>(a);
+}
+KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_gemv_mix_r1x2(QpGemvArgs a) {
+    kq_gemv_seg<QP_KQ_MIX, 1, 2>(a);
+}
+KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_gemv_mix_r2x2(QpGemvArgs a) {
+    kq_gemv_seg<QP_KQ_MIX, 2, 2>(a);
+}
 
 // ====================================================================================== multi-token GEMM
 // Prefill y[t][r] (+)= W[r].x[t] for T tokens (reference matmul_*_4 and the tiled matmul_*_t,

@@ -203,6 +203,11 @@ uint32_t kq_nbp(uint32_t K) {
 uint32_t kq_lds(uint32_t K) { return (K / 256) * 65 * 16 + (K / 16) * 4; }
 uint64_t kq_tensor_bytes(int fmt, uint64_t rows, uint32_t K) { return rows * (K / 256) * (fmt == QP_Q4_K ? 144 : 210); }
 
+Kid kq_mix_kid(int R, bool x2) {
+    static const Kid t[2][2] = {{K_gemv_mix_r1, K_gemv_mix_r1x2}, {K_gemv_mix_r2, K_gemv_mix_r2x2}};
+    return t[R == 2][x2];
+}
+
 Kid kq_kid(int fmt, int R, bool x2, bool expert) {
     static const Kid t[2][2][2][2] = {
         {{{K_gemv_q4k_r1, K_gemv_q4k_r1x2}, {K_gemv_q4k_r2, K_gemv_q4k_r2x2}},
@@ -216,8 +221,11 @@ Kid kq_kid(int fmt, int R, bool x2, bool expert) {
 // over further units); max_wg caps it (the ARGMAX partials hold one entry per workgroup).
 int run_gemv_kq(int fmt, QpGemvArgs& a, uint32_t max_wg, uint32_t* grid_out) {
     int R = 1;
-    for (uint32_t i = 0; i < a.nseg; i++)
+    bool mixed = false;
+    for (uint32_t i = 0; i < a.nseg; i++) {
         if (a.seg[i].mode == QP_GEMV_SWIGLU) R = 2;
+        if (a.seg[i].fmt != a.seg[0].fmt) mixed = true;
+    }
     const uint32_t S = 64 / kq_nbp(a.k);
     uint32_t total = 0;
     for (uint32_t i = 0; i < a.nseg; i++) {
@@ -227,7 +235,7 @@ int run_gemv_kq(int fmt, QpGemvArgs& a, uint32_t max_wg, uint32_t* grid_out) {
         if ((uint64_t)s.row_base + s.n > s.rows_total)
             return fail(QP_E_ARG, "gemv: segment %u rows %u..%u past the tensor's %u", i, s.row_base, s.row_base + s.n,
                         s.rows_total);
-        if (kq_tensor_bytes(fmt, s.rows_total, a.k) >= (1ull << 31))
+        if (kq_tensor_bytes((int)s.fmt, s.rows_total, a.k) >= (1ull << 31))
             return fail(QP_E_ARG, "gemv: tensor of segment %u is 2 GiB or larger", i);
         s.wg0 = total;  // first unit of the segment
         total += cdiv(s.n, (s.mode == QP_GEMV_SWIGLU ? 1 : R) * S);
@@ -239,7 +247,8 @@ int run_gemv_kq(int fmt, QpGemvArgs& a, uint32_t max_wg, uint32_t* grid_out) {
     if (max_wg && grid > max_wg) grid = max_wg;
     if (grid == 0) grid = 1;
     if (grid_out) *grid_out = grid;
-    return launch(kq_kid(fmt, R, a.k > 8192, false), grid, 1, 1, 256, kq_lds(a.k), a);
+    const Kid kid = mixed ? kq_mix_kid(R, a.k > 8192) : kq_kid((int)a.seg[0].fmt, R, a.k > 8192, false);
+    return launch(kid, grid, 1, 1, 256, kq_lds(a.k), a);
 }
 
 // Lays out the segments' workgroups and launches the GEMV kernel of `fmt`.  max_wg caps the grid (the
@@ -504,7 +513,8 @@ int op_moe_comb(const Ctx& c) {
 
 // ------------------------------------------------------------------------------------------------ backend ops
 // gemv: fused one-token GEMV over up to 4 same-format segments.
-// P{nseg, K, eps, last_row, R, max_wg, fmt, 0, then per segment {mode, n, row_base, rows_total}};
+// P{nseg, K, eps, last_row, R, max_wg, fmt, 0, then per segment {mode | seg_fmt << 8, n, row_base, rows_total}};
+// seg_fmt 0 means fmt; Q4_K and Q6_K segments may share a launch.
 // [paso, x, norm_w|0, amax|0, then per segment w, w2|0, y].
 int op_gemv(const Ctx& c) {
     const uint32_t nseg = c.U(0);
@@ -526,11 +536,14 @@ int op_gemv(const Ctx& c) {
     a.amax = c.B(3);
     for (uint32_t i = 0; i < nseg; i++) {
         QpGemvSeg& s = a.seg[i];
-        s.mode = c.U(8 + 4 * i);
+        const uint32_t mw = c.U(8 + 4 * i);
+        s.mode = mw & 0xffu;
         s.n = c.U(9 + 4 * i);
         s.row_base = c.U(10 + 4 * i);
         s.rows_total = c.U(11 + 4 * i);
-        s.fmt = fmt;
+        s.fmt = (mw >> 8) & 0xffu ? (mw >> 8) & 0xffu : (uint32_t)fmt;  // per-segment format (0: the launch's)
+        if (s.fmt != (uint32_t)fmt && !((s.fmt == QP_Q4_K || s.fmt == QP_Q6_K) && (fmt == QP_Q4_K || fmt == QP_Q6_K)))
+            return fail(QP_E_ARG, "gemv: segment %u format %u cannot share a launch with format %d", i, s.fmt, fmt);
         s.w = c.B(4 + 3 * i);
         s.w2 = c.B(5 + 3 * i);
         s.y = c.B(6 + 3 * i);

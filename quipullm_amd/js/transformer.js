@@ -296,19 +296,22 @@ class ModeloTransformer {
       ['u', opts.maxWg || 0], ['u', fmt], ['u', 0]];
     const b = [this.bPaso, x, norm || null, opts.amax || null];
     for (const s of segs) {
-      if (FMT_ID[s.W.tipo] !== fmt) throw new Error('gemv segments must share one format');
-      u.push(['u', s.mode], ['u', s.W.N], ['u', 0], ['u', s.W.N]);
+      const f = FMT_ID[s.W.tipo];
+      if (f !== fmt && !(KQ.has(s.W.tipo) && KQ.has(segs[0].W.tipo))) throw new Error('gemv segments must share one format');
+      u.push(['u', s.mode | ((f !== fmt ? f : 0) << 8)], ['u', s.W.N], ['u', 0], ['u', s.W.N]);
       b.push(s.W.w, s.W2 ? s.W2.w : null, s.y);
     }
     return gpu.grupo('gemv', [gpu.uniforme(u)].concat(b));
   }
 
-  // GEMV segments grouped by format (one launch per format present).
+  // GEMV segments in as few launches as possible: K-quant formats (Q4_K, Q6_K) share one launch, any other
+  // format gets its own.
   _gemvPorFormato(segs, x, norm, K) {
     const porFmt = new Map();
     for (const s of segs) {
-      if (!porFmt.has(s.W.tipo)) porFmt.set(s.W.tipo, []);
-      porFmt.get(s.W.tipo).push(s);
+      const clave = KQ.has(s.W.tipo) ? 'kq' : s.W.tipo;
+      if (!porFmt.has(clave)) porFmt.set(clave, []);
+      porFmt.get(clave).push(s);
     }
     const out = [];
     for (const lista of porFmt.values()) out.push(this._gemv(lista, x, norm, K));

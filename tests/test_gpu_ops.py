@@ -150,6 +150,27 @@ def test_gemv_segments_norm_and_persistent_grid(quipu, dev, oracle, fmt, R):
         assert np.all(np.abs(got - w_) <= b)
 
 
+@pytest.mark.parametrize("K", [1024, 4096, 12288])
+def test_gemv_mixed_k_quant_segments(quipu, dev, oracle, K):
+    """Q, K (Q4_K) and V (Q6_K) of the Q4_K_M models in one launch over one RMS-normalized input."""
+    x = (np.random.default_rng(14).standard_normal(K) * 2).astype(np.float32)
+    nw = (1 + 0.2 * np.random.default_rng(15).standard_normal(K)).astype(np.float32)
+    eps = 1e-5
+    xn = oracle.rmsnorm(x[None], nw, eps)[0]
+    segs, bufs, checks = [], [], []
+    for i, (fmt, n) in enumerate([(capi.Q4_K, 200), (capi.Q4_K, 72), (capi.Q6_K, 72)]):
+        raw = raw_matrix(fmt, n, K, 80 + i)
+        W = oracle.dequant(fmt, raw, n * K).reshape(n, K)
+        y = dev.zeros(n * 4)
+        segs.append((capi.STORE, n, 0, n, fmt))
+        bufs += [dev.matrix(fmt, raw, n, K), 0, y]
+        checks.append((y, n, oracle.matmul(fmt, raw, n, K, xn)[0], dot_bound(W, xn, 3e-5)))
+    u = capi.gemv_uniform(3, K, eps=eps, fmt=capi.Q4_K, segs=segs)
+    quipu.dispatch("gemv", u, [dev.paso(1, 0), dev.buf(x), dev.buf(nw), 0] + bufs)
+    for y, n, want, bound in checks:
+        assert np.all(np.abs(dev.get(y, (n,)) - want) <= bound)
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 def test_gemv_acc_last_row(quipu, dev, oracle, fmt):
     """ACC mode (the residual add of wo / ffn_down) reading the last of T = 3 input rows."""
