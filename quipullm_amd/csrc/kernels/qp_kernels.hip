@@ -1568,15 +1568,15 @@ QP_DEV float rope_elem_f(const float* v, uint32_t i, uint32_t nrot, bool neox, f
 QP_DEV void wave_norm_rope_f(float* v, const float* w, uint32_t hd, bool use_norm, float eps, float pos_esc,
                              const float* freq, uint32_t nrot, bool neox, int lane) {
     float vals[4];
-    float ss = 0.0f;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const uint32_t i = lane + 64 * c;
-        vals[c] = i < hd ? v[i] : 0.0f;
-        ss += vals[c] * vals[c];
-    }
-    ss = wave_sum(ss);
     if (use_norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t i = lane + 64 * c;
+            vals[c] = i < hd ? v[i] : 0.0f;
+            ss += vals[c] * vals[c];
+        }
+        ss = wave_sum(ss);
         const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -1612,17 +1612,21 @@ struct DecBuf {
     uint4 k[4], v[4];
 };
 
+// Loads of KS keys from kb for this lane's key slot: through buffer resources over the cache, so a key at or past
+// kend (past the wavefront's range) passes an offset past the end and costs no memory traffic.
 template <int HD, bool F16>
-QP_DEV void dec_load(DecBuf& b, const QpDecAttnArgs& a, uint32_t kvh, uint32_t kb, uint32_t klast, uint32_t kq,
-                     uint32_t dsub) {
+QP_DEV void dec_load(DecBuf& b, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, uint32_t nkv, uint32_t kvh,
+                     uint32_t kb, uint32_t kend, uint32_t kq, uint32_t dsub) {
     using C = DecCfg<HD, F16>;
-    const uint64_t kvd = (uint64_t)a.nkv * HD, eb = F16 ? 2 : 4;
+    const uint32_t kvd = nkv * HD, eb = F16 ? 2 : 4;
 #pragma unroll
     for (int u = 0; u < C::U; u++) {
-        const uint32_t key = min(kb + u * C::KPI + kq, klast);  // clamped: keys past the range are loaded, unused
-        const uint64_t off = ((uint64_t)key * kvd + (uint64_t)kvh * HD) * eb + dsub * 16;
-        b.k[u] = gload<uint4>(a.kc + off);
-        b.v[u] = gload<uint4>(a.vc + off);
+        const uint32_t key = kb + u * C::KPI + kq;
+        const uint32_t off = key < kend ? (key * kvd + kvh * HD) * eb + dsub * 16 : 0x80000000u;
+        const u32x4 kk = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+        const u32x4 vv = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+        b.k[u] = uint4{kk[0], kk[1], kk[2], kk[3]};
+        b.v[u] = uint4{vv[0], vv[1], vv[2], vv[3]};
     }
 }
 
@@ -1704,6 +1708,41 @@ QP_DEV void dec_consume(const DecBuf& b, uint32_t kb, uint32_t kend, uint32_t po
     }
 }
 
+// The value of lane `lane ^ OFF`.  Exchanges across 16-lane rows use the gfx950 permlane swaps (plain VALU
+// operations); within a row, a shuffle.  permlane16_swap(x, x) returns {x with odd rows replaced by the row below,
+// x with even rows replaced by the row above}; permlane32_swap(x, x) likewise for the two halves.
+template <int OFF>
+QP_DEV float lane_xor(float x, uint32_t lane) {
+    if constexpr (OFF == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return __uint_as_float(lane < 32 ? r[1] : r[0]);
+    } else if constexpr (OFF == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return __uint_as_float(((lane >> 4) & 1) == 0 ? r[1] : r[0]);
+    } else {
+        return __shfl_xor(x, OFF, 64);
+    }
+}
+
+// Online-softmax states of lane groups OFF apart merged: (m, l, acc) <- the combination of both.
+template <int OFF, int G, int E>
+QP_DEV void dec_merge_groups(float (&m)[G], float (&l)[G], float (&acc)[G][E], uint32_t lane) {
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float mo = lane_xor<OFF>(m[g], lane), lo = lane_xor<OFF>(l[g], lane);
+        const float M = fmaxf(m[g], mo);
+        const float fa = __builtin_amdgcn_exp2f((m[g] - M) * QP_LOG2E);
+        const float fb = __builtin_amdgcn_exp2f((mo - M) * QP_LOG2E);
+        l[g] = l[g] * fa + lo * fb;
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const float ao = lane_xor<OFF>(acc[g][e], lane);
+            acc[g][e] = acc[g][e] * fa + ao * fb;
+        }
+        m[g] = M;
+    }
+}
+
 // LDS (floats): kn [HD] | vn [HD] | freq [HD/2] | q-norm, k-norm weights [HD] each | region R: q [G][HD]
 // during the preparation, then the wavefront partials wacc [4][G][HD], wm [4][8], wl [4][8].
 template <int HD, bool F16, int G>
@@ -1746,12 +1785,13 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
     if (a.freq && tid < a.nrot / 2) ft = gload<float>(a.freq + 4ull * tid);
     if (a.qnorm && tid < HD) qwt = gload<float>(a.qnorm + 4ull * tid);
     if (a.knorm && wg_new && tid < HD) kwt = gload<float>(a.knorm + 4ull * tid);
-    // unconditional (a wavefront with no keys loads row 0, which always exists), so the waits below can count
-    // these loads as still in flight
-    const uint32_t klast = kw1 > kw0 ? kw1 - 1 : 0;
+    // issued by every wavefront (one without keys loads nothing: its offsets are past the end), so the waits below
+    // can count these loads as still in flight
+    const uint64_t cbytes = (uint64_t)a.rows * a.nkv * HD * (F16 ? 2 : 4);
+    const __amdgpu_buffer_rsrc_t rk = kq_rsrc(a.kc, cbytes), rv = kq_rsrc(a.vc, cbytes);
     DecBuf A, B;
-    dec_load<HD, F16>(A, a, kvh, kw0, klast, kq, dsub);
-    dec_load<HD, F16>(B, a, kvh, kw0 + KS, klast, kq, dsub);
+    dec_load<HD, F16>(A, rk, rv, a.nkv, kvh, kw0, kw1, kq, dsub);
+    dec_load<HD, F16>(B, rk, rv, a.nkv, kvh, kw0 + KS, kw1, kq, dsub);
     // 2. the preparation (waits for the loads of 1 only)
     if (tid < a.nrot / 2)
         freq[tid] = a.freq ? ft : (float)pow((double)a.base, (double)((-2.0f * (float)tid) / (float)a.nrot));
@@ -1778,19 +1818,11 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
             wave_norm_rope_f(kn, kw, HD, a.knorm != 0, a.eps, pos_esc, freq, a.nrot, a.neox != 0, (int)lane);
     }
     __syncthreads();
-    if (wg_new && tid < HD) {
-        // append to the cache at slot pos0; in f16 mode the LDS copy is rounded the same way
-        const uint64_t o = (uint64_t)pos0 * a.nkv * HD + (uint64_t)kvh * HD + tid;
-        if (F16) {
-            const uint16_t hk = f2h(kn[tid]), hv = f2h(vn[tid]);
-            gstore<uint16_t>(a.kc + 2 * o, hk);
-            gstore<uint16_t>(a.vc + 2 * o, hv);
-            kn[tid] = h2f(hk);
-            vn[tid] = h2f(hv);
-        } else {
-            gstore<float>(a.kc + 4 * o, kn[tid]);
-            gstore<float>(a.vc + 4 * o, vn[tid]);
-        }
+    if (F16 && wg_new && tid < HD) {
+        // in f16 mode the new key and value are used as the cache will hold them (appended at the end: a store in
+        // flight here would make the key loop wait for it)
+        kn[tid] = h2f(f2h(kn[tid]));
+        vn[tid] = h2f(f2h(vn[tid]));
     }
     __syncthreads();
     float qr[G][E];
@@ -1807,35 +1839,22 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
 #pragma unroll
         for (int e = 0; e < E; e++) acc[g][e] = 0.0f;
     }
-    // 3. the key stream: two steps in flight from the start, loads issued unconditionally (clamped to the last
-    // key, so the steps past the end re-read cached rows) and keys past kw1 masked
+    // 3. the key stream: two steps in flight from the start, loads issued unconditionally (steps past the range
+    // load nothing) and keys past kw1 masked
     if (kw0 < kw1) {
         const uint32_t nsteps = (kw1 - kw0 + KS - 1) / KS;
         for (uint32_t s = 0; s < nsteps; s += 2) {
             dec_consume<HD, F16, G>(A, kw0 + s * KS, kw1, pos0, kn, vn, kq, dsub, qr, a.scale, m, l, acc);
-            dec_load<HD, F16>(A, a, kvh, kw0 + (s + 2) * KS, klast, kq, dsub);
+            dec_load<HD, F16>(A, rk, rv, a.nkv, kvh, kw0 + (s + 2) * KS, kw1, kq, dsub);
             dec_consume<HD, F16, G>(B, kw0 + (s + 1) * KS, kw1, pos0, kn, vn, kq, dsub, qr, a.scale, m, l, acc);
-            dec_load<HD, F16>(B, a, kvh, kw0 + (s + 3) * KS, klast, kq, dsub);
+            dec_load<HD, F16>(B, rk, rv, a.nkv, kvh, kw0 + (s + 3) * KS, kw1, kq, dsub);
         }
     }
     // 4. merge the lane groups of this wavefront (groups hold different keys, the same dims)
-#pragma unroll
-    for (int off = LPK; off < 64; off *= 2) {
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float mo = __shfl_xor(m[g], off, 64), lo = __shfl_xor(l[g], off, 64);
-            const float M = fmaxf(m[g], mo);
-            const float fa = __builtin_amdgcn_exp2f((m[g] - M) * QP_LOG2E);
-            const float fb = __builtin_amdgcn_exp2f((mo - M) * QP_LOG2E);
-            l[g] = l[g] * fa + lo * fb;
-#pragma unroll
-            for (int e = 0; e < E; e++) {
-                const float ao = __shfl_xor(acc[g][e], off, 64);
-                acc[g][e] = acc[g][e] * fa + ao * fb;
-            }
-            m[g] = M;
-        }
-    }
+    if constexpr (LPK <= 4) dec_merge_groups<4, G, E>(m, l, acc, lane);
+    if constexpr (LPK <= 8) dec_merge_groups<8, G, E>(m, l, acc, lane);
+    if constexpr (LPK <= 16) dec_merge_groups<16, G, E>(m, l, acc, lane);
+    if constexpr (LPK <= 32) dec_merge_groups<32, G, E>(m, l, acc, lane);
     if (lane < LPK) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -1863,9 +1882,17 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
             }
         const uint64_t i = (uint64_t)(h0 + g) * a.nsplit + wg;
         gstore<float>(a.part_o + 4 * (i * HD + d), o);
-        if (d == 0) {
-            gstore<float>(a.part_ml + 8 * i, M);
-            gstore<float>(a.part_ml + 8 * i + 4, L);
+        if (d == 0) gstore<float2>(a.part_ml + 8 * i, make_float2(M, L));
+    }
+    if (wg_new && tid < HD) {
+        // append the new key and value to the cache at slot pos0 (kn / vn hold them, f16-rounded in f16 mode)
+        const uint64_t o = (uint64_t)pos0 * a.nkv * HD + (uint64_t)kvh * HD + tid;
+        if (F16) {
+            gstore<uint16_t>(a.kc + 2 * o, f2h(kn[tid]));
+            gstore<uint16_t>(a.vc + 2 * o, f2h(vn[tid]));
+        } else {
+            gstore<float>(a.kc + 4 * o, kn[tid]);
+            gstore<float>(a.vc + 4 * o, vn[tid]);
         }
     }
 }
