@@ -40,6 +40,10 @@ from quipullm_amd import synth  # noqa: E402
 PEAK_HBM_GBS = 8000.0
 MODEL = "llama8b_q4km"
 METRIC = "decode tok/s @8B-shape Q4_K ctx 4096; Q4_K GEMV HBM GB/s vs peak"
+# Prefill of 2048 tokens on the 8B shape: 2*M*sum(N*K) over the 7 matrices of 32 layers, causal attention
+# 2*2*sum_i(i)*hd*nh*L, and the last token's output row (algorithmic FLOPs, not the MFMA instructions issued)
+PREFILL_2048_FLOP = (2 * 2048 * 32 * (4096 * 4096 * 2 + 1024 * 4096 * 2 + 14336 * 4096 * 3)
+                     + 2 * 2 * (2048 * 2049 // 2) * 128 * 32 * 32 + 2 * 128256 * 4096)
 
 
 def log(*a):
@@ -59,16 +63,19 @@ def ensure_built():
         build.build_all(oracle=True)
 
 
-def decode_bytes_per_token(path, P, n):
+def decode_bytes_per_token(model, path, P, n):
     """Algorithmic HBM bytes of one decode token, averaged over the n timed steps after a P-token prefill:
-    every weight tensor read once (embedding: one row), plus the f16 K and V rows of every cached position."""
+    every weight tensor read once (embedding: one row; stacked expert tensors: the n_used selected experts of
+    n_exp), plus the f16 K and V rows of every cached position."""
     from oracle.oracle import GGUF  # header reader only
     g = GGUF(path)
-    c = synth.CONFIGS[MODEL]
+    c = synth.CONFIGS[model]
     w = 0
     for name, t in g.tensors.items():
         if name == "token_embd.weight":
             w += t["bytes"] // c.vocab
+        elif "_exps." in name:
+            w += t["bytes"] * c.n_used // c.n_exp
         else:
             w += t["bytes"]
     kv_per_pos = c.n_layers * 2 * c.nkv * c.hd * 2
@@ -103,27 +110,51 @@ def cpu_baseline(path, seconds=20.0):
                       f"OpenMP threads; C restatement of the reference WGSL semantics"}, ids, lgs
 
 
-def run_decode(path, steps, warmup, prefills, check_n, eager=False):
-    c = synth.CONFIGS[MODEL]
+def run_decode(model, path, steps, warmup, prefills, check_n=0, eager=False, seed=7):
+    """The product host (Node.js CLI) on `model`: for each P in prefills, prefill P uniform-random ids, then time
+    `steps` greedy decode tokens.  With check_n, first generates check_n greedy tokens from CHECK_PROMPT and
+    returns their logits (the parity check)."""
+    c = synth.CONFIGS[model]
     ctx = max(prefills) + steps + warmup + 8
-    ids = synth.random_prompt(c.vocab, max(prefills), 7)
-    pf = os.path.join(model_dir(), f"{MODEL}.bench_prompt.json")
-    cf = os.path.join(model_dir(), f"{MODEL}.check_prompt.json")
-    lf = os.path.join(model_dir(), f"{MODEL}.check_logits.f32")
+    ids = synth.random_prompt(c.vocab, max(prefills), seed)
+    pf = os.path.join(model_dir(), f"{model}.bench_prompt.json")
     with open(pf, "w") as f:
         json.dump(ids, f)
-    with open(cf, "w") as f:
-        json.dump(CHECK_PROMPT, f)
     cmd = ["node", os.path.join(ROOT, "quipullm_amd", "js", "cli.js"), "bench", "--model", path, "--prompt-file", pf,
            "--n", str(steps), "--warmup", str(warmup), "--kv", "f16", "--ctx", str(ctx), "--batch", "512",
-           "--max-gen", str(max(steps, warmup, check_n) + 8), "--prefill", ",".join(str(p) for p in prefills),
-           "--check-prompt-file", cf, "--check-n", str(check_n), "--check-logits", lf] + (["--eager"] if eager else [])
+           "--max-gen", str(max(steps, warmup, check_n) + 8), "--prefill", ",".join(str(p) for p in prefills)]
+    if check_n:
+        cf = os.path.join(model_dir(), f"{model}.check_prompt.json")
+        lf = os.path.join(model_dir(), f"{model}.check_logits.f32")
+        with open(cf, "w") as f:
+            json.dump(CHECK_PROMPT, f)
+        cmd += ["--check-prompt-file", cf, "--check-n", str(check_n), "--check-logits", lf]
+    if eager:
+        cmd.append("--eager")
     log("bench: " + " ".join(cmd))
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         raise RuntimeError("decode benchmark failed:\n" + r.stderr[-3000:])
     out = json.loads(r.stdout.strip().splitlines()[-1])
-    out["check_logits"] = np.fromfile(lf, np.float32).reshape(-1, c.vocab)
+    if check_n:
+        out["check_logits"] = np.fromfile(lf, np.float32).reshape(-1, c.vocab)
+    return out
+
+
+def side_configs(steps, warmup, eager):
+    """The other decode workloads of the hot path, measured on the same product path (no parity check here; the
+    GPU tests pin their parity on smaller models of the same formats): the MoE model (48 layers, 128 experts,
+    top-8, Q4_K) at ctx 2048 and the tiny Q8_0 LLaMA after a 32-token prompt."""
+    out = {}
+    for model, P, n in (("qwen3moe_q4k", 2048, steps), ("tiny_q8", 32, 128)):
+        path = synth.ensure_model(model, model_dir())
+        r = run_decode(model, path, n, warmup, [P], eager=eager, seed=11)["runs"][0]
+        _, bpt = decode_bytes_per_token(model, path, P, n)
+        out[model] = {"prompt_tokens": P, "steps": n, "decode_tok_s": round(r["decode_tok_s"], 3),
+                      "ms_per_token": round(r["ms_per_token"], 4), "prefill_tok_s": round(r["prefill_tok_s"], 1),
+                      "bytes_per_token": int(bpt), "hbm_GBs": round(bpt * r["decode_tok_s"] / 1e9, 1),
+                      "roofline_frac": round(bpt * r["decode_tok_s"] / 1e9 / PEAK_HBM_GBS, 4)}
+        log(f"bench: {model} " + json.dumps(out[model]))
     return out
 
 
@@ -157,6 +188,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-side", action="store_true", help="skip the MoE and tiny Q8_0 decode measurements")
     ap.add_argument("--decode-launch", choices=["graph", "eager"], default="graph",
                     help="the one-token step as a captured HIP graph (default) or dispatched op by op (same kernels; "
                          "for profilers that cannot follow graph launches)")
@@ -174,8 +206,8 @@ def main():
     log(f"bench: model {path} ready in {time.time() - t0:.1f}s")
     cpu, cpu_ids, cpu_lg = cpu_baseline(path, a.cpu_seconds)
     log(f"bench: cpu baseline {cpu['value']:.3f} tok/s")
-    prefills = [4096, 512]
-    dec = run_decode(path, a.steps, a.warmup, prefills, len(cpu_ids), a.decode_launch == "eager")
+    prefills = [4096, 2048, 512]
+    dec = run_decode(MODEL, path, a.steps, a.warmup, prefills, len(cpu_ids), a.decode_launch == "eager")
     check = parity(dec["check_ids"], dec.pop("check_logits"), cpu_ids, cpu_lg)
     runs = {r["prompt_tokens"]: r for r in dec["runs"]}
     log("bench: decode " + json.dumps(dec))
@@ -185,8 +217,9 @@ def main():
                            (capi.Q6_K, 4096, 4096), (capi.Q6_K, 14336, 4096), (capi.Q6_K, 4096, 14336)])
     dom = gem[0]
     main_run = runs[4096]
-    wbytes, bpt = decode_bytes_per_token(path, 4096, a.steps)
-    _, bpt512 = decode_bytes_per_token(path, 512, a.steps)
+    wbytes, bpt = decode_bytes_per_token(MODEL, path, 4096, a.steps)
+    _, bpt512 = decode_bytes_per_token(MODEL, path, 512, a.steps)
+    side = {} if a.no_side else side_configs(a.steps, a.warmup, a.decode_launch == "eager")
     tok_s = main_run["decode_tok_s"]
     result = {
         "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
@@ -202,6 +235,10 @@ def main():
                    "bytes_per_token_ctx4096": int(bpt), "weight_bytes_per_token": int(wbytes),
                    "wall_tok_s_ctx4096": round(main_run["wall_tok_s"], 3),
                    "prefill_tok_s_4096": round(main_run["prefill_tok_s"], 1),
+                   "prefill_tok_s_2048": round(runs[2048]["prefill_tok_s"], 1),
+                   "decode_tok_s_ctx2048": round(runs[2048]["decode_tok_s"], 3),
+                   "prefill_2048_TFLOPs": round(PREFILL_2048_FLOP / (runs[2048]["prefill_ms"] * 1e-3) / 1e12, 2),
+                   "side_configs": side,
                    "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()} for g in gem],
                    "parity_vs_oracle": check},
         "roofline": {"bound": "hbm", "kernel": "qp_gemv_q4k (Q4_K GEMV 14336x4096, batch 1)",

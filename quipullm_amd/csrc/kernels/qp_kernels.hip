@@ -659,11 +659,22 @@ QP_DEV void kq_dot_q6k(const U& B, const float4* xb4, const float* xsb, float (&
     }
 }
 
+// Where the weights of x-block b of row `row` live.  KDense: the row's own blocks (row r of a tensor with nb blocks
+// per row, the chunk-plane layout above).  A gathered layout maps the x blocks onto rows of several tensors.
+struct KDense {
+    static constexpr bool SCALED = false;
+    QP_DEV uint32_t nbw(uint32_t nb) const { return nb; }  // blocks per weight row
+    // weight row and block within it that multiply x-block b of output row `row`
+    QP_DEV void loc(uint32_t row, uint32_t b, uint32_t& wr, uint32_t& wb) const { wr = row; wb = b; }
+    QP_DEV float xscale(uint32_t) const { return 1.0f; }
+};
+
 // The unit loop.  seg_at(i) returns segment i (i < nseg); the wave's units are w, w + W, ... < total_units,
 // segment i owning units [u0_i, u0_{i+1}).  XS: x sub-blocks of 32 per thread for staging (K <= XS * 8192).
-template <int FMT, int R, int XS, class SegAt>
+// lay: the weight layout (KDense, or a gathered one whose x sub-blocks may also carry a scale).
+template <int FMT, int R, int XS, class SegAt, class Lay = KDense>
 QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t x, uint64_t norm_w, float eps,
-                    uint32_t K, uint64_t amax) {
+                    uint32_t K, uint64_t amax, Lay lay = Lay()) {
     extern __shared__ float4 xs[];
     float* xsum = reinterpret_cast<float*>(xs + (K >> 8) * 65);
     __shared__ float red[4];
@@ -693,6 +704,12 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
             for (int j = 0; j < 8; j++) nr[i][j] = gload<float4>(norm_w + 128ull * q + 16ull * j);
         }
     }
+    float xsc[XS];
+#pragma unroll
+    for (int i = 0; i < XS; i++) {
+        const uint32_t q = tid + 256 * i;
+        xsc[i] = lay.xscale(q < (K >> 5) ? q : 0);  // every lane (a gathered layout shuffles across the wave)
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. the first unit's weights
@@ -709,24 +726,26 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         const uint32_t u = (uv ? g : w) - sg.u0;
         const bool pair = sg.mode == QP_GEMV_SWIGLU;
         const bool q6 = FMT == QP_KQ_MIX ? sg.fmt == QP_Q6_K : FMT == QP_Q6_K;
-        const uint32_t rb = q6 ? 208 : 144;
-        const uint64_t tbytes = (uint64_t)sg.rows_total * nb * (q6 ? 210 : 144);
+        const uint32_t nbw = lay.nbw(nb);
+        const uint64_t tbytes = (uint64_t)sg.rows_total * nbw * (q6 ? 210 : 144);
         const __amdgpu_buffer_rsrc_t rs0 = kq_rsrc(sg.w, tbytes);
         const __amdgpu_buffer_rsrc_t rs1 = kq_rsrc(pair ? sg.w2 : sg.w, tbytes);
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint32_t lr = pair ? u * S + s : (u * R + r) * S + s;
             const bool on = uv && lane_on && lr < sg.n;
-            const uint32_t row = sg.row_base + lr;
-            const uint32_t vo = on ? row * nb * rb + b * 16 : 0x80000000u;
+            // weight row wr, block wb: chunk c at wr*nbw*rb + c*nbw*16 + wb*16
+            uint32_t wr, wb;
+            lay.loc(sg.row_base + lr, b, wr, wb);
+            const uint32_t vo = on ? wr * nbw * (q6 ? 208 : 144) + wb * 16 : 0x80000000u;
             const __amdgpu_buffer_rsrc_t rs = (pair && r == 1) ? rs1 : rs0;
 #pragma unroll
             for (int c = 0; c < KQ<FMT>::CPB; c++)
                 B.c[r][c] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rs, (FMT != QP_KQ_MIX || c < 9 || q6) ? vo : 0x80000000u, c * nb * 16, 0);
+                    rs, (FMT != QP_KQ_MIX || c < 9 || q6) ? vo : 0x80000000u, c * nbw * 16, 0);
             if constexpr (FMT != QP_Q4_K)
                 B.d[r] = __builtin_amdgcn_raw_buffer_load_b16(
-                    rs, (on && q6) ? sg.rows_total * nb * 208 + (row * nb + b) * 2 : 0x80000000u, 0, 0);
+                    rs, (on && q6) ? sg.rows_total * nbw * 208 + (wr * nbw + wb) * 2 : 0x80000000u, 0, 0);
         }
     };
     issue(buf, 0);
@@ -748,6 +767,13 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
 #pragma unroll
             for (int t = 0; t < 8; t++) {
                 float4 v = xr[i][t];
+                if constexpr (Lay::SCALED) {
+                    const float f = xsc[i];
+                    v.x *= f;
+                    v.y *= f;
+                    v.z *= f;
+                    v.w *= f;
+                }
                 if (norm_w) {
                     ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
                     const float4 nw4 = nr[i][t];
@@ -911,6 +937,135 @@ QP_DEV void kq_gemv_exp(const QpGemvExpArgs& a) {
     kq_gemv<FMT, R, XS>([&](uint32_t) __attribute__((always_inline)) { return one; }, 1, units,
                         a.x + 4ull * (job / a.tfijo) * a.k, 0, 0.0f, a.k, 0);
 }
+
+// ------------------------------------------------------------------------ fused MoE FFN of one decode token
+// Routing of the token as one wavefront computes it (reference moe_topk, kds.js:191-221): softmax over the e <= 256
+// router logits, kused rounds of strict maximum over the probabilities (ties to the lower expert index), weights =
+// chosen probabilities times scale, divided by their running sum (at least 2^-14) when norm.  Lane i < kused
+// returns slot i's expert and weight.
+QP_DEV void moe_route(const QpMoeArgs& a, uint32_t lane, uint32_t& sel, float& wt) {
+    float p[4];
+    float m = -3.0e38f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t e = lane + 64 * j;
+        p[j] = e < a.e ? gload<float>(a.logits + 4ull * e) : -3.0e38f;
+        m = fmaxf(m, p[j]);
+    }
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        p[j] = lane + 64 * j < a.e ? expf(p[j] - m) : 0.0f;
+        s += p[j];
+    }
+    s = wave_sum(s);
+#pragma unroll
+    for (int j = 0; j < 4; j++) p[j] = lane + 64 * j < a.e ? p[j] / s : -3.0f;  // -3: below every candidate
+    float tot = 0.0f;
+    sel = 0;
+    wt = 0.0f;
+    for (uint32_t i = 0; i < a.kused; i++) {
+        float bv = -1.0f;
+        uint32_t bi = 0xffffffffu;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (p[j] > bv) {
+                bv = p[j];
+                bi = lane + 64 * j;
+            }
+#pragma unroll
+        for (int msk = 32; msk >= 1; msk >>= 1) {
+            const float ov = __shfl_xor(bv, msk, 64);
+            const uint32_t oi = __shfl_xor(bi, msk, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (bi == 0xffffffffu) bi = 0;  // nothing left above -1 (kused > e): expert 0, weight -1, as the reference
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (lane + 64 * j == bi) p[j] = -2.0f;
+        if (lane == i) {
+            sel = bi;
+            wt = bv;
+        }
+        tot = tot + bv;
+    }
+    float f = a.scale;
+    if (a.norm) f = f / fmaxf(tot, 6.103515625e-5f);
+    wt = wt * f;
+}
+
+template <int FMT, int XS>
+QP_DEV void moe_gate_up_body(const QpMoeArgs& a) {
+    const uint32_t lane = threadIdx.x & 63, job = blockIdx.y;
+    uint32_t sel;
+    float wt;
+    moe_route(a, lane, sel, wt);
+    uint32_t ex = (uint32_t)__builtin_amdgcn_readlane((int)sel, (int)job);
+    if (ex >= a.e) ex = a.e - 1;
+    const KSeg one{a.w, a.w2, a.y + 4ull * job * a.n, a.n, ex * a.n, a.e * a.n, (uint32_t)QP_GEMV_SWIGLU, 0,
+                   (uint32_t)FMT};
+    uint32_t nbp = 1;
+    while (nbp < (a.k >> 8)) nbp <<= 1;
+    const uint32_t units = (a.n + 64 / nbp - 1) / (64 / nbp);
+    kq_gemv<FMT, 2, XS>([&](uint32_t) __attribute__((always_inline)) { return one; }, 1, units, a.x, a.norm_w, a.eps,
+                        a.k, 0);
+    if (blockIdx.x == 0 && job == 0 && threadIdx.x < a.kused) {
+        gstore<uint32_t>(a.sel + 4ull * lane, sel);
+        gstore<float>(a.wts + 4ull * lane, wt);
+    }
+}
+
+// moe_down's gathered layout: x block b (of kused * nbwv) is block b % nbwv of row r of expert sel[b / nbwv], and
+// the input sub-blocks of slot j are scaled by wts[j].  Lane j < kused of every wavefront holds sel[j], wts[j].
+struct KMoeDown {
+    static constexpr bool SCALED = true;
+    uint32_t nbwv, rows, nin, ne, selv;
+    float wv;
+    QP_DEV uint32_t nbw(uint32_t) const { return nbwv; }
+    QP_DEV void loc(uint32_t row, uint32_t b, uint32_t& wr, uint32_t& wb) const {
+        const uint32_t slot = b / nbwv;
+        uint32_t ex = (uint32_t)__shfl((int)selv, (int)(slot & 63), 64);
+        ex = ex < ne ? ex : ne - 1;
+        wr = ex * rows + row;
+        wb = b - slot * nbwv;
+    }
+    QP_DEV float xscale(uint32_t q) const { return __shfl(wv, (int)((q * 32 / nin) & 63), 64); }
+};
+
+template <int FMT, int XS>
+QP_DEV void moe_down_body(const QpMoeArgs& a) {
+    const uint32_t lane = threadIdx.x & 63;
+    KMoeDown lay;
+    lay.nbwv = a.k >> 8;
+    lay.rows = a.n;
+    lay.nin = a.k;
+    lay.ne = a.e;
+    lay.selv = lane < a.kused ? gload<uint32_t>(a.sel + 4ull * lane) : 0u;
+    lay.wv = lane < a.kused ? gload<float>(a.wts + 4ull * lane) : 0.0f;
+    const uint32_t K = a.kused * a.k;
+    const KSeg one{a.w, a.w, a.y, a.n, 0, a.e * a.n, (uint32_t)QP_GEMV_ACC, 0, (uint32_t)FMT};
+    uint32_t nbp = 1;
+    while (nbp < (K >> 8)) nbp <<= 1;
+    const uint32_t units = (a.n + 64 / nbp - 1) / (64 / nbp);
+    kq_gemv<FMT, 1, XS>([&](uint32_t) __attribute__((always_inline)) { return one; }, 1, units, a.x, 0, 0.0f, K, 0,
+                        lay);
+}
+
+#define MOE_KERNELS(NAME, FMT)                                                                                    \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_moe_gate_up_##NAME##_x1(    \
+        QpMoeArgs a) { moe_gate_up_body<FMT, 1>(a); }                                                             \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_moe_gate_up_##NAME##_x2(    \
+        QpMoeArgs a) { moe_gate_up_body<FMT, 2>(a); }                                                             \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void qp_moe_down_##NAME##_x1(       \
+        QpMoeArgs a) { moe_down_body<FMT, 1>(a); }                                                                \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_moe_down_##NAME##_x2(       \
+        QpMoeArgs a) { moe_down_body<FMT, 2>(a); }
+MOE_KERNELS(q4k, QP_Q4_K)
+MOE_KERNELS(q6k, QP_Q6_K)
 
 #define KQ_KERNELS(NAME, FMT)                                                                                     \
     KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void qp_gemv_##NAME##_r1(           \

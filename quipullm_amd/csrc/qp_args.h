@@ -68,6 +68,22 @@ typedef struct {
     uint64_t w2;
 } QpGemvExpArgs;
 
+// Fused MoE FFN of one decode token: the arithmetic of the reference's moe_topk, matmul_*_e (gate, up), swiglu,
+// matmul_*_e (down) and moe_comb sequence (deepseek2.js:375-386) in two launches.
+// moe_gate_up: every workgroup routes the token from the router logits [e] (softmax, kused strict maxima, ties to
+//   the lower expert, weights times scale, divided by their sum when norm); job blockIdx.y then computes
+//   y[job][0..n) = silu(gate_x . xn) * (up_x . xn) for its expert x, with xn = rmsnorm(x, eps) * norm_w over k
+//   inputs.  Workgroup (0, 0) also writes sel[kused] and wts[kused].
+// moe_down: y[r] += sum_j wts[j] * (down_{sel[j]} row r) . x[j][0..k), r < n, as one GEMV over kused * k inputs.
+typedef struct {
+    uint64_t w, w2;      // gate, up (stacked [e * n][k]) | down (stacked [e * n][k]), 0
+    uint64_t x, y;       // gate/up: residual in, h out [kused][n] | down: h in [kused][k], residual accumulated
+    uint64_t logits, sel, wts, norm_w;
+    uint32_t n, k, e, kused;
+    float eps, scale;
+    uint32_t norm, pad;
+} QpMoeArgs;
+
 // Multi-token GEMV for prefill (reference matmul_*_4 / matmul_*_t semantics): y[t][r] (+)= W[r].x[t].
 typedef struct {
     uint64_t w, x, y, paso;

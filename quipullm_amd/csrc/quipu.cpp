@@ -498,6 +498,56 @@ int op_moe_topk(const Ctx& c) {
     return launch(K_moe_topk, (c.gx ? c.gx : 1) * 64, 1, 1, 256, 0, a);
 }
 
+// moe_gate_up_<fmt> / moe_down_<fmt>: the MoE FFN of one decode token in two launches (the reference runs
+// moe_topk, matmul_*_e for gate and up, swiglu, matmul_*_e for down and moe_comb; deepseek2.js:375-386).
+// P{n, k, e, kused, eps, scale, norm}; binding 0 (paso) is not read: one token
+//   gate/up: [paso, gate, up, x, norm_w|0, logits, h, sel, wts]: routes from logits [e], h[j] = silu(gate . xn) *
+//            (up . xn) over experts sel[j], xn = rmsnorm(x) * norm_w; writes sel, wts [kused]
+//   down:    [paso, down, h, x, sel, wts]: x += sum_j wts[j] * down_{sel[j]} . h[j]
+int op_moe(const Ctx& c, int fmt, bool down, const char* name) {
+    if (int e = need_bufs(c, down ? 6 : 9, name)) return e;
+    QpMoeArgs a = {};
+    a.n = c.U(0);
+    a.k = c.U(1);
+    a.e = c.U(2);
+    a.kused = c.U(3);
+    a.eps = c.F(4);
+    a.scale = c.F(5);
+    a.norm = c.U(6);
+    if (int e = check_k(fmt, a.k, name)) return e;
+    if (a.n == 0) return fail(QP_E_ARG, "%s: n is 0", name);
+    if (a.e == 0 || a.e > 256) return fail(QP_E_ARG, "%s: %u experts (this kernel routes 1..256)", name, a.e);
+    if (a.kused == 0 || a.kused > a.e || a.kused > 64)
+        return fail(QP_E_ARG, "%s: %u experts used of %u", name, a.kused, a.e);
+    const uint32_t K = down ? a.kused * a.k : a.k;
+    if (K > 16384) return fail(QP_E_ARG, "%s: %u inputs per row (at most 16384)", name, K);
+    if (kq_tensor_bytes(fmt, (uint64_t)a.e * a.n, a.k) >= (1ull << 31))
+        return fail(QP_E_ARG, "%s: expert tensor is 2 GiB or larger", name);
+    const int q6 = fmt == QP_Q6_K, x2 = K > 8192;
+    const uint32_t units = cdiv(a.n, 64 / kq_nbp(K));
+    a.w = c.B(1);
+    if (down) {
+        static const Kid kd[2][2] = {{K_moe_down_q4k_x1, K_moe_down_q4k_x2}, {K_moe_down_q6k_x1, K_moe_down_q6k_x2}};
+        a.x = c.B(2);
+        a.y = c.B(3);
+        a.sel = c.B(4);
+        a.wts = c.B(5);
+        uint32_t grid = cdiv(units, 4);
+        if (grid > 2 * (uint32_t)g_cus) grid = 2 * (uint32_t)g_cus;
+        return launch(kd[q6][x2], grid, 1, 1, 256, kq_lds(K), a);
+    }
+    static const Kid kg[2][2] = {{K_moe_gate_up_q4k_x1, K_moe_gate_up_q4k_x2},
+                                 {K_moe_gate_up_q6k_x1, K_moe_gate_up_q6k_x2}};
+    a.w2 = c.B(2);
+    a.x = c.B(3);
+    a.norm_w = c.B(4);
+    a.logits = c.B(5);
+    a.y = c.B(6);
+    a.sel = c.B(7);
+    a.wts = c.B(8);
+    return launch(kg[q6][x2], cdiv(units, 4), a.kused, 1, 256, kq_lds(K), a);
+}
+
 // moe_comb (kds.js:224-240): P{D, k}; [paso, x, de, wts].
 int op_moe_comb(const Ctx& c) {
     if (int e = need_bufs(c, 4, "moe_comb")) return e;
@@ -735,6 +785,10 @@ void register_ops() {
     v.push_back({"swiglu", op_swiglu});
     v.push_back({"moe_topk", op_moe_topk});
     v.push_back({"moe_comb", op_moe_comb});
+    v.push_back({"moe_gate_up_q4k", [](const Ctx& c) { return op_moe(c, QP_Q4_K, false, "moe_gate_up_q4k"); }});
+    v.push_back({"moe_gate_up_q6k", [](const Ctx& c) { return op_moe(c, QP_Q6_K, false, "moe_gate_up_q6k"); }});
+    v.push_back({"moe_down_q4k", [](const Ctx& c) { return op_moe(c, QP_Q4_K, true, "moe_down_q4k"); }});
+    v.push_back({"moe_down_q6k", [](const Ctx& c) { return op_moe(c, QP_Q6_K, true, "moe_down_q6k"); }});
     v.push_back({"gemv", op_gemv});
     v.push_back({"dec_attn", op_dec_attn});
     v.push_back({"dec_attn_comb", op_dec_attn_comb});

@@ -318,8 +318,16 @@ class ModeloTransformer {
     return out;
   }
 
+  // Whether the fused MoE decode ops take this layer: Q4_K/Q6_K experts with gate and up in one format, at most 256
+  // experts to route, and inputs the kernels stage whole (D and kused * ffe at most 16384).
+  _moeFusionable(c) {
+    const kq = function (t) { return t === 'q4k' || t === 'q6k'; };
+    return kq(c.eg.tipo) && c.eg.tipo === c.eu.tipo && kq(c.ed.tipo) && this.nExp <= 256 && this.nUsados <= 64 &&
+      this.D <= 16384 && this.nUsados * this.ffe <= 16384 && this.ffe % 256 === 0 && this.D % 256 === 0;
+  }
+
   _armarDecode() {
-    const gpu = this.gpu, P = this.bPaso, D = this.D, qd = this.nh * this.hd;
+    const gpu = this.gpu, P = this.bPaso, D = this.D, qd = this.nh * this.hd, self = this;
     const plan = [];
     plan.push([this._embedGrupo(this.bIds, this.x), Math.ceil(D / 256)]);
     const uAtt = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', this.nsplit], ['f', this.escAtt],
@@ -333,7 +341,19 @@ class ModeloTransformer {
         this.ropeFreq]), 1]);
       plan.push([gpu.grupo('dec_attn_comb', [uComb, P, this.partO, this.partML, this.att]), 1]);
       plan.push([this._gemv([{ W: c.wo, mode: ACC, y: this.x }], this.att, null, qd), 1]);
-      if (this.nExp) {
+      if (this.nExp && this._moeFusionable(c)) {
+        // routing, gate/up with SwiGLU, down and the weighted combine in two launches (the norm is fused in both
+        // the router GEMV and the gate/up kernel)
+        const K = this.nUsados, E = this.nExp;
+        const u = function (n, k) {
+          return gpu.uniforme([['u', n], ['u', k], ['u', E], ['u', K], ['f', self.eps], ['f', self.escExp],
+            ['u', self.normExp ? 1 : 0]]);
+        };
+        plan.push([this._gemv([{ W: c.router, mode: STORE, y: this.rl }], this.x, c.ffnNorm, D), 1]);
+        plan.push([gpu.grupo('moe_gate_up_' + c.eg.tipo, [u(this.ffe, D), P, c.eg.w, c.eu.w, this.x, c.ffnNorm, this.rl,
+          this.g, this.sel, this.wts]), 1]);
+        plan.push([gpu.grupo('moe_down_' + c.ed.tipo, [u(D, this.ffe), P, c.ed.w, this.g, this.x, this.sel, this.wts]), 1]);
+      } else if (this.nExp) {
         plan.push([gc.ffnNorm, 1]);
         plan.push([this._gemv([{ W: c.router, mode: STORE, y: this.rl }], this.xn, null, D), 1]);
         plan.push([gc.topk, 1]);

@@ -314,6 +314,57 @@ def test_matmul_expert_jobs(quipu, dev, oracle, fmt):
     np.testing.assert_allclose(got2, want2, rtol=1e-4, atol=1e-4 * np.abs(want2).max())
 
 
+def expert_rows(oracle, fmt, raw, e, N, K):
+    """Dequantized rows of expert e of a stacked [E*N][K] K-quant tensor (GGUF block bytes)."""
+    bb = {capi.Q4_K: 144, capi.Q6_K: 210}[fmt] * (K // 256)
+    return oracle.dequant(fmt, raw[e * N * bb:(e + 1) * N * bb], N * K).reshape(N, K).astype(np.float64)
+
+
+@pytest.mark.parametrize("fmt", [capi.Q4_K, capi.Q6_K])
+@pytest.mark.parametrize("E,k,D,Fe,norm", [(128, 8, 2048, 768, 1), (16, 4, 512, 256, 0), (20, 6, 8448, 1536, 1)])
+def test_moe_fused_decode(quipu, dev, oracle, fmt, E, k, D, Fe, norm):
+    """moe_gate_up_<fmt> then moe_down_<fmt> (one token) against the reference sequence in float64: rmsnorm, routing
+    (oracle moe_topk, ties to the lower expert), gate/up GEMVs of the chosen experts, SwiGLU, down GEMVs and the
+    weighted combine into the residual.  The last shape stages more than 8192 inputs (the two-pass variants)."""
+    rng = np.random.default_rng([E, k, D, fmt])
+    rg, ru, rd = raw_matrix(fmt, E * Fe, D, 81), raw_matrix(fmt, E * Fe, D, 82), raw_matrix(fmt, E * D, Fe, 83)
+    hg, hu, hd = dev.matrix(fmt, rg, E * Fe, D), dev.matrix(fmt, ru, E * Fe, D), dev.matrix(fmt, rd, E * D, Fe)
+    nw = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    eps, scale = 1e-6, 1.0 if norm else 2.5
+    name = capi.FMT_NAME[fmt]
+    for call in range(2):
+        x = rng.standard_normal(D).astype(np.float32)
+        lg = rng.standard_normal(E).astype(np.float32)
+        if call == 0:
+            lg[3] = lg[E - 2] = lg.max() + 1.0  # an exact tie at the top: the lower expert first
+        s_want, w_want = oracle.moe_topk(lg[None, :], E, k, norm, scale)
+        xb, h, sel, wts = dev.buf(x), dev.zeros(k * Fe * 4), dev.zeros(k * 4), dev.zeros(k * 4)
+        ug = [("u", Fe), ("u", D), ("u", E), ("u", k), ("f", eps), ("f", scale), ("u", norm)]
+        ud = [("u", D), ("u", Fe), ("u", E), ("u", k), ("f", eps), ("f", scale), ("u", norm)]
+        quipu.dispatch("moe_gate_up_" + name, ug, [dev.paso(1, 0), hg, hu, xb, dev.buf(nw), dev.buf(lg), h, sel, wts])
+        np.testing.assert_array_equal(dev.get(sel, (k,), np.uint32), s_want)
+        np.testing.assert_allclose(dev.get(wts, (k,)), w_want, rtol=2e-6, atol=1e-7)
+        if call == 0:
+            assert list(s_want[:2]) == [3, E - 2]
+        xn = oracle.rmsnorm(x[None, :], nw, eps)[0].astype(np.float64)
+        got_h = dev.get(h, (k, Fe))
+        for j, e in enumerate(s_want):
+            g = expert_rows(oracle, fmt, rg, e, Fe, D) @ xn
+            u = expert_rows(oracle, fmt, ru, e, Fe, D) @ xn
+            want = g / (1 + np.exp(-g)) * u
+            np.testing.assert_allclose(got_h[j], want, rtol=1e-4, atol=1e-4 * np.abs(want).max(), err_msg=str(j))
+        # down + combine on the GPU's h: x + sum_j wts_j Wd_j h_j
+        quipu.dispatch("moe_down_" + name, ud, [dev.paso(1, 0), hd, h, xb, sel, wts])
+        got = dev.get(xb, (D,))
+        want = x.astype(np.float64)
+        bound = 2e-7 * np.abs(want) + 1e-30
+        for j, e in enumerate(s_want):
+            Wd = expert_rows(oracle, fmt, rd, e, D, Fe)
+            want = want + float(w_want[j]) * (Wd @ got_h[j].astype(np.float64))
+            bound = bound + 2e-5 * abs(float(w_want[j])) * (np.abs(Wd) @ np.abs(got_h[j].astype(np.float64)))
+        assert np.all(np.abs(got - want) <= bound), np.abs(got - want).max()
+
+
 # ------------------------------------------------------------------------------------------------ elementwise
 def test_rmsnorm(quipu, dev, oracle):
     T, D = 5, 4096

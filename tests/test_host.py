@@ -52,8 +52,7 @@ OPS = ["matmul_%s_%s" % (f, s) for f in ("q4k", "q6k", "q8", "f32") for s in ("1
       ["embed_%s" % f for f in ("q4k", "q6k", "q8", "f32")] + \
       ["rmsnorm", "norm_rope", "kv_write", "atencion", "swiglu", "moe_topk", "moe_comb", "gemv", "dec_attn",
        "dec_attn_comb", "argmax", "argmax_fin", "repack_q4k", "repack_q6k", "repack_q8", "fill_u32", "dequant",
-       "copy_f4",
-       "read_f4"]
+       "copy_f4", "read_f4", "moe_gate_up_q4k", "moe_gate_up_q6k", "moe_down_q4k", "moe_down_q6k"]
 
 
 def test_op_table(built):
@@ -69,8 +68,8 @@ def test_ops_used_by_the_js_host_exist(built):
     for f in ("transformer.js", "weights.js"):
         src = open(os.path.join(JS, f)).read()
         used |= set(re.findall(r"['\"]((?:matmul|embed)_[a-z0-9_]+|rmsnorm|norm_rope|kv_write|atencion|swiglu|"
-                               r"moe_topk|moe_comb|gemv|dec_attn(?:_comb)?|argmax(?:_fin)?|repack_q[468]k?|"
-                               r"fill_u32)['\"]", src))
+                               r"moe_topk|moe_comb|moe_(?:gate_up|down)_|gemv|dec_attn(?:_comb)?|argmax(?:_fin)?|"
+                               r"repack_q[468]k?|fill_u32)['\"]", src))
     # names built by concatenation in the host: matmul_<fmt>_<suffix> and embed_<fmt>
     assert used, "no op names found"
     lib = capi.load_library()
