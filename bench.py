@@ -241,7 +241,7 @@ def main():
                    "side_configs": side,
                    "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()} for g in gem],
                    "parity_vs_oracle": check},
-        "roofline": {"bound": "hbm", "kernel": "qp_gemv_q4k (Q4_K GEMV 14336x4096, batch 1)",
+        "roofline": {"bound": "hbm", "kernel": "qp_gemv_q4k_r1 (Q4_K GEMV 14336x4096, batch 1)",
                      "achieved": round(dom["GBs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(dom["GBs"] / PEAK_HBM_GBS, 4), "traffic": committed_traffic(),
                      "bytes_per_launch": dom["bytes"], "us_per_launch": round(dom["us_per_launch"], 3)},

@@ -50,6 +50,44 @@ QP_DEV float half_max(float v) {
     return v;
 }
 
+// Value of the partner lane in step S of a wavefront butterfly made of VALU lane exchanges (no LDS traffic):
+// S = 0: lane ^ 1, 1: lane ^ 2 (quad permutes), 2: mirror within 8 lanes, 3: mirror within 16 lanes (DPP),
+// 4: the other row of a row pair, 5: the other half (gfx950 permlane swaps).  A commutative, associative
+// reduction through the six steps leaves every lane with the reduction of all 64, bit-identical in every lane.
+template <int S>
+QP_DEV uint32_t bfly(uint32_t v, uint32_t lane) {
+    if constexpr (S == 0) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, false);
+    else if constexpr (S == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, false);
+    else if constexpr (S == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, false);
+    else if constexpr (S == 3) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, false);
+    else if constexpr (S == 4) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return ((lane >> 4) & 1) == 0 ? r[1] : r[0];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return lane < 32 ? r[1] : r[0];
+    }
+}
+template <int S>
+QP_DEV float bfly_f(float v, uint32_t lane) { return __uint_as_float(bfly<S>(__float_as_uint(v), lane)); }
+
+QP_DEV float wave_max_v(float v, uint32_t lane) {
+    v = fmaxf(v, bfly_f<0>(v, lane));
+    v = fmaxf(v, bfly_f<1>(v, lane));
+    v = fmaxf(v, bfly_f<2>(v, lane));
+    v = fmaxf(v, bfly_f<3>(v, lane));
+    v = fmaxf(v, bfly_f<4>(v, lane));
+    return fmaxf(v, bfly_f<5>(v, lane));
+}
+QP_DEV float wave_sum_v(float v, uint32_t lane) {
+    v += bfly_f<0>(v, lane);
+    v += bfly_f<1>(v, lane);
+    v += bfly_f<2>(v, lane);
+    v += bfly_f<3>(v, lane);
+    v += bfly_f<4>(v, lane);
+    return v + bfly_f<5>(v, lane);
+}
+
 // Paso in device memory: {T, pos0, a, b}
 QP_DEV uint32_t paso_T(uint64_t p) { return cptr<uint32_t>(p)[0]; }
 QP_DEV uint32_t paso_pos(uint64_t p) { return cptr<uint32_t>(p)[1]; }

@@ -671,10 +671,14 @@ struct KDense {
 
 // The unit loop.  seg_at(i) returns segment i (i < nseg); the wave's units are w, w + W, ... < total_units,
 // segment i owning units [u0_i, u0_{i+1}).  XS: x sub-blocks of 32 per thread for staging (K <= XS * 8192).
-// lay: the weight layout (KDense, or a gathered one whose x sub-blocks may also carry a scale).
-template <int FMT, int R, int XS, class SegAt, class Lay = KDense>
+// lay: the weight layout (KDense, or a gathered one whose x sub-blocks may also carry a scale).  pro: called once
+// the input loads are issued and before the first segment is read (work that decides the segments overlaps them).
+struct KNoPro {
+    QP_DEV void operator()() const {}
+};
+template <int FMT, int R, int XS, class SegAt, class Lay = KDense, class Pro = KNoPro>
 QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t x, uint64_t norm_w, float eps,
-                    uint32_t K, uint64_t amax, Lay lay = Lay()) {
+                    uint32_t K, uint64_t amax, Lay lay = Lay(), Pro pro = Pro()) {
     extern __shared__ float4 xs[];
     float* xsum = reinterpret_cast<float*>(xs + (K >> 8) * 65);
     __shared__ float red[4];
@@ -710,6 +714,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         const uint32_t q = tid + 256 * i;
         xsc[i] = lay.xscale(q < (K >> 5) ? q : 0);  // every lane (a gathered layout shuffles across the wave)
     }
+    pro();
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. the first unit's weights
@@ -952,19 +957,27 @@ QP_DEV void moe_route(const QpMoeArgs& a, uint32_t lane, uint32_t& sel, float& w
         p[j] = e < a.e ? gload<float>(a.logits + 4ull * e) : -3.0e38f;
         m = fmaxf(m, p[j]);
     }
-    m = wave_max(m);
+    m = wave_max_v(m, lane);
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         p[j] = lane + 64 * j < a.e ? expf(p[j] - m) : 0.0f;
         s += p[j];
     }
-    s = wave_sum(s);
+    s = wave_sum_v(s, lane);
 #pragma unroll
     for (int j = 0; j < 4; j++) p[j] = lane + 64 * j < a.e ? p[j] / s : -3.0f;  // -3: below every candidate
     float tot = 0.0f;
     sel = 0;
     wt = 0.0f;
+    // (value, index) of the best candidate kept by a lane and its butterfly partner: higher value, then lower index
+    auto step = [&](auto S, float& bv, uint32_t& bi) __attribute__((always_inline)) {
+        const float ov = bfly_f<decltype(S)::value>(bv, lane);
+        const uint32_t oi = bfly<decltype(S)::value>(bi, lane);
+        const bool take = ov > bv || (ov == bv && oi < bi);
+        bv = take ? ov : bv;
+        bi = take ? oi : bi;
+    };
     for (uint32_t i = 0; i < a.kused; i++) {
         float bv = -1.0f;
         uint32_t bi = 0xffffffffu;
@@ -974,15 +987,12 @@ QP_DEV void moe_route(const QpMoeArgs& a, uint32_t lane, uint32_t& sel, float& w
                 bv = p[j];
                 bi = lane + 64 * j;
             }
-#pragma unroll
-        for (int msk = 32; msk >= 1; msk >>= 1) {
-            const float ov = __shfl_xor(bv, msk, 64);
-            const uint32_t oi = __shfl_xor(bi, msk, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
+        step(std::integral_constant<int, 0>(), bv, bi);
+        step(std::integral_constant<int, 1>(), bv, bi);
+        step(std::integral_constant<int, 2>(), bv, bi);
+        step(std::integral_constant<int, 3>(), bv, bi);
+        step(std::integral_constant<int, 4>(), bv, bi);
+        step(std::integral_constant<int, 5>(), bv, bi);
         if (bi == 0xffffffffu) bi = 0;  // nothing left above -1 (kused > e): expert 0, weight -1, as the reference
 #pragma unroll
         for (int j = 0; j < 4; j++)
@@ -1001,18 +1011,23 @@ QP_DEV void moe_route(const QpMoeArgs& a, uint32_t lane, uint32_t& sel, float& w
 template <int FMT, int XS>
 QP_DEV void moe_gate_up_body(const QpMoeArgs& a) {
     const uint32_t lane = threadIdx.x & 63, job = blockIdx.y;
-    uint32_t sel;
-    float wt;
-    moe_route(a, lane, sel, wt);
-    uint32_t ex = (uint32_t)__builtin_amdgcn_readlane((int)sel, (int)job);
-    if (ex >= a.e) ex = a.e - 1;
-    const KSeg one{a.w, a.w2, a.y + 4ull * job * a.n, a.n, ex * a.n, a.e * a.n, (uint32_t)QP_GEMV_SWIGLU, 0,
-                   (uint32_t)FMT};
+    uint32_t sel = 0, ex = 0;
+    float wt = 0.0f;
+    // the routing runs while the input loads are in flight; the job's expert decides its weight rows
+    auto route = [&]() __attribute__((always_inline)) {
+        moe_route(a, lane, sel, wt);
+        ex = (uint32_t)__builtin_amdgcn_readlane((int)sel, (int)job);
+        if (ex >= a.e) ex = a.e - 1;
+    };
     uint32_t nbp = 1;
     while (nbp < (a.k >> 8)) nbp <<= 1;
     const uint32_t units = (a.n + 64 / nbp - 1) / (64 / nbp);
-    kq_gemv<FMT, 2, XS>([&](uint32_t) __attribute__((always_inline)) { return one; }, 1, units, a.x, a.norm_w, a.eps,
-                        a.k, 0);
+    kq_gemv<FMT, 2, XS>(
+        [&](uint32_t) __attribute__((always_inline)) {
+            return KSeg{a.w, a.w2, a.y + 4ull * job * a.n, a.n, ex * a.n, a.e * a.n, (uint32_t)QP_GEMV_SWIGLU, 0,
+                        (uint32_t)FMT};
+        },
+        1, units, a.x, a.norm_w, a.eps, a.k, 0, KDense(), route);
     if (blockIdx.x == 0 && job == 0 && threadIdx.x < a.kused) {
         gstore<uint32_t>(a.sel + 4ull * lane, sel);
         gstore<float>(a.wts + 4ull * lane, wt);

@@ -290,6 +290,13 @@ if __name__ == "__main__":
     ap.add_argument("config", choices=sorted(CONFIGS))
     ap.add_argument("out")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--prompt", type=int, default=0, help="also write N uniform-random prompt ids to OUT.prompt.json")
+    ap.add_argument("--prompt-seed", type=int, default=7)
     a = ap.parse_args()
-    write_gguf(a.out, CONFIGS[a.config], a.seed)
+    if not os.path.exists(a.out):
+        write_gguf(a.out, CONFIGS[a.config], a.seed)
+    if a.prompt:
+        import json
+        with open(a.out + ".prompt.json", "w") as f:
+            json.dump(random_prompt(CONFIGS[a.config].vocab, a.prompt, a.prompt_seed), f)
     print(a.out)
