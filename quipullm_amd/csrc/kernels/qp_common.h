@@ -167,6 +167,17 @@ QP_DEV uint64_t total_blocks(uint32_t fmt, uint64_t nrows, uint32_t K) {
     return nrows * K;
 }
 
+// ------------------------------------------------------------------ f16 V cache layout
+// The f16 value cache is stored in tiles of 32 slots: for each of the kvd channels c of a tile, the 32 slots' values
+// sit in one 64-byte row, in the order the matrix-core P.V step of the decode attention consumes them.  Slot k of
+// a tile goes to position 8 * ((k % 16) / 4) + 4 * (k / 16) + k % 4 of the row, so the row's 16-byte quarter q holds
+// slots 4q..4q+3 and 16+4q..16+4q+3.  Channel c of slot s: element ((s / 32) * kvd + c) * 32 + vt_pos(s % 32).
+// (The f32 cache keeps the reference's row layout [slot][kvd].)
+QP_DEV uint32_t vt_pos(uint32_t k) { return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3); }
+QP_DEV uint64_t vt_index(uint64_t slot, uint32_t kvd, uint32_t c) {
+    return ((slot >> 5) * kvd + c) * 32 + vt_pos((uint32_t)(slot & 31));
+}
+
 // ------------------------------------------------------------------ sin/cos (reference gpu.js:13-25)
 // Cody-Waite reduction by pi/2 in three parts and the Cephes single-precision minimax polynomials.
 QP_DEV void sincos2(float x, float& sn_out, float& cs_out) {

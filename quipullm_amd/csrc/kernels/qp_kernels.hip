@@ -1470,7 +1470,7 @@ KERNEL __launch_bounds__(256) void qp_kv_write(QpKvArgs a) {
         const uint64_t o = (uint64_t)slot * a.kvd + c;
         if (a.f16) {
             mptr<uint16_t>(a.kc)[o] = f2h(cptr<float>(a.k)[i]);
-            mptr<uint16_t>(a.vc)[o] = f2h(cptr<float>(a.v)[i]);
+            mptr<uint16_t>(a.vc)[vt_index(slot, a.kvd, c)] = f2h(cptr<float>(a.v)[i]);
         } else {
             mptr<float>(a.kc)[o] = cptr<float>(a.k)[i];
             mptr<float>(a.vc)[o] = cptr<float>(a.v)[i];
@@ -1622,7 +1622,7 @@ QP_DEV void attn_gen_body(const QpAttnArgs& a) {
                 const uint32_t sl = a.cap ? key % a.cap : key;
                 const uint64_t idx = (uint64_t)sl * kvd + kvh * HD + dd;
                 kv = kv_load<HD>(a.kc, a.f16, idx);
-                vv = kv_load<HD>(a.vc, a.f16, idx);
+                vv = kv_load<HD>(a.vc, a.f16, a.f16 ? vt_index(sl, kvd, kvh * HD + dd) : idx);
             }
             ks[jj * (HD + 1) + dd] = kv;
             vs[jj * HD + dd] = vv;
@@ -1913,6 +1913,96 @@ QP_DEV void dec_merge_groups(float (&m)[G], float (&l)[G], float (&acc)[G][E], u
     }
 }
 
+// ---- matrix-core key stream (f16 cache).  A wavefront takes its keys in tiles of 32 with v_mfma_f32_16x16x32_f16
+// (lane l: r = l % 16, q = l / 16; an A/B operand lane holds 8 consecutive k of row/column r, k = 8q..8q+7; the
+// 16x16 result lane holds rows 4q..4q+3 of column r):
+//   S^T (16 keys x 16 heads) = K (16 keys x 32 dims) . Q^T, per half of the tile and 32-dim chunk, with q split in
+//     f16 high and low parts (two products: near-f32 scores; the cache values are exact f16);
+//   O^T (16 channels x 16 heads) += V^T (16 channels x 32 slots) . P^T, with P split likewise.  The S^T result lane
+//     holds keys 4q+i and 16+4q+i of head r, exactly the slots 8q..8q+7 of the P^T operand in the V tile order.
+// Heads past G are zero columns.
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// k[hh][c]: key t + 16 hh + r, dims 32 c + 8 q .. + 7; v[mm]: V tile row of channel 16 mm + r, slots 8q..8q+7
+template <int HD>
+struct MTile {
+    u32x4 k[2][HD / 32];
+    u32x4 v[HD / 16];
+};
+
+// Loads of the tile of keys t..t+31 (keys at or past kend load nothing and read as 0; a V tile is loaded whole
+// when it holds any key below kend: its other slots are finite values of the cache, weighted by 0).
+template <int HD>
+QP_DEV void mt_load(MTile<HD>& b, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, uint32_t kvd, uint32_t kvh,
+                    uint32_t t, uint32_t kend, uint32_t lane) {
+    const uint32_t r = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const uint32_t key = t + 16 * hh + r;
+        const uint32_t off = key < kend ? (key * kvd + kvh * HD + 8 * q) * 2 : 0x80000000u;
+#pragma unroll
+        for (int c = 0; c < HD / 32; c++) b.k[hh][c] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 64 * c, 0);
+    }
+    const uint32_t offv = t < kend ? ((t >> 5) * kvd + kvh * HD + r) * 64 + 16 * q : 0x80000000u;
+#pragma unroll
+    for (int mm = 0; mm < HD / 16; mm++) b.v[mm] = __builtin_amdgcn_raw_buffer_load_b128(rv, offv, mm * 1024, 0);
+}
+
+// The online-softmax step of one tile: keys at or past kend and the new key pos0 (not in the cache yet) are
+// masked.  m: running max of this lane's head (the same in its 4 lane groups); l: this lane's share of the sum
+// (its 8 keys per tile); acc: O^T, channels 16 mm + 4q + i of head r.
+template <int HD>
+QP_DEV void mt_consume(const MTile<HD>& b, uint32_t t, uint32_t kend, uint32_t pos0, const h8v (&qh)[HD / 32],
+                       const h8v (&ql)[HD / 32], float scale, float& m, float& l, f4v (&acc)[HD / 16],
+                       uint32_t lane) {
+    const uint32_t q = lane >> 4;
+    f4v s[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        s[hh] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < HD / 32; c++) {
+            const h8v kk = __builtin_bit_cast(h8v, b.k[hh][c]);
+            s[hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, qh[c], s[hh], 0, 0, 0);
+            s[hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, ql[c], s[hh], 0, 0, 0);
+        }
+    }
+    float sv[8];
+    bool ok[8];
+    float mx = -3.0e38f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t key = t + 16 * (j >> 2) + 4 * q + (j & 3);
+        ok[j] = key < kend && key != pos0;
+        sv[j] = s[j >> 2][j & 3] * scale;
+        if (ok[j]) mx = fmaxf(mx, sv[j]);
+    }
+    mx = fmaxf(mx, bfly_f<4>(mx, lane));
+    mx = fmaxf(mx, bfly_f<5>(mx, lane));
+    const float mn = fmaxf(m, mx);
+    const float cf = __builtin_amdgcn_exp2f((m - mn) * QP_LOG2E);
+    m = mn;
+    float ps = 0.0f;
+    h8v ph, pl;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float p = ok[j] ? __builtin_amdgcn_exp2f((sv[j] - mn) * QP_LOG2E) : 0.0f;
+        ps += p;
+        const _Float16 hi = (_Float16)p;
+        ph[j] = hi;
+        pl[j] = (_Float16)(p - (float)hi);
+    }
+    l = l * cf + ps;
+#pragma unroll
+    for (int mm = 0; mm < HD / 16; mm++) {
+        acc[mm] = acc[mm] * cf;
+        const h8v vv = __builtin_bit_cast(h8v, b.v[mm]);
+        acc[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, ph, acc[mm], 0, 0, 0);
+        acc[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pl, acc[mm], 0, 0, 0);
+    }
+}
+
 // LDS (floats): kn [HD] | vn [HD] | freq [HD/2] | q-norm, k-norm weights [HD] each | region R: q [G][HD]
 // during the preparation, then the wavefront partials wacc [4][G][HD], wm [4][8], wl [4][8].
 template <int HD, bool F16, int G>
@@ -1937,7 +2027,8 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
     const uint32_t pos0 = paso_pos(a.paso);
     const uint32_t nk = pos0 < a.rows ? pos0 + 1 : 0;  // a position past the cache reads and writes nothing
     const uint32_t W = 4 * a.nsplit;
-    const uint32_t per = (nk + W - 1) / W;
+    // keys per wavefront (whole tiles of 32 for the matrix-core stream)
+    const uint32_t per = F16 ? ((nk + W - 1) / W + 31) & ~31u : (nk + W - 1) / W;
     const uint32_t kw0 = min(nk, (wg * 4 + wave) * per), kw1 = min(nk, kw0 + per);
     const uint32_t g0 = min(nk, wg * 4 * per), g1 = min(nk, g0 + 4 * per);
     const bool wg_new = g0 <= pos0 && pos0 < g1;  // this workgroup holds the new key: it appends it
@@ -1957,11 +2048,18 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
     if (a.knorm && wg_new && tid < HD) kwt = gload<float>(a.knorm + 4ull * tid);
     // issued by every wavefront (one without keys loads nothing: its offsets are past the end), so the waits below
     // can count these loads as still in flight
-    const uint64_t cbytes = (uint64_t)a.rows * a.nkv * HD * (F16 ? 2 : 4);
-    const __amdgpu_buffer_rsrc_t rk = kq_rsrc(a.kc, cbytes), rv = kq_rsrc(a.vc, cbytes);
+    const uint32_t kvd = a.nkv * HD;
+    const uint64_t cbytes = (uint64_t)a.rows * kvd * (F16 ? 2 : 4);
+    const uint64_t vbytes = F16 ? (uint64_t)((a.rows + 31) / 32) * 32 * kvd * 2 : cbytes;  // whole tiles
+    const __amdgpu_buffer_rsrc_t rk = kq_rsrc(a.kc, cbytes), rv = kq_rsrc(a.vc, vbytes);
     DecBuf A, B;
-    dec_load<HD, F16>(A, rk, rv, a.nkv, kvh, kw0, kw1, kq, dsub);
-    dec_load<HD, F16>(B, rk, rv, a.nkv, kvh, kw0 + KS, kw1, kq, dsub);
+    MTile<HD> MA;  // one tile in flight: a workgroup covers about 128 keys, one tile per wavefront
+    if constexpr (F16) {
+        mt_load<HD>(MA, rk, rv, kvd, kvh, kw0, kw1, lane);
+    } else {
+        dec_load<HD, F16>(A, rk, rv, a.nkv, kvh, kw0, kw1, kq, dsub);
+        dec_load<HD, F16>(B, rk, rv, a.nkv, kvh, kw0 + KS, kw1, kq, dsub);
+    }
     // 2. the preparation (waits for the loads of 1 only)
     if (tid < a.nrot / 2)
         freq[tid] = a.freq ? ft : (float)pow((double)a.base, (double)((-2.0f * (float)tid) / (float)a.nrot));
@@ -1995,6 +2093,61 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
         vn[tid] = h2f(f2h(vn[tid]));
     }
     __syncthreads();
+    if constexpr (F16) {
+        // q of head r = lane % 16 as the B operand (dims 32c + 8q + j), split in f16 high and low parts
+        const uint32_t hr = lane & 15, qg = lane >> 4;
+        h8v qh[HD / 32], ql[HD / 32];
+#pragma unroll
+        for (int c = 0; c < HD / 32; c++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float v = hr < G ? qs[hr * HD + 32 * c + 8 * qg + j] : 0.0f;
+                const _Float16 hi = (_Float16)v;
+                qh[c][j] = hi;
+                ql[c][j] = (_Float16)(v - (float)hi);
+            }
+        __syncthreads();  // every wavefront holds its q before region R is reused
+        float m = -3.0e38f, l = 0.0f;
+        f4v acc[HD / 16];
+#pragma unroll
+        for (int mm = 0; mm < HD / 16; mm++) acc[mm] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t t = kw0; t < kw1; t += 32) {
+            mt_consume<HD>(MA, t, kw1, pos0, qh, ql, a.scale, m, l, acc, lane);
+            if (t + 32 < kw1) mt_load<HD>(MA, rk, rv, kvd, kvh, t + 32, kw1, lane);
+        }
+        if (kw0 <= pos0 && pos0 < kw1) {
+            // the new key, from kn / vn (the cache slot is written at the end)
+            float d = 0.0f;
+#pragma unroll
+            for (int c = 0; c < HD / 32; c++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) d = fmaf((float)qh[c][j] + (float)ql[c][j], kn[32 * c + 8 * qg + j], d);
+            d += bfly_f<4>(d, lane);
+            d += bfly_f<5>(d, lane);
+            const float sn = d * a.scale;
+            const float mn = fmaxf(m, sn);
+            const float cf = __builtin_amdgcn_exp2f((m - mn) * QP_LOG2E);
+            const float p = __builtin_amdgcn_exp2f((sn - mn) * QP_LOG2E);
+            m = mn;
+            l = l * cf + (qg == 0 ? p : 0.0f);
+#pragma unroll
+            for (int mm = 0; mm < HD / 16; mm++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[mm][i] = fmaf(p, vn[16 * mm + 4 * qg + i], acc[mm][i] * cf);
+        }
+        float lt = l + bfly_f<4>(l, lane);
+        lt += bfly_f<5>(lt, lane);
+        if (hr < G) {
+#pragma unroll
+            for (int mm = 0; mm < HD / 16; mm++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) wacc[(wave * G + hr) * HD + 16 * mm + 4 * qg + i] = acc[mm][i];
+            if (qg == 0) {
+                wm[wave * 8 + hr] = m;
+                wl[wave * 8 + hr] = lt;
+            }
+        }
+    } else {
     float qr[G][E];
 #pragma unroll
     for (int g = 0; g < G; g++)
@@ -2036,6 +2189,7 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
             }
         }
     }
+    }
     __syncthreads();
     // 5. this workgroup's partial per head: merge of its 4 wavefronts (those with no key have l = 0)
     for (uint32_t t = tid; t < G * HD; t += 256) {
@@ -2056,10 +2210,10 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
     }
     if (wg_new && tid < HD) {
         // append the new key and value to the cache at slot pos0 (kn / vn hold them, f16-rounded in f16 mode)
-        const uint64_t o = (uint64_t)pos0 * a.nkv * HD + (uint64_t)kvh * HD + tid;
+        const uint64_t o = (uint64_t)pos0 * kvd + (uint64_t)kvh * HD + tid;
         if (F16) {
             gstore<uint16_t>(a.kc + 2 * o, f2h(kn[tid]));
-            gstore<uint16_t>(a.vc + 2 * o, f2h(vn[tid]));
+            gstore<uint16_t>(a.vc + 2 * vt_index(pos0, kvd, kvh * HD + tid), f2h(vn[tid]));
         } else {
             gstore<float>(a.kc + 4 * o, kn[tid]);
             gstore<float>(a.vc + 4 * o, vn[tid]);
@@ -2067,8 +2221,10 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
     }
 }
 
-#define DEC_ATTN_KERNEL(HD, KV, F16, G) \
-    KERNEL __launch_bounds__(256) void qp_dec_attn_h##HD##_##KV##_g##G(QpDecAttnArgs a) { attn_dec_body<HD, F16, G>(a); }
+// (two workgroups per CU: at most 256 registers per lane)
+#define DEC_ATTN_KERNEL(HD, KV, F16, G)                                                                          \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qp_dec_attn_h##HD##_##KV##_g##G( \
+        QpDecAttnArgs a) { attn_dec_body<HD, F16, G>(a); }
 #define DEC_ATTN_KERNELS(HD, KV, F16) \
     DEC_ATTN_KERNEL(HD, KV, F16, 1) DEC_ATTN_KERNEL(HD, KV, F16, 2) DEC_ATTN_KERNEL(HD, KV, F16, 4) DEC_ATTN_KERNEL(HD, KV, F16, 8)
 DEC_ATTN_KERNELS(64, f16, true)

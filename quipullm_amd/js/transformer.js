@@ -73,7 +73,7 @@ class ModeloTransformer {
       this.salida = c.existe('output.weight') ? c.matriz('output.weight') : this.emb;
       this.normFinal = c.f32('output_norm.weight');
       this.capas = [];
-      let F = 0;
+      let F = 0, ceros = null;
       for (let i = 0; i < this.nLayers; i++) {
         const p = 'blk.' + i + '.';
         for (const n of ['attn_q.bias', 'attn_k.bias', 'attn_v.bias', 'attn_output.bias', 'post_attention_norm.weight', 'post_ffw_norm.weight'])
@@ -102,7 +102,12 @@ class ModeloTransformer {
         }
         const kvd = this.nkv * this.hd, eb = this.kvF16 ? 2 : 4;
         capa.kc = gpu.buffer(this.ctx * kvd * eb, undefined, 'kcache' + i);
-        capa.vc = gpu.buffer(this.ctx * kvd * eb, undefined, 'vcache' + i);
+        // the f16 value cache is stored in whole tiles of 32 slots, read whole by the decode attention: it starts
+        // zeroed so that slots not yet written hold finite values (they are weighted by 0)
+        const vBytes = (this.kvF16 ? Math.ceil(this.ctx / 32) * 32 : this.ctx) * kvd * eb;
+        capa.vc = gpu.buffer(vBytes, undefined, 'vcache' + i);
+        if (!ceros || ceros.length < vBytes) ceros = new Uint8Array(vBytes);
+        gpu.escribir(capa.vc, 0, ceros.subarray(0, vBytes));
         this.bufs.push(capa.kc, capa.vc);
         this.capas.push(capa);
       }

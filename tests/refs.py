@@ -219,3 +219,26 @@ class Model64:
 def rel_err(a, b):
     a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
     return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def vt_pos(k):
+    """Position of slot k (of 32) in a row of the device's f16 value-cache tile."""
+    return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3)
+
+
+def v_tiled(v, kvd):
+    """f16 value cache rows [slots][kvd] -> the device tile layout: tiles of 32 slots, each [kvd][32] with slot k
+    at vt_pos(k) (slots past the last row are zero)."""
+    v = np.asarray(v).reshape(-1, kvd)
+    nt = (v.shape[0] + 31) // 32
+    pad = np.zeros((nt * 32, kvd), v.dtype)
+    pad[:v.shape[0]] = v
+    out = np.zeros((nt, kvd, 32), v.dtype)
+    out[:, :, [vt_pos(k) for k in range(32)]] = pad.reshape(nt, 32, kvd).transpose(0, 2, 1)
+    return out
+
+
+def v_rows(tiled, rows, kvd):
+    """Inverse of v_tiled: rows [rows][kvd]."""
+    t = np.asarray(tiled).reshape(-1, kvd, 32)[:, :, [vt_pos(k) for k in range(32)]]
+    return t.transpose(0, 2, 1).reshape(-1, kvd)[:rows]

@@ -397,11 +397,14 @@ def test_kv_write(quipu, dev, oracle, f16):
     k = np.random.default_rng(16).standard_normal((T, kvd)).astype(np.float32)
     v = np.random.default_rng(17).standard_normal((T, kvd)).astype(np.float32)
     es = 2 if f16 else 4
-    kc, vc = dev.zeros(rows * kvd * es), dev.zeros(rows * kvd * es)
+    vrows = (rows + 31) // 32 * 32 if f16 else rows  # the f16 value cache is stored in whole tiles of 32 slots
+    kc, vc = dev.zeros(rows * kvd * es), dev.zeros(vrows * kvd * es)
     quipu.dispatch("kv_write", [("u", kvd), ("u", 0), ("u", f16), ("u", rows)],
                    [dev.paso(T, pos0), dev.buf(k), dev.buf(v), kc, vc], ((T * kvd + 255) // 256,))
     dt = np.float16 if f16 else np.float32
-    gk, gv = dev.get(kc, (rows, kvd), dt), dev.get(vc, (rows, kvd), dt)
+    gk, gv = dev.get(kc, (rows, kvd), dt), dev.get(vc, (vrows, kvd), dt)
+    if f16:
+        gv = refs.v_rows(gv, rows, kvd)
     # rows 15..18 written (f16: round to nearest even), everything else untouched
     np.testing.assert_array_equal(gk[pos0:pos0 + T], k.astype(dt))
     np.testing.assert_array_equal(gv[pos0:pos0 + T], v.astype(dt))
@@ -485,7 +488,8 @@ def test_atencion_prefill(quipu, dev, oracle, hd, nh, nkv, T, pos0, f16):
     scale = float(np.float32(1 / np.sqrt(hd)))
     quipu.dispatch("atencion", [("u", hd), ("u", nh), ("u", nkv), ("u", 0), ("f", scale), ("u", 0), ("u", 0), ("u", 0),
                                 ("u", f16), ("u", rows)],
-                   [dev.paso(T, pos0), dev.buf(q), dev.buf(kc.astype(dt)), dev.buf(vc.astype(dt)), o], (nh, T))
+                   [dev.paso(T, pos0), dev.buf(q), dev.buf(kc.astype(dt)),
+                    dev.buf(refs.v_tiled(vc.astype(dt), kvd) if f16 else vc), o], (nh, T))
     got = dev.get(o, (T, nh * hd))
     want = oracle.attention(q, kc, vc, T, pos0, nh, nkv, hd, scale)
     np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
@@ -495,7 +499,8 @@ def test_atencion_prefill(quipu, dev, oracle, hd, nh, nkv, T, pos0, f16):
 @pytest.mark.parametrize("hd,nh,nkv,pos0,nsplit,f16,neox,qk_norm",
                          [(128, 32, 8, 0, 4, 0, 0, 0), (128, 32, 8, 4095, 64, 1, 0, 0), (128, 32, 8, 777, 7, 0, 1, 1),
                           (64, 16, 16, 100, 3, 1, 1, 0), (64, 8, 1, 31, 1, 0, 0, 1), (128, 16, 8, 33, 200, 0, 0, 0),
-                          (64, 32, 4, 2000, 16, 1, 0, 1), (128, 32, 4, 1500, 33, 1, 1, 1), (128, 8, 8, 5, 256, 0, 0, 0)])
+                          (64, 32, 4, 2000, 16, 1, 0, 1), (128, 32, 4, 1500, 33, 1, 1, 1), (128, 8, 8, 5, 256, 0, 0, 0),
+                          (128, 16, 8, 31, 2, 1, 0, 0), (128, 8, 1, 64, 5, 1, 1, 1), (64, 8, 4, 95, 1, 1, 0, 0)])
 def test_dec_attn_fused(quipu, dev, oracle, hd, nh, nkv, pos0, nsplit, f16, neox, qk_norm, table):
     """One-token attention with the fused q/k norm + RoPE + KV append, split over the keys and merged by
     dec_attn_comb, with the RoPE frequency table bound or computed in the kernel; the expected result is the
@@ -515,7 +520,7 @@ def test_dec_attn_fused(quipu, dev, oracle, hd, nh, nkv, pos0, nsplit, f16, neox
     eps, base = 1e-6, 1e6
     scale = float(np.float32(1 / np.sqrt(hd)))
     dt = np.float16 if f16 else np.float32
-    kcb, vcb = dev.buf(kc.astype(dt)), dev.buf(vc.astype(dt))
+    kcb, vcb = dev.buf(kc.astype(dt)), dev.buf(refs.v_tiled(vc.astype(dt), kvd) if f16 else vc)
     po, pml, o = dev.zeros(nh * nsplit * hd * 4), dev.zeros(nh * nsplit * 8), dev.zeros(nh * hd * 4)
     paso = dev.paso(1, pos0)
     u = [("u", hd), ("u", nh), ("u", nkv), ("u", nsplit), ("f", scale), ("f", eps), ("f", base), ("u", 0),
@@ -535,7 +540,8 @@ def test_dec_attn_fused(quipu, dev, oracle, hd, nh, nkv, pos0, nsplit, f16, neox
     want = oracle.attention(qr, kc2, vc2, 1, pos0, nh, nkv, hd, scale)[0]
     np.testing.assert_allclose(got, want, rtol=5e-5, atol=5e-5)
     # the appended cache row: RoPE'd key (to within the rotation's rounding), value copied (rounded if f16)
-    gk, gv = dev.get(kcb, (rows, kvd), dt), dev.get(vcb, (rows, kvd), dt)
+    gk = dev.get(kcb, (rows, kvd), dt)
+    gv = refs.v_rows(dev.get(vcb, ((rows + 31) // 32 * 32, kvd), dt), rows, kvd) if f16 else dev.get(vcb, (rows, kvd))
     np.testing.assert_allclose(gk[pos0].astype(np.float32), kc2[pos0], rtol=1e-5, atol=2e-3 if f16 else 1e-5)
     np.testing.assert_array_equal(gv[pos0].astype(np.float32), vc2[pos0])
     np.testing.assert_array_equal(gv[pos0 + 1:].astype(np.float32), vc[pos0 + 1:])
