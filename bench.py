@@ -162,7 +162,8 @@ def parity(gpu_ids, gpu_lg, cpu_ids, cpu_lg):
     """Greedy ids and logits of the GPU run against the oracle's on the same prompt (f16 KV on both)."""
     n = min(len(gpu_ids), len(cpu_ids))
     rel = [float(np.max(np.abs(a - b)) / np.max(np.abs(b))) for a, b in zip(gpu_lg[:n], cpu_lg[:n])]
-    return {"tokens": n, "ids_identical": gpu_ids[:n] == cpu_ids[:n], "max_rel_logits": max(rel),
+    # np.max propagates a NaN (Python's max would skip it depending on the order)
+    return {"tokens": n, "ids_identical": gpu_ids[:n] == cpu_ids[:n], "max_rel_logits": float(np.max(rel)),
             "prompt": CHECK_PROMPT}
 
 

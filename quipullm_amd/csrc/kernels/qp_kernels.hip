@@ -1924,6 +1924,39 @@ QP_DEV void dec_merge_groups(float (&m)[G], float (&l)[G], float (&acc)[G][E], u
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
+// The f16 high/low split of a lane's row of q (8 dims per 32-dim chunk, the row spread over the 4 lane groups).
+// The row is first scaled by an exact power of two f that puts its largest magnitude in [2^13, 2^14), so the low
+// parts stay normal f16 numbers (a subnormal low part would lose the precision the split is for); returns 1/f,
+// the factor that takes the products back to the row's scale.
+template <int HD>
+QP_DEV float mt_split_q(const float (&v)[HD / 32][8], h8v (&qh)[HD / 32], h8v (&ql)[HD / 32], uint32_t lane) {
+    float mx = 0.0f;
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[c][j]));
+    mx = fmaxf(mx, bfly_f<4>(mx, lane));
+    mx = fmaxf(mx, bfly_f<5>(mx, lane));
+    int e = 0;
+    (void)frexpf(mx, &e);  // mx = m * 2^e, m in [0.5, 1)
+    const int sh = mx > 0.0f ? min(max(14 - e, -100), 100) : 0;
+    const float f = ldexpf(1.0f, sh);
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float x = v[c][j] * f;
+            const _Float16 hi = (_Float16)x;
+            qh[c][j] = hi;
+            ql[c][j] = (_Float16)(x - (float)hi);
+        }
+    return ldexpf(1.0f, -sh);
+}
+
+// Probabilities enter P.V scaled by 2^14 (exact): their low f16 parts stay normal down to p ~ 1e-5.  The running
+// sums l carry the same factor, so o = acc / l is unchanged.
+constexpr float QP_PSCALE = 16384.0f;
+
 // k[hh][c]: key t + 16 hh + r, dims 32 c + 8 q .. + 7; v[mm]: V tile row of channel 16 mm + r, slots 8q..8q+7
 template <int HD>
 struct MTile {
@@ -1950,12 +1983,16 @@ QP_DEV void mt_load(MTile<HD>& b, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsr
 }
 
 // The online-softmax step of one tile: keys at or past kend and the new key pos0 (not in the cache yet) are
-// masked.  m: running max of this lane's head (the same in its 4 lane groups); l: this lane's share of the sum
-// (its 8 keys per tile); acc: O^T, channels 16 mm + 4q + i of head r.
+// masked.  scale: this lane's score factor (the attention scale times the 1/f of its q split).  m: running max of
+// this lane's row (the same in its 4 lane groups); l: this lane's share of the sum (its 8 keys per tile), times
+// QP_PSCALE; acc: O^T, channels 16 mm + 4q + i of row r, times QP_PSCALE.
 template <int HD>
 QP_DEV void mt_consume(const MTile<HD>& b, uint32_t t, uint32_t kend, uint32_t pos0, const h8v (&qh)[HD / 32],
                        const h8v (&ql)[HD / 32], float scale, float& m, float& l, f4v (&acc)[HD / 16],
                        uint32_t lane) {
+    // no contraction: the exponent must use the same rounded score the max was taken over (an FMA of s * scale - m
+    // would not, and with large scores p could exceed 1 and the scaled p the f16 range)
+#pragma clang fp contract(off)
     const uint32_t q = lane >> 4;
     f4v s[2];
 #pragma unroll
@@ -1987,7 +2024,7 @@ QP_DEV void mt_consume(const MTile<HD>& b, uint32_t t, uint32_t kend, uint32_t p
     h8v ph, pl;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        const float p = ok[j] ? __builtin_amdgcn_exp2f((sv[j] - mn) * QP_LOG2E) : 0.0f;
+        const float p = ok[j] ? __builtin_amdgcn_exp2f(fminf(sv[j] - mn, 0.0f) * QP_LOG2E) * QP_PSCALE : 0.0f;
         ps += p;
         const _Float16 hi = (_Float16)p;
         ph[j] = hi;
@@ -2097,26 +2134,24 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
         // q of head r = lane % 16 as the B operand (dims 32c + 8q + j), split in f16 high and low parts
         const uint32_t hr = lane & 15, qg = lane >> 4;
         h8v qh[HD / 32], ql[HD / 32];
+        float qv[HD / 32][8];
 #pragma unroll
         for (int c = 0; c < HD / 32; c++)
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float v = hr < G ? qs[hr * HD + 32 * c + 8 * qg + j] : 0.0f;
-                const _Float16 hi = (_Float16)v;
-                qh[c][j] = hi;
-                ql[c][j] = (_Float16)(v - (float)hi);
-            }
+            for (int j = 0; j < 8; j++) qv[c][j] = hr < G ? qs[hr * HD + 32 * c + 8 * qg + j] : 0.0f;
+        const float qsc = a.scale * mt_split_q<HD>(qv, qh, ql, lane);
         __syncthreads();  // every wavefront holds its q before region R is reused
         float m = -3.0e38f, l = 0.0f;
         f4v acc[HD / 16];
 #pragma unroll
         for (int mm = 0; mm < HD / 16; mm++) acc[mm] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
         for (uint32_t t = kw0; t < kw1; t += 32) {
-            mt_consume<HD>(MA, t, kw1, pos0, qh, ql, a.scale, m, l, acc, lane);
+            mt_consume<HD>(MA, t, kw1, pos0, qh, ql, qsc, m, l, acc, lane);
             if (t + 32 < kw1) mt_load<HD>(MA, rk, rv, kvd, kvh, t + 32, kw1, lane);
         }
         if (kw0 <= pos0 && pos0 < kw1) {
             // the new key, from kn / vn (the cache slot is written at the end)
+#pragma clang fp contract(off)
             float d = 0.0f;
 #pragma unroll
             for (int c = 0; c < HD / 32; c++)
@@ -2124,10 +2159,10 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
                 for (int j = 0; j < 8; j++) d = fmaf((float)qh[c][j] + (float)ql[c][j], kn[32 * c + 8 * qg + j], d);
             d += bfly_f<4>(d, lane);
             d += bfly_f<5>(d, lane);
-            const float sn = d * a.scale;
+            const float sn = d * qsc;
             const float mn = fmaxf(m, sn);
             const float cf = __builtin_amdgcn_exp2f((m - mn) * QP_LOG2E);
-            const float p = __builtin_amdgcn_exp2f((sn - mn) * QP_LOG2E);
+            const float p = __builtin_amdgcn_exp2f(fminf(sn - mn, 0.0f) * QP_LOG2E) * QP_PSCALE;
             m = mn;
             l = l * cf + (qg == 0 ? p : 0.0f);
 #pragma unroll
@@ -2231,6 +2266,72 @@ DEC_ATTN_KERNELS(64, f16, true)
 DEC_ATTN_KERNELS(64, f32, false)
 DEC_ATTN_KERNELS(128, f16, true)
 DEC_ATTN_KERNELS(128, f32, false)
+
+// Causal attention of a prefill chunk on the matrix cores (f16 cache; no sliding window, no ring cap), the
+// reference atencion (gpu.js:467-539).  Wavefront w of workgroup (kvh, y) takes 16 rows: TPW = 16 / G tokens x the
+// G heads of KV head kvh (row r: token t0 + r / G, head r % G), and streams keys 0 .. pos0 + its last token in
+// tiles of 32 with the decode tile step (two tiles in flight), each row masked at its own causal limit.
+template <int HD, int G>
+QP_DEV void attn_mfma_body(const QpAttnArgs& a) {
+    constexpr uint32_t TPW = 16 / G;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t T = paso_T(a.paso), pos0 = paso_pos(a.paso);
+    const uint32_t kvh = blockIdx.x, t0 = (blockIdx.y * 4 + wave) * TPW;
+    if (t0 >= T) return;  // the whole wavefront (no barriers below)
+    const uint32_t kvd = a.nkv * HD, r = lane & 15, qg = lane >> 4;
+    const uint32_t tr = t0 + r / G, hr = kvh * G + r % G;  // this lane's row
+    const bool row_ok = tr < T;
+    const uint32_t tlast = min(t0 + TPW, T) - 1;
+    const uint32_t kend = min(pos0 + tlast + 1, a.rows);                      // keys this wavefront reads
+    const uint32_t kend_row = row_ok ? min(pos0 + tr + 1, a.rows) : 0u;       // keys this row attends to
+    const __amdgpu_buffer_rsrc_t rk = kq_rsrc(a.kc, (uint64_t)a.rows * kvd * 2);
+    const __amdgpu_buffer_rsrc_t rv = kq_rsrc(a.vc, (uint64_t)((a.rows + 31) / 32) * 32 * kvd * 2);
+    MTile<HD> A, B;
+    mt_load<HD>(A, rk, rv, kvd, kvh, 0, kend, lane);
+    mt_load<HD>(B, rk, rv, kvd, kvh, 32, kend, lane);
+    h8v qh[HD / 32], ql[HD / 32];
+    float qv[HD / 32][8];
+    const uint64_t qrow = a.q + 4ull * (((uint64_t)(row_ok ? tr : 0) * a.nh + hr) * HD);
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++) {
+        const float4 x0 = gload<float4>(qrow + 4 * (32 * c + 8 * qg));
+        const float4 x1 = gload<float4>(qrow + 4 * (32 * c + 8 * qg + 4));
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) qv[c][j] = row_ok ? xv[j] : 0.0f;
+    }
+    const float qsc = a.scale * mt_split_q<HD>(qv, qh, ql, lane);
+    float m = -3.0e38f, l = 0.0f;
+    f4v acc[HD / 16];
+#pragma unroll
+    for (int mm = 0; mm < HD / 16; mm++) acc[mm] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t t = 0; t < kend; t += 64) {
+        mt_consume<HD>(A, t, kend_row, 0xffffffffu, qh, ql, qsc, m, l, acc, lane);
+        mt_load<HD>(A, rk, rv, kvd, kvh, t + 64, kend, lane);
+        if (t + 32 < kend) mt_consume<HD>(B, t + 32, kend_row, 0xffffffffu, qh, ql, qsc, m, l, acc, lane);
+        mt_load<HD>(B, rk, rv, kvd, kvh, t + 96, kend, lane);
+    }
+    float lt = l + bfly_f<4>(l, lane);
+    lt += bfly_f<5>(lt, lane);
+    if (row_ok) {
+        const uint64_t orow = a.o + 4ull * (((uint64_t)tr * a.nh + hr) * HD);
+#pragma unroll
+        for (int mm = 0; mm < HD / 16; mm++) {
+            float4 v;
+            v.x = lt > 0.0f ? acc[mm][0] / lt : 0.0f;
+            v.y = lt > 0.0f ? acc[mm][1] / lt : 0.0f;
+            v.z = lt > 0.0f ? acc[mm][2] / lt : 0.0f;
+            v.w = lt > 0.0f ? acc[mm][3] / lt : 0.0f;
+            gstore<float4>(orow + 4 * (16 * mm + 4 * qg), v);
+        }
+    }
+}
+
+#define ATTN_MFMA_KERNEL(HD, G)                                                                                   \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qp_attn_mfma_h##HD##_g##G(        \
+        QpAttnArgs a) { attn_mfma_body<HD, G>(a); }
+ATTN_MFMA_KERNEL(64, 1) ATTN_MFMA_KERNEL(64, 2) ATTN_MFMA_KERNEL(64, 4) ATTN_MFMA_KERNEL(64, 8)
+ATTN_MFMA_KERNEL(128, 1) ATTN_MFMA_KERNEL(128, 2) ATTN_MFMA_KERNEL(128, 4) ATTN_MFMA_KERNEL(128, 8)
 
 // Merge of the split partials: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), splits with l = 0 skipped
 // (all of them empty, for a position past the cache: o = 0).

@@ -465,7 +465,16 @@ int op_atencion(const Ctx& c) {
     a.kc = c.B(2);
     a.vc = c.B(3);
     a.o = c.B(4);
-    const uint32_t qb = 32 / (a.nh / a.nkv);
+    const uint32_t G = a.nh / a.nkv;
+    if (a.f16 && !a.swa && !a.cap && (G == 1 || G == 2 || G == 4 || G == 8) && !getenv_flag("QP_NO_MFMA")) {
+        // matrix-core path: a wavefront takes 16 / G tokens x G heads, a workgroup four wavefronts
+        static const Kid km[2][4] = {{K_attn_mfma_h64_g1, K_attn_mfma_h64_g2, K_attn_mfma_h64_g4, K_attn_mfma_h64_g8},
+                                     {K_attn_mfma_h128_g1, K_attn_mfma_h128_g2, K_attn_mfma_h128_g4,
+                                      K_attn_mfma_h128_g8}};
+        const uint32_t gi = G == 1 ? 0 : G == 2 ? 1 : G == 4 ? 2 : 3;
+        return launch(km[a.hd == 128][gi], a.nkv, cdiv(c.gy ? c.gy : 1, 4 * (16 / G)), 1, 256, 0, a);
+    }
+    const uint32_t qb = 32 / G;
     a.qb = qb;
     return launch(a.hd == 64 ? K_attn_hd64 : K_attn_hd128, a.nkv, cdiv(c.gy ? c.gy : 1, qb), 1, 256, attn_lds(a.hd),
                   a);

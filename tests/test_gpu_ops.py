@@ -473,9 +473,12 @@ def f16r(a):
 
 @pytest.mark.parametrize("hd,nh,nkv,T,pos0,f16", [(128, 32, 8, 1, 0, 0), (128, 32, 8, 9, 100, 0),
                                                   (64, 8, 2, 33, 40, 1), (128, 16, 16, 5, 300, 1),
-                                                  (64, 16, 1, 3, 7, 0)])
+                                                  (64, 16, 1, 3, 7, 0), (128, 32, 4, 70, 1000, 1),
+                                                  (64, 16, 8, 17, 0, 1), (128, 32, 8, 64, 1031, 1),
+                                                  (128, 8, 8, 1, 31, 1)])
 def test_atencion_prefill(quipu, dev, oracle, hd, nh, nkv, T, pos0, f16):
-    rows = 512
+    """The reference atencion op for a prefill chunk; with the f16 cache it runs on the matrix cores."""
+    rows = max(512, pos0 + T + 5)
     kvd = nkv * hd
     rng = np.random.default_rng(20)
     q = rng.standard_normal((T, nh * hd)).astype(np.float32)
@@ -545,6 +548,48 @@ def test_dec_attn_fused(quipu, dev, oracle, hd, nh, nkv, pos0, nsplit, f16, neox
     np.testing.assert_allclose(gk[pos0].astype(np.float32), kc2[pos0], rtol=1e-5, atol=2e-3 if f16 else 1e-5)
     np.testing.assert_array_equal(gv[pos0].astype(np.float32), vc2[pos0])
     np.testing.assert_array_equal(gv[pos0 + 1:].astype(np.float32), vc[pos0 + 1:])
+
+
+@pytest.mark.parametrize("pos0", [4, 40, 700])
+def test_attention_large_scores_stay_finite(quipu, dev, oracle, pos0):
+    """Scores of order 1e8 (q and k of order 1e4) through the matrix-core decode and prefill attention: the softmax
+    exponent must use the rounded score the running max was taken over, or p (scaled into the f16 range) overflows
+    and the result turns NaN."""
+    hd, nh, nkv, nsplit, rows = 128, 32, 8, 35, 1024
+    kvd = nkv * hd
+    rng = np.random.default_rng(pos0)
+    q = (rng.standard_normal(nh * hd) * 1e4).astype(np.float32)
+    k = (rng.standard_normal(kvd) * 1e4).astype(np.float32)
+    v = rng.standard_normal(kvd).astype(np.float32)
+    kc = f16r(rng.standard_normal((rows, kvd)) * 1e4)
+    vc = f16r(rng.standard_normal((rows, kvd)))
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    kcb, vcb = dev.buf(kc.astype(np.float16)), dev.buf(refs.v_tiled(vc.astype(np.float16), kvd))
+    po, pml, o = dev.zeros(nh * nsplit * hd * 4), dev.zeros(nh * nsplit * 8), dev.zeros(nh * hd * 4)
+    paso = dev.paso(1, pos0)
+    u = [("u", hd), ("u", nh), ("u", nkv), ("u", nsplit), ("f", scale), ("f", 1e-5), ("f", 1e4), ("u", 0),
+         ("u", hd), ("u", 0), ("u", 1), ("u", rows)]
+    quipu.dispatch("dec_attn", u, [paso, dev.buf(q), dev.buf(k), dev.buf(v), kcb, vcb, 0, 0, po, pml])
+    quipu.dispatch("dec_attn_comb", [("u", hd), ("u", nh), ("u", nsplit)], [paso, po, pml, o])
+    got = dev.get(o, (nh * hd,))
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[pos0] = f16r(oracle.norm_rope(k, None, nkv, hd, 0, 0, 1e-5, 1e4, hd, pos0))
+    vc2[pos0] = f16r(v)
+    want = oracle.attention(oracle.norm_rope(q, None, nh, hd, 0, 0, 1e-5, 1e4, hd, pos0), kc2, vc2, 1, pos0, nh, nkv,
+                            hd, scale)[0]
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4)
+    # the prefill op over the same cache (up to 8 queries ending at pos0)
+    T = min(8, pos0 + 1)
+    qp = (rng.standard_normal((T, nh * hd)) * 1e4).astype(np.float32)
+    op = dev.zeros(T * nh * hd * 4)
+    quipu.dispatch("atencion", [("u", hd), ("u", nh), ("u", nkv), ("u", 0), ("f", scale), ("u", 0), ("u", 0), ("u", 0),
+                                ("u", 1), ("u", rows)],
+                   [dev.paso(T, pos0 - T + 1), dev.buf(qp), kcb, vcb, op], (nh, T))  # the cache after the append
+    gotp = dev.get(op, (T, nh * hd))
+    assert np.isfinite(gotp).all()
+    np.testing.assert_allclose(gotp, oracle.attention(qp, kc2, vc2, T, pos0 - T + 1, nh, nkv, hd, scale), rtol=1e-4,
+                               atol=1e-4)
 
 
 def test_dec_attn_past_the_cache_reads_and_writes_nothing(quipu, dev):
