@@ -676,16 +676,19 @@ struct KDense {
 struct KNoPro {
     QP_DEV void operator()() const {}
 };
-template <int FMT, int R, int XS, class SegAt, class Lay = KDense, class Pro = KNoPro>
+// NT: threads per workgroup (256, or 512 for the no-norm variant of long rows: one input staging shared by eight
+// wavefronts).  NORM: the fused RMSNorm prologue is compiled in.
+template <int FMT, int R, int XS, class SegAt, class Lay = KDense, class Pro = KNoPro, int NT = 256, bool NORM = true>
 QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t x, uint64_t norm_w, float eps,
                     uint32_t K, uint64_t amax, Lay lay = Lay(), Pro pro = Pro()) {
     extern __shared__ float4 xs[];
     float* xsum = reinterpret_cast<float*>(xs + (K >> 8) * 65);
-    __shared__ float red[4];
-    __shared__ uint64_t wbest[4];
+    constexpr uint32_t nwv = NT / 64;
+    __shared__ float red[nwv];
+    __shared__ uint64_t wbest[nwv];
+    if constexpr (!NORM) norm_w = 0;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    constexpr uint32_t nwv = 4;  // launched with 256 threads
     const uint32_t nb = K >> 8;
     uint32_t nbp = 1;
     while (nbp < nb) nbp <<= 1;
@@ -695,11 +698,11 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     const uint32_t nmine = w < total_units ? (total_units - 1 - w) / W + 1 : 0;
     const uint32_t ngrp = K / KQ<FMT>::GROUP;
 
-    // 1. this thread's share of x (and of the norm weight): sub-blocks q = tid + 256 i
+    // 1. this thread's share of x (and of the norm weight): sub-blocks q = tid + NT i
     float4 xr[XS][8], nr[XS][8];
 #pragma unroll
     for (int i = 0; i < XS; i++) {
-        uint32_t q = tid + 256 * i;
+        uint32_t q = tid + NT * i;
         q = q < (K >> 5) ? q : 0;
 #pragma unroll
         for (int j = 0; j < 8; j++) xr[i][j] = gload<float4>(x + 128ull * q + 16ull * j);
@@ -711,7 +714,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     float xsc[XS];
 #pragma unroll
     for (int i = 0; i < XS; i++) {
-        const uint32_t q = tid + 256 * i;
+        const uint32_t q = tid + NT * i;
         xsc[i] = lay.xscale(q < (K >> 5) ? q : 0);  // every lane (a gathered layout shuffles across the wave)
     }
     pro();
@@ -765,7 +768,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < XS; i++) {
-        const uint32_t q = tid + 256 * i;
+        const uint32_t q = tid + NT * i;
         if (q < (K >> 5)) {
             const uint32_t bb = q >> 3, j = q & 7;
             float s0 = 0.0f, s1 = 0.0f;
@@ -914,14 +917,16 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     }
 }
 
-template <int FMT, int R, int XS>
+template <int FMT, int R, int XS, int NT = 256, bool NORM = true>
 QP_DEV void kq_gemv_seg(const QpGemvArgs& a) {
     auto seg_at = [&](uint32_t i) __attribute__((always_inline)) {
         const QpGemvSeg& q = a.seg[i];
         return KSeg{q.w, q.w2, q.y, q.n, q.row_base, q.rows_total, q.mode, q.wg0, q.fmt};
     };
     const uint32_t xrow = a.last_row ? paso_T(a.paso) - 1 : 0;
-    kq_gemv<FMT, R, XS>(seg_at, a.nseg, a.total_wg, a.x + 4ull * xrow * a.k, a.norm_w, a.eps, a.k, a.amax);
+    kq_gemv<FMT, R, XS, decltype(seg_at), KDense, KNoPro, NT, NORM>(seg_at, a.nseg, a.total_wg,
+                                                                  a.x + 4ull * xrow * a.k, a.norm_w, a.eps, a.k,
+                                                                  a.amax);
 }
 
 // Gathered expert GEMV: grid.y = job, job z uses expert sel[z] and input row z / tfijo.
@@ -1101,6 +1106,13 @@ MOE_KERNELS(q6k, QP_Q6_K)
         QpGemvExpArgs a) { kq_gemv_exp<FMT, 2, 2>(a); }
 KQ_KERNELS(q4k, QP_Q4_K)
 KQ_KERNELS(q6k, QP_Q6_K)
+// rows of more than 8192 inputs without the fused norm: 512 threads share one input staging, one sub-block each
+KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void qp_gemv_q4k_r1k2(QpGemvArgs a) {
+    kq_gemv_seg<QP_Q4_K, 1, 1, 512, false>(a);
+}
+KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void qp_gemv_q6k_r1k2(QpGemvArgs a) {
+    kq_gemv_seg<QP_Q6_K, 1, 1, 512, false>(a);
+}
 KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void qp_gemv_mix_r1(QpGemvArgs a) {
     kq_gemv_seg<QP_KQ_MIX, 1, 1>(a);
 }

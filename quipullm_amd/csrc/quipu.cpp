@@ -242,11 +242,16 @@ int run_gemv_kq(int fmt, QpGemvArgs& a, uint32_t max_wg, uint32_t* grid_out) {
     }
     a.total_wg = total;
     a.rows_per_wg = R * S;
-    uint32_t grid = cdiv(total, 4);
+    // rows of more than 8192 inputs without the fused norm: 512-thread workgroups sharing one input staging
+    const bool wide = a.k > 8192 && R == 1 && !mixed && !a.norm_w;
+    const uint32_t waves = wide ? 8 : 4;
+    uint32_t grid = cdiv(total, waves);
     if (grid > 2 * (uint32_t)g_cus) grid = 2 * (uint32_t)g_cus;
     if (max_wg && grid > max_wg) grid = max_wg;
     if (grid == 0) grid = 1;
     if (grid_out) *grid_out = grid;
+    if (wide)
+        return launch(fmt == QP_Q6_K ? K_gemv_q6k_r1k2 : K_gemv_q4k_r1k2, grid, 1, 1, 512, kq_lds(a.k), a);
     const Kid kid = mixed ? kq_mix_kid(R, a.k > 8192) : kq_kid((int)a.seg[0].fmt, R, a.k > 8192, false);
     return launch(kid, grid, 1, 1, 256, kq_lds(a.k), a);
 }

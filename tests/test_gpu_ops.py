@@ -104,7 +104,8 @@ def test_embed_rows_bit_exact(quipu, dev, oracle, fmt):
 
 # ------------------------------------------------------------------------------------------------ GEMV
 @pytest.mark.parametrize("fmt,N,K", [(capi.Q4_K, 1000, 4096), (capi.Q6_K, 513, 2048), (capi.Q8_0, 700, 1536),
-                                     (capi.F32, 130, 1024), (capi.Q4_K, 64, 14336), (capi.Q6_K, 40, 14336)])
+                                     (capi.F32, 130, 1024), (capi.Q4_K, 64, 14336), (capi.Q6_K, 40, 14336),
+                                     (capi.Q6_K, 700, 9216), (capi.Q4_K, 4100, 15360)])
 def test_matmul_1_reference_op(quipu, dev, oracle, fmt, N, K):
     raw = raw_matrix(fmt, N, K, 13)
     w = dev.matrix(fmt, raw, N, K)
