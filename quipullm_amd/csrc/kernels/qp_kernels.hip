@@ -1206,10 +1206,17 @@ namespace mm {
 constexpr int TM = 128, TN = 128, TK = 64, LDK = 72;  // LDS rows padded to 72 bf16 (144 B)
 }
 
-QP_DEV void split_store(float v, __bf16* hi, __bf16* lo) {
-    const __bf16 h = (__bf16)v;
-    *hi = h;
-    *lo = (__bf16)(v - (float)h);
+// Eight values -> their bf16 high parts and the bf16 of the remainders, each written to LDS as one 16-byte store.
+QP_DEV void split_store8(const float* v, __bf16* hi, __bf16* lo) {
+    bf16x8 h, l;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const __bf16 t = (__bf16)v[i];
+        h[i] = t;
+        l[i] = (__bf16)(v[i] - (float)t);
+    }
+    *reinterpret_cast<bf16x8*>(hi) = h;
+    *reinterpret_cast<bf16x8*>(lo) = l;
 }
 
 // Source registers of one thread's 32 weights for one K step (row `row`, k = k0 + koff .. ).
@@ -1355,28 +1362,33 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
         {
             __bf16* xh_r = xh + lr * LDK + 32 * part;
             __bf16* xl_r = xl + lr * LDK + 32 * part;
+            float xv[32];
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float4 v = xon ? xr[i] : float4{0.f, 0.f, 0.f, 0.f};
-                split_store(v.x, xh_r + 4 * i + 0, xl_r + 4 * i + 0);
-                split_store(v.y, xh_r + 4 * i + 1, xl_r + 4 * i + 1);
-                split_store(v.z, xh_r + 4 * i + 2, xl_r + 4 * i + 2);
-                split_store(v.w, xh_r + 4 * i + 3, xl_r + 4 * i + 3);
+                xv[4 * i] = v.x;
+                xv[4 * i + 1] = v.y;
+                xv[4 * i + 2] = v.z;
+                xv[4 * i + 3] = v.w;
             }
+#pragma unroll
+            for (int i = 0; i < 4; i++) split_store8(xv + 8 * i, xh_r + 8 * i, xl_r + 8 * i);
             float w[32];
             mm_wdeq<FMT>(wrg, g, wr, won, k0, part, w);
+#pragma unroll
+            for (int i = 0; i < 32; i++) w[i] = won ? w[i] : 0.f;
             __bf16* wh_r = wh + lr * LDK;
             __bf16* wl_r = wl + lr * LDK;
             if constexpr (FMT == QP_Q4_K) {
                 // w[0..15] -> k = 16*part + i (sub-block 2p), w[16..31] -> k = 32 + 16*part + i (sub-block 2p+1)
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    split_store(won ? w[i] : 0.f, wh_r + 16 * part + i, wl_r + 16 * part + i);
-                    split_store(won ? w[16 + i] : 0.f, wh_r + 32 + 16 * part + i, wl_r + 32 + 16 * part + i);
+                for (int i = 0; i < 2; i++) {
+                    split_store8(w + 8 * i, wh_r + 16 * part + 8 * i, wl_r + 16 * part + 8 * i);
+                    split_store8(w + 16 + 8 * i, wh_r + 32 + 16 * part + 8 * i, wl_r + 32 + 16 * part + 8 * i);
                 }
             } else {
 #pragma unroll
-                for (int i = 0; i < 32; i++) split_store(won ? w[i] : 0.f, wh_r + 32 * part + i, wl_r + 32 * part + i);
+                for (int i = 0; i < 4; i++) split_store8(w + 8 * i, wh_r + 32 * part + 8 * i, wl_r + 32 * part + 8 * i);
             }
         }
         __syncthreads();
