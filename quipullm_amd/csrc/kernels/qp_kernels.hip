@@ -1319,14 +1319,18 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
     const uint32_t T = g.tfix ? g.tfix : paso_T(g.paso);
     const uint32_t N = g.n, K = g.k;
     // XCD-aware tile order: workgroup i runs on XCD i % 8, as the j-th workgroup of that XCD; XCD x holds
-    // base + (x < rem) of the workgroups, so it takes the contiguous logical tiles starting at x*base + min(x, rem)
-    const uint32_t mt = (uint32_t)gridDim.y, ntl = (uint32_t)gridDim.x;
-    const uint32_t total = mt * ntl, id = blockIdx.y * ntl + blockIdx.x;
+    // base + (x < rem) of the workgroups, so it takes the contiguous logical tiles starting at x*base + min(x, rem).
+    // Logical order: weight tile, then K split, then token tile (the token tiles of one weight tile and split are
+    // neighbours: they share its dequantized rows through one L2).
+    const uint32_t mt = (uint32_t)gridDim.y, ntl = (uint32_t)gridDim.x, nz = (uint32_t)gridDim.z;
+    const uint32_t total = mt * ntl * nz, id = (blockIdx.z * mt + blockIdx.y) * ntl + blockIdx.x;
     const uint32_t base = total >> 3, rem = total & 7, xcd = id & 7, j = id >> 3;
     const uint32_t L = xcd * base + (xcd < rem ? xcd : rem) + j;
-    const uint32_t n_tile = L / mt, m_tile = L - n_tile * mt;
+    const uint32_t m_tile = L % mt, rest = L / mt, zs = rest % nz, n_tile = rest / nz;
     const uint32_t t0 = m_tile * TM, n0 = n_tile * TN;
     if (t0 >= T) return;
+    const uint32_t kbeg = g.kchunk ? zs * g.kchunk : 0;
+    const uint32_t kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t wm = wave >> 1, wn = wave & 1;
     // loader roles: token / row = tid >> 1, 32-element part = tid & 1
@@ -1343,36 +1347,57 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
 
+    // x as f32 (split here) or, with xs, as its bf16 high / low planes (copied to LDS as they are)
     float4 xr[8];
+    uint4 xp[8];
+    const bool pre = g.xs != 0;
+    const uint64_t xplane = 2ull * g.rows * K;
+    const uint64_t xsrow = g.xs + 2ull * (uint64_t)(xon ? xt : 0) * K;
     MmW wrg;
     auto load = [&](uint32_t k0) __attribute__((always_inline)) {
         const uint32_t kb = k0 + 32 * part;
+        if (pre) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t k = kb + 4 * i;
-            xr[i] = (k < K) ? gload<float4>(xrow + 4ull * k) : float4{0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < 4; i++) {
+                xp[i] = gload<uint4>(xsrow + 2ull * (kb + 8 * i));
+                xp[4 + i] = gload<uint4>(xsrow + xplane + 2ull * (kb + 8 * i));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t k = kb + 4 * i;
+                xr[i] = (k < K) ? gload<float4>(xrow + 4ull * k) : float4{0.f, 0.f, 0.f, 0.f};
+            }
         }
         mm_wload<FMT>(wrg, g, wr, won, k0, part);
     };
-    const uint32_t nsteps = (K + TK - 1) / TK;
-    load(0);
+    const uint32_t nsteps = (kend - kbeg + TK - 1) / TK;
+    load(kbeg);
     for (uint32_t s = 0; s < nsteps; s++) {
-        const uint32_t k0 = s * TK;
+        const uint32_t k0 = kbeg + s * TK;
         // registers -> LDS (bf16 hi / lo)
         {
             __bf16* xh_r = xh + lr * LDK + 32 * part;
             __bf16* xl_r = xl + lr * LDK + 32 * part;
-            float xv[32];
+            if (pre) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 v = xon ? xr[i] : float4{0.f, 0.f, 0.f, 0.f};
-                xv[4 * i] = v.x;
-                xv[4 * i + 1] = v.y;
-                xv[4 * i + 2] = v.z;
-                xv[4 * i + 3] = v.w;
+                for (int i = 0; i < 4; i++) {
+                    *reinterpret_cast<uint4*>(xh_r + 8 * i) = xon ? xp[i] : uint4{0, 0, 0, 0};
+                    *reinterpret_cast<uint4*>(xl_r + 8 * i) = xon ? xp[4 + i] : uint4{0, 0, 0, 0};
+                }
+            } else {
+                float xv[32];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float4 v = xon ? xr[i] : float4{0.f, 0.f, 0.f, 0.f};
+                    xv[4 * i] = v.x;
+                    xv[4 * i + 1] = v.y;
+                    xv[4 * i + 2] = v.z;
+                    xv[4 * i + 3] = v.w;
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) split_store8(xv + 8 * i, xh_r + 8 * i, xl_r + 8 * i);
             }
-#pragma unroll
-            for (int i = 0; i < 4; i++) split_store8(xv + 8 * i, xh_r + 8 * i, xl_r + 8 * i);
             float w[32];
             mm_wdeq<FMT>(wrg, g, wr, won, k0, part, w);
 #pragma unroll
@@ -1418,8 +1443,10 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
         }
         __syncthreads();
     }
-    // D layout (32 x 32 block): lane holds column lane & 31, rows 8*(v/4) + 4*(lane/32) + v%4
-    float* Y = mptr<float>(g.y);
+    // D layout (32 x 32 block): lane holds column lane & 31, rows 8*(v/4) + 4*(lane/32) + v%4.  With ws, the
+    // split's partial goes to its own plane.
+    float* Y = g.ws ? mptr<float>(g.ws) + (uint64_t)zs * g.rows * N : mptr<float>(g.y);
+    const bool add = g.acc && !g.ws;
 #pragma unroll
     for (int a = 0; a < 2; a++)
 #pragma unroll
@@ -1430,10 +1457,32 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
                 const uint32_t t = t0 + wm * 64 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                 if (t < T && n < N) {
                     float* o = Y + (uint64_t)t * N + n;
-                    *o = g.acc ? *o + acc[a][b][v] : acc[a][b][v];
+                    *o = add ? *o + acc[a][b][v] : acc[a][b][v];
                 }
             }
         }
+}
+
+// x [T][k] -> its bf16 high / low planes for the matrix-core matmul (8 values per thread and step).
+KERNEL __launch_bounds__(256) void qp_split_bf16(QpSplitArgs a) {
+    const uint64_t n8 = (uint64_t)paso_T(a.paso) * a.k / 8, plane = 2ull * a.rows * a.k;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n8; i += (uint64_t)gridDim.x * 256ull) {
+        const float4 v0 = gload<float4>(a.x + 32 * i), v1 = gload<float4>(a.x + 32 * i + 16);
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        split_store8(v, reinterpret_cast<__bf16*>(a.xs + 16 * i), reinterpret_cast<__bf16*>(a.xs + plane + 16 * i));
+    }
+}
+
+// y[t][n] = (acc ? y : 0) + (ws[0] + ws[1] + ...)[t][n], the splits summed in order.
+KERNEL __launch_bounds__(256) void qp_gemm_reduce(QpReduceArgs a) {
+    const uint64_t tn = (uint64_t)paso_T(a.paso) * a.n, plane = (uint64_t)a.rows * a.n;
+    const float* ws = cptr<float>(a.ws);
+    float* y = mptr<float>(a.y);
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < tn; i += (uint64_t)gridDim.x * 256ull) {
+        float s = ws[i];
+        for (uint32_t z = 1; z < a.splits; z++) s += ws[z * plane + i];
+        y[i] = a.acc ? y[i] + s : s;
+    }
 }
 
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q4k(QpGemmArgs a) { gemm_mfma_body<QP_Q4_K>(a); }

@@ -87,10 +87,18 @@ typedef struct {
 // Multi-token GEMV for prefill (reference matmul_*_4 / matmul_*_t semantics): y[t][r] (+)= W[r].x[t].
 typedef struct {
     uint64_t w, x, y, paso;
+    uint64_t xs;      // matrix-core path: 0, or x split into bf16 high and low planes ([rows][k] each, lo at xs + 2*rows*k)
+    uint64_t ws;      // matrix-core path: 0, or the split-K partials [splits][rows][n] (summed by qp_gemm_reduce)
     uint32_t fmt, n, k, acc;
-    uint32_t tfix;   // 0: T from paso
-    uint32_t pad[3];
+    uint32_t tfix;    // 0: T from paso
+    uint32_t kchunk;  // matrix-core path: inputs per K split (grid z = splits; a multiple of 64), or 0: all of k
+    uint32_t rows;    // matrix-core path: token rows the xs planes and the ws partials are sized for (>= T)
+    uint32_t pad;
 } QpGemmArgs;
+// x [T][k] -> bf16 high / low planes (hi = bf16(v), lo = bf16(v - hi)) at xs and xs + 2*rows*k.
+typedef struct { uint64_t x, xs, paso; uint32_t k, rows; } QpSplitArgs;
+// y[t][n] = (acc ? y : 0) + sum over s (in order) of ws[s][t][n].
+typedef struct { uint64_t ws, y, paso; uint32_t n, rows, splits, acc; } QpReduceArgs;
 
 // ---------------------------------------------------------------- elementwise / small ops
 typedef struct { uint64_t w, ids, y, paso; uint32_t fmt, d, rows, pad; } QpEmbedArgs;  // rows: tensor rows

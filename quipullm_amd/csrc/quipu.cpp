@@ -306,6 +306,27 @@ int op_matmul_1(const Ctx& c, int fmt, const char* name) {
 }
 
 // matmul_<fmt>_4 / matmul_<fmt>_t (prefill, kquants.js:188-251 nt=4 and 309-386): T tokens from paso.
+// The library's scratch buffer for the prefill matmul (split input planes, split-K partials): grown on demand
+// (the stream is drained before the old one is freed) and kept until the process ends.  Not while capturing.
+uint64_t g_ws = 0, g_ws_bytes = 0;
+int workspace(uint64_t bytes, uint64_t* out) {
+    if (bytes > g_ws_bytes) {
+        if (g_capturing) return fail(QP_E_CAPTURE, "prefill workspace growth during graph capture");
+        if (g_ws) {
+            HIPCHK(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+            HIPCHK(hipFree((void*)g_ws), "hipFree");
+            g_ws = 0;
+            g_ws_bytes = 0;
+        }
+        void* p = nullptr;
+        HIPCHK(hipMalloc(&p, bytes), "hipMalloc (prefill workspace)");
+        g_ws = (uint64_t)p;
+        g_ws_bytes = bytes;
+    }
+    *out = g_ws;
+    return 0;
+}
+
 int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z) {
     const bool q8 = fmt == QP_Q8_0;
     if (int e = need_bufs(c, q8 ? 5 : 4, name)) return e;
@@ -327,7 +348,29 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
         // matrix cores: 128 x 128 tiles (the kernel reads T from paso; tiles past it exit)
         const Kid k = fmt == QP_Q4_K ? K_gemm_mfma_q4k : fmt == QP_Q6_K ? K_gemm_mfma_q6k
                     : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
-        return launch(k, cdiv(N, 128), cdiv(tmax, 128), 1, 256, 0, a);
+        const uint32_t mt = cdiv(tmax, 128), nt = cdiv(N, 128);
+        if ((fmt == QP_Q4_K || fmt == QP_Q6_K) && !g_capturing) {
+            // K-quants: x split into bf16 planes once (not in every weight tile's workgroup), and the K range split
+            // when the tiles alone cannot occupy the CUs (two workgroups each); partials summed in order
+            const uint32_t steps = K / 64, slots = 2 * (uint32_t)g_cus;
+            uint32_t ns = 1;
+            while (mt * nt * ns * 2 <= slots && steps / (ns * 2) >= 4) ns *= 2;
+            a.kchunk = ns > 1 ? cdiv(steps, ns) * 64 : 0;
+            if (ns > 1) ns = cdiv(K, a.kchunk);
+            a.rows = mt * 128;
+            const uint64_t xs_bytes = 4ull * a.rows * K, ws_bytes = ns > 1 ? 4ull * ns * a.rows * N : 0;
+            uint64_t ws = 0;
+            if (int e = workspace(xs_bytes + ws_bytes, &ws)) return e;
+            a.xs = ws;
+            a.ws = ns > 1 ? ws + xs_bytes : 0;
+            QpSplitArgs sa = {a.x, a.xs, a.paso, K, a.rows};
+            if (int e = launch(K_split_bf16, grid_cap((uint64_t)tmax * K / 8), 1, 1, 256, 0, sa)) return e;
+            if (int e = launch(k, nt, mt, ns, 256, 0, a)) return e;
+            if (ns == 1) return 0;
+            QpReduceArgs ra = {a.ws, a.y, a.paso, N, a.rows, ns, acc};
+            return launch(K_gemm_reduce, grid_cap((uint64_t)tmax * N), 1, 1, 256, 0, ra);
+        }
+        return launch(k, nt, mt, 1, 256, 0, a);
     }
     return launch(K_gemm_mt, cdiv(N, 64), cdiv(tmax ? tmax : 1, 64), 1, 256, 0, a);
 }
