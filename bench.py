@@ -121,7 +121,7 @@ def run_decode(model, path, steps, warmup, prefills, check_n=0, eager=False, see
     with open(pf, "w") as f:
         json.dump(ids, f)
     cmd = ["node", os.path.join(ROOT, "quipullm_amd", "js", "cli.js"), "bench", "--model", path, "--prompt-file", pf,
-           "--n", str(steps), "--warmup", str(warmup), "--kv", "f16", "--ctx", str(ctx), "--batch", "512",
+           "--n", str(steps), "--warmup", str(warmup), "--kv", "f16", "--ctx", str(ctx), "--batch", "2048",
            "--max-gen", str(max(steps, warmup, check_n) + 8), "--prefill", ",".join(str(p) for p in prefills)]
     if check_n:
         cf = os.path.join(model_dir(), f"{model}.check_prompt.json")

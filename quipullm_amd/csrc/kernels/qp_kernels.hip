@@ -1485,6 +1485,240 @@ KERNEL __launch_bounds__(256) void qp_gemm_reduce(QpReduceArgs a) {
     }
 }
 
+// ---- 256-token tiles (T >= 256, K-quant weights, the input split beforehand): 8 wavefronts in 4 x 2, each 64 x 64,
+// so each dequantized weight tile feeds 256 tokens.  K steps of 32 with two LDS buffers and three register
+// buffers: while the matrix instructions of step s read one LDS buffer, the waves dequantize step s + 1 into the
+// other (the arithmetic overlaps the matrix cores) and the global loads of step s + 2 are in flight; one barrier
+// per step.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// bf16 high/low parts of 8 floats, both rounded to nearest: 3 vector operations per value (the packed conversion
+// of a pair, unpacking the high parts, the exact difference).
+QP_DEV void split_store8_pk(const float (&v)[8], __bf16* hi, __bf16* lo) {
+    u32x4 h, l;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){v[2 * p], v[2 * p + 1]}, bf16x2));
+        const float l0 = v[2 * p] - __uint_as_float(hb << 16), l1 = v[2 * p + 1] - __uint_as_float(hb & 0xffff0000u);
+        h[p] = hb;
+        l[p] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){l0, l1}, bf16x2));
+    }
+    *reinterpret_cast<u32x4*>(hi) = h;
+    *reinterpret_cast<u32x4*>(lo) = l;
+}
+
+// One thread's share of one 32-input K step: 16 inputs of one token row (both bf16 planes) and 8 weights of one
+// output row.
+struct MmW8 {
+    u32x4 x[4];   // bf16 high (x[0..1]) and low (x[2..3]) of the 16 inputs
+    u32x2 q;      // Q4_K: the 8 nibble bytes; Q6_K: the 8 low-bit bytes
+    u32x4 h;      // Q4_K: the super-block header (d, dmin, 12 scale bytes)
+    u32x2 qh;     // Q6_K: the 8 high-bit bytes
+    uint32_t sc;  // Q6_K: the dword holding this sub-block's scale byte
+    uint32_t d;   // Q6_K: the f16 super-block scale
+};
+
+// Per-thread byte offsets, fixed over the K loop; the step's own offsets are uniform (scalar soffset).  Weights of
+// row r, inputs 8*sub .. 8*sub + 7 of the step at k0.  Q4_K: sub-block j = (k0 % 256) / 32 is the low (j even) or
+// high (j odd) nibble of bytes l = 8*sub .. of the 32 qs bytes 32*(j/2) .., chunk 1 + 2*(j/2) + l/16.  Q6_K:
+// block half h, quarter qd: ql chunk h*4 + (qd%2)*2 + l/16, qh chunk 8 + h*2 + l/16, scale byte h*8 + qd*2 + l/16.
+struct MmOff {
+    uint32_t x, q, h, d;
+};
+
+template <int FMT>
+QP_DEV void mm8_load(MmW8& r, const MmOff& o, __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, uint32_t xplane,
+                     uint32_t nb, uint32_t k0) {
+    r.x[0] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x, 2 * k0, 0);
+    r.x[1] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x + 16, 2 * k0, 0);
+    r.x[2] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x, xplane + 2 * k0, 0);
+    r.x[3] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x + 16, xplane + 2 * k0, 0);
+    const uint32_t b = k0 >> 8, e0 = k0 & 255;
+    if constexpr (FMT == QP_Q4_K) {
+        const uint32_t j = e0 >> 5;
+        r.q = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16 + (1 + 2 * (j >> 1)) * nb * 16, 0);
+        r.h = __builtin_amdgcn_raw_buffer_load_b128(rw, o.h, b * 16, 0);
+    } else {
+        const uint32_t h = e0 >> 7, qd = (e0 & 127) >> 5;
+        r.q = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16 + (h * 4 + (qd & 1) * 2) * nb * 16, 0);
+        r.qh = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16 + (8 + h * 2) * nb * 16, 0);
+        r.sc = __builtin_amdgcn_raw_buffer_load_b32(rw, o.h, b * 16 + 12 * nb * 16 + 4 * (h * 2 + (qd >> 1)), 0);
+        r.d = __builtin_amdgcn_raw_buffer_load_b16(rw, o.d, b * 2, 0);
+    }
+}
+
+template <int FMT>
+QP_DEV void mm8_deq(const MmW8& r, uint32_t k0, uint32_t sub, float (&w)[8]) {
+    const uint32_t e0 = k0 & 255;
+    uint32_t v[2];
+    float f, c;
+    if constexpr (FMT == QP_Q4_K) {
+        // fd*q - fm; a high nibble is masked in place (16*q) with the scale divided by 16 (exact)
+        const uint32_t j = e0 >> 5, jj = (j & 3) * 8;  // the scale/min unpack of q4k_sm, without a branch
+        const uint32_t sa = (r.h.y >> jj) & 0xffu, sb = (r.h.z >> jj) & 0xffu, s8 = (r.h.w >> jj) & 0xffu;
+        const uint32_t lo4 = 0u - (uint32_t)(j < 4);  // all ones for j < 4: a blend, not a branch
+        const uint32_t sc = ((sa & 63u) & lo4) | (((s8 & 15u) | ((sa >> 6) << 4)) & ~lo4);
+        const uint32_t mn = ((sb & 63u) & lo4) | (((s8 >> 4) | ((sb >> 6) << 4)) & ~lo4);
+        const uint32_t mask = (j & 1) ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+        f = h2f(r.h.x & 0xffffu) * (float)sc * ((j & 1) ? 0.0625f : 1.0f);
+        c = -(h2f(r.h.x >> 16) * (float)mn);
+        v[0] = r.q.x & mask;
+        v[1] = r.q.y & mask;
+    } else {
+        // fd*(q - 32) = fma(fd, q, -32*fd) exactly (both are one rounding of the same product)
+        const uint32_t qd = (e0 & 127) >> 5, sb = ((qd & 1) * 2 + (sub >> 1)) * 8;
+        f = h2f(r.d & 0xffffu) * (float)(int8_t)((r.sc >> sb) & 0xffu);
+        c = -32.0f * f;
+        const uint32_t ls = (qd >> 1) * 4, hs = qd * 2;
+        v[0] = ((r.q.x >> ls) & 0x0f0f0f0fu) | (((r.qh.x >> hs) & 0x03030303u) << 4);
+        v[1] = ((r.q.y >> ls) & 0x0f0f0f0fu) | (((r.qh.y >> hs) & 0x03030303u) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i] = __builtin_fmaf(f, (float)((v[i >> 2] >> (8 * (i & 3))) & 0xffu), c);
+}
+
+template <int FMT>
+QP_DEV void gemm_mfma256_body(const QpGemmArgs& g) {
+    constexpr int TM = 256, TN = 128, TK = 32, LDK = 40, BUF = (TM + TM + TN + TN) * LDK;  // bf16 per buffer
+    extern __shared__ float4 smem4[];
+    __bf16* lds = reinterpret_cast<__bf16*>(smem4);
+    const uint32_t T = g.tfix ? g.tfix : paso_T(g.paso);
+    const uint32_t N = g.n, K = g.k;
+    const uint32_t mt = (uint32_t)gridDim.y, ntl = (uint32_t)gridDim.x, nz = (uint32_t)gridDim.z;
+    const uint32_t total = mt * ntl * nz, id = (blockIdx.z * mt + blockIdx.y) * ntl + blockIdx.x;
+    const uint32_t base = total >> 3, rem = total & 7, xcd = id & 7, j = id >> 3;
+    const uint32_t L = xcd * base + (xcd < rem ? xcd : rem) + j;
+    const uint32_t m_tile = L % mt, rest = L / mt, zs = rest % nz, n_tile = rest / nz;
+    const uint32_t t0 = m_tile * TM, n0 = n_tile * TN;
+    if (t0 >= T) return;
+    const uint32_t kbeg = g.kchunk ? zs * g.kchunk : 0;
+    const uint32_t kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    // loaders, so that each 16-lane phase of an LDS store covers 16 rows: input row lr (16 inputs at 16*part),
+    // weight row wq (8 inputs at 8*sub).  Rows past T or N load row 0 (finite values whose outputs are not stored).
+    const uint32_t lr = wave * 32 + (lane & 31), part = lane >> 5, wq = wave * 16 + (lane & 15), sub = lane >> 4;
+    const uint32_t xt = t0 + lr < T ? t0 + lr : 0, wr = n0 + wq < N ? n0 + wq : 0;
+    const uint32_t nb = K >> 8, xplane = 2 * g.rows * K;
+    const __amdgpu_buffer_rsrc_t rx = kq_rsrc(g.xs, 2ull * xplane);
+    const __amdgpu_buffer_rsrc_t rw = kq_rsrc(g.w, (uint64_t)N * nb * (FMT == QP_Q4_K ? 144 : 210));
+    MmOff off;
+    off.x = 2 * (xt * K + 16 * part);
+    off.q = wr * nb * (FMT == QP_Q4_K ? 144 : 208) + (sub >> 1) * nb * 16 + (sub & 1) * 8;
+    off.h = wr * nb * (FMT == QP_Q4_K ? 144 : 208);
+    off.d = N * nb * 208 + wr * nb * 2;
+    const uint32_t nsteps = (kend - kbeg + TK - 1) / TK;
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
+    MmW8 r0, r1;
+    auto load = [&](MmW8& r, uint32_t st) __attribute__((always_inline)) {
+        // past the last step: reload it (unused)
+        mm8_load<FMT>(r, off, rx, rw, xplane, nb, kbeg + min(st, nsteps - 1) * TK);
+    };
+    auto stage = [&](const MmW8& r, uint32_t st, __bf16* buf) __attribute__((always_inline)) {
+        __bf16* xh = buf;
+        __bf16* xl = xh + TM * LDK;
+        __bf16* wh = xl + TM * LDK;
+        __bf16* wl = wh + TN * LDK;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            *reinterpret_cast<u32x4*>(xh + lr * LDK + 16 * part + 8 * i) = r.x[i];
+            *reinterpret_cast<u32x4*>(xl + lr * LDK + 16 * part + 8 * i) = r.x[2 + i];
+        }
+        float w[8];
+        mm8_deq<FMT>(r, kbeg + min(st, nsteps - 1) * TK, sub, w);
+        split_store8_pk(w, wh + wq * LDK + 8 * sub, wl + wq * LDK + 8 * sub);
+    };
+    // step s: the loads of step s + 2 go into the registers step s came in (staged during step s - 1), the
+    // matrix instructions read LDS buffer s % 2, and step s + 1 is dequantized into the other buffer
+    auto step = [&](uint32_t s, MmW8& mine, MmW8& next) __attribute__((always_inline)) {
+        load(mine, s + 2);
+        const __bf16* xh = lds + (s & 1) * BUF;
+        const __bf16* xl = xh + TM * LDK;
+        const __bf16* wh = xl + TM * LDK;
+        const __bf16* wl = wh + TN * LDK;
+#pragma unroll
+        for (int ks = 0; ks < TK / 16; ks++) {
+            const uint32_t kk = ks * 16 + 8 * (lane >> 5);
+            bf16x8 ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+            for (int a = 0; a < 2; a++) {
+                const uint32_t tr = wm * 64 + a * 32 + (lane & 31);
+                ah[a] = *reinterpret_cast<const bf16x8*>(xh + tr * LDK + kk);
+                al[a] = *reinterpret_cast<const bf16x8*>(xl + tr * LDK + kk);
+                const uint32_t nr = wn * 64 + a * 32 + (lane & 31);
+                bh[a] = *reinterpret_cast<const bf16x8*>(wh + nr * LDK + kk);
+                bl[a] = *reinterpret_cast<const bf16x8*>(wl + nr * LDK + kk);
+            }
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[a], bh[b], acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[a], bl[b], acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[a], bh[b], acc[a][b], 0, 0, 0);
+                }
+        }
+        stage(next, s + 1, lds + ((s + 1) & 1) * BUF);  // after the last step: a copy of it, never read
+        // issue order: the step's global loads, the first operand reads, then each matrix instruction followed by
+        // two vector operations of the next step's dequantization (so both pipes stay busy), the remaining operand
+        // reads spread between them, the LDS stores last
+        __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);  // VMEM reads
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);   // DS reads (ks 0)
+#pragma unroll
+        for (int i = 0; i < 12; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (ks 1)
+            __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+        }
+#pragma unroll
+        for (int i = 0; i < 12; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        }
+        __builtin_amdgcn_sched_group_barrier(0x200, 16, 0);  // DS writes
+        __syncthreads();
+    };
+    load(r0, 0);
+    load(r1, 1);
+    stage(r0, 0, lds);
+    __syncthreads();
+    for (uint32_t s = 0; s < nsteps; s += 2) {  // nsteps is even: every K range is whole 64-input steps
+        step(s, r0, r1);
+        step(s + 1, r1, r0);
+    }
+    float* Y = g.ws ? mptr<float>(g.ws) + (uint64_t)zs * g.rows * N : mptr<float>(g.y);
+    const bool add = g.acc && !g.ws;
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const uint32_t n = n0 + wn * 64 + b * 32 + (lane & 31);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const uint32_t t = t0 + wm * 64 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (t < T && n < N) {
+                    float* o = Y + (uint64_t)t * N + n;
+                    *o = add ? *o + acc[a][b][v] : acc[a][b][v];
+                }
+            }
+        }
+}
+
+KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q4k(QpGemmArgs a) { gemm_mfma256_body<QP_Q4_K>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q6k(QpGemmArgs a) { gemm_mfma256_body<QP_Q6_K>(a); }
+
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q4k(QpGemmArgs a) { gemm_mfma_body<QP_Q4_K>(a); }
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q6k(QpGemmArgs a) { gemm_mfma_body<QP_Q6_K>(a); }
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q8(QpGemmArgs a) { gemm_mfma_body<QP_Q8_0>(a); }

@@ -348,16 +348,21 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
         // matrix cores: 128 x 128 tiles (the kernel reads T from paso; tiles past it exit)
         const Kid k = fmt == QP_Q4_K ? K_gemm_mfma_q4k : fmt == QP_Q6_K ? K_gemm_mfma_q6k
                     : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
-        const uint32_t mt = cdiv(tmax, 128), nt = cdiv(N, 128);
+        uint32_t mt = cdiv(tmax, 128);
+        const uint32_t nt = cdiv(N, 128);
         if ((fmt == QP_Q4_K || fmt == QP_Q6_K) && !g_capturing) {
             // K-quants: x split into bf16 planes once (not in every weight tile's workgroup), and the K range split
-            // when the tiles alone cannot occupy the CUs (two workgroups each); partials summed in order
-            const uint32_t steps = K / 64, slots = 2 * (uint32_t)g_cus;
+            // when the tiles alone cannot occupy the CUs; partials summed in order.  From 256 tokens on, 256-token
+            // tiles (one 512-thread workgroup per CU, K steps of 32 double-buffered in LDS) dequantize each weight
+            // tile half as often.
+            const bool big = tmax >= 256;
+            if (big) mt = cdiv(tmax, 256);
+            const uint32_t steps = K / 64, slots = (big ? 1 : 2) * (uint32_t)g_cus;
             uint32_t ns = 1;
             while (mt * nt * ns * 2 <= slots && steps / (ns * 2) >= 4) ns *= 2;
-            a.kchunk = ns > 1 ? cdiv(steps, ns) * 64 : 0;
+            a.kchunk = ns > 1 ? cdiv(steps, ns) * 64 : 0;  // whole 64-input steps (the 256-token tiles take 32)
             if (ns > 1) ns = cdiv(K, a.kchunk);
-            a.rows = mt * 128;
+            a.rows = mt * (big ? 256 : 128);
             const uint64_t xs_bytes = 4ull * a.rows * K, ws_bytes = ns > 1 ? 4ull * ns * a.rows * N : 0;
             uint64_t ws = 0;
             if (int e = workspace(xs_bytes + ws_bytes, &ws)) return e;
@@ -365,7 +370,12 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
             a.ws = ns > 1 ? ws + xs_bytes : 0;
             QpSplitArgs sa = {a.x, a.xs, a.paso, K, a.rows};
             if (int e = launch(K_split_bf16, grid_cap((uint64_t)tmax * K / 8), 1, 1, 256, 0, sa)) return e;
-            if (int e = launch(k, nt, mt, ns, 256, 0, a)) return e;
+            if (big) {
+                const Kid kb = fmt == QP_Q4_K ? K_gemm_mfma256_q4k : K_gemm_mfma256_q6k;
+                if (int e = launch(kb, nt, mt, ns, 512, 2 * (256 + 256 + 128 + 128) * 40 * 2, a)) return e;
+            } else if (int e = launch(k, nt, mt, ns, 256, 0, a)) {
+                return e;
+            }
             if (ns == 1) return 0;
             QpReduceArgs ra = {a.ws, a.y, a.paso, N, a.rows, ns, acc};
             return launch(K_gemm_reduce, grid_cap((uint64_t)tmax * N), 1, 1, 256, 0, ra);

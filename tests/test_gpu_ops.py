@@ -267,12 +267,13 @@ def test_matmul_multi_token(quipu, dev, oracle, fmt, T, op):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,N,K,acc", [(200, 300, 2048, 1), (128, 256, 1024, 0), (64, 77, 512, 0),
-                                        (300, 500, 256, 1), (128, 1024, 5632, 1), (512, 4096, 1024, 0)])
+                                        (300, 500, 256, 1), (128, 1024, 5632, 1), (512, 4096, 1024, 0),
+                                        (1000, 700, 4864, 1), (256, 130, 2048, 0)])
 def test_matmul_prefill_mfma(quipu, dev, oracle, fmt, T, N, K, acc):
     """The matrix-core prefill path (T >= 64): bf16 hi/lo products stay within the float32 dot bound, with
     partial token and row tiles, and tile counts that are not a multiple of the 8 XCDs (3 x 4 = 12 tiles).  For
     K-quants the input is split into bf16 planes once and small tile grids split K (K = 5632: 15 splits, the last
-    one partial), partials summed in order."""
+    one partial), partials summed in order; from T = 256 on they take the 256-token tiles."""
     if fmt == capi.Q8_0 and K % 64:
         K += 32
     raw = raw_matrix(fmt, N, K, 61)
