@@ -110,10 +110,11 @@ def cpu_baseline(path, seconds=20.0):
                       f"OpenMP threads; C restatement of the reference WGSL semantics"}, ids, lgs
 
 
-def run_decode(model, path, steps, warmup, prefills, check_n=0, eager=False, seed=7):
+def run_decode(model, path, steps, warmup, prefills, check_n=0, eager=False, seed=7, sample=False):
     """The product host (Node.js CLI) on `model`: for each P in prefills, prefill P uniform-random ids, then time
-    `steps` greedy decode tokens.  With check_n, first generates check_n greedy tokens from CHECK_PROMPT and
-    returns their logits (the parity check)."""
+    `steps` greedy decode tokens (with `sample`, also `steps` tokens with the reference's default sampler from the
+    same position).  With check_n, first generates check_n greedy tokens from CHECK_PROMPT and returns their
+    logits (the parity check)."""
     c = synth.CONFIGS[model]
     ctx = max(prefills) + steps + warmup + 8
     ids = synth.random_prompt(c.vocab, max(prefills), seed)
@@ -131,6 +132,8 @@ def run_decode(model, path, steps, warmup, prefills, check_n=0, eager=False, see
         cmd += ["--check-prompt-file", cf, "--check-n", str(check_n), "--check-logits", lf]
     if eager:
         cmd.append("--eager")
+    if sample:
+        cmd.append("--sample")
     log("bench: " + " ".join(cmd))
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
@@ -208,7 +211,7 @@ def main():
     cpu, cpu_ids, cpu_lg = cpu_baseline(path, a.cpu_seconds)
     log(f"bench: cpu baseline {cpu['value']:.3f} tok/s")
     prefills = [4096, 2048, 512]
-    dec = run_decode(MODEL, path, a.steps, a.warmup, prefills, len(cpu_ids), a.decode_launch == "eager")
+    dec = run_decode(MODEL, path, a.steps, a.warmup, prefills, len(cpu_ids), a.decode_launch == "eager", sample=True)
     check = parity(dec["check_ids"], dec.pop("check_logits"), cpu_ids, cpu_lg)
     runs = {r["prompt_tokens"]: r for r in dec["runs"]}
     log("bench: decode " + json.dumps(dec))
@@ -238,6 +241,7 @@ def main():
                    "prefill_tok_s_4096": round(main_run["prefill_tok_s"], 1),
                    "prefill_tok_s_2048": round(runs[2048]["prefill_tok_s"], 1),
                    "decode_tok_s_ctx2048": round(runs[2048]["decode_tok_s"], 3),
+                   "decode_sampled_tok_s_ctx4096": round(main_run["sampled_tok_s"], 3),
                    "prefill_2048_TFLOPs": round(PREFILL_2048_FLOP / (runs[2048]["prefill_ms"] * 1e-3) / 1e12, 2),
                    "side_configs": side,
                    "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()} for g in gem],

@@ -2761,6 +2761,105 @@ KERNEL __launch_bounds__(256) void qp_argmax_fin(QpArgmaxFinArgs a) {
     }
 }
 
+// ====================================================================================== sampling
+// The reference samples on the host (web/js/sampling.js:25-82) from the whole logits array.  These kernels apply
+// the penalties and select the top-k candidates on the device, so the host reads back k (value, id) pairs and
+// draws from them with the reference's float64 steps.
+
+// sampling.js:30-36 for the window's (token, count) pairs: in double like the JavaScript (no contraction), stored
+// rounded to float as a Float32Array store rounds.
+KERNEL __launch_bounds__(64) void qp_penalizar(QpPenaltyArgs a) {
+#pragma clang fp contract(off)
+    const uint32_t i = threadIdx.x;
+    if (i >= a.count) return;
+    const uint32_t t = cptr<uint32_t>(a.hist)[2 * i], n = cptr<uint32_t>(a.hist)[2 * i + 1];
+    if (t >= a.n) return;
+    float* lg = mptr<float>(a.logits);
+    double l = (double)lg[t];
+    if (a.rep != 1.0) l = l > 0 ? l / a.rep : l * a.rep;
+    l -= (double)n * a.freq + a.pres;
+    lg[t] = (float)l;
+}
+
+// Order-preserving key of (logit, id): a larger key is a larger value, then a lower id.
+QP_DEV uint64_t topk_key(float v, uint32_t i) {
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)o << 32) | (0xffffffffu - i);
+}
+QP_DEV float topk_val(uint64_t k) {
+    const uint32_t o = (uint32_t)(k >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+QP_DEV uint32_t topk_id(uint64_t k) { return 0xffffffffu - (uint32_t)k; }
+
+// Descending bitonic sort of n (a power of two) keys in LDS by nt threads.
+QP_DEV void bitonic_desc(uint64_t* s, uint32_t n, uint32_t tid, uint32_t nt) {
+    for (uint32_t size = 2; size <= n; size <<= 1)
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t t = tid; t < n / 2; t += nt) {
+                const uint32_t i = 2 * t - (t & (stride - 1)), j = i + stride;
+                const uint64_t x = s[i], y = s[j];
+                if ((i & size) == 0 ? x < y : x > y) {
+                    s[i] = y;
+                    s[j] = x;
+                }
+            }
+            __syncthreads();
+        }
+}
+
+// Stage 1: workgroup g sorts logits [2048 g, 2048 g + 2048) and keeps its kp = k + 1 largest keys, plus a NaN
+// flag.  part: kp keys per workgroup, then one u32 flag per workgroup.
+KERNEL __launch_bounds__(256) void qp_topk_part(QpCandArgs a) {
+    __shared__ uint64_t s[2048];
+    const uint32_t tid = threadIdx.x, base = blockIdx.x * 2048;
+    const float* lg = cptr<float>(a.logits);
+    int nan = 0;
+    for (uint32_t i = tid; i < 2048; i += 256) {
+        const uint32_t g = base + i;
+        uint64_t key = 0;  // padding sorts below every non-NaN value
+        if (g < a.n) {
+            const float v = lg[g];
+            nan |= v != v;
+            key = topk_key(v, g);
+        }
+        s[i] = key;
+    }
+    nan = __syncthreads_or(nan);
+    bitonic_desc(s, 2048, tid, 256);
+    uint64_t* part = mptr<uint64_t>(a.part);
+    for (uint32_t i = tid; i < a.kp; i += 256) part[(uint64_t)blockIdx.x * a.kp + i] = s[i];
+    if (tid == 0) reinterpret_cast<uint32_t*>(part + (uint64_t)a.g * a.kp)[blockIdx.x] = nan ? 1u : 0u;
+}
+
+// Stage 2 (one workgroup): merges the g*kp partial keys (n2 = next power of two, in dynamic LDS) and writes
+// out = {flags, k, (value bits, id) x k} in descending order.  flags bit 0: a NaN logit; bit 1: two equal values
+// among the k + 1 largest (float equality, so -0 == +0), i.e. the candidate set or its order would depend on the
+// reference's heap; the host then takes the whole logits array.
+KERNEL __launch_bounds__(1024) void qp_topk_merge(QpCandArgs a) {
+    extern __shared__ float4 smk[];
+    uint64_t* s = reinterpret_cast<uint64_t*>(smk);
+    const uint32_t tid = threadIdx.x, tot = a.g * a.kp;
+    const uint64_t* part = cptr<uint64_t>(a.part);
+    const uint32_t* pf = reinterpret_cast<const uint32_t*>(part + tot);
+    for (uint32_t i = tid; i < a.n2; i += 1024) s[i] = i < tot ? part[i] : 0ull;
+    int nan = 0;
+    for (uint32_t i = tid; i < a.g; i += 1024) nan |= pf[i] != 0;
+    nan = __syncthreads_or(nan);
+    bitonic_desc(s, a.n2, tid, 1024);
+    const int tie = __syncthreads_or(tid < a.k && topk_val(s[tid]) == topk_val(s[tid + 1]));
+    uint32_t* out = mptr<uint32_t>(a.out);
+    if (tid == 0) {
+        out[0] = (nan ? 1u : 0u) | (tie ? 2u : 0u);
+        out[1] = a.k;
+    }
+    if (tid < a.k) {
+        out[2 + 2 * tid] = __float_as_uint(topk_val(s[tid]));
+        out[3 + 2 * tid] = topk_id(s[tid]);
+    }
+}
+
 // ====================================================================================== calibration
 // Plain streaming kernels of known traffic: copy n float4s (reads and writes 16n bytes each) and a read-only
 // sum of n float4s (one float written per thread).  Used to calibrate HBM traffic counters and bandwidth.

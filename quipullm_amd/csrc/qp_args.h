@@ -148,6 +148,12 @@ typedef struct { uint64_t amax, ids, tokens, step, paso; uint32_t count, advance
 // Plain argmax over n floats (lowest index wins ties; NaN never chosen) -> out[0].
 typedef struct { uint64_t v, out; uint32_t n, pad; } QpArgmaxArgs;
 
+// Sampling helpers (no counterpart in the reference, which samples on the host): penalties over (token, count)
+// pairs with double factors; top-k candidates in two stages (kp = k + 1 keys per 2048-logit chunk, g chunks,
+// n2 = the merge's power-of-two size).
+typedef struct { uint64_t logits, hist; double rep, freq, pres; uint32_t count, n; } QpPenaltyArgs;
+typedef struct { uint64_t logits, part, out; uint32_t n, k, kp, g, n2, pad; } QpCandArgs;
+
 // Load-time repacks from the GGUF block layout to the device layout (k: row length, for Q4_K / Q6_K).
 typedef struct { uint64_t src, dst; uint64_t nblocks; uint32_t k, pad; } QpRepackArgs;
 typedef struct { uint64_t dst; uint64_t count; uint32_t value, pad; } QpFillArgs;

@@ -762,6 +762,49 @@ int op_argmax_fin(const Ctx& c) {
     return launch(K_argmax_fin, 1, 1, 1, 256, 0, a);
 }
 
+// penalizar: P{count, V, rep lo, rep hi, freq lo, hi, pres lo, hi} (the factors as IEEE double bits); [logits,
+// pairs]: pairs = count (token, count) u32 pairs of the penalty window, count <= 64.  No reference counterpart (the
+// reference penalizes on the host, sampling.js:27-37).
+int op_penalizar(const Ctx& c) {
+    if (int e = need_bufs(c, 2, "penalizar")) return e;
+    QpPenaltyArgs a = {};
+    a.count = c.U(0);
+    a.n = c.U(1);
+    const uint64_t r = c.U64(2), f = c.U64(4), p = c.U64(6);
+    memcpy(&a.rep, &r, 8);
+    memcpy(&a.freq, &f, 8);
+    memcpy(&a.pres, &p, 8);
+    if (a.count > 64) return fail(QP_E_ARG, "penalizar: %u pairs (the window holds at most 64)", a.count);
+    a.logits = c.B(0);
+    a.hist = c.B(1);
+    return launch(K_penalizar, 1, 1, 1, 64, 0, a);
+}
+
+// topk_cand: P{V, k}; [logits, part, out].  part: ceil(V/2048)*(k+1) u64 keys + ceil(V/2048) u32 flags; out:
+// 2 + 2k u32 ({flags, k, (value bits, id) x k}, descending).  1 <= k <= 128, k < V, ceil(V/2048)*(k+1) <= 16384.
+// No reference counterpart (the reference's top-k heap runs on the host, sampling.js:44-57).
+int op_topk_cand(const Ctx& c) {
+    if (int e = need_bufs(c, 3, "topk_cand")) return e;
+    QpCandArgs a = {};
+    a.n = c.U(0);
+    a.k = c.U(1);
+    if (a.k < 1 || a.k > 128 || a.k >= a.n)
+        return fail(QP_E_ARG, "topk_cand: k=%u must be in 1..128 and below V=%u", a.k, a.n);
+    a.kp = a.k + 1;
+    a.g = cdiv(a.n, 2048);
+    const uint64_t tot = (uint64_t)a.g * a.kp;
+    if (tot > 16384) return fail(QP_E_ARG, "topk_cand: V=%u, k=%u: %llu partial candidates exceed 16384", a.n, a.k,
+                                 (unsigned long long)tot);
+    uint32_t n2 = 2;
+    while (n2 < tot) n2 <<= 1;
+    a.n2 = n2;
+    a.logits = c.B(0);
+    a.part = c.B(1);
+    a.out = c.B(2);
+    if (int e = launch(K_topk_part, a.g, 1, 1, 256, 0, a)) return e;
+    return launch(K_topk_merge, 1, 1, 1, 1024, n2 * 8, a);
+}
+
 // repack_q4k / repack_q6k: P{nblocks lo, hi, K}; repack_q8: P{nblocks lo, hi}; [paso|0, src, dst].  K (the row
 // length) places the blocks in the row chunk-plane layout of Q4_K / Q6_K.
 int op_repack(const Ctx& c, Kid k, const char* name) {
@@ -861,6 +904,8 @@ void register_ops() {
     v.push_back({"dec_attn_comb", op_dec_attn_comb});
     v.push_back({"argmax", op_argmax});
     v.push_back({"argmax_fin", op_argmax_fin});
+    v.push_back({"penalizar", op_penalizar});
+    v.push_back({"topk_cand", op_topk_cand});
     v.push_back({"repack_q4k", [](const Ctx& c) { return op_repack(c, K_repack_q4k, "repack_q4k"); }});
     v.push_back({"repack_q6k", [](const Ctx& c) { return op_repack(c, K_repack_q6k, "repack_q6k"); }});
     v.push_back({"repack_q8", [](const Ctx& c) { return op_repack(c, K_repack_q8, "repack_q8"); }});

@@ -1,24 +1,26 @@
 'use strict';
 // Command-line driver of the engine, for tests and the benchmark.
 //
-//   node cli.js generate --model M.gguf --prompt-file ids.json --n 128 [--mode fast|ref|engine] [--kv f16|f32]
+//   node cli.js generate --model M.gguf --prompt-file ids.json --n 128 [--mode fast|ref|engine|sample] [--kv f16|f32]
 //                        [--ctx N] [--batch N] [--no-tiled] [--logits-out file.f32]
 //                        [--repeat-penalty R] [--frequency-penalty F] [--presence-penalty P] [--host-loop]
+//                        [--temperature T] [--top-k K] [--top-p P] [--min-p M] [--seed S]
 //   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
-//                        [--warmup W] [--prefill P1,P2] [--eager]
+//                        [--warmup W] [--prefill P1,P2] [--eager] [--sample]
 //                        [--check-prompt-file ids.json --check-n N --check-logits file.f32]
 //
 // generate prints one JSON line {ids, prompt_ms, decode_ms, tps}; with --logits-out the logits each token was
 // chosen from are appended to the file as float32 (vocab floats per token).  mode "ref" runs the reference op
 // sequence with a host argmax per token; "fast" runs the captured one-token graph with the device argmax;
-// "engine" runs engine.generar with the given sampler parameters (no logits file).
+// "engine" runs engine.generar with the given sampler parameters (no logits file); "sample" the sampled
+// continuation with the host cross-check of every token (result field `control`).
 // bench prefills the prompt, then times n decode steps (device events around the graph replays, and the wall
 // clock) and prints {decode_tok_s, ms_per_token, ...}; with --check-prompt-file it first generates --check-n
 // greedy tokens from that prompt on the fused path (ids in check_ids, logits to --check-logits) for a parity
 // check by the caller.
 const fs = require('fs');
 const engine = require('./engine');
-const { argmax } = require('./sampling');
+const { argmax, Muestreador } = require('./sampling');
 
 function args(argv) {
   const o = { _: [] };
@@ -50,15 +52,39 @@ async function generate(o) {
   const logits = await engine.prefill(modelo, ids);
   const tPrompt = Date.now();
   const toks = [];
+  const extra = {};
   if (o.mode === 'engine') {
     // the engine's generation loop with sampler parameters (penalties -> host loop, greedy -> device loop)
     const params = { temperature: 0, max_tokens: n, host_loop: !!o['host-loop'] };
-    for (const k of ['repeat_penalty', 'frequency_penalty', 'presence_penalty']) {
+    for (const k of ['repeat_penalty', 'frequency_penalty', 'presence_penalty', 'temperature', 'top_k', 'top_p', 'min_p',
+      'seed']) {
       const v = o[k.replace(/_/g, '-')];
       if (v !== undefined) params[k] = parseFloat(v);
     }
     const r = await engine.generar(modelo, ids, params);
     for (const t of r.ids) toks.push(t);
+  } else if (o.mode === 'sample') {
+    // sampled continuation on the fused one-token plan (device penalties and top-k candidates, host draw); each
+    // token is also chosen on the host from the same logits by a second sampler of the same seed (the reference's
+    // procedure over the whole array), and the disagreements are counted
+    const params = {};
+    for (const k of ['repeat_penalty', 'frequency_penalty', 'presence_penalty', 'temperature', 'top_k', 'top_p', 'min_p',
+      'seed']) {
+      const v = o[k.replace(/_/g, '-')];
+      if (v !== undefined) params[k] = parseFloat(v);
+    }
+    const mu = new Muestreador(params);
+    const control = { mu: new Muestreador(params), penalizacion: 0, distintos: 0, candidatos: 0 };
+    const hist = ids.slice();
+    let id = mu.elegir(Float32Array.from(logits), hist);
+    if (control.mu.elegir(Float32Array.from(logits), hist) !== id) control.distintos++;
+    while (toks.length < n) {
+      toks.push(id); hist.push(id);
+      if (toks.length >= n) break;
+      id = modelo.pasoMuestreado(id, mu, hist, control);
+    }
+    delete control.mu;
+    extra.control = control;
   } else if (o.mode === 'ref') {
     let lg = logits;
     while (toks.length < n) {
@@ -78,14 +104,14 @@ async function generate(o) {
   }
   const tEnd = Date.now();
   if (out !== null) fs.closeSync(out);
-  const r = { ids: toks, prompt_ms: tPrompt - t0, decode_ms: tEnd - tPrompt, pos: modelo.pos };
+  const r = Object.assign({ ids: toks, prompt_ms: tPrompt - t0, decode_ms: tEnd - tPrompt, pos: modelo.pos }, extra);
   modelo.free();
   process.stdout.write(JSON.stringify(r) + '\n');
 }
 
 // One decode measurement after prefilling the first P ids: warm-up steps (then the position is rewound; the KV
 // slots they wrote are overwritten by the timed run), then n timed steps.
-async function medir(modelo, ids, P, n, warm, eager) {
+async function medir(modelo, ids, P, n, warm, eager, muestreo) {
   const gpu = modelo.gpu;
   const tp0 = Date.now();
   const logits = await engine.prefill(modelo, ids.slice(0, P));
@@ -102,11 +128,28 @@ async function medir(modelo, ids, P, n, warm, eager) {
   const tw0 = process.hrtime.bigint();
   const toks = modelo.decodificarVoraz(primero, n, { tiempos: tiempos, eager: eager });
   const wallMs = Number(process.hrtime.bigint() - tw0) / 1e6;
-  return {
+  const r = {
     prompt_tokens: P, n: n, decode_tok_s: n / (tiempos.ms / 1000), ms_per_token: tiempos.ms / n,
     device_ms: tiempos.ms, wall_ms: wallMs, wall_tok_s: n / (wallMs / 1000), prefill_ms: prefillMs,
     prefill_tok_s: P / (prefillMs / 1000), first_ids: [primero].concat(toks.slice(0, 7)),
   };
+  if (muestreo) {
+    // the same n steps from the same position with the reference's default sampler (temperature 0.8, top_k 40,
+    // top_p 0.95, min_p 0.05) and a fixed seed: one graph step, the device top-k and the host draw per token,
+    // timed on the wall clock (the host takes part in every token)
+    modelo.pos = pos0;
+    const mu = new Muestreador({ seed: 1 });
+    const hist = [primero];
+    let id = primero;
+    const ts0 = process.hrtime.bigint();
+    for (let i = 0; i < n; i++) { id = modelo.pasoMuestreado(id, mu, hist); hist.push(id); }
+    gpu.sincronizar();
+    const ms = Number(process.hrtime.bigint() - ts0) / 1e6;
+    r.sampled_tok_s = n / (ms / 1000);
+    r.sampled_ms_per_token = ms / n;
+    r.sampled_first_ids = hist.slice(0, 8);
+  }
+  return r;
 }
 
 // Greedy generation of n tokens from `ids` on the fused path, with the logits each token was chosen from
@@ -141,7 +184,7 @@ async function bench(o) {
   const runs = [];
   for (const P of prefills) {
     if (P > ids.length) throw new Error('prompt file has ' + ids.length + ' ids, ' + P + ' requested');
-    runs.push(await medir(modelo, ids, P, n, warm, !!o.eager));
+    runs.push(await medir(modelo, ids, P, n, warm, !!o.eager, !!o.sample));
   }
   const r = { runs: runs, load_ms: loadMs, ctx: modelo.ctx, nsplit: modelo.nsplit, kv_f16: modelo.kvF16,
     batch: modelo.batch, bytes_on_gpu: modelo.gpu.bytesUsados, check_ids: check };

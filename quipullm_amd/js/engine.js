@@ -97,6 +97,16 @@ async function generar(modelo, ids, params) {
         if (parar) break;
       }
     }
+  } else if (modelo.pasoMuestreado && !params.host_loop) {
+    // each step on the fused one-token plan; penalties and top-k candidates on the device where the sampler
+    // allows, the draw on the host (the first token from the prefill's logits)
+    let id = mu.elegir(logits, hist);
+    while (out.length < maxTok) {
+      if (esFin(id)) break;
+      hist.push(id); out.push(id); porToken(id);
+      if (out.length >= maxTok) break;
+      id = modelo.pasoMuestreado(id, mu, hist);
+    }
   } else {
     while (out.length < maxTok) {
       const id = mu.elegir(logits, hist);

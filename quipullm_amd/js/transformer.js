@@ -148,6 +148,12 @@ class ModeloTransformer {
     gpu.escribir(this.amax, 0, new Uint8Array(8 * AMAX_WG));
     this.maxGen = op_max_gen(this.meta);
     this.tokens = B(4 * this.maxGen, 'tokens');
+    // sampling on the device: top-k partials (ceil(V/2048) chunks x (k + 1) keys, k <= 128, plus a flag each),
+    // the candidates read back, and the penalty window's (token, count) pairs
+    const nParte = Math.ceil(this.vocab / 2048);
+    this.candParte = B(nParte * 129 * 8 + nParte * 4, 'topk_partials');
+    this.candSalida = B(4 * (2 + 2 * 128), 'topk_candidates');
+    this.penPares = B(4 * 2 * 64, 'penalty_pairs');
     this.contador = B(16, 'step_counter');
     this._armarGrupos();
     this.prepararDecode();
@@ -457,6 +463,81 @@ class ModeloTransformer {
     gpu.leer(this.tokens, 0, out);
     this.pos += n;
     return Array.from(out);
+  }
+
+  // ---------------------------------------------------------------- sampled decode
+  // One step of the fused plan from token `id` (a graph replay), then the next token chosen by the sampler `mu`
+  // (sampling.js) with the history `historial`: when mu allows it, the penalties and the top-k candidates on the
+  // device and only the draw on the host; otherwise, or when the candidates tie, from the whole logits on the
+  // host, exactly as the reference.  The position advances by one.
+  // control (checks): {mu: a second sampler with the same parameters and seed, penalizacion, distintos,
+  // candidatos: counters}; the same logits are also read back and the host's choice made with control.mu, which
+  // must agree bit for bit on the penalized logits and on the token.
+  pasoMuestreado(id, mu, historial, control) {
+    if (this.pos + 1 > this.ctx) throw new Error('context exceeded (' + this.ctx + ' tokens)');
+    if (!(id >= 0 && id < this.vocab)) throw new Error('token id ' + id + ' outside the vocabulary');
+    this.prepararDecode();
+    const gpu = this.gpu;
+    gpu.escribir(this.bPaso, 0, new Uint32Array([1, this.pos, 0, 0]));
+    gpu.escribir(this.bIds, 0, new Uint32Array([id]));
+    this._pasos(1);
+    this.pos += 1;
+    const lg = new Float32Array(this.vocab);
+    let ref = null;
+    if (control) {
+      gpu.leer(this.logits, 0, lg);
+      ref = Float32Array.from(lg);
+      control.mu.penalizar(ref, historial);
+    }
+    let t;
+    if (mu.usaCandidatosDispositivo(this.vocab)) {
+      this.penalizarDispositivo(mu, historial);
+      if (control) {
+        gpu.leer(this.logits, 0, lg);
+        const a = new Uint32Array(lg.buffer), b = new Uint32Array(ref.buffer);
+        for (let i = 0; i < a.length; i++) if (a[i] !== b[i]) { control.penalizacion++; break; }
+      }
+      const c = this.candidatosDispositivo(mu.topK);
+      if (c) {
+        if (control) control.candidatos++;
+        t = mu.muestrear(c.ids, c.vals);
+      } else {
+        gpu.leer(this.logits, 0, lg);
+        t = mu.elegirPenalizado(lg);
+      }
+    } else {
+      gpu.leer(this.logits, 0, lg);
+      t = mu.elegir(lg, historial);
+    }
+    if (control && control.mu.elegirPenalizado(ref) !== t) control.distintos++;
+    return t;
+  }
+
+  // The sampler's penalties (sampling.js:27-37) applied to the logits buffer in place.
+  penalizarDispositivo(mu, historial) {
+    if (!historial || !historial.length || !mu.penaliza()) return;
+    const pares = mu.conteos(historial);
+    const d = new Float64Array([mu.rep, mu.freq, mu.pres]), w = new Uint32Array(d.buffer);
+    const flat = new Uint32Array(2 * pares.length);
+    pares.forEach(function (p, i) { flat[2 * i] = p[0] >>> 0; flat[2 * i + 1] = p[1]; });
+    const gpu = this.gpu;
+    gpu.escribir(this.penPares, 0, flat);
+    despachar(null, gpu.grupo('penalizar', [gpu.uniforme([['u', pares.length], ['u', this.vocab], ['u', w[0]], ['u', w[1]],
+      ['u', w[2]], ['u', w[3]], ['u', w[4]], ['u', w[5]]]), this.logits, this.penPares]), 1);
+  }
+
+  // The k largest logits {ids, vals} in descending order, or null when two of the k + 1 largest are equal (the
+  // candidate set or order would then depend on the reference's heap) or a logit is NaN.
+  candidatosDispositivo(k) {
+    const gpu = this.gpu;
+    despachar(null, gpu.grupo('topk_cand', [gpu.uniforme([['u', this.vocab], ['u', k]]), this.logits, this.candParte,
+      this.candSalida]), 1);
+    const o = new Uint32Array(2 + 2 * k);
+    gpu.leer(this.candSalida, 0, o);
+    if (o[0] !== 0) return null;
+    const bits = new Uint32Array(k), ids = new Array(k);
+    for (let i = 0; i < k; i++) { bits[i] = o[2 + 2 * i]; ids[i] = o[3 + 2 * i]; }
+    return { ids: ids, vals: Float64Array.from(new Float32Array(bits.buffer)) };
   }
 
   // Greedy argmax of the current logits buffer on the device (same tie rule as the reference).

@@ -44,13 +44,13 @@ def generate(path, prompt, n, mode, kv, tmp, extra=()):
     if os.path.exists(lf):
         os.remove(lf)
     cmd = ["timeout", "-k", "5", "110", "node", CLI, "generate", "--model", path, "--prompt-file", pf, "--n", str(n),
-           "--mode", mode, "--kv", kv, "--ctx", "256"] + (["--logits-out", lf] if mode != "engine" else []) + \
+           "--mode", mode, "--kv", kv, "--ctx", "256"] + (["--logits-out", lf] if mode in ("fast", "ref") else []) + \
         list(extra)
     print("node generate", os.path.basename(path), mode, kv, flush=True)
     rc, out, err = run(cmd, timeout=120)
     assert rc == 0, err[-3000:]
     r = json.loads(out.strip().splitlines()[-1])
-    lg = np.fromfile(lf, np.float32) if mode != "engine" else None
+    lg = np.fromfile(lf, np.float32) if mode in ("fast", "ref") else None
     return r, lg
 
 
@@ -156,3 +156,53 @@ def test_engine_rejects_bad_input(models_dir, tmp_path):
         rc, out, err = run(["timeout", "-k", "5", "110", "node", CLI, "generate", "--model", path, "--prompt-file",
                             pf, "--n", "4", "--mode", "engine", "--ctx", "256"], timeout=120)
         assert rc == 1 and "error" in err, (ids, rc, err[-500:])
+
+
+SAMPLER_PARAMS = [
+    ["--temperature", "0.8", "--seed", "3"],                                    # the reference's defaults otherwise
+    ["--temperature", "1.5", "--top-k", "128", "--top-p", "1", "--min-p", "0", "--seed", "4"],
+    ["--temperature", "0.9", "--top-k", "20", "--repeat-penalty", "1.3", "--frequency-penalty", "0.2",
+     "--presence-penalty", "0.1", "--seed", "5"],
+    ["--temperature", "1.0", "--top-k", "0", "--seed", "6"],                   # all tokens: the host's path
+    ["--temperature", "0", "--repeat-penalty", "1.5", "--seed", "7"],          # greedy with penalties: host path
+]
+
+
+@pytest.mark.parametrize("name", ["mini_llama_q4km_c", "mini_qwen3moe_q4k_c", "tiny_q8"])
+@pytest.mark.parametrize("pi", range(len(SAMPLER_PARAMS)))
+def test_sampled_decode_matches_host_sampler(models_dir, tmp_path, name, pi):
+    """Stochastic decode on the fused one-token plan: penalties and top-k candidates on the device, the draw on the
+    host.  Every token is also chosen on the host from the same logits by a second sampler with the same seed
+    (the reference's procedure over the whole array): the penalized logits agree bit for bit and the chosen
+    tokens are identical; the device candidates serve every step where the sampler allows them."""
+    if name == "tiny_q8" and pi not in (0, 2):
+        pytest.skip("the realistic vocabulary runs the device-candidate cases only")
+    params = SAMPLER_PARAMS[pi]
+    path = synth.ensure_model(name, models_dir)
+    vocab = synth.CONFIGS[name].vocab
+    prompt = synth.random_prompt(vocab, 12, 5 + pi)
+    n = 40
+    r, _ = generate(path, prompt, n, "sample", "f16", str(tmp_path), params)
+    c = r["control"]
+    assert len(r["ids"]) == n and all(0 <= t < vocab for t in r["ids"])
+    assert c["distintos"] == 0 and c["penalizacion"] == 0, c
+    device = "--top-k" not in params or params[params.index("--top-k") + 1] != "0"
+    device = device and params[1] != "0"
+    if device:
+        assert c["candidatos"] >= n - 3, c     # a rare tie falls back to the host's heap
+    else:
+        assert c["candidatos"] == 0, c
+
+
+def test_engine_sampling_is_seeded(models_dir, tmp_path):
+    """engine.generar with a temperature runs the sampled device loop; the same seed gives the same tokens as the
+    checked loop, another seed other tokens (temperature 100: the random-weight models' logits are too peaked
+    for the draw to matter at ordinary temperatures)."""
+    path = synth.ensure_model("mini_llama_q4km_c", models_dir)
+    prompt = synth.random_prompt(1000, 12, 9)
+    p = ["--temperature", "100", "--top-k", "64", "--top-p", "1", "--min-p", "0"]
+    a, _ = generate(path, prompt, 30, "engine", "f16", str(tmp_path), p + ["--seed", "11"])
+    b, _ = generate(path, prompt, 30, "sample", "f16", str(tmp_path), p + ["--seed", "11"])
+    c, _ = generate(path, prompt, 30, "engine", "f16", str(tmp_path), p + ["--seed", "12"])
+    assert a["ids"] == b["ids"]
+    assert a["ids"] != c["ids"]

@@ -464,6 +464,80 @@ def test_argmax_ties_nan_negative(quipu, dev, oracle):
         assert int(dev.get(out, (1,), np.uint32)[0]) == oracle.argmax(v)
 
 
+# ------------------------------------------------------------------------------------------------ sampling
+def topk_cand(quipu, dev, v, k):
+    """topk_cand with its buffers sized as the op documents: ceil(V/2048)*(k+1) keys + flags, 2 + 2k words."""
+    g = (v.size + 2047) // 2048
+    part, out = dev.zeros(g * (k + 1) * 8 + g * 4), dev.zeros(4 * (2 + 2 * k))
+    quipu.dispatch("topk_cand", [("u", v.size), ("u", k)], [dev.buf(v), part, out])
+    o = dev.get(out, (2 + 2 * k,), np.uint32)
+    return int(o[0]), int(o[1]), o[2::2].view(np.float32), o[3::2].astype(np.int64)
+
+
+def distinct_logits(V, seed):
+    # a permutation of V integers over 7: distinct float32 values (V < 2^24), negative and positive
+    return ((np.random.default_rng(seed).permutation(V) - V // 2) / 7.0).astype(np.float32)
+
+
+@pytest.mark.parametrize("V,k", [(3, 2), (100, 1), (100, 40), (2048, 128), (2049, 40), (4096, 7), (32000, 40),
+                                 (128256, 40), (128256, 128), (151936, 100)])
+def test_topk_candidates(quipu, dev, V, k):
+    """The k largest logits, descending, with ids; chunk edges (2048, 2049) and the 8B / MoE vocabularies."""
+    v = distinct_logits(V, V + k)
+    flags, kk, vals, ids = topk_cand(quipu, dev, v, k)
+    order = np.lexsort((np.arange(V), -v))[:k]
+    assert (flags, kk) == (0, k)
+    assert ids.tolist() == order.tolist()
+    assert vals.view(np.uint32).tolist() == v[order].view(np.uint32).tolist()
+
+
+def test_topk_candidates_flags(quipu, dev):
+    """Bit 1 for two equal values among the k+1 largest (inside the set, or the k-th against the (k+1)-th), not
+    below it; -0 and +0 count as equal; bit 0 for a NaN anywhere."""
+    k = 40
+    base = distinct_logits(5000, 3)
+    top = np.argsort(-base)
+    for i, j, want in ((2, 3, 2), (k - 1, k, 2), (k, k + 1, 0), (0, 1, 2)):
+        v = base.copy()
+        v[top[j]] = v[top[i]]
+        assert topk_cand(quipu, dev, v, k)[0] == want, (i, j)
+    v = -np.arange(1, 301, dtype=np.float32)
+    v[10], v[20] = 0.0, -0.0
+    assert topk_cand(quipu, dev, v, 5)[0] == 2
+    v = base.copy()
+    v[4321] = np.nan
+    assert topk_cand(quipu, dev, v, k)[0] & 1
+
+
+def test_topk_candidates_rejects(quipu):
+    """k outside 1..128, k >= V and partial lists beyond the merge's 16384 keys fail before any launch."""
+    for V, k in ((100, 0), (100, 100), (1000, 129), (300000, 128)):
+        with pytest.raises(Exception, match="topk_cand"):
+            quipu.dispatch("topk_cand", [("u", V), ("u", k)], [0, 0, 0])
+
+
+@pytest.mark.parametrize("rep,freq,pres", [(1.3, 0.2, 0.1), (1.0, 0.5, 0.0), (0.7, 0.0, 1.25), (1.1, 0.0, 0.0)])
+def test_penalizar_matches_oracle(quipu, dev, rep, freq, pres):
+    """The reference's penalty arithmetic in double, stored to float: bit-exact with the oracle (ids >= V and
+    history beyond the 64-token window are skipped)."""
+    from oracle.sampling import Sampler
+    rng = np.random.default_rng(int(rep * 100 + freq * 10 + pres))
+    V = 5000
+    lg = (rng.standard_normal(V) * 3).astype(np.float32)
+    hist = rng.integers(0, V + 20, 90).tolist()
+    want = lg.copy()
+    Sampler(temperature=0.0, repeat_penalty=rep, frequency_penalty=freq, presence_penalty=pres).penalize(want, hist)
+    cnt = {}
+    for t in hist[-64:]:
+        cnt[t] = cnt.get(t, 0) + 1
+    pairs = np.array([x for kv in cnt.items() for x in kv], np.uint32)
+    d = np.array([rep, freq, pres], np.float64).view(np.uint32)
+    lb = dev.buf(lg)
+    quipu.dispatch("penalizar", [("u", len(cnt)), ("u", V)] + [("u", int(w)) for w in d], [lb, dev.buf(pairs)])
+    got = dev.get(lb, (V,))
+    assert got.view(np.uint32).tolist() == want.view(np.uint32).tolist()
+
+
 # ------------------------------------------------------------------------------------------------ attention
 def rope_table(base, nrot):
     """base^(-2j/nrot) rounded once to float, with the exponent the float quotient (as the JS host builds it)."""

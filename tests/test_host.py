@@ -52,7 +52,8 @@ OPS = ["matmul_%s_%s" % (f, s) for f in ("q4k", "q6k", "q8", "f32") for s in ("1
       ["embed_%s" % f for f in ("q4k", "q6k", "q8", "f32")] + \
       ["rmsnorm", "norm_rope", "kv_write", "atencion", "swiglu", "moe_topk", "moe_comb", "gemv", "dec_attn",
        "dec_attn_comb", "argmax", "argmax_fin", "repack_q4k", "repack_q6k", "repack_q8", "fill_u32", "dequant",
-       "copy_f4", "read_f4", "moe_gate_up_q4k", "moe_gate_up_q6k", "moe_down_q4k", "moe_down_q6k"]
+       "copy_f4", "read_f4", "moe_gate_up_q4k", "moe_gate_up_q6k", "moe_down_q4k", "moe_down_q6k", "penalizar",
+       "topk_cand"]
 
 
 def test_op_table(built):
@@ -177,13 +178,15 @@ out.pick = m.elegir(lg, [0, 0, 1]);
 out.lg = Array.from(lg);
 out.greedy = new s.Muestreador({temperature: 0}).esVoraz();
 out.notGreedy = new s.Muestreador({temperature: 0, repeat_penalty: 1.1}).esVoraz();
-try { new s.Muestreador({temperature: 0.8}); out.threw = false; } catch (e) { out.threw = true; }
+const st = new s.Muestreador({temperature: 0.8});
+out.stochastic = !st.esVoraz() && st.usaCandidatosDispositivo(32000) && !st.usaCandidatosDispositivo(40) &&
+  !new s.Muestreador({temperature: 0.8, top_k: 0}).usaCandidatosDispositivo(32000);
 console.log(JSON.stringify(out));
 """ % os.path.join(JS, "sampling.js"))
     assert r["tie"] == 1 and r["nan"] == 1 and r["neg"] == 1
     # token 0 (seen twice): 4 / 2 - (2 * 0.5 + 0.25) = 0.75; token 1 (once): -2 * 2 - (0.5 + 0.25) = -4.75
     assert r["lg"] == [0.75, -4.75, 3.5, 1.0] and r["pick"] == 2
-    assert r["greedy"] and not r["notGreedy"] and r["threw"]
+    assert r["greedy"] and not r["notGreedy"] and r["stochastic"]
 
 
 def test_js_rope_table_matches_double_power():
