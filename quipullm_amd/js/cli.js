@@ -123,6 +123,7 @@ async function medir(modelo, ids, P, n, warm, eager, muestreo) {
     modelo.decodificarVoraz(primero, warm);
     gpu.sincronizar();
     modelo.pos = pos0;
+    modelo.hist.length = Math.min(modelo.hist.length, pos0);
   }
   const tiempos = {};
   const tw0 = process.hrtime.bigint();
@@ -138,6 +139,7 @@ async function medir(modelo, ids, P, n, warm, eager, muestreo) {
     // top_p 0.95, min_p 0.05) and a fixed seed: one graph step, the device top-k and the host draw per token,
     // timed on the wall clock (the host takes part in every token)
     modelo.pos = pos0;
+    modelo.hist.length = Math.min(modelo.hist.length, pos0);
     const mu = new Muestreador({ seed: 1 });
     const hist = [primero];
     let id = primero;

@@ -50,12 +50,14 @@ async function cargarModelo(ruta, opciones) {
   return modelo;
 }
 
-// Prompt processing in chunks of modelo.batch (reference engine.js:253-288); returns the last logits.
-async function prefill(modelo, ids) {
-  modelo.reset();
+// Prompt processing in chunks of modelo.batch from id `desde` (reference engine.js:253-288); returns the last
+// logits.  desde = 0 resets the model.
+async function prefill(modelo, ids, desde) {
+  desde = desde || 0;
+  if (!desde) modelo.reset();
   const TL = modelo.batch;
   let logits = null;
-  for (let i = 0; i < ids.length; i += TL) {
+  for (let i = desde; i < ids.length; i += TL) {
     const fin = Math.min(i + TL, ids.length);
     logits = await modelo.forward(ids.slice(i, fin), fin >= ids.length);
   }
@@ -74,7 +76,9 @@ async function generar(modelo, ids, params) {
   const porToken = params.onToken || function () {};
   const mu = new Muestreador(params);
   const t0 = Date.now();
-  let logits = await prefill(modelo, ids);
+  // prompt cache (reference engine.js:254-256): the ids already in the model's state are not computed again
+  const saltar = modelo.cacheOn && modelo.reutilizar && params.prompt_cache !== false ? modelo.reutilizar(ids) : 0;
+  let logits = await prefill(modelo, ids, saltar);
   const tPrompt = Date.now();
   const hist = ids.slice();
   const out = [];
@@ -118,7 +122,8 @@ async function generar(modelo, ids, params) {
   }
   const tEnd = Date.now();
   const seg = (tEnd - tPrompt) / 1000;
-  return { ids: out, prompt_ms: tPrompt - t0, decode_ms: tEnd - tPrompt, tps: out.length && seg > 0 ? out.length / seg : null };
+  return { ids: out, prompt_ms: tPrompt - t0, decode_ms: tEnd - tPrompt, tps: out.length && seg > 0 ? out.length / seg : null,
+    reutilizados: saltar };
 }
 
 module.exports = { cargarRegistro: cargarRegistro, cargarModelo: cargarModelo, prefill: prefill, generar: generar, gpu: gpu };

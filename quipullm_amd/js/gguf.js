@@ -98,7 +98,7 @@ function metaDe(ruta, opciones) {
   return {
     id: opciones.id || ruta, kv: g.kv, tensors: g.tensors, data_start: g.data_start,
     ctx: opciones.ctx || 4096, overrides: opciones.overrides || {}, arch_options: man.options || {},
-    options: Object.assign({ tiled_prefill: true, prompt_cache: false }, opciones.options || {}),
+    options: Object.assign({ tiled_prefill: true, prompt_cache: true }, opciones.options || {}),   // server.py:808-809 defaults
   };
 }
 

@@ -61,6 +61,11 @@ class ModeloTransformer {
     this.bufs = [];
     this.pos = 0;
     this.grafo = null;
+    // prompt cache (the reference's interface, engine.js:254-290 / lfm2.js:205-245): the ids whose KV rows are
+    // written, in order; hist.length === pos whenever the cache is usable
+    this.cacheOn = op.prompt_cache !== false;
+    this.hist = [];
+    this.intervaloCP = 64;
   }
 
   load(ruta, progreso) {
@@ -238,7 +243,25 @@ class ModeloTransformer {
 
   reset() {
     this.pos = 0;   // the KV cache is overwritten by position (reference transformer.js:243-245)
+    this.hist = [];
   }
+
+  // Prompt cache: how many leading ids of a new prompt are already in the KV cache (pos is set there), or 0 (the
+  // caller then resets).  The KV rows are written by position and depend only on the ids before them, so the
+  // longest common prefix with the processed history stays valid and no state snapshot is needed (unlike the
+  // reference's LFM2 convolution states).  The last id is always recomputed: its logits are the result.
+  reutilizar(ids) {
+    if (!this.cacheOn || !this.hist.length || this.pos !== this.hist.length) return 0;
+    const h = this.hist, m = Math.min(h.length, ids.length - 1);
+    let n = 0;
+    while (n < m && h[n] === ids[n]) n++;
+    h.length = n;
+    this.pos = n;
+    return n;
+  }
+
+  // The reference engine saves recurrent-state checkpoints here; a KV cache needs none.
+  guardarPunto() {}
 
   _despacharCapas(T) {
     const G = this.G, self = this;
@@ -292,6 +315,7 @@ class ModeloTransformer {
       mm(this.G.salida, true);
     }
     this.pos += T;
+    for (const id of ids) this.hist.push(id);
     if (!conLogits) return Promise.resolve(null);
     const out = new Float32Array(this.vocab);
     gpu.leer(this.logits, 0, out);
@@ -462,6 +486,8 @@ class ModeloTransformer {
     const out = new Uint32Array(n);
     gpu.leer(this.tokens, 0, out);
     this.pos += n;
+    this.hist.push(primero);                                    // the n processed ids: primero and out[0..n-2]
+    for (let i = 0; i + 1 < n; i++) this.hist.push(out[i]);
     return Array.from(out);
   }
 
@@ -482,6 +508,7 @@ class ModeloTransformer {
     gpu.escribir(this.bIds, 0, new Uint32Array([id]));
     this._pasos(1);
     this.pos += 1;
+    this.hist.push(id);
     const lg = new Float32Array(this.vocab);
     let ref = null;
     if (control) {

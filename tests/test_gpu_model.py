@@ -206,3 +206,45 @@ def test_engine_sampling_is_seeded(models_dir, tmp_path):
     c, _ = generate(path, prompt, 30, "engine", "f16", str(tmp_path), p + ["--seed", "12"])
     assert a["ids"] == b["ids"]
     assert a["ids"] != c["ids"]
+
+
+PROMPT_CACHE = r"""
+const engine = require(%s);
+(async () => {
+  const p1 = %s, extra = %s, kv = %s;
+  const m = await engine.cargarModelo(%s, {ctx: 256, options: {kv_f16: kv === 'f16'}});
+  const a = await engine.generar(m, p1, {temperature: 0, max_tokens: 10});
+  const p2 = p1.concat(a.ids, extra);
+  const b = await engine.generar(m, p2, {temperature: 0, max_tokens: 10});
+  const c = await engine.generar(m, p2, {temperature: 0, max_tokens: 10});
+  const d = await engine.generar(m, p1.slice(0, 5).concat(extra), {temperature: 0, max_tokens: 10});
+  m.free();
+  const f = await engine.cargarModelo(%s, {ctx: 256, options: {kv_f16: kv === 'f16', prompt_cache: false}});
+  const b2 = await engine.generar(f, p2, {temperature: 0, max_tokens: 10});
+  const d2 = await engine.generar(f, p1.slice(0, 5).concat(extra), {temperature: 0, max_tokens: 10});
+  f.free();
+  console.log(JSON.stringify({a: a.ids, b: b.ids, c: c.ids, d: d.ids, b2: b2.ids, d2: d2.ids, p2: p2.length,
+    rb: b.reutilizados, rc: c.reutilizados, rd: d.reutilizados, rb2: b2.reutilizados}));
+})().catch((e) => { console.error(e.stack); process.exit(1); });
+"""
+
+
+@pytest.mark.parametrize("name,kv", [("mini_llama_q4km_c", "f16"), ("mini_qwen3moe_q4k_c", "f32")])
+def test_prompt_cache_reuses_the_common_prefix(models_dir, name, kv):
+    """A second request whose prompt extends the first request's prompt and answer computes only the new ids
+    (the answer's last id was never processed, so it is recomputed); the same prompt again recomputes only its
+    last id; a prompt sharing 5 ids reuses 5.  Greedy ids equal those of a model with the cache off."""
+    path = synth.ensure_model(name, models_dir)
+    p1 = synth.random_prompt(1000, 20, 21)
+    extra = synth.random_prompt(1000, 7, 22)
+    eng = os.path.join(ROOT, "quipullm_amd", "js", "engine.js")
+    script = PROMPT_CACHE % (json.dumps(eng), json.dumps(p1), json.dumps(extra), json.dumps(kv), json.dumps(path),
+                             json.dumps(path))
+    print("node prompt cache", name, kv, flush=True)
+    rc, out, err = run(["timeout", "-k", "5", "110", "node", "-e", script], timeout=120)
+    assert rc == 0, err[-3000:]
+    r = json.loads(out.strip().splitlines()[-1])
+    assert r["rb"] == len(p1) + len(r["a"]) - 1
+    assert r["rc"] == r["p2"] - 1
+    assert r["rd"] == 5 and r["rb2"] == 0
+    assert r["b"] == r["b2"] and r["c"] == r["b2"] and r["d"] == r["d2"]
