@@ -10,7 +10,7 @@
  * -ffp-contract=off so that no multiply-add is fused: the reference's dequant formula is defined as the
  * non-fused f32 sequence.
  *
- * Raw weight blocks are the GGUF/ggml layouts (Q4_K 144 B, Q6_K 210 B, Q8_0 34 B), unpadded.
+ * Raw weight blocks are the GGUF/ggml layouts (Q4_K 144 B, Q5_K 176 B, Q6_K 210 B, Q8_0 34 B), unpadded.
  */
 #include <math.h>
 #include <stdint.h>
@@ -23,6 +23,7 @@
 #define OR_F32 0
 #define OR_Q8_0 8
 #define OR_Q4_K 12
+#define OR_Q5_K 13
 #define OR_Q6_K 14
 
 /* ------------------------------------------------------------------ f16 -> f32 (exact)
@@ -106,6 +107,19 @@ static inline float q4k_deq(const uint8_t* blk, int e) {
     return a - fm;
 }
 
+/* ------------------------------------------------------------------ Q5_K
+ * Block: d f16, dmin f16, scales[12], qh[32], qs[128] (kquants.js:8); the Q4_K scale/min unpack.  Element
+ * dequant: kquants.js:151-153 (sm.x * (nibble + 16 * bit j of qh[l]) - sm.y). */
+static inline float q5k_deq(const uint8_t* blk, int e) {
+    int j = e >> 5, l = e & 31;
+    float fd, fm;
+    q4k_scmin(blk, j, &fd, &fm);
+    unsigned lo = (blk[48 + (j >> 1) * 32 + l] >> ((j & 1) * 4)) & 15u;
+    unsigned hi = (blk[16 + l] >> j) & 1u;
+    float a = fd * (float)(lo + (hi << 4));
+    return a - fm;
+}
+
 /* ------------------------------------------------------------------ Q6_K
  * Block: ql[128], qh[64], scales[16] int8, d f16 (kquants.js:9).  scq6: kquants.js:92-96.
  * Element dequant: kquants.js:172-175 (scq6(s) * (q - 32)). */
@@ -133,6 +147,8 @@ void or_dequant(int fmt, const uint8_t* raw, int64_t nelem, float* out) {
     int64_t i;
     if (fmt == OR_Q4_K) {
         for (i = 0; i < nelem; i++) out[i] = q4k_deq(raw + (i >> 8) * 144, (int)(i & 255));
+    } else if (fmt == OR_Q5_K) {
+        for (i = 0; i < nelem; i++) out[i] = q5k_deq(raw + (i >> 8) * 176, (int)(i & 255));
     } else if (fmt == OR_Q6_K) {
         for (i = 0; i < nelem; i++) out[i] = q6k_deq(raw + (i >> 8) * 210, (int)(i & 255));
     } else if (fmt == OR_Q8_0) {
@@ -170,6 +186,37 @@ static float row_q4k(const uint8_t* row, int K, const float* x) {
                 uint32_t w = rd32(qb + wi * 4);
                 float q[4] = {(float)((w >> sh) & 15u), (float)((w >> (sh + 8)) & 15u),
                               (float)((w >> (sh + 16)) & 15u), (float)((w >> (sh + 24)) & 15u)};
+                s = s + dot4(q, xb + wi * 4);
+                m = m + sum4(xb + wi * 4);
+            }
+            a = a + (fd * s - fm * m);
+        }
+        lanes[lane] = a;
+    }
+    return tree32(lanes);
+}
+
+/* Q5_K: the Q4_K item loop of kquants.js:188-251 with the q5k setup/q of kquants.js:134-138 (quants at word 12,
+ * q = nibble + 16 * bit j of the qh bytes at word 4). */
+static float row_q5k(const uint8_t* row, int K, const float* x) {
+    int nb = K / 256, ni = nb * 8;
+    float lanes[32];
+    for (int lane = 0; lane < 32; lane++) {
+        float a = 0.0f;
+        for (int it = lane; it < ni; it += 32) {
+            int b = it / 8, j = it % 8;
+            const uint8_t* blk = row + (size_t)b * 176;
+            float fd, fm;
+            q4k_scmin(blk, j, &fd, &fm);
+            const uint8_t* qb = blk + 48 + (j >> 1) * 32;
+            int sh = (j & 1) * 4;
+            const float* xb = x + b * 256 + j * 32;
+            float s = 0.0f, m = 0.0f;
+            for (int wi = 0; wi < 8; wi++) {
+                uint32_t w = rd32(qb + wi * 4), h = rd32(blk + 16 + wi * 4);
+                float q[4];
+                for (int t = 0; t < 4; t++)
+                    q[t] = (float)((w >> (sh + 8 * t)) & 15u) + 16.0f * (float)((h >> (8 * t + j)) & 1u);
                 s = s + dot4(q, xb + wi * 4);
                 m = m + sum4(xb + wi * 4);
             }
@@ -248,6 +295,7 @@ static float row_f32(const float* row, int K, const float* x) {
 static size_t row_bytes(int fmt, int K) {
     switch (fmt) {
     case OR_Q4_K: return (size_t)(K / 256) * 144;
+    case OR_Q5_K: return (size_t)(K / 256) * 176;
     case OR_Q6_K: return (size_t)(K / 256) * 210;
     case OR_Q8_0: return (size_t)(K / 32) * 34;
     default: return (size_t)K * 4;
@@ -257,6 +305,7 @@ static size_t row_bytes(int fmt, int K) {
 static float row_dot(int fmt, const uint8_t* row, int K, const float* x) {
     switch (fmt) {
     case OR_Q4_K: return row_q4k(row, K, x);
+    case OR_Q5_K: return row_q5k(row, K, x);
     case OR_Q6_K: return row_q6k(row, K, x);
     case OR_Q8_0: return row_q8(row, K, x);
     default: return row_f32((const float*)row, K, x);
@@ -270,6 +319,7 @@ static float row_serial(int fmt, const uint8_t* row, int K, const float* x) {
     for (int k = 0; k < K; k++) {
         float w;
         if (fmt == OR_Q4_K) w = q4k_deq(row + (size_t)(k >> 8) * 144, k & 255);
+        else if (fmt == OR_Q5_K) w = q5k_deq(row + (size_t)(k >> 8) * 176, k & 255);
         else if (fmt == OR_Q6_K) w = q6k_deq(row + (size_t)(k >> 8) * 210, k & 255);
         else if (fmt == OR_Q8_0) w = q8_deq(row + (size_t)(k >> 5) * 34, k & 31);
         else w = ((const float*)row)[k];
@@ -320,6 +370,7 @@ void or_embed(int fmt, const uint8_t* W, int D, const uint32_t* ids, int T, floa
         for (int k = 0; k < D; k++) {
             float v;
             if (fmt == OR_Q4_K) v = q4k_deq(row + (size_t)(k >> 8) * 144, k & 255);
+            else if (fmt == OR_Q5_K) v = q5k_deq(row + (size_t)(k >> 8) * 176, k & 255);
             else if (fmt == OR_Q6_K) v = q6k_deq(row + (size_t)(k >> 8) * 210, k & 255);
             else if (fmt == OR_Q8_0) v = q8_deq(row + (size_t)(k >> 5) * 34, k & 31);
             else v = ((const float*)row)[k];
@@ -590,7 +641,7 @@ size_t or_layer_sizeof(void) { return sizeof(OrLayer); }
 
 /* mm() of transformer.js:268-284: one token -> lane order; T >= 8 with a K-quant and tiling on -> tiled. */
 static void mm(const OrModel* m, int fmt, const uint8_t* W, int N, int K, const float* x, int T, float* y, int acc) {
-    int kq = fmt == OR_Q4_K || fmt == OR_Q6_K;
+    int kq = fmt == OR_Q4_K || fmt == OR_Q5_K || fmt == OR_Q6_K;
     int mode = (T >= 8 && kq && m->tiled) ? 1 : 0;
     or_matmul(fmt, W, N, K, x, T, y, acc, mode);
 }

@@ -18,9 +18,9 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "lib", "libquipu.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "quipu.h")
 
-F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
-BLOCK = {F32: (1, 4), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
-FMT_NAME = {F32: "f32", Q8_0: "q8", Q4_K: "q4k", Q6_K: "q6k"}
+F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
+BLOCK = {F32: (1, 4), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+FMT_NAME = {F32: "f32", Q8_0: "q8", Q4_K: "q4k", Q5_K: "q5k", Q6_K: "q6k"}
 
 # gemv segment modes (qp_args.h)
 STORE, ACC, SWIGLU, ARGMAX = 0, 1, 2, 3
@@ -173,8 +173,8 @@ class Quipu:
 
     # -------------------------------------------------------------- weights (device layout)
     def upload_matrix(self, fmt, raw, N, K):
-        """GGUF blocks of an N x K matrix -> device tensor in this backend's layout (repacked on the device: Q4_K
-        and Q6_K to row chunk planes, Q8_0 to planar qs | d).  Returns the handle."""
+        """GGUF blocks of an N x K matrix -> device tensor in this backend's layout (repacked on the device: Q4_K,
+        Q5_K and Q6_K to row chunk planes, Q8_0 to planar qs | d).  Returns the handle."""
         raw = np.ascontiguousarray(np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray)) else raw)
         nbytes = device_bytes(fmt, N, K)
         assert raw.nbytes == nbytes, (raw.nbytes, nbytes)
@@ -183,7 +183,7 @@ class Quipu:
         staging = self.buffer_from(raw)
         dst = self.alloc(nbytes)
         nb = N * K // BLOCK[fmt][0]
-        op = {Q4_K: "repack_q4k", Q6_K: "repack_q6k", Q8_0: "repack_q8"}[fmt]
+        op = {Q4_K: "repack_q4k", Q5_K: "repack_q5k", Q6_K: "repack_q6k", Q8_0: "repack_q8"}[fmt]
         self.dispatch(op, [("u", nb & 0xFFFFFFFF), ("u", nb >> 32), ("u", K)], [0, staging, dst])
         self.sync()
         self.free(staging)

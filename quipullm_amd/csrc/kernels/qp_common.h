@@ -153,16 +153,36 @@ QP_DEV float deq_q8_planar(const uint8_t* base, uint64_t NB, uint64_t gb, uint32
     return (float)q * h2f(dp[0] | (dp[1] << 8));
 }
 
+// Q5_K (reference kquants.js:8, deq at 151-153): the Q4_K header and sub-block scales, qh[32] at bytes 16..47 and
+// qs[128] at 48..175; q = nibble (low for even sub-blocks, high for odd) + 16 * bit j of qh[l].
+QP_DEV float deq_q5k_dev(const uint8_t* base, uint32_t nb, uint64_t row, uint32_t b, uint32_t e) {
+#pragma clang fp contract(off)
+    const uint32_t j = e >> 5, l = e & 31;
+    uint8_t s[12];
+    for (int i = 0; i < 12; i++) s[i] = kq_byte<176>(base, nb, row, b, 4 + i);
+    uint32_t sc, mn;
+    q4k_scmin_bytes(s, j, sc, mn);
+    const float d = h2f(kq_byte<176>(base, nb, row, b, 0) | (kq_byte<176>(base, nb, row, b, 1) << 8));
+    const float dmin = h2f(kq_byte<176>(base, nb, row, b, 2) | (kq_byte<176>(base, nb, row, b, 3) << 8));
+    const float fd = d * (float)sc;
+    const float fm = dmin * (float)mn;
+    const uint32_t lo = (kq_byte<176>(base, nb, row, b, 48 + (j >> 1) * 32 + l) >> ((j & 1) * 4)) & 15u;
+    const uint32_t hi = (kq_byte<176>(base, nb, row, b, 16 + l) >> j) & 1u;
+    const float a = fd * (float)(lo + 16 * hi);
+    return a - fm;
+}
+
 // Element k of row `row` of a K-wide matrix in device layout fmt (NB = total blocks of the tensor).
 QP_DEV float deq_elem(uint32_t fmt, const uint8_t* base, uint64_t NB, uint64_t row, uint32_t K, uint32_t k) {
     if (fmt == QP_Q4_K) return deq_q4k_dev(base, K >> 8, row, k >> 8, k & 255);
+    if (fmt == QP_Q5_K) return deq_q5k_dev(base, K >> 8, row, k >> 8, k & 255);
     if (fmt == QP_Q6_K) return deq_q6k_dev(base, K >> 8, NB, row, k >> 8, k & 255);
     if (fmt == QP_Q8_0) return deq_q8_planar(base, NB, row * (K >> 5) + (k >> 5), k & 31);
     return reinterpret_cast<const float*>(base)[row * K + k];
 }
 
 QP_DEV uint64_t total_blocks(uint32_t fmt, uint64_t nrows, uint32_t K) {
-    if (fmt == QP_Q4_K || fmt == QP_Q6_K) return nrows * (K >> 8);
+    if (fmt == QP_Q4_K || fmt == QP_Q5_K || fmt == QP_Q6_K) return nrows * (K >> 8);
     if (fmt == QP_Q8_0) return nrows * (K >> 5);
     return nrows * K;
 }

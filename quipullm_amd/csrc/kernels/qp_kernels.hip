@@ -11,16 +11,20 @@
 // ====================================================================================== load-time ops
 // GGUF blocks -> the row chunk-plane layout of Q4_K / Q6_K (qp_args.h).  One thread per 16-byte chunk; a.k is
 // the row length (nb = K/256 blocks per row).
-KERNEL __launch_bounds__(256) void qp_repack_q4k(QpRepackArgs a) {
-    const uint64_t NB = a.nblocks, nchunk = NB * 9;
+// Q4_K (144-byte blocks, 9 chunks) and Q5_K (176 bytes, 11 chunks): every chunk of a GGUF block moves whole.
+template <int NCH>
+QP_DEV void repack_chunks(const QpRepackArgs& a) {
+    const uint64_t NB = a.nblocks, nchunk = NB * NCH;
     const uint32_t nb = a.k >> 8;
     for (uint64_t t = blockIdx.x * 256ull + threadIdx.x; t < nchunk; t += (uint64_t)gridDim.x * 256ull) {
-        const uint64_t blk = t / 9, row = blk / nb;
-        const uint32_t c = (uint32_t)(t - blk * 9), b = (uint32_t)(blk - row * nb);
-        const uint4 v = cptr<uint4>(a.src)[t];  // GGUF offset blk*144 + c*16
-        mptr<uint4>(a.dst + row * nb * 144 + (uint64_t)c * nb * 16 + b * 16)[0] = v;
+        const uint64_t blk = t / NCH, row = blk / nb;
+        const uint32_t c = (uint32_t)(t - blk * NCH), b = (uint32_t)(blk - row * nb);
+        const uint4 v = cptr<uint4>(a.src)[t];  // GGUF offset blk*16*NCH + c*16
+        mptr<uint4>(a.dst + row * nb * (16 * NCH) + (uint64_t)c * nb * 16 + b * 16)[0] = v;
     }
 }
+KERNEL __launch_bounds__(256) void qp_repack_q4k(QpRepackArgs a) { repack_chunks<9>(a); }
+KERNEL __launch_bounds__(256) void qp_repack_q5k(QpRepackArgs a) { repack_chunks<11>(a); }
 
 KERNEL __launch_bounds__(256) void qp_repack_q6k(QpRepackArgs a) {
     const uint64_t NB = a.nblocks, nchunk = NB * 14;
@@ -494,6 +498,10 @@ struct KQ<QP_Q4_K> {
     static constexpr int CPB = 9, RB = 144, LOADS = 9, GROUP = 32;  // GROUP: elements per x sum
 };
 template <>
+struct KQ<QP_Q5_K> {
+    static constexpr int CPB = 11, RB = 176, LOADS = 11, GROUP = 32;
+};
+template <>
 struct KQ<QP_Q6_K> {
     static constexpr int CPB = 13, RB = 208, LOADS = 14, GROUP = 16;
 };
@@ -600,6 +608,72 @@ QP_DEV void kq_dot_q4k(const U& B, const float4* xb4, const float* xsb, float (&
             q4k_sm(hd[1], hd[2], hd[3], 2 * p, sc0, mn0);
             q4k_sm(hd[1], hd[2], hd[3], 2 * p + 1, sc1, mn1);
             // low nibbles were summed as q*2^-24, high nibbles as 16q*2^-24
+            tot[r] += (d * (float)sc0) * (alo[r] * 16777216.0f) - (dm * (float)mn0) * sxs[2 * p];
+            tot[r] += (d * (float)sc1) * (ahi[r] * 1048576.0f) - (dm * (float)mn1) * sxs[2 * p + 1];
+        }
+    }
+}
+
+// Q5_K: chunk 0 the Q4_K header, chunks 1-2 qh[32], chunks 3-10 qs[128].  Each nibble mask of kq_dot_q4k also
+// takes its element's high bit: with g = qh >> 2p, bit 2p of a qh byte lands on the nibble's 16 (low nibbles, q
+// summed as q*2^-24) and bit 2p+1 on its 256 (high nibbles, summed as 16q*2^-24).
+template <class U, int R>
+QP_DEV void kq_dot_q5k(const U& B, const float4* xb4, const float* xsb, float (&tot)[R]) {
+    float sxs[8];
+    {
+        const float4 sa = *reinterpret_cast<const float4*>(xsb);
+        const float4 sb = *reinterpret_cast<const float4*>(xsb + 4);
+        sxs[0] = sa.x; sxs[1] = sa.y; sxs[2] = sa.z; sxs[3] = sa.w;
+        sxs[4] = sb.x; sxs[5] = sb.y; sxs[6] = sb.z; sxs[7] = sb.w;
+    }
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        float alo[R], ahi[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) alo[r] = ahi[r] = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float4 x0[4], x1[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                x0[i] = xb4[(2 * p) * 8 + 4 * h + i];
+                x1[i] = xb4[(2 * p + 1) * 8 + 4 * h + i];
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const u32x4 qq = B.c[r][3 + 2 * p + h];
+                const u32x4 hh = B.c[r][1 + h];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t wv = qq[i], g = hh[i] >> (2 * p);  // bytes l .. l+3
+                    const uint32_t tw = wv >> 8;
+                    const uint32_t m0 = (wv & 0x000f000fu) | ((g << 4) & 0x00100010u);
+                    const uint32_t m1 = (wv & 0x00f000f0u) | ((g << 7) & 0x01000100u);
+                    const uint32_t m2 = (tw & 0x000f000fu) | ((g >> 4) & 0x00100010u);
+                    const uint32_t m3 = (tw & 0x00f000f0u) | ((g >> 1) & 0x01000100u);
+                    alo[r] = fmix<0>(m0, x0[i].x, alo[r]);
+                    alo[r] = fmix<0>(m2, x0[i].y, alo[r]);
+                    alo[r] = fmix<1>(m0, x0[i].z, alo[r]);
+                    alo[r] = fmix<1>(m2, x0[i].w, alo[r]);
+                    ahi[r] = fmix<0>(m1, x1[i].x, ahi[r]);
+                    ahi[r] = fmix<0>(m3, x1[i].y, ahi[r]);
+                    ahi[r] = fmix<1>(m1, x1[i].z, ahi[r]);
+                    ahi[r] = fmix<1>(m3, x1[i].w, ahi[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                kq_fence(alo[r]);
+                kq_fence(ahi[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const u32x4 hd = B.c[r][0];
+            const float d = h2f(hd[0] & 0xffffu), dm = h2f(hd[0] >> 16);
+            uint32_t sc0, mn0, sc1, mn1;
+            q4k_sm(hd[1], hd[2], hd[3], 2 * p, sc0, mn0);
+            q4k_sm(hd[1], hd[2], hd[3], 2 * p + 1, sc1, mn1);
             tot[r] += (d * (float)sc0) * (alo[r] * 16777216.0f) - (dm * (float)mn0) * sxs[2 * p];
             tot[r] += (d * (float)sc1) * (ahi[r] * 1048576.0f) - (dm * (float)mn1) * sxs[2 * p + 1];
         }
@@ -735,7 +809,9 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         const bool pair = sg.mode == QP_GEMV_SWIGLU;
         const bool q6 = FMT == QP_KQ_MIX ? sg.fmt == QP_Q6_K : FMT == QP_Q6_K;
         const uint32_t nbw = lay.nbw(nb);
-        const uint64_t tbytes = (uint64_t)sg.rows_total * nbw * (q6 ? 210 : 144);
+        // bytes per weight row (and per tensor row, with the Q6_K d array after the rows)
+        const uint32_t rbw = FMT == QP_KQ_MIX ? (q6 ? 208 : 144) : KQ<FMT>::RB;
+        const uint64_t tbytes = (uint64_t)sg.rows_total * nbw * (q6 ? 210 : rbw);
         const __amdgpu_buffer_rsrc_t rs0 = kq_rsrc(sg.w, tbytes);
         const __amdgpu_buffer_rsrc_t rs1 = kq_rsrc(pair ? sg.w2 : sg.w, tbytes);
 #pragma unroll
@@ -745,13 +821,13 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
             // weight row wr, block wb: chunk c at wr*nbw*rb + c*nbw*16 + wb*16
             uint32_t wr, wb;
             lay.loc(sg.row_base + lr, b, wr, wb);
-            const uint32_t vo = on ? wr * nbw * (q6 ? 208 : 144) + wb * 16 : 0x80000000u;
+            const uint32_t vo = on ? wr * nbw * rbw + wb * 16 : 0x80000000u;
             const __amdgpu_buffer_rsrc_t rs = (pair && r == 1) ? rs1 : rs0;
 #pragma unroll
             for (int c = 0; c < KQ<FMT>::CPB; c++)
                 B.c[r][c] = __builtin_amdgcn_raw_buffer_load_b128(
                     rs, (FMT != QP_KQ_MIX || c < 9 || q6) ? vo : 0x80000000u, c * nbw * 16, 0);
-            if constexpr (FMT != QP_Q4_K)
+            if constexpr (FMT == QP_Q6_K || FMT == QP_KQ_MIX)
                 B.d[r] = __builtin_amdgcn_raw_buffer_load_b16(
                     rs, (on && q6) ? sg.rows_total * nbw * 208 + (wr * nbw + wb) * 2 : 0x80000000u, 0, 0);
         }
@@ -794,7 +870,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
                 if (t < 4) s0 += (v.x + v.y) + (v.z + v.w);
                 else s1 += (v.x + v.y) + (v.z + v.w);
             }
-            if constexpr (FMT == QP_Q4_K) {
+            if constexpr (KQ<FMT>::GROUP == 32) {
                 xsum[q] = s0 + s1;
             } else {
                 xsum[2 * q] = s0;
@@ -854,6 +930,8 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         const KSeg sg = seg_at(si);
         if constexpr (FMT == QP_Q4_K) {
             kq_dot_q4k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
+        } else if constexpr (FMT == QP_Q5_K) {
+            kq_dot_q5k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
         } else if constexpr (FMT == QP_Q6_K) {
             kq_dot_q6k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
         } else {
@@ -1105,10 +1183,14 @@ MOE_KERNELS(q6k, QP_Q6_K)
     KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void qp_gemv_exp_##NAME##_r2x2(     \
         QpGemvExpArgs a) { kq_gemv_exp<FMT, 2, 2>(a); }
 KQ_KERNELS(q4k, QP_Q4_K)
+KQ_KERNELS(q5k, QP_Q5_K)
 KQ_KERNELS(q6k, QP_Q6_K)
 // rows of more than 8192 inputs without the fused norm: 512 threads share one input staging, one sub-block each
 KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void qp_gemv_q4k_r1k2(QpGemvArgs a) {
     kq_gemv_seg<QP_Q4_K, 1, 1, 512, false>(a);
+}
+KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void qp_gemv_q5k_r1k2(QpGemvArgs a) {
+    kq_gemv_seg<QP_Q5_K, 1, 1, 512, false>(a);
 }
 KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void qp_gemv_q6k_r1k2(QpGemvArgs a) {
     kq_gemv_seg<QP_Q6_K, 1, 1, 512, false>(a);
@@ -1515,7 +1597,7 @@ struct MmW8 {
     u32x4 x[4];   // bf16 high (x[0..1]) and low (x[2..3]) of the 16 inputs
     u32x2 q;      // Q4_K: the 8 nibble bytes; Q6_K: the 8 low-bit bytes
     u32x4 h;      // Q4_K: the super-block header (d, dmin, 12 scale bytes)
-    u32x2 qh;     // Q6_K: the 8 high-bit bytes
+    u32x2 qh;     // Q6_K: the 8 high-bit bytes; Q5_K: the 8 qh bytes
     uint32_t sc;  // Q6_K: the dword holding this sub-block's scale byte
     uint32_t d;   // Q6_K: the f16 super-block scale
 };
@@ -1540,6 +1622,12 @@ QP_DEV void mm8_load(MmW8& r, const MmOff& o, __amdgpu_buffer_rsrc_t rx, __amdgp
         const uint32_t j = e0 >> 5;
         r.q = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16 + (1 + 2 * (j >> 1)) * nb * 16, 0);
         r.h = __builtin_amdgcn_raw_buffer_load_b128(rw, o.h, b * 16, 0);
+    } else if constexpr (FMT == QP_Q5_K) {
+        // qs chunk 3 + 2*(j/2) + l/16, qh chunk 1 + l/16 (the same 8 bytes l of both)
+        const uint32_t j = e0 >> 5;
+        r.q = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16 + (3 + 2 * (j >> 1)) * nb * 16, 0);
+        r.qh = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16 + nb * 16, 0);
+        r.h = __builtin_amdgcn_raw_buffer_load_b128(rw, o.h, b * 16, 0);
     } else {
         const uint32_t h = e0 >> 7, qd = (e0 & 127) >> 5;
         r.q = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16 + (h * 4 + (qd & 1) * 2) * nb * 16, 0);
@@ -1554,18 +1642,26 @@ QP_DEV void mm8_deq(const MmW8& r, uint32_t k0, uint32_t sub, float (&w)[8]) {
     const uint32_t e0 = k0 & 255;
     uint32_t v[2];
     float f, c;
-    if constexpr (FMT == QP_Q4_K) {
-        // fd*q - fm; a high nibble is masked in place (16*q) with the scale divided by 16 (exact)
+    if constexpr (FMT == QP_Q4_K || FMT == QP_Q5_K) {
+        // fd*q - fm; a Q4_K high nibble is masked in place (16*q) with the scale divided by 16 (exact); Q5_K
+        // shifts the nibble down and adds 16 * bit j of qh
         const uint32_t j = e0 >> 5, jj = (j & 3) * 8;  // the scale/min unpack of q4k_sm, without a branch
         const uint32_t sa = (r.h.y >> jj) & 0xffu, sb = (r.h.z >> jj) & 0xffu, s8 = (r.h.w >> jj) & 0xffu;
         const uint32_t lo4 = 0u - (uint32_t)(j < 4);  // all ones for j < 4: a blend, not a branch
         const uint32_t sc = ((sa & 63u) & lo4) | (((s8 & 15u) | ((sa >> 6) << 4)) & ~lo4);
         const uint32_t mn = ((sb & 63u) & lo4) | (((s8 >> 4) | ((sb >> 6) << 4)) & ~lo4);
-        const uint32_t mask = (j & 1) ? 0xf0f0f0f0u : 0x0f0f0f0fu;
-        f = h2f(r.h.x & 0xffffu) * (float)sc * ((j & 1) ? 0.0625f : 1.0f);
         c = -(h2f(r.h.x >> 16) * (float)mn);
-        v[0] = r.q.x & mask;
-        v[1] = r.q.y & mask;
+        if constexpr (FMT == QP_Q4_K) {
+            const uint32_t mask = (j & 1) ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+            f = h2f(r.h.x & 0xffffu) * (float)sc * ((j & 1) ? 0.0625f : 1.0f);
+            v[0] = r.q.x & mask;
+            v[1] = r.q.y & mask;
+        } else {
+            const uint32_t ns = (j & 1) * 4;
+            f = h2f(r.h.x & 0xffffu) * (float)sc;
+            v[0] = ((r.q.x >> ns) & 0x0f0f0f0fu) | (((r.qh.x >> j) & 0x01010101u) << 4);
+            v[1] = ((r.q.y >> ns) & 0x0f0f0f0fu) | (((r.qh.y >> j) & 0x01010101u) << 4);
+        }
     } else {
         // fd*(q - 32) = fma(fd, q, -32*fd) exactly (both are one rounding of the same product)
         const uint32_t qd = (e0 & 127) >> 5, sb = ((qd & 1) * 2 + (sub >> 1)) * 8;
@@ -1603,11 +1699,12 @@ QP_DEV void gemm_mfma256_body(const QpGemmArgs& g) {
     const uint32_t xt = t0 + lr < T ? t0 + lr : 0, wr = n0 + wq < N ? n0 + wq : 0;
     const uint32_t nb = K >> 8, xplane = 2 * g.rows * K;
     const __amdgpu_buffer_rsrc_t rx = kq_rsrc(g.xs, 2ull * xplane);
-    const __amdgpu_buffer_rsrc_t rw = kq_rsrc(g.w, (uint64_t)N * nb * (FMT == QP_Q4_K ? 144 : 210));
+    constexpr uint32_t RBW = KQ<FMT>::RB;  // bytes per weight row and 256 inputs (Q6_K: its d array follows)
+    const __amdgpu_buffer_rsrc_t rw = kq_rsrc(g.w, (uint64_t)N * nb * (FMT == QP_Q6_K ? 210 : RBW));
     MmOff off;
     off.x = 2 * (xt * K + 16 * part);
-    off.q = wr * nb * (FMT == QP_Q4_K ? 144 : 208) + (sub >> 1) * nb * 16 + (sub & 1) * 8;
-    off.h = wr * nb * (FMT == QP_Q4_K ? 144 : 208);
+    off.q = wr * nb * RBW + (sub >> 1) * nb * 16 + (sub & 1) * 8;
+    off.h = wr * nb * RBW;
     off.d = N * nb * 208 + wr * nb * 2;
     const uint32_t nsteps = (kend - kbeg + TK - 1) / TK;
     f32x16 acc[2][2];
@@ -1717,6 +1814,7 @@ QP_DEV void gemm_mfma256_body(const QpGemmArgs& g) {
 }
 
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q4k(QpGemmArgs a) { gemm_mfma256_body<QP_Q4_K>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q5k(QpGemmArgs a) { gemm_mfma256_body<QP_Q5_K>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q6k(QpGemmArgs a) { gemm_mfma256_body<QP_Q6_K>(a); }
 
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q4k(QpGemmArgs a) { gemm_mfma_body<QP_Q4_K>(a); }

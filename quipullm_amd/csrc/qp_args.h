@@ -8,6 +8,7 @@
 #define QP_F32 0
 #define QP_Q8_0 8
 #define QP_Q4_K 12
+#define QP_Q5_K 13
 #define QP_Q6_K 14
 
 // Device layouts (private to the ops that read them; produced at load time by the repack ops):
@@ -33,7 +34,7 @@ typedef struct {
     uint64_t w;     // weights (device layout of fmt)
     uint64_t w2;    // second matrix (QP_GEMV_SWIGLU: the up projection; same fmt and shape)
     uint64_t y;     // output floats
-    uint32_t fmt;   // QP_F32 / QP_Q8_0 / QP_Q4_K / QP_Q6_K
+    uint32_t fmt;   // QP_F32 / QP_Q8_0 / QP_Q4_K / QP_Q5_K / QP_Q6_K
     uint32_t n;     // output rows of this segment
     uint32_t wg0;   // first workgroup of this segment
     uint32_t mode;  // QP_GEMV_*

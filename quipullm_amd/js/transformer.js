@@ -14,8 +14,9 @@ const { despachar, dim2, vista } = require('./gpu');
 const { CargadorPesos } = require('./weights');
 
 const ROPE_NEOX = new Set(['qwen2', 'qwen3', 'qwen3moe', 'phi3', 'gemma', 'gemma2', 'gemma3', 'stablelm', 'olmo2']);
-const KQ = new Set(['q4k', 'q6k']);
-const FMT_ID = { f32: 0, q8: 8, q4k: 12, q6k: 14 };
+const KQ = new Set(['q4k', 'q5k', 'q6k']);
+const MEZCLA = new Set(['q4k', 'q6k']);    // formats whose GEMV segments may share one launch
+const FMT_ID = { f32: 0, q8: 8, q4k: 12, q5k: 13, q6k: 14 };
 // gemv segment modes (qp_args.h)
 const STORE = 0, ACC = 1, SWIGLU = 2, ARGMAX = 3;
 const AMAX_WG = 512;   // workgroups of the fused output GEMV = partial maxima for the device argmax
@@ -332,7 +333,7 @@ class ModeloTransformer {
     const b = [this.bPaso, x, norm || null, opts.amax || null];
     for (const s of segs) {
       const f = FMT_ID[s.W.tipo];
-      if (f !== fmt && !(KQ.has(s.W.tipo) && KQ.has(segs[0].W.tipo))) throw new Error('gemv segments must share one format');
+      if (f !== fmt && !(MEZCLA.has(s.W.tipo) && MEZCLA.has(segs[0].W.tipo))) throw new Error('gemv segments must share one format');
       u.push(['u', s.mode | ((f !== fmt ? f : 0) << 8)], ['u', s.W.N], ['u', 0], ['u', s.W.N]);
       b.push(s.W.w, s.W2 ? s.W2.w : null, s.y);
     }
@@ -344,7 +345,7 @@ class ModeloTransformer {
   _gemvPorFormato(segs, x, norm, K) {
     const porFmt = new Map();
     for (const s of segs) {
-      const clave = KQ.has(s.W.tipo) ? 'kq' : s.W.tipo;
+      const clave = MEZCLA.has(s.W.tipo) ? 'kq' : s.W.tipo;
       if (!porFmt.has(clave)) porFmt.set(clave, []);
       porFmt.get(clave).push(s);
     }

@@ -3,12 +3,12 @@
 //
 // Same interface as quipullm's CargadorPesos (web/js/weights.js:15-139): existe(name), info(name),
 // f32(name) -> buffer, matriz(name) -> {tipo, N, K, w} ({tipo:'q8', N, K, qs, ds} for Q8_0).  The device
-// layout behind a handle is this backend's own: Q4_K blocks unchanged; Q6_K and Q8_0 repacked on the device
+// layout behind a handle is this backend's own: Q4_K, Q5_K and Q6_K blocks and Q8_0 repacked on the device
 // into planar arrays (quants | scales) so every lane load is a 16-byte vector load.
 const fs = require('fs');
 const { despachar, vista } = require('./gpu');
 
-const K_QUANTS = { 12: { nombre: 'q4k', bytes: 144 }, 14: { nombre: 'q6k', bytes: 210 } };
+const K_QUANTS = { 12: { nombre: 'q4k', bytes: 144 }, 13: { nombre: 'q5k', bytes: 176 }, 14: { nombre: 'q6k', bytes: 210 } };
 
 const F16 = (function () {
   const t = new Float32Array(65536);
@@ -87,7 +87,7 @@ class CargadorPesos {
     return b;
   }
 
-  // Raw blocks -> device layout, repacked on the device (Q4_K / Q6_K row chunk planes, Q8_0 planar).
+  // Raw blocks -> device layout, repacked on the device (Q4_K / Q5_K / Q6_K row chunk planes, Q8_0 planar).
   _subirRepack(u8, op, nblocks, K, etiqueta) {
     const gpu = this.gpu;
     const staging = gpu.subir(u8, etiqueta + '.raw');
@@ -121,7 +121,7 @@ class CargadorPesos {
       const w = this.f32(nombre);
       return { tipo: 'f32', N: N, K: K, w: w };
     }
-    throw new Error(nombre + ': quantization ' + t.tipo_nombre + ' not supported yet (supported: Q4_K, Q6_K, Q8_0, F16, BF16, F32)');
+    throw new Error(nombre + ': quantization ' + t.tipo_nombre + ' not supported yet (supported: Q4_K, Q5_K, Q6_K, Q8_0, F16, BF16, F32)');
   }
 }
 

@@ -7,12 +7,13 @@ the configurations specify, so no quantizer is needed:
 * Q8_0 (34 B blocks): int8 quants uniform in [-127, 127]; f16 scale |N(0, 0.02)| / 127.
 * Q4_K (144 B): d and dmin f16 |N(0, 0.01)|; the 12 packed bytes of 6-bit scales/mins uniform (every byte
   pattern decodes to 6-bit values, each uniform on 0..63); 4-bit quants uniform 0..15.
+* Q5_K (176 B): the Q4_K header distributions; qh and qs bytes uniform (5-bit quants uniform 0..31).
 * Q6_K (210 B): 6-bit quants uniform 0..63 (ql/qh bytes uniform); int8 sub-scales uniform in [-64, 63];
   d f16 |N(0, 0.01)|.
 * F32 vectors (norms, f32 embeddings): N(1, 0.02); the f32 MoE router: N(0, 0.02).
 
 Test variants marked `centered` make the weights zero-mean, so that greedy decoding does not collapse onto
-one token: Q4_K blocks get mins equal to their scales and dmin = f16(7.5 d) (the mean nibble is 7.5), and
+one token: Q4_K blocks get mins equal to their scales and dmin = f16(7.5 d) (the mean nibble is 7.5; Q5_K: 15.5), and
 f32 embeddings are N(0, 1).
 
 Every tensor draws from its own generator seeded by (seed, tensor index), so a tensor's bytes do not depend on
@@ -26,8 +27,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-GGML_F32, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 8, 12, 14
-BLOCK = {GGML_F32: (1, 4), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210)}
+GGML_F32, GGML_Q8_0, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 0, 8, 12, 13, 14
+BLOCK = {GGML_F32: (1, 4), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q5_K: (256, 176), GGML_Q6_K: (256, 210)}
 ALIGN = 32
 
 # GGUF metadata value types
@@ -57,6 +58,11 @@ class ModelConfig:
 
     def tensor_type(self, kind: str) -> int:
         return self.fmt.get(kind, self.fmt.get("default", GGML_Q4_K))
+
+
+def _q5km():
+    """Q5_K_M: Q5_K for most tensors, Q6_K for attn_v, ffn_down and output."""
+    return {"default": GGML_Q5_K, "attn_v": GGML_Q6_K, "ffn_down": GGML_Q6_K, "output": GGML_Q6_K}
 
 
 def _q4km(**kw):
@@ -93,6 +99,11 @@ CONFIGS = {
                                    {"default": GGML_Q8_0, "token_embd": GGML_F32}, ctx=256, centered=True),
     "mini_qwen3_q4km_c": ModelConfig("mini_qwen3_q4km_c", "qwen3", 2, 512, 8, 2, 128, 768, 1000, 1e-6, 1000000.0,
                                      _q4km(), qk_norm=True, ctx=512, centered=True),
+    "mini_llama_q5km_c": ModelConfig("mini_llama_q5km_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
+                                     _q5km(), ctx=512, centered=True),
+    "mini_qwen3moe_q5k_c": ModelConfig("mini_qwen3moe_q5k_c", "qwen3moe", 2, 512, 8, 2, 128, 0, 1000, 1e-6,
+                                       1000000.0, {"default": GGML_Q5_K}, n_exp=16, n_used=4, ffe=256,
+                                       qk_norm=True, ctx=512, centered=True),
     "mini_qwen3moe_q4k_c": ModelConfig("mini_qwen3moe_q4k_c", "qwen3moe", 2, 512, 8, 2, 128, 0, 1000, 1e-6,
                                        1000000.0, {"default": GGML_Q4_K}, n_exp=16, n_used=4, ffe=256,
                                        qk_norm=True, ctx=512, centered=True),
@@ -170,12 +181,13 @@ def gen_blocks(rng, gtype, nelem, kind="w", centered=False):
         blk[:, 2:34] = q.view(np.uint8)
         return blk.tobytes()
     blk = np.frombuffer(rng.bytes(nb * bpb), np.uint8).reshape(nb, bpb).copy()
-    if gtype == GGML_Q4_K:
+    if gtype in (GGML_Q4_K, GGML_Q5_K):
         d = _abs_normal_f16(rng, nb, 0.01)
         blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         if centered:
+            mean = np.float32(7.5 if gtype == GGML_Q4_K else 15.5)
             sc = rng.integers(0, 64, size=(nb, 8), dtype=np.uint8)
-            blk[:, 2:4] = (d.astype(np.float32) * np.float32(7.5)).astype(np.float16).view(np.uint8).reshape(nb, 2)
+            blk[:, 2:4] = (d.astype(np.float32) * mean).astype(np.float16).view(np.uint8).reshape(nb, 2)
             blk[:, 4:16] = pack_q4k_scales(sc, sc)
         else:
             blk[:, 2:4] = _abs_normal_f16(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)

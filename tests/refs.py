@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import numpy as np
 
-F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
+F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
 
 
 # ------------------------------------------------------------------------------------------------ dequant
@@ -42,6 +42,32 @@ def dequant_q4k(raw: np.ndarray) -> np.ndarray:
         mm2 = (dmin * m2.astype(np.float32)).astype(np.float32)
         out[:, half * 64:half * 64 + 32] = (d1[:, None] * (q & 0xF).astype(np.float32)) - mm1[:, None]
         out[:, half * 64 + 32:half * 64 + 64] = (d2[:, None] * (q >> 4).astype(np.float32)) - mm2[:, None]
+    return out.reshape(-1)
+
+
+def dequant_q5k(raw: np.ndarray) -> np.ndarray:
+    """ggml's dequantize_row_q5_K, vectorized: the Q4_K scheme with a fifth bit per element taken from qh, bit
+    2h (low nibbles) / 2h+1 (high nibbles) for the h-th 64-element step."""
+    b = raw.reshape(-1, 176)
+    nb = b.shape[0]
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(nb)
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float32).reshape(nb)
+    s = b[:, 4:16].astype(np.uint32)
+    qh = b[:, 16:48].astype(np.uint32)
+    qs = b[:, 48:176]
+    out = np.empty((nb, 256), np.float32)
+    for half in range(4):
+        q = qs[:, half * 32:(half + 1) * 32].astype(np.uint32)
+        sc1, m1 = _scale_min_k4(s, 2 * half)
+        sc2, m2 = _scale_min_k4(s, 2 * half + 1)
+        d1 = (d * sc1.astype(np.float32)).astype(np.float32)
+        mm1 = (dmin * m1.astype(np.float32)).astype(np.float32)
+        d2 = (d * sc2.astype(np.float32)).astype(np.float32)
+        mm2 = (dmin * m2.astype(np.float32)).astype(np.float32)
+        lo = (q & 0xF) + 16 * ((qh >> (2 * half)) & 1)
+        hi = (q >> 4) + 16 * ((qh >> (2 * half + 1)) & 1)
+        out[:, half * 64:half * 64 + 32] = (d1[:, None] * lo.astype(np.float32)) - mm1[:, None]
+        out[:, half * 64 + 32:half * 64 + 64] = (d2[:, None] * hi.astype(np.float32)) - mm2[:, None]
     return out.reshape(-1)
 
 
@@ -77,6 +103,8 @@ def dequant(fmt, raw):
     raw = np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray)) else np.asarray(raw, np.uint8)
     if fmt == Q4_K:
         return dequant_q4k(raw)
+    if fmt == Q5_K:
+        return dequant_q5k(raw)
     if fmt == Q6_K:
         return dequant_q6k(raw)
     if fmt == Q8_0:

@@ -15,7 +15,7 @@ from quipullm_amd import capi, synth
 
 pytestmark = pytest.mark.gpu
 
-FMTS = [capi.Q4_K, capi.Q6_K, capi.Q8_0, capi.F32]
+FMTS = [capi.Q4_K, capi.Q5_K, capi.Q6_K, capi.Q8_0, capi.F32]
 
 
 def raw_matrix(fmt, N, K, seed, centered=False):

@@ -48,10 +48,10 @@ def test_header_declares_the_facade():
 
 
 # every op name the JavaScript host dispatches (transformer.js, weights.js) and the tests use
-OPS = ["matmul_%s_%s" % (f, s) for f in ("q4k", "q6k", "q8", "f32") for s in ("1", "4", "t", "e", "e_swiglu")] + \
-      ["embed_%s" % f for f in ("q4k", "q6k", "q8", "f32")] + \
+OPS = ["matmul_%s_%s" % (f, s) for f in ("q4k", "q5k", "q6k", "q8", "f32") for s in ("1", "4", "t", "e", "e_swiglu")] + \
+      ["embed_%s" % f for f in ("q4k", "q5k", "q6k", "q8", "f32")] + \
       ["rmsnorm", "norm_rope", "kv_write", "atencion", "swiglu", "moe_topk", "moe_comb", "gemv", "dec_attn",
-       "dec_attn_comb", "argmax", "argmax_fin", "repack_q4k", "repack_q6k", "repack_q8", "fill_u32", "dequant",
+       "dec_attn_comb", "argmax", "argmax_fin", "repack_q4k", "repack_q5k", "repack_q6k", "repack_q8", "fill_u32", "dequant",
        "copy_f4", "read_f4", "moe_gate_up_q4k", "moe_gate_up_q6k", "moe_down_q4k", "moe_down_q6k", "penalizar",
        "topk_cand"]
 
@@ -60,7 +60,7 @@ def test_op_table(built):
     lib = capi.load_library()
     ids = [lib.qp_op_id(n.encode()) for n in OPS]
     assert min(ids) >= 0 and len(set(ids)) == len(ids)
-    assert lib.qp_op_id(b"matmul_q5k_1") == -1 and lib.qp_op_id(b"") == -1 and lib.qp_op_id(None) == -1
+    assert lib.qp_op_id(b"matmul_q3k_1") == -1 and lib.qp_op_id(b"") == -1 and lib.qp_op_id(None) == -1
 
 
 def test_ops_used_by_the_js_host_exist(built):

@@ -40,7 +40,8 @@ def test_f16_rounding_matches_numpy(oracle):
     assert oracle.f16_from(float("nan")) & 0x7c00 == 0x7c00 and oracle.f16_from(float("nan")) & 0x3ff
 
 
-@pytest.mark.parametrize("fmt,n", [(refs.Q4_K, 256 * 300), (refs.Q6_K, 256 * 300), (refs.Q8_0, 32 * 500)])
+@pytest.mark.parametrize("fmt,n", [(refs.Q4_K, 256 * 300), (refs.Q5_K, 256 * 300), (refs.Q6_K, 256 * 300),
+                                   (refs.Q8_0, 32 * 500)])
 @pytest.mark.parametrize("centered", [False, True])
 def test_dequant_bit_exact_vs_ggml_spec(oracle, fmt, n, centered):
     raw = blocks(fmt, n, 1, centered)
@@ -64,6 +65,26 @@ def test_q4k_known_answer(oracle):
     got = oracle.dequant(refs.Q4_K, b, 256)
     j = np.arange(256) // 32
     np.testing.assert_array_equal(got, (j + 1) * q - 0.5 * j)
+
+
+def test_q5k_known_answer(oracle):
+    # the Q4_K case above with a fifth bit: h = 1 for elements e with (e // 3) odd, so q5 = e % 16 + 16 h and the
+    # value is (j + 1) * q5 - 0.5 j; bit j of qh[l] holds h of element 32 j + l
+    sc = np.arange(1, 9, dtype=np.uint8)[None]
+    mn = np.arange(0, 8, dtype=np.uint8)[None]
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.array([1.0], np.float16).view(np.uint8)
+    b[2:4] = np.array([0.5], np.float16).view(np.uint8)
+    b[4:16] = synth.pack_q4k_scales(sc, mn)[0]
+    e = np.arange(256)
+    q, h, j, l = e % 16, (e // 3) % 2, e // 32, e % 32
+    for i in range(256):
+        b[16 + l[i]] |= h[i] << j[i]
+    for g in range(4):
+        lo, hi = q[g * 64:g * 64 + 32], q[g * 64 + 32:g * 64 + 64]
+        b[48 + g * 32:48 + g * 32 + 32] = (lo | (hi << 4)).astype(np.uint8)
+    got = oracle.dequant(refs.Q5_K, b, 256)
+    np.testing.assert_array_equal(got, (j + 1) * (q + 16 * h) - 0.5 * j)
 
 
 def test_q6k_known_answer(oracle):
@@ -91,8 +112,8 @@ def test_q8_known_answer(oracle):
 
 
 # ------------------------------------------------------------------------------------------------ matmul
-@pytest.mark.parametrize("fmt,N,K", [(refs.Q4_K, 33, 512), (refs.Q6_K, 17, 768), (refs.Q8_0, 19, 320),
-                                     (refs.F32, 9, 96)])
+@pytest.mark.parametrize("fmt,N,K", [(refs.Q4_K, 33, 512), (refs.Q5_K, 21, 512), (refs.Q6_K, 17, 768),
+                                     (refs.Q8_0, 19, 320), (refs.F32, 9, 96)])
 @pytest.mark.parametrize("T,mode", [(1, 0), (3, 0), (9, 1)])
 def test_matmul_vs_float64(oracle, fmt, N, K, T, mode):
     rng = np.random.default_rng(5)
@@ -228,7 +249,8 @@ def test_argmax_ties_nan(oracle):
 
 
 # ------------------------------------------------------------------------------------------------ model
-@pytest.mark.parametrize("name,neox", [("mini_llama_q4km_c", 0), ("mini_qwen3_q4km_c", 1), ("mini_qwen3moe_q4k_c", 1),
+@pytest.mark.parametrize("name,neox", [("mini_llama_q4km_c", 0), ("mini_llama_q5km_c", 0), ("mini_qwen3_q4km_c", 1),
+                                       ("mini_qwen3moe_q5k_c", 1), ("mini_qwen3moe_q4k_c", 1),
                                        ("mini_llama_q8_c", 0)])
 def test_model_forward_vs_float64(oracle, models_dir, name, neox):
     # float32 rounding, amplified by near-ties of the large activations of the centered models, stays below these
