@@ -10,7 +10,8 @@
  * -ffp-contract=off so that no multiply-add is fused: the reference's dequant formula is defined as the
  * non-fused f32 sequence.
  *
- * Raw weight blocks are the GGUF/ggml layouts (Q4_K 144 B, Q5_K 176 B, Q6_K 210 B, Q8_0 34 B), unpadded.
+ * Raw weight blocks are the GGUF/ggml layouts (Q2_K 84 B, Q3_K 110 B, Q4_K 144 B, Q5_K 176 B, Q6_K 210 B,
+ * Q8_0 34 B), unpadded.
  */
 #include <math.h>
 #include <stdint.h>
@@ -22,6 +23,8 @@
 
 #define OR_F32 0
 #define OR_Q8_0 8
+#define OR_Q2_K 10
+#define OR_Q3_K 11
 #define OR_Q4_K 12
 #define OR_Q5_K 13
 #define OR_Q6_K 14
@@ -120,6 +123,41 @@ static inline float q5k_deq(const uint8_t* blk, int e) {
     return a - fm;
 }
 
+/* ------------------------------------------------------------------ Q3_K
+ * Block: hmask[32], qs[64], scales[12], d f16 (kquants.js:10).  scq3: kquants.js:78-90 (6-bit scale of group s,
+ * minus 32, times d).  Element dequant: kquants.js:159-162 (scq3(s) * (q2 - 4 * (1 - hmask bit))). */
+static inline float q3k_scale(const uint8_t* blk, int s) {
+    uint32_t a0 = rd32(blk + 96), a1 = rd32(blk + 100), tmp = rd32(blk + 104);
+    uint32_t k1 = 0x03030303u, k2 = 0x0f0f0f0fu, wd;
+    int g = s >> 2;
+    if (g == 0) wd = (a0 & k2) | (((tmp >> 0) & k1) << 4);
+    else if (g == 1) wd = (a1 & k2) | (((tmp >> 2) & k1) << 4);
+    else if (g == 2) wd = ((a0 >> 4) & k2) | (((tmp >> 4) & k1) << 4);
+    else wd = ((a1 >> 4) & k2) | (((tmp >> 6) & k1) << 4);
+    float sc = (float)((wd >> ((s & 3) * 8)) & 0xffu) - 32.0f;
+    return or_f16(rd16(blk + 108)) * sc;
+}
+
+static inline float q3k_deq(const uint8_t* blk, int e) {
+    int s = e >> 4, n = e >> 7, r = e & 127, jj = r >> 5, l = r & 31;
+    unsigned q2 = (blk[32 + n * 32 + l] >> (jj * 2)) & 3u;
+    unsigned hm = (blk[l] >> (n * 4 + jj)) & 1u;
+    return q3k_scale(blk, s) * ((float)q2 - 4.0f * (float)(1u - hm));
+}
+
+/* ------------------------------------------------------------------ Q2_K
+ * Block: scales[16] (low nibble scale, high nibble min), qs[64], d f16, dmin f16 (kquants.js:11).  Setup:
+ * kquants.js:108-116 (fd = d * (sc & 15), fm = dmin * (sc >> 4)); element = fd * q - fm (ggml's
+ * dequantize_row_q2_K; the reference has no single-element form for Q2_K). */
+static inline float q2k_deq(const uint8_t* blk, int e) {
+    int j = e >> 4, n = e >> 7, jj = (e & 127) >> 5, l = e & 31;
+    unsigned sc = blk[j];
+    float fd = or_f16(rd16(blk + 80)) * (float)(sc & 15u), fm = or_f16(rd16(blk + 82)) * (float)(sc >> 4);
+    unsigned q = (blk[16 + n * 32 + l] >> (jj * 2)) & 3u;
+    float a = fd * (float)q;
+    return a - fm;
+}
+
 /* ------------------------------------------------------------------ Q6_K
  * Block: ql[128], qh[64], scales[16] int8, d f16 (kquants.js:9).  scq6: kquants.js:92-96.
  * Element dequant: kquants.js:172-175 (scq6(s) * (q - 32)). */
@@ -149,6 +187,10 @@ void or_dequant(int fmt, const uint8_t* raw, int64_t nelem, float* out) {
         for (i = 0; i < nelem; i++) out[i] = q4k_deq(raw + (i >> 8) * 144, (int)(i & 255));
     } else if (fmt == OR_Q5_K) {
         for (i = 0; i < nelem; i++) out[i] = q5k_deq(raw + (i >> 8) * 176, (int)(i & 255));
+    } else if (fmt == OR_Q3_K) {
+        for (i = 0; i < nelem; i++) out[i] = q3k_deq(raw + (i >> 8) * 110, (int)(i & 255));
+    } else if (fmt == OR_Q2_K) {
+        for (i = 0; i < nelem; i++) out[i] = q2k_deq(raw + (i >> 8) * 84, (int)(i & 255));
     } else if (fmt == OR_Q6_K) {
         for (i = 0; i < nelem; i++) out[i] = q6k_deq(raw + (i >> 8) * 210, (int)(i & 255));
     } else if (fmt == OR_Q8_0) {
@@ -217,6 +259,60 @@ static float row_q5k(const uint8_t* row, int K, const float* x) {
                 float q[4];
                 for (int t = 0; t < 4; t++)
                     q[t] = (float)((w >> (sh + 8 * t)) & 15u) + 16.0f * (float)((h >> (8 * t + j)) & 1u);
+                s = s + dot4(q, xb + wi * 4);
+                m = m + sum4(xb + wi * 4);
+            }
+            a = a + (fd * s - fm * m);
+        }
+        lanes[lane] = a;
+    }
+    return tree32(lanes);
+}
+
+/* Q3_K / Q2_K: the 16-element items of kquants.js:188-251 with the q3k / q2k setup and q (kquants.js:106-116,
+ * 140-148): item j of block b covers elements 128 n + 32 jj + l0 .. + 15 (n = j >> 3, jj = (j & 7) >> 1,
+ * l0 = 16 (j & 1)). */
+static float row_q3k(const uint8_t* row, int K, const float* x) {
+    int nb = K / 256, ni = nb * 16;
+    float lanes[32];
+    for (int lane = 0; lane < 32; lane++) {
+        float a = 0.0f;
+        for (int it = lane; it < ni; it += 32) {
+            int b = it / 16, j = it % 16, n = j >> 3, jj = (j & 7) >> 1, l0 = (j & 1) * 16;
+            const uint8_t* blk = row + (size_t)b * 110;
+            float fd = q3k_scale(blk, j);
+            const float* xb = x + b * 256 + n * 128 + jj * 32 + l0;
+            float s = 0.0f;
+            for (int wi = 0; wi < 4; wi++) {
+                uint32_t w = rd32(blk + 32 + n * 32 + l0 + wi * 4), h = rd32(blk + l0 + wi * 4);
+                float q[4];
+                for (int t = 0; t < 4; t++)
+                    q[t] = (float)(((w >> (8 * t + 2 * jj)) & 3u) + 4u * ((h >> (8 * t + n * 4 + jj)) & 1u)) - 4.0f;
+                s = s + dot4(q, xb + wi * 4);
+            }
+            a = a + fd * s;
+        }
+        lanes[lane] = a;
+    }
+    return tree32(lanes);
+}
+
+static float row_q2k(const uint8_t* row, int K, const float* x) {
+    int nb = K / 256, ni = nb * 16;
+    float lanes[32];
+    for (int lane = 0; lane < 32; lane++) {
+        float a = 0.0f;
+        for (int it = lane; it < ni; it += 32) {
+            int b = it / 16, j = it % 16, n = j >> 3, jj = (j & 7) >> 1, l0 = (j & 1) * 16;
+            const uint8_t* blk = row + (size_t)b * 84;
+            unsigned sc = blk[j];
+            float fd = or_f16(rd16(blk + 80)) * (float)(sc & 15u), fm = or_f16(rd16(blk + 82)) * (float)(sc >> 4);
+            const float* xb = x + b * 256 + n * 128 + jj * 32 + l0;
+            float s = 0.0f, m = 0.0f;
+            for (int wi = 0; wi < 4; wi++) {
+                uint32_t w = rd32(blk + 16 + n * 32 + l0 + wi * 4);
+                float q[4];
+                for (int t = 0; t < 4; t++) q[t] = (float)((w >> (8 * t + 2 * jj)) & 3u);
                 s = s + dot4(q, xb + wi * 4);
                 m = m + sum4(xb + wi * 4);
             }
@@ -296,6 +392,8 @@ static size_t row_bytes(int fmt, int K) {
     switch (fmt) {
     case OR_Q4_K: return (size_t)(K / 256) * 144;
     case OR_Q5_K: return (size_t)(K / 256) * 176;
+    case OR_Q3_K: return (size_t)(K / 256) * 110;
+    case OR_Q2_K: return (size_t)(K / 256) * 84;
     case OR_Q6_K: return (size_t)(K / 256) * 210;
     case OR_Q8_0: return (size_t)(K / 32) * 34;
     default: return (size_t)K * 4;
@@ -306,6 +404,8 @@ static float row_dot(int fmt, const uint8_t* row, int K, const float* x) {
     switch (fmt) {
     case OR_Q4_K: return row_q4k(row, K, x);
     case OR_Q5_K: return row_q5k(row, K, x);
+    case OR_Q3_K: return row_q3k(row, K, x);
+    case OR_Q2_K: return row_q2k(row, K, x);
     case OR_Q6_K: return row_q6k(row, K, x);
     case OR_Q8_0: return row_q8(row, K, x);
     default: return row_f32((const float*)row, K, x);
@@ -320,6 +420,8 @@ static float row_serial(int fmt, const uint8_t* row, int K, const float* x) {
         float w;
         if (fmt == OR_Q4_K) w = q4k_deq(row + (size_t)(k >> 8) * 144, k & 255);
         else if (fmt == OR_Q5_K) w = q5k_deq(row + (size_t)(k >> 8) * 176, k & 255);
+        else if (fmt == OR_Q3_K) w = q3k_deq(row + (size_t)(k >> 8) * 110, k & 255);
+        else if (fmt == OR_Q2_K) w = q2k_deq(row + (size_t)(k >> 8) * 84, k & 255);
         else if (fmt == OR_Q6_K) w = q6k_deq(row + (size_t)(k >> 8) * 210, k & 255);
         else if (fmt == OR_Q8_0) w = q8_deq(row + (size_t)(k >> 5) * 34, k & 31);
         else w = ((const float*)row)[k];
@@ -371,6 +473,8 @@ void or_embed(int fmt, const uint8_t* W, int D, const uint32_t* ids, int T, floa
             float v;
             if (fmt == OR_Q4_K) v = q4k_deq(row + (size_t)(k >> 8) * 144, k & 255);
             else if (fmt == OR_Q5_K) v = q5k_deq(row + (size_t)(k >> 8) * 176, k & 255);
+            else if (fmt == OR_Q3_K) v = q3k_deq(row + (size_t)(k >> 8) * 110, k & 255);
+            else if (fmt == OR_Q2_K) v = q2k_deq(row + (size_t)(k >> 8) * 84, k & 255);
             else if (fmt == OR_Q6_K) v = q6k_deq(row + (size_t)(k >> 8) * 210, k & 255);
             else if (fmt == OR_Q8_0) v = q8_deq(row + (size_t)(k >> 5) * 34, k & 31);
             else v = ((const float*)row)[k];
@@ -641,7 +745,7 @@ size_t or_layer_sizeof(void) { return sizeof(OrLayer); }
 
 /* mm() of transformer.js:268-284: one token -> lane order; T >= 8 with a K-quant and tiling on -> tiled. */
 static void mm(const OrModel* m, int fmt, const uint8_t* W, int N, int K, const float* x, int T, float* y, int acc) {
-    int kq = fmt == OR_Q4_K || fmt == OR_Q5_K || fmt == OR_Q6_K;
+    int kq = fmt == OR_Q2_K || fmt == OR_Q3_K || fmt == OR_Q4_K || fmt == OR_Q5_K || fmt == OR_Q6_K;
     int mode = (T >= 8 && kq && m->tiled) ? 1 : 0;
     or_matmul(fmt, W, N, K, x, T, y, acc, mode);
 }

@@ -18,9 +18,10 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "lib", "libquipu.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "quipu.h")
 
-F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
-BLOCK = {F32: (1, 4), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
-FMT_NAME = {F32: "f32", Q8_0: "q8", Q4_K: "q4k", Q5_K: "q5k", Q6_K: "q6k"}
+F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 8, 10, 11, 12, 13, 14
+BLOCK = {F32: (1, 4), Q8_0: (32, 34), Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176),
+         Q6_K: (256, 210)}
+FMT_NAME = {F32: "f32", Q8_0: "q8", Q2_K: "q2k", Q3_K: "q3k", Q4_K: "q4k", Q5_K: "q5k", Q6_K: "q6k"}
 
 # gemv segment modes (qp_args.h)
 STORE, ACC, SWIGLU, ARGMAX = 0, 1, 2, 3
@@ -94,9 +95,15 @@ def dim2(n):
     return (math.ceil(n / y), y)
 
 
-def device_bytes(fmt, N, K):
+def gguf_bytes(fmt, N, K):
+    """Packed bytes of an N x K matrix in the GGUF block format (the algorithmic bytes of one pass over it)."""
     epb, bpb = BLOCK[fmt]
     return N * K // epb * bpb
+
+
+def device_bytes(fmt, N, K):
+    """Bytes of the device tensor: the GGUF size, except Q3_K blocks padded to 112 bytes."""
+    return N * K // 256 * 112 if fmt == Q3_K else gguf_bytes(fmt, N, K)
 
 
 class Quipu:
@@ -176,14 +183,14 @@ class Quipu:
         """GGUF blocks of an N x K matrix -> device tensor in this backend's layout (repacked on the device: Q4_K,
         Q5_K and Q6_K to row chunk planes, Q8_0 to planar qs | d).  Returns the handle."""
         raw = np.ascontiguousarray(np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray)) else raw)
-        nbytes = device_bytes(fmt, N, K)
-        assert raw.nbytes == nbytes, (raw.nbytes, nbytes)
+        assert raw.nbytes == gguf_bytes(fmt, N, K), (raw.nbytes, gguf_bytes(fmt, N, K))
         if fmt == F32:
             return self.buffer_from(raw)
         staging = self.buffer_from(raw)
-        dst = self.alloc(nbytes)
+        dst = self.alloc(device_bytes(fmt, N, K))
         nb = N * K // BLOCK[fmt][0]
-        op = {Q4_K: "repack_q4k", Q5_K: "repack_q5k", Q6_K: "repack_q6k", Q8_0: "repack_q8"}[fmt]
+        op = {Q2_K: "repack_q2k", Q3_K: "repack_q3k", Q4_K: "repack_q4k", Q5_K: "repack_q5k", Q6_K: "repack_q6k",
+              Q8_0: "repack_q8"}[fmt]
         self.dispatch(op, [("u", nb & 0xFFFFFFFF), ("u", nb >> 32), ("u", K)], [0, staging, dst])
         self.sync()
         self.free(staging)

@@ -172,17 +172,60 @@ QP_DEV float deq_q5k_dev(const uint8_t* base, uint32_t nb, uint64_t row, uint32_
     return a - fm;
 }
 
+// Q3_K (reference kquants.js:10, scq3 at 78-90, deq at 159-162), padded to 112 bytes (7 chunks): hmask[32] at
+// 0..31, qs[64] at 32..95, 12 scale bytes at 96..107, d f16 at 108.  Element e = 128 n + 32 jj + l of scale group
+// s = e / 16: (d * (s6 - 32)) * (q2 - 4 * (1 - bit (4n + jj) of hmask[l])), q2 = (qs[32 n + l] >> 2 jj) & 3.
+QP_DEV uint32_t q3k_scale6(uint32_t a0, uint32_t a1, uint32_t tmp, uint32_t s) {
+    const uint32_t k1 = 0x03030303u, k2 = 0x0f0f0f0fu, g = s >> 2;
+    const uint32_t wd = g == 0 ? (a0 & k2) | ((tmp & k1) << 4)
+                      : g == 1 ? (a1 & k2) | (((tmp >> 2) & k1) << 4)
+                      : g == 2 ? ((a0 >> 4) & k2) | (((tmp >> 4) & k1) << 4)
+                               : ((a1 >> 4) & k2) | (((tmp >> 6) & k1) << 4);
+    return (wd >> ((s & 3) * 8)) & 0xffu;
+}
+QP_DEV float deq_q3k_dev(const uint8_t* base, uint32_t nb, uint64_t row, uint32_t b, uint32_t e) {
+#pragma clang fp contract(off)
+    const uint32_t s = e >> 4, n = e >> 7, r = e & 127, jj = r >> 5, l = r & 31;
+    uint32_t w[3];
+    for (int i = 0; i < 3; i++)
+        w[i] = kq_byte<112>(base, nb, row, b, 96 + 4 * i) | (kq_byte<112>(base, nb, row, b, 97 + 4 * i) << 8) |
+               (kq_byte<112>(base, nb, row, b, 98 + 4 * i) << 16) | (kq_byte<112>(base, nb, row, b, 99 + 4 * i) << 24);
+    const float d = h2f(kq_byte<112>(base, nb, row, b, 108) | (kq_byte<112>(base, nb, row, b, 109) << 8));
+    const float fd = d * ((float)q3k_scale6(w[0], w[1], w[2], s) - 32.0f);
+    const uint32_t q2 = (kq_byte<112>(base, nb, row, b, 32 + n * 32 + l) >> (jj * 2)) & 3u;
+    const uint32_t hm = (kq_byte<112>(base, nb, row, b, l) >> (n * 4 + jj)) & 1u;
+    return fd * ((float)q2 - 4.0f * (float)(1u - hm));
+}
+
+// Q2_K (reference kquants.js:11, setup at 108-116): 16 scale bytes (low nibble scale, high nibble min) at 0..15,
+// qs[64] at 16..79 in 5 chunks per block; d and dmin (f16 each) in an array of 4 bytes per block after the rows.
+// Element e = 128 n + 32 jj + l of group j = e / 16: (d * (sc_j & 15)) * q - dmin * (sc_j >> 4),
+// q = (qs[32 n + l] >> 2 jj) & 3.
+QP_DEV float deq_q2k_dev(const uint8_t* base, uint32_t nb, uint64_t NB, uint64_t row, uint32_t b, uint32_t e) {
+#pragma clang fp contract(off)
+    const uint32_t j = e >> 4, n = e >> 7, jj = (e & 127) >> 5, l = e & 31;
+    const uint32_t sc = kq_byte<80>(base, nb, row, b, j);
+    const uint8_t* dp = base + NB * 80 + (row * nb + b) * 4;
+    const float d = h2f(dp[0] | (dp[1] << 8)), dmin = h2f(dp[2] | (dp[3] << 8));
+    const float fd = d * (float)(sc & 15u), fm = dmin * (float)(sc >> 4);
+    const uint32_t q = (kq_byte<80>(base, nb, row, b, 16 + n * 32 + l) >> (jj * 2)) & 3u;
+    const float a = fd * (float)q;
+    return a - fm;
+}
+
 // Element k of row `row` of a K-wide matrix in device layout fmt (NB = total blocks of the tensor).
 QP_DEV float deq_elem(uint32_t fmt, const uint8_t* base, uint64_t NB, uint64_t row, uint32_t K, uint32_t k) {
     if (fmt == QP_Q4_K) return deq_q4k_dev(base, K >> 8, row, k >> 8, k & 255);
     if (fmt == QP_Q5_K) return deq_q5k_dev(base, K >> 8, row, k >> 8, k & 255);
+    if (fmt == QP_Q3_K) return deq_q3k_dev(base, K >> 8, row, k >> 8, k & 255);
+    if (fmt == QP_Q2_K) return deq_q2k_dev(base, K >> 8, NB, row, k >> 8, k & 255);
     if (fmt == QP_Q6_K) return deq_q6k_dev(base, K >> 8, NB, row, k >> 8, k & 255);
     if (fmt == QP_Q8_0) return deq_q8_planar(base, NB, row * (K >> 5) + (k >> 5), k & 31);
     return reinterpret_cast<const float*>(base)[row * K + k];
 }
 
 QP_DEV uint64_t total_blocks(uint32_t fmt, uint64_t nrows, uint32_t K) {
-    if (fmt == QP_Q4_K || fmt == QP_Q5_K || fmt == QP_Q6_K) return nrows * (K >> 8);
+    if (fmt == QP_Q2_K || fmt == QP_Q3_K || fmt == QP_Q4_K || fmt == QP_Q5_K || fmt == QP_Q6_K) return nrows * (K >> 8);
     if (fmt == QP_Q8_0) return nrows * (K >> 5);
     return nrows * K;
 }

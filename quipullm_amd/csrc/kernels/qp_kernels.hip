@@ -26,6 +26,37 @@ QP_DEV void repack_chunks(const QpRepackArgs& a) {
 KERNEL __launch_bounds__(256) void qp_repack_q4k(QpRepackArgs a) { repack_chunks<9>(a); }
 KERNEL __launch_bounds__(256) void qp_repack_q5k(QpRepackArgs a) { repack_chunks<11>(a); }
 
+// Q3_K: 110-byte GGUF blocks (2-byte aligned) into 112-byte slots of 7 chunks (the last chunk: scales, d, 2 zero
+// bytes).  Q2_K: 84-byte blocks, bytes 0..79 as 5 chunks, d and dmin (bytes 80..83) to an array after the rows.
+KERNEL __launch_bounds__(256) void qp_repack_q3k(QpRepackArgs a) {
+    const uint64_t NB = a.nblocks, nchunk = NB * 7;
+    const uint32_t nb = a.k >> 8;
+    for (uint64_t t = blockIdx.x * 256ull + threadIdx.x; t < nchunk; t += (uint64_t)gridDim.x * 256ull) {
+        const uint64_t blk = t / 7, row = blk / nb;
+        const uint32_t c = (uint32_t)(t - blk * 7), b = (uint32_t)(blk - row * nb);
+        const uint8_t* src = cptr<uint8_t>(a.src) + blk * 110;
+        uint8_t* o = mptr<uint8_t>(a.dst) + row * nb * 112 + (uint64_t)c * nb * 16 + b * 16;
+        for (int i = 0; i < 16; i++) o[i] = c * 16 + i < 110 ? src[c * 16 + i] : 0;
+    }
+}
+
+KERNEL __launch_bounds__(256) void qp_repack_q2k(QpRepackArgs a) {
+    const uint64_t NB = a.nblocks, nchunk = NB * 6;
+    const uint32_t nb = a.k >> 8;
+    for (uint64_t t = blockIdx.x * 256ull + threadIdx.x; t < nchunk; t += (uint64_t)gridDim.x * 256ull) {
+        const uint64_t blk = t / 6, row = blk / nb;
+        const uint32_t c = (uint32_t)(t - blk * 6), b = (uint32_t)(blk - row * nb);
+        const uint32_t* src = cptr<uint32_t>(a.src) + blk * 21;  // 84-byte blocks: 4-byte aligned
+        uint32_t* dst = mptr<uint32_t>(a.dst);
+        if (c < 5) {
+            uint32_t* o = dst + (row * nb * 80 + (uint64_t)c * nb * 16 + b * 16) / 4;
+            for (int i = 0; i < 4; i++) o[i] = src[c * 4 + i];
+        } else {
+            dst[(NB * 80) / 4 + blk] = src[20];
+        }
+    }
+}
+
 KERNEL __launch_bounds__(256) void qp_repack_q6k(QpRepackArgs a) {
     const uint64_t NB = a.nblocks, nchunk = NB * 14;
     const uint32_t nb = a.k >> 8;
@@ -498,6 +529,14 @@ struct KQ<QP_Q4_K> {
     static constexpr int CPB = 9, RB = 144, LOADS = 9, GROUP = 32;  // GROUP: elements per x sum
 };
 template <>
+struct KQ<QP_Q2_K> {
+    static constexpr int CPB = 5, RB = 80, LOADS = 6, GROUP = 16;  // + the (d, dmin) word
+};
+template <>
+struct KQ<QP_Q3_K> {
+    static constexpr int CPB = 7, RB = 112, LOADS = 7, GROUP = 16;
+};
+template <>
 struct KQ<QP_Q5_K> {
     static constexpr int CPB = 11, RB = 176, LOADS = 11, GROUP = 32;
 };
@@ -516,7 +555,7 @@ struct KQ<QP_KQ_MIX> {
 template <int FMT, int R>
 struct KUnit {
     u32x4 c[R][KQ<FMT>::CPB];
-    uint32_t d[R];  // Q6_K: the block's f16 d
+    uint32_t d[R];  // Q6_K: the block's f16 d; Q2_K: d | dmin << 16
 };
 
 // acc + (f16 half SEL of m) * x, in one v_fma_mix_f32 (the f16 operand may be subnormal).
@@ -680,6 +719,113 @@ QP_DEV void kq_dot_q5k(const U& B, const float4* xb4, const float* xsb, float (&
     }
 }
 
+// acc + the dot of 16 consecutive x (4 float4) with the bytes of q4[0..3] (4 per dword, each < 256), as f16
+// subnormals q*2^-24.
+template <int R>
+QP_DEV float kq_dot16(const u32x4& q4, const float4 (&xv)[4], float acc) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t e = __builtin_amdgcn_perm(0u, q4[c], 0x0c020c00u);  // bytes 0, 2 as f16 halves
+        const uint32_t o = __builtin_amdgcn_perm(0u, q4[c], 0x0c030c01u);  // bytes 1, 3
+        acc = fmix<0>(e, xv[c].x, acc);
+        acc = fmix<0>(o, xv[c].y, acc);
+        acc = fmix<1>(e, xv[c].z, acc);
+        acc = fmix<1>(o, xv[c].w, acc);
+    }
+    return acc;
+}
+
+// Q3_K (chunks: hmask 0-1, qs 2-5, scales and d 6): element (h, jj, l) has q' = q2 | hbit << 2 in 0..7 and the
+// value (d * (s6 - 32)) * (q' - 4) over 16-element groups s = 8h + 2jj + l/16.
+template <class U, int R>
+QP_DEV void kq_dot_q3k(const U& B, const float4* xb4, const float* xsb, float (&tot)[R]) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int lh = 0; lh < 2; lh++) {
+            float aq[R][4];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int qd = 0; qd < 4; qd++) aq[r][qd] = 0.0f;
+#pragma unroll
+            for (int qd = 0; qd < 4; qd++) {
+                float4 xv[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) xv[c] = xb4[(h * 128 + qd * 32 + lh * 16) / 4 + c];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const u32x4 qs = B.c[r][2 + 2 * h + lh], hm = B.c[r][lh];
+                    u32x4 q;
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        q[c] = ((qs[c] >> (2 * qd)) & 0x03030303u) | (((hm[c] >> (4 * h + qd)) & 0x01010101u) << 2);
+                    aq[r][qd] = kq_dot16<R>(q, xv, aq[r][qd]);
+                }
+#pragma unroll
+                for (int r = 0; r < R; r++) kq_fence(aq[r][qd]);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const u32x4 sw = B.c[r][6];
+                const float dd = h2f(sw[3] & 0xffffu);
+#pragma unroll
+                for (int qd = 0; qd < 4; qd++) {
+                    const uint32_t si = h * 8 + qd * 2 + lh;
+                    const float sc = (float)q3k_scale6(sw[0], sw[1], sw[2], si) - 32.0f;
+                    const float sx = xsb[(h * 128 + qd * 32 + lh * 16) / 16];
+                    tot[r] += (dd * sc) * (aq[r][qd] * 16777216.0f - 4.0f * sx);
+                }
+            }
+        }
+    }
+}
+
+// Q2_K (chunks: scales 0, qs 1-4; d and dmin in B.d): element (h, jj, l) has q = (qs >> 2jj) & 3 and the value
+// (d * (sc & 15)) * q - dmin * (sc >> 4) over 16-element groups j = 8h + 2jj + l/16.
+template <class U, int R>
+QP_DEV void kq_dot_q2k(const U& B, const float4* xb4, const float* xsb, float (&tot)[R]) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int lh = 0; lh < 2; lh++) {
+            float aq[R][4];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int qd = 0; qd < 4; qd++) aq[r][qd] = 0.0f;
+#pragma unroll
+            for (int qd = 0; qd < 4; qd++) {
+                float4 xv[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) xv[c] = xb4[(h * 128 + qd * 32 + lh * 16) / 4 + c];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const u32x4 qs = B.c[r][1 + 2 * h + lh];
+                    u32x4 q;
+#pragma unroll
+                    for (int c = 0; c < 4; c++) q[c] = (qs[c] >> (2 * qd)) & 0x03030303u;
+                    aq[r][qd] = kq_dot16<R>(q, xv, aq[r][qd]);
+                }
+#pragma unroll
+                for (int r = 0; r < R; r++) kq_fence(aq[r][qd]);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const u32x4 scw = B.c[r][0];
+                const float d = h2f(B.d[r] & 0xffffu), dm = h2f(B.d[r] >> 16);
+#pragma unroll
+                for (int qd = 0; qd < 4; qd++) {
+                    const uint32_t j = h * 8 + qd * 2 + lh;
+                    const uint32_t sc = (scw[j >> 2] >> ((j & 3) * 8)) & 0xffu;
+                    const float sx = xsb[(h * 128 + qd * 32 + lh * 16) / 16];
+                    tot[r] += (d * (float)(sc & 15u)) * (aq[r][qd] * 16777216.0f) - (dm * (float)(sc >> 4)) * sx;
+                }
+            }
+        }
+    }
+}
+
 template <class U, int R>
 QP_DEV void kq_dot_q6k(const U& B, const float4* xb4, const float* xsb, float (&tot)[R]) {
     // element (h, qd, l): ql chunk h*4 + (qd&1)*2 + l/16, nibble qd>>1; qh chunk 8 + h*2 + l/16, bits 2qd;
@@ -811,7 +957,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         const uint32_t nbw = lay.nbw(nb);
         // bytes per weight row (and per tensor row, with the Q6_K d array after the rows)
         const uint32_t rbw = FMT == QP_KQ_MIX ? (q6 ? 208 : 144) : KQ<FMT>::RB;
-        const uint64_t tbytes = (uint64_t)sg.rows_total * nbw * (q6 ? 210 : rbw);
+        const uint64_t tbytes = (uint64_t)sg.rows_total * nbw * (q6 ? 210 : FMT == QP_Q2_K ? 84 : rbw);
         const __amdgpu_buffer_rsrc_t rs0 = kq_rsrc(sg.w, tbytes);
         const __amdgpu_buffer_rsrc_t rs1 = kq_rsrc(pair ? sg.w2 : sg.w, tbytes);
 #pragma unroll
@@ -830,6 +976,9 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
             if constexpr (FMT == QP_Q6_K || FMT == QP_KQ_MIX)
                 B.d[r] = __builtin_amdgcn_raw_buffer_load_b16(
                     rs, (on && q6) ? sg.rows_total * nbw * 208 + (wr * nbw + wb) * 2 : 0x80000000u, 0, 0);
+            if constexpr (FMT == QP_Q2_K)
+                B.d[r] = __builtin_amdgcn_raw_buffer_load_b32(
+                    rs, on ? sg.rows_total * nbw * 80 + (wr * nbw + wb) * 4 : 0x80000000u, 0, 0);
         }
     };
     issue(buf, 0);
@@ -932,6 +1081,10 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
             kq_dot_q4k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
         } else if constexpr (FMT == QP_Q5_K) {
             kq_dot_q5k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
+        } else if constexpr (FMT == QP_Q3_K) {
+            kq_dot_q3k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
+        } else if constexpr (FMT == QP_Q2_K) {
+            kq_dot_q2k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
         } else if constexpr (FMT == QP_Q6_K) {
             kq_dot_q6k<KUnit<FMT, R>, R>(buf, xb4, xsb, tot);
         } else {
@@ -1184,10 +1337,18 @@ MOE_KERNELS(q6k, QP_Q6_K)
         QpGemvExpArgs a) { kq_gemv_exp<FMT, 2, 2>(a); }
 KQ_KERNELS(q4k, QP_Q4_K)
 KQ_KERNELS(q5k, QP_Q5_K)
+KQ_KERNELS(q3k, QP_Q3_K)
+KQ_KERNELS(q2k, QP_Q2_K)
 KQ_KERNELS(q6k, QP_Q6_K)
 // rows of more than 8192 inputs without the fused norm: 512 threads share one input staging, one sub-block each
 KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void qp_gemv_q4k_r1k2(QpGemvArgs a) {
     kq_gemv_seg<QP_Q4_K, 1, 1, 512, false>(a);
+}
+KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void qp_gemv_q3k_r1k2(QpGemvArgs a) {
+    kq_gemv_seg<QP_Q3_K, 1, 1, 512, false>(a);
+}
+KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void qp_gemv_q2k_r1k2(QpGemvArgs a) {
+    kq_gemv_seg<QP_Q2_K, 1, 1, 512, false>(a);
 }
 KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void qp_gemv_q5k_r1k2(QpGemvArgs a) {
     kq_gemv_seg<QP_Q5_K, 1, 1, 512, false>(a);
@@ -1622,6 +1783,19 @@ QP_DEV void mm8_load(MmW8& r, const MmOff& o, __amdgpu_buffer_rsrc_t rx, __amdgp
         const uint32_t j = e0 >> 5;
         r.q = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16 + (1 + 2 * (j >> 1)) * nb * 16, 0);
         r.h = __builtin_amdgcn_raw_buffer_load_b128(rw, o.h, b * 16, 0);
+    } else if constexpr (FMT == QP_Q3_K || FMT == QP_Q2_K) {
+        // element 128 n + 32 jj + l: Q3_K qs chunk 2 + 2n + l/16, hmask chunk l/16, scales and d chunk 6; Q2_K qs
+        // chunk 1 + 2n + l/16, the scale byte 8n + 2jj + l/16 in chunk 0, (d, dmin) in the array after the rows
+        const uint32_t n = e0 >> 7;
+        if constexpr (FMT == QP_Q3_K) {
+            r.q = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16 + (2 + 2 * n) * nb * 16, 0);
+            r.qh = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16, 0);
+            r.h = __builtin_amdgcn_raw_buffer_load_b128(rw, o.h, b * 16 + 6 * nb * 16, 0);
+        } else {
+            r.q = __builtin_amdgcn_raw_buffer_load_b64(rw, o.q, b * 16 + (1 + 2 * n) * nb * 16, 0);
+            r.sc = __builtin_amdgcn_raw_buffer_load_b32(rw, o.h, b * 16 + 4 * ((8 * n + 2 * ((e0 & 127) >> 5)) >> 2), 0);
+            r.d = __builtin_amdgcn_raw_buffer_load_b32(rw, o.d, b * 4, 0);
+        }
     } else if constexpr (FMT == QP_Q5_K) {
         // qs chunk 3 + 2*(j/2) + l/16, qh chunk 1 + l/16 (the same 8 bytes l of both)
         const uint32_t j = e0 >> 5;
@@ -1642,7 +1816,21 @@ QP_DEV void mm8_deq(const MmW8& r, uint32_t k0, uint32_t sub, float (&w)[8]) {
     const uint32_t e0 = k0 & 255;
     uint32_t v[2];
     float f, c;
-    if constexpr (FMT == QP_Q4_K || FMT == QP_Q5_K) {
+    if constexpr (FMT == QP_Q3_K) {
+        // fma(fd, q', -4 fd) = fd * (q' - 4) exactly (one rounding of the same value), q' = q2 | hbit << 2
+        const uint32_t n = e0 >> 7, jj = (e0 & 127) >> 5, s = 8 * n + 2 * jj + (sub >> 1);
+        f = h2f(r.h.w & 0xffffu) * ((float)q3k_scale6(r.h.x, r.h.y, r.h.z, s) - 32.0f);
+        c = -4.0f * f;
+        v[0] = ((r.q.x >> (2 * jj)) & 0x03030303u) | (((r.qh.x >> (4 * n + jj)) & 0x01010101u) << 2);
+        v[1] = ((r.q.y >> (2 * jj)) & 0x03030303u) | (((r.qh.y >> (4 * n + jj)) & 0x01010101u) << 2);
+    } else if constexpr (FMT == QP_Q2_K) {
+        const uint32_t n = e0 >> 7, jj = (e0 & 127) >> 5, j = 8 * n + 2 * jj + (sub >> 1);
+        const uint32_t sc = (r.sc >> ((j & 3) * 8)) & 0xffu;
+        f = h2f(r.d & 0xffffu) * (float)(sc & 15u);
+        c = -(h2f(r.d >> 16) * (float)(sc >> 4));
+        v[0] = (r.q.x >> (2 * jj)) & 0x03030303u;
+        v[1] = (r.q.y >> (2 * jj)) & 0x03030303u;
+    } else if constexpr (FMT == QP_Q4_K || FMT == QP_Q5_K) {
         // fd*q - fm; a Q4_K high nibble is masked in place (16*q) with the scale divided by 16 (exact); Q5_K
         // shifts the nibble down and adds 16 * bit j of qh
         const uint32_t j = e0 >> 5, jj = (j & 3) * 8;  // the scale/min unpack of q4k_sm, without a branch
@@ -1700,12 +1888,12 @@ QP_DEV void gemm_mfma256_body(const QpGemmArgs& g) {
     const uint32_t nb = K >> 8, xplane = 2 * g.rows * K;
     const __amdgpu_buffer_rsrc_t rx = kq_rsrc(g.xs, 2ull * xplane);
     constexpr uint32_t RBW = KQ<FMT>::RB;  // bytes per weight row and 256 inputs (Q6_K: its d array follows)
-    const __amdgpu_buffer_rsrc_t rw = kq_rsrc(g.w, (uint64_t)N * nb * (FMT == QP_Q6_K ? 210 : RBW));
+    const __amdgpu_buffer_rsrc_t rw = kq_rsrc(g.w, (uint64_t)N * nb * (FMT == QP_Q6_K ? 210 : FMT == QP_Q2_K ? 84 : RBW));
     MmOff off;
     off.x = 2 * (xt * K + 16 * part);
     off.q = wr * nb * RBW + (sub >> 1) * nb * 16 + (sub & 1) * 8;
     off.h = wr * nb * RBW;
-    off.d = N * nb * 208 + wr * nb * 2;
+    off.d = FMT == QP_Q2_K ? N * nb * 80 + wr * nb * 4 : N * nb * 208 + wr * nb * 2;
     const uint32_t nsteps = (kend - kbeg + TK - 1) / TK;
     f32x16 acc[2][2];
 #pragma unroll
@@ -1815,6 +2003,8 @@ QP_DEV void gemm_mfma256_body(const QpGemmArgs& g) {
 
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q4k(QpGemmArgs a) { gemm_mfma256_body<QP_Q4_K>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q5k(QpGemmArgs a) { gemm_mfma256_body<QP_Q5_K>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q3k(QpGemmArgs a) { gemm_mfma256_body<QP_Q3_K>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q2k(QpGemmArgs a) { gemm_mfma256_body<QP_Q2_K>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q6k(QpGemmArgs a) { gemm_mfma256_body<QP_Q6_K>(a); }
 
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q4k(QpGemmArgs a) { gemm_mfma_body<QP_Q4_K>(a); }

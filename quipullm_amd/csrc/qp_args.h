@@ -7,6 +7,8 @@
 // ---------------------------------------------------------------- weight formats (ggml type ids)
 #define QP_F32 0
 #define QP_Q8_0 8
+#define QP_Q2_K 10
+#define QP_Q3_K 11
 #define QP_Q4_K 12
 #define QP_Q5_K 13
 #define QP_Q6_K 14

@@ -132,13 +132,19 @@ int need_bufs(const Ctx& c, uint32_t n, const char* op) {
 int fmt_of(const char* s) {
     if (!strcmp(s, "q4k")) return QP_Q4_K;
     if (!strcmp(s, "q5k")) return QP_Q5_K;
+    if (!strcmp(s, "q3k")) return QP_Q3_K;
+    if (!strcmp(s, "q2k")) return QP_Q2_K;
     if (!strcmp(s, "q6k")) return QP_Q6_K;
     if (!strcmp(s, "q8")) return QP_Q8_0;
     if (!strcmp(s, "f32")) return QP_F32;
     return -1;
 }
 
-bool is_kq(int fmt) { return fmt == QP_Q4_K || fmt == QP_Q5_K || fmt == QP_Q6_K; }
+bool is_kq(int fmt) {
+    return fmt == QP_Q2_K || fmt == QP_Q3_K || fmt == QP_Q4_K || fmt == QP_Q5_K || fmt == QP_Q6_K;
+}
+// index of a K-quant format in the kernel tables: Q4_K, Q5_K, Q6_K, Q3_K, Q2_K
+int kq_index(int fmt) { return fmt == QP_Q5_K ? 1 : fmt == QP_Q6_K ? 2 : fmt == QP_Q3_K ? 3 : fmt == QP_Q2_K ? 4 : 0; }
 
 int check_k(int fmt, uint32_t K, const char* op) {
     if (is_kq(fmt) && K % 256)
@@ -204,8 +210,10 @@ uint32_t kq_nbp(uint32_t K) {
     return p;
 }
 uint32_t kq_lds(uint32_t K) { return (K / 256) * 65 * 16 + (K / 16) * 4; }
+// device bytes of a K-quant tensor (Q3_K blocks padded to 112 bytes; Q6_K / Q2_K with their d arrays)
 uint64_t kq_tensor_bytes(int fmt, uint64_t rows, uint32_t K) {
-    return rows * (K / 256) * (fmt == QP_Q4_K ? 144 : fmt == QP_Q5_K ? 176 : 210);
+    static const uint32_t bpb[5] = {144, 176, 210, 112, 84};
+    return rows * (K / 256) * bpb[kq_index(fmt)];
 }
 
 Kid kq_mix_kid(int R, bool x2) {
@@ -214,14 +222,18 @@ Kid kq_mix_kid(int R, bool x2) {
 }
 
 Kid kq_kid(int fmt, int R, bool x2, bool expert) {
-    static const Kid t[2][3][2][2] = {
+    static const Kid t[2][5][2][2] = {
         {{{K_gemv_q4k_r1, K_gemv_q4k_r1x2}, {K_gemv_q4k_r2, K_gemv_q4k_r2x2}},
          {{K_gemv_q5k_r1, K_gemv_q5k_r1x2}, {K_gemv_q5k_r2, K_gemv_q5k_r2x2}},
-         {{K_gemv_q6k_r1, K_gemv_q6k_r1x2}, {K_gemv_q6k_r2, K_gemv_q6k_r2x2}}},
+         {{K_gemv_q6k_r1, K_gemv_q6k_r1x2}, {K_gemv_q6k_r2, K_gemv_q6k_r2x2}},
+         {{K_gemv_q3k_r1, K_gemv_q3k_r1x2}, {K_gemv_q3k_r2, K_gemv_q3k_r2x2}},
+         {{K_gemv_q2k_r1, K_gemv_q2k_r1x2}, {K_gemv_q2k_r2, K_gemv_q2k_r2x2}}},
         {{{K_gemv_exp_q4k_r1, K_gemv_exp_q4k_r1x2}, {K_gemv_exp_q4k_r2, K_gemv_exp_q4k_r2x2}},
          {{K_gemv_exp_q5k_r1, K_gemv_exp_q5k_r1x2}, {K_gemv_exp_q5k_r2, K_gemv_exp_q5k_r2x2}},
-         {{K_gemv_exp_q6k_r1, K_gemv_exp_q6k_r1x2}, {K_gemv_exp_q6k_r2, K_gemv_exp_q6k_r2x2}}}};
-    return t[expert ? 1 : 0][fmt == QP_Q6_K ? 2 : fmt == QP_Q5_K ? 1 : 0][R == 2 ? 1 : 0][x2 ? 1 : 0];
+         {{K_gemv_exp_q6k_r1, K_gemv_exp_q6k_r1x2}, {K_gemv_exp_q6k_r2, K_gemv_exp_q6k_r2x2}},
+         {{K_gemv_exp_q3k_r1, K_gemv_exp_q3k_r1x2}, {K_gemv_exp_q3k_r2, K_gemv_exp_q3k_r2x2}},
+         {{K_gemv_exp_q2k_r1, K_gemv_exp_q2k_r1x2}, {K_gemv_exp_q2k_r2, K_gemv_exp_q2k_r2x2}}}};
+    return t[expert ? 1 : 0][kq_index(fmt)][R == 2 ? 1 : 0][x2 ? 1 : 0];
 }
 
 // Units per segment, then the grid: one unit per wavefront, at most two workgroups per CU (the kernel strides
@@ -257,9 +269,11 @@ int run_gemv_kq(int fmt, QpGemvArgs& a, uint32_t max_wg, uint32_t* grid_out) {
     if (max_wg && grid > max_wg) grid = max_wg;
     if (grid == 0) grid = 1;
     if (grid_out) *grid_out = grid;
-    if (wide)
-        return launch(fmt == QP_Q6_K ? K_gemv_q6k_r1k2 : fmt == QP_Q5_K ? K_gemv_q5k_r1k2 : K_gemv_q4k_r1k2, grid, 1, 1,
-                      512, kq_lds(a.k), a);
+    if (wide) {
+        static const Kid wide_kid[5] = {K_gemv_q4k_r1k2, K_gemv_q5k_r1k2, K_gemv_q6k_r1k2, K_gemv_q3k_r1k2,
+                                        K_gemv_q2k_r1k2};
+        return launch(wide_kid[kq_index(fmt)], grid, 1, 1, 512, kq_lds(a.k), a);
+    }
     const Kid kid = mixed ? kq_mix_kid(R, a.k > 8192) : kq_kid((int)a.seg[0].fmt, R, a.k > 8192, false);
     return launch(kid, grid, 1, 1, 256, kq_lds(a.k), a);
 }
@@ -363,7 +377,8 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
             // when the tiles alone cannot occupy the CUs; partials summed in order.  From 256 tokens on, 256-token
             // tiles (one 512-thread workgroup per CU, K steps of 32 double-buffered in LDS) dequantize each weight
             // tile half as often.
-            const bool big = tmax >= 256 || fmt == QP_Q5_K;  // Q5_K has only the 256-token tiles
+            // Q5_K, Q3_K and Q2_K have only the 256-token tiles
+            const bool big = tmax >= 256 || fmt == QP_Q5_K || fmt == QP_Q3_K || fmt == QP_Q2_K;
             if (big) mt = cdiv(tmax, 256);
             const uint32_t steps = K / 64, slots = (big ? 1 : 2) * (uint32_t)g_cus;
             uint32_t ns = 1;
@@ -379,7 +394,9 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
             QpSplitArgs sa = {a.x, a.xs, a.paso, K, a.rows};
             if (int e = launch(K_split_bf16, grid_cap((uint64_t)tmax * K / 8), 1, 1, 256, 0, sa)) return e;
             if (big) {
-                const Kid kb = fmt == QP_Q4_K ? K_gemm_mfma256_q4k : fmt == QP_Q5_K ? K_gemm_mfma256_q5k : K_gemm_mfma256_q6k;
+                static const Kid kb_of[5] = {K_gemm_mfma256_q4k, K_gemm_mfma256_q5k, K_gemm_mfma256_q6k,
+                                             K_gemm_mfma256_q3k, K_gemm_mfma256_q2k};
+                const Kid kb = kb_of[kq_index(fmt)];
                 if (int e = launch(kb, nt, mt, ns, 512, 2 * (256 + 256 + 128 + 128) * 40 * 2, a)) return e;
             } else if (int e = launch(k, nt, mt, ns, 256, 0, a)) {
                 return e;
@@ -388,7 +405,8 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
             QpReduceArgs ra = {a.ws, a.y, a.paso, N, a.rows, ns, acc};
             return launch(K_gemm_reduce, grid_cap((uint64_t)tmax * N), 1, 1, 256, 0, ra);
         }
-        if (fmt == QP_Q5_K) return launch(K_gemm_mt, cdiv(N, 64), cdiv(tmax, 64), 1, 256, 0, a);  // under capture
+        if (fmt == QP_Q5_K || fmt == QP_Q3_K || fmt == QP_Q2_K)
+            return launch(K_gemm_mt, cdiv(N, 64), cdiv(tmax, 64), 1, 256, 0, a);  // under capture
         return launch(k, nt, mt, 1, 256, 0, a);
     }
     return launch(K_gemm_mt, cdiv(N, 64), cdiv(tmax ? tmax : 1, 64), 1, 256, 0, a);
@@ -814,8 +832,8 @@ int op_topk_cand(const Ctx& c) {
     return launch(K_topk_merge, 1, 1, 1, 1024, n2 * 8, a);
 }
 
-// repack_q4k / repack_q5k / repack_q6k: P{nblocks lo, hi, K}; repack_q8: P{nblocks lo, hi}; [paso|0, src, dst].  K
-// (the row length) places the blocks in the row chunk-plane layout of Q4_K / Q5_K / Q6_K.
+// repack_q2k .. repack_q6k: P{nblocks lo, hi, K}; repack_q8: P{nblocks lo, hi}; [paso|0, src, dst].  K (the row
+// length) places the blocks in the row chunk-plane layout of the K-quants (dst: kq_tensor_bytes).
 int op_repack(const Ctx& c, Kid k, const char* name) {
     if (int e = need_bufs(c, 3, name)) return e;
     QpRepackArgs a = {};
@@ -824,11 +842,11 @@ int op_repack(const Ctx& c, Kid k, const char* name) {
     a.src = c.B(1);
     a.dst = c.B(2);
     uint64_t threads = a.nblocks;
-    if (k == K_repack_q4k || k == K_repack_q5k || k == K_repack_q6k) {
+    if (k == K_repack_q4k || k == K_repack_q5k || k == K_repack_q6k || k == K_repack_q3k || k == K_repack_q2k) {
         if (a.k == 0 || a.k % 256 || a.k > 15360) return fail(QP_E_ARG, "%s: K=%u must be a multiple of 256 <= 15360", name, a.k);
         if (a.nblocks % (a.k / 256)) return fail(QP_E_ARG, "%s: %llu blocks are not whole rows of K=%u", name,
                                                  (unsigned long long)a.nblocks, a.k);
-        threads = a.nblocks * (k == K_repack_q4k ? 9 : k == K_repack_q5k ? 11 : 14);
+        threads = a.nblocks * (k == K_repack_q4k ? 9 : k == K_repack_q5k ? 11 : k == K_repack_q3k ? 7 : k == K_repack_q2k ? 6 : 14);
     }
     return launch(k, grid_cap(threads), 1, 1, 256, 0, a);
 }
@@ -885,7 +903,7 @@ std::vector<Op>& ops() {
 void register_ops() {
     auto& v = ops();
     if (!v.empty()) return;
-    for (const char* f : {"q4k", "q5k", "q6k", "q8", "f32"}) {
+    for (const char* f : {"q2k", "q3k", "q4k", "q5k", "q6k", "q8", "f32"}) {
         const int fmt = fmt_of(f);
         std::string s(f);
         std::string n1 = "matmul_" + s + "_1", n4 = "matmul_" + s + "_4", nt = "matmul_" + s + "_t";
@@ -917,6 +935,8 @@ void register_ops() {
     v.push_back({"topk_cand", op_topk_cand});
     v.push_back({"repack_q4k", [](const Ctx& c) { return op_repack(c, K_repack_q4k, "repack_q4k"); }});
     v.push_back({"repack_q5k", [](const Ctx& c) { return op_repack(c, K_repack_q5k, "repack_q5k"); }});
+    v.push_back({"repack_q3k", [](const Ctx& c) { return op_repack(c, K_repack_q3k, "repack_q3k"); }});
+    v.push_back({"repack_q2k", [](const Ctx& c) { return op_repack(c, K_repack_q2k, "repack_q2k"); }});
     v.push_back({"repack_q6k", [](const Ctx& c) { return op_repack(c, K_repack_q6k, "repack_q6k"); }});
     v.push_back({"repack_q8", [](const Ctx& c) { return op_repack(c, K_repack_q8, "repack_q8"); }});
     v.push_back({"fill_u32", op_fill});

@@ -24,7 +24,7 @@ from quipullm_amd.gemv_bench import parse_shape  # noqa: E402
 
 
 def time_gemm(q, fmt, N, K, T, iters=20, rotate_bytes=640 << 20):
-    nbytes = capi.device_bytes(fmt, N, K)
+    nbytes = capi.gguf_bytes(fmt, N, K)
     ncopy = max(2, rotate_bytes // nbytes + 1)
     raw = np.frombuffer(synth.gen_blocks(np.random.default_rng([5, N, K]), fmt, N * K), np.uint8)
     hs = [q.upload_matrix(fmt, raw, N, K) for _ in range(ncopy)]

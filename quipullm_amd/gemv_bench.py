@@ -35,7 +35,7 @@ def parse_shape(s):
 def time_gemv(q, fmt, N, K, iters=200, rotate_bytes=640 << 20, R=0):
     """Average launch duration of the fused GEMV on one shape; returns a dict."""
     paso = q.paso(1, 0)
-    nbytes = capi.device_bytes(fmt, N, K)
+    nbytes = capi.gguf_bytes(fmt, N, K)
     ncopy = max(2, rotate_bytes // nbytes + 1)
     raw = np.frombuffer(synth.gen_blocks(np.random.default_rng([3, N, K]), fmt, N * K), np.uint8)
     hs = [q.upload_matrix(fmt, raw, N, K) for _ in range(ncopy)]

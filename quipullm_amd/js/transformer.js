@@ -14,9 +14,9 @@ const { despachar, dim2, vista } = require('./gpu');
 const { CargadorPesos } = require('./weights');
 
 const ROPE_NEOX = new Set(['qwen2', 'qwen3', 'qwen3moe', 'phi3', 'gemma', 'gemma2', 'gemma3', 'stablelm', 'olmo2']);
-const KQ = new Set(['q4k', 'q5k', 'q6k']);
+const KQ = new Set(['q2k', 'q3k', 'q4k', 'q5k', 'q6k']);
 const MEZCLA = new Set(['q4k', 'q6k']);    // formats whose GEMV segments may share one launch
-const FMT_ID = { f32: 0, q8: 8, q4k: 12, q5k: 13, q6k: 14 };
+const FMT_ID = { f32: 0, q8: 8, q2k: 10, q3k: 11, q4k: 12, q5k: 13, q6k: 14 };
 // gemv segment modes (qp_args.h)
 const STORE = 0, ACC = 1, SWIGLU = 2, ARGMAX = 3;
 const AMAX_WG = 512;   // workgroups of the fused output GEMV = partial maxima for the device argmax

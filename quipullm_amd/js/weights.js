@@ -3,12 +3,15 @@
 //
 // Same interface as quipullm's CargadorPesos (web/js/weights.js:15-139): existe(name), info(name),
 // f32(name) -> buffer, matriz(name) -> {tipo, N, K, w} ({tipo:'q8', N, K, qs, ds} for Q8_0).  The device
-// layout behind a handle is this backend's own: Q4_K, Q5_K and Q6_K blocks and Q8_0 repacked on the device
+// layout behind a handle is this backend's own: K-quant blocks and Q8_0 repacked on the device
 // into planar arrays (quants | scales) so every lane load is a 16-byte vector load.
 const fs = require('fs');
 const { despachar, vista } = require('./gpu');
 
-const K_QUANTS = { 12: { nombre: 'q4k', bytes: 144 }, 13: { nombre: 'q5k', bytes: 176 }, 14: { nombre: 'q6k', bytes: 210 } };
+// GGUF K-quant types: name, GGUF block bytes, device bytes per block (Q3_K padded to 112)
+const K_QUANTS = { 10: { nombre: 'q2k', bytes: 84, disp: 84 }, 11: { nombre: 'q3k', bytes: 110, disp: 112 },
+  12: { nombre: 'q4k', bytes: 144, disp: 144 }, 13: { nombre: 'q5k', bytes: 176, disp: 176 },
+  14: { nombre: 'q6k', bytes: 210, disp: 210 } };
 
 const F16 = (function () {
   const t = new Float32Array(65536);
@@ -87,11 +90,11 @@ class CargadorPesos {
     return b;
   }
 
-  // Raw blocks -> device layout, repacked on the device (Q4_K / Q5_K / Q6_K row chunk planes, Q8_0 planar).
-  _subirRepack(u8, op, nblocks, K, etiqueta) {
+  // Raw blocks -> device layout, repacked on the device (K-quant row chunk planes, Q8_0 planar).
+  _subirRepack(u8, op, nblocks, K, etiqueta, bytesDisp) {
     const gpu = this.gpu;
     const staging = gpu.subir(u8, etiqueta + '.raw');
-    const dst = gpu.buffer(u8.length, undefined, etiqueta);
+    const dst = gpu.buffer(bytesDisp || u8.length, undefined, etiqueta);
     const lo = nblocks % 4294967296, hi = Math.floor(nblocks / 4294967296);
     despachar(null, gpu.grupo(op, [gpu.uniforme([['u', lo], ['u', hi], ['u', K]]), null, staging, dst]), 1);
     gpu.liberar([staging]);
@@ -106,7 +109,7 @@ class CargadorPesos {
       const info = K_QUANTS[t.tipo];
       if (K % 256) throw new Error(nombre + ': K=' + K + ' is not a multiple of 256 (' + info.nombre + ')');
       const u8 = this.bytes(t);
-      const w = this._subirRepack(u8, 'repack_' + info.nombre, N * K / 256, K, nombre);
+      const w = this._subirRepack(u8, 'repack_' + info.nombre, N * K / 256, K, nombre, N * K / 256 * info.disp);
       this.buffers.push(w);
       return { tipo: info.nombre, N: N, K: K, w: w };
     }
@@ -121,7 +124,7 @@ class CargadorPesos {
       const w = this.f32(nombre);
       return { tipo: 'f32', N: N, K: K, w: w };
     }
-    throw new Error(nombre + ': quantization ' + t.tipo_nombre + ' not supported yet (supported: Q4_K, Q5_K, Q6_K, Q8_0, F16, BF16, F32)');
+    throw new Error(nombre + ': quantization ' + t.tipo_nombre + ' not supported yet (supported: Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, F16, BF16, F32)');
   }
 }
 

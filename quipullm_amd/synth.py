@@ -8,6 +8,9 @@ the configurations specify, so no quantizer is needed:
 * Q4_K (144 B): d and dmin f16 |N(0, 0.01)|; the 12 packed bytes of 6-bit scales/mins uniform (every byte
   pattern decodes to 6-bit values, each uniform on 0..63); 4-bit quants uniform 0..15.
 * Q5_K (176 B): the Q4_K header distributions; qh and qs bytes uniform (5-bit quants uniform 0..31).
+* Q3_K (110 B): hmask, 2-bit quants and the 12 packed 6-bit scale bytes uniform; d f16 |N(0, 0.01)|.
+* Q2_K (84 B): 4-bit scale/min nibbles and 2-bit quants uniform; d and dmin f16 |N(0, 0.01)| (centered: mins
+  equal to scales and dmin = 1.5 d, the mean quant).
 * Q6_K (210 B): 6-bit quants uniform 0..63 (ql/qh bytes uniform); int8 sub-scales uniform in [-64, 63];
   d f16 |N(0, 0.01)|.
 * F32 vectors (norms, f32 embeddings): N(1, 0.02); the f32 MoE router: N(0, 0.02).
@@ -27,8 +30,9 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-GGML_F32, GGML_Q8_0, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 0, 8, 12, 13, 14
-BLOCK = {GGML_F32: (1, 4), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q5_K: (256, 176), GGML_Q6_K: (256, 210)}
+GGML_F32, GGML_Q8_0, GGML_Q2_K, GGML_Q3_K, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 0, 8, 10, 11, 12, 13, 14
+BLOCK = {GGML_F32: (1, 4), GGML_Q8_0: (32, 34), GGML_Q2_K: (256, 84), GGML_Q3_K: (256, 110), GGML_Q4_K: (256, 144),
+         GGML_Q5_K: (256, 176), GGML_Q6_K: (256, 210)}
 ALIGN = 32
 
 # GGUF metadata value types
@@ -101,6 +105,12 @@ CONFIGS = {
                                      _q4km(), qk_norm=True, ctx=512, centered=True),
     "mini_llama_q5km_c": ModelConfig("mini_llama_q5km_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
                                      _q5km(), ctx=512, centered=True),
+    "mini_llama_q3k_c": ModelConfig("mini_llama_q3k_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
+                                    {"default": GGML_Q3_K, "attn_v": GGML_Q5_K, "output": GGML_Q6_K}, ctx=512,
+                                    centered=True),
+    "mini_llama_q2k_c": ModelConfig("mini_llama_q2k_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
+                                    {"default": GGML_Q2_K, "ffn_down": GGML_Q3_K, "output": GGML_Q6_K}, ctx=512,
+                                    centered=True),
     "mini_qwen3moe_q5k_c": ModelConfig("mini_qwen3moe_q5k_c", "qwen3moe", 2, 512, 8, 2, 128, 0, 1000, 1e-6,
                                        1000000.0, {"default": GGML_Q5_K}, n_exp=16, n_used=4, ffe=256,
                                        qk_norm=True, ctx=512, centered=True),
@@ -191,6 +201,17 @@ def gen_blocks(rng, gtype, nelem, kind="w", centered=False):
             blk[:, 4:16] = pack_q4k_scales(sc, sc)
         else:
             blk[:, 2:4] = _abs_normal_f16(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)
+    elif gtype == GGML_Q3_K:
+        blk[:, 108:110] = _abs_normal_f16(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)
+    elif gtype == GGML_Q2_K:
+        d = _abs_normal_f16(rng, nb, 0.01)
+        blk[:, 80:82] = d.view(np.uint8).reshape(nb, 2)
+        if centered:
+            sc = rng.integers(0, 16, size=(nb, 16), dtype=np.uint8)
+            blk[:, 0:16] = sc | (sc << 4)
+            blk[:, 82:84] = (d.astype(np.float32) * np.float32(1.5)).astype(np.float16).view(np.uint8).reshape(nb, 2)
+        else:
+            blk[:, 82:84] = _abs_normal_f16(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)
     elif gtype == GGML_Q6_K:
         blk[:, 192:208] = rng.integers(-64, 64, size=(nb, 16), dtype=np.int8).view(np.uint8)
         blk[:, 208:210] = _abs_normal_f16(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)

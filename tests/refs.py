@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import numpy as np
 
-F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
+F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 8, 10, 11, 12, 13, 14
 
 
 # ------------------------------------------------------------------------------------------------ dequant
@@ -71,6 +71,56 @@ def dequant_q5k(raw: np.ndarray) -> np.ndarray:
     return out.reshape(-1)
 
 
+def dequant_q3k(raw: np.ndarray) -> np.ndarray:
+    """ggml's dequantize_row_q3_K, vectorized: 16 signed 6-bit scales (low 4 bits from bytes 0..7, high 2 bits
+    from bytes 8..11) minus 32; y = d*(scale - 32) * (q2 - (hmask bit set ? 0 : 4)), the hmask bit advancing
+    per 32-element step of the 256."""
+    b = raw.reshape(-1, 110)
+    nb = b.shape[0]
+    hm = b[:, 0:32].astype(np.int32)
+    qs = b[:, 32:96].astype(np.int32)
+    sb = b[:, 96:108].astype(np.int32)
+    d = b[:, 108:110].copy().view(np.float16).astype(np.float32).reshape(nb)
+    sc = np.empty((nb, 16), np.int32)
+    for i in range(16):
+        lo = (sb[:, i % 8] >> (4 * (i // 8))) & 0xF          # scales 0..7: low nibbles, 8..15: high nibbles
+        hi = (sb[:, 8 + i % 4] >> (2 * (i // 4))) & 3
+        sc[:, i] = (lo | (hi << 4)) - 32
+    out = np.empty((nb, 256), np.float32)
+    for n in range(2):
+        for j in range(4):
+            for lh in range(2):
+                idx = n * 8 + j * 2 + lh
+                dl = (d * sc[:, idx].astype(np.float32)).astype(np.float32)
+                l = np.arange(16) + 16 * lh
+                q = (qs[:, n * 32 + l] >> (2 * j)) & 3
+                h = (hm[:, l] >> (4 * n + j)) & 1
+                out[:, n * 128 + j * 32 + 16 * lh:n * 128 + j * 32 + 16 * lh + 16] = \
+                    dl[:, None] * (q - 4 * (1 - h)).astype(np.float32)
+    return out.reshape(-1)
+
+
+def dequant_q2k(raw: np.ndarray) -> np.ndarray:
+    """ggml's dequantize_row_q2_K, vectorized: y = d*(sc & 15) * q - dmin*(sc >> 4), q the 2-bit quant."""
+    b = raw.reshape(-1, 84)
+    nb = b.shape[0]
+    sc = b[:, 0:16].astype(np.int32)
+    qs = b[:, 16:80].astype(np.int32)
+    d = b[:, 80:82].copy().view(np.float16).astype(np.float32).reshape(nb)
+    dmin = b[:, 82:84].copy().view(np.float16).astype(np.float32).reshape(nb)
+    out = np.empty((nb, 256), np.float32)
+    for n in range(2):
+        for j in range(4):
+            for lh in range(2):
+                idx = n * 8 + j * 2 + lh
+                dl = (d * (sc[:, idx] & 0xF).astype(np.float32)).astype(np.float32)
+                ml = (dmin * (sc[:, idx] >> 4).astype(np.float32)).astype(np.float32)
+                q = (qs[:, n * 32 + 16 * lh:n * 32 + 16 * lh + 16] >> (2 * j)) & 3
+                out[:, n * 128 + j * 32 + 16 * lh:n * 128 + j * 32 + 16 * lh + 16] = \
+                    dl[:, None] * q.astype(np.float32) - ml[:, None]
+    return out.reshape(-1)
+
+
 def dequant_q6k(raw: np.ndarray) -> np.ndarray:
     b = raw.reshape(-1, 210)
     nb = b.shape[0]
@@ -105,6 +155,10 @@ def dequant(fmt, raw):
         return dequant_q4k(raw)
     if fmt == Q5_K:
         return dequant_q5k(raw)
+    if fmt == Q3_K:
+        return dequant_q3k(raw)
+    if fmt == Q2_K:
+        return dequant_q2k(raw)
     if fmt == Q6_K:
         return dequant_q6k(raw)
     if fmt == Q8_0:

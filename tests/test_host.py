@@ -48,10 +48,11 @@ def test_header_declares_the_facade():
 
 
 # every op name the JavaScript host dispatches (transformer.js, weights.js) and the tests use
-OPS = ["matmul_%s_%s" % (f, s) for f in ("q4k", "q5k", "q6k", "q8", "f32") for s in ("1", "4", "t", "e", "e_swiglu")] + \
-      ["embed_%s" % f for f in ("q4k", "q5k", "q6k", "q8", "f32")] + \
+FORMATS = ("q2k", "q3k", "q4k", "q5k", "q6k", "q8", "f32")
+OPS = ["matmul_%s_%s" % (f, s) for f in FORMATS for s in ("1", "4", "t", "e", "e_swiglu")] + \
+      ["embed_%s" % f for f in FORMATS] + \
       ["rmsnorm", "norm_rope", "kv_write", "atencion", "swiglu", "moe_topk", "moe_comb", "gemv", "dec_attn",
-       "dec_attn_comb", "argmax", "argmax_fin", "repack_q4k", "repack_q5k", "repack_q6k", "repack_q8", "fill_u32", "dequant",
+       "dec_attn_comb", "argmax", "argmax_fin", "repack_q2k", "repack_q3k", "repack_q4k", "repack_q5k", "repack_q6k", "repack_q8", "fill_u32", "dequant",
        "copy_f4", "read_f4", "moe_gate_up_q4k", "moe_gate_up_q6k", "moe_down_q4k", "moe_down_q6k", "penalizar",
        "topk_cand"]
 
@@ -60,7 +61,7 @@ def test_op_table(built):
     lib = capi.load_library()
     ids = [lib.qp_op_id(n.encode()) for n in OPS]
     assert min(ids) >= 0 and len(set(ids)) == len(ids)
-    assert lib.qp_op_id(b"matmul_q3k_1") == -1 and lib.qp_op_id(b"") == -1 and lib.qp_op_id(None) == -1
+    assert lib.qp_op_id(b"matmul_iq4nl_1") == -1 and lib.qp_op_id(b"") == -1 and lib.qp_op_id(None) == -1
 
 
 def test_ops_used_by_the_js_host_exist(built):
@@ -70,7 +71,7 @@ def test_ops_used_by_the_js_host_exist(built):
         src = open(os.path.join(JS, f)).read()
         used |= set(re.findall(r"['\"]((?:matmul|embed)_[a-z0-9_]+|rmsnorm|norm_rope|kv_write|atencion|swiglu|"
                                r"moe_topk|moe_comb|moe_(?:gate_up|down)_|gemv|dec_attn(?:_comb)?|argmax(?:_fin)?|"
-                               r"repack_q[468]k?|fill_u32)['\"]", src))
+                               r"repack_q[2-68]k?|fill_u32)['\"]", src))
     # names built by concatenation in the host: matmul_<fmt>_<suffix> and embed_<fmt>
     assert used, "no op names found"
     lib = capi.load_library()
@@ -114,6 +115,8 @@ def test_device_layout_sizes():
     assert capi.device_bytes(capi.Q6_K, 4096, 4096) == 4096 * 16 * 210
     assert capi.device_bytes(capi.Q8_0, 64, 2048) == 64 * 64 * 34
     assert capi.device_bytes(capi.F32, 3, 5) == 60
+    assert capi.gguf_bytes(capi.Q3_K, 8, 512) == 8 * 2 * 110 and capi.device_bytes(capi.Q3_K, 8, 512) == 8 * 2 * 112
+    assert capi.device_bytes(capi.Q2_K, 8, 512) == capi.gguf_bytes(capi.Q2_K, 8, 512) == 8 * 2 * 84
 
 
 # ------------------------------------------------------------------------------------------------ N-API addon + JS

@@ -40,8 +40,8 @@ def test_f16_rounding_matches_numpy(oracle):
     assert oracle.f16_from(float("nan")) & 0x7c00 == 0x7c00 and oracle.f16_from(float("nan")) & 0x3ff
 
 
-@pytest.mark.parametrize("fmt,n", [(refs.Q4_K, 256 * 300), (refs.Q5_K, 256 * 300), (refs.Q6_K, 256 * 300),
-                                   (refs.Q8_0, 32 * 500)])
+@pytest.mark.parametrize("fmt,n", [(refs.Q2_K, 256 * 300), (refs.Q3_K, 256 * 300), (refs.Q4_K, 256 * 300),
+                                   (refs.Q5_K, 256 * 300), (refs.Q6_K, 256 * 300), (refs.Q8_0, 32 * 500)])
 @pytest.mark.parametrize("centered", [False, True])
 def test_dequant_bit_exact_vs_ggml_spec(oracle, fmt, n, centered):
     raw = blocks(fmt, n, 1, centered)
@@ -87,6 +87,45 @@ def test_q5k_known_answer(oracle):
     np.testing.assert_array_equal(got, (j + 1) * (q + 16 * h) - 0.5 * j)
 
 
+def test_q3k_known_answer(oracle):
+    # d = 0.5; 6-bit scale of group s: v_s = (7 s + 5) % 64 (value v_s - 32, negative for some groups), packed as
+    # ggml does (low nibbles of groups 0..7 / high nibbles of 8..15 in bytes 0..7, the top 2 bits of group 4g + k
+    # at bits 2g of byte 8 + k); element e = 128 n + 32 jj + l: q2 = e % 4, hmask bit h = (e // 5) % 2, so the
+    # value is 0.5 (v_s - 32) (q2 - 4 (1 - h))
+    v = (7 * np.arange(16) + 5) % 64
+    b = np.zeros(110, np.uint8)
+    for i in range(8):
+        b[96 + i] = (v[i] & 15) | ((v[i + 8] & 15) << 4)
+    for g in range(4):
+        for k in range(4):
+            b[104 + k] |= ((v[4 * g + k] >> 4) & 3) << (2 * g)
+    b[108:110] = np.array([0.5], np.float16).view(np.uint8)
+    e = np.arange(256)
+    n, jj, l = e // 128, (e % 128) // 32, e % 32
+    q2, h = e % 4, (e // 5) % 2
+    for i in range(256):
+        b[32 + 32 * n[i] + l[i]] |= q2[i] << (2 * jj[i])
+        b[l[i]] |= h[i] << (4 * n[i] + jj[i])
+    want = 0.5 * (v[e // 16] - 32) * (q2 - 4 * (1 - h))
+    np.testing.assert_array_equal(oracle.dequant(refs.Q3_K, b, 256), want.astype(np.float32))
+
+
+def test_q2k_known_answer(oracle):
+    # d = 1, dmin = 0.5; group j: scale j % 16, min (3 j) % 16; q = e % 4: value = (j % 16) q - 0.5 ((3 j) % 16)
+    b = np.zeros(84, np.uint8)
+    j = np.arange(16)
+    b[0:16] = (j % 16) | (((3 * j) % 16) << 4)
+    e = np.arange(256)
+    n, jj, l, q = e // 128, (e % 128) // 32, e % 32, e % 4
+    for i in range(256):
+        b[16 + 32 * n[i] + l[i]] |= q[i] << (2 * jj[i])
+    b[80:82] = np.array([1.0], np.float16).view(np.uint8)
+    b[82:84] = np.array([0.5], np.float16).view(np.uint8)
+    g = e // 16
+    want = (g % 16) * q - 0.5 * ((3 * g) % 16)
+    np.testing.assert_array_equal(oracle.dequant(refs.Q2_K, b, 256), want.astype(np.float32))
+
+
 def test_q6k_known_answer(oracle):
     # d = 1, all scales 1: value = q - 32 with q the 6-bit quant (low 4 bits in ql, high 2 in qh)
     q = (np.arange(256) * 7) % 64
@@ -112,7 +151,8 @@ def test_q8_known_answer(oracle):
 
 
 # ------------------------------------------------------------------------------------------------ matmul
-@pytest.mark.parametrize("fmt,N,K", [(refs.Q4_K, 33, 512), (refs.Q5_K, 21, 512), (refs.Q6_K, 17, 768),
+@pytest.mark.parametrize("fmt,N,K", [(refs.Q2_K, 13, 512), (refs.Q3_K, 15, 768), (refs.Q4_K, 33, 512),
+                                     (refs.Q5_K, 21, 512), (refs.Q6_K, 17, 768),
                                      (refs.Q8_0, 19, 320), (refs.F32, 9, 96)])
 @pytest.mark.parametrize("T,mode", [(1, 0), (3, 0), (9, 1)])
 def test_matmul_vs_float64(oracle, fmt, N, K, T, mode):
@@ -249,7 +289,8 @@ def test_argmax_ties_nan(oracle):
 
 
 # ------------------------------------------------------------------------------------------------ model
-@pytest.mark.parametrize("name,neox", [("mini_llama_q4km_c", 0), ("mini_llama_q5km_c", 0), ("mini_qwen3_q4km_c", 1),
+@pytest.mark.parametrize("name,neox", [("mini_llama_q4km_c", 0), ("mini_llama_q5km_c", 0), ("mini_llama_q3k_c", 0),
+                                       ("mini_llama_q2k_c", 0), ("mini_qwen3_q4km_c", 1),
                                        ("mini_qwen3moe_q5k_c", 1), ("mini_qwen3moe_q4k_c", 1),
                                        ("mini_llama_q8_c", 0)])
 def test_model_forward_vs_float64(oracle, models_dir, name, neox):
