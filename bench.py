@@ -147,9 +147,10 @@ def run_decode(model, path, steps, warmup, prefills, check_n=0, eager=False, see
 def side_configs(steps, warmup, eager):
     """The other decode workloads of the hot path, measured on the same product path (no parity check here; the
     GPU tests pin their parity on smaller models of the same formats): the MoE model (48 layers, 128 experts,
-    top-8, Q4_K) at ctx 2048 and the tiny Q8_0 LLaMA after a 32-token prompt."""
+    top-8, Q4_K) at ctx 2048, the 8B shape in Q5_K_M at ctx 4096 and the tiny Q8_0 LLaMA after a 32-token
+    prompt."""
     out = {}
-    for model, P, n in (("qwen3moe_q4k", 2048, steps), ("tiny_q8", 32, 128)):
+    for model, P, n in (("qwen3moe_q4k", 2048, steps), ("llama8b_q5km", 4096, steps), ("tiny_q8", 32, 128)):
         path = synth.ensure_model(model, model_dir())
         r = run_decode(model, path, n, warmup, [P], eager=eager, seed=11)["runs"][0]
         _, bpt = decode_bytes_per_token(model, path, P, n)

@@ -83,6 +83,9 @@ CONFIGS = {
     # Llama-3-8B shape, Q4_K_M
     "llama8b_q4km": ModelConfig("llama8b_q4km", "llama", 32, 4096, 32, 8, 128, 14336, 128256, 1e-5, 500000.0,
                                 _q4km()),
+    # the same shape in Q5_K_M (Q5_K, with Q6_K for attn_v, ffn_down and output)
+    "llama8b_q5km": ModelConfig("llama8b_q5km", "llama", 32, 4096, 32, 8, 128, 14336, 128256, 1e-5, 500000.0,
+                                _q5km()),
     # Qwen3-30B-A3B-like MoE, Q4_K everywhere except the f32 router
     "qwen3moe_q4k": ModelConfig("qwen3moe_q4k", "qwen3moe", 48, 2048, 32, 4, 128, 0, 151936, 1e-6, 1000000.0,
                                 {"default": GGML_Q4_K}, n_exp=128, n_used=8, ffe=768, qk_norm=True),
