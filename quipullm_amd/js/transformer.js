@@ -57,7 +57,9 @@ class ModeloTransformer {
     this.batch = op.batch || 32;                 // tokens per prefill pass (reference transformer.js:10 uses 32)
     this.kvF16 = !!op.kv_f16;                    // f16 KV cache (the reference keeps it in f32)
     this.eagerDecode = !!op.eager_decode;        // fused step dispatched op by op instead of a captured graph
-    this.attnPorSplit = op.attn_keys_per_split || 128;   // decode attention: keys per workgroup at full context
+    // decode attention: keys per workgroup at full context: 256 (two 32-key tiles per wavefront) while that still
+    // gives at least 64 workgroups (nkv x splits), else 128
+    this.attnPorSplit = op.attn_keys_per_split || (this.nkv * Math.ceil(this.ctx / 256) >= 64 ? 256 : 128);
     this.baldosa = op.tiled_prefill !== false;   // config.json "tiled_prefill"
     this.bufs = [];
     this.pos = 0;
