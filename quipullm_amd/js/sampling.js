@@ -81,8 +81,12 @@ class Muestreador {
     return this.muestrear(cand, val);
   }
 
-  // The device path applies to: stochastic, 1 <= top_k <= 128 and below the vocabulary.
-  usaCandidatosDispositivo(V) { return this.temp > 0 && this.topK >= 1 && this.topK <= 128 && this.topK < V; }
+  // The device path applies to: stochastic, 1 <= top_k <= 128 and below the vocabulary, and partial lists that
+  // fit the device merge (ceil(V / 2048) chunks of top_k + 1 keys, at most 16384).
+  usaCandidatosDispositivo(V) {
+    return this.temp > 0 && this.topK >= 1 && this.topK <= 128 && this.topK < V &&
+      Math.ceil(V / 2048) * (this.topK + 1) <= 16384;
+  }
 
   // sampling.js:58-81 from candidate ids `cand` and their logits `val` (same order).
   muestrear(cand, val) {

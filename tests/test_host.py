@@ -183,7 +183,9 @@ out.greedy = new s.Muestreador({temperature: 0}).esVoraz();
 out.notGreedy = new s.Muestreador({temperature: 0, repeat_penalty: 1.1}).esVoraz();
 const st = new s.Muestreador({temperature: 0.8});
 out.stochastic = !st.esVoraz() && st.usaCandidatosDispositivo(32000) && !st.usaCandidatosDispositivo(40) &&
-  !new s.Muestreador({temperature: 0.8, top_k: 0}).usaCandidatosDispositivo(32000);
+  !new s.Muestreador({temperature: 0.8, top_k: 0}).usaCandidatosDispositivo(32000) &&
+  new s.Muestreador({temperature: 0.8, top_k: 128}).usaCandidatosDispositivo(151936) &&
+  !new s.Muestreador({temperature: 0.8, top_k: 128}).usaCandidatosDispositivo(262144);
 console.log(JSON.stringify(out));
 """ % os.path.join(JS, "sampling.js"))
     assert r["tie"] == 1 and r["nan"] == 1 and r["neg"] == 1
