@@ -1448,6 +1448,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 namespace mm {
 constexpr int TM = 128, TN = 128, TK = 64, LDK = 72;  // LDS rows padded to 72 bf16 (144 B)
 }
+#define QP_NOJOB 0xffffffffu  // a grouped tile's row without a job
 
 // Eight values -> their bf16 high parts and the bf16 of the remainders, each written to LDS as one 16-byte store.
 QP_DEV void split_store8(const float* v, __bf16* hi, __bf16* lo) {
@@ -1488,10 +1489,10 @@ QP_DEV void mm_wload(MmW& r, const QpGemmArgs& g, uint32_t row, bool on, uint32_
         r.c = gload<uint4>(base + (uint64_t)ch * nb * 16);
         r.d = gload<uint4>(base + (uint64_t)(ch + 1) * nb * 16);
         r.e = gload<uint4>(base + (uint64_t)12 * nb * 16);
-        const uint64_t NB = (uint64_t)g.n * nb;
+        const uint64_t NB = (uint64_t)(g.wrows ? g.wrows : g.n) * nb;
         r.f = gload<uint16_t>(g.w + NB * 208 + ((uint64_t)row * nb + b) * 2);
     } else if constexpr (FMT == QP_Q8_0) {
-        const uint64_t NB = (uint64_t)g.n * (K >> 5);
+        const uint64_t NB = (uint64_t)(g.wrows ? g.wrows : g.n) * (K >> 5);
         const uint64_t blk = (uint64_t)row * (K >> 5) + (k0 >> 5) + part;
         const bool in = k0 + 32 * part < K;
         const uint64_t bb = in ? blk : (uint64_t)row * (K >> 5);
@@ -1570,16 +1571,42 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
     const uint32_t base = total >> 3, rem = total & 7, xcd = id & 7, j = id >> 3;
     const uint32_t L = xcd * base + (xcd < rem ? xcd : rem) + j;
     const uint32_t m_tile = L % mt, rest = L / mt, zs = rest % nz, n_tile = rest / nz;
-    const uint32_t t0 = m_tile * TM, n0 = n_tile * TN;
-    if (t0 >= T) return;
+    uint32_t t0 = m_tile * TM;
+    const uint32_t n0 = n_tile * TN;
+    // grouped by expert: this slot's expert and 128 jobs (staged in LDS; an entry past the list or whose x / y row
+    // does not exist is QP_NOJOB and loads row 0, stores nothing)
+    const bool grp = g.lst != 0;
+    __shared__ uint32_t jobs[TM];
+    uint32_t ex = 0;
+    if (grp) {
+        ex = m_tile / g.tpe;
+        t0 = (m_tile % g.tpe) * TM;
+        if (ex >= g.n_exp) return;
+        const uint32_t c0 = min(gload<uint32_t>(g.off + 4ull * ex), g.nlst);
+        const uint32_t c1 = min(gload<uint32_t>(g.off + 4ull * (ex + 1)), g.nlst);
+        const uint32_t cn = c1 > c0 ? c1 - c0 : 0;
+        if (t0 >= cn) return;
+        if (threadIdx.x < TM) {
+            uint32_t jb = QP_NOJOB;
+            if (t0 + threadIdx.x < cn) {
+                const uint32_t j = gload<uint32_t>(g.lst + 4ull * (c0 + t0 + threadIdx.x));
+                if (j / g.tfijo < g.xrows && j < g.yrows) jb = j;
+            }
+            jobs[threadIdx.x] = jb;
+        }
+        __syncthreads();
+    } else if (t0 >= T) {
+        return;
+    }
     const uint32_t kbeg = g.kchunk ? zs * g.kchunk : 0;
     const uint32_t kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t wm = wave >> 1, wn = wave & 1;
     // loader roles: token / row = tid >> 1, 32-element part = tid & 1
     const uint32_t lr = tid >> 1, part = tid & 1;
-    const uint32_t xt = t0 + lr, wr = n0 + lr;
-    const bool xon = xt < T, won = wr < N;
+    const uint32_t wr = n0 + lr, wrow = grp ? ex * N + wr : wr;
+    const bool xon = grp ? jobs[lr] != QP_NOJOB : t0 + lr < T, won = wr < N;
+    const uint32_t xt = grp ? (xon ? jobs[lr] / g.tfijo : 0) : t0 + lr;
     const uint64_t xrow = g.x + 4ull * (uint64_t)(xon ? xt : 0) * K;
 
     f32x16 acc[2][2];
@@ -1612,7 +1639,7 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
                 xr[i] = (k < K) ? gload<float4>(xrow + 4ull * k) : float4{0.f, 0.f, 0.f, 0.f};
             }
         }
-        mm_wload<FMT>(wrg, g, wr, won, k0, part);
+        mm_wload<FMT>(wrg, g, wrow, won, k0, part);
     };
     const uint32_t nsteps = (kend - kbeg + TK - 1) / TK;
     load(kbeg);
@@ -1642,7 +1669,7 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
                 for (int i = 0; i < 4; i++) split_store8(xv + 8 * i, xh_r + 8 * i, xl_r + 8 * i);
             }
             float w[32];
-            mm_wdeq<FMT>(wrg, g, wr, won, k0, part, w);
+            mm_wdeq<FMT>(wrg, g, wrow, won, k0, part, w);
 #pragma unroll
             for (int i = 0; i < 32; i++) w[i] = won ? w[i] : 0.f;
             __bf16* wh_r = wh + lr * LDK;
@@ -1697,9 +1724,10 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
             const uint32_t n = n0 + wn * 64 + b * 32 + (lane & 31);
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const uint32_t t = t0 + wm * 64 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                if (t < T && n < N) {
-                    float* o = Y + (uint64_t)t * N + n;
+                const uint32_t lt = wm * 64 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3), t = t0 + lt;
+                const uint32_t row = grp ? jobs[lt] : t;
+                if ((grp ? row != QP_NOJOB : t < T) && n < N) {
+                    float* o = Y + (uint64_t)row * N + n;
                     *o = add ? *o + acc[a][b][v] : acc[a][b][v];
                 }
             }
@@ -2153,6 +2181,57 @@ KERNEL __launch_bounds__(256) void qp_moe_comb(QpCombArgs a) {
         for (uint32_t s = 0; s < a.k; s++)
             acc = acc + cptr<float>(a.wts)[t * a.k + s] * cptr<float>(a.de)[((uint64_t)t * a.k + s) * a.d + c];
         mptr<float>(a.x)[i] = mptr<float>(a.x)[i] + acc;
+    }
+}
+
+// Reference moe_group (kds.js:491-516): the jobs i < T*n of each expert e < n_exp, in increasing i, listed at
+// lst[off[e] .. off[e + 1]).  One workgroup: thread t takes the contiguous jobs [t*c, t*c + c) and counts them per
+// expert in its own LDS row (16-bit counts, c <= 65535); each expert's counts become running offsets over t; the
+// experts' totals are scanned into off; a second pass over the same jobs writes each at off[e] + its running
+// offset.  The order within an expert is the jobs' order, the reference's.  LDS: 256 * n_exp * 2 + 2 KB.
+KERNEL __launch_bounds__(256) void qp_moe_group(QpMoeGroupArgs a) {
+    extern __shared__ float4 smg[];
+    uint16_t* cnt = reinterpret_cast<uint16_t*>(smg);  // [256][n_exp]
+    uint32_t* base = reinterpret_cast<uint32_t*>(cnt + 256 * a.n_exp + (a.n_exp & 1));  // [n_exp]
+    const uint32_t tid = threadIdx.x, E = a.n_exp;
+    uint64_t nj64 = (uint64_t)paso_T(a.paso) * a.n;
+    const uint32_t nj = (uint32_t)(nj64 < a.nsel ? nj64 : a.nsel);
+    const uint32_t c = (nj + 255) / 256, i0 = min(nj, tid * c), i1 = min(nj, i0 + c);
+    uint16_t* mine = cnt + tid * E;
+    for (uint32_t e = 0; e < E; e++) mine[e] = 0;
+    for (uint32_t i = i0; i < i1; i++) {
+        const uint32_t e = gload<uint32_t>(a.sel + 4ull * i);
+        if (e < E) mine[e] = (uint16_t)(mine[e] + 1);
+    }
+    __syncthreads();
+    if (tid < E) {
+        uint32_t run = 0;
+        for (uint32_t t = 0; t < 256; t++) {
+            const uint32_t v = cnt[t * E + tid];
+            cnt[t * E + tid] = (uint16_t)run;  // (fits: nsel < 65536)
+            run += v;
+        }
+        base[tid] = run;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t acc = 0;
+        for (uint32_t e = 0; e < E; e++) {
+            const uint32_t v = base[e];
+            base[e] = acc;
+            gstore<uint32_t>(a.off + 4ull * e, acc);
+            acc += v;
+        }
+        gstore<uint32_t>(a.off + 4ull * E, acc);
+    }
+    __syncthreads();
+    for (uint32_t i = i0; i < i1; i++) {
+        const uint32_t e = gload<uint32_t>(a.sel + 4ull * i);
+        if (e < E) {
+            const uint32_t r = mine[e];
+            mine[e] = (uint16_t)(r + 1);
+            gstore<uint32_t>(a.lst + 4ull * (base[e] + r), i);
+        }
     }
 }
 

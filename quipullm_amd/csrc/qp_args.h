@@ -96,8 +96,20 @@ typedef struct {
     uint32_t tfix;    // 0: T from paso
     uint32_t kchunk;  // matrix-core path: inputs per K split (grid z = splits; a multiple of 64), or 0: all of k
     uint32_t rows;    // matrix-core path: token rows the xs planes and the ws partials are sized for (>= T)
-    uint32_t pad;
+    uint32_t wrows;   // rows of the weight tensor (the Q6_K / Q8_0 scale arrays follow them), or 0: n
+    // grouped by expert (matmul_*_eg): lst != 0.  Grid y = n_exp * tpe slots; slot s takes tile s % tpe (128 jobs)
+    // of expert s / tpe, jobs lst[off[e] ..off[e + 1]); job j reads x row j / tfijo and writes y row j, weights
+    // rows e * n .. of the stacked tensor.  xrows, yrows, nlst: rows of x, y and entries of lst that exist.
+    uint64_t lst, off;
+    uint32_t n_exp, tpe, tfijo, xrows, yrows, nlst;
 } QpGemmArgs;
+
+// moe_group: lst[off[e] .. off[e + 1]) = the jobs i < T * n (in increasing order) with sel[i] == e, e < n_exp;
+// off[n_exp] = the number listed.  nsel: entries of sel and lst that exist.
+typedef struct {
+    uint64_t sel, lst, off, paso;
+    uint32_t n_exp, n, nsel, pad;
+} QpMoeGroupArgs;
 // x [T][k] -> bf16 high / low planes (hi = bf16(v), lo = bf16(v - hi)) at xs and xs + 2*rows*k.
 typedef struct { uint64_t x, xs, paso; uint32_t k, rows; } QpSplitArgs;
 // y[t][n] = (acc ? y : 0) + sum over s (in order) of ws[s][t][n].

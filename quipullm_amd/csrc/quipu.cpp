@@ -655,6 +655,80 @@ int op_moe_comb(const Ctx& c) {
     return launch(K_moe_comb, c.gx ? (c.gx > 4096 ? 4096 : c.gx) : 1, 1, 1, 256, 0, a);
 }
 
+// Bytes from p to the end of the library buffer that holds it (0: not inside one).
+uint64_t buf_room(uint64_t p) {
+    for (const auto& kv : g_allocs)
+        if (p >= kv.first && p < kv.first + kv.second) return kv.first + kv.second - p;
+    return 0;
+}
+
+// moe_group (kds.js:491-516): P{E, n}; [paso, sel, lst, off]; one workgroup.  lst[off[e] .. off[e+1]) = the jobs
+// i < T*n with sel[i] == e, in increasing order.
+int op_moe_group(const Ctx& c) {
+    if (int e = need_bufs(c, 4, "moe_group")) return e;
+    QpMoeGroupArgs a = {};
+    a.n_exp = c.U(0);
+    a.n = c.U(1);
+    a.paso = c.B(0);
+    a.sel = c.B(1);
+    a.lst = c.B(2);
+    a.off = c.B(3);
+    if (a.n_exp == 0 || a.n_exp > 256 || a.n == 0) return fail(QP_E_ARG, "moe_group: E=%u n=%u", a.n_exp, a.n);
+    const uint64_t rs = buf_room(a.sel), rl = buf_room(a.lst), ro = buf_room(a.off);
+    if (!rs || !rl || !ro) return fail(QP_E_ARG, "moe_group: sel, lst and off must be library buffers");
+    if (ro < 4ull * (a.n_exp + 1)) return fail(QP_E_ARG, "moe_group: off holds %llu bytes, E+1 entries need %u",
+                                               (unsigned long long)ro, 4 * (a.n_exp + 1));
+    const uint64_t ns = (rs < rl ? rs : rl) / 4;
+    if (ns > 65535) return fail(QP_E_ARG, "moe_group: sel and lst hold %llu jobs; at most 65535", (unsigned long long)ns);
+    a.nsel = (uint32_t)ns;
+    return launch(K_moe_group, 1, 1, 1, 256, 256 * a.n_exp * 2 + 4 + 4 * a.n_exp, a);
+}
+
+// matmul_<fmt>_eg (kquants.js:386-460, the expert matmul grouped by expert): P{N, K, acc, tfijo};
+// [paso, w, x, y, lst, off] (q8: [paso, qs, ds, x, y, lst, off]), dispatched as (ceil(N/64), E, ceil(T/32)).
+// y[j][r] (+)= W[e*N + r] . x[j / tfijo] for every job j of expert e (lst / off from moe_group), on the matrix
+// cores: 128 jobs x 128 rows per workgroup, E * ceil(32*gz / 128) job tiles.
+int op_matmul_eg(const Ctx& c, int fmt, const char* name) {
+    const bool q8 = fmt == QP_Q8_0;
+    if (int e = need_bufs(c, q8 ? 7 : 6, name)) return e;
+    const uint32_t N = c.U(0), K = c.U(1), acc = c.U(2), tfijo = c.U(3), E = c.gy, tz = c.gz;
+    if (int e = check_k(fmt, K, name)) return e;
+    if (N == 0 || tfijo == 0 || E == 0 || tz == 0)
+        return fail(QP_E_ARG, "%s: N=%u tfijo=%u, dispatch y (experts)=%u z=%u", name, N, tfijo, E, tz);
+    if (q8)
+        if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)E * N * K / 32, name)) return e;
+    if (is_kq(fmt) && kq_tensor_bytes(fmt, (uint64_t)E * N, K) >= (1ull << 31))
+        return fail(QP_E_ARG, "%s: expert tensor is 2 GiB or larger", name);
+    QpGemmArgs a = {};
+    uint32_t i = 1;
+    a.w = c.B(i++);
+    if (q8) i++;
+    a.x = c.B(i++);
+    a.y = c.B(i++);
+    a.lst = c.B(i++);
+    a.off = c.B(i++);
+    a.paso = c.B(0);
+    a.fmt = fmt;
+    a.n = N;
+    a.k = K;
+    a.acc = acc;
+    a.wrows = E * N;
+    a.n_exp = E;
+    a.tfijo = tfijo;
+    const uint64_t rx = buf_room(a.x), ry = buf_room(a.y), rl = buf_room(a.lst), ro = buf_room(a.off);
+    if (!rx || !ry || !rl || !ro) return fail(QP_E_ARG, "%s: x, y, lst and off must be library buffers", name);
+    if (ro < 4ull * (E + 1)) return fail(QP_E_ARG, "%s: off holds fewer than E+1 = %u entries", name, E + 1);
+    auto cap = [](uint64_t v) { return (uint32_t)(v > 0xffffffffull ? 0xffffffffull : v); };
+    a.xrows = cap(rx / (4ull * K));
+    a.yrows = cap(ry / (4ull * N));
+    a.nlst = cap(rl / 4);
+    a.tpe = cdiv(32 * tz, 128);
+    if ((uint64_t)E * a.tpe > 65535) return fail(QP_E_ARG, "%s: %u experts x %u job tiles", name, E, a.tpe);
+    const Kid k = fmt == QP_Q4_K ? K_gemm_mfma_q4k : fmt == QP_Q6_K ? K_gemm_mfma_q6k
+                : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
+    return launch(k, cdiv(N, 128), E * a.tpe, 1, 256, 0, a);
+}
+
 // ------------------------------------------------------------------------------------------------ backend ops
 // gemv: fused one-token GEMV over up to 4 same-format segments.
 // P{nseg, K, eps, last_row, R, max_wg, fmt, 0, then per segment {mode | seg_fmt << 8, n, row_base, rows_total}};
@@ -922,6 +996,12 @@ void register_ops() {
     v.push_back({"swiglu", op_swiglu});
     v.push_back({"moe_topk", op_moe_topk});
     v.push_back({"moe_comb", op_moe_comb});
+    v.push_back({"moe_group", op_moe_group});
+    for (const char* f : {"q4k", "q6k", "q8", "f32"}) {
+        const int fmt = fmt_of(f);
+        const std::string n = std::string("matmul_") + f + "_eg";
+        v.push_back({n, [fmt, n](const Ctx& c) { return op_matmul_eg(c, fmt, n.c_str()); }});
+    }
     v.push_back({"moe_gate_up_q4k", [](const Ctx& c) { return op_moe(c, QP_Q4_K, false, "moe_gate_up_q4k"); }});
     v.push_back({"moe_gate_up_q6k", [](const Ctx& c) { return op_moe(c, QP_Q6_K, false, "moe_gate_up_q6k"); }});
     v.push_back({"moe_down_q4k", [](const Ctx& c) { return op_moe(c, QP_Q4_K, true, "moe_down_q4k"); }});

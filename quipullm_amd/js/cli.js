@@ -7,6 +7,7 @@
 //                        [--temperature T] [--top-k K] [--top-p P] [--min-p M] [--seed S]
 //   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
 //                        [--warmup W] [--prefill P1,P2] [--eager] [--sample] [--keys-per-split N]
+//                        [--no-moe-grouped]
 //                        [--check-prompt-file ids.json --check-n N --check-logits file.f32]
 //
 // generate prints one JSON line {ids, prompt_ms, decode_ms, tps}; with --logits-out the logits each token was
@@ -40,6 +41,7 @@ async function cargar(o) {
   if (o['max-gen']) options.max_gen = parseInt(o['max-gen'], 10);
   if (o.eager) options.eager_decode = true;
   if (o['keys-per-split']) options.attn_keys_per_split = parseInt(o['keys-per-split'], 10);
+  if (o['no-moe-grouped']) options.moe_grouped = false;
   return engine.cargarModelo(o.model, { ctx: o.ctx ? parseInt(o.ctx, 10) : undefined, options: options });
 }
 

@@ -16,6 +16,7 @@ const { CargadorPesos } = require('./weights');
 const ROPE_NEOX = new Set(['qwen2', 'qwen3', 'qwen3moe', 'phi3', 'gemma', 'gemma2', 'gemma3', 'stablelm', 'olmo2']);
 const KQ = new Set(['q2k', 'q3k', 'q4k', 'q5k', 'q6k']);
 const MEZCLA = new Set(['q4k', 'q6k']);    // formats whose GEMV segments may share one launch
+const EG = new Set(['q4k', 'q6k', 'q8', 'f32']);   // formats with a grouped expert matmul (matmul_<fmt>_eg)
 const FMT_ID = { f32: 0, q8: 8, q2k: 10, q3k: 11, q4k: 12, q5k: 13, q6k: 14 };
 // gemv segment modes (qp_args.h)
 const STORE = 0, ACC = 1, SWIGLU = 2, ARGMAX = 3;
@@ -61,6 +62,9 @@ class ModeloTransformer {
     // gives at least 64 workgroups (nkv x splits), else 128
     this.attnPorSplit = op.attn_keys_per_split || (this.nkv * Math.ceil(this.ctx / 256) >= 64 ? 256 : 128);
     this.baldosa = op.tiled_prefill !== false;   // config.json "tiled_prefill"
+    // MoE prompt batches of 8 or more tokens grouped by expert on the matrix cores (moe_group + matmul_*_eg, the
+    // reference's deepseek2.js:353-378); false: one job per (token, expert) on the expert GEMV
+    this.agrupado = op.moe_grouped !== false;
     this.bufs = [];
     this.pos = 0;
     this.grafo = null;
@@ -142,6 +146,8 @@ class ModeloTransformer {
       this.sel = B(4 * TB * this.nUsados, 'sel');
       this.wts = B(4 * TB * this.nUsados, 'wts');
       this.de = B(4 * TB * this.nUsados * D, 'de');
+      this.lst = B(4 * TB * this.nUsados, 'lst');
+      this.off = B(4 * (this.nExp + 1), 'off');
     }
     this.xl = B(4 * D, 'xlast');
     this.logits = B(4 * this.vocab, 'logits');
@@ -187,7 +193,10 @@ class ModeloTransformer {
     const gpu = this.gpu;
     const u = gpu.uniforme([['u', W.N / this.nExp], ['u', W.K], ['u', 0], ['u', tfijo], ['u', this.nExp]]);
     const wb = W.tipo === 'q8' ? [W.qs, W.ds] : [W.w];
-    return { g: gpu.grupo('matmul_' + W.tipo + '_e', [u, this.bPaso].concat(wb, [x, y, this.sel])), filas: W.N / this.nExp };
+    // grouped by expert (the reference's matmul_<fmt>_eg: P{N, K, acc, tfijo}; [paso, w, x, y, lst, off])
+    const ug = gpu.uniforme([['u', W.N / this.nExp], ['u', W.K], ['u', 0], ['u', tfijo]]);
+    const gg = EG.has(W.tipo) ? gpu.grupo('matmul_' + W.tipo + '_eg', [ug, this.bPaso].concat(wb, [x, y, this.lst, this.off])) : null;
+    return { g: gpu.grupo('matmul_' + W.tipo + '_e', [u, this.bPaso].concat(wb, [x, y, this.sel])), gg: gg, filas: W.N / this.nExp };
   }
 
   _embedGrupo(ids, y) {
@@ -229,6 +238,8 @@ class ModeloTransformer {
         gc.eact = gpu.grupo('swiglu', [gpu.uniforme([['u', K * this.ffe]]), P, this.g, this.u]);
         gc.ed = this._mmE(c.ed, this.g, this.de, 1);
         gc.comb = gpu.grupo('moe_comb', [gpu.uniforme([['u', D], ['u', K]]), P, this.x, this.de, this.wts]);
+        gc.grupar = gpu.grupo('moe_group', [gpu.uniforme([['u', this.nExp], ['u', K]]), P, this.sel, this.lst, this.off]);
+        gc.agrupado = !!(gc.eg.gg && gc.eu.gg && gc.ed.gg);
       } else {
         gc.gate = this._mm(c.gate, this.xn, this.g, 0);
         gc.up = this._mm(c.up, this.xn, this.u, 0);
@@ -288,7 +299,13 @@ class ModeloTransformer {
       if (this.nExp) {
         mm(gc.router);
         despachar(null, gc.topk, Math.ceil(T / 64));
-        const e = function (m) { const xy = dim2(Math.ceil(m.filas / 8)); despachar(null, m.g, xy[0], xy[1], T * self.nUsados); };
+        const gr = T >= 8 && gc.agrupado && this.agrupado;
+        if (gr) despachar(null, gc.grupar, 1);
+        const e = function (m) {
+          if (gr) { despachar(null, m.gg, Math.ceil(m.filas / 64), self.nExp, Math.ceil(T / 32)); return; }
+          const xy = dim2(Math.ceil(m.filas / 8));
+          despachar(null, m.g, xy[0], xy[1], T * self.nUsados);
+        };
         e(gc.eg); e(gc.eu);
         despachar(null, gc.eact, filas(this.nUsados * this.ffe));
         e(gc.ed);

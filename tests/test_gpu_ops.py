@@ -292,6 +292,67 @@ def test_matmul_prefill_mfma(quipu, dev, oracle, fmt, T, N, K, acc):
     assert np.all(np.abs(got - want) <= bound)
 
 
+def group_jobs(sel, E):
+    """moe_group's result from its definition: per expert, the job indices holding it, in increasing order."""
+    lst = [i for e in range(E) for i in range(len(sel)) if sel[i] == e]
+    cnt = np.bincount(np.asarray(sel, np.int64)[np.asarray(sel) < E], minlength=E)
+    return np.array(lst, np.uint32), np.concatenate([[0], np.cumsum(cnt)]).astype(np.uint32)
+
+
+@pytest.mark.parametrize("E,k,T", [(16, 4, 70), (128, 8, 300), (7, 1, 1)])
+def test_moe_group(quipu, dev, E, k, T):
+    """moe_group (kds.js:491-516): jobs listed per expert in increasing order, off the running counts; one expert
+    takes more than half of the tokens, several none; an id >= E (not a valid expert) is not listed."""
+    rng = np.random.default_rng(E + T)
+    sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint32).ravel()
+    if T > 2:
+        sel[0:T * k // 2:k] = 3 % E  # a popular expert (first slot of half the tokens)
+        sel[k * (T - 1)] = E + 5      # not an expert
+    lst_want, off_want = group_jobs(sel, E)
+    sb, lb, ob = dev.buf(sel), dev.zeros(4 * T * k), dev.zeros(4 * (E + 1))
+    quipu.dispatch("moe_group", [("u", E), ("u", k)], [dev.paso(T, 0), sb, lb, ob])
+    off = dev.get(ob, (E + 1,), np.uint32)
+    assert off.tolist() == off_want.tolist()
+    assert dev.get(lb, (T * k,), np.uint32)[:int(off[E])].tolist() == lst_want.tolist()
+
+
+@pytest.mark.parametrize("fmt", [capi.Q4_K, capi.Q6_K, capi.Q8_0, capi.F32])
+@pytest.mark.parametrize("tfijo,acc", [(4, 0), (1, 1)])
+def test_matmul_grouped_by_expert(quipu, dev, oracle, fmt, tfijo, acc):
+    """matmul_<fmt>_eg (kquants.js:386-460): the expert matmul over the job lists of moe_group, on the matrix cores.
+    Expert 2 has 150 jobs (two job tiles), several experts none; rows N = 200 (a partial row tile).  tfijo = 4:
+    job j reads input row j / 4 (gate/up); tfijo = 1 with acc: row j, added to y (down)."""
+    E, N, K, k = 8, 200, 512, 4
+    T = 160 if tfijo > 1 else 40
+    rng = np.random.default_rng(9)
+    njob = T * k
+    sel = np.stack([rng.choice([0, 2, 3, 5], k, replace=False) for _ in range(T)]).astype(np.uint32).ravel()
+    sel[2::k] = 2                          # expert 2 in every token (150+ jobs)
+    sel[1::k] = np.where(sel[1::k] == 2, 7, sel[1::k])
+    raw = raw_matrix(fmt, E * N, K, 31)
+    W = (oracle.dequant(fmt, raw, E * N * K) if fmt != capi.F32 else raw.view(np.float32)).reshape(E, N, K)
+    xr = njob // tfijo
+    x = rng.standard_normal((xr, K)).astype(np.float32)
+    y0 = rng.standard_normal((njob, N)).astype(np.float32)
+    sb, lb, ob = dev.buf(sel), dev.zeros(4 * njob), dev.zeros(4 * (E + 1))
+    quipu.dispatch("moe_group", [("u", E), ("u", k)], [dev.paso(T, 0), sb, lb, ob])
+    hw = dev.matrix(fmt, raw, E * N, K)
+    wb = [hw, hw + E * N * K] if fmt == capi.Q8_0 else [hw]
+    yb = dev.buf(y0)
+    u = [("u", N), ("u", K), ("u", acc), ("u", tfijo)]
+    quipu.dispatch("matmul_%s_eg" % capi.FMT_NAME[fmt], u, [dev.paso(T, 0)] + wb + [dev.buf(x), yb, lb, ob],
+                   ((N + 63) // 64, E, (T + 31) // 32))
+    got = dev.get(yb, (njob, N))
+    for j in range(njob):
+        e = int(sel[j])
+        if e >= E:
+            continue
+        xv = x[j // tfijo].astype(np.float64)
+        want = W[e].astype(np.float64) @ xv + (y0[j] if acc else 0)
+        bound = 2e-5 * (np.abs(W[e].astype(np.float64)) @ np.abs(xv)) + 2e-7 * np.abs(y0[j]) + 1e-30
+        assert np.all(np.abs(got[j] - want) <= bound), (j, e, np.abs(got[j] - want).max())
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 def test_matmul_expert_jobs(quipu, dev, oracle, fmt):
     """matmul_<fmt>_e (one job per selected expert) and the fused gate/up _e_swiglu; tfijo = k routes job z to
