@@ -372,13 +372,13 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
                     : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
         uint32_t mt = cdiv(tmax, 128);
         const uint32_t nt = cdiv(N, 128);
-        if (is_kq(fmt) && !g_capturing) {
-            // K-quants: x split into bf16 planes once (not in every weight tile's workgroup), and the K range split
-            // when the tiles alone cannot occupy the CUs; partials summed in order.  From 256 tokens on, 256-token
-            // tiles (one 512-thread workgroup per CU, K steps of 32 double-buffered in LDS) dequantize each weight
-            // tile half as often.
+        if (!g_capturing) {
+            // x split into bf16 planes once (not in every weight tile's workgroup), and the K range split when the
+            // tiles alone cannot occupy the CUs (a 128-row router at 2048 tokens is 16 tiles); partials summed in
+            // order.  K-quants from 256 tokens on: 256-token tiles (one 512-thread workgroup per CU, K steps of 32
+            // double-buffered in LDS) dequantize each weight tile half as often.
             // Q5_K, Q3_K and Q2_K have only the 256-token tiles
-            const bool big = tmax >= 256 || fmt == QP_Q5_K || fmt == QP_Q3_K || fmt == QP_Q2_K;
+            const bool big = is_kq(fmt) && (tmax >= 256 || fmt == QP_Q5_K || fmt == QP_Q3_K || fmt == QP_Q2_K);
             if (big) mt = cdiv(tmax, 256);
             const uint32_t steps = K / 64, slots = (big ? 1 : 2) * (uint32_t)g_cus;
             uint32_t ns = 1;
