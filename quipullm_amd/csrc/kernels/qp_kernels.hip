@@ -2066,18 +2066,29 @@ KERNEL __launch_bounds__(256) void qp_rmsnorm(QpRmsArgs a) {
 }
 
 // ====================================================================================== norm + RoPE
-// Reference norm_rope (gpu.js:394-444): grid (heads, T), one wavefront per head vector.
-KERNEL __launch_bounds__(64) void qp_norm_rope(QpRopeArgs a) {
-    __shared__ float v[256];
-    const uint32_t h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+// Reference norm_rope (gpu.js:394-444), one wavefront per head vector.
+QP_DEV void wave_norm_rope_f(float* v, const float* w, uint32_t hd, bool use_norm, float eps, float pos_esc,
+                             const float* freq, uint32_t nrot, bool neox, int lane);
+
+// grid (ceil(nh / 4), T): wavefront i of a workgroup takes head 4*blockIdx.x + i of token blockIdx.y.  The
+// frequency table base^(-2j/nrot) (each value rounded once to float from double, as rope_elem computes it per
+// element) is built once per workgroup.
+KERNEL __launch_bounds__(256) void qp_norm_rope(QpRopeArgs a) {
+    __shared__ float v[4][256];
+    __shared__ float freq[128];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = blockIdx.x * 4 + wave, t = blockIdx.y;
     if (t >= paso_T(a.paso)) return;
+    if (threadIdx.x < a.nrot / 2)
+        freq[threadIdx.x] = (float)pow((double)a.base, (double)((-2.0f * (float)threadIdx.x) / (float)a.nrot));
+    __syncthreads();
+    if (h >= a.nh) return;
     float* row = mptr<float>(a.v) + ((uint64_t)t * a.nh + h) * a.hd;
-    for (uint32_t i = lane; i < a.hd; i += 64) v[i] = row[i];
+    for (uint32_t i = lane; i < a.hd; i += 64) v[wave][i] = row[i];
     __builtin_amdgcn_wave_barrier();
     const float pos = (float)(paso_pos(a.paso) + t);
-    wave_norm_rope(v, a.w ? cptr<float>(a.w) : nullptr, a.hd, a.use_norm != 0, a.eps, pos * a.esc, a.base, a.nrot,
-                   a.neox != 0, (int)lane);
-    for (uint32_t i = lane; i < a.hd; i += 64) row[i] = v[i];
+    wave_norm_rope_f(v[wave], a.w ? cptr<float>(a.w) : nullptr, a.hd, a.use_norm != 0, a.eps, pos * a.esc, freq,
+                     a.nrot, a.neox != 0, (int)lane);
+    for (uint32_t i = lane; i < a.hd; i += 64) row[i] = v[wave][i];
 }
 
 // ====================================================================================== KV write

@@ -502,7 +502,7 @@ int op_norm_rope(const Ctx& c) {
     a.paso = c.B(0);
     a.v = c.B(1);
     a.w = c.B(2);
-    return launch(K_norm_rope, a.nh, c.gy, 1, 64, 0, a);
+    return launch(K_norm_rope, cdiv(a.nh, 4), c.gy, 1, 256, 0, a);
 }
 
 // kv_write (gpu.js:447-466): P{kvd, cap, f16, rows}; [paso, k, v, kc, vc].  rows = cache slots (required).
