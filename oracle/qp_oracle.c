@@ -430,17 +430,123 @@ static float row_serial(int fmt, const uint8_t* row, int K, const float* x) {
     return c;
 }
 
+/* One row dequantized with the values the element functions give (row_serial's w): Q4_K and Q6_K hoist the
+ * per-sub-block factors, which the element functions recompute with the same operations. */
+static void row_deq(int fmt, const uint8_t* row, int K, float* w) {
+    if (fmt == OR_Q4_K) {
+        for (int b = 0; b < K / 256; b++) {
+            const uint8_t* blk = row + (size_t)b * 144;
+            for (int j = 0; j < 8; j++) {
+                float fd, fm;
+                q4k_scmin(blk, j, &fd, &fm);
+                const uint8_t* qb = blk + 16 + (j >> 1) * 32;
+                const int sh = (j & 1) * 4;
+                for (int l = 0; l < 32; l++) {
+                    float a = fd * (float)((qb[l] >> sh) & 15u);
+                    w[b * 256 + j * 32 + l] = a - fm;
+                }
+            }
+        }
+    } else if (fmt == OR_Q6_K) {
+        for (int b = 0; b < K / 256; b++) {
+            const uint8_t* blk = row + (size_t)b * 210;
+            for (int s = 0; s < 16; s++) {
+                const float sc = q6k_scale(blk, s);
+                for (int e = s * 16; e < s * 16 + 16; e++) {
+                    int h = e >> 7, r = e & 127, qd = r >> 5, l = r & 31;
+                    unsigned lo = (blk[h * 64 + (qd & 1) * 32 + l] >> ((qd >> 1) * 4)) & 15u;
+                    unsigned hi = (blk[128 + h * 32 + l] >> (qd * 2)) & 3u;
+                    float q = (float)(lo | (hi << 4)) - 32.0f;
+                    w[b * 256 + e] = sc * q;
+                }
+            }
+        }
+    } else {
+        for (int k = 0; k < K; k++) {
+            float v;
+            if (fmt == OR_Q5_K) v = q5k_deq(row + (size_t)(k >> 8) * 176, k & 255);
+            else if (fmt == OR_Q3_K) v = q3k_deq(row + (size_t)(k >> 8) * 110, k & 255);
+            else if (fmt == OR_Q2_K) v = q2k_deq(row + (size_t)(k >> 8) * 84, k & 255);
+            else if (fmt == OR_Q8_0) v = q8_deq(row + (size_t)(k >> 5) * 34, k & 31);
+            else v = ((const float*)row)[k];
+            w[k] = v;
+        }
+    }
+}
+
+/* The serial order of row_serial for many (row, token) pairs at once: out(t, r) = sum over k = 0..K-1, in that
+ * order, of w_r[k] * x_t[k], every product and sum rounded separately.  Rows row0 .. row0+N-1 of W are
+ * dequantized once per call (4 at a time); xT holds the inputs transposed, [K][ntp] (ntp = nt rounded up to 16,
+ * zero padded), so the sums of 16 tokens advance together in vector lanes (each token's own operation sequence
+ * is unchanged: lanes do not mix).  Token t's value for row r goes to y[yoff[t] + r] (added to it after the sum
+ * when acc, as row_serial's callers do). */
+#define OR_TB 16
+__attribute__((target_clones("avx2", "default")))
+static void serial_rows(int fmt, const uint8_t* W, size_t rb, size_t row0, int N, int K, const float* xT, int nt,
+                        float* y, const size_t* yoff, int acc) {
+    const int ntp = (nt + OR_TB - 1) / OR_TB * OR_TB;
+#pragma omp parallel
+    {
+        float* w = (float*)calloc((size_t)4 * K, 4);
+#pragma omp for schedule(dynamic, 1)
+        for (int r0 = 0; r0 < N; r0 += 4) {
+            const int nr = N - r0 < 4 ? N - r0 : 4;
+            for (int i = 0; i < nr; i++) row_deq(fmt, W + rb * (row0 + (size_t)r0 + i), K, w + (size_t)i * K);
+            for (int tb = 0; tb < ntp; tb += OR_TB) {
+                float c[4][OR_TB];
+                memset(c, 0, sizeof(c));
+                for (int k = 0; k < K; k++) {
+                    const float* xk = xT + (size_t)k * ntp + tb;
+                    for (int i = 0; i < 4; i++) {
+                        const float wv = w[(size_t)i * K + k];
+                        for (int j = 0; j < OR_TB; j++) c[i][j] = c[i][j] + wv * xk[j];
+                    }
+                }
+                for (int i = 0; i < nr; i++)
+                    for (int j = 0; j < OR_TB && tb + j < nt; j++) {
+                        float* o = y + yoff[tb + j] + r0 + i;
+                        *o = acc ? *o + c[i][j] : c[i][j];
+                    }
+            }
+        }
+        free(w);
+    }
+}
+
+/* [K][ntp] transpose of nt input rows (row j at xrows[j]), zero padded to a multiple of 16 tokens. */
+static float* transpose_in(const float* const* xrows, int nt, int K) {
+    const int ntp = (nt + OR_TB - 1) / OR_TB * OR_TB;
+    float* xT = (float*)calloc((size_t)K * ntp, 4);
+    for (int j = 0; j < nt; j++)
+        for (int k = 0; k < K; k++) xT[(size_t)k * ntp + j] = xrows[j][k];
+    return xT;
+}
+
 /* y[t][r] (+)= W[r] . x[t].  mode 0 = per-token lane order (matmul_*_1 and matmul_*_4, whose per-token
- * sums are identical), mode 1 = tiled serial order (matmul_*_t, used by transformer.js:276-279 when T>=8). */
+ * sums are identical), mode 1 = tiled serial order (matmul_*_t, used by transformer.js:276-279 when T>=8),
+ * computed by serial_rows; mode 2 = the same serial order one (token, row) at a time with the element
+ * functions (row_serial: the definition mode 1 is checked against). */
 void or_matmul(int fmt, const uint8_t* W, int N, int K, const float* x, int T, float* y, int acc, int mode) {
     size_t rb = row_bytes(fmt, K);
+    if (mode == 1) {
+        const float** xr = (const float**)malloc(sizeof(float*) * (size_t)T);
+        size_t* yo = (size_t*)malloc(sizeof(size_t) * (size_t)T);
+        for (int t = 0; t < T; t++) {
+            xr[t] = x + (size_t)t * K;
+            yo[t] = (size_t)t * N;
+        }
+        float* xT = transpose_in(xr, T, K);
+        serial_rows(fmt, W, rb, 0, N, K, xT, T, y, yo, acc);
+        free(xT); free(xr); free(yo);
+        return;
+    }
     for (int t = 0; t < T; t++) {
         const float* xt = x + (size_t)t * K;
         float* yt = y + (size_t)t * N;
 #pragma omp parallel for schedule(static)
         for (int r = 0; r < N; r++) {
             const uint8_t* row = W + rb * (size_t)r;
-            float v = mode == 1 ? row_serial(fmt, row, K, xt) : row_dot(fmt, row, K, xt);
+            float v = mode == 2 ? row_serial(fmt, row, K, xt) : row_dot(fmt, row, K, xt);
             yt[r] = acc ? yt[r] + v : v;
         }
     }
@@ -448,17 +554,39 @@ void or_matmul(int fmt, const uint8_t* W, int N, int K, const float* x, int T, f
 
 /* Gathered expert GEMV (kquants.js:256-304, kds.js:110-186): job z uses expert sel[z], row ex*N + r of the
  * stacked tensor, input row z / tfijo; output y[z*N + r].  mode 1 = grouped-tile serial order
- * (kquants.js:392-479, used for T >= 8 by deepseek2.js:377-381). */
+ * (kquants.js:392-479, used for T >= 8 by deepseek2.js:377-381): the jobs of each expert together through
+ * serial_rows (its rows dequantized once); mode 2 = the same order one (job, row) at a time. */
 void or_matmul_e(int fmt, const uint8_t* W, int N, int K, const float* x, const uint32_t* sel, int njobs,
                  int tfijo, float* y, int mode) {
     size_t rb = row_bytes(fmt, K);
+    if (mode == 1) {
+        uint32_t emax = 0;
+        for (int z = 0; z < njobs; z++) emax = sel[z] > emax ? sel[z] : emax;
+        const float** xr = (const float**)malloc(sizeof(float*) * (size_t)njobs);
+        size_t* yo = (size_t*)malloc(sizeof(size_t) * (size_t)njobs);
+        for (uint32_t e = 0; e <= emax; e++) {
+            int nj = 0;
+            for (int z = 0; z < njobs; z++)
+                if (sel[z] == e) {
+                    xr[nj] = x + (size_t)(z / tfijo) * K;
+                    yo[nj] = (size_t)z * N;
+                    nj++;
+                }
+            if (!nj) continue;
+            float* xT = transpose_in(xr, nj, K);
+            serial_rows(fmt, W, rb, (size_t)e * N, N, K, xT, nj, y, yo, 0);
+            free(xT);
+        }
+        free(xr); free(yo);
+        return;
+    }
     for (int z = 0; z < njobs; z++) {
         const float* xz = x + (size_t)(z / tfijo) * K;
         size_t ex = sel[z];
 #pragma omp parallel for schedule(static)
         for (int r = 0; r < N; r++) {
             const uint8_t* row = W + rb * (ex * (size_t)N + (size_t)r);
-            y[(size_t)z * N + r] = mode == 1 ? row_serial(fmt, row, K, xz) : row_dot(fmt, row, K, xz);
+            y[(size_t)z * N + r] = mode == 2 ? row_serial(fmt, row, K, xz) : row_dot(fmt, row, K, xz);
         }
     }
 }

@@ -1627,10 +1627,13 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
     auto load = [&](uint32_t k0) __attribute__((always_inline)) {
         const uint32_t kb = k0 + 32 * part;
         if (pre) {
+            // K is a multiple of 16 (f32) or 32 (Q8_0), so a group of 8 is wholly inside or past the row; a group
+            // past it reads as zeros (the row's end is not a 64-multiple when K % 64 != 0)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                xp[i] = gload<uint4>(xsrow + 2ull * (kb + 8 * i));
-                xp[4 + i] = gload<uint4>(xsrow + xplane + 2ull * (kb + 8 * i));
+                const bool in = kb + 8 * i < K;
+                xp[i] = in ? gload<uint4>(xsrow + 2ull * (kb + 8 * i)) : uint4{0, 0, 0, 0};
+                xp[4 + i] = in ? gload<uint4>(xsrow + xplane + 2ull * (kb + 8 * i)) : uint4{0, 0, 0, 0};
             }
         } else {
 #pragma unroll

@@ -17,6 +17,12 @@ const ROPE_NEOX = new Set(['qwen2', 'qwen3', 'qwen3moe', 'phi3', 'gemma', 'gemma
 const KQ = new Set(['q2k', 'q3k', 'q4k', 'q5k', 'q6k']);
 const MEZCLA = new Set(['q4k', 'q6k']);    // formats whose GEMV segments may share one launch
 const EG = new Set(['q4k', 'q6k', 'q8', 'f32']);   // formats with a grouped expert matmul (matmul_<fmt>_eg)
+// moe_group lists at most 65535 jobs (16-bit counts) of at most 256 experts: a batch whose jobs (tokens x
+// experts used) exceed that takes the ungrouped per-job expert path instead of failing.
+const MOE_GROUP_JOBS = 65535, MOE_GROUP_EXPERTS = 256;
+function agrupable(formatos, batch, nUsados, nExp) {
+  return formatos && batch * nUsados <= MOE_GROUP_JOBS && nExp <= MOE_GROUP_EXPERTS;
+}
 const FMT_ID = { f32: 0, q8: 8, q2k: 10, q3k: 11, q4k: 12, q5k: 13, q6k: 14 };
 // gemv segment modes (qp_args.h)
 const STORE = 0, ACC = 1, SWIGLU = 2, ARGMAX = 3;
@@ -239,7 +245,7 @@ class ModeloTransformer {
         gc.ed = this._mmE(c.ed, this.g, this.de, 1);
         gc.comb = gpu.grupo('moe_comb', [gpu.uniforme([['u', D], ['u', K]]), P, this.x, this.de, this.wts]);
         gc.grupar = gpu.grupo('moe_group', [gpu.uniforme([['u', this.nExp], ['u', K]]), P, this.sel, this.lst, this.off]);
-        gc.agrupado = !!(gc.eg.gg && gc.eu.gg && gc.ed.gg);
+        gc.agrupado = agrupable(!!(gc.eg.gg && gc.eu.gg && gc.ed.gg), this.batch, K, this.nExp);
       } else {
         gc.gate = this._mm(c.gate, this.xn, this.g, 0);
         gc.up = this._mm(c.up, this.xn, this.u, 0);
@@ -616,4 +622,4 @@ function op_max_gen(meta) {
   return op.max_gen || 4096;
 }
 
-module.exports = { ModeloTransformer: ModeloTransformer, tablaRope: tablaRope };
+module.exports = { ModeloTransformer: ModeloTransformer, tablaRope: tablaRope, agrupable: agrupable };

@@ -292,6 +292,35 @@ def test_matmul_prefill_mfma(quipu, dev, oracle, fmt, T, N, K, acc):
     assert np.all(np.abs(got - want) <= bound)
 
 
+@pytest.mark.parametrize("fmt,K", [(capi.Q8_0, 288), (capi.Q8_0, 544), (capi.F32, 80), (capi.F32, 272),
+                                   (capi.F32, 528)])
+@pytest.mark.parametrize("T,N", [(64, 77), (130, 300)])
+def test_matmul_prefill_mfma_ragged_k(quipu, dev, oracle, fmt, T, N, K):
+    """Q8_0 (K % 32) and f32 (K % 16) prefill matmuls whose K is not a multiple of the 64-input step, through the
+    pre-split bf16 planes, without and with split-K (K = 544, 528: three K chunks, the last one partial).  The
+    workspace is first filled by a call whose input is all NaN at more tokens, so a read past the end of a row's
+    planes would bring NaN into the result."""
+    raw = raw_matrix(fmt, N, K, 77)
+    W = (oracle.dequant(fmt, raw, N * K) if fmt != capi.F32 else raw.view(np.float32)).reshape(N, K)
+    wb = [dev.matrix(fmt, raw, N, K)]
+    if fmt == capi.Q8_0:
+        wb.append(wb[0] + N * K)
+    name = "matmul_%s_t" % capi.FMT_NAME[fmt]
+    uni = [("u", N), ("u", K), ("u", 0), ("u", 0)]
+    Tp = T + 200
+    nan_x = np.full((Tp, K), np.nan, np.float32)
+    quipu.dispatch(name, uni, [dev.paso(Tp, 0)] + wb + [dev.buf(nan_x), dev.zeros(4 * Tp * N)],
+                   ((N + 63) // 64, 1, (Tp + 31) // 32))
+    x = np.random.default_rng(5).standard_normal((T, K)).astype(np.float32)
+    y = dev.zeros(4 * T * N)
+    quipu.dispatch(name, uni, [dev.paso(T, 0)] + wb + [dev.buf(x), y], ((N + 63) // 64, 1, (T + 31) // 32))
+    got = dev.get(y, (T, N))
+    want = (W.astype(np.float64) @ x.astype(np.float64).T).T
+    bound = (np.abs(W.astype(np.float64)) @ np.abs(x.astype(np.float64)).T).T * 2e-5 + 1e-30
+    assert np.all(np.isfinite(got))
+    assert np.all(np.abs(got - want) <= bound)
+
+
 def group_jobs(sel, E):
     """moe_group's result from its definition: per expert, the job indices holding it, in increasing order."""
     lst = [i for e in range(E) for i in range(len(sel)) if sel[i] == e]

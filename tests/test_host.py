@@ -205,6 +205,15 @@ def test_js_rope_table_matches_double_power():
         np.testing.assert_array_equal(np.array(vals, np.float32), want)
 
 
+def test_js_moe_grouping_falls_back_past_the_job_limit():
+    """Grouping by expert (moe_group + matmul_*_eg) is chosen only when the batch's jobs fit moe_group's 16-bit
+    lists (batch x experts used <= 65535) and there are at most 256 experts; otherwise the per-job expert path."""
+    r = node("const t = require(%r); console.log(JSON.stringify(["
+             "t.agrupable(true, 2048, 8, 128), t.agrupable(true, 8191, 8, 128), t.agrupable(true, 8192, 8, 128),"
+             "t.agrupable(true, 512, 8, 257), t.agrupable(false, 512, 8, 128)]));" % os.path.join(JS, "transformer.js"))
+    assert r == [True, True, False, False, False]
+
+
 def test_js_registry():
     r = node("""
 const e = require(%r);

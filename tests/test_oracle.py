@@ -166,6 +166,48 @@ def test_matmul_vs_float64(oracle, fmt, N, K, T, mode):
     assert np.all(np.abs(got - ref) <= bound)
 
 
+@pytest.mark.parametrize("fmt,N,K", [(refs.Q2_K, 13, 512), (refs.Q3_K, 6, 256), (refs.Q4_K, 33, 512),
+                                     (refs.Q5_K, 7, 256), (refs.Q6_K, 17, 768), (refs.Q8_0, 19, 320),
+                                     (refs.F32, 9, 96)])
+@pytest.mark.parametrize("T,acc", [(9, 0), (17, 1), (40, 0)])
+def test_matmul_serial_order_is_exact(oracle, fmt, N, K, T, acc):
+    """The tiled prefill order (mode 1: rows dequantized once, 16 tokens' sums advanced together) gives every
+    (token, row) exactly the serial sum c = c + w[k] * x[k] over k = 0..K-1: against numpy float32 arithmetic of
+    that definition (each product and sum rounded to float32, weights from the independent numpy dequantizer)
+    and against mode 2 (the oracle's one-pair-at-a-time loop), bit for bit, for token counts that are not a
+    multiple of 16 and row counts that are not a multiple of 4."""
+    rng = np.random.default_rng(7)
+    raw = blocks(fmt, N * K, 9) if fmt != refs.F32 else rng.standard_normal(N * K).astype(np.float32).view(np.uint8)
+    W = refs.dequant(fmt, raw).reshape(N, K).astype(np.float32)
+    x = (rng.standard_normal((T, K)) * 2).astype(np.float32)
+    y0 = rng.standard_normal((T, N)).astype(np.float32)
+    c = np.zeros((T, N), np.float32)
+    for k in range(K):
+        c = c + x[:, k:k + 1] * W[None, :, k]
+    want = (y0 + c) if acc else c
+    got1 = oracle.matmul(fmt, raw, N, K, x, T, y=y0, acc=bool(acc), mode=1)
+    got2 = oracle.matmul(fmt, raw, N, K, x, T, y=y0, acc=bool(acc), mode=2)
+    np.testing.assert_array_equal(got2, want)
+    np.testing.assert_array_equal(got1, want)
+
+
+def test_matmul_e_serial_order_is_exact(oracle):
+    """The grouped expert order (mode 1: each expert's jobs together over its rows dequantized once) equals the
+    one-(job, row)-at-a-time serial loop (mode 2) bit for bit, with experts of 0, 1 and 20 jobs."""
+    E, N, K, k = 5, 11, 512, 3
+    raw = blocks(refs.Q4_K, E * N * K, 6)
+    x = np.random.default_rng(3).standard_normal((12, K)).astype(np.float32)
+    sel = np.array([(z * 7 + (z // 3)) % 4 for z in range(36)], np.uint32)
+    sel[:20] = 2
+    sel[35] = 4
+    got1 = oracle.matmul_e(refs.Q4_K, raw, N, K, x, sel, tfijo=k, mode=1)
+    got2 = oracle.matmul_e(refs.Q4_K, raw, N, K, x, sel, tfijo=k, mode=2)
+    np.testing.assert_array_equal(got1, got2)
+    W = refs.dequant(refs.Q4_K, raw).reshape(E, N, K).astype(np.float64)
+    for z in (0, 25, 35):
+        np.testing.assert_allclose(got1[z], W[sel[z]] @ x[z // k], rtol=1e-5, atol=1e-5 * np.abs(W[sel[z]]).sum())
+
+
 def test_matmul_acc_onehot_zero(oracle):
     N, K = 8, 256
     raw = blocks(refs.Q4_K, N * K, 3)
