@@ -4,21 +4,25 @@
 
 A "step" is one greedy decode token of the Llama-3-8B-shaped Q4_K_M model (32 layers, hidden 4096, GQA 32/8,
 head_dim 128, FFN 14336, vocab 128256; random weights written to a seeded synthetic GGUF), batch 1, f16 KV.
-The KV cache is first filled by prefilling 4096 uniform-random prompt ids (the headline figure) and, in a
-second measurement, 512.  Weights and activations are resident in HBM when the timed region starts; the
-timed region is K back-to-back replays of the captured one-token step, bracketed by HIP events on the
-backend's stream, with the greedy argmax on the device.
+The KV cache is first filled by prefilling 4096 uniform-random prompt ids (the headline figure) and, in further
+measurements, 2048 and 512.  Weights and activations are resident in HBM when the timed region starts; the timed
+region is K back-to-back replays of the captured one-token step, bracketed by HIP events on the backend's stream,
+with the greedy argmax on the device.
 
 Also measured live: the dominant kernel, the Q4_K GEMV (14336 x 4096, batch 1), over back-to-back launches that
 rotate through >= 512 MB of weight copies (so the 256 MB last-level cache cannot hold them), timed with HIP
-events on the backend's stream.  The CPU baseline is the C restatement of the reference semantics (the test
-oracle) timed on this host's cores on a bounded sample of the same decode; the greedy ids and logits of that
-sample are also the parity check of the GPU run, which generates from the same prompt on the fused path before
-its timed runs (config.parity_vs_oracle: ids identical, max relative logit error).
+events on the backend's stream.
 
-Process layout: this process loads the CPU checker first, runs the GPU decode in a child Node.js process
-(the product host) and only then opens the GPU itself (ctypes) for the GEMV measurement, so no program is
-started from a process that has initialised the GPU.  One JSON line is printed.
+Parity (config.parity_vs_oracle): the same 8B model after a 512-token prompt, 128 greedy tokens on the fused path
+with the reference's f32 KV cache, against the CPU oracle's fixture tests/golden/e2e_c3_ctx512.npz (ids; the 16
+largest logits of every step and two whole rows within 1e-3 of max|logit|).  The CPU baseline is the C
+restatement of the reference semantics (the test oracle) on this host's cores: decode steps of the same model
+at KV length 4096 (cpu_baseline), and in config.cpu_baselines the C1 tiny Q8_0 model end to end and the C2 GEMVs,
+on all threads and on one.
+
+Process layout: this process runs the CPU checker first, then the GPU decode in child Node.js processes (the
+product host), and only then opens the GPU itself (ctypes) for the GEMV measurement, so no program is started
+from a process that has initialised the GPU.  One JSON line is printed.
 """
 from __future__ import annotations
 
@@ -83,38 +87,82 @@ def decode_bytes_per_token(model, path, P, n):
     return w, w + kv_per_pos * mean_pos
 
 
-CHECK_PROMPT = [1, 128000, 9906, 1917]
+CPU_PROMPT = [1, 128000, 9906, 1917]
 
 
-def cpu_baseline(path, seconds=20.0):
-    """The oracle on this host: greedy decode steps of the same model (f16 KV, as the GPU run) after a short
-    prompt, as many as fit in about `seconds` (at least 2).  Also returns the greedy ids and the logits each
-    was chosen from, for the parity check of the GPU run."""
+def cpu_baseline(path, seconds=20.0, kv_len=4096):
+    """The oracle on this host: greedy decode steps of the same model (f16 KV, as the GPU run) at KV length kv_len,
+    as many as fit in about `seconds` (at least 2).  The cache holds a 4-token prompt's rows copied over positions
+    4 .. kv_len-1, so each step does the arithmetic of a decode step at that length (a real 4096-token prefill
+    would take the checker minutes)."""
     from oracle import oracle as O
     threads = O.lib().or_num_threads()
-    m = O.Model(path, ctx=64, kv_f16=True)
-    lg = m.forward(CHECK_PROMPT, True)  # also pages the weights in
-    ids, lgs = [O.argmax(lg)], [lg]
+    m = O.Model(path, ctx=kv_len + 48, kv_f16=True)
+    lg = m.forward(CPU_PROMPT, True)  # also pages the weights in
+    m.fill_cache_to(kv_len)
+    ids = [O.argmax(lg)]
     t0 = time.time()
     steps = 0
     while steps < 2 or (time.time() - t0 < seconds and steps < 40):
         lg = m.forward([ids[-1]], True)
         ids.append(O.argmax(lg))
-        lgs.append(lg)
         steps += 1
     dt = time.time() - t0
     m.close()
     return {"value": steps / dt, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} greedy decode steps of the same 8B Q4_K_M model after a {len(CHECK_PROMPT)}-token "
-                      f"prompt (KV length <= {steps + len(CHECK_PROMPT)}, f16 KV) in {dt:.1f} s on {threads} "
-                      f"OpenMP threads; C restatement of the reference WGSL semantics"}, ids, lgs
+            "sample": f"{steps} greedy decode steps of the same 8B Q4_K_M model at KV length {kv_len}..{kv_len + steps} "
+                      f"(f16 KV; the cache filled with copies of a 4-token prompt's rows) in {dt:.1f} s on {threads} "
+                      f"OpenMP threads; C restatement of the reference WGSL semantics"}
 
 
-def run_decode(model, path, steps, warmup, prefills, check_n=0, eager=False, seed=7, sample=False):
+def cpu_side_baselines(tiny_path, gemv_shapes, rotate=3):
+    """The other CPU timings of the hot path on the oracle, on all threads and on one: the C1 tiny Q8_0 LLaMA end to
+    end (32-token prompt, then greedy tokens: 128 on all threads, 16 on one) and the C2 GEMVs (lane order of
+    matmul_*_1, the best of `rotate` calls on distinct weights)."""
+    from oracle import oracle as O
+    L = O.lib()
+    nthr = L.or_num_threads()
+    out = {"threads_all": nthr}
+    prompt = synth.random_prompt(32000, 32, 2)
+    for thr, n in ((nthr, 128), (1, 16)):
+        L.or_set_threads(thr)
+        m = O.Model(tiny_path, ctx=200)
+        t0 = time.time()
+        lg = m.forward(prompt, True)
+        t1 = time.time()
+        tok = O.argmax(lg)
+        for _ in range(n - 1):
+            tok = O.argmax(m.forward([tok], True))
+        t2 = time.time()
+        m.close()
+        out[f"c1_tiny_q8_{thr}thr"] = {"prompt_tokens": 32, "decode_tokens": n, "prefill_ms": round(1e3 * (t1 - t0), 1),
+                                       "decode_tok_s": round((n - 1) / (t2 - t1), 2)}
+    gem = []
+    for fmt, N, K in gemv_shapes:
+        bpr = {synth.GGML_Q4_K: 144, synth.GGML_Q6_K: 210}[fmt] * (K // 256)
+        raws = [np.frombuffer(synth.gen_blocks(np.random.default_rng(40 + i), fmt, N * K), np.uint8)
+                for i in range(rotate)]
+        x = np.random.default_rng(3).standard_normal(K).astype(np.float32)
+        for thr in (nthr, 1):
+            L.or_set_threads(thr)
+            best = 1e9
+            for r in raws:
+                t0 = time.time()
+                O.matmul(fmt, r, N, K, x)
+                best = min(best, time.time() - t0)
+            nbytes = N * bpr + 4 * K + 4 * N
+            gem.append({"format": {synth.GGML_Q4_K: "q4k", synth.GGML_Q6_K: "q6k"}[fmt], "N": N, "K": K,
+                        "threads": thr, "ms": round(1e3 * best, 3), "GBs": round(nbytes / best / 1e9, 2)})
+    L.or_set_threads(nthr)
+    out["c2_gemv"] = gem
+    out["kind"] = "port (C restatement of the reference WGSL semantics)"
+    return out
+
+
+def run_decode(model, path, steps, warmup, prefills, eager=False, seed=7, sample=False):
     """The product host (Node.js CLI) on `model`: for each P in prefills, prefill P uniform-random ids, then time
     `steps` greedy decode tokens (with `sample`, also `steps` tokens with the reference's default sampler from the
-    same position).  With check_n, first generates check_n greedy tokens from CHECK_PROMPT and returns their
-    logits (the parity check)."""
+    same position)."""
     c = synth.CONFIGS[model]
     ctx = max(prefills) + steps + warmup + 8
     ids = synth.random_prompt(c.vocab, max(prefills), seed)
@@ -123,13 +171,7 @@ def run_decode(model, path, steps, warmup, prefills, check_n=0, eager=False, see
         json.dump(ids, f)
     cmd = ["node", os.path.join(ROOT, "quipullm_amd", "js", "cli.js"), "bench", "--model", path, "--prompt-file", pf,
            "--n", str(steps), "--warmup", str(warmup), "--kv", "f16", "--ctx", str(ctx), "--batch", "2048",
-           "--max-gen", str(max(steps, warmup, check_n) + 8), "--prefill", ",".join(str(p) for p in prefills)]
-    if check_n:
-        cf = os.path.join(model_dir(), f"{model}.check_prompt.json")
-        lf = os.path.join(model_dir(), f"{model}.check_logits.f32")
-        with open(cf, "w") as f:
-            json.dump(CHECK_PROMPT, f)
-        cmd += ["--check-prompt-file", cf, "--check-n", str(check_n), "--check-logits", lf]
+           "--max-gen", str(max(steps, warmup) + 8), "--prefill", ",".join(str(p) for p in prefills)]
     if eager:
         cmd.append("--eager")
     if sample:
@@ -138,10 +180,7 @@ def run_decode(model, path, steps, warmup, prefills, check_n=0, eager=False, see
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         raise RuntimeError("decode benchmark failed:\n" + r.stderr[-3000:])
-    out = json.loads(r.stdout.strip().splitlines()[-1])
-    if check_n:
-        out["check_logits"] = np.fromfile(lf, np.float32).reshape(-1, c.vocab)
-    return out
+    return json.loads(r.stdout.strip().splitlines()[-1])
 
 
 def side_configs(steps, warmup, eager):
@@ -162,13 +201,38 @@ def side_configs(steps, warmup, eager):
     return out
 
 
-def parity(gpu_ids, gpu_lg, cpu_ids, cpu_lg):
-    """Greedy ids and logits of the GPU run against the oracle's on the same prompt (f16 KV on both)."""
-    n = min(len(gpu_ids), len(cpu_ids))
-    rel = [float(np.max(np.abs(a - b)) / np.max(np.abs(b))) for a, b in zip(gpu_lg[:n], cpu_lg[:n])]
+def parity_fixture(case="c3_ctx512"):
+    """The fused path against the CPU oracle's fixture of `case` (tests/golden/make_e2e.py): the same 8B model,
+    prompt and greedy length, the reference's f32 KV cache.  Reports the ids, the largest relative logit error over
+    the fixture's per-step top-16 logits and its whole rows, and the smallest oracle top-1 / top-2 margin."""
+    fp = os.path.join(ROOT, "tests", "golden", f"e2e_{case}.npz")
+    if not os.path.exists(fp):
+        return {"case": case, "error": "fixture missing"}
+    fx = np.load(fp, allow_pickle=False)
+    model = str(fx["model"])
+    P, n, batch = int(fx["prompt_len"]), len(fx["ids"]), int(fx["batch"])
+    c = synth.CONFIGS[model]
+    path = synth.ensure_model(model, model_dir())
+    pf, lf = os.path.join(model_dir(), f"{case}.prompt.json"), os.path.join(model_dir(), f"{case}.logits.f32")
+    with open(pf, "w") as f:
+        json.dump(synth.random_prompt(c.vocab, P, int(fx["prompt_seed"])), f)
+    cmd = ["node", os.path.join(ROOT, "quipullm_amd", "js", "cli.js"), "generate", "--model", path, "--prompt-file",
+           pf, "--n", str(n), "--mode", "fast", "--kv", "f32", "--ctx", str(P + n + 8), "--batch", str(batch),
+           "--logits-out", lf]
+    log("bench: " + " ".join(cmd))
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError("parity run failed:\n" + r.stderr[-3000:])
+    ids = json.loads(r.stdout.strip().splitlines()[-1])["ids"]
+    lg = np.fromfile(lf, np.float32).reshape(n, c.vocab)
+    maxabs, want = fx["maxabs"], fx["ids"].tolist()
+    rel = [float(np.max(np.abs(lg[i, fx["top_ids"][i]] - fx["top_vals"][i])) / maxabs[i]) for i in range(n)]
+    for s_, q, sc in zip(fx["full_steps"], fx["full_rows"], fx["full_scale"]):
+        rel.append(float(np.max(np.abs(lg[s_] - q.astype(np.float64) * float(sc))) / maxabs[s_]))
     # np.max propagates a NaN (Python's max would skip it depending on the order)
-    return {"tokens": n, "ids_identical": gpu_ids[:n] == cpu_ids[:n], "max_rel_logits": float(np.max(rel)),
-            "prompt": CHECK_PROMPT}
+    return {"case": case, "model": model, "prompt_tokens": P, "tokens": n, "kv": "f32", "ids_identical": ids == want,
+            "max_rel_logits": float(np.max(rel)), "min_margin_rel": float(np.min(fx["margin"] / maxabs)),
+            "distinct_ids": len(set(want)), "reference": "CPU restatement of the reference semantics (oracle fixture)"}
 
 
 def gemv_microbench(shapes, iters=200, rotate_bytes=640 << 20):
@@ -209,11 +273,16 @@ def main():
     t0 = time.time()
     path = synth.ensure_model(MODEL, model_dir())
     log(f"bench: model {path} ready in {time.time() - t0:.1f}s")
-    cpu, cpu_ids, cpu_lg = cpu_baseline(path, a.cpu_seconds)
+    cpu = cpu_baseline(path, a.cpu_seconds)
     log(f"bench: cpu baseline {cpu['value']:.3f} tok/s")
+    cpu_side = {} if a.no_side else cpu_side_baselines(
+        synth.ensure_model("tiny_q8", model_dir()),
+        [(synth.GGML_Q4_K, 4096, 4096), (synth.GGML_Q4_K, 14336, 4096), (synth.GGML_Q4_K, 4096, 14336),
+         (synth.GGML_Q6_K, 4096, 4096), (synth.GGML_Q6_K, 14336, 4096), (synth.GGML_Q6_K, 4096, 14336)])
+    log("bench: cpu side baselines " + json.dumps(cpu_side))
     prefills = [4096, 2048, 512]
-    dec = run_decode(MODEL, path, a.steps, a.warmup, prefills, len(cpu_ids), a.decode_launch == "eager", sample=True)
-    check = parity(dec["check_ids"], dec.pop("check_logits"), cpu_ids, cpu_lg)
+    dec = run_decode(MODEL, path, a.steps, a.warmup, prefills, a.decode_launch == "eager", sample=True)
+    check = parity_fixture()
     runs = {r["prompt_tokens"]: r for r in dec["runs"]}
     log("bench: decode " + json.dumps(dec))
     log("bench: parity " + json.dumps(check))
@@ -230,8 +299,10 @@ def main():
         "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(main_run["ms_per_token"], 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "Llama-3-8B-shape Q4_K_M (Q6_K attn_v/ffn_down/output) greedy decode, batch 1, "
-                               "KV prefilled with 4096 random prompt ids, f16 KV, 256 timed tokens",
+        "config": {"workload": f"Llama-3-8B-shape Q4_K_M (Q6_K attn_v/ffn_down/output) greedy decode, batch 1, "
+                               f"KV prefilled with {prefills[0]} random prompt ids, f16 KV, {a.steps} timed tokens "
+                               f"after {a.warmup} warm-up tokens (also after prefills of {prefills[1]} and "
+                               f"{prefills[2]} ids)",
                    "ctx": 4096, "kv": "f16", "batch": 1, "prefill_tokens": 4096, "decode_launch": a.decode_launch,
                    "decode_tok_s_ctx512": round(runs[512]["decode_tok_s"], 3),
                    "decode_hbm_GBs_ctx4096": round(bpt * tok_s / 1e9, 1),
@@ -246,7 +317,7 @@ def main():
                    "prefill_2048_TFLOPs": round(PREFILL_2048_FLOP / (runs[2048]["prefill_ms"] * 1e-3) / 1e12, 2),
                    "side_configs": side,
                    "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()} for g in gem],
-                   "parity_vs_oracle": check},
+                   "parity_vs_oracle": check, "cpu_baselines": cpu_side},
         "roofline": {"bound": "hbm", "kernel": "qp_gemv_q4k_r1 (Q4_K GEMV 14336x4096, batch 1)",
                      "achieved": round(dom["GBs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(dom["GBs"] / PEAK_HBM_GBS, 4), "traffic": committed_traffic(),

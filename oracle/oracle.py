@@ -273,7 +273,8 @@ class _Model(C.Structure):
                [(n, C.c_float) for n in ("eps", "base", "escala", "moe_scale")] + \
                [("tok_embd", C.c_void_p), ("output", C.c_void_p), ("output_norm", C.c_void_p),
                 ("f_embd", C.c_int), ("f_output", C.c_int), ("layers", C.POINTER(_Layer)), ("pos", C.c_int),
-                ("kc", C.c_void_p), ("vc", C.c_void_p), ("kv_f16", C.c_int)]
+                ("kc", C.c_void_p), ("vc", C.c_void_p), ("kv_f16", C.c_int), ("kref", C.c_void_p),
+                ("vref", C.c_void_p), ("nref", C.c_int)]
 
 
 ROPE_NEOX = {"qwen2", "qwen3", "qwen3moe", "phi3", "gemma", "gemma2", "gemma3", "stablelm", "olmo2"}
@@ -344,6 +345,32 @@ class Model:
         if L.or_model_alloc_kv(self.ptr) != 0:
             raise MemoryError("oracle KV cache")
         self.batch = 32
+
+    def set_kv_reference(self, k16, v16):
+        """f16 mode: take the cache rows of the first positions from another implementation's f16 cache (k16, v16:
+        uint16 [n_layers][npos][nkv * hd]) instead of rounding this model's own k and v."""
+        m = _Model.from_address(self.ptr)
+        assert m.kv_f16, "set_kv_reference needs kv_f16"
+        kvd = self.nkv * self.hd
+        k16 = np.ascontiguousarray(k16, np.uint16)
+        v16 = np.ascontiguousarray(v16, np.uint16)
+        assert k16.shape == v16.shape and k16.ndim == 3 and k16.shape[0] == self.n_layers and k16.shape[2] == kvd
+        self._kvref = (k16, v16)
+        m.kref, m.vref, m.nref = k16.ctypes.data, v16.ctypes.data, k16.shape[1]
+
+    def fill_cache_to(self, npos):
+        """For timing only: copies the cached rows of positions 0 .. pos-1 over positions pos .. npos-1 and moves the
+        position to npos, so the next forward does the arithmetic of a decode step at KV length npos (without a
+        prefill of npos tokens, which would take the checker minutes)."""
+        m = _Model.from_address(self.ptr)
+        kvd, p = self.nkv * self.hd, m.pos
+        assert 0 < p <= npos < self.ctx
+        n = self.n_layers * self.ctx * kvd
+        for ptr in (m.kc, m.vc):
+            a = np.ctypeslib.as_array((C.c_float * n).from_address(ptr)).reshape(self.n_layers, self.ctx, kvd)
+            for q in range(p, npos, p):
+                a[:, q:min(q + p, npos)] = a[:, :min(p, npos - q)]
+        m.pos = npos
 
     def reset(self):
         lib().or_model_reset(self.ptr)

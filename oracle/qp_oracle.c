@@ -481,6 +481,7 @@ static void row_deq(int fmt, const uint8_t* row, int K, float* w) {
  * is unchanged: lanes do not mix).  Token t's value for row r goes to y[yoff[t] + r] (added to it after the sum
  * when acc, as row_serial's callers do). */
 #define OR_TB 16
+typedef float or_v8 __attribute__((vector_size(32)));
 __attribute__((target_clones("avx2", "default")))
 static void serial_rows(int fmt, const uint8_t* W, size_t rb, size_t row0, int N, int K, const float* xT, int nt,
                         float* y, const size_t* yoff, int acc) {
@@ -493,19 +494,25 @@ static void serial_rows(int fmt, const uint8_t* W, size_t rb, size_t row0, int N
             const int nr = N - r0 < 4 ? N - r0 : 4;
             for (int i = 0; i < nr; i++) row_deq(fmt, W + rb * (row0 + (size_t)r0 + i), K, w + (size_t)i * K);
             for (int tb = 0; tb < ntp; tb += OR_TB) {
-                float c[4][OR_TB];
+                /* c[i][h]: lanes = tokens tb + 8h .. tb + 8h + 7 of row r0 + i; elementwise mul then add */
+                or_v8 c[4][2];
                 memset(c, 0, sizeof(c));
                 for (int k = 0; k < K; k++) {
-                    const float* xk = xT + (size_t)k * ntp + tb;
+                    or_v8 x0, x1;
+                    memcpy(&x0, xT + (size_t)k * ntp + tb, 32);
+                    memcpy(&x1, xT + (size_t)k * ntp + tb + 8, 32);
                     for (int i = 0; i < 4; i++) {
                         const float wv = w[(size_t)i * K + k];
-                        for (int j = 0; j < OR_TB; j++) c[i][j] = c[i][j] + wv * xk[j];
+                        const or_v8 wb = {wv, wv, wv, wv, wv, wv, wv, wv};
+                        c[i][0] = c[i][0] + wb * x0;
+                        c[i][1] = c[i][1] + wb * x1;
                     }
                 }
                 for (int i = 0; i < nr; i++)
                     for (int j = 0; j < OR_TB && tb + j < nt; j++) {
                         float* o = y + yoff[tb + j] + r0 + i;
-                        *o = acc ? *o + c[i][j] : c[i][j];
+                        const float v = c[i][j >> 3][j & 7];
+                        *o = acc ? *o + v : v;
                     }
             }
         }
@@ -848,6 +855,10 @@ typedef struct {
     int pos;
     float *kc, *vc; /* [L][ctx][kvd] */
     int kv_f16;     /* option of this backend: cache rows rounded to f16 when written (reference: f32 only) */
+    /* f16 mode, for checking a GPU run: the cache rows of positions < nref are taken from kref / vref
+     * ([L][nref][kvd] f16, the GPU's own cache) instead of this restatement's rounding of its own k and v */
+    const uint16_t *kref, *vref;
+    int nref;
 } OrModel;
 
 OrModel* or_model_new(void) { return (OrModel*)calloc(1, sizeof(OrModel)); }
@@ -915,8 +926,15 @@ int or_model_forward(OrModel* m, const uint32_t* ids, int T, float* logits) {
         or_kv_write(k, v, kc, vc, T, kvd, m->pos, 0);
         if (m->kv_f16)
             for (size_t i = (size_t)m->pos * kvd; i < (size_t)(m->pos + T) * kvd; i++) {
-                kc[i] = f16_round(kc[i]);
-                vc[i] = f16_round(vc[i]);
+                const size_t p = i / kvd;
+                if ((int)p < m->nref) {
+                    const size_t r = ((size_t)li * m->nref + p) * kvd + i % kvd;
+                    kc[i] = or_f16(m->kref[r]);
+                    vc[i] = or_f16(m->vref[r]);
+                } else {
+                    kc[i] = f16_round(kc[i]);
+                    vc[i] = f16_round(vc[i]);
+                }
             }
         or_attention(q, kc, vc, att, T, m->pos, nh, nkv, hd, m->escala, 0, 0);
         mm(m, L->fo, L->wo, D, qd, att, T, x, 1);

@@ -2,12 +2,13 @@
 // Command-line driver of the engine, for tests and the benchmark.
 //
 //   node cli.js generate --model M.gguf --prompt-file ids.json --n 128 [--mode fast|ref|engine|sample] [--kv f16|f32]
-//                        [--ctx N] [--batch N] [--no-tiled] [--logits-out file.f32]
+//                        [--ctx N] [--batch N] [--no-tiled] [--logits-out file.f32] [--kv-out file]
 //                        [--repeat-penalty R] [--frequency-penalty F] [--presence-penalty P] [--host-loop]
 //                        [--temperature T] [--top-k K] [--top-p P] [--min-p M] [--seed S]
 //   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
 //                        [--warmup W] [--prefill P1,P2] [--eager] [--sample] [--keys-per-split N]
 //                        [--no-moe-grouped]
+//   node cli.js motor    --servidor http://127.0.0.1:PORT [--id ID] [--kv f16] [--batch N]   (the server's engine)
 //                        [--check-prompt-file ids.json --check-n N --check-logits file.f32]
 //
 // generate prints one JSON line {ids, prompt_ms, decode_ms, tps}; with --logits-out the logits each token was
@@ -107,6 +108,7 @@ async function generate(o) {
   }
   const tEnd = Date.now();
   if (out !== null) fs.closeSync(out);
+  if (o['kv-out']) modelo.volcarKV(o['kv-out']);
   const r = Object.assign({ ids: toks, prompt_ms: tPrompt - t0, decode_ms: tEnd - tPrompt, pos: modelo.pos }, extra);
   modelo.free();
   process.stdout.write(JSON.stringify(r) + '\n');
@@ -197,11 +199,23 @@ async function bench(o) {
   process.stdout.write(JSON.stringify(r) + '\n');
 }
 
+// The engine of quipullm's server (motor.js): hello, then jobs from the long poll until the server says "cerrar".
+async function motor(o) {
+  const { Motor } = require('./motor');
+  const opciones = { kv_f16: o.kv === 'f16' };
+  if (o.batch) opciones.batch = parseInt(o.batch, 10);
+  if (o['max-gen']) opciones.max_gen = parseInt(o['max-gen'], 10);
+  if (o['keys-per-split']) opciones.attn_keys_per_split = parseInt(o['keys-per-split'], 10);
+  const m = new Motor({ servidor: o.servidor || 'http://127.0.0.1:8080', id: o.id, opciones: opciones });
+  const r = await m.correr();
+  process.stdout.write(JSON.stringify({ fin: r }) + '\n');
+}
+
 const o = args(process.argv.slice(2));
 const cmd = o._[0];
-const fn = { generate: generate, bench: bench }[cmd];
+const fn = { generate: generate, bench: bench, motor: motor }[cmd];
 if (!fn) {
-  process.stderr.write('usage: node cli.js generate|bench --model M.gguf --prompt-file ids.json ...\n');
+  process.stderr.write('usage: node cli.js generate|bench --model M.gguf --prompt-file ids.json ... | motor --servidor URL\n');
   process.exit(2);
 }
 fn(o).catch(function (e) {

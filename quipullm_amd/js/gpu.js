@@ -36,6 +36,7 @@ function empaquetar(valores) {
 
 class Buffer {
   constructor(h, tam, label) { this.h = h; this._tam = tam; this.label = label; }
+  get size() { return this._tam; }   // bytes, as WebGPU's GPUBuffer.size
 }
 
 class GPU {

@@ -81,11 +81,13 @@ class ModeloTransformer {
     this.intervaloCP = 64;
   }
 
-  load(ruta, progreso) {
-    const gpu = this.gpu, c = new CargadorPesos(gpu, this.meta, ruta, progreso);
+  // fuente: the GGUF path, or {url} of the server's file route (tensors fetched by ranges, layer by layer)
+  async load(fuente, progreso) {
+    const gpu = this.gpu, c = new CargadorPesos(gpu, this.meta, fuente, progreso);
     this.cargador = c;
     try {
       if (c.existe('rope_freqs.weight')) throw new Error('this model uses rope_freqs.weight (scaled RoPE), which is not supported');
+      await c.precargar(['token_embd.weight', 'output.weight', 'output_norm.weight']);
       this.emb = c.matriz('token_embd.weight');
       this.vocab = this.emb.N;
       this.salida = c.existe('output.weight') ? c.matriz('output.weight') : this.emb;
@@ -96,6 +98,9 @@ class ModeloTransformer {
         const p = 'blk.' + i + '.';
         for (const n of ['attn_q.bias', 'attn_k.bias', 'attn_v.bias', 'attn_output.bias', 'post_attention_norm.weight', 'post_ffw_norm.weight'])
           if (c.existe(p + n)) throw new Error(p + n + ': biases and post-norms are not supported by this backend');
+        await c.precargar(['attn_norm', 'attn_q', 'attn_k', 'attn_v', 'attn_output', 'attn_q_norm', 'attn_k_norm',
+          'ffn_norm', 'ffn_gate_inp', 'ffn_gate_exps', 'ffn_up_exps', 'ffn_down_exps', 'ffn_gate', 'ffn_up',
+          'ffn_down'].map(function (n) { return p + n + '.weight'; }));
         const capa = {};
         capa.attnNorm = c.f32(p + 'attn_norm.weight');
         capa.wq = c.matriz(p + 'attn_q.weight');
@@ -599,6 +604,23 @@ class ModeloTransformer {
     const t = new Uint32Array(1);
     this.gpu.leer(this.bIds, 0, t);
     return t[0];
+  }
+
+  // The KV cache as this backend holds it, for checking against the CPU oracle: per layer the K cache bytes then
+  // the V cache bytes ([ctx][kvd] f32 or f16 rows; the f16 V cache in its 32-slot tiles), written to `ruta`.
+  volcarKV(ruta) {
+    const fs = require('fs');
+    const fd = fs.openSync(ruta, 'w');
+    try {
+      for (const c of this.capas)
+        for (const b of [c.kc, c.vc]) {
+          const u = new Uint8Array(b.size);
+          this.gpu.leer(b, 0, u);
+          fs.writeSync(fd, u);
+        }
+    } finally {
+      fs.closeSync(fd);
+    }
   }
 
   free() {

@@ -1,12 +1,15 @@
 'use strict';
-// Loading of GGUF tensors from a local file into device buffers.
+// Loading of GGUF tensors into device buffers, from a local file or from the server's file URL by ranges.
 //
 // Same interface as quipullm's CargadorPesos (web/js/weights.js:15-139): existe(name), info(name),
 // f32(name) -> buffer, matriz(name) -> {tipo, N, K, w} ({tipo:'q8', N, K, qs, ds} for Q8_0).  The device
 // layout behind a handle is this backend's own: K-quant blocks and Q8_0 repacked on the device
 // into planar arrays (quants | scales) so every lane load is a 16-byte vector load.
+// Source: a path (read synchronously), or {url} (the reference engine's /engine/file/<id>, web/js/weights.js:51):
+// then the caller awaits precargar(names) before the synchronous calls that use those tensors.
 const fs = require('fs');
 const { despachar, vista } = require('./gpu');
+const { rango } = require('./http');
 
 // GGUF K-quant types: name, GGUF block bytes, device bytes per block (Q3_K padded to 112)
 const K_QUANTS = { 10: { nombre: 'q2k', bytes: 84, disp: 84 }, 11: { nombre: 'q3k', bytes: 110, disp: 112 },
@@ -25,19 +28,30 @@ const F16 = (function () {
 })();
 
 class CargadorPesos {
-  constructor(gpu, meta, ruta, progreso) {
+  constructor(gpu, meta, fuente, progreso) {
     this.gpu = gpu;
     this.meta = meta;
-    this.ruta = ruta;
+    this.url = typeof fuente === 'string' ? null : fuente.url;
     this.progreso = progreso || function () {};
     this.tensores = new Map(meta.tensors.map(function (t) { return [t.nombre, t]; }));
     this.totalBytes = meta.tensors.reduce(function (a, t) { return a + (t.bytes || 0); }, 0);
     this.leidos = 0;
     this.buffers = [];
-    this.fd = fs.openSync(ruta, 'r');
+    this.previos = new Map();   // tensors fetched by precargar (URL source), taken by bytes()
+    this.fd = this.url ? null : fs.openSync(fuente, 'r');
   }
 
-  cerrar() { if (this.fd !== null) { fs.closeSync(this.fd); this.fd = null; } }
+  cerrar() { if (this.fd !== null) { fs.closeSync(this.fd); this.fd = null; } this.previos.clear(); }
+
+  // URL source: fetches the named tensors that exist (one range request each, in turn); a path source needs nothing.
+  async precargar(nombres) {
+    if (!this.url) return;
+    for (const n of nombres) {
+      const t = this.tensores.get(n);
+      if (!t || this.previos.has(n) || t.bytes === null || t.bytes === undefined) continue;
+      this.previos.set(n, await rango(this.url, t.abs, t.bytes));
+    }
+  }
 
   existe(nombre) { return this.tensores.has(nombre); }
 
@@ -49,12 +63,19 @@ class CargadorPesos {
 
   bytes(t) {
     if (t.bytes === null || t.bytes === undefined) throw new Error('unsupported tensor type (' + t.tipo_nombre + ') in ' + t.nombre);
-    const b = Buffer.allocUnsafe(t.bytes);
-    let got = 0;
-    while (got < t.bytes) {
-      const n = fs.readSync(this.fd, b, got, Math.min(t.bytes - got, 1 << 30), t.abs + got);
-      if (n <= 0) throw new Error('incomplete read of ' + t.nombre);
-      got += n;
+    let b;
+    if (this.url) {
+      b = this.previos.get(t.nombre);
+      if (!b) throw new Error('tensor ' + t.nombre + ' was not fetched from ' + this.url);
+      this.previos.delete(t.nombre);
+    } else {
+      b = Buffer.allocUnsafe(t.bytes);
+      let got = 0;
+      while (got < t.bytes) {
+        const n = fs.readSync(this.fd, b, got, Math.min(t.bytes - got, 1 << 30), t.abs + got);
+        if (n <= 0) throw new Error('incomplete read of ' + t.nombre);
+        got += n;
+      }
     }
     this.leidos += t.bytes;
     this.progreso(this.leidos / this.totalBytes, t.nombre);

@@ -89,6 +89,13 @@ CONFIGS = {
     # Qwen3-30B-A3B-like MoE, Q4_K everywhere except the f32 router
     "qwen3moe_q4k": ModelConfig("qwen3moe_q4k", "qwen3moe", 48, 2048, 32, 4, 128, 0, 151936, 1e-6, 1000000.0,
                                 {"default": GGML_Q4_K}, n_exp=128, n_used=8, ffe=768, qk_norm=True),
+    # the configs' shapes in depth the CPU checker can follow through long prompts, centered (varied greedy ids):
+    # the 8B shape in 2 layers (ctx 4096 parity, the 2048-token prefill) and the MoE shape in 4 layers
+    "llama8b_q4km_c2": ModelConfig("llama8b_q4km_c2", "llama", 2, 4096, 32, 8, 128, 14336, 128256, 1e-5, 500000.0,
+                                   _q4km(), ctx=4400, centered=True),
+    "qwen3moe_q4k_c4": ModelConfig("qwen3moe_q4k_c4", "qwen3moe", 4, 2048, 32, 4, 128, 0, 151936, 1e-6, 1000000.0,
+                                   {"default": GGML_Q4_K}, n_exp=128, n_used=8, ffe=768, qk_norm=True, ctx=2400,
+                                   centered=True),
     # small variants with the same formats, for parity tests
     "mini_llama_q4km": ModelConfig("mini_llama_q4km", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
                                    _q4km(), ctx=512),
