@@ -59,6 +59,7 @@ class ModelConfig:
     qk_norm: bool = False
     ctx: int = 4096
     centered: bool = False    # zero-mean weights (test variants; see gen_blocks)
+    wstd: float = 0.0         # > 0: K-quant block scales drawn so the weights' standard deviation is about wstd
 
     def tensor_type(self, kind: str) -> int:
         return self.fmt.get(kind, self.fmt.get("default", GGML_Q4_K))
@@ -89,13 +90,15 @@ CONFIGS = {
     # Qwen3-30B-A3B-like MoE, Q4_K everywhere except the f32 router
     "qwen3moe_q4k": ModelConfig("qwen3moe_q4k", "qwen3moe", 48, 2048, 32, 4, 128, 0, 151936, 1e-6, 1000000.0,
                                 {"default": GGML_Q4_K}, n_exp=128, n_used=8, ffe=768, qk_norm=True),
-    # the configs' shapes in depth the CPU checker can follow through long prompts, centered (varied greedy ids):
-    # the 8B shape in 2 layers (ctx 4096 parity, the 2048-token prefill) and the MoE shape in 4 layers
+    # the configs' shapes in depth the CPU checker can follow through long prompts, centered (varied greedy ids)
+    # and with weights of standard deviation 0.02 (about 1/sqrt(hidden)), so activations and attention scores stay
+    # of the order of a real model's: the 8B shape in 2 layers (ctx 4096 parity, the 2048-token prefill) and the MoE
+    # shape in 4 layers
     "llama8b_q4km_c2": ModelConfig("llama8b_q4km_c2", "llama", 2, 4096, 32, 8, 128, 14336, 128256, 1e-5, 500000.0,
-                                   _q4km(), ctx=4400, centered=True),
+                                   _q4km(), ctx=4400, centered=True, wstd=0.02),
     "qwen3moe_q4k_c4": ModelConfig("qwen3moe_q4k_c4", "qwen3moe", 4, 2048, 32, 4, 128, 0, 151936, 1e-6, 1000000.0,
                                    {"default": GGML_Q4_K}, n_exp=128, n_used=8, ffe=768, qk_norm=True, ctx=2400,
-                                   centered=True),
+                                   centered=True, wstd=0.02),
     # small variants with the same formats, for parity tests
     "mini_llama_q4km": ModelConfig("mini_llama_q4km", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
                                    _q4km(), ctx=512),
@@ -181,8 +184,15 @@ def pack_q4k_scales(sc, mn):
     return s
 
 
-def gen_blocks(rng, gtype, nelem, kind="w", centered=False):
-    """Bytes of one tensor of `nelem` elements."""
+# Standard deviation of a K-quant weight per unit of the d scale's sigma: Q4_K / Q5_K centered (scale uniform 0..63,
+# rms 36.4; q - 7.5 or q - 15.5 with rms 4.6 or 9.2) and Q6_K (int8 scale, rms 36.9; q - 32, rms 18.5).
+_STD_PER_SIGMA = {GGML_Q4_K: 36.4 * 4.61, GGML_Q5_K: 36.4 * 9.23, GGML_Q6_K: 36.9 * 18.5}
+
+
+def gen_blocks(rng, gtype, nelem, kind="w", centered=False, wstd=0.0):
+    """Bytes of one tensor of `nelem` elements.  wstd > 0 (Q4_K, Q5_K centered and Q6_K): the d scales' sigma
+    is chosen so that the weights' standard deviation is about wstd, instead of the configs' 0.01."""
+    sig = np.float32(wstd / _STD_PER_SIGMA[gtype]) if wstd > 0 and gtype in _STD_PER_SIGMA else 0.01
     if gtype == GGML_F32:
         if kind == "embd" and centered:
             a = rng.standard_normal(nelem, dtype=np.float32)
@@ -202,7 +212,7 @@ def gen_blocks(rng, gtype, nelem, kind="w", centered=False):
         return blk.tobytes()
     blk = np.frombuffer(rng.bytes(nb * bpb), np.uint8).reshape(nb, bpb).copy()
     if gtype in (GGML_Q4_K, GGML_Q5_K):
-        d = _abs_normal_f16(rng, nb, 0.01)
+        d = _abs_normal_f16(rng, nb, sig)
         blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         if centered:
             mean = np.float32(7.5 if gtype == GGML_Q4_K else 15.5)
@@ -224,7 +234,7 @@ def gen_blocks(rng, gtype, nelem, kind="w", centered=False):
             blk[:, 82:84] = _abs_normal_f16(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)
     elif gtype == GGML_Q6_K:
         blk[:, 192:208] = rng.integers(-64, 64, size=(nb, 16), dtype=np.int8).view(np.uint8)
-        blk[:, 208:210] = _abs_normal_f16(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)
+        blk[:, 208:210] = _abs_normal_f16(rng, nb, sig).view(np.uint8).reshape(nb, 2)
     else:
         raise ValueError(gtype)
     return blk.tobytes()
@@ -306,7 +316,7 @@ def write_gguf(path: str, c: ModelConfig, seed: int = 0) -> str:
                 f.write(b"\0" * (o - pos))
                 pos = o
             rng = np.random.default_rng([seed, i])
-            data = gen_blocks(rng, gtype, int(np.prod(dims)), kind, c.centered)
+            data = gen_blocks(rng, gtype, int(np.prod(dims)), kind, c.centered, c.wstd)
             f.write(data)
             pos += len(data)
     os.replace(tmp, path)

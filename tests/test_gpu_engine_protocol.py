@@ -42,11 +42,22 @@ def test_engine_protocol_generates_the_oracle_ids(oracle, models_dir):
     assert "AMD" in stub.hellos[0]["gpu"]["summary"]
     e1 = stub.events[j1]
     got = [int(e["texto"]) for e in e1 if e["tipo"] == "token"]
-    assert e1[0] == {"motor": e1[0]["motor"], "tipo": "inicio", "id": j1, "prompt_tokens": len(prompt)}
-    assert got == want, (got, want)
+    ini = [e for e in e1 if e["tipo"] == "inicio"]
+    assert len(ini) == 1 and ini[0]["prompt_tokens"] == len(prompt)
+    assert all(e["tipo"] == "progreso" for e in e1[:e1.index(ini[0])])  # model loading progress
+    # the synthetic files declare the last id as the end token (tokenizer.ggml.eos_token_id): generation stops there
+    eos = vocab - 1
+    cut = want.index(eos) if eos in want else None
+    want1 = want[:cut] if cut is not None else want
+    assert got == want1, (got, want, [e["tipo"] for e in e1], e1[-1])
     f = e1[-1]
-    assert f["tipo"] == "fin" and f["razon"] == "length" and f["completion_tokens"] == n + 1 and f["tps"] > 0
+    assert f["tipo"] == "fin" and f["tps"] > 0
+    if cut is None:
+        assert f["razon"] == "length" and f["completion_tokens"] == n + 1
+    else:
+        assert f["razon"] == "stop" and f["completion_tokens"] == cut
     e2 = stub.events[j2]
     got2 = [int(e["texto"]) for e in e2 if e["tipo"] == "token"]
-    assert got2 == want[10:18], (got2, want[10:18])
+    want2 = want[10:18] if cut is None or cut >= 18 else want[10:cut]
+    assert got2 == want2, (got2, want2, e2[-1])
     assert e2[-1]["diag"]["reutilizados"] >= len(prompt), e2[-1]["diag"]

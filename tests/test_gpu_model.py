@@ -136,27 +136,32 @@ def test_greedy_matches_oracle(oracle, models_dir, tmp_path, name, kv):
 
 
 def test_f16_cache_rows_are_the_rounded_values(oracle, models_dir, tmp_path):
-    """The GPU's f16 cache rows are f16 roundings of the oracle's own float32 K/V: every element within one f16
-    step (the two sides' float32 values differ only in their last bits), most of them equal."""
+    """The GPU's f16 cache rows of layer 0 (computed from the embeddings only, before any f16 cache value is
+    used) are the f16 roundings of the oracle's float32 K and V of that layer: every element within one f16 step
+    (the two sides' float32 values differ only in their last bits), nearly all equal.  (Deeper layers see the
+    rounded cache of the layers before them, so their rows are not comparable element by element.)"""
     name = "mini_llama_q4km_c"
     path = synth.ensure_model(name, models_dir)
     vocab = oracle.GGUF(path).tensors["token_embd.weight"]["dims"][1]
     prompt = synth.random_prompt(vocab, 40, 1)
     kvf = os.path.join(str(tmp_path), "kv.bin")
-    generate(path, prompt, 4, "fast", "f16", str(tmp_path), kv_out=kvf)
-    c = synth.CONFIGS[name]
-    npos = len(prompt) + 3
-    k16, v16 = read_kv_f16(kvf, c.n_layers, 256, c.nkv * c.hd, npos)
-    m = oracle.Model(path, ctx=256, kv_f16=False)
-    m.generate(prompt, 4)
-    kvd = c.nkv * c.hd
-    kc = np.ctypeslib.as_array((ctypes.c_float * (c.n_layers * 256 * kvd)).from_address(
-        oracle._Model.from_address(m.ptr).kc)).reshape(c.n_layers, 256, kvd)[:, :npos]
-    ours = kc.astype(np.float16)
-    gpu = k16.view(np.float16)
-    ulp = np.abs(ours.view(np.int16).astype(np.int32) - gpu.view(np.int16).astype(np.int32))
-    m.close()
-    assert ulp.max() <= 1 and np.mean(ulp == 0) > 0.99, (ulp.max(), np.mean(ulp == 0))
+    for mode in ("ref", "fast"):
+        generate(path, prompt, 4, mode, "f16", str(tmp_path), kv_out=kvf)
+        c = synth.CONFIGS[name]
+        npos, kvd = len(prompt) + 3, c.nkv * c.hd
+        k16, v16 = read_kv_f16(kvf, c.n_layers, 256, kvd, npos)
+        m = oracle.Model(path, ctx=256, kv_f16=False)
+        m.generate(prompt, 4)
+        mm = oracle._Model.from_address(m.ptr)
+        for name_, gpu, ptr in (("K", k16, mm.kc), ("V", v16, mm.vc)):
+            ours = np.ctypeslib.as_array((ctypes.c_float * (c.n_layers * 256 * kvd)).from_address(ptr)).reshape(
+                c.n_layers, 256, kvd)[0, :npos].astype(np.float16)
+            g = gpu[0].view(np.float16)
+            step = np.spacing(np.maximum(np.abs(ours), np.abs(g))).astype(np.float32)
+            d = np.abs(ours.astype(np.float32) - g.astype(np.float32))
+            assert np.all(d <= step), (mode, name_, float(np.max(d / step)))
+            assert np.mean(d == 0) > 0.99, (mode, name_, float(np.mean(d == 0)))
+        m.close()
 
 
 def test_tiny_q8_config(oracle, models_dir, tmp_path):
