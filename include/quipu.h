@@ -65,6 +65,15 @@ int qp_op_id(const char* name);
 int qp_dispatch(int op, const void* uniform, uint32_t uniform_size, const uint64_t* bufs, uint32_t nbuf,
                 uint32_t gx, uint32_t gy, uint32_t gz);
 
+/* qp_dispatch for callers that cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc); no counterpart in the reference.  The same ops and results as qp_dispatch, and no allocation: the
+ * prefill matmul (matmul_<fmt>_4 / _t), whose workspace qp_dispatch grows with hipMalloc, takes it from a fixed
+ * device array of 32 MiB that each device holds from qp_init until the process ends (its split input planes, 4
+ * bytes per input value, and split-K partials: up to 256 tokens at K = 14336); a call that would need more fails
+ * with QP_E_ARG.  Every call on a device shares that array and finds the last call's contents; calls that overlap
+ * on one device race. */
+int qp_dispatch_noalloc(int op, const void* uniform, uint32_t uniform_size, const uint64_t* bufs, uint32_t nbuf,
+                        uint32_t gx, uint32_t gy, uint32_t gz);
 /* ---------------------------------------------------------------- raw code objects (no reference counterpart) */
 /* hipModuleLoad of a gfx950 code object; hipModuleGetFunction; hipModuleLaunchKernel with one packed
  * argument block.  For host code that brings its own kernels. */

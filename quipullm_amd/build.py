@@ -57,9 +57,14 @@ def build_kernels():
 
 def build_lib():
     src = os.path.join(CSRC, "quipu.cpp")
+    # the scratch array of qp_dispatch_noalloc: a device array, so its file goes through hipcc (device code for
+    # gfx950 embedded in the object) and is linked into the library
+    scratch = os.path.join(CSRC, "qp_scratch.hip")
+    obj = os.path.join(LIB, "qp_scratch.o")
+    _atomic(obj, lambda o: _run([HIPCC, "-c", "-fPIC", *HIP_FLAGS, "-o", o, scratch], "scratch array"))
     cmd = lambda o: ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-parameter",
-                     "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", "-o", o, src, f"-L{ROCM}/lib", "-lamdhip64",
-                     f"-Wl,-rpath,{ROCM}/lib", "-Wl,-soname,libquipu.so"]
+                     "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", "-o", o, src, obj, f"-L{ROCM}/lib",
+                     "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-Wl,-soname,libquipu.so"]
     _atomic(SO, lambda o: _run(cmd(o), "libquipu"))
     return SO
 

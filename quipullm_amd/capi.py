@@ -53,6 +53,7 @@ def load_library():
         L.qp_copy.argtypes = [u64, u64, u64, u64, u64]
         L.qp_op_id.argtypes = [C.c_char_p]
         L.qp_dispatch.argtypes = [C.c_int, vp, u32, vp, u32, u32, u32, u32]
+        L.qp_dispatch_noalloc.argtypes = [C.c_int, vp, u32, vp, u32, u32, u32, u32]
         L.qp_module_load.argtypes = [C.c_char_p, C.POINTER(u64)]
         L.qp_kernel.argtypes = [u64, C.c_char_p, C.POINTER(u64)]
         L.qp_launch.argtypes = [u64, vp, vp, u32, vp, u64]
@@ -170,13 +171,15 @@ class Quipu:
             self._ops[name] = i
         return i
 
-    def dispatch(self, name, u, bufs, grid=(1, 1, 1)):
-        """grupo(name, [u, paso, ...bufs]) + despachar(pass, g, *grid) of the reference facade."""
+    def dispatch(self, name, u, bufs, grid=(1, 1, 1), noalloc=False):
+        """grupo(name, [u, paso, ...bufs]) + despachar(pass, g, *grid) of the reference facade; noalloc: through
+        qp_dispatch_noalloc (workspace from the library's fixed scratch array)."""
         ub = uniform(u) if isinstance(u, (list, tuple)) else bytes(u)
         b = (C.c_uint64 * len(bufs))(*[int(x or 0) for x in bufs])
         g = tuple(grid) + (1,) * (3 - len(grid))
         ubuf = C.create_string_buffer(ub, len(ub))
-        self._check(self.L.qp_dispatch(self.op(name), ubuf, len(ub), b, len(bufs), *g), name)
+        fn = self.L.qp_dispatch_noalloc if noalloc else self.L.qp_dispatch
+        self._check(fn(self.op(name), ubuf, len(ub), b, len(bufs), *g), name)
 
     # -------------------------------------------------------------- weights (device layout)
     def upload_matrix(self, fmt, raw, N, K):

@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "qp_args.h"
+#include "qp_scratch.h"
 
 namespace {
 
@@ -35,6 +36,8 @@ std::mutex g_mu;
 std::unordered_map<uint64_t, uint64_t> g_allocs;  // address -> bytes
 uint64_t g_bytes = 0;
 bool g_capturing = false;
+bool g_noalloc = false;    // inside qp_dispatch_noalloc: the prefill workspace is the fixed scratch array
+uint64_t g_scratch = 0;    // its device address on this device (qp_scratch.hip)
 long g_fail_alloc = -1, g_fail_launch = -1;  // QP_FAIL_ALLOC / QP_FAIL_LAUNCH: fail the Nth call (1-based)
 long g_n_alloc = 0, g_n_launch = 0;
 std::string g_summary, g_arch;
@@ -332,6 +335,13 @@ int op_matmul_1(const Ctx& c, int fmt, const char* name) {
 // (the stream is drained before the old one is freed) and kept until the process ends.  Not while capturing.
 uint64_t g_ws = 0, g_ws_bytes = 0;
 int workspace(uint64_t bytes, uint64_t* out) {
+    if (g_noalloc) {
+        if (bytes > QP_SCRATCH_BYTES)
+            return fail(QP_E_ARG, "qp_dispatch_noalloc: this matmul needs %llu bytes of workspace; the scratch holds %u "
+                                  "(fewer tokens per call)", (unsigned long long)bytes, QP_SCRATCH_BYTES);
+        *out = g_scratch;
+        return 0;
+    }
     if (bytes > g_ws_bytes) {
         if (g_capturing) return fail(QP_E_CAPTURE, "prefill workspace growth during graph capture");
         if (g_ws) {
@@ -372,7 +382,7 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
                     : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
         uint32_t mt = cdiv(tmax, 128);
         const uint32_t nt = cdiv(N, 128);
-        if (!g_capturing) {
+        if (!g_capturing || g_noalloc) {
             // x split into bf16 planes once (not in every weight tile's workgroup), and the K range split when the
             // tiles alone cannot occupy the CUs (a 128-row router at 2048 tokens is 16 tiles); partials summed in
             // order.  K-quants from 256 tokens on: 256-token tiles (one 512-thread workgroup per CU, K steps of 32
@@ -1062,6 +1072,7 @@ int qp_init(int device) {
     if (g_arch.rfind("gfx950", 0) != 0)
         return fail(QP_E_ARG, "device %d is %s; this backend is built for gfx950 only", device, g_arch.c_str());
     HIPCHK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreate");
+    if (int e = qp_scratch::lookup(device, &g_scratch)) return hip_fail((hipError_t)e, "hipGetSymbolAddress (scratch)");
     std::string path;
     if (const char* e = getenv("QP_KERNELS")) path = e;
     else path = self_dir() + "/quipu_kernels.hsaco";
@@ -1177,6 +1188,16 @@ int qp_dispatch(int op, const void* uniform, uint32_t usize, const uint64_t* buf
     if (usize && !uniform) return fail(QP_E_ARG, "%s: null uniform", v[op].name.c_str());
     Ctx c{(const uint8_t*)uniform, usize, bufs, nbuf, gx, gy, gz};
     return v[op].fn(c);
+}
+
+int qp_dispatch_noalloc(int op, const void* uniform, uint32_t usize, const uint64_t* bufs, uint32_t nbuf,
+                        uint32_t gx, uint32_t gy, uint32_t gz) {
+    NEED_INIT();
+    struct Flag {
+        Flag() { g_noalloc = true; }
+        ~Flag() { g_noalloc = false; }
+    } flag;
+    return qp_dispatch(op, uniform, usize, bufs, nbuf, gx, gy, gz);
 }
 
 int qp_module_load(const char* path, uint64_t* module) {
