@@ -505,6 +505,65 @@ def test_kv_write(quipu, dev, oracle, f16):
     assert not gk[:pos0].any() and not gk[pos0 + T:].any()
 
 
+@pytest.mark.parametrize("f16", [0, 1])
+def test_kv_write_ring(quipu, dev, f16):
+    """kv_write into a ring of cap slots (the reference's sliding-window cache, transformer.js:106-111 and
+    gpu.js:461-462): position p goes to slot p % cap; 8 tokens from position 20 of a 24-slot ring wrap to slots
+    20..23 and 0..3, and the other slots keep their contents."""
+    kvd, cap, T, pos0 = 128, 24, 8, 20
+    rng = np.random.default_rng(26)
+    k = rng.standard_normal((T, kvd)).astype(np.float32)
+    v = rng.standard_normal((T, kvd)).astype(np.float32)
+    dt = np.float16 if f16 else np.float32
+    old_k = rng.standard_normal((cap, kvd)).astype(dt)
+    old_v = rng.standard_normal((cap, kvd)).astype(dt)
+    kc = dev.buf(old_k)
+    vc = dev.buf(refs.v_tiled(old_v, kvd) if f16 else old_v)
+    quipu.dispatch("kv_write", [("u", kvd), ("u", cap), ("u", f16), ("u", cap)],
+                   [dev.paso(T, pos0), dev.buf(k), dev.buf(v), kc, vc], ((T * kvd + 255) // 256,))
+    gk = dev.get(kc, (cap, kvd), dt)
+    gv = dev.get(vc, ((cap + 31) // 32 * 32 if f16 else cap, kvd), dt)
+    if f16:
+        gv = refs.v_rows(gv, cap, kvd)
+    want_k, want_v = old_k.copy(), old_v.copy()
+    for t in range(T):
+        want_k[(pos0 + t) % cap] = k[t].astype(dt)
+        want_v[(pos0 + t) % cap] = v[t].astype(dt)
+    np.testing.assert_array_equal(gk, want_k)
+    np.testing.assert_array_equal(gv, want_v)
+
+
+@pytest.mark.parametrize("f16", [0, 1])
+@pytest.mark.parametrize("hd,nh,nkv,T,pos0,swa", [(64, 8, 2, 16, 150, 40), (128, 16, 4, 1, 300, 100),
+                                                  (64, 4, 4, 32, 10, 40)])
+def test_atencion_window_over_a_ring(quipu, dev, oracle, hd, nh, nkv, T, pos0, swa, f16):
+    """atencion with a sliding window of swa keys (measured from each query position) over a ring cache of
+    cap = swa + 32 slots holding positions p at slot p % cap: the same result as the window over the whole cache
+    (the oracle, reference gpu.js:467-539 with swa)."""
+    kvd, cap = nkv * hd, swa + 32
+    rng = np.random.default_rng(27)
+    full = pos0 + T
+    kf = rng.standard_normal((full, kvd)).astype(np.float32)
+    vf = rng.standard_normal((full, kvd)).astype(np.float32)
+    if f16:
+        kf, vf = f16r(kf), f16r(vf)
+    q = rng.standard_normal((T, nh * hd)).astype(np.float32)
+    kr = np.zeros((cap, kvd), np.float32)
+    vr = np.zeros((cap, kvd), np.float32)
+    for p in range(max(0, full - cap), full):
+        kr[p % cap], vr[p % cap] = kf[p], vf[p]
+    dt = np.float16 if f16 else np.float32
+    o = dev.zeros(T * nh * hd * 4)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    quipu.dispatch("atencion", [("u", hd), ("u", nh), ("u", nkv), ("u", swa), ("f", scale), ("u", cap), ("u", 0),
+                                ("u", 0), ("u", f16), ("u", cap)],
+                   [dev.paso(T, pos0), dev.buf(q), dev.buf(kr.astype(dt)),
+                    dev.buf(refs.v_tiled(vr.astype(dt), kvd) if f16 else vr), o], (nh, T))
+    got = dev.get(o, (T, nh * hd))
+    want = oracle.attention(q, kf, vf, T, pos0, nh, nkv, hd, scale, swa=swa)
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
+
+
 def test_kv_write_past_the_cache_writes_nothing(quipu, dev):
     kvd, rows = 64, 4
     kc, vc = dev.zeros(rows * kvd * 4), dev.zeros(rows * kvd * 4)
