@@ -918,23 +918,22 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     const uint32_t nmine = w < total_units ? (total_units - 1 - w) / W + 1 : 0;
     const uint32_t ngrp = K / KQ<FMT>::GROUP;
 
-    // 1. this thread's share of x (and of the norm weight): sub-blocks q = tid + NT i
-    float4 xr[XS][8], nr[XS][8];
+    // 1. this thread's share of x (and of the norm weight): float4 f = tid + NT i of the K / 4, so that each load
+    // instruction of a wave reads 1 KB contiguous (8 lanes per cache line; one lane per line costs the address
+    // unit 8x more work, and the weight loads queue behind it).  K % 256 == 0 keeps the bound wave-uniform.
+    constexpr int NF = 8 * XS;
+    const uint32_t nf4 = K >> 2;
+    float4 xr[NF], nr[NF];
 #pragma unroll
-    for (int i = 0; i < XS; i++) {
-        uint32_t q = tid + NT * i;
-        q = q < (K >> 5) ? q : 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) xr[i][j] = gload<float4>(x + 128ull * q + 16ull * j);
-        if (norm_w) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) nr[i][j] = gload<float4>(norm_w + 128ull * q + 16ull * j);
-        }
+    for (int i = 0; i < NF; i++) {
+        const uint32_t f = tid + NT * i;
+        xr[i] = f < nf4 ? gload<float4>(x + 16ull * f) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (norm_w) nr[i] = f < nf4 ? gload<float4>(norm_w + 16ull * f) : float4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    float xsc[XS];
+    float xsc[NF];
 #pragma unroll
-    for (int i = 0; i < XS; i++) {
-        const uint32_t q = tid + NT * i;
+    for (int i = 0; i < NF; i++) {
+        const uint32_t q = (tid + NT * i) >> 3;   // the float4's sub-block of 32
         xsc[i] = lay.xscale(q < (K >> 5) ? q : 0);  // every lane (a gathered layout shuffles across the wave)
     }
     pro();
@@ -990,40 +989,39 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     }
 
     // 3. stage x (times the norm weight) in LDS with the group sums; sum of squares for the norm
+    // LDS: float4 f at f + f / 64 (one pad per 256 inputs); the group sums of 32 (or 16) inputs over the 8 (or 4)
+    // consecutive lanes that hold them
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < XS; i++) {
-        const uint32_t q = tid + NT * i;
-        if (q < (K >> 5)) {
-            const uint32_t bb = q >> 3, j = q & 7;
-            float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 8; t++) {
-                float4 v = xr[i][t];
-                if constexpr (Lay::SCALED) {
-                    const float f = xsc[i];
-                    v.x *= f;
-                    v.y *= f;
-                    v.z *= f;
-                    v.w *= f;
-                }
-                if (norm_w) {
-                    ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-                    const float4 nw4 = nr[i][t];
-                    v.x *= nw4.x;
-                    v.y *= nw4.y;
-                    v.z *= nw4.z;
-                    v.w *= nw4.w;
-                }
-                xs[bb * 65 + j * 8 + t] = v;
-                if (t < 4) s0 += (v.x + v.y) + (v.z + v.w);
-                else s1 += (v.x + v.y) + (v.z + v.w);
-            }
+    for (int i = 0; i < NF; i++) {
+        const uint32_t f = tid + NT * i;
+        if (NT * i >= nf4) break;  // uniform: no float4 of this round exists
+        float4 v = xr[i];
+        if constexpr (Lay::SCALED) {
+            const float c = xsc[i];
+            v.x *= c;
+            v.y *= c;
+            v.z *= c;
+            v.w *= c;
+        }
+        if (norm_w) {
+            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+            const float4 nw4 = nr[i];
+            v.x *= nw4.x;
+            v.y *= nw4.y;
+            v.z *= nw4.z;
+            v.w *= nw4.w;
+        }
+        float gs = (v.x + v.y) + (v.z + v.w);
+        gs += bfly_f<0>(gs, lane);
+        gs += bfly_f<1>(gs, lane);
+        if constexpr (KQ<FMT>::GROUP == 32) gs += bfly_f<2>(gs, lane);
+        if (f < nf4) {
+            xs[f + (f >> 6)] = v;
             if constexpr (KQ<FMT>::GROUP == 32) {
-                xsum[q] = s0 + s1;
+                if ((lane & 7) == 0) xsum[f >> 3] = gs;
             } else {
-                xsum[2 * q] = s0;
-                xsum[2 * q + 1] = s1;
+                if ((lane & 3) == 0) xsum[f >> 2] = gs;
             }
         }
     }

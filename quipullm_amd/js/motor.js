@@ -41,7 +41,14 @@ class Motor {
 
   post(ruta, datos) { return pedirJSON(this.servidor + ruta, 'POST', datos, 60000); }
 
-  evento(d) { return this.post('/engine/api/event', Object.assign({ motor: this.id }, d)); }
+  // Events reach the server in the order they are made: each is posted after the previous one completed (progress
+  // events are not awaited by the generation loop, so without the chain two of them could overtake each other).
+  evento(d) {
+    const self = this, cuerpo = Object.assign({ motor: this.id }, d);
+    const p = (this.cadena || Promise.resolve()).then(function () { return self.post('/engine/api/event', cuerpo); });
+    this.cadena = p.catch(function () {});
+    return p;
+  }
 
   informarEstado(estado) {
     return this.evento({ tipo: 'estado', modelo_cargado: this.modeloId, estado: estado, info: this.info });
