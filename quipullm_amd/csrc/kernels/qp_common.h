@@ -260,66 +260,3 @@ QP_DEV void sincos2(float x, float& sn_out, float& cs_out) {
     else { sn_out = -cs; cs_out = sn; }
 }
 
-// RoPE of element i of a head vector v (shared memory), reference norm_rope (gpu.js:424-441).
-QP_DEV float rope_elem(const float* v, uint32_t i, uint32_t nrot, bool neox, float pos_esc, float base) {
-    float r = v[i];
-    if (i < nrot) {
-        const uint32_t mitad = nrot / 2;
-        uint32_t j;
-        float a, b;
-        bool primero;
-        if (neox) {
-            j = i % mitad;
-            if (i < mitad) { a = v[i]; b = v[i + mitad]; } else { a = v[i - mitad]; b = v[i]; }
-            primero = i < mitad;
-        } else {
-            j = i / 2;
-            const uint32_t i0 = i - (i % 2);
-            a = v[i0]; b = v[i0 + 1];
-            primero = (i % 2) == 0;
-        }
-        const float ex = (-2.0f * (float)j) / (float)nrot;
-        // base^ex rounded once to float (evaluated in double): the frequency does not depend on a powf's accuracy
-        const float theta = pos_esc * (float)pow((double)base, (double)ex);
-        float sn, c;
-        sincos2(theta, sn, c);
-        r = primero ? (a * c - b * sn) : (a * sn + b * c);
-    }
-    return r;
-}
-
-// Optional per-head RMSNorm then RoPE of one head vector held in shared memory (hd <= 256), done by one
-// wavefront; `lane` in 0..63.
-QP_DEV void wave_norm_rope(float* v, const float* w, uint32_t hd, bool use_norm, float eps, float pos_esc,
-                           float base, uint32_t nrot, bool neox, int lane) {
-    float vals[4];
-    float ss = 0.0f;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const uint32_t i = lane + 64 * c;
-        vals[c] = i < hd ? v[i] : 0.0f;
-        ss += vals[c] * vals[c];
-    }
-    ss = wave_sum(ss);
-    if (use_norm) {
-        const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const uint32_t i = lane + 64 * c;
-            if (i < hd) v[i] = (vals[c] * inv) * w[i];
-        }
-    }
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const uint32_t i = lane + 64 * c;
-        if (i < hd) vals[c] = rope_elem(v, i, nrot, neox, pos_esc, base);
-    }
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const uint32_t i = lane + 64 * c;
-        if (i < hd) v[i] = vals[c];
-    }
-    __builtin_amdgcn_wave_barrier();
-}

@@ -2394,63 +2394,42 @@ QP_DEV float group_sum(float v) {
     return v;
 }
 
-// RoPE of element i with the frequency table freq[j] = base^(-2j/nrot) (rounded once to float).
-QP_DEV float rope_elem_f(const float* v, uint32_t i, uint32_t nrot, bool neox, float pos_esc, const float* freq) {
-    float r = v[i];
-    if (i < nrot) {
-        const uint32_t mitad = nrot / 2;
-        uint32_t j;
-        float a, b;
-        bool primero;
-        if (neox) {
-            j = i % mitad;
-            if (i < mitad) { a = v[i]; b = v[i + mitad]; } else { a = v[i - mitad]; b = v[i]; }
-            primero = i < mitad;
-        } else {
-            j = i / 2;
-            const uint32_t i0 = i - (i % 2);
-            a = v[i0]; b = v[i0 + 1];
-            primero = (i % 2) == 0;
-        }
-        const float theta = pos_esc * freq[j];
-        float sn, c;
-        sincos2(theta, sn, c);
-        r = primero ? (a * c - b * sn) : (a * sn + b * c);
-    }
-    return r;
-}
-
-// wave_norm_rope with a frequency table in LDS (same values as rope_elem computes per element).
+// A wavefront's head in LDS: optional RMSNorm (weight w), then RoPE at angle pos_esc * freq[j] (the frequency
+// table base^(-2j/nrot) in LDS), pairs (j, j + nrot/2) when neox, else (2j, 2j + 1).
 QP_DEV void wave_norm_rope_f(float* v, const float* w, uint32_t hd, bool use_norm, float eps, float pos_esc,
                              const float* freq, uint32_t nrot, bool neox, int lane) {
-    float vals[4];
     if (use_norm) {
-        float ss = 0.0f;
+        float vals[4], ss = 0.0f;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t i = lane + 64 * c;
             vals[c] = i < hd ? v[i] : 0.0f;
             ss += vals[c] * vals[c];
         }
-        ss = wave_sum(ss);
+        ss = wave_sum_v(ss, (uint32_t)lane);  // the cross-lane steps on DPP / permlane, not through LDS
         const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t i = lane + 64 * c;
             if (i < hd) v[i] = (vals[c] * inv) * w[i];
         }
+        __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_wave_barrier();
+    // one lane per rotated pair (elements p and p + nrot/2, or 2p and 2p + 1): the angle's sine and cosine once
+    // per pair; each lane reads and writes only its own pair, so no barrier separates the reads from the writes
+    const uint32_t mitad = nrot / 2;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const uint32_t i = lane + 64 * c;
-        if (i < hd) vals[c] = rope_elem_f(v, i, nrot, neox, pos_esc, freq);
-    }
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const uint32_t i = lane + 64 * c;
-        if (i < hd) v[i] = vals[c];
+    for (int c = 0; c < 2; c++) {
+        const uint32_t pr = lane + 64 * c;
+        if (pr < mitad) {
+            const uint32_t i0 = neox ? pr : 2 * pr, i1 = neox ? pr + mitad : 2 * pr + 1;
+            const float a = v[i0], b = v[i1];
+            const float theta = pos_esc * freq[pr];
+            float sn, cs;
+            sincos2(theta, sn, cs);
+            v[i0] = a * cs - b * sn;
+            v[i1] = a * sn + b * cs;
+        }
     }
     __builtin_amdgcn_wave_barrier();
 }

@@ -292,6 +292,33 @@ def test_matmul_prefill_mfma(quipu, dev, oracle, fmt, T, N, K, acc):
     assert np.all(np.abs(got - want) <= bound)
 
 
+@pytest.mark.parametrize("T,N,K", [(256, 300, 4096), (700, 130, 1024)])
+def test_matmul_q4k_prefill_row_magnitudes(quipu, dev, oracle, T, N, K):
+    """Q4_K prefill from 256 tokens on (the 256-token tiles, inputs as bf16 high + low planes): token rows of
+    magnitude 1e-20 .. 1e20, an all-zero row and rows with one outlier 1e6 times the rest stay within the float32
+    dot bound; the all-zero row gives exact zeros."""
+    raw = raw_matrix(capi.Q4_K, N, K, 62)
+    W = oracle.dequant(capi.Q4_K, raw, N * K).reshape(N, K)
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    mags = 10.0 ** rng.integers(-20, 21, size=T)
+    x *= mags[:, None].astype(np.float32)
+    x[3] = 0.0
+    x[5, 7] *= 1e6
+    x[6, K - 1] = 1e4
+    x = x.astype(np.float32)
+    y = dev.zeros(4 * T * N)
+    quipu.dispatch("matmul_q4k_t", [("u", N), ("u", K), ("u", 0), ("u", 0)],
+                   [dev.paso(T, 0), dev.matrix(capi.Q4_K, raw, N, K), dev.buf(x), y],
+                   ((N + 63) // 64, 1, (T + 31) // 32))
+    got = dev.get(y, (T, N))
+    want = (W.astype(np.float64) @ x.astype(np.float64).T).T
+    bound = (np.abs(W.astype(np.float64)) @ np.abs(x.astype(np.float64)).T).T * 2e-5 + 1e-30
+    assert np.all(np.isfinite(got))
+    assert np.all(got[3] == 0.0)
+    assert np.all(np.abs(got - want) <= bound)
+
+
 @pytest.mark.parametrize("fmt,K", [(capi.Q8_0, 288), (capi.Q8_0, 544), (capi.F32, 80), (capi.F32, 272),
                                    (capi.F32, 528)])
 @pytest.mark.parametrize("T,N", [(64, 77), (130, 300)])
