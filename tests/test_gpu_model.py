@@ -244,8 +244,6 @@ def test_sampled_decode_matches_host_sampler(models_dir, tmp_path, name, pi):
     host.  Every token is also chosen on the host from the same logits by a second sampler with the same seed
     (the reference's procedure over the whole array): the penalized logits agree bit for bit and the chosen
     tokens are identical; the device candidates serve every step where the sampler allows them."""
-    if name == "tiny_q8" and pi not in (0, 2):
-        pytest.skip("the realistic vocabulary runs the device-candidate cases only")
     params = SAMPLER_PARAMS[pi]
     path = synth.ensure_model(name, models_dir)
     vocab = synth.CONFIGS[name].vocab
