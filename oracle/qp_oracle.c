@@ -28,6 +28,7 @@
 #define OR_Q4_K 12
 #define OR_Q5_K 13
 #define OR_Q6_K 14
+#define OR_IQ4_NL 20
 
 /* ------------------------------------------------------------------ f16 -> f32 (exact)
  * web/js/gpu.js:939-948 (F16 table); unpack2x16float in kquants.js:67 is the same map. */
@@ -181,6 +182,18 @@ static inline float q8_deq(const uint8_t* blk, int e) {
     return (float)(int8_t)blk[2 + e] * d;
 }
 
+/* ------------------------------------------------------------------ IQ4_NL
+ * Block: d f16 + 16 bytes; the low nibble of byte l indexes weight l, the high nibble weight 16 + l, in the
+ * 16-entry table (kds.js:36-39, the reference's conversion tests/conformance/gen_ds.py:104-129); element =
+ * d * table[nibble] (kds.js:80-84 scale the block's sum by d; one product per element here). */
+static const float IQ4NL_KV[16] = {-127.0f, -104.0f, -83.0f, -65.0f, -49.0f, -35.0f, -22.0f, -10.0f,
+                                   1.0f,    13.0f,   25.0f,  38.0f,  53.0f,  69.0f,  89.0f,  113.0f};
+static inline float iq4nl_deq(const uint8_t* blk, int e) {
+    float d = or_f16(rd16(blk));
+    unsigned q = e < 16 ? (blk[2 + e] & 15u) : (blk[2 + e - 16] >> 4);
+    return d * IQ4NL_KV[q];
+}
+
 void or_dequant(int fmt, const uint8_t* raw, int64_t nelem, float* out) {
     int64_t i;
     if (fmt == OR_Q4_K) {
@@ -195,6 +208,8 @@ void or_dequant(int fmt, const uint8_t* raw, int64_t nelem, float* out) {
         for (i = 0; i < nelem; i++) out[i] = q6k_deq(raw + (i >> 8) * 210, (int)(i & 255));
     } else if (fmt == OR_Q8_0) {
         for (i = 0; i < nelem; i++) out[i] = q8_deq(raw + (i >> 5) * 34, (int)(i & 31));
+    } else if (fmt == OR_IQ4_NL) {
+        for (i = 0; i < nelem; i++) out[i] = iq4nl_deq(raw + (i >> 5) * 18, (int)(i & 31));
     } else {
         memcpy(out, raw, (size_t)nelem * 4);
     }
@@ -377,6 +392,33 @@ static float row_q8(const uint8_t* row, int K, const float* x) {
     return tree32(lanes);
 }
 
+/* matmul_iq4nl_1 (kds.js:41-101, nt = 1): 32 lanes stride over the blocks; a block's sum s over its four words
+ * (dot of the 4 low-nibble weights with x[8b + w], then of the 4 high ones with x[8b + 4 + w]), then
+ * acc += d * s; the LDS tree over the lanes. */
+static float row_iq4nl(const uint8_t* row, int K, const float* x) {
+    int nb = K / 32;
+    float lanes[32];
+    for (int lane = 0; lane < 32; lane++) {
+        float acc = 0.0f;
+        for (int b = lane; b < nb; b += 32) {
+            const uint8_t* blk = row + (size_t)b * 18;
+            float d = or_f16(rd16(blk));
+            float s = 0.0f;
+            for (int w = 0; w < 4; w++) {
+                float lo[4], hi[4];
+                for (int c = 0; c < 4; c++) {
+                    lo[c] = IQ4NL_KV[blk[2 + w * 4 + c] & 15u];
+                    hi[c] = IQ4NL_KV[blk[2 + w * 4 + c] >> 4];
+                }
+                s = s + (dot4(lo, x + b * 32 + w * 4) + dot4(hi, x + b * 32 + 16 + w * 4));
+            }
+            acc = acc + d * s;
+        }
+        lanes[lane] = acc;
+    }
+    return tree32(lanes);
+}
+
 static float row_f32(const float* row, int K, const float* x) {
     int k4 = K / 4;
     float lanes[32];
@@ -396,6 +438,7 @@ static size_t row_bytes(int fmt, int K) {
     case OR_Q2_K: return (size_t)(K / 256) * 84;
     case OR_Q6_K: return (size_t)(K / 256) * 210;
     case OR_Q8_0: return (size_t)(K / 32) * 34;
+    case OR_IQ4_NL: return (size_t)(K / 32) * 18;
     default: return (size_t)K * 4;
     }
 }
@@ -408,6 +451,7 @@ static float row_dot(int fmt, const uint8_t* row, int K, const float* x) {
     case OR_Q2_K: return row_q2k(row, K, x);
     case OR_Q6_K: return row_q6k(row, K, x);
     case OR_Q8_0: return row_q8(row, K, x);
+    case OR_IQ4_NL: return row_iq4nl(row, K, x);
     default: return row_f32((const float*)row, K, x);
     }
 }
@@ -424,6 +468,7 @@ static float row_serial(int fmt, const uint8_t* row, int K, const float* x) {
         else if (fmt == OR_Q2_K) w = q2k_deq(row + (size_t)(k >> 8) * 84, k & 255);
         else if (fmt == OR_Q6_K) w = q6k_deq(row + (size_t)(k >> 8) * 210, k & 255);
         else if (fmt == OR_Q8_0) w = q8_deq(row + (size_t)(k >> 5) * 34, k & 31);
+        else if (fmt == OR_IQ4_NL) w = iq4nl_deq(row + (size_t)(k >> 5) * 18, k & 31);
         else w = ((const float*)row)[k];
         c = c + w * x[k];
     }
@@ -468,6 +513,7 @@ static void row_deq(int fmt, const uint8_t* row, int K, float* w) {
             else if (fmt == OR_Q3_K) v = q3k_deq(row + (size_t)(k >> 8) * 110, k & 255);
             else if (fmt == OR_Q2_K) v = q2k_deq(row + (size_t)(k >> 8) * 84, k & 255);
             else if (fmt == OR_Q8_0) v = q8_deq(row + (size_t)(k >> 5) * 34, k & 31);
+            else if (fmt == OR_IQ4_NL) v = iq4nl_deq(row + (size_t)(k >> 5) * 18, k & 31);
             else v = ((const float*)row)[k];
             w[k] = v;
         }
@@ -612,6 +658,7 @@ void or_embed(int fmt, const uint8_t* W, int D, const uint32_t* ids, int T, floa
             else if (fmt == OR_Q2_K) v = q2k_deq(row + (size_t)(k >> 8) * 84, k & 255);
             else if (fmt == OR_Q6_K) v = q6k_deq(row + (size_t)(k >> 8) * 210, k & 255);
             else if (fmt == OR_Q8_0) v = q8_deq(row + (size_t)(k >> 5) * 34, k & 31);
+            else if (fmt == OR_IQ4_NL) v = iq4nl_deq(row + (size_t)(k >> 5) * 18, k & 31);
             else v = ((const float*)row)[k];
             y[(size_t)t * D + k] = v;
         }

@@ -18,10 +18,11 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "lib", "libquipu.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "quipu.h")
 
-F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 8, 10, 11, 12, 13, 14
+F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL = 0, 8, 10, 11, 12, 13, 14, 20
 BLOCK = {F32: (1, 4), Q8_0: (32, 34), Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176),
-         Q6_K: (256, 210)}
-FMT_NAME = {F32: "f32", Q8_0: "q8", Q2_K: "q2k", Q3_K: "q3k", Q4_K: "q4k", Q5_K: "q5k", Q6_K: "q6k"}
+         Q6_K: (256, 210), IQ4_NL: (32, 18)}
+FMT_NAME = {F32: "f32", Q8_0: "q8", Q2_K: "q2k", Q3_K: "q3k", Q4_K: "q4k", Q5_K: "q5k", Q6_K: "q6k",
+            IQ4_NL: "iq4nl"}
 
 # gemv segment modes (qp_args.h)
 STORE, ACC, SWIGLU, ARGMAX = 0, 1, 2, 3
@@ -103,8 +104,16 @@ def gguf_bytes(fmt, N, K):
 
 
 def device_bytes(fmt, N, K):
-    """Bytes of the device tensor: the GGUF size, except Q3_K blocks padded to 112 bytes."""
+    """Bytes of the device tensor: the GGUF size, except Q3_K blocks padded to 112 bytes and IQ4_NL repacked into
+    the Q8_0 layout (34 bytes per 32 weights)."""
+    if fmt == IQ4_NL:
+        return N * K // 32 * 34
     return N * K // 256 * 112 if fmt == Q3_K else gguf_bytes(fmt, N, K)
+
+
+def layout_fmt(fmt):
+    """The format code of the device layout a tensor of GGUF type fmt is held in (IQ4_NL: Q8_0)."""
+    return Q8_0 if fmt == IQ4_NL else fmt
 
 
 class Quipu:
@@ -184,7 +193,7 @@ class Quipu:
     # -------------------------------------------------------------- weights (device layout)
     def upload_matrix(self, fmt, raw, N, K):
         """GGUF blocks of an N x K matrix -> device tensor in this backend's layout (repacked on the device: Q4_K,
-        Q5_K and Q6_K to row chunk planes, Q8_0 to planar qs | d).  Returns the handle."""
+        Q5_K and Q6_K to row chunk planes, Q8_0 to planar qs | d, IQ4_NL to the Q8_0 layout).  Returns the handle."""
         raw = np.ascontiguousarray(np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray)) else raw)
         assert raw.nbytes == gguf_bytes(fmt, N, K), (raw.nbytes, gguf_bytes(fmt, N, K))
         if fmt == F32:
@@ -193,7 +202,7 @@ class Quipu:
         dst = self.alloc(device_bytes(fmt, N, K))
         nb = N * K // BLOCK[fmt][0]
         op = {Q2_K: "repack_q2k", Q3_K: "repack_q3k", Q4_K: "repack_q4k", Q5_K: "repack_q5k", Q6_K: "repack_q6k",
-              Q8_0: "repack_q8"}[fmt]
+              Q8_0: "repack_q8", IQ4_NL: "repack_iq4nl"}[fmt]
         self.dispatch(op, [("u", nb & 0xFFFFFFFF), ("u", nb >> 32), ("u", K)], [0, staging, dst])
         self.sync()
         self.free(staging)
@@ -202,7 +211,7 @@ class Quipu:
     def dequant(self, fmt, h, nelem, K):
         """The device tensor h (rows of K elements) dequantized to f32, in element order."""
         y = self.alloc(nelem * 4)
-        self.dispatch("dequant", [("u", fmt), ("u", nelem & 0xFFFFFFFF), ("u", nelem >> 32), ("u", K)], [0, h, y])
+        self.dispatch("dequant", [("u", layout_fmt(fmt)), ("u", nelem & 0xFFFFFFFF), ("u", nelem >> 32), ("u", K)], [0, h, y])
         out = self.download(y, (nelem,))
         self.free(y)
         return out
@@ -246,10 +255,12 @@ class Quipu:
 
 def gemv_uniform(nseg, K, eps=0.0, last_row=0, R=0, max_wg=0, fmt=Q4_K, segs=()):
     """P of the fused `gemv` op: segs = [(mode, n, row_base, rows_total[, seg_fmt]), ...]; a segment's own format
-    (Q4_K / Q6_K mixed in one launch) rides in bits 8..15 of its mode word."""
-    u = [("u", nseg), ("u", K), ("f", eps), ("u", last_row), ("u", R), ("u", max_wg), ("u", fmt), ("u", 0)]
+    (Q4_K / Q6_K mixed in one launch) rides in bits 8..15 of its mode word.  Formats are GGUF types, written as
+    the code of their device layout (IQ4_NL: Q8_0)."""
+    u = [("u", nseg), ("u", K), ("f", eps), ("u", last_row), ("u", R), ("u", max_wg), ("u", layout_fmt(fmt)),
+         ("u", 0)]
     for sg in segs:
         mode, n, rb, rt = sg[:4]
-        sf = sg[4] if len(sg) > 4 else 0
+        sf = layout_fmt(sg[4]) if len(sg) > 4 else 0
         u += [("u", mode | (sf << 8)), ("u", n), ("u", rb), ("u", rt)]
     return u

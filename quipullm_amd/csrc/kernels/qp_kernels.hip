@@ -88,6 +88,26 @@ KERNEL __launch_bounds__(256) void qp_repack_q8(QpRepackArgs a) {
     }
 }
 
+// IQ4_NL (GGML type 20, reference weights.js:110-116 and kds.js:36-39): 18-byte blocks of 32 weights, d (f16)
+// then 16 bytes whose low nibbles index weights 0..15 and high nibbles weights 16..31 in the non-linear table
+// below; weight = d * table[nibble].  Repacked into the planar Q8_0 layout with q = table[nibble] (every entry
+// is an int8): the Q8_0 element q * d is the same single product, so every Q8_0 kernel computes IQ4_NL exactly.
+KERNEL __launch_bounds__(256) void qp_repack_iq4nl(QpRepackArgs a) {
+    constexpr int8_t kv[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+    const uint64_t NB = a.nblocks;
+    for (uint64_t b = blockIdx.x * 256ull + threadIdx.x; b < NB; b += (uint64_t)gridDim.x * 256ull) {
+        const uint8_t* s = cptr<uint8_t>(a.src) + b * 18;
+        uint8_t* d = mptr<uint8_t>(a.dst);
+        for (int l = 0; l < 16; l++) {
+            const uint8_t q = s[2 + l];
+            d[b * 32 + l] = (uint8_t)kv[q & 15];
+            d[b * 32 + 16 + l] = (uint8_t)kv[q >> 4];
+        }
+        d[NB * 32 + b * 2] = s[0];
+        d[NB * 32 + b * 2 + 1] = s[1];
+    }
+}
+
 KERNEL __launch_bounds__(256) void qp_fill_u32(QpFillArgs a) {
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < a.count; i += (uint64_t)gridDim.x * 256ull)
         mptr<uint32_t>(a.dst)[i] = a.value;
@@ -1489,6 +1509,25 @@ QP_DEV void mm_wload(MmW& r, const QpGemmArgs& g, uint32_t row, bool on, uint32_
         r.e = gload<uint4>(base + (uint64_t)12 * nb * 16);
         const uint64_t NB = (uint64_t)(g.wrows ? g.wrows : g.n) * nb;
         r.f = gload<uint16_t>(g.w + NB * 208 + ((uint64_t)row * nb + b) * 2);
+    } else if constexpr (FMT == QP_Q5_K || FMT == QP_Q3_K || FMT == QP_Q2_K) {
+        // sub-block J of 32 (elements l = 0..31 in k order): its 32 quant bytes (a, b), the high-bit bytes (c, d:
+        // Q5_K qh, Q3_K hmask), the scales chunk (e) and, for Q2_K, the (d, dmin) word (f)
+        constexpr uint32_t RB = KQ<FMT>::RB;
+        const uint32_t nb = K >> 8, b = k0 >> 8, J = ((k0 & 255) >> 5) + part, n = J >> 2;
+        const uint64_t base = g.w + (uint64_t)row * nb * RB + b * 16;
+        const uint32_t cq = FMT == QP_Q5_K ? 3 + 2 * (J >> 1) : FMT == QP_Q3_K ? 2 + 2 * n : 1 + 2 * n;
+        r.a = gload<uint4>(base + (uint64_t)cq * nb * 16);
+        r.b = gload<uint4>(base + (uint64_t)(cq + 1) * nb * 16);
+        if constexpr (FMT != QP_Q2_K) {
+            const uint32_t ch = FMT == QP_Q5_K ? 1 : 0;
+            r.c = gload<uint4>(base + (uint64_t)ch * nb * 16);
+            r.d = gload<uint4>(base + (uint64_t)(ch + 1) * nb * 16);
+        }
+        r.e = gload<uint4>(base + (uint64_t)(FMT == QP_Q3_K ? 6 : 0) * nb * 16);
+        if constexpr (FMT == QP_Q2_K) {
+            const uint64_t NB = (uint64_t)(g.wrows ? g.wrows : g.n) * nb;
+            r.f = gload<uint32_t>(g.w + NB * 80 + ((uint64_t)row * nb + b) * 4);
+        }
     } else if constexpr (FMT == QP_Q8_0) {
         const uint64_t NB = (uint64_t)(g.wrows ? g.wrows : g.n) * (K >> 5);
         const uint64_t blk = (uint64_t)row * (K >> 5) + (k0 >> 5) + part;
@@ -1536,6 +1575,49 @@ QP_DEV void mm_wdeq(const MmW& r, const QpGemmArgs& g, uint32_t row, bool on, ui
             const uint32_t hb = (hi[l >> 2] >> ((l & 3) * 8 + qd * 2)) & 3u;
             const float q = (float)(lb | (hb << 4)) - 32.0f;
             w[l] = (l < 16 ? fd0 : fd1) * q;
+        }
+    } else if constexpr (FMT == QP_Q5_K || FMT == QP_Q3_K || FMT == QP_Q2_K) {
+        // the element formulas of deq_q5k_dev / deq_q3k_dev / deq_q2k_dev, same roundings
+        const uint32_t J = ((k0 & 255) >> 5) + part, n = J >> 2, jj = J & 3;
+        const uint32_t qv[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+        if constexpr (FMT == QP_Q5_K) {
+            const uint32_t hv[8] = {r.c.x, r.c.y, r.c.z, r.c.w, r.d.x, r.d.y, r.d.z, r.d.w};
+            uint32_t sc, mn;
+            q4k_sm(r.e.y, r.e.z, r.e.w, J, sc, mn);
+            const float fd = h2f(r.e.x & 0xffffu) * (float)sc, fm = h2f(r.e.x >> 16) * (float)mn;
+#pragma unroll
+            for (int l = 0; l < 32; l++) {
+                const uint32_t lo = (qv[l >> 2] >> ((l & 3) * 8 + (J & 1) * 4)) & 15u;
+                const uint32_t hi = (hv[l >> 2] >> ((l & 3) * 8 + J)) & 1u;
+                const float a = fd * (float)(lo + 16u * hi);
+                w[l] = a - fm;
+            }
+        } else if constexpr (FMT == QP_Q3_K) {
+            const uint32_t hv[8] = {r.c.x, r.c.y, r.c.z, r.c.w, r.d.x, r.d.y, r.d.z, r.d.w};
+            const float d = h2f(r.e.w & 0xffffu);
+            const uint32_t s0 = 8 * n + 2 * jj;  // scale group of l < 16; s0 + 1 for l >= 16
+            const float fd0 = d * ((float)q3k_scale6(r.e.x, r.e.y, r.e.z, s0) - 32.0f);
+            const float fd1 = d * ((float)q3k_scale6(r.e.x, r.e.y, r.e.z, s0 + 1) - 32.0f);
+#pragma unroll
+            for (int l = 0; l < 32; l++) {
+                const uint32_t q2 = (qv[l >> 2] >> ((l & 3) * 8 + 2 * jj)) & 3u;
+                const uint32_t hm = (hv[l >> 2] >> ((l & 3) * 8 + 4 * n + jj)) & 1u;
+                w[l] = (l < 16 ? fd0 : fd1) * ((float)q2 - 4.0f * (float)(1u - hm));
+            }
+        } else {
+            const float d = h2f(r.f & 0xffffu), dmin = h2f(r.f >> 16);
+            const uint32_t sv[4] = {r.e.x, r.e.y, r.e.z, r.e.w};
+            const uint32_t j0 = 8 * n + 2 * jj;  // scale byte of l < 16; j0 + 1 for l >= 16
+            const uint32_t sc0 = (sv[j0 >> 2] >> ((j0 & 3) * 8)) & 0xffu;
+            const uint32_t sc1 = (sv[(j0 + 1) >> 2] >> (((j0 + 1) & 3) * 8)) & 0xffu;
+            const float fd0 = d * (float)(sc0 & 15u), fm0 = dmin * (float)(sc0 >> 4);
+            const float fd1 = d * (float)(sc1 & 15u), fm1 = dmin * (float)(sc1 >> 4);
+#pragma unroll
+            for (int l = 0; l < 32; l++) {
+                const uint32_t q = (qv[l >> 2] >> ((l & 3) * 8 + 2 * jj)) & 3u;
+                const float a = (l < 16 ? fd0 : fd1) * (float)q;
+                w[l] = a - (l < 16 ? fm0 : fm1);
+            }
         }
     } else if constexpr (FMT == QP_Q8_0) {
         const float d = h2f(r.f);
@@ -2039,6 +2121,9 @@ KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q6k(QpGemmArgs a) { gemm_mfma
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q4k(QpGemmArgs a) { gemm_mfma_body<QP_Q4_K>(a); }
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q6k(QpGemmArgs a) { gemm_mfma_body<QP_Q6_K>(a); }
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q8(QpGemmArgs a) { gemm_mfma_body<QP_Q8_0>(a); }
+KERNEL __launch_bounds__(256) void qp_gemm_mfma_q5k(QpGemmArgs a) { gemm_mfma_body<QP_Q5_K>(a); }
+KERNEL __launch_bounds__(256) void qp_gemm_mfma_q3k(QpGemmArgs a) { gemm_mfma_body<QP_Q3_K>(a); }
+KERNEL __launch_bounds__(256) void qp_gemm_mfma_q2k(QpGemmArgs a) { gemm_mfma_body<QP_Q2_K>(a); }
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_f32(QpGemmArgs a) { gemm_mfma_body<QP_F32>(a); }
 
 // ====================================================================================== RMSNorm

@@ -139,6 +139,7 @@ int fmt_of(const char* s) {
     if (!strcmp(s, "q2k")) return QP_Q2_K;
     if (!strcmp(s, "q6k")) return QP_Q6_K;
     if (!strcmp(s, "q8")) return QP_Q8_0;
+    if (!strcmp(s, "iq4nl")) return QP_Q8_0;  // IQ4_NL matrices are repacked into the Q8_0 layout
     if (!strcmp(s, "f32")) return QP_F32;
     return -1;
 }
@@ -735,11 +736,31 @@ int op_matmul_eg(const Ctx& c, int fmt, const char* name) {
     a.tpe = cdiv(32 * tz, 128);
     if ((uint64_t)E * a.tpe > 65535) return fail(QP_E_ARG, "%s: %u experts x %u job tiles", name, E, a.tpe);
     const Kid k = fmt == QP_Q4_K ? K_gemm_mfma_q4k : fmt == QP_Q6_K ? K_gemm_mfma_q6k
-                : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
+                : fmt == QP_Q5_K ? K_gemm_mfma_q5k : fmt == QP_Q3_K ? K_gemm_mfma_q3k
+                : fmt == QP_Q2_K ? K_gemm_mfma_q2k : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
     return launch(k, cdiv(N, 128), E * a.tpe, 1, 256, 0, a);
 }
 
 // ------------------------------------------------------------------------------------------------ backend ops
+// Formats a format word may name: f32, Q8_0 (planar) and the K-quants (row chunk planes).
+bool known_fmt(int f) { return f == QP_F32 || f == QP_Q8_0 || is_kq(f); }
+
+// Bytes of a device tensor of `rows` rows of K elements in the layout of fmt.
+uint64_t tensor_bytes(int fmt, uint64_t rows, uint32_t K) {
+    if (is_kq(fmt)) return kq_tensor_bytes(fmt, rows, K);
+    if (fmt == QP_Q8_0) return rows * K + rows * (K / 32) * 2;
+    return rows * K * 4ull;
+}
+
+// A library buffer bound at p must hold `bytes` from p (pointers the library did not allocate are not checked).
+int need_room(uint64_t p, uint64_t bytes, const char* op, const char* what) {
+    const uint64_t r = buf_room(p);
+    if (r && r < bytes)
+        return fail(QP_E_ARG, "%s: %s holds %llu bytes from its binding, %llu needed", op, what,
+                    (unsigned long long)r, (unsigned long long)bytes);
+    return 0;
+}
+
 // gemv: fused one-token GEMV over up to 4 same-format segments.
 // P{nseg, K, eps, last_row, R, max_wg, fmt, 0, then per segment {mode | seg_fmt << 8, n, row_base, rows_total}};
 // seg_fmt 0 means fmt; Q4_K and Q6_K segments may share a launch.
@@ -758,6 +779,7 @@ int op_gemv(const Ctx& c) {
     if (R != 1 && R != 2 && R != 4 && R != 8) return fail(QP_E_ARG, "gemv: R=%d", R);
     const uint32_t max_wg = c.U(5);
     const int fmt = (int)c.U(6);
+    if (!known_fmt(fmt)) return fail(QP_E_ARG, "gemv: format %d is not a device layout (f32 0, Q8_0 8, K-quants 10..14)", fmt);
     a.paso = c.B(0);
     a.x = c.B(1);
     a.norm_w = c.B(2);
@@ -778,6 +800,13 @@ int op_gemv(const Ctx& c) {
         if (s.mode > QP_GEMV_ARGMAX) return fail(QP_E_ARG, "gemv: mode %u", s.mode);
         if (s.mode == QP_GEMV_SWIGLU && !s.w2) return fail(QP_E_ARG, "gemv: SwiGLU segment without w2");
         if (s.mode == QP_GEMV_ARGMAX && !a.amax) return fail(QP_E_ARG, "gemv: argmax segment without amax");
+        if (s.row_base + (uint64_t)s.n > s.rows_total)
+            return fail(QP_E_ARG, "gemv: segment %u rows %u..%u past the tensor's %u", i, s.row_base,
+                        s.row_base + s.n, s.rows_total);
+        const uint64_t tb = tensor_bytes((int)s.fmt, s.rows_total, a.k);
+        if (int e = need_room(s.w, tb, "gemv", "a segment's weight buffer")) return e;
+        if (s.mode == QP_GEMV_SWIGLU)
+            if (int e = need_room(s.w2, tb, "gemv", "a segment's second weight buffer")) return e;
     }
     return run_gemv(fmt, a, R, max_wg, nullptr);
 }
@@ -926,6 +955,13 @@ int op_repack(const Ctx& c, Kid k, const char* name) {
     a.src = c.B(1);
     a.dst = c.B(2);
     uint64_t threads = a.nblocks;
+    if (k == K_repack_q8 || k == K_repack_iq4nl) {
+        // raw blocks of 34 (Q8_0) or 18 (IQ4_NL) bytes -> 34 bytes each in the planar layout
+        const uint64_t rs = buf_room(a.src), rd = buf_room(a.dst), in = a.nblocks * (k == K_repack_q8 ? 34 : 18);
+        if ((rs && rs < in) || (rd && rd < a.nblocks * 34))
+            return fail(QP_E_ARG, "%s: %llu blocks need %llu source and %llu destination bytes", name,
+                        (unsigned long long)a.nblocks, (unsigned long long)in, (unsigned long long)(a.nblocks * 34));
+    }
     if (k == K_repack_q4k || k == K_repack_q5k || k == K_repack_q6k || k == K_repack_q3k || k == K_repack_q2k) {
         if (a.k == 0 || a.k % 256 || a.k > 15360) return fail(QP_E_ARG, "%s: K=%u must be a multiple of 256 <= 15360", name, a.k);
         if (a.nblocks % (a.k / 256)) return fail(QP_E_ARG, "%s: %llu blocks are not whole rows of K=%u", name,
@@ -966,10 +1002,13 @@ int op_dequant(const Ctx& c) {
     a.k = c.U(3);
     a.w = c.B(1);
     a.y = c.B(2);
+    if (!known_fmt((int)a.fmt)) return fail(QP_E_ARG, "dequant: format %u is not a device layout", a.fmt);
     if (a.k == 0) a.k = (a.fmt == QP_Q8_0) ? 32 : (a.fmt == QP_F32 ? 1 : 256);  // one row per block
     if (int e = check_k((int)a.fmt, a.k, "dequant")) return e;
     if (a.nelem % a.k) return fail(QP_E_ARG, "dequant: %llu elements are not whole rows of K=%u",
                                    (unsigned long long)a.nelem, a.k);
+    if (int e = need_room(a.w, tensor_bytes((int)a.fmt, a.nelem / a.k, a.k), "dequant", "the tensor")) return e;
+    if (int e = need_room(a.y, a.nelem * 4, "dequant", "the output")) return e;
     return launch(K_dequant, grid_cap(a.nelem), 1, 1, 256, 0, a);
 }
 
@@ -987,7 +1026,7 @@ std::vector<Op>& ops() {
 void register_ops() {
     auto& v = ops();
     if (!v.empty()) return;
-    for (const char* f : {"q2k", "q3k", "q4k", "q5k", "q6k", "q8", "f32"}) {
+    for (const char* f : {"q2k", "q3k", "q4k", "q5k", "q6k", "q8", "f32", "iq4nl"}) {
         const int fmt = fmt_of(f);
         std::string s(f);
         std::string n1 = "matmul_" + s + "_1", n4 = "matmul_" + s + "_4", nt = "matmul_" + s + "_t";
@@ -1007,7 +1046,7 @@ void register_ops() {
     v.push_back({"moe_topk", op_moe_topk});
     v.push_back({"moe_comb", op_moe_comb});
     v.push_back({"moe_group", op_moe_group});
-    for (const char* f : {"q4k", "q6k", "q8", "f32"}) {
+    for (const char* f : {"q2k", "q3k", "q4k", "q5k", "q6k", "q8", "f32", "iq4nl"}) {
         const int fmt = fmt_of(f);
         const std::string n = std::string("matmul_") + f + "_eg";
         v.push_back({n, [fmt, n](const Ctx& c) { return op_matmul_eg(c, fmt, n.c_str()); }});
@@ -1029,6 +1068,7 @@ void register_ops() {
     v.push_back({"repack_q2k", [](const Ctx& c) { return op_repack(c, K_repack_q2k, "repack_q2k"); }});
     v.push_back({"repack_q6k", [](const Ctx& c) { return op_repack(c, K_repack_q6k, "repack_q6k"); }});
     v.push_back({"repack_q8", [](const Ctx& c) { return op_repack(c, K_repack_q8, "repack_q8"); }});
+    v.push_back({"repack_iq4nl", [](const Ctx& c) { return op_repack(c, K_repack_iq4nl, "repack_iq4nl"); }});
     v.push_back({"fill_u32", op_fill});
     v.push_back({"dequant", op_dequant});
     v.push_back({"copy_f4", [](const Ctx& c) { return op_stream(c, K_copy_f4, "copy_f4"); }});

@@ -16,14 +16,16 @@ const { CargadorPesos } = require('./weights');
 const ROPE_NEOX = new Set(['qwen2', 'qwen3', 'qwen3moe', 'phi3', 'gemma', 'gemma2', 'gemma3', 'stablelm', 'olmo2']);
 const KQ = new Set(['q2k', 'q3k', 'q4k', 'q5k', 'q6k']);
 const MEZCLA = new Set(['q4k', 'q6k']);    // formats whose GEMV segments may share one launch
-const EG = new Set(['q4k', 'q6k', 'q8', 'f32']);   // formats with a grouped expert matmul (matmul_<fmt>_eg)
+const EG = new Set(['q2k', 'q3k', 'q4k', 'q5k', 'q6k', 'q8', 'f32', 'iq4nl']);   // grouped expert matmul (matmul_<fmt>_eg)
+// handles bound as two buffers (quants, scales): Q8_0 and IQ4_NL (held in the Q8_0 layout)
+function plano(W) { return W.tipo === 'q8' || W.tipo === 'iq4nl'; }
 // moe_group lists at most 65535 jobs (16-bit counts) of at most 256 experts: a batch whose jobs (tokens x
 // experts used) exceed that takes the ungrouped per-job expert path instead of failing.
 const MOE_GROUP_JOBS = 65535, MOE_GROUP_EXPERTS = 256;
 function agrupable(formatos, batch, nUsados, nExp) {
   return formatos && batch * nUsados <= MOE_GROUP_JOBS && nExp <= MOE_GROUP_EXPERTS;
 }
-const FMT_ID = { f32: 0, q8: 8, q2k: 10, q3k: 11, q4k: 12, q5k: 13, q6k: 14 };
+const FMT_ID = { f32: 0, q8: 8, q2k: 10, q3k: 11, q4k: 12, q5k: 13, q6k: 14, iq4nl: 8 };  // iq4nl: the Q8_0 layout
 // gemv segment modes (qp_args.h)
 const STORE = 0, ACC = 1, SWIGLU = 2, ARGMAX = 3;
 const AMAX_WG = 512;   // workgroups of the fused output GEMV = partial maxima for the device argmax
@@ -192,7 +194,7 @@ class ModeloTransformer {
   _mm(W, x, y, acc) {
     const gpu = this.gpu;
     const u = gpu.uniforme([['u', W.N], ['u', W.K], ['u', acc ? 1 : 0], ['u', 0]]);
-    const wb = W.tipo === 'q8' ? [W.qs, W.ds] : [W.w];
+    const wb = plano(W) ? [W.qs, W.ds] : [W.w];
     const b = [u, this.bPaso].concat(wb, [x, y]);
     return {
       uno: gpu.grupo('matmul_' + W.tipo + '_1', b), lote: gpu.grupo('matmul_' + W.tipo + '_4', b),
@@ -203,7 +205,7 @@ class ModeloTransformer {
   _mmE(W, x, y, tfijo) {
     const gpu = this.gpu;
     const u = gpu.uniforme([['u', W.N / this.nExp], ['u', W.K], ['u', 0], ['u', tfijo], ['u', this.nExp]]);
-    const wb = W.tipo === 'q8' ? [W.qs, W.ds] : [W.w];
+    const wb = plano(W) ? [W.qs, W.ds] : [W.w];
     // grouped by expert (the reference's matmul_<fmt>_eg: P{N, K, acc, tfijo}; [paso, w, x, y, lst, off])
     const ug = gpu.uniforme([['u', W.N / this.nExp], ['u', W.K], ['u', 0], ['u', tfijo]]);
     const gg = EG.has(W.tipo) ? gpu.grupo('matmul_' + W.tipo + '_eg', [ug, this.bPaso].concat(wb, [x, y, this.lst, this.off])) : null;
@@ -213,7 +215,7 @@ class ModeloTransformer {
   _embedGrupo(ids, y) {
     const gpu = this.gpu, E = this.emb;
     const u = gpu.uniforme([['u', this.D], ['u', E.N]]);
-    const wb = E.tipo === 'q8' ? [E.qs, E.ds] : [E.w];
+    const wb = plano(E) ? [E.qs, E.ds] : [E.w];
     return gpu.grupo('embed_' + E.tipo, [u, this.bPaso].concat(wb, [ids, y]));
   }
 
@@ -426,7 +428,7 @@ class ModeloTransformer {
         const K = this.nUsados, E = this.nExp;
         const eg = c.eg, eu = c.eu, ed = c.ed;
         if (eg.tipo === eu.tipo) {
-          const wb = eg.tipo === 'q8' ? [eg.qs, eg.ds] : [eg.w];
+          const wb = plano(eg) ? [eg.qs, eg.ds] : [eg.w];
           plan.push([gpu.grupo('matmul_' + eg.tipo + '_e_swiglu', [gpu.uniforme([['u', this.ffe], ['u', D], ['u', 0], ['u', K], ['u', E]]),
             P].concat(wb, [eu.w, this.xn, this.g, this.sel])), [1, 1, K]]);
         } else {

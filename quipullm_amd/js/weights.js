@@ -2,7 +2,7 @@
 // Loading of GGUF tensors into device buffers, from a local file or from the server's file URL by ranges.
 //
 // Same interface as quipullm's CargadorPesos (web/js/weights.js:15-139): existe(name), info(name),
-// f32(name) -> buffer, matriz(name) -> {tipo, N, K, w} ({tipo:'q8', N, K, qs, ds} for Q8_0).  The device
+// f32(name) -> buffer, matriz(name) -> {tipo, N, K, w} ({tipo:'q8' | 'iq4nl', N, K, qs, ds} for Q8_0, IQ4_NL).  The device
 // layout behind a handle is this backend's own: K-quant blocks and Q8_0 repacked on the device
 // into planar arrays (quants | scales) so every lane load is a 16-byte vector load.
 // Source: a path (read synchronously), or {url} (the reference engine's /engine/file/<id>, web/js/weights.js:51):
@@ -141,11 +141,20 @@ class CargadorPesos {
       this.buffers.push(w);
       return { tipo: 'q8', N: N, K: K, w: w, qs: w, ds: vista(w, N * K) };
     }
+    if (t.tipo === 20) {
+      // IQ4_NL (reference weights.js:110-116): repacked on the device into the Q8_0 layout (q = table[nibble],
+      // the same d), which every Q8_0 kernel reads; the ops are dispatched under the matmul_iq4nl_* names
+      if (K % 32) throw new Error(nombre + ': K=' + K + ' is not a multiple of 32');
+      const u8 = this.bytes(t);
+      const w = this._subirRepack(u8, 'repack_iq4nl', N * K / 32, K, nombre, N * K / 32 * 34);
+      this.buffers.push(w);
+      return { tipo: 'iq4nl', N: N, K: K, w: w, qs: w, ds: vista(w, N * K) };
+    }
     if (t.tipo === 0 || t.tipo === 1 || t.tipo === 30) {
       const w = this.f32(nombre);
       return { tipo: 'f32', N: N, K: K, w: w };
     }
-    throw new Error(nombre + ': quantization ' + t.tipo_nombre + ' not supported yet (supported: Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, F16, BF16, F32)');
+    throw new Error(nombre + ': quantization ' + t.tipo_nombre + ' not supported yet (supported: Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, IQ4_NL, F16, BF16, F32)');
   }
 }
 

@@ -31,8 +31,9 @@ from dataclasses import dataclass, field
 import numpy as np
 
 GGML_F32, GGML_Q8_0, GGML_Q2_K, GGML_Q3_K, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 0, 8, 10, 11, 12, 13, 14
+GGML_IQ4_NL = 20
 BLOCK = {GGML_F32: (1, 4), GGML_Q8_0: (32, 34), GGML_Q2_K: (256, 84), GGML_Q3_K: (256, 110), GGML_Q4_K: (256, 144),
-         GGML_Q5_K: (256, 176), GGML_Q6_K: (256, 210)}
+         GGML_Q5_K: (256, 176), GGML_Q6_K: (256, 210), GGML_IQ4_NL: (32, 18)}
 ALIGN = 32
 
 # GGUF metadata value types
@@ -118,6 +119,13 @@ CONFIGS = {
                                      _q4km(), qk_norm=True, ctx=512, centered=True),
     "mini_llama_q5km_c": ModelConfig("mini_llama_q5km_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
                                      _q5km(), ctx=512, centered=True),
+    # IQ4_NL matrices (the reference loads them for its DeepSeek2 class, weights.js:110-116): dense and MoE
+    "mini_llama_iq4nl_c": ModelConfig("mini_llama_iq4nl_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
+                                      {"default": GGML_IQ4_NL, "token_embd": GGML_F32}, ctx=512, centered=True),
+    "mini_qwen3moe_iq4nl_c": ModelConfig("mini_qwen3moe_iq4nl_c", "qwen3moe", 2, 512, 8, 2, 64, 0, 1000, 1e-6,
+                                         1000000.0, {"default": GGML_IQ4_NL, "token_embd": GGML_F32},
+                                         n_exp=16, n_used=4, ffe=256,
+                                         qk_norm=True, ctx=512, centered=True),
     "mini_llama_q3k_c": ModelConfig("mini_llama_q3k_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
                                     {"default": GGML_Q3_K, "attn_v": GGML_Q5_K, "output": GGML_Q6_K}, ctx=512,
                                     centered=True),
@@ -203,6 +211,13 @@ def gen_blocks(rng, gtype, nelem, kind="w", centered=False, wstd=0.0):
         return a.astype("<f4").tobytes()
     epb, bpb = BLOCK[gtype]
     nb = nelem // epb
+    if gtype == GGML_IQ4_NL:
+        # f16 scale |N(0, 0.02)| / 127 (the table spans -127 .. 113), random 4-bit indices
+        blk = np.empty((nb, 18), np.uint8)
+        d = (np.abs(rng.standard_normal(nb, dtype=np.float32) * np.float32(0.02)) / np.float32(127.0))
+        blk[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(nb, 2)
+        blk[:, 2:18] = np.frombuffer(rng.bytes(nb * 16), np.uint8).reshape(nb, 16)
+        return blk.tobytes()
     if gtype == GGML_Q8_0:
         blk = np.empty((nb, 34), np.uint8)
         d = (np.abs(rng.standard_normal(nb, dtype=np.float32) * np.float32(0.02)) / np.float32(127.0))

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import numpy as np
 
-F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 8, 10, 11, 12, 13, 14
+F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL = 0, 8, 10, 11, 12, 13, 14, 20
 
 
 # ------------------------------------------------------------------------------------------------ dequant
@@ -149,6 +149,19 @@ def dequant_q8_0(raw: np.ndarray) -> np.ndarray:
     return (b[:, 2:].view(np.int8).astype(np.float32) * d).reshape(-1)
 
 
+# ggml's kvalues_iq4nl (the table of the reference's conversion script tests/conformance/gen_ds.py:104)
+_IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
+
+
+def dequant_iq4_nl(raw: np.ndarray) -> np.ndarray:
+    """ggml dequantize_row_iq4_nl: per 18-byte block, y[j] = d * table[qs[j] & 15], y[j + 16] = d * table[qs[j] >> 4]."""
+    b = raw.reshape(-1, 18)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)
+    q = b[:, 2:18]
+    vals = np.concatenate([_IQ4NL[q & 15], _IQ4NL[q >> 4]], axis=1)
+    return (d * vals).astype(np.float32).reshape(-1)
+
+
 def dequant(fmt, raw):
     raw = np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray)) else np.asarray(raw, np.uint8)
     if fmt == Q4_K:
@@ -163,6 +176,8 @@ def dequant(fmt, raw):
         return dequant_q6k(raw)
     if fmt == Q8_0:
         return dequant_q8_0(raw)
+    if fmt == IQ4_NL:
+        return dequant_iq4_nl(raw)
     return raw.view(np.float32).copy()
 
 

@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 CLI = os.path.join(ROOT, "quipullm_amd", "js", "cli.js")
 
 MINI = ["mini_llama_q4km_c", "mini_llama_q5km_c", "mini_qwen3moe_q5k_c", "mini_llama_q3k_c", "mini_llama_q2k_c",
-        "mini_llama_q8_c", "mini_qwen3_q4km_c",
+        "mini_llama_q8_c", "mini_qwen3_q4km_c", "mini_llama_iq4nl_c", "mini_qwen3moe_iq4nl_c",
         "mini_qwen3moe_q4k_c", "mini_llama_q4km",
         "mini_qwen3moe_q4k"]
 
@@ -89,7 +89,8 @@ def read_kv_f16(path, n_layers, ctx, kvd, npos):
 
 @pytest.mark.parametrize("name", ["mini_llama_q4km_c", "mini_llama_q5km_c", "mini_llama_q3k_c", "mini_llama_q2k_c",
                                   "mini_llama_q8_c", "mini_qwen3_q4km_c",
-                                  "mini_qwen3moe_q4k_c", "mini_qwen3moe_q5k_c"])
+                                  "mini_qwen3moe_q4k_c", "mini_qwen3moe_q5k_c", "mini_llama_iq4nl_c",
+                                  "mini_qwen3moe_iq4nl_c"])
 def test_long_prefill_on_matrix_cores_matches_oracle(oracle, models_dir, tmp_path, name):
     """A 150-token prompt in one chunk runs the prefill matmuls on MFMA (bf16 hi/lo products); the logits of the
     prompt's last token and the greedy continuation must still match the oracle."""

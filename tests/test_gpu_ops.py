@@ -15,7 +15,8 @@ from quipullm_amd import capi, synth
 
 pytestmark = pytest.mark.gpu
 
-FMTS = [capi.Q2_K, capi.Q3_K, capi.Q4_K, capi.Q5_K, capi.Q6_K, capi.Q8_0, capi.F32]
+FMTS = [capi.Q2_K, capi.Q3_K, capi.Q4_K, capi.Q5_K, capi.Q6_K, capi.Q8_0, capi.F32, capi.IQ4_NL]
+PLANAR = (capi.Q8_0, capi.IQ4_NL)  # bound as two buffers: quants, then the f16 scales after them
 
 
 def raw_matrix(fmt, N, K, seed, centered=False):
@@ -76,7 +77,7 @@ def test_info(quipu):
 
 
 # ------------------------------------------------------------------------------------------------ dequant / embed
-@pytest.mark.parametrize("fmt", [capi.Q4_K, capi.Q6_K, capi.Q8_0])
+@pytest.mark.parametrize("fmt", [capi.Q4_K, capi.Q6_K, capi.Q8_0, capi.IQ4_NL])
 @pytest.mark.parametrize("centered", [False, True])
 def test_dequant_bit_exact(quipu, dev, oracle, fmt, centered):
     N, K = 96, 1024
@@ -96,7 +97,7 @@ def test_embed_rows_bit_exact(quipu, dev, oracle, fmt):
     T = len(ids)
     y = dev.zeros(T * D * 4)
     nm = "embed_" + capi.FMT_NAME[fmt]
-    wb = [w, w + V * D] if fmt == capi.Q8_0 else [w]
+    wb = [w, w + V * D] if fmt in PLANAR else [w]
     quipu.dispatch(nm, [("u", D), ("u", V)], [dev.paso(T, 0)] + wb + [dev.buf(ids), y], ((T * D + 255) // 256,))
     got = dev.get(y, (T, D))
     np.testing.assert_array_equal(got.view(np.uint32), oracle.embed(fmt, raw, D, ids).view(np.uint32))
@@ -104,7 +105,8 @@ def test_embed_rows_bit_exact(quipu, dev, oracle, fmt):
 
 # ------------------------------------------------------------------------------------------------ GEMV
 @pytest.mark.parametrize("fmt,N,K", [(capi.Q4_K, 1000, 4096), (capi.Q6_K, 513, 2048), (capi.Q8_0, 700, 1536),
-                                     (capi.F32, 130, 1024), (capi.Q4_K, 64, 14336), (capi.Q6_K, 40, 14336),
+                                     (capi.IQ4_NL, 700, 1536), (capi.F32, 130, 1024), (capi.Q4_K, 64, 14336),
+                                     (capi.Q6_K, 40, 14336),
                                      (capi.Q6_K, 700, 9216), (capi.Q4_K, 4100, 15360)])
 def test_matmul_1_reference_op(quipu, dev, oracle, fmt, N, K):
     raw = raw_matrix(fmt, N, K, 13)
@@ -112,7 +114,7 @@ def test_matmul_1_reference_op(quipu, dev, oracle, fmt, N, K):
     x = np.random.default_rng(1).standard_normal(K).astype(np.float32)
     y0 = np.random.default_rng(2).standard_normal(N).astype(np.float32)
     W = oracle.dequant(fmt, raw, N * K).reshape(N, K) if fmt != capi.F32 else raw.view(np.float32).reshape(N, K)
-    wb = [w, w + N * K] if fmt == capi.Q8_0 else [w]
+    wb = [w, w + N * K] if fmt in PLANAR else [w]
     for acc in (0, 1):
         y = dev.buf(y0)
         quipu.dispatch("matmul_%s_1" % capi.FMT_NAME[fmt], [("u", N), ("u", K), ("u", acc), ("u", 0)],
@@ -254,7 +256,7 @@ def test_matmul_multi_token(quipu, dev, oracle, fmt, T, op):
     y0 = np.random.default_rng(10).standard_normal((T, N)).astype(np.float32)
     y = dev.buf(y0)
     wb = [dev.matrix(fmt, raw, N, K)]
-    if fmt == capi.Q8_0:
+    if fmt in PLANAR:
         wb.append(wb[0] + N * K)
     grid = ((N + 63) // 64, 1, (T + 31) // 32) if op == "t" else capi.dim2((N + 7) // 8) + ((T + 3) // 4,)
     quipu.dispatch("matmul_%s_%s" % (capi.FMT_NAME[fmt], op), [("u", N), ("u", K), ("u", 1), ("u", 0)],
@@ -274,7 +276,7 @@ def test_matmul_prefill_mfma(quipu, dev, oracle, fmt, T, N, K, acc):
     partial token and row tiles, and tile counts that are not a multiple of the 8 XCDs (3 x 4 = 12 tiles).  For
     K-quants the input is split into bf16 planes once and small tile grids split K (K = 5632: 15 splits, the last
     one partial), partials summed in order; from T = 256 on they take the 256-token tiles."""
-    if fmt == capi.Q8_0 and K % 64:
+    if fmt in PLANAR and K % 64:
         K += 32
     raw = raw_matrix(fmt, N, K, 61)
     W = (oracle.dequant(fmt, raw, N * K) if fmt != capi.F32 else raw.view(np.float32)).reshape(N, K)
@@ -282,7 +284,7 @@ def test_matmul_prefill_mfma(quipu, dev, oracle, fmt, T, N, K, acc):
     y0 = np.random.default_rng(13).standard_normal((T, N)).astype(np.float32)
     y = dev.buf(y0)
     wb = [dev.matrix(fmt, raw, N, K)]
-    if fmt == capi.Q8_0:
+    if fmt in PLANAR:
         wb.append(wb[0] + N * K)
     quipu.dispatch("matmul_%s_t" % capi.FMT_NAME[fmt], [("u", N), ("u", K), ("u", acc), ("u", 0)],
                    [dev.paso(T, 0)] + wb + [dev.buf(x), y], ((N + 63) // 64, 1, (T + 31) // 32))
@@ -319,7 +321,8 @@ def test_matmul_q4k_prefill_row_magnitudes(quipu, dev, oracle, T, N, K):
     assert np.all(np.abs(got - want) <= bound)
 
 
-@pytest.mark.parametrize("fmt,K", [(capi.Q8_0, 288), (capi.Q8_0, 544), (capi.F32, 80), (capi.F32, 272),
+@pytest.mark.parametrize("fmt,K", [(capi.Q8_0, 288), (capi.Q8_0, 544), (capi.IQ4_NL, 288), (capi.F32, 80),
+                                   (capi.F32, 272),
                                    (capi.F32, 528)])
 @pytest.mark.parametrize("T,N", [(64, 77), (130, 300)])
 def test_matmul_prefill_mfma_ragged_k(quipu, dev, oracle, fmt, T, N, K):
@@ -330,7 +333,7 @@ def test_matmul_prefill_mfma_ragged_k(quipu, dev, oracle, fmt, T, N, K):
     raw = raw_matrix(fmt, N, K, 77)
     W = (oracle.dequant(fmt, raw, N * K) if fmt != capi.F32 else raw.view(np.float32)).reshape(N, K)
     wb = [dev.matrix(fmt, raw, N, K)]
-    if fmt == capi.Q8_0:
+    if fmt in PLANAR:
         wb.append(wb[0] + N * K)
     name = "matmul_%s_t" % capi.FMT_NAME[fmt]
     uni = [("u", N), ("u", K), ("u", 0), ("u", 0)]
@@ -372,7 +375,8 @@ def test_moe_group(quipu, dev, E, k, T):
     assert dev.get(lb, (T * k,), np.uint32)[:int(off[E])].tolist() == lst_want.tolist()
 
 
-@pytest.mark.parametrize("fmt", [capi.Q4_K, capi.Q6_K, capi.Q8_0, capi.F32])
+@pytest.mark.parametrize("fmt", [capi.Q4_K, capi.Q6_K, capi.Q5_K, capi.Q3_K, capi.Q2_K, capi.Q8_0, capi.F32,
+                                 capi.IQ4_NL])
 @pytest.mark.parametrize("tfijo,acc", [(4, 0), (1, 1)])
 def test_matmul_grouped_by_expert(quipu, dev, oracle, fmt, tfijo, acc):
     """matmul_<fmt>_eg (kquants.js:386-460): the expert matmul over the job lists of moe_group, on the matrix cores.
@@ -393,7 +397,7 @@ def test_matmul_grouped_by_expert(quipu, dev, oracle, fmt, tfijo, acc):
     sb, lb, ob = dev.buf(sel), dev.zeros(4 * njob), dev.zeros(4 * (E + 1))
     quipu.dispatch("moe_group", [("u", E), ("u", k)], [dev.paso(T, 0), sb, lb, ob])
     hw = dev.matrix(fmt, raw, E * N, K)
-    wb = [hw, hw + E * N * K] if fmt == capi.Q8_0 else [hw]
+    wb = [hw, hw + E * N * K] if fmt in PLANAR else [hw]
     yb = dev.buf(y0)
     u = [("u", N), ("u", K), ("u", acc), ("u", tfijo)]
     quipu.dispatch("matmul_%s_eg" % capi.FMT_NAME[fmt], u, [dev.paso(T, 0)] + wb + [dev.buf(x), yb, lb, ob],
@@ -421,7 +425,7 @@ def test_matmul_expert_jobs(quipu, dev, oracle, fmt):
     hg, hu = dev.matrix(fmt, rg, E * N, K), dev.matrix(fmt, ru, E * N, K)
     y = dev.zeros(T * k * N * 4)
     u = [("u", N), ("u", K), ("u", 0), ("u", k), ("u", E)]
-    wb = [hg, hg + E * N * K] if fmt == capi.Q8_0 else [hg]
+    wb = [hg, hg + E * N * K] if fmt in PLANAR else [hg]
     xb, sb, pb = dev.buf(x), dev.buf(sel), dev.paso(T, 0)
     quipu.dispatch("matmul_%s_e" % capi.FMT_NAME[fmt], u, [pb] + wb + [xb, y, sb], (1, 1, T * k))
     got = dev.get(y, (T * k, N))
@@ -930,6 +934,13 @@ def test_graph_replay_matches_eager(quipu, dev, oracle):
 
 
 # ------------------------------------------------------------------------------------------------ errors
+def raw_fmt_word(u, fmt):
+    """A gemv uniform with its format word replaced by fmt as given (no mapping to a device layout)."""
+    u = list(u)
+    u[6] = ("u", fmt)
+    return u
+
+
 def test_host_checks_reject_bad_dispatches(quipu, dev):
     """Shapes and bindings the kernels cannot take are refused on the host, before any launch."""
     x = dev.zeros(4096 * 4)
@@ -951,6 +962,14 @@ def test_host_checks_reject_bad_dispatches(quipu, dev):
                       ("u", 0), ("u", 0), ("u", 8)], [p, x, x, x, y, y, 0, 0, y, y]),
         ("moe_topk", [("u", 2000), ("u", 8), ("u", 1), ("f", 1)], [p, x, y, y]),
         ("matmul_q8_1", [("u", 16), ("u", 256), ("u", 0), ("u", 0)], [p, w, w + 8, x, y]),
+        # a format word that is not a device layout (the GGUF type of IQ4_NL), and weights smaller than their
+        # format and rows need (16 f32 rows of 256 in 2304 bytes; 32 Q4_K rows)
+        ("gemv", raw_fmt_word(capi.gemv_uniform(1, 256, segs=[(capi.STORE, 16, 0, 16)]), capi.IQ4_NL),
+         [p, x, 0, 0, w, 0, y]),
+        ("gemv", capi.gemv_uniform(1, 256, fmt=capi.F32, R=1, segs=[(capi.STORE, 16, 0, 16)]), [p, x, 0, 0, w, 0, y]),
+        ("gemv", capi.gemv_uniform(1, 256, segs=[(capi.STORE, 16, 0, 32)]), [p, x, 0, 0, w, 0, y]),
+        ("dequant", [("u", capi.IQ4_NL), ("u", 512), ("u", 0), ("u", 256)], [0, w, y]),
+        ("dequant", [("u", capi.Q4_K), ("u", 32 * 256), ("u", 0), ("u", 256)], [0, w, y]),
     ]
     for name, u, b in bad:
         with pytest.raises(capi.QuipuError):

@@ -48,20 +48,20 @@ def test_header_declares_the_facade():
 
 
 # every op name the JavaScript host dispatches (transformer.js, weights.js) and the tests use
-FORMATS = ("q2k", "q3k", "q4k", "q5k", "q6k", "q8", "f32")
+FORMATS = ("q2k", "q3k", "q4k", "q5k", "q6k", "q8", "f32", "iq4nl")
 OPS = ["matmul_%s_%s" % (f, s) for f in FORMATS for s in ("1", "4", "t", "e", "e_swiglu")] + \
       ["embed_%s" % f for f in FORMATS] + \
       ["rmsnorm", "norm_rope", "kv_write", "atencion", "swiglu", "moe_topk", "moe_comb", "gemv", "dec_attn",
-       "dec_attn_comb", "argmax", "argmax_fin", "repack_q2k", "repack_q3k", "repack_q4k", "repack_q5k", "repack_q6k", "repack_q8", "fill_u32", "dequant",
+       "dec_attn_comb", "argmax", "argmax_fin", "repack_q2k", "repack_q3k", "repack_q4k", "repack_q5k", "repack_q6k", "repack_q8", "repack_iq4nl", "fill_u32", "dequant",
        "copy_f4", "read_f4", "moe_gate_up_q4k", "moe_gate_up_q6k", "moe_down_q4k", "moe_down_q6k", "penalizar",
-       "topk_cand", "moe_group"] + ["matmul_%s_eg" % f for f in ("q4k", "q6k", "q8", "f32")]
+       "topk_cand", "moe_group"] + ["matmul_%s_eg" % f for f in FORMATS]
 
 
 def test_op_table(built):
     lib = capi.load_library()
     ids = [lib.qp_op_id(n.encode()) for n in OPS]
     assert min(ids) >= 0 and len(set(ids)) == len(ids)
-    assert lib.qp_op_id(b"matmul_iq4nl_1") == -1 and lib.qp_op_id(b"") == -1 and lib.qp_op_id(None) == -1
+    assert lib.qp_op_id(b"matmul_iq2xs_1") == -1 and lib.qp_op_id(b"") == -1 and lib.qp_op_id(None) == -1
 
 
 def test_ops_used_by_the_js_host_exist(built):

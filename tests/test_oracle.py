@@ -41,7 +41,8 @@ def test_f16_rounding_matches_numpy(oracle):
 
 
 @pytest.mark.parametrize("fmt,n", [(refs.Q2_K, 256 * 300), (refs.Q3_K, 256 * 300), (refs.Q4_K, 256 * 300),
-                                   (refs.Q5_K, 256 * 300), (refs.Q6_K, 256 * 300), (refs.Q8_0, 32 * 500)])
+                                   (refs.Q5_K, 256 * 300), (refs.Q6_K, 256 * 300), (refs.Q8_0, 32 * 500),
+                                   (refs.IQ4_NL, 32 * 500)])
 @pytest.mark.parametrize("centered", [False, True])
 def test_dequant_bit_exact_vs_ggml_spec(oracle, fmt, n, centered):
     raw = blocks(fmt, n, 1, centered)
@@ -150,10 +151,20 @@ def test_q8_known_answer(oracle):
     np.testing.assert_array_equal(oracle.dequant(refs.Q8_0, b, 32), np.arange(-16, 16) * 0.25)
 
 
+def test_iq4nl_known_answer(oracle):
+    # d = 0.5; byte l holds index l (weight l) and 15 - l (weight 16 + l): the table in order, then reversed
+    table = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+    b = np.zeros(18, np.uint8)
+    b[0:2] = np.array([0.5], np.float16).view(np.uint8)
+    b[2:] = np.arange(16, dtype=np.uint8) | ((15 - np.arange(16, dtype=np.uint8)) << 4)
+    want = np.array(table + table[::-1], np.float32) * 0.5
+    np.testing.assert_array_equal(oracle.dequant(refs.IQ4_NL, b, 32), want)
+
+
 # ------------------------------------------------------------------------------------------------ matmul
 @pytest.mark.parametrize("fmt,N,K", [(refs.Q2_K, 13, 512), (refs.Q3_K, 15, 768), (refs.Q4_K, 33, 512),
                                      (refs.Q5_K, 21, 512), (refs.Q6_K, 17, 768),
-                                     (refs.Q8_0, 19, 320), (refs.F32, 9, 96)])
+                                     (refs.Q8_0, 19, 320), (refs.IQ4_NL, 19, 1088), (refs.F32, 9, 96)])
 @pytest.mark.parametrize("T,mode", [(1, 0), (3, 0), (9, 1)])
 def test_matmul_vs_float64(oracle, fmt, N, K, T, mode):
     rng = np.random.default_rng(5)
@@ -334,7 +345,8 @@ def test_argmax_ties_nan(oracle):
 @pytest.mark.parametrize("name,neox", [("mini_llama_q4km_c", 0), ("mini_llama_q5km_c", 0), ("mini_llama_q3k_c", 0),
                                        ("mini_llama_q2k_c", 0), ("mini_qwen3_q4km_c", 1),
                                        ("mini_qwen3moe_q5k_c", 1), ("mini_qwen3moe_q4k_c", 1),
-                                       ("mini_llama_q8_c", 0)])
+                                       ("mini_llama_q8_c", 0), ("mini_llama_iq4nl_c", 0),
+                                       ("mini_qwen3moe_iq4nl_c", 1)])
 def test_model_forward_vs_float64(oracle, models_dir, name, neox):
     # float32 rounding, amplified by near-ties of the large activations of the centered models, stays below these
     # bounds; a semantic slip (RoPE pairing, norm placement, GQA head map, missing residual) is O(0.1)
