@@ -54,6 +54,9 @@ def lib():
         L.or_kv_write.argtypes = [vp, vp, vp, vp, i, i, i, i]
         L.or_attention.argtypes = [vp, vp, vp, vp, i, i, i, i, i, f, i, i]
         L.or_swiglu.argtypes = [vp, vp, C.c_int64]
+        L.or_geglu.argtypes = [vp, vp, C.c_int64]
+        L.or_escalar.argtypes = [vp, C.c_int64, f]
+        L.or_suma_esc.argtypes = [vp, vp, C.c_int64, f]
         L.or_moe_topk.argtypes = [vp, i, i, i, i, f, vp, vp]
         L.or_moe_comb.argtypes = [vp, vp, vp, i, i, i]
         L.or_argmax.restype = i
@@ -162,6 +165,24 @@ def swiglu(g, u):
     return g
 
 
+def geglu(g, u):
+    g = _f32(g).copy()
+    lib().or_geglu(_p(g), _p(_f32(u)), g.size)
+    return g
+
+
+def escalar(x, s):
+    x = _f32(x).copy()
+    lib().or_escalar(_p(x), x.size, s)
+    return x
+
+
+def suma_esc(x, t, s):
+    x = _f32(x).copy()
+    lib().or_suma_esc(_p(x), _p(_f32(t)), x.size, s)
+    return x
+
+
 def moe_topk(lg, E, k, norm, scale):
     lg = _f32(lg)
     T = lg.size // E
@@ -264,7 +285,9 @@ class _Layer(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("attn_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm", "ffn_norm",
                                           "gate", "up", "down", "router", "gate_e", "up_e", "down_e")] + \
                [(n, C.c_int) for n in ("fq", "fk", "fv", "fo", "fgate", "fup", "fdown", "frouter", "fgate_e",
-                                       "fup_e", "fdown_e")]
+                                       "fup_e", "fdown_e")] + \
+               [("post_att", C.c_void_p), ("post_ffn", C.c_void_p), ("swa", C.c_int), ("rbase", C.c_float),
+                ("resc", C.c_float)]
 
 
 class _Model(C.Structure):
@@ -274,7 +297,8 @@ class _Model(C.Structure):
                [("tok_embd", C.c_void_p), ("output", C.c_void_p), ("output_norm", C.c_void_p),
                 ("f_embd", C.c_int), ("f_output", C.c_int), ("layers", C.POINTER(_Layer)), ("pos", C.c_int),
                 ("kc", C.c_void_p), ("vc", C.c_void_p), ("kv_f16", C.c_int), ("kref", C.c_void_p),
-                ("vref", C.c_void_p), ("nref", C.c_int)]
+                ("vref", C.c_void_p), ("nref", C.c_int)] + \
+               [(n, C.c_float) for n in ("emb_scale", "res_scale", "logit_scale", "softcap")] + [("geglu", C.c_int)]
 
 
 ROPE_NEOX = {"qwen2", "qwen3", "qwen3moe", "phi3", "gemma", "gemma2", "gemma3", "stablelm", "olmo2"}
@@ -310,7 +334,28 @@ class Model:
         m.vocab, m.nrot, m.neox, m.ctx, m.tiled = self.vocab, self.nrot, int(self.neox), self.ctx, int(tiled)
         m.eps, m.base = self.eps, self.base
         m.kv_f16 = int(kv_f16)
-        m.escala = float(np.float32(1.0 / np.sqrt(self.hd)))
+        # scales (transformer.js:35-45): 0 = not set; the attention scale defaults to 1/sqrt(hd)
+        m.escala = float(np.float32(get("attention.scale", 0) or 1.0 / np.sqrt(self.hd)))
+        m.emb_scale = get("embedding_scale", 0) or 0
+        m.res_scale = get("residual_scale", 0) or 0
+        m.logit_scale = get("logit_scale", 0) or 0
+        m.softcap = get("final_logit_softcapping", 0) or 0
+        # gemma3 (transformer.js:46-54): windowed layers (pattern: the last of every `patron` layers is global),
+        # their RoPE base, the global layers' linear RoPE scaling, sqrt(D) embedding scale, GeGLU
+        self.gemma = a == "gemma3"
+        ventana = patron = 0
+        base_swa, esc_global = 10000.0, 1.0
+        if self.gemma:
+            ventana = get("attention.sliding_window", 0) or 0
+            patron = get("attention.sliding_window_pattern", 6) or 6
+            base_swa = get("rope.freq_base_swa", 10000.0)
+            fac = get("rope.scaling.factor", 1.0)
+            esc_global = 1.0 / fac if get("rope.scaling.type", "") == "linear" and fac > 0 else 1.0
+            m.emb_scale = float(np.float32(np.sqrt(self.D)))
+            m.escala = float(np.float32(1.0 / np.sqrt(self.D / self.nh) if self.n_layers == 62 else
+                                        1.0 / np.sqrt(self.hd)))
+            m.geglu = 1
+        self.swa = [ventana if ventana > 0 and (i % patron) < patron - 1 else 0 for i in range(self.n_layers)]
         m.n_exp = self.n_exp
         m.n_used = get("expert_used_count", 0)
         m.ffe = get("expert_feed_forward_length", 0)
@@ -342,6 +387,10 @@ class Model:
                 setattr(ly, field, t[n]["tipo"] if n in t else 0)
             if self.n_exp == 0 and m.F == 0:
                 m.F = t[p + "ffn_gate.weight"]["dims"][1]
+            ly.post_att, ly.post_ffn = ptr(p + "post_attention_norm.weight"), ptr(p + "post_ffw_norm.weight")
+            ly.swa = self.swa[i]
+            ly.rbase = base_swa if self.gemma and self.swa[i] else self.base
+            ly.resc = esc_global if self.gemma and not self.swa[i] else 1.0
         if L.or_model_alloc_kv(self.ptr) != 0:
             raise MemoryError("oracle KV cache")
         self.batch = 32

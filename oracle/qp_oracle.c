@@ -832,6 +832,25 @@ void or_swiglu(float* g, const float* u, int64_t n) {
     }
 }
 
+/* GeGLU, tanh form (gpu.js:318-330), in the WGSL expression's order with one rounding per operation. */
+void or_geglu(float* g, const float* u, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        float a = g[i];
+        float c = ((0.044715f * a) * a) * a;
+        float z = 0.79788456f * (a + c);
+        z = fminf(fmaxf(z, -20.0f), 20.0f);
+        g[i] = ((0.5f * a) * (1.0f + tanhf(z))) * u[i];
+    }
+}
+
+/* escalar (gpu.js:635-646): x = x * s; suma_esc (gpu.js:648-660): x = x + s * t. */
+void or_escalar(float* x, int64_t n, float s) {
+    for (int64_t i = 0; i < n; i++) x[i] = x[i] * s;
+}
+void or_suma_esc(float* x, const float* t, int64_t n, float s) {
+    for (int64_t i = 0; i < n; i++) x[i] = x[i] + s * t[i];
+}
+
 /* ------------------------------------------------------------------ MoE routing (kds.js:191-221)
  * softmax over E logits; k rounds of strict max (ties -> lower index); weights = probs * f with
  * f = scale / max(sum, 2^-14) when norm, else scale. */
@@ -888,6 +907,11 @@ typedef struct {
     const uint8_t *gate, *up, *down;             /* dense FFN */
     const uint8_t *router, *gate_e, *up_e, *down_e; /* MoE FFN */
     int fq, fk, fv, fo, fgate, fup, fdown, frouter, fgate_e, fup_e, fdown_e;
+    /* gemma3 (transformer.js:46-54, 106-111, 206-207, 218-231): normalized outputs before the residual add,
+     * a sliding window of swa keys (0: none), the layer's RoPE base and angle scale (0: the model's, 1) */
+    const uint8_t *post_att, *post_ffn;
+    int swa;
+    float rbase, resc;
 } OrLayer;
 
 typedef struct {
@@ -906,6 +930,9 @@ typedef struct {
      * ([L][nref][kvd] f16, the GPU's own cache) instead of this restatement's rounding of its own k and v */
     const uint16_t *kref, *vref;
     int nref;
+    /* scales (transformer.js:35-45; 0: none) and the GeGLU FFN of gemma3 */
+    float emb_scale, res_scale, logit_scale, softcap;
+    int geglu;
 } OrModel;
 
 OrModel* or_model_new(void) { return (OrModel*)calloc(1, sizeof(OrModel)); }
@@ -950,6 +977,8 @@ int or_model_forward(OrModel* m, const uint32_t* ids, int T, float* logits) {
     float* att = (float*)calloc((size_t)T * qd, 4);
     float* g = (float*)calloc((size_t)T * F, 4);
     float* u = (float*)calloc((size_t)T * F, 4);
+    float* tmp = (float*)calloc((size_t)T * D, 4);
+    const float resid = m->res_scale ? m->res_scale : 1.0f;
     float* rl = NULL; float* de = NULL; float* wts = NULL; uint32_t* sel = NULL;
     if (m->n_exp) {
         rl = (float*)calloc((size_t)T * m->n_exp, 4);
@@ -958,18 +987,20 @@ int or_model_forward(OrModel* m, const uint32_t* ids, int T, float* logits) {
         sel = (uint32_t*)calloc((size_t)T * m->n_used, 4);
     }
     or_embed(m->f_embd, m->tok_embd, D, ids, T, x);
+    if (m->emb_scale) or_escalar(x, (int64_t)T * D, m->emb_scale);
     for (int li = 0; li < m->n_layers; li++) {
         const OrLayer* L = &m->layers[li];
+        const float rbase = L->rbase ? L->rbase : m->base, resc = L->resc ? L->resc : 1.0f;
         float* kc = m->kc + (size_t)li * m->ctx * kvd;
         float* vc = m->vc + (size_t)li * m->ctx * kvd;
         or_rmsnorm(x, (const float*)L->attn_norm, xn, T, D, m->eps, 0);
         mm(m, L->fq, L->wq, qd, D, xn, T, q, 0);
         mm(m, L->fk, L->wk, kvd, D, xn, T, k, 0);
         mm(m, L->fv, L->wv, kvd, D, xn, T, v, 0);
-        or_norm_rope(q, (const float*)L->q_norm, T, nh, hd, L->q_norm != NULL, m->neox, m->eps, m->base, m->nrot,
-                     1.0f, m->pos);
-        or_norm_rope(k, (const float*)L->k_norm, T, nkv, hd, L->k_norm != NULL, m->neox, m->eps, m->base, m->nrot,
-                     1.0f, m->pos);
+        or_norm_rope(q, (const float*)L->q_norm, T, nh, hd, L->q_norm != NULL, m->neox, m->eps, rbase, m->nrot,
+                     resc, m->pos);
+        or_norm_rope(k, (const float*)L->k_norm, T, nkv, hd, L->k_norm != NULL, m->neox, m->eps, rbase, m->nrot,
+                     resc, m->pos);
         or_kv_write(k, v, kc, vc, T, kvd, m->pos, 0);
         if (m->kv_f16)
             for (size_t i = (size_t)m->pos * kvd; i < (size_t)(m->pos + T) * kvd; i++) {
@@ -983,14 +1014,28 @@ int or_model_forward(OrModel* m, const uint32_t* ids, int T, float* logits) {
                     vc[i] = f16_round(vc[i]);
                 }
             }
-        or_attention(q, kc, vc, att, T, m->pos, nh, nkv, hd, m->escala, 0, 0);
-        mm(m, L->fo, L->wo, D, qd, att, T, x, 1);
+        /* a window over the whole cache: the same keys as the reference's ring of swa + batch slots */
+        or_attention(q, kc, vc, att, T, m->pos, nh, nkv, hd, m->escala, L->swa, 0);
+        if (L->post_att || m->res_scale) { /* transformer.js:218-231: into tmp, normalized, x += resid * it */
+            mm(m, L->fo, L->wo, D, qd, att, T, tmp, 0);
+            if (L->post_att) or_rmsnorm(tmp, (const float*)L->post_att, xn, T, D, m->eps, 0);
+            or_suma_esc(x, L->post_att ? xn : tmp, (int64_t)T * D, resid);
+        } else {
+            mm(m, L->fo, L->wo, D, qd, att, T, x, 1);
+        }
         or_rmsnorm(x, (const float*)L->ffn_norm, xn, T, D, m->eps, 0);
         if (!m->n_exp) {
             mm(m, L->fgate, L->gate, m->F, D, xn, T, g, 0);
             mm(m, L->fup, L->up, m->F, D, xn, T, u, 0);
-            or_swiglu(g, u, (int64_t)T * m->F);
-            mm(m, L->fdown, L->down, D, m->F, g, T, x, 1);
+            if (m->geglu) or_geglu(g, u, (int64_t)T * m->F);
+            else or_swiglu(g, u, (int64_t)T * m->F);
+            if (L->post_ffn || m->res_scale) {
+                mm(m, L->fdown, L->down, D, m->F, g, T, tmp, 0);
+                if (L->post_ffn) or_rmsnorm(tmp, (const float*)L->post_ffn, xn, T, D, m->eps, 0);
+                or_suma_esc(x, L->post_ffn ? xn : tmp, (int64_t)T * D, resid);
+            } else {
+                mm(m, L->fdown, L->down, D, m->F, g, T, x, 1);
+            }
         } else {
             int E = m->n_exp, K = m->n_used, ffe = m->ffe;
             int grp = T >= 8 && m->tiled; /* deepseek2.js:373, 377 */
@@ -1008,9 +1053,18 @@ int or_model_forward(OrModel* m, const uint32_t* ids, int T, float* logits) {
         or_rmsnorm(x, (const float*)m->output_norm, xl, T, D, m->eps, 1);
         or_matmul(m->f_output, m->output, m->vocab, D, xl, 1, logits, 0, 0);
         free(xl);
+        /* on the host in double, stored to float (transformer.js:333-334) */
+        if (m->logit_scale) {
+            const double kk = 1.0 / (double)m->logit_scale;
+            for (int i = 0; i < m->vocab; i++) logits[i] = (float)((double)logits[i] * kk);
+        }
+        if (m->softcap) {
+            const double c = (double)m->softcap;
+            for (int i = 0; i < m->vocab; i++) logits[i] = (float)(c * tanh((double)logits[i] / c));
+        }
     }
     m->pos += T;
-    free(x); free(xn); free(q); free(k); free(v); free(att); free(g); free(u);
+    free(x); free(xn); free(q); free(k); free(v); free(att); free(g); free(u); free(tmp);
     free(rl); free(de); free(wts); free(sel);
     return 0;
 }

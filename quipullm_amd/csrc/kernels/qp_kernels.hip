@@ -2200,6 +2200,32 @@ KERNEL __launch_bounds__(256) void qp_kv_write(QpKvArgs a) {
 
 // ====================================================================================== SwiGLU
 // Reference swiglu (gpu.js:570-582): g = g / (1 + exp(-g)) * u over T*F.
+// GeGLU, the tanh form (reference geglu, gpu.js:318-330): g = 0.5 a (1 + tanh(z)) u with
+// z = clamp(0.79788456 (a + 0.044715 a^3), -20, 20), evaluated in the reference's order, one rounding per operation.
+KERNEL __launch_bounds__(256) void qp_geglu(QpSwigluArgs a) {
+#pragma clang fp contract(off)
+    const uint64_t n = (uint64_t)paso_T(a.paso) * a.f;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull) {
+        const float g = cptr<float>(a.g)[i];
+        const float c = ((0.044715f * g) * g) * g;
+        const float z = fminf(fmaxf(0.79788456f * (g + c), -20.0f), 20.0f);
+        mptr<float>(a.g)[i] = ((0.5f * g) * (1.0f + tanhf(z))) * cptr<float>(a.u)[i];
+    }
+}
+
+// escalar (gpu.js:635-646): x = x * s over T rows of d; suma_esc (gpu.js:648-660): x = x + s * t.
+KERNEL __launch_bounds__(256) void qp_escalar(QpScaleArgs a) {
+    const uint64_t n = (uint64_t)paso_T(a.paso) * a.d;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull)
+        mptr<float>(a.x)[i] = cptr<float>(a.x)[i] * a.s;
+}
+KERNEL __launch_bounds__(256) void qp_suma_esc(QpScaleArgs a) {
+#pragma clang fp contract(off)
+    const uint64_t n = (uint64_t)paso_T(a.paso) * a.d;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull)
+        mptr<float>(a.x)[i] = cptr<float>(a.x)[i] + a.s * cptr<float>(a.t)[i];
+}
+
 KERNEL __launch_bounds__(256) void qp_swiglu(QpSwigluArgs a) {
     const uint64_t n = (uint64_t)paso_T(a.paso) * a.f;
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull) {

@@ -128,6 +128,7 @@ typedef struct {
 // rows: slots of the cache (writes at or past it are dropped, never out of bounds)
 typedef struct { uint64_t k, v, kc, vc, paso; uint32_t kvd, cap, f16, rows; } QpKvArgs;
 typedef struct { uint64_t g, u, paso; uint32_t f, pad; } QpSwigluArgs;
+typedef struct { uint64_t x, t, paso; uint32_t d; float s; } QpScaleArgs;  // escalar (t unused), suma_esc
 typedef struct { uint64_t lg, sel, wts, paso; uint32_t e, k, norm; float scale; } QpTopkArgs;
 typedef struct { uint64_t x, de, wts, paso; uint32_t d, k, pad0, pad1; } QpCombArgs;
 

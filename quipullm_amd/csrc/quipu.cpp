@@ -587,6 +587,30 @@ int op_swiglu(const Ctx& c) {
     return launch(K_swiglu, c.gx ? (c.gx > 4096 ? 4096 : c.gx) : 1, 1, 1, 256, 0, a);
 }
 
+// geglu (gpu.js:318-330): P{F}; [paso, g, u].
+int op_geglu(const Ctx& c) {
+    if (int e = need_bufs(c, 3, "geglu")) return e;
+    QpSwigluArgs a = {};
+    a.f = c.U(0);
+    a.paso = c.B(0);
+    a.g = c.B(1);
+    a.u = c.B(2);
+    return launch(K_geglu, c.gx ? (c.gx > 4096 ? 4096 : c.gx) : 1, 1, 1, 256, 0, a);
+}
+
+// escalar (gpu.js:635-646): P{D, escala}; [paso, x].  suma_esc (gpu.js:648-660): P{D, escala}; [paso, x, t].
+int op_scale(const Ctx& c, bool suma) {
+    const char* name = suma ? "suma_esc" : "escalar";
+    if (int e = need_bufs(c, suma ? 3 : 2, name)) return e;
+    QpScaleArgs a = {};
+    a.d = c.U(0);
+    a.s = c.F(1);
+    a.paso = c.B(0);
+    a.x = c.B(1);
+    a.t = suma ? c.B(2) : 0;
+    return launch(suma ? K_suma_esc : K_escalar, c.gx ? (c.gx > 4096 ? 4096 : c.gx) : 1, 1, 1, 256, 0, a);
+}
+
 // moe_topk (kds.js:191-221): P{E, k, norm, escala}; [paso, lg, sel, wts]; ceil(T/64) groups.
 int op_moe_topk(const Ctx& c) {
     if (int e = need_bufs(c, 4, "moe_topk")) return e;
@@ -1043,6 +1067,9 @@ void register_ops() {
     v.push_back({"kv_write", op_kv_write});
     v.push_back({"atencion", op_atencion});
     v.push_back({"swiglu", op_swiglu});
+    v.push_back({"geglu", op_geglu});
+    v.push_back({"escalar", [](const Ctx& c) { return op_scale(c, false); }});
+    v.push_back({"suma_esc", [](const Ctx& c) { return op_scale(c, true); }});
     v.push_back({"moe_topk", op_moe_topk});
     v.push_back({"moe_comb", op_moe_comb});
     v.push_back({"moe_group", op_moe_group});

@@ -68,6 +68,7 @@ async function generate(o) {
     const r = await engine.generar(modelo, ids, params);
     for (const t of r.ids) toks.push(t);
   } else if (o.mode === 'sample') {
+    if (!modelo.pasoMuestreado) throw new Error('this model has no fused one-token plan for the sampled mode');
     // sampled continuation on the fused one-token plan (device penalties and top-k candidates, host draw); each
     // token is also chosen on the host from the same logits by a second sampler of the same seed (the reference's
     // procedure over the whole array), and the disagreements are counted
@@ -89,7 +90,8 @@ async function generate(o) {
     }
     delete control.mu;
     extra.control = control;
-  } else if (o.mode === 'ref') {
+  } else if (o.mode === 'ref' || !modelo.decodificarVoraz) {
+    // the reference's loop (also the fast mode of models without the fused one-token plan)
     let lg = logits;
     while (toks.length < n) {
       escribe(lg);

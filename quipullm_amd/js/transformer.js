@@ -50,8 +50,26 @@ class ModeloTransformer {
     const oa = meta.arch_options || {};
     this.neox = oa.rope ? (oa.rope === 'neox' ? 1 : 0) : (ROPE_NEOX.has(a) ? 1 : 0);
     this.escAtt = g('attention.scale', 0) || 1 / Math.sqrt(this.hd);
-    if (g('embedding_scale', 0) || g('residual_scale', 0) || g('logit_scale', 0) || g('attention.sliding_window', 0))
-      throw new Error(a + ': embedding/residual/logit scales and sliding windows are not supported by this backend');
+    // scales (0: none) and soft-capping of the logits, as the reference reads them (transformer.js:35-45)
+    this.escEmb = g('embedding_scale', 0) || 0;
+    this.escRes = g('residual_scale', 0) || 0;
+    this.escLogit = g('logit_scale', 0) || 0;
+    if (oa.embedding_scale === 'sqrt_d') this.escEmb = Math.fround(Math.sqrt(this.D));
+    else if (typeof oa.embedding_scale === 'number') this.escEmb = oa.embedding_scale;
+    this.softcap = g('final_logit_softcapping', 0) || 0;
+    // gemma3 (transformer.js:46-54): sliding windows on all but every `patron`-th layer, their own RoPE base, the
+    // global layers' linear RoPE scaling, sqrt(D) embedding scale, GeGLU
+    this.gemma = a === 'gemma3';
+    this.ventana = 0;
+    if (this.gemma) {
+      this.ventana = g('attention.sliding_window', 0) || 0;
+      this.patron = g('attention.sliding_window_pattern', 6) || 6;
+      this.baseSwa = g('rope.freq_base_swa', 10000);
+      const fac = g('rope.scaling.factor', 1);
+      this.escalaGlobal = g('rope.scaling.type', '') === 'linear' && fac > 0 ? 1 / fac : 1;
+      this.escEmb = Math.fround(Math.sqrt(this.D));
+      this.escAtt = this.nLayers === 62 ? 1 / Math.sqrt(this.D / this.nh) : 1 / Math.sqrt(this.hd);
+    }
     this.ctx = meta.ctx || 4096;
     this.vocab = kv['tokenizer.ggml.tokens'].length;
     this.nExp = g('expert_count', 0);
@@ -81,7 +99,17 @@ class ModeloTransformer {
     this.cacheOn = op.prompt_cache !== false;
     this.hist = [];
     this.intervaloCP = 64;
+    // The fused one-token plan (decodificarVoraz, pasoMuestreado) covers the llama / qwen families; models with
+    // scales, soft-capping or gemma3's post norms, GeGLU and windows decode through forward(), the reference's op
+    // sequence, one token at a time (engine.generar takes that path when the fused methods are absent).
+    this.fusion = !this.gemma && !this.escEmb && !this.escRes && !this.escLogit && !this.softcap;
+    if (!this.fusion) {
+      this.decodificarVoraz = null;
+      this.pasoMuestreado = null;
+    }
   }
+
+  esSwa(i) { return this.ventana > 0 && (i % this.patron) < this.patron - 1; }
 
   // fuente: the GGUF path, or {url} of the server's file route (tensors fetched by ranges, layer by layer)
   async load(fuente, progreso) {
@@ -98,8 +126,8 @@ class ModeloTransformer {
       let F = 0, ceros = null;
       for (let i = 0; i < this.nLayers; i++) {
         const p = 'blk.' + i + '.';
-        for (const n of ['attn_q.bias', 'attn_k.bias', 'attn_v.bias', 'attn_output.bias', 'post_attention_norm.weight', 'post_ffw_norm.weight'])
-          if (c.existe(p + n)) throw new Error(p + n + ': biases and post-norms are not supported by this backend');
+        for (const n of ['attn_q.bias', 'attn_k.bias', 'attn_v.bias', 'attn_output.bias'])
+          if (c.existe(p + n)) throw new Error(p + n + ': biases are not supported by this backend');
         await c.precargar(['attn_norm', 'attn_q', 'attn_k', 'attn_v', 'attn_output', 'attn_q_norm', 'attn_k_norm',
           'ffn_norm', 'ffn_gate_inp', 'ffn_gate_exps', 'ffn_up_exps', 'ffn_down_exps', 'ffn_gate', 'ffn_up',
           'ffn_down'].map(function (n) { return p + n + '.weight'; }));
@@ -112,6 +140,16 @@ class ModeloTransformer {
         capa.qNorm = c.existe(p + 'attn_q_norm.weight') ? c.f32(p + 'attn_q_norm.weight') : null;
         capa.kNorm = c.existe(p + 'attn_k_norm.weight') ? c.f32(p + 'attn_k_norm.weight') : null;
         capa.ffnNorm = c.f32(p + 'ffn_norm.weight');
+        // outputs normalized before the residual add (gemma3; transformer.js:100-101, 218-226)
+        capa.postAtt = c.existe(p + 'post_attention_norm.weight') ? c.f32(p + 'post_attention_norm.weight') : null;
+        capa.postFfn = c.existe(p + 'post_ffw_norm.weight') ? c.f32(p + 'post_ffw_norm.weight') : null;
+        if (this.nExp && (capa.postAtt || capa.postFfn || this.escRes))
+          throw new Error('layer ' + i + ': post norms and residual scales are not supported with experts');
+        if (capa.postAtt || capa.postFfn) {
+          this.fusion = false;
+          this.decodificarVoraz = null;
+          this.pasoMuestreado = null;
+        }
         if (this.nExp) {
           capa.router = c.matriz(p + 'ffn_gate_inp.weight');
           capa.eg = c.matriz(p + 'ffn_gate_exps.weight');
@@ -126,10 +164,15 @@ class ModeloTransformer {
           F = Math.max(F, capa.gate.N);
         }
         const kvd = this.nkv * this.hd, eb = this.kvF16 ? 2 : 4;
-        capa.kc = gpu.buffer(this.ctx * kvd * eb, undefined, 'kcache' + i);
+        // windowed layers keep a ring of window + batch slots (transformer.js:106-111): position p in slot p % cap
+        // holds the window of every token of a batch as it is processed
+        capa.swa = this.esSwa(i) ? this.ventana : 0;
+        capa.anillo = capa.swa && this.ctx > capa.swa + this.batch ? capa.swa + this.batch : 0;
+        capa.slots = capa.anillo || this.ctx;
+        capa.kc = gpu.buffer(capa.slots * kvd * eb, undefined, 'kcache' + i);
         // the f16 value cache is stored in whole tiles of 32 slots, read whole by the decode attention: it starts
         // zeroed so that slots not yet written hold finite values (they are weighted by 0)
-        const vBytes = (this.kvF16 ? Math.ceil(this.ctx / 32) * 32 : this.ctx) * kvd * eb;
+        const vBytes = (this.kvF16 ? Math.ceil(capa.slots / 32) * 32 : capa.slots) * kvd * eb;
         capa.vc = gpu.buffer(vBytes, undefined, 'vcache' + i);
         if (!ceros || ceros.length < vBytes) ceros = new Uint8Array(vBytes);
         gpu.escribir(capa.vc, 0, ceros.subarray(0, vBytes));
@@ -162,6 +205,7 @@ class ModeloTransformer {
       this.lst = B(4 * TB * this.nUsados, 'lst');
       this.off = B(4 * (this.nExp + 1), 'off');
     }
+    if (!this.fusion) this.tmp = B(4 * TB * D, 'tmp');   // a block's output before its norm / scaled add
     this.xl = B(4 * D, 'xlast');
     this.logits = B(4 * this.vocab, 'logits');
     // decode fast path
@@ -183,7 +227,7 @@ class ModeloTransformer {
     this.penPares = B(4 * 2 * 64, 'penalty_pairs');
     this.contador = B(16, 'step_counter');
     this._armarGrupos();
-    this.prepararDecode();
+    if (this.fusion) this.prepararDecode();
     this.reset();
     return Promise.resolve();
   }
@@ -223,23 +267,38 @@ class ModeloTransformer {
     const gpu = this.gpu, D = this.D, P = this.bPaso;
     const G = {};
     G.embed = this._embedGrupo(this.bIds, this.x);
+    if (this.escEmb) G.escEmb = gpu.grupo('escalar', [gpu.uniforme([['u', D], ['f', this.escEmb]]), P, this.x]);
     const uNorm = gpu.uniforme([['u', D], ['u', 0], ['f', this.eps], ['u', 0]]);
     const dummy = this.normFinal;
     const f16 = this.kvF16 ? 1 : 0;
     const kvd = this.nkv * this.hd;
+    const resid = this.escRes || 1;
+    // a block's output into the residual (transformer.js:218-233): added by the matmul itself (acc = 1), or, with
+    // a post norm or a residual scale, written to tmp, normalized, then x += resid * it (suma_esc)
+    const directo = (W, x, post) => {
+      if (!post && resid === 1) return { mm: this._mm(W, x, this.x, 1) };
+      return {
+        mm: this._mm(W, x, this.tmp, 0),
+        norma: post ? gpu.grupo('rmsnorm', [uNorm, P, this.tmp, post, this.xn]) : null,
+        suma: gpu.grupo('suma_esc', [gpu.uniforme([['u', D], ['f', resid]]), P, this.x, post ? this.xn : this.tmp]),
+      };
+    };
     G.capas = this.capas.map((c) => {
+      const baseCapa = this.gemma && c.swa ? this.baseSwa : this.base;
+      const escRope = this.gemma && !c.swa ? this.escalaGlobal : 1;
       const ur = (nh, norm) => gpu.uniforme([['u', this.hd], ['u', nh], ['u', norm ? 1 : 0], ['u', this.neox],
-        ['f', this.eps], ['f', this.base], ['u', this.nrot], ['u', 0]]);
+        ['f', this.eps], ['f', baseCapa], ['u', this.nrot], ['f', escRope === 1 ? 0 : escRope]]);
       const gc = {
         attnNorm: gpu.grupo('rmsnorm', [uNorm, P, this.x, c.attnNorm, this.xn]),
         ffnNorm: gpu.grupo('rmsnorm', [uNorm, P, this.x, c.ffnNorm, this.xn]),
         wq: this._mm(c.wq, this.xn, this.q, 0), wk: this._mm(c.wk, this.xn, this.k, 0), wv: this._mm(c.wv, this.xn, this.v, 0),
         ropeQ: gpu.grupo('norm_rope', [ur(this.nh, !!c.qNorm), P, this.q, c.qNorm || dummy]),
         ropeK: gpu.grupo('norm_rope', [ur(this.nkv, !!c.kNorm), P, this.k, c.kNorm || dummy]),
-        kvw: gpu.grupo('kv_write', [gpu.uniforme([['u', kvd], ['u', 0], ['u', f16], ['u', this.ctx]]), P, this.k, this.v, c.kc, c.vc]),
-        att: gpu.grupo('atencion', [gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', 0],
-          ['f', this.escAtt], ['u', 0], ['u', 0], ['u', 0], ['u', f16], ['u', this.ctx]]), P, this.q, c.kc, c.vc, this.att]),
-        wo: this._mm(c.wo, this.att, this.x, 1),
+        kvw: gpu.grupo('kv_write', [gpu.uniforme([['u', kvd], ['u', c.anillo], ['u', f16], ['u', c.slots]]), P, this.k, this.v,
+          c.kc, c.vc]),
+        att: gpu.grupo('atencion', [gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', c.swa],
+          ['f', this.escAtt], ['u', c.anillo], ['u', 0], ['u', 0], ['u', f16], ['u', c.slots]]), P, this.q, c.kc, c.vc, this.att]),
+        wo: directo(c.wo, this.att, c.postAtt),
       };
       if (this.nExp) {
         const K = this.nUsados;
@@ -256,9 +315,9 @@ class ModeloTransformer {
       } else {
         gc.gate = this._mm(c.gate, this.xn, this.g, 0);
         gc.up = this._mm(c.up, this.xn, this.u, 0);
-        gc.swiglu = gpu.grupo('swiglu', [gpu.uniforme([['u', c.gate.N]]), P, this.g, this.u]);
+        gc.swiglu = gpu.grupo(this.gemma ? 'geglu' : 'swiglu', [gpu.uniforme([['u', c.gate.N]]), P, this.g, this.u]);
         gc.F = c.gate.N;
-        gc.down = this._mm(c.down, this.g, this.x, 1);
+        gc.down = directo(c.down, this.g, c.postFfn);
       }
       return gc;
     });
@@ -282,6 +341,9 @@ class ModeloTransformer {
     const h = this.hist, m = Math.min(h.length, ids.length - 1);
     let n = 0;
     while (n < m && h[n] === ids[n]) n++;
+    // a ring of cap slots still holds the keys the recomputed positions need (from n + 1 - window on) only while
+    // no later position has taken their slots: the history may not reach the first of them plus cap
+    for (const c of this.capas) if (c.anillo && h.length > Math.max(0, n + 1 - c.swa) + c.anillo) n = 0;
     h.length = n;
     this.pos = n;
     return n;
@@ -300,6 +362,13 @@ class ModeloTransformer {
     };
     const filas = function (n) { return Math.ceil(T * n / 256); };
     despachar(null, G.embed, filas(this.D));
+    if (G.escEmb) despachar(null, G.escEmb, filas(this.D));
+    const salida = function (d) {
+      mm(d.mm);
+      if (!d.suma) return;
+      if (d.norma) despachar(null, d.norma, T);
+      despachar(null, d.suma, filas(self.D));
+    };
     for (const gc of G.capas) {
       despachar(null, gc.attnNorm, T);
       mm(gc.wq); mm(gc.wk); mm(gc.wv);
@@ -307,7 +376,7 @@ class ModeloTransformer {
       despachar(null, gc.ropeK, this.nkv, T);
       despachar(null, gc.kvw, Math.ceil(T * this.nkv * this.hd / 256));
       despachar(null, gc.att, this.nh, T);
-      mm(gc.wo);
+      salida(gc.wo);
       despachar(null, gc.ffnNorm, T);
       if (this.nExp) {
         mm(gc.router);
@@ -326,7 +395,7 @@ class ModeloTransformer {
       } else {
         mm(gc.gate); mm(gc.up);
         despachar(null, gc.swiglu, filas(gc.F));
-        mm(gc.down);
+        salida(gc.down);
       }
     }
     return mm;
@@ -352,6 +421,9 @@ class ModeloTransformer {
     if (!conLogits) return Promise.resolve(null);
     const out = new Float32Array(this.vocab);
     gpu.leer(this.logits, 0, out);
+    // on the host, as the reference (transformer.js:333-334)
+    if (this.escLogit) { const k = 1 / this.escLogit; for (let i = 0; i < out.length; i++) out[i] *= k; }
+    if (this.softcap) { const c = this.softcap; for (let i = 0; i < out.length; i++) out[i] = c * Math.tanh(out[i] / c); }
     return Promise.resolve(out);
   }
 

@@ -61,6 +61,8 @@ class ModelConfig:
     ctx: int = 4096
     centered: bool = False    # zero-mean weights (test variants; see gen_blocks)
     wstd: float = 0.0         # > 0: K-quant block scales drawn so the weights' standard deviation is about wstd
+    post_norms: bool = False  # post_attention_norm / post_ffw_norm per layer (gemma3)
+    extra_kv: tuple = ()      # further (key after "<arch>.", gguf value type, value) entries
 
     def tensor_type(self, kind: str) -> int:
         return self.fmt.get(kind, self.fmt.get("default", GGML_Q4_K))
@@ -119,6 +121,17 @@ CONFIGS = {
                                      _q4km(), qk_norm=True, ctx=512, centered=True),
     "mini_llama_q5km_c": ModelConfig("mini_llama_q5km_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
                                      _q5km(), ctx=512, centered=True),
+    # Gemma 3 text (reference transformer.js:46-54): windows of 24 keys on the even layers (pattern 2), their RoPE
+    # base 1e4 against 1e6 on the odd (global) layers with linear scaling 8, q/k norms, post norms, GeGLU, logit
+    # soft-capping 30, sqrt(D) embedding scale
+    "mini_gemma3_q4km_c": ModelConfig("mini_gemma3_q4km_c", "gemma3", 4, 512, 8, 2, 64, 768, 1000, 1e-6, 1000000.0,
+                                      _q4km(), qk_norm=True, ctx=512, centered=True, post_norms=True,
+                                      extra_kv=(("attention.sliding_window", _U32, 24),
+                                                ("attention.sliding_window_pattern", _U32, 2),
+                                                ("rope.freq_base_swa", _F32, 10000.0),
+                                                ("rope.scaling.type", _STR, "linear"),
+                                                ("rope.scaling.factor", _F32, 8.0),
+                                                ("final_logit_softcapping", _F32, 30.0))),
     # IQ4_NL matrices (the reference loads them for its DeepSeek2 class, weights.js:110-116): dense and MoE
     "mini_llama_iq4nl_c": ModelConfig("mini_llama_iq4nl_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
                                       {"default": GGML_IQ4_NL, "token_embd": GGML_F32}, ctx=512, centered=True),
@@ -167,6 +180,9 @@ def tensor_plan(c: ModelConfig):
             out += [(p + "ffn_gate.weight", [c.D, c.F], c.tensor_type("ffn_gate"), "w"),
                     (p + "ffn_up.weight", [c.D, c.F], c.tensor_type("ffn_up"), "w"),
                     (p + "ffn_down.weight", [c.F, c.D], c.tensor_type("ffn_down"), "w")]
+        if c.post_norms:
+            out += [(p + "post_attention_norm.weight", [c.D], GGML_F32, "norm"),
+                    (p + "post_ffw_norm.weight", [c.D], GGML_F32, "norm")]
     return out
 
 
@@ -299,6 +315,7 @@ def metadata(c: ModelConfig):
                (f"{a}.expert_feed_forward_length", _U32, c.ffe), (f"{a}.expert_weights_norm", _BOOL, True)]
     else:
         kv.append((f"{a}.feed_forward_length", _U32, c.F))
+    kv += [(f"{a}.{k}", t, v) for k, t, v in c.extra_kv]
     kv += [("tokenizer.ggml.model", _STR, "synthetic"),
            ("tokenizer.ggml.tokens", _ARR, (_STR, [f"<t{i}>" for i in range(c.vocab)])),
            ("tokenizer.ggml.eos_token_id", _U32, c.vocab - 1)]

@@ -228,6 +228,12 @@ def silu64(g):
         return g / (1.0 + np.exp(-g))
 
 
+def gelu_tanh64(g):
+    """GELU, tanh approximation: 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3)))."""
+    g = np.asarray(g, np.float64)
+    return 0.5 * g * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g + 0.044715 * g ** 3)))
+
+
 def topk64(logits, k, norm, scale):
     p = np.exp(logits - logits.max())
     p /= p.sum()
@@ -255,6 +261,27 @@ class Model64:
         self.nexp, self.k = get("expert_count", 0), get("expert_used_count", 0)
         self.norm_w = bool(get("expert_weights_norm", False))
         self.neox = neox
+        self.scale = get("attention.scale", 0) or 1.0 / np.sqrt(self.hd)
+        self.emb_scale = get("embedding_scale", 0) or 0
+        self.res_scale = get("residual_scale", 0) or 1.0
+        self.logit_scale = get("logit_scale", 0) or 0
+        self.softcap = get("final_logit_softcapping", 0) or 0
+        # Gemma 3: local layers see the last `window` positions (every `pattern`-th layer is global) and rotate with
+        # their own base; global layers divide positions by the linear scaling factor; embeddings times sqrt(D);
+        # GELU(tanh) gating
+        self.gemma = a == "gemma3"
+        self.window = [0] * self.L
+        self.rbase, self.rpos = [self.base] * self.L, [1.0] * self.L
+        if self.gemma:
+            w, pat = get("attention.sliding_window", 0) or 0, get("attention.sliding_window_pattern", 6) or 6
+            fac = get("rope.scaling.factor", 1.0)
+            lin = 1.0 / fac if get("rope.scaling.type", "") == "linear" and fac > 0 else 1.0
+            for i in range(self.L):
+                local = w > 0 and i % pat != pat - 1
+                self.window[i] = w if local else 0
+                self.rbase[i] = get("rope.freq_base_swa", 10000.0) if local else self.base
+                self.rpos[i] = 1.0 if local else lin
+            self.emb_scale = np.sqrt(self.D)
         self.cache = {}
         self.kc = [[] for _ in range(self.L)]
         self.vc = [[] for _ in range(self.L)]
@@ -274,6 +301,8 @@ class Model64:
         pos = len(self.kc[0])
         emb = self.W("token_embd.weight")
         x = emb[tok].copy()
+        if self.emb_scale:
+            x = x * self.emb_scale
         for i in range(self.L):
             p = f"blk.{i}."
             h = rmsnorm64(x, self.v(p + "attn_norm.weight"), self.eps)
@@ -283,16 +312,17 @@ class Model64:
             if p + "attn_q_norm.weight" in self.g.tensors:
                 q = rmsnorm64(q, self.v(p + "attn_q_norm.weight"), self.eps)
                 k = rmsnorm64(k, self.v(p + "attn_k_norm.weight"), self.eps)
-            q = rope64(q, pos, self.base, self.hd, self.neox)
-            k = rope64(k, pos, self.base, self.hd, self.neox)
+            q = rope64(q, pos * self.rpos[i], self.rbase[i], self.hd, self.neox)
+            k = rope64(k, pos * self.rpos[i], self.rbase[i], self.hd, self.neox)
             if self.kv_f16:  # cache rows stored in half precision (rounded to nearest even from float32)
                 k = k.astype(np.float32).astype(np.float16).astype(np.float64)
                 v = v.astype(np.float32).astype(np.float16).astype(np.float64)
             self.kc[i].append(k)
             self.vc[i].append(v)
-            att = attention64(q.reshape(1, -1), np.array(self.kc[i]), np.array(self.vc[i]), pos, self.nh, self.nkv,
-                              self.hd, 1.0 / np.sqrt(self.hd))[0]
-            x = x + self.W(p + "attn_output.weight") @ att
+            lo = max(0, pos + 1 - self.window[i]) if self.window[i] else 0
+            att = attention64(q.reshape(1, -1), np.array(self.kc[i][lo:]), np.array(self.vc[i][lo:]), pos - lo,
+                              self.nh, self.nkv, self.hd, self.scale)[0]
+            x = x + self.res_scale * self.post(p + "post_attention_norm.weight", self.W(p + "attn_output.weight") @ att)
             h = rmsnorm64(x, self.v(p + "ffn_norm.weight"), self.eps)
             if self.nexp:
                 sel, w = topk64(self.v(p + "ffn_gate_inp.weight").reshape(self.nexp, self.D) @ h, self.k,
@@ -307,10 +337,20 @@ class Model64:
             else:
                 gg = self.W(p + "ffn_gate.weight") @ h
                 uu = self.W(p + "ffn_up.weight") @ h
-                x = x + self.W(p + "ffn_down.weight") @ (silu64(gg) * uu)
+                act = gelu_tanh64(gg) if self.gemma else silu64(gg)
+                x = x + self.res_scale * self.post(p + "post_ffw_norm.weight", self.W(p + "ffn_down.weight") @ (act * uu))
         h = rmsnorm64(x, self.v("output_norm.weight"), self.eps)
         out = "output.weight" if "output.weight" in self.g.tensors else "token_embd.weight"
-        return self.W(out) @ h
+        lg = self.W(out) @ h
+        if self.logit_scale:
+            lg = lg / self.logit_scale
+        if self.softcap:
+            lg = self.softcap * np.tanh(lg / self.softcap)
+        return lg
+
+    def post(self, name, y):
+        """A block's output before the residual add: RMS-normalized when the model has the post-norm weight."""
+        return rmsnorm64(y, self.v(name), self.eps) if name in self.g.tensors else y
 
 
 def rel_err(a, b):

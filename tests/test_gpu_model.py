@@ -90,7 +90,7 @@ def read_kv_f16(path, n_layers, ctx, kvd, npos):
 @pytest.mark.parametrize("name", ["mini_llama_q4km_c", "mini_llama_q5km_c", "mini_llama_q3k_c", "mini_llama_q2k_c",
                                   "mini_llama_q8_c", "mini_qwen3_q4km_c",
                                   "mini_qwen3moe_q4k_c", "mini_qwen3moe_q5k_c", "mini_llama_iq4nl_c",
-                                  "mini_qwen3moe_iq4nl_c"])
+                                  "mini_qwen3moe_iq4nl_c", "mini_gemma3_q4km_c"])
 def test_long_prefill_on_matrix_cores_matches_oracle(oracle, models_dir, tmp_path, name):
     """A 150-token prompt in one chunk runs the prefill matmuls on MFMA (bf16 hi/lo products); the logits of the
     prompt's last token and the greedy continuation must still match the oracle."""
@@ -297,6 +297,25 @@ const engine = require(%s);
 """
 
 
+def test_gemma3_windows_on_rings_match_oracle(oracle, models_dir, tmp_path):
+    """Gemma 3 text (windows of 24 keys on the even layers, rings of 24 + 32 slots at batch 32): 40 prompt ids and
+    24 greedy tokens, so the rings wrap; the reference loop and the engine loop against the oracle (f32 KV, as
+    the reference keeps it), ids identical and logits within 1e-3 relative."""
+    name = "mini_gemma3_q4km_c"
+    path = synth.ensure_model(name, models_dir)
+    vocab = synth.CONFIGS[name].vocab
+    prompt = synth.random_prompt(vocab, 40, 4)
+    n = 24
+    want_ids, want_lg = oracle_run(oracle, path, prompt, n, False)
+    r, lg = generate(path, prompt, n, "ref", "f32", str(tmp_path), ["--batch", "32"])
+    lg = lg.reshape(-1, vocab)
+    errs = [rel(a, b) for a, b in zip(lg, want_lg)]
+    assert r["ids"] == want_ids, (r["ids"], want_ids, errs)
+    assert max(errs) < 1e-3, errs
+    r2, _ = generate(path, prompt, n, "engine", "f32", str(tmp_path), ["--batch", "32"])
+    assert r2["ids"] == want_ids
+
+
 @pytest.mark.parametrize("name,kv", [("mini_llama_q4km_c", "f16"), ("mini_qwen3moe_q4k_c", "f32")])
 def test_prompt_cache_reuses_the_common_prefix(models_dir, name, kv):
     """A second request whose prompt extends the first request's prompt and answer computes only the new ids
@@ -315,4 +334,25 @@ def test_prompt_cache_reuses_the_common_prefix(models_dir, name, kv):
     assert r["rb"] == len(p1) + len(r["a"]) - 1
     assert r["rc"] == r["p2"] - 1
     assert r["rd"] == 5 and r["rb2"] == 0
+    assert r["b"] == r["b2"] and r["c"] == r["b2"] and r["d"] == r["d2"]
+
+
+@pytest.mark.parametrize("plen,rd", [(20, 5), (60, 0)])
+def test_prompt_cache_on_rings(models_dir, plen, rd):
+    """The prompt cache of a model with ring caches (gemma3: windows of 24, rings of 56 slots): a prefix is reused
+    only while the ring still holds the window keys of the positions after it.  With a 20-id prompt every reuse
+    stands (the history stays under 56 positions); with 60 ids, the 5-id prefix of the last request is refused
+    (86 positions written since) and everything is recomputed.  Greedy ids equal those of the cache-off model."""
+    path = synth.ensure_model("mini_gemma3_q4km_c", models_dir)
+    p1 = synth.random_prompt(1000, plen, 21)
+    extra = synth.random_prompt(1000, 7, 22)
+    eng = os.path.join(ROOT, "quipullm_amd", "js", "engine.js")
+    script = PROMPT_CACHE % (json.dumps(eng), json.dumps(p1), json.dumps(extra), json.dumps("f32"), json.dumps(path),
+                             json.dumps(path))
+    print("node prompt cache (rings)", plen, flush=True)
+    rc, out, err = run(["timeout", "-k", "5", "110", "node", "-e", script], timeout=120)
+    assert rc == 0, err[-3000:]
+    r = json.loads(out.strip().splitlines()[-1])
+    assert r["rb"] == len(p1) + len(r["a"]) - 1 and r["rc"] == r["p2"] - 1
+    assert r["rd"] == rd and r["rb2"] == 0
     assert r["b"] == r["b2"] and r["c"] == r["b2"] and r["d"] == r["d2"]

@@ -605,6 +605,29 @@ def test_kv_write_past_the_cache_writes_nothing(quipu, dev):
     assert gk[3].all() and not gk[:3].any()  # slot 4 is past the cache: skipped
 
 
+def test_geglu_escalar_suma_esc(quipu, dev, oracle):
+    """geglu (gpu.js:318-330; tanhf of the device library against the C library's, so within a float32 bound
+    scaled like the computation), escalar and suma_esc (gpu.js:635-660; one product and one sum per element:
+    bit-exact)."""
+    rng = np.random.default_rng(19)
+    T, F = 3, 2500
+    g = (rng.standard_normal(T * F) * 4).astype(np.float32)
+    g[:5] = [-30.0, -9.0, 0.0, 9.0, 30.0]
+    uu = rng.standard_normal(T * F).astype(np.float32)
+    gb = dev.buf(g)
+    quipu.dispatch("geglu", [("u", F)], [dev.paso(T, 0), gb, dev.buf(uu)], ((T * F + 255) // 256,))
+    got, want = dev.get(gb, (T * F,)), oracle.geglu(g, uu)
+    assert np.all(np.abs(got - want) <= 2e-6 * (np.abs(g) + 1.0) * np.abs(uu) + 1e-30)
+    D = 700
+    x, t = rng.standard_normal(T * D).astype(np.float32), rng.standard_normal(T * D).astype(np.float32)
+    xb = dev.buf(x)
+    quipu.dispatch("escalar", [("u", D), ("f", 22.627417)], [dev.paso(T, 0), xb], ((T * D + 255) // 256,))
+    x1 = dev.get(xb, (T * D,))
+    np.testing.assert_array_equal(x1, oracle.escalar(x, 22.627417))
+    quipu.dispatch("suma_esc", [("u", D), ("f", 0.375)], [dev.paso(T, 0), xb, dev.buf(t)], ((T * D + 255) // 256,))
+    np.testing.assert_array_equal(dev.get(xb, (T * D,)), oracle.suma_esc(x1, t, 0.375))
+
+
 def test_swiglu_moe_ops(quipu, dev, oracle):
     rng = np.random.default_rng(18)
     T, F = 2, 3000

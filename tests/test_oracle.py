@@ -306,6 +306,26 @@ def test_swiglu(oracle):
     np.testing.assert_allclose(oracle.swiglu(g, u), refs.silu64(g) * u, rtol=1e-6, atol=1e-30)
 
 
+def test_geglu_vs_float64(oracle):
+    # the tanh-form GELU gate; |a| large enough that the clamp of the tanh argument (at 20) is reached
+    rng = np.random.default_rng(31)
+    g = np.concatenate([rng.standard_normal(4000) * 3, [-30.0, -9.0, 0.0, 9.0, 30.0]]).astype(np.float32)
+    u = rng.standard_normal(g.size).astype(np.float32)
+    got = oracle.geglu(g, u)
+    want = refs.gelu_tanh64(g) * u.astype(np.float64)
+    # float32 rounding of a (|a| + 1) |u|-sized computation: for large negative a, 1 + tanh(z) cancels, so the
+    # bound is absolute in that scale rather than relative to the (tiny) result
+    assert np.all(np.abs(got - want) <= 1e-6 * (np.abs(g) + 1.0) * np.abs(u) + 1e-30)
+    assert np.all(np.abs(got - want) <= 2e-6 * np.abs(want) + 1e-30 + 1e-6 * np.abs(u) * (g < 0))
+
+
+def test_escalar_suma_esc(oracle):
+    rng = np.random.default_rng(32)
+    x, t = rng.standard_normal(1000).astype(np.float32), rng.standard_normal(1000).astype(np.float32)
+    np.testing.assert_array_equal(oracle.escalar(x, 22.627417), x * np.float32(22.627417))
+    np.testing.assert_array_equal(oracle.suma_esc(x, t, 0.25), x + np.float32(0.25) * t)
+
+
 def test_moe_topk(oracle):
     lg = np.array([[0.5, 2.0, 2.0, -1.0, 1.0, 2.0]], np.float32)
     sel, wts = oracle.moe_topk(lg, 6, 3, 1, 2.5)
@@ -346,7 +366,7 @@ def test_argmax_ties_nan(oracle):
                                        ("mini_llama_q2k_c", 0), ("mini_qwen3_q4km_c", 1),
                                        ("mini_qwen3moe_q5k_c", 1), ("mini_qwen3moe_q4k_c", 1),
                                        ("mini_llama_q8_c", 0), ("mini_llama_iq4nl_c", 0),
-                                       ("mini_qwen3moe_iq4nl_c", 1)])
+                                       ("mini_qwen3moe_iq4nl_c", 1), ("mini_gemma3_q4km_c", 1)])
 def test_model_forward_vs_float64(oracle, models_dir, name, neox):
     # float32 rounding, amplified by near-ties of the large activations of the centered models, stays below these
     # bounds; a semantic slip (RoPE pairing, norm placement, GQA head map, missing residual) is O(0.1)
@@ -362,6 +382,24 @@ def test_model_forward_vs_float64(oracle, models_dir, name, neox):
     ref2 = refs.Model64(m2.g, neox)
     for t in prompt:  # T = 1: the lane order
         assert refs.rel_err(m2.forward([t], True), ref2.step(t)) < 2e-4
+
+
+def test_gemma3_windows_vs_float64(oracle, models_dir):
+    """Gemma 3 over 46 positions (windows of 24 keys on the local layers): a 30-token chunk (the tiled order), then
+    16 single tokens, each against the float64 model.  The float64 model without windows disagrees (the test would
+    catch a window that is ignored or off by one position)."""
+    path = synth.ensure_model("mini_gemma3_q4km_c", models_dir)
+    m = oracle.Model(path, ctx=128)
+    prompt = synth.random_prompt(m.vocab, 46, 8)
+    ref, nowin = refs.Model64(m.g, 1), refs.Model64(m.g, 1)
+    nowin.window = [0] * nowin.L
+    lg = m.forward(prompt[:30], True)
+    for t in prompt[:30]:
+        lr, ln = ref.step(t), nowin.step(t)
+    assert refs.rel_err(lg, lr) < 2e-3
+    assert refs.rel_err(lr, ln) > 1e-2
+    for t in prompt[30:]:
+        assert refs.rel_err(m.forward([t], True), ref.step(t)) < 2e-4
 
 
 @pytest.mark.parametrize("name,neox", [("mini_llama_q4km_c", 0), ("mini_qwen3moe_q4k_c", 1)])
