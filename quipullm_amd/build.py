@@ -49,35 +49,52 @@ def _atomic(out, build):
             os.remove(tmp)
 
 
-def build_kernels():
+# The timeline build (profiling only): the same sources with -DQP_TIMELINE, in lib/timeline/.  Its kernels record
+# per-workgroup start / end times of the launches captured in a graph; select it with QP_ADDON (Node.js) or
+# QP_LIB (Python) and name the output with QP_TIMELINE_OUT; `python -m quipullm_amd.timeline` summarizes it.
+TIMELINE_LIB = os.path.join(LIB, "timeline")
+
+
+def build_kernels(lib=LIB, defs=()):
     src = os.path.join(CSRC, "kernels", "qp_kernels.hip")
-    _atomic(HSACO, lambda o: _run([HIPCC, "--genco", *HIP_FLAGS, "-o", o, src], "kernels"))
-    return HSACO
+    out = os.path.join(lib, "quipu_kernels.hsaco")
+    _atomic(out, lambda o: _run([HIPCC, "--genco", *HIP_FLAGS, *defs, "-o", o, src], "kernels"))
+    return out
 
 
-def build_lib():
+def build_lib(lib=LIB, defs=()):
     src = os.path.join(CSRC, "quipu.cpp")
     # the scratch array of qp_dispatch_noalloc: a device array, so its file goes through hipcc (device code for
     # gfx950 embedded in the object) and is linked into the library
     scratch = os.path.join(CSRC, "qp_scratch.hip")
-    obj = os.path.join(LIB, "qp_scratch.o")
+    obj = os.path.join(lib, "qp_scratch.o")
     _atomic(obj, lambda o: _run([HIPCC, "-c", "-fPIC", *HIP_FLAGS, "-o", o, scratch], "scratch array"))
+    out = os.path.join(lib, "libquipu.so")
     cmd = lambda o: ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-parameter",
-                     "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", "-o", o, src, obj, f"-L{ROCM}/lib",
+                     "-D__HIP_PLATFORM_AMD__", *defs, f"-I{ROCM}/include", "-o", o, src, obj, f"-L{ROCM}/lib",
                      "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-Wl,-soname,libquipu.so"]
-    _atomic(SO, lambda o: _run(cmd(o), "libquipu"))
-    return SO
+    _atomic(out, lambda o: _run(cmd(o), "libquipu"))
+    return out
 
 
-def build_napi():
+def build_napi(lib=LIB):
     if not os.path.isdir(NODE_INC):
         return None
     src = os.path.join(CSRC, "napi", "quipu_napi.cpp")
+    out = os.path.join(lib, "quipu_napi.node")
     cmd = lambda o: ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-parameter",
-                     f"-I{NODE_INC}", f"-I{os.path.join(ROOT, 'include')}", "-o", o, src, f"-L{LIB}", "-lquipu",
+                     f"-I{NODE_INC}", f"-I{os.path.join(ROOT, 'include')}", "-o", o, src, f"-L{lib}", "-lquipu",
                      "-Wl,-rpath,$ORIGIN"]
-    _atomic(NAPI, lambda o: _run(cmd(o), "N-API addon"))
-    return NAPI
+    _atomic(out, lambda o: _run(cmd(o), "N-API addon"))
+    return out
+
+
+def build_timeline():
+    """The profiling build of the kernels, library and addon into lib/timeline/ (not part of build_all)."""
+    os.makedirs(TIMELINE_LIB, exist_ok=True)
+    defs = ("-DQP_TIMELINE",)
+    out = [build_kernels(TIMELINE_LIB, defs), build_lib(TIMELINE_LIB, defs), build_napi(TIMELINE_LIB)]
+    return [o for o in out if o]
 
 
 def build_oracle():
@@ -100,5 +117,5 @@ def built() -> bool:
 
 
 if __name__ == "__main__":
-    for p in build_all():
+    for p in (build_timeline() if "--timeline" in sys.argv[1:] else build_all()):
         print(p)

@@ -15,7 +15,8 @@ import struct
 import numpy as np
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "lib", "libquipu.so")
+# QP_LIB selects another build of the library (the profiling build in lib/timeline/)
+LIB_PATH = os.path.abspath(os.environ["QP_LIB"]) if os.environ.get("QP_LIB") else os.path.join(PKG, "lib", "libquipu.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "quipu.h")
 
 F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL = 0, 8, 10, 11, 12, 13, 14, 20

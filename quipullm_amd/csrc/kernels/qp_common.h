@@ -92,6 +92,38 @@ QP_DEV float wave_sum_v(float v, uint32_t lane) {
 QP_DEV uint32_t paso_T(uint64_t p) { return cptr<uint32_t>(p)[0]; }
 QP_DEV uint32_t paso_pos(uint64_t p) { return cptr<uint32_t>(p)[1]; }
 
+// ------------------------------------------------------------------ timeline (profiling builds only)
+// Built with -DQP_TIMELINE, each workgroup of a launch captured in a graph (tseq > 0, set by the host) records its
+// start and end (s_memrealtime, 100 MHz), hardware id and XCC into slot (tseq - 1) * QP_TL_SLOTS + workgroup, and
+// thread 0 of the GEMV and decode-attention workgroups stamps its phase boundaries (per kernel kind; the last
+// launch of a kind keeps its stamps).  The host reads both arrays back when it frees the graph.  Without
+// QP_TIMELINE these compile to nothing.
+#ifdef QP_TIMELINE
+#define QP_TL_SLOTS 4096
+#define QP_TL_MAXSEQ 420
+__device__ uint4 qp_tl[QP_TL_MAXSEQ * QP_TL_SLOTS];
+__device__ uint32_t qp_tl_ph[8 * QP_TL_SLOTS * 8];
+QP_DEV uint64_t tl_now() { return __builtin_amdgcn_s_memrealtime(); }
+QP_DEV void tl_rec(uint32_t tseq, uint64_t t0) {
+    if (tseq == 0 || tseq > QP_TL_MAXSEQ || threadIdx.x != 0) return;
+    const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+    const uint32_t wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    if (wg >= QP_TL_SLOTS) return;
+    const uint32_t hw = __builtin_amdgcn_s_getreg(4 | (31 << 11));     // HW_REG_HW_ID, 32 bits
+    const uint32_t xcc = __builtin_amdgcn_s_getreg(20 | (15 << 11));   // HW_REG_XCC_ID
+    qp_tl[(uint64_t)(tseq - 1) * QP_TL_SLOTS + wg] = make_uint4((uint32_t)t0, (uint32_t)t1, hw, xcc | 0x80000000u);
+}
+QP_DEV void tl_ph(uint32_t kind, uint32_t i) {
+    if (threadIdx.x != 0) return;
+    const uint32_t wg = blockIdx.x + gridDim.x * blockIdx.y;
+    if (wg < QP_TL_SLOTS) qp_tl_ph[(kind * QP_TL_SLOTS + wg) * 8 + i] = (uint32_t)__builtin_amdgcn_s_memrealtime();
+}
+#else
+QP_DEV uint64_t tl_now() { return 0; }
+QP_DEV void tl_rec(uint32_t, uint64_t) {}
+QP_DEV void tl_ph(uint32_t, uint32_t) {}
+#endif
+
 // ------------------------------------------------------------------ scalar dequant (bit-exact formulas)
 // These follow the reference's element formulas (kquants.js:166-175, gpu.js:601-603) with every product and
 // difference rounded separately; fp-contract is switched off inside them.

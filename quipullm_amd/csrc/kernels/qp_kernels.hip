@@ -126,7 +126,13 @@ KERNEL __launch_bounds__(256) void qp_dequant(QpDequantArgs a) {
 // ====================================================================================== embeddings
 // Reference embed_q4k/q6k (kquants.js:481-504), embed_q8 (gpu.js:585-604), embed_f32 (gpu.js:605-618):
 // y[t][k] = deq(W[ids[t]][k]).  a.rows (the tensor's row count) sizes the planar sub-arrays.
+QP_DEV void qp_embed_impl(QpEmbedArgs a);
 KERNEL __launch_bounds__(256) void qp_embed(QpEmbedArgs a) {
+    const uint64_t t0 = tl_now();
+    qp_embed_impl(a);
+    tl_rec(a.tseq, t0);
+}
+QP_DEV void qp_embed_impl(QpEmbedArgs a) {
     const uint32_t T = paso_T(a.paso), D = a.d;
     const uint64_t nrows = a.rows;
     const uint64_t NB = total_blocks(a.fmt, nrows, D);
@@ -372,7 +378,15 @@ QP_DEV void pass_setup(const QpGemvArgs& a, uint32_t wg, uint32_t wave, Pass<R>&
 // every lane (the piece index is clamped), which keeps the wait counters exact; lanes past the row's last piece
 // skip the arithmetic.  The first item's loads are issued before the input vector is staged.
 template <int FMT, int R>
+QP_DEV void gemv_seg_body_(const QpGemvArgs& a);
+template <int FMT, int R>
 QP_DEV void gemv_seg_body(const QpGemvArgs& a) {
+    const uint64_t t0 = tl_now();
+    gemv_seg_body_<FMT, R>(a);
+    tl_rec(a.tseq, t0);
+}
+template <int FMT, int R>
+QP_DEV void gemv_seg_body_(const QpGemvArgs& a) {
     extern __shared__ float4 xs[];
     float* xsum = reinterpret_cast<float*>(xs + (a.k >> 2));  // after the K floats of x
     __shared__ float red[4];
@@ -927,6 +941,10 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     __shared__ float red[nwv];
     __shared__ uint64_t wbest[nwv];
     if constexpr (!NORM) norm_w = 0;
+    // timeline phase kinds: 0 mixed Q/K/V, 1 Q4_K one row per slot, 2 Q4_K pairs, 3 Q6_K long rows, 4 Q6_K, 5 other
+    constexpr uint32_t TLK = FMT == QP_KQ_MIX ? 0 : (FMT == QP_Q4_K && R == 1 && NT == 256) ? 1
+                           : (FMT == QP_Q4_K && R == 2) ? 2 : (FMT == QP_Q6_K && NT == 512) ? 3 : FMT == QP_Q6_K ? 4 : 5;
+    tl_ph(TLK, 0);
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nb = K >> 8;
@@ -1007,6 +1025,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         constexpr int n = R * KQ<FMT>::LOADS > 63 ? 63 : R * KQ<FMT>::LOADS;
         __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8));
     }
+    tl_ph(TLK, 1);  // input arrived
 
     // 3. stage x (times the norm weight) in LDS with the group sums; sum of squares for the norm
     // LDS: float4 f at f + f / 64 (one pad per 256 inputs); the group sums of 32 (or 16) inputs over the 8 (or 4)
@@ -1057,6 +1076,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         inv = 1.0f / sqrtf(t / (float)K + eps);
     }
     (void)ngrp;
+    tl_ph(TLK, 2);  // input staged
 
     // 4. units
     constexpr int NO = 2;  // deferred outputs: lane L of register k holds output L + 64k of this wave
@@ -1111,6 +1131,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         }
         const uint32_t u = g - sg.u0;
         const bool pair = sg.mode == QP_GEMV_SWIGLU;
+        if (n == 0) tl_ph(TLK, 3);  // first unit's weights consumed
         issue(buf, n + 1);
         // reduce over the nbp lanes of each slot, then hand each output to its deferred lane
         float v[R];
@@ -1148,6 +1169,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         }
         nout += nper * S;
     }
+    tl_ph(TLK, 4);  // all units
     flush(false);
     if (amax) {
 #pragma unroll
@@ -1172,10 +1194,12 @@ QP_DEV void kq_gemv_seg(const QpGemvArgs& a) {
         const QpGemvSeg& q = a.seg[i];
         return KSeg{q.w, q.w2, q.y, q.n, q.row_base, q.rows_total, q.mode, q.wg0, q.fmt};
     };
+    const uint64_t t0 = tl_now();
     const uint32_t xrow = a.last_row ? paso_T(a.paso) - 1 : 0;
     kq_gemv<FMT, R, XS, decltype(seg_at), KDense, KNoPro, NT, NORM>(seg_at, a.nseg, a.total_wg,
                                                                   a.x + 4ull * xrow * a.k, a.norm_w, a.eps, a.k,
                                                                   a.amax);
+    tl_rec(a.tseq, t0);
 }
 
 // Gathered expert GEMV: grid.y = job, job z uses expert sel[z] and input row z / tfijo.
@@ -1263,7 +1287,15 @@ QP_DEV void moe_route(const QpMoeArgs& a, uint32_t lane, uint32_t& sel, float& w
 }
 
 template <int FMT, int XS>
+QP_DEV void moe_gate_up_body_(const QpMoeArgs& a);
+template <int FMT, int XS>
 QP_DEV void moe_gate_up_body(const QpMoeArgs& a) {
+    const uint64_t t0 = tl_now();
+    moe_gate_up_body_<FMT, XS>(a);
+    tl_rec(a.tseq, t0);
+}
+template <int FMT, int XS>
+QP_DEV void moe_gate_up_body_(const QpMoeArgs& a) {
     const uint32_t lane = threadIdx.x & 63, job = blockIdx.y;
     uint32_t sel = 0, ex = 0;
     float wt = 0.0f;
@@ -1306,7 +1338,15 @@ struct KMoeDown {
 };
 
 template <int FMT, int XS>
+QP_DEV void moe_down_body_(const QpMoeArgs& a);
+template <int FMT, int XS>
 QP_DEV void moe_down_body(const QpMoeArgs& a) {
+    const uint64_t t0 = tl_now();
+    moe_down_body_<FMT, XS>(a);
+    tl_rec(a.tseq, t0);
+}
+template <int FMT, int XS>
+QP_DEV void moe_down_body_(const QpMoeArgs& a) {
     const uint32_t lane = threadIdx.x & 63;
     KMoeDown lay;
     lay.nbwv = a.k >> 8;
@@ -2819,7 +2859,17 @@ QP_DEV void mt_consume(const MTile<HD>& b, uint32_t t, uint32_t kend, uint32_t p
 // LDS (floats): kn [HD] | vn [HD] | freq [HD/2] | q-norm, k-norm weights [HD] each | region R: q [G][HD]
 // during the preparation, then the wavefront partials wacc [4][G][HD], wm [4][8], wl [4][8].
 template <int HD, bool F16, int G>
+QP_DEV void attn_dec_body_(const QpDecAttnArgs& a);
+template <int HD, bool F16, int G>
 QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
+    const uint64_t t0 = tl_now();
+    tl_ph(6, 0);
+    attn_dec_body_<HD, F16, G>(a);
+    tl_ph(6, 6);
+    tl_rec(a.tseq, t0);
+}
+template <int HD, bool F16, int G>
+QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
     using C = DecCfg<HD, F16>;
     constexpr int E = C::E, LPK = C::LPK, KS = C::KS;
     constexpr int QN = (G * HD + 255) / 256;  // q floats per thread
@@ -2890,6 +2940,7 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
         kw[tid] = kwt;
     }
     __syncthreads();
+    tl_ph(6, 1);  // q, k, v loaded
     const float pos_esc = (float)pos0 * a.esc;
     for (uint32_t g = wave; g < G + (wg_new ? 1u : 0u); g += 4) {
         if (g < G)
@@ -2915,8 +2966,10 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
         for (int c = 0; c < HD / 32; c++)
 #pragma unroll
             for (int j = 0; j < 8; j++) qv[c][j] = hr < G ? qs[hr * HD + 32 * c + 8 * qg + j] : 0.0f;
+        tl_ph(6, 2);  // norm + RoPE done
         const float qsc = a.scale * mt_split_q<HD>(qv, qh, ql, lane);
         __syncthreads();  // every wavefront holds its q before region R is reused
+        tl_ph(6, 3);
         float m = -3.0e38f, l = 0.0f;
         f4v acc[HD / 16];
 #pragma unroll
@@ -2946,6 +2999,7 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) acc[mm][i] = fmaf(p, vn[16 * mm + 4 * qg + i], acc[mm][i] * cf);
         }
+        tl_ph(6, 4);  // key stream done
         float lt = l + bfly_f<4>(l, lane);
         lt += bfly_f<5>(lt, lane);
         if (hr < G) {
@@ -3002,6 +3056,7 @@ QP_DEV void attn_dec_body(const QpDecAttnArgs& a) {
     }
     }
     __syncthreads();
+    tl_ph(6, 5);
     // 5. this workgroup's partial per head: merge of its 4 wavefronts (those with no key have l = 0)
     for (uint32_t t = tid; t < G * HD; t += 256) {
         const uint32_t g = t / HD, d = t % HD;
@@ -3113,7 +3168,13 @@ ATTN_MFMA_KERNEL(128, 1) ATTN_MFMA_KERNEL(128, 2) ATTN_MFMA_KERNEL(128, 4) ATTN_
 // (all of them empty, for a position past the cache: o = 0).
 // grid nh; every load of the first batch of splits (up to 16 per thread) and of the (m, l) pairs is issued
 // before any of them is used, so the kernel waits for one memory round trip.
+QP_DEV void qp_dec_attn_comb_impl(QpDecCombArgs a);
 KERNEL __launch_bounds__(256) void qp_dec_attn_comb(QpDecCombArgs a) {
+    const uint64_t t0 = tl_now();
+    qp_dec_attn_comb_impl(a);
+    tl_rec(a.tseq, t0);
+}
+QP_DEV void qp_dec_attn_comb_impl(QpDecCombArgs a) {
     constexpr int CB = 16;
     __shared__ float ws[1024];
     __shared__ float red[4];
@@ -3199,7 +3260,13 @@ KERNEL __launch_bounds__(1024) void qp_argmax(QpArgmaxArgs a) {
 }
 
 // Finish of the fused output GEMV's partial maxima: ids[0] = token, tokens[step] = token, step++, pos0 += T.
+QP_DEV void qp_argmax_fin_impl(QpArgmaxFinArgs a);
 KERNEL __launch_bounds__(256) void qp_argmax_fin(QpArgmaxFinArgs a) {
+    const uint64_t t0 = tl_now();
+    qp_argmax_fin_impl(a);
+    tl_rec(a.tseq, t0);
+}
+QP_DEV void qp_argmax_fin_impl(QpArgmaxFinArgs a) {
     __shared__ uint64_t wb[4];
     const uint32_t tid = threadIdx.x;
     uint64_t best = 0;

@@ -57,7 +57,7 @@ typedef struct {
     uint32_t last_row;  // 1: read x row T-1 (the reference's rmsnorm "ultima" mode)
     uint32_t rows_per_wg;  // weight rows per workgroup pass (4 waves x R)
     uint32_t total_wg;     // workgroups covering all segments (grid-stride over them)
-    uint32_t pad[2];
+    uint32_t tseq, pad;    // tseq: timeline slot of a captured launch (timeline builds; 0: none)
 } QpGemvArgs;
 
 // Gathered expert GEMV (reference matmul_*_e, kquants.js:256-304): job z uses expert sel[z].
@@ -84,7 +84,7 @@ typedef struct {
     uint64_t logits, sel, wts, norm_w;
     uint32_t n, k, e, kused;
     float eps, scale;
-    uint32_t norm, pad;
+    uint32_t norm, tseq;
 } QpMoeArgs;
 
 // Multi-token GEMV for prefill (reference matmul_*_4 / matmul_*_t semantics): y[t][r] (+)= W[r].x[t].
@@ -116,7 +116,7 @@ typedef struct { uint64_t x, xs, paso; uint32_t k, rows; } QpSplitArgs;
 typedef struct { uint64_t ws, y, paso; uint32_t n, rows, splits, acc; } QpReduceArgs;
 
 // ---------------------------------------------------------------- elementwise / small ops
-typedef struct { uint64_t w, ids, y, paso; uint32_t fmt, d, rows, pad; } QpEmbedArgs;  // rows: tensor rows
+typedef struct { uint64_t w, ids, y, paso; uint32_t fmt, d, rows, tseq; } QpEmbedArgs;  // rows: tensor rows
 typedef struct { uint64_t x, w, y, paso; uint32_t d, ultima; float eps; uint32_t rows_fixed; } QpRmsArgs;
 typedef struct {
     uint64_t v, w, paso;
@@ -150,17 +150,18 @@ typedef struct {
     uint32_t hd, nh, nkv, nsplit;
     float scale, eps, base, esc;
     uint32_t nrot, neox, f16, rows;  // rows: slots of the cache; a position at or past it writes an empty result
+    uint32_t tseq, pad[3];
 } QpDecAttnArgs;
 
 typedef struct {
     uint64_t part_o, part_ml, o, paso;
-    uint32_t hd, nh, nsplit, pad;
+    uint32_t hd, nh, nsplit, tseq;
 } QpDecCombArgs;
 
 // Greedy argmax finish: reads the packed max, writes ids[0] and tokens[step], clears the max, advances
 // paso.pos0 by T and the step counter.
 // cap: entries of `tokens`; steps at or past it are not recorded
-typedef struct { uint64_t amax, ids, tokens, step, paso; uint32_t count, advance, cap, pad; } QpArgmaxFinArgs;
+typedef struct { uint64_t amax, ids, tokens, step, paso; uint32_t count, advance, cap, tseq; } QpArgmaxFinArgs;
 // Plain argmax over n floats (lowest index wins ties; NaN never chosen) -> out[0].
 typedef struct { uint64_t v, out; uint32_t n, pad; } QpArgmaxArgs;
 

@@ -87,11 +87,37 @@ const char* kNames[] = {
 };
 hipFunction_t g_fn[K_COUNT];
 
+#ifdef QP_TIMELINE
+// Timeline builds: each launch captured into a graph gets a slot (tseq) in the kernels' record array; the kinds
+// whose kernels record take it in their argument block.
+struct TlLaunch {
+    int k;
+    uint32_t gx, gy, gz, block;
+};
+std::vector<TlLaunch> g_tl;
+template <class A> void tl_tag(A&, uint32_t) {}
+void tl_tag(QpGemvArgs& a, uint32_t v) { a.tseq = v; }
+void tl_tag(QpDecAttnArgs& a, uint32_t v) { a.tseq = v; }
+void tl_tag(QpDecCombArgs& a, uint32_t v) { a.tseq = v; }
+void tl_tag(QpArgmaxFinArgs& a, uint32_t v) { a.tseq = v; }
+void tl_tag(QpEmbedArgs& a, uint32_t v) { a.tseq = v; }
+void tl_tag(QpMoeArgs& a, uint32_t v) { a.tseq = v; }
+#endif
+
 template <class A>
-int launch(Kid k, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block, uint32_t lds, const A& args) {
+int launch(Kid k, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block, uint32_t lds, const A& args0) {
     if (g_fail_launch > 0 && ++g_n_launch == g_fail_launch)
         return fail(QP_E_INJECTED, "injected launch failure (QP_FAIL_LAUNCH=%ld)", g_fail_launch);
     if (gx == 0 || gy == 0 || gz == 0) return 0;
+#ifdef QP_TIMELINE
+    A args = args0;
+    if (g_capturing && g_tl.size() < 420) {
+        g_tl.push_back({(int)k, gx, gy, gz, block});
+        tl_tag(args, (uint32_t)g_tl.size());
+    }
+#else
+    const A& args = args0;
+#endif
     void* params[] = {(void*)&args};
     HIPCHK(hipModuleLaunchKernel(g_fn[k], gx, gy, gz, block, 1, 1, lds, g_stream, params, nullptr), kNames[k]);
     return 0;
@@ -1325,8 +1351,42 @@ int qp_graph_launch(uint64_t graph) {
     return 0;
 }
 
+#ifdef QP_TIMELINE
+// Writes the kernels' records of the launches captured since the last graph was freed to QP_TIMELINE_OUT (uint4 per
+// workgroup slot, 4096 slots per launch; the last replay's), the phase stamps to QP_TIMELINE_OUT.ph and the
+// launches (kernel, grid, block) to QP_TIMELINE_OUT.json.
+void tl_dump() {
+    const char* out = getenv("QP_TIMELINE_OUT");
+    if (!out || g_tl.empty()) return;
+    hipStreamSynchronize(g_stream);
+    hipDeviceptr_t d;
+    size_t sz = 0;
+    if (hipModuleGetGlobal(&d, &sz, g_mod, "qp_tl") != hipSuccess) return;
+    std::vector<uint8_t> h(std::min(sz, g_tl.size() * 4096 * 16));
+    hipMemcpy(h.data(), (void*)d, h.size(), hipMemcpyDeviceToHost);
+    if (FILE* f = fopen(out, "wb")) { fwrite(h.data(), 1, h.size(), f); fclose(f); }
+    if (hipModuleGetGlobal(&d, &sz, g_mod, "qp_tl_ph") == hipSuccess) {
+        std::vector<uint8_t> p(sz);
+        hipMemcpy(p.data(), (void*)d, sz, hipMemcpyDeviceToHost);
+        if (FILE* f = fopen((std::string(out) + ".ph").c_str(), "wb")) { fwrite(p.data(), 1, sz, f); fclose(f); }
+    }
+    if (FILE* f = fopen((std::string(out) + ".json").c_str(), "w")) {
+        fprintf(f, "[");
+        for (size_t i = 0; i < g_tl.size(); i++)
+            fprintf(f, "%s[\"%s\", %u, %u, %u, %u]", i ? ", " : "", kNames[g_tl[i].k], g_tl[i].gx, g_tl[i].gy,
+                    g_tl[i].gz, g_tl[i].block);
+        fprintf(f, "]\n");
+        fclose(f);
+    }
+    g_tl.clear();  // the next graph captured numbers its launches from 1 again
+}
+#endif
+
 int qp_graph_free(uint64_t graph) {
     NEED_INIT();
+#ifdef QP_TIMELINE
+    tl_dump();
+#endif
     HIPCHK(hipGraphExecDestroy((hipGraphExec_t)graph), "hipGraphExecDestroy");
     return 0;
 }

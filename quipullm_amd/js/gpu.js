@@ -8,7 +8,8 @@
 // first argument is accepted and ignored.  Node 12 syntax (CommonJS, no ?? or ?.).
 const path = require('path');
 
-const ADDON = path.join(__dirname, '..', 'lib', 'quipu_napi.node');
+// QP_ADDON selects another build of the addon (the profiling build in lib/timeline/)
+const ADDON = process.env.QP_ADDON ? path.resolve(process.env.QP_ADDON) : path.join(__dirname, '..', 'lib', 'quipu_napi.node');
 let native = null;
 function addon() {
   if (!native) {

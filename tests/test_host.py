@@ -237,3 +237,24 @@ def test_hip_flags_disable_packed_fp32():
     f = build.HIP_FLAGS
     i = f.index("-packed-fp32-ops")
     assert f[i - 1] == "-Xclang" and f[i - 2] == "-target-feature" and "--offload-arch=gfx950" in f
+
+
+def test_timeline_summary(tmp_path):
+    """The profiling build's record files, made up here: two launches of 3 and 2 workgroups."""
+    from quipullm_amd import timeline
+    p = str(tmp_path / "tl.bin")
+    raw = np.zeros((2, timeline.SLOTS, 4), np.uint32)
+    base = (1 << 32) - 50                                   # the 32-bit stamps wrap inside the step
+    for wg, (a, b) in enumerate([(0, 300), (10, 320), (20, 310)]):
+        raw[0, wg] = [(base + a) % (1 << 32), (base + b) % (1 << 32), 0, 0x80000000 | wg]
+    for wg, (a, b) in enumerate([(420, 600), (430, 650)]):
+        raw[1, wg] = [(base + a) % (1 << 32), (base + b) % (1 << 32), 0, 0x80000003]
+    raw.tofile(p)
+    json.dump([["gemv_a", 3, 1, 1, 256], ["dec_attn", 2, 1, 1, 256]], open(p + ".json", "w"))
+    recs = timeline.launches(*timeline.load(p)[:2])
+    assert [d["wgs"] for d in recs] == [3, 2]
+    assert recs[0]["span"] == pytest.approx(3.2) and recs[0]["gap"] == 0.0
+    assert recs[1]["gap"] == pytest.approx(1.0) and recs[1]["span"] == pytest.approx(2.3)
+    assert recs[1]["wg_max"] == pytest.approx(2.2) and recs[0]["xccs"] == 3
+    txt = timeline.report(p)
+    assert "sum of gaps 1.0 us" in txt and "first start to last end 6.5 us" in txt
