@@ -1508,6 +1508,12 @@ constexpr int TM = 128, TN = 128, TK = 64, LDK = 72;  // LDS rows padded to 72 b
 }
 #define QP_NOJOB 0xffffffffu  // a grouped tile's row without a job
 
+// Byte offset of input k of token row t in a bf16 plane written by qp_split_bf16 (rows token rows per plane): the
+// 8 inputs 8q .. 8q + 7 of 32-input chunk c are 16 bytes at ((4c + q) * rows + t) * 16.
+QP_DEV uint64_t xs_off(uint32_t t, uint32_t k, uint32_t rows) {
+    return ((uint64_t)((k >> 5) * 4 + ((k >> 3) & 3)) * rows + t) * 16 + (k & 7) * 2;
+}
+
 // Eight values -> their bf16 high parts and the bf16 of the remainders, each written to LDS as one 16-byte store.
 QP_DEV void split_store8(const float* v, __bf16* hi, __bf16* lo) {
     bf16x8 h, l;
@@ -1741,19 +1747,20 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
     float4 xr[8];
     uint4 xp[8];
     const bool pre = g.xs != 0;
-    const uint64_t xplane = 2ull * g.rows * K;
-    const uint64_t xsrow = g.xs + 2ull * (uint64_t)(xon ? xt : 0) * K;
+    const uint64_t xplane = 2ull * g.rows * (((K + 31) >> 5) << 5);
+    const uint32_t xst = xon ? xt : 0;
     MmW wrg;
     auto load = [&](uint32_t k0) __attribute__((always_inline)) {
         const uint32_t kb = k0 + 32 * part;
         if (pre) {
             // K is a multiple of 16 (f32) or 32 (Q8_0), so a group of 8 is wholly inside or past the row; a group
-            // past it reads as zeros (the row's end is not a 64-multiple when K % 64 != 0)
+            // past the last 32-input chunk reads as zeros (the row's end is not a 64-multiple when K % 64 != 0)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const bool in = kb + 8 * i < K;
-                xp[i] = in ? gload<uint4>(xsrow + 2ull * (kb + 8 * i)) : uint4{0, 0, 0, 0};
-                xp[4 + i] = in ? gload<uint4>(xsrow + xplane + 2ull * (kb + 8 * i)) : uint4{0, 0, 0, 0};
+                const uint64_t o = g.xs + xs_off(xst, kb + 8 * i, g.rows);
+                xp[i] = in ? gload<uint4>(o) : uint4{0, 0, 0, 0};
+                xp[4 + i] = in ? gload<uint4>(o + xplane) : uint4{0, 0, 0, 0};
             }
         } else {
 #pragma unroll
@@ -1857,13 +1864,27 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
         }
 }
 
-// x [T][k] -> its bf16 high / low planes for the matrix-core matmul (8 values per thread and step).
+// x [T][k] -> its bf16 high / low planes for the matrix-core matmul, in the layout of xs_off: one K step's quarter
+// q of 256 consecutive tokens is 4 KB contiguous (a wavefront's load covers 1 KB), and a chunk's inputs past K
+// are zeros.  Token rows T .. rows - 1 are not written: their products reach only outputs that are not
+// stored.  One 16-byte group per thread and step, consecutive threads on consecutive tokens.
 KERNEL __launch_bounds__(256) void qp_split_bf16(QpSplitArgs a) {
-    const uint64_t n8 = (uint64_t)paso_T(a.paso) * a.k / 8, plane = 2ull * a.rows * a.k;
-    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n8; i += (uint64_t)gridDim.x * 256ull) {
-        const float4 v0 = gload<float4>(a.x + 32 * i), v1 = gload<float4>(a.x + 32 * i + 16);
-        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        split_store8(v, reinterpret_cast<__bf16*>(a.xs + 16 * i), reinterpret_cast<__bf16*>(a.xs + plane + 16 * i));
+    const uint32_t T = paso_T(a.paso), nq = ((a.k + 31) >> 5) * 4;
+    const uint64_t n = (uint64_t)nq * T, plane = 2ull * a.rows * (((a.k + 31) >> 5) << 5);
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull) {
+        const uint32_t cq = (uint32_t)(i / T), t = (uint32_t)(i - (uint64_t)cq * T), k8 = cq * 8;
+        float v[8];
+        if (k8 < a.k) {  // K is a multiple of 8 (16 for f32, 32 for Q8_0): a group is wholly inside or past the row
+            const float4 v0 = gload<float4>(a.x + 4ull * ((uint64_t)t * a.k + k8));
+            const float4 v1 = gload<float4>(a.x + 4ull * ((uint64_t)t * a.k + k8) + 16);
+            v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+            v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = 0.0f;
+        }
+        const uint64_t o = xs_off(t, k8, a.rows);
+        split_store8(v, reinterpret_cast<__bf16*>(a.xs + o), reinterpret_cast<__bf16*>(a.xs + plane + o));
     }
 }
 
@@ -1924,11 +1945,13 @@ struct MmOff {
 
 template <int FMT>
 QP_DEV void mm8_load(MmW8& r, const MmOff& o, __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, uint32_t xplane,
-                     uint32_t nb, uint32_t k0) {
-    r.x[0] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x, 2 * k0, 0);
-    r.x[1] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x + 16, 2 * k0, 0);
-    r.x[2] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x, xplane + 2 * k0, 0);
-    r.x[3] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x + 16, xplane + 2 * k0, 0);
+                     uint32_t xrows, uint32_t nb, uint32_t k0) {
+    // quarters q and q + 2 of the step's 32-input chunk (xs_off), high plane then low plane
+    const uint32_t xk = (k0 >> 5) * 64 * xrows, xq2 = 32 * xrows;
+    r.x[0] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x, xk, 0);
+    r.x[1] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x + xq2, xk, 0);
+    r.x[2] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x, xplane + xk, 0);
+    r.x[3] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x + xq2, xplane + xk, 0);
     const uint32_t b = k0 >> 8, e0 = k0 & 255;
     if constexpr (FMT == QP_Q4_K) {
         const uint32_t j = e0 >> 5;
@@ -2032,16 +2055,18 @@ QP_DEV void gemm_mfma256_body(const QpGemmArgs& g) {
     const uint32_t kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t wm = wave >> 1, wn = wave & 1;
-    // loaders, so that each 16-lane phase of an LDS store covers 16 rows: input row lr (16 inputs at 16*part),
-    // weight row wq (8 inputs at 8*sub).  Rows past T or N load row 0 (finite values whose outputs are not stored).
-    const uint32_t lr = wave * 32 + (lane & 31), part = lane >> 5, wq = wave * 16 + (lane & 15), sub = lane >> 4;
-    const uint32_t xt = t0 + lr < T ? t0 + lr : 0, wr = n0 + wq < N ? n0 + wq : 0;
+    // loaders, so that each 16-lane phase of an LDS store covers 16 rows: input row lr, quarters xq and xq + 2 of
+    // the step's 32 inputs (a wavefront loads 64 consecutive rows of one quarter: 1 KB contiguous); weight row wq (8
+    // inputs at 8*sub).  Weight rows past N load row 0; input rows past T read rows of the planes that the split
+    // did not write (rows < g.rows, inside the buffer), whose outputs are not stored.
+    const uint32_t lr = tid & 255, xq = tid >> 8, wq = wave * 16 + (lane & 15), sub = lane >> 4;
+    const uint32_t wr = n0 + wq < N ? n0 + wq : 0;
     const uint32_t nb = K >> 8, xplane = 2 * g.rows * K;
     const __amdgpu_buffer_rsrc_t rx = kq_rsrc(g.xs, 2ull * xplane);
     constexpr uint32_t RBW = KQ<FMT>::RB;  // bytes per weight row and 256 inputs (Q6_K: its d array follows)
     const __amdgpu_buffer_rsrc_t rw = kq_rsrc(g.w, (uint64_t)N * nb * (FMT == QP_Q6_K ? 210 : FMT == QP_Q2_K ? 84 : RBW));
     MmOff off;
-    off.x = 2 * (xt * K + 16 * part);
+    off.x = (xq * g.rows + t0 + lr) * 16;
     off.q = wr * nb * RBW + (sub >> 1) * nb * 16 + (sub & 1) * 8;
     off.h = wr * nb * RBW;
     off.d = FMT == QP_Q2_K ? N * nb * 80 + wr * nb * 4 : N * nb * 208 + wr * nb * 2;
@@ -2056,7 +2081,7 @@ QP_DEV void gemm_mfma256_body(const QpGemmArgs& g) {
     MmW8 r0, r1;
     auto load = [&](MmW8& r, uint32_t st) __attribute__((always_inline)) {
         // past the last step: reload it (unused)
-        mm8_load<FMT>(r, off, rx, rw, xplane, nb, kbeg + min(st, nsteps - 1) * TK);
+        mm8_load<FMT>(r, off, rx, rw, xplane, g.rows, nb, kbeg + min(st, nsteps - 1) * TK);
     };
     auto stage = [&](const MmW8& r, uint32_t st, __bf16* buf) __attribute__((always_inline)) {
         __bf16* xh = buf;
@@ -2065,8 +2090,8 @@ QP_DEV void gemm_mfma256_body(const QpGemmArgs& g) {
         __bf16* wl = wh + TN * LDK;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            *reinterpret_cast<u32x4*>(xh + lr * LDK + 16 * part + 8 * i) = r.x[i];
-            *reinterpret_cast<u32x4*>(xl + lr * LDK + 16 * part + 8 * i) = r.x[2 + i];
+            *reinterpret_cast<u32x4*>(xh + lr * LDK + 8 * (xq + 2 * i)) = r.x[i];
+            *reinterpret_cast<u32x4*>(xl + lr * LDK + 8 * (xq + 2 * i)) = r.x[2 + i];
         }
         float w[8];
         mm8_deq<FMT>(r, kbeg + min(st, nsteps - 1) * TK, sub, w);

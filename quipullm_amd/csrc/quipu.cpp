@@ -423,7 +423,8 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
             a.kchunk = ns > 1 ? cdiv(steps, ns) * 64 : 0;  // whole 64-input steps (the 256-token tiles take 32)
             if (ns > 1) ns = cdiv(K, a.kchunk);
             a.rows = mt * (big ? 256 : 128);
-            const uint64_t xs_bytes = 4ull * a.rows * K, ws_bytes = ns > 1 ? 4ull * ns * a.rows * N : 0;
+            // the bf16 planes: 2 x 2 bytes per token row and input, K rounded up to whole 32-input chunks
+            const uint64_t xs_bytes = 4ull * a.rows * ((K + 31) / 32 * 32), ws_bytes = ns > 1 ? 4ull * ns * a.rows * N : 0;
             uint64_t ws = 0;
             if (int e = workspace(xs_bytes + ws_bytes, &ws)) return e;
             a.xs = ws;
