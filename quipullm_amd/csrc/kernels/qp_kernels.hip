@@ -1943,15 +1943,18 @@ struct MmOff {
     uint32_t x, q, h, d;
 };
 
-template <int FMT>
-QP_DEV void mm8_load(MmW8& r, const MmOff& o, __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, uint32_t xplane,
-                     uint32_t xrows, uint32_t nb, uint32_t k0) {
-    // quarters q and q + 2 of the step's 32-input chunk (xs_off), high plane then low plane
+// quarters q and q + 2 of the step's 32-input chunk (xs_off), high plane then low plane
+QP_DEV void mm8_xload(MmW8& r, const MmOff& o, __amdgpu_buffer_rsrc_t rx, uint32_t xplane, uint32_t xrows,
+                      uint32_t k0) {
     const uint32_t xk = (k0 >> 5) * 64 * xrows, xq2 = 32 * xrows;
     r.x[0] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x, xk, 0);
     r.x[1] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x + xq2, xk, 0);
     r.x[2] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x, xplane + xk, 0);
     r.x[3] = __builtin_amdgcn_raw_buffer_load_b128(rx, o.x + xq2, xplane + xk, 0);
+}
+
+template <int FMT>
+QP_DEV void mm8_wload(MmW8& r, const MmOff& o, __amdgpu_buffer_rsrc_t rw, uint32_t nb, uint32_t k0) {
     const uint32_t b = k0 >> 8, e0 = k0 & 255;
     if constexpr (FMT == QP_Q4_K) {
         const uint32_t j = e0 >> 5;
@@ -1983,6 +1986,13 @@ QP_DEV void mm8_load(MmW8& r, const MmOff& o, __amdgpu_buffer_rsrc_t rx, __amdgp
         r.sc = __builtin_amdgcn_raw_buffer_load_b32(rw, o.h, b * 16 + 12 * nb * 16 + 4 * (h * 2 + (qd >> 1)), 0);
         r.d = __builtin_amdgcn_raw_buffer_load_b16(rw, o.d, b * 2, 0);
     }
+}
+
+template <int FMT>
+QP_DEV void mm8_load(MmW8& r, const MmOff& o, __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, uint32_t xplane,
+                     uint32_t xrows, uint32_t nb, uint32_t k0) {
+    mm8_xload(r, o, rx, xplane, xrows, k0);
+    mm8_wload<FMT>(r, o, rw, nb, k0);
 }
 
 template <int FMT>
@@ -2177,6 +2187,163 @@ QP_DEV void gemm_mfma256_body(const QpGemmArgs& g) {
         }
 }
 
+// ---- 256-token x 256-row tiles (large K-quant matmuls): 8 wavefronts in 2 x 4, each 128 tokens x 64 rows (4 x 2
+// matrix blocks), so that every operand fragment read from LDS feeds more matrix instructions and each input step
+// loaded feeds twice the rows of the 256 x 128 tile.  Same K steps of 32, two LDS buffers of 80 KB (the whole
+// 160 KB), the loads of step s + 2 in flight during step s, one barrier per step.  Thread tid stages input row
+// tid % 256 (quarters tid / 256 and + 2) and the 8 weights at 8*sub of rows wq and wq + 128.
+template <int FMT>
+QP_DEV void gemm_mfma256w_body(const QpGemmArgs& g) {
+    constexpr int TM = 256, TN = 256, TK = 32, LDK = 40, BUF = (TM + TM + TN + TN) * LDK;  // bf16 per buffer
+    extern __shared__ float4 smem4[];
+    __bf16* lds = reinterpret_cast<__bf16*>(smem4);
+    const uint32_t T = g.tfix ? g.tfix : paso_T(g.paso);
+    const uint32_t N = g.n, K = g.k;
+    const uint32_t mt = (uint32_t)gridDim.y, ntl = (uint32_t)gridDim.x, nz = (uint32_t)gridDim.z;
+    const uint32_t total = mt * ntl * nz, id = (blockIdx.z * mt + blockIdx.y) * ntl + blockIdx.x;
+    const uint32_t base = total >> 3, rem = total & 7, xcd = id & 7, j = id >> 3;
+    const uint32_t L = xcd * base + (xcd < rem ? xcd : rem) + j;
+    const uint32_t m_tile = L % mt, rest = L / mt, zs = rest % nz, n_tile = rest / nz;
+    const uint32_t t0 = m_tile * TM, n0 = n_tile * TN;
+    if (t0 >= T) return;
+    const uint32_t kbeg = g.kchunk ? zs * g.kchunk : 0;
+    const uint32_t kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wm = wave >> 2, wn = wave & 3;
+    const uint32_t lr = tid & 255, xq = tid >> 8, wq = wave * 16 + (lane & 15), sub = lane >> 4;
+    // weight rows past N load row 0 (finite values whose outputs are not stored)
+    const uint32_t wr0 = n0 + wq < N ? n0 + wq : 0, wr1 = n0 + wq + 128 < N ? n0 + wq + 128 : 0;
+    const uint32_t nb = K >> 8, xplane = 2 * g.rows * K;
+    const __amdgpu_buffer_rsrc_t rx = kq_rsrc(g.xs, 2ull * xplane);
+    constexpr uint32_t RBW = KQ<FMT>::RB;
+    const __amdgpu_buffer_rsrc_t rw = kq_rsrc(g.w, (uint64_t)N * nb * (FMT == QP_Q6_K ? 210 : FMT == QP_Q2_K ? 84 : RBW));
+    MmOff o0;
+    o0.x = (xq * g.rows + t0 + lr) * 16;
+    o0.q = wr0 * nb * RBW + (sub >> 1) * nb * 16 + (sub & 1) * 8;
+    o0.h = wr0 * nb * RBW;
+    o0.d = FMT == QP_Q2_K ? N * nb * 80 + wr0 * nb * 4 : N * nb * 208 + wr0 * nb * 2;
+    MmOff o1 = o0;  // row wq + 128
+    o1.q = wr1 * nb * RBW + (sub >> 1) * nb * 16 + (sub & 1) * 8;
+    o1.h = wr1 * nb * RBW;
+    o1.d = FMT == QP_Q2_K ? N * nb * 80 + wr1 * nb * 4 : N * nb * 208 + wr1 * nb * 2;
+    const uint32_t nsteps = (kend - kbeg + TK - 1) / TK;
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
+    struct R2 {
+        MmW8 a, b;  // a: the inputs and the weights of row wq; b: the weights of row wq + 128
+    };
+    R2 r0, r1;
+    auto load = [&](R2& r, uint32_t st) __attribute__((always_inline)) {
+        const uint32_t k0 = kbeg + min(st, nsteps - 1) * TK;  // past the last step: reload it (unused)
+        mm8_xload(r.a, o0, rx, xplane, g.rows, k0);
+        mm8_wload<FMT>(r.a, o0, rw, nb, k0);
+        mm8_wload<FMT>(r.b, o1, rw, nb, k0);
+    };
+    auto stage = [&](const R2& r, uint32_t st, __bf16* buf) __attribute__((always_inline)) {
+        __bf16* xh = buf;
+        __bf16* xl = xh + TM * LDK;
+        __bf16* wh = xl + TM * LDK;
+        __bf16* wl = wh + TN * LDK;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            *reinterpret_cast<u32x4*>(xh + lr * LDK + 8 * (xq + 2 * i)) = r.a.x[i];
+            *reinterpret_cast<u32x4*>(xl + lr * LDK + 8 * (xq + 2 * i)) = r.a.x[2 + i];
+        }
+        const uint32_t k0 = kbeg + min(st, nsteps - 1) * TK;
+        float w[8];
+        mm8_deq<FMT>(r.a, k0, sub, w);
+        split_store8_pk(w, wh + wq * LDK + 8 * sub, wl + wq * LDK + 8 * sub);
+        mm8_deq<FMT>(r.b, k0, sub, w);
+        split_store8_pk(w, wh + (wq + 128) * LDK + 8 * sub, wl + (wq + 128) * LDK + 8 * sub);
+    };
+    auto step = [&](uint32_t s, R2& mine, R2& next) __attribute__((always_inline)) {
+        load(mine, s + 2);
+        const __bf16* xh = lds + (s & 1) * BUF;
+        const __bf16* xl = xh + TM * LDK;
+        const __bf16* wh = xl + TM * LDK;
+        const __bf16* wl = wh + TN * LDK;
+#pragma unroll
+        for (int ks = 0; ks < TK / 16; ks++) {
+            const uint32_t kk = ks * 16 + 8 * (lane >> 5);
+            // the weight fragments for all four token blocks; the token fragments one block at a time (registers)
+            bf16x8 bh[2], bl[2];
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const uint32_t nr = wn * 64 + b * 32 + (lane & 31);
+                bh[b] = *reinterpret_cast<const bf16x8*>(wh + nr * LDK + kk);
+                bl[b] = *reinterpret_cast<const bf16x8*>(wl + nr * LDK + kk);
+            }
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                const uint32_t tr = wm * 128 + a * 32 + (lane & 31);
+                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(xh + tr * LDK + kk);
+                const bf16x8 al = *reinterpret_cast<const bf16x8*>(xl + tr * LDK + kk);
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    f32x16& c = acc[a][b];
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh[b], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl[b], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh[b], c, 0, 0, 0);
+                }
+            }
+        }
+        stage(next, s + 1, lds + ((s + 1) & 1) * BUF);  // after the last step: a copy of it, never read
+        __builtin_amdgcn_sched_group_barrier(0x020, 24, 0);  // VMEM reads
+        __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // DS reads (ks 0)
+#pragma unroll
+        for (int i = 0; i < 24; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        }
+#pragma unroll
+        for (int i = 0; i < 12; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (ks 1)
+            __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+        }
+#pragma unroll
+        for (int i = 0; i < 24; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        }
+        __builtin_amdgcn_sched_group_barrier(0x200, 16, 0);  // DS writes
+        __syncthreads();
+    };
+    load(r0, 0);
+    load(r1, 1);
+    stage(r0, 0, lds);
+    __syncthreads();
+    for (uint32_t s = 0; s < nsteps; s += 2) {  // nsteps is even: every K range is whole 64-input steps
+        step(s, r0, r1);
+        step(s + 1, r1, r0);
+    }
+    float* Y = g.ws ? mptr<float>(g.ws) + (uint64_t)zs * g.rows * N : mptr<float>(g.y);
+    const bool add = g.acc && !g.ws;
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const uint32_t n = n0 + wn * 64 + b * 32 + (lane & 31);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const uint32_t t = t0 + wm * 128 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (t < T && n < N) {
+                    float* o = Y + (uint64_t)t * N + n;
+                    *o = add ? *o + acc[a][b][v] : acc[a][b][v];
+                }
+            }
+        }
+}
+
+KERNEL __launch_bounds__(512) void qp_gemm_mfma256w_q4k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q4_K>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_mfma256w_q5k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q5_K>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_mfma256w_q6k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q6_K>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_mfma256w_q3k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q3_K>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_mfma256w_q2k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q2_K>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q4k(QpGemmArgs a) { gemm_mfma256_body<QP_Q4_K>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q5k(QpGemmArgs a) { gemm_mfma256_body<QP_Q5_K>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q3k(QpGemmArgs a) { gemm_mfma256_body<QP_Q3_K>(a); }

@@ -408,7 +408,7 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
         const Kid k = fmt == QP_Q4_K ? K_gemm_mfma_q4k : fmt == QP_Q6_K ? K_gemm_mfma_q6k
                     : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
         uint32_t mt = cdiv(tmax, 128);
-        const uint32_t nt = cdiv(N, 128);
+        uint32_t nt = cdiv(N, 128);
         if (!g_capturing || g_noalloc) {
             // x split into bf16 planes once (not in every weight tile's workgroup), and the K range split when the
             // tiles alone cannot occupy the CUs (a 128-row router at 2048 tokens is 16 tiles); partials summed in
@@ -417,6 +417,13 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
             // Q5_K, Q3_K and Q2_K have only the 256-token tiles
             const bool big = is_kq(fmt) && (tmax >= 256 || fmt == QP_Q5_K || fmt == QP_Q3_K || fmt == QP_Q2_K);
             if (big) mt = cdiv(tmax, 256);
+            // 256 x 256 tiles when they alone give at least half a tile per CU (QP_GEMM_TILES=wide / narrow forces
+            // one kind, for tests and comparisons)
+            const char* tiles = getenv("QP_GEMM_TILES");
+            const bool wide = big && (tiles && !strcmp(tiles, "wide") ? true
+                                      : tiles && !strcmp(tiles, "narrow") ? false
+                                      : mt * cdiv(N, 256) * 2 >= (uint32_t)g_cus);
+            if (wide) nt = cdiv(N, 256);
             const uint32_t steps = K / 64, slots = (big ? 1 : 2) * (uint32_t)g_cus;
             uint32_t ns = 1;
             while (mt * nt * ns * 2 <= slots && steps / (ns * 2) >= 4) ns *= 2;
@@ -431,7 +438,12 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
             a.ws = ns > 1 ? ws + xs_bytes : 0;
             QpSplitArgs sa = {a.x, a.xs, a.paso, K, a.rows};
             if (int e = launch(K_split_bf16, grid_cap((uint64_t)tmax * K / 8), 1, 1, 256, 0, sa)) return e;
-            if (big) {
+            if (wide) {
+                static const Kid kw_of[5] = {K_gemm_mfma256w_q4k, K_gemm_mfma256w_q5k, K_gemm_mfma256w_q6k,
+                                             K_gemm_mfma256w_q3k, K_gemm_mfma256w_q2k};
+                if (int e = launch(kw_of[kq_index(fmt)], nt, mt, ns, 512, 2 * (256 + 256 + 256 + 256) * 40 * 2, a))
+                    return e;
+            } else if (big) {
                 static const Kid kb_of[5] = {K_gemm_mfma256_q4k, K_gemm_mfma256_q5k, K_gemm_mfma256_q6k,
                                              K_gemm_mfma256_q3k, K_gemm_mfma256_q2k};
                 const Kid kb = kb_of[kq_index(fmt)];

@@ -294,6 +294,31 @@ def test_matmul_prefill_mfma(quipu, dev, oracle, fmt, T, N, K, acc):
     assert np.all(np.abs(got - want) <= bound)
 
 
+KQ_FMTS = [capi.Q2_K, capi.Q3_K, capi.Q4_K, capi.Q5_K, capi.Q6_K]
+
+
+@pytest.mark.parametrize("fmt", KQ_FMTS)
+@pytest.mark.parametrize("tiles", ["wide", "narrow"])
+@pytest.mark.parametrize("T,N,K,acc", [(256, 300, 2048, 1), (512, 520, 1024, 0), (300, 700, 4864, 1),
+                                        (768, 256, 512, 0)])
+def test_matmul_prefill_tile_kinds(quipu, dev, oracle, monkeypatch, fmt, tiles, T, N, K, acc):
+    """Both K-quant tile kinds from 256 tokens on, forced (QP_GEMM_TILES): 256 x 256 tiles (8 wavefronts of 128
+    tokens x 64 rows, each thread staging two weight rows) and 256 x 128 tiles, at partial token and row tiles,
+    small grids split along K (the last split partial at K = 4864, 19 blocks)."""
+    monkeypatch.setenv("QP_GEMM_TILES", tiles)
+    raw = raw_matrix(fmt, N, K, 67)
+    W = oracle.dequant(fmt, raw, N * K).reshape(N, K)
+    x = (np.random.default_rng(14).standard_normal((T, K)) * 3).astype(np.float32)
+    y0 = np.random.default_rng(15).standard_normal((T, N)).astype(np.float32)
+    y = dev.buf(y0)
+    quipu.dispatch("matmul_%s_t" % capi.FMT_NAME[fmt], [("u", N), ("u", K), ("u", acc), ("u", 0)],
+                   [dev.paso(T, 0), dev.matrix(fmt, raw, N, K), dev.buf(x), y], ((N + 63) // 64, 1, (T + 31) // 32))
+    got = dev.get(y, (T, N))
+    want = (W.astype(np.float64) @ x.astype(np.float64).T).T + (y0 if acc else 0)
+    bound = (np.abs(W.astype(np.float64)) @ np.abs(x.astype(np.float64)).T).T * 2e-5 + 2e-7 * np.abs(y0) + 1e-30
+    assert np.all(np.abs(got - want) <= bound)
+
+
 @pytest.mark.parametrize("T,N,K", [(256, 300, 4096), (700, 130, 1024)])
 def test_matmul_q4k_prefill_row_magnitudes(quipu, dev, oracle, T, N, K):
     """Q4_K prefill from 256 tokens on (the 256-token tiles, inputs as bf16 high + low planes): token rows of
