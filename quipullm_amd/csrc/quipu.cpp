@@ -417,12 +417,15 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
             // Q5_K, Q3_K and Q2_K have only the 256-token tiles
             const bool big = is_kq(fmt) && (tmax >= 256 || fmt == QP_Q5_K || fmt == QP_Q3_K || fmt == QP_Q2_K);
             if (big) mt = cdiv(tmax, 256);
-            // 256 x 256 tiles when they alone give at least half a tile per CU (QP_GEMM_TILES=wide / narrow forces
-            // one kind, for tests and comparisons)
+            // 256 x 256 tiles when they alone occupy three quarters of the CUs, or half of them at K >= 8192 (where
+            // splitting K in two costs little); measured at 2048 tokens: 14336 x 4096 789 vs 886 us, 6144 x 4096 375
+            // vs 439, 4096 x 14336 917 vs 941, and 4096 x 2048 130 vs 121 against the 256 x 128 tiles.
+            // QP_GEMM_TILES=wide / narrow forces one kind, for tests and comparisons.
             const char* tiles = getenv("QP_GEMM_TILES");
+            const uint32_t wt = mt * cdiv(N, 256);
             const bool wide = big && (tiles && !strcmp(tiles, "wide") ? true
                                       : tiles && !strcmp(tiles, "narrow") ? false
-                                      : mt * cdiv(N, 256) * 2 >= (uint32_t)g_cus);
+                                      : 4 * wt >= 3 * (uint32_t)g_cus || (2 * wt >= (uint32_t)g_cus && K >= 8192));
             if (wide) nt = cdiv(N, 256);
             const uint32_t steps = K / 64, slots = (big ? 1 : 2) * (uint32_t)g_cus;
             uint32_t ns = 1;
