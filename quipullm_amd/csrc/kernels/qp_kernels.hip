@@ -2192,7 +2192,10 @@ QP_DEV void gemm_mfma256_body(const QpGemmArgs& g) {
 // loaded feeds twice the rows of the 256 x 128 tile.  Same K steps of 32, two LDS buffers of 80 KB (the whole
 // 160 KB), the loads of step s + 2 in flight during step s, one barrier per step.  Thread tid stages input row
 // tid % 256 (quarters tid / 256 and + 2) and the 8 weights at 8*sub of rows wq and wq + 128.
-template <int FMT>
+// GLU (matmul_<fmt>_t_swiglu): the tile's rows 0..127 are rows n0.. of the gate tensor and rows 128..255 the same
+// rows of the up tensor (w2), so a tile covers 128 outputs; the up wavefronts hand their sums to the gate
+// wavefronts through LDS and y = silu(gate) * up is stored (the swiglu kernel's formula; no K split).
+template <int FMT, bool GLU = false>
 QP_DEV void gemm_mfma256w_body(const QpGemmArgs& g) {
     constexpr int TM = 256, TN = 256, TK = 32, LDK = 40, BUF = (TM + TM + TN + TN) * LDK;  // bf16 per buffer
     extern __shared__ float4 smem4[];
@@ -2204,7 +2207,7 @@ QP_DEV void gemm_mfma256w_body(const QpGemmArgs& g) {
     const uint32_t base = total >> 3, rem = total & 7, xcd = id & 7, j = id >> 3;
     const uint32_t L = xcd * base + (xcd < rem ? xcd : rem) + j;
     const uint32_t m_tile = L % mt, rest = L / mt, zs = rest % nz, n_tile = rest / nz;
-    const uint32_t t0 = m_tile * TM, n0 = n_tile * TN;
+    const uint32_t t0 = m_tile * TM, n0 = n_tile * (GLU ? TN / 2 : TN);
     if (t0 >= T) return;
     const uint32_t kbeg = g.kchunk ? zs * g.kchunk : 0;
     const uint32_t kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
@@ -2212,17 +2215,20 @@ QP_DEV void gemm_mfma256w_body(const QpGemmArgs& g) {
     const uint32_t wm = wave >> 2, wn = wave & 3;
     const uint32_t lr = tid & 255, xq = tid >> 8, wq = wave * 16 + (lane & 15), sub = lane >> 4;
     // weight rows past N load row 0 (finite values whose outputs are not stored)
-    const uint32_t wr0 = n0 + wq < N ? n0 + wq : 0, wr1 = n0 + wq + 128 < N ? n0 + wq + 128 : 0;
+    const uint32_t wr0 = n0 + wq < N ? n0 + wq : 0;
+    const uint32_t wr1 = GLU ? wr0 : n0 + wq + 128 < N ? n0 + wq + 128 : 0;
     const uint32_t nb = K >> 8, xplane = 2 * g.rows * K;
     const __amdgpu_buffer_rsrc_t rx = kq_rsrc(g.xs, 2ull * xplane);
     constexpr uint32_t RBW = KQ<FMT>::RB;
-    const __amdgpu_buffer_rsrc_t rw = kq_rsrc(g.w, (uint64_t)N * nb * (FMT == QP_Q6_K ? 210 : FMT == QP_Q2_K ? 84 : RBW));
+    const uint64_t wbytes = (uint64_t)N * nb * (FMT == QP_Q6_K ? 210 : FMT == QP_Q2_K ? 84 : RBW);
+    const __amdgpu_buffer_rsrc_t rw = kq_rsrc(g.w, wbytes);
+    const __amdgpu_buffer_rsrc_t rw1 = GLU ? kq_rsrc(g.w2, wbytes) : rw;  // the tensor of row wq + 128
     MmOff o0;
     o0.x = (xq * g.rows + t0 + lr) * 16;
     o0.q = wr0 * nb * RBW + (sub >> 1) * nb * 16 + (sub & 1) * 8;
     o0.h = wr0 * nb * RBW;
     o0.d = FMT == QP_Q2_K ? N * nb * 80 + wr0 * nb * 4 : N * nb * 208 + wr0 * nb * 2;
-    MmOff o1 = o0;  // row wq + 128
+    MmOff o1 = o0;  // row wq + 128 (GLU: row wq of the up tensor)
     o1.q = wr1 * nb * RBW + (sub >> 1) * nb * 16 + (sub & 1) * 8;
     o1.h = wr1 * nb * RBW;
     o1.d = FMT == QP_Q2_K ? N * nb * 80 + wr1 * nb * 4 : N * nb * 208 + wr1 * nb * 2;
@@ -2242,7 +2248,7 @@ QP_DEV void gemm_mfma256w_body(const QpGemmArgs& g) {
         const uint32_t k0 = kbeg + min(st, nsteps - 1) * TK;  // past the last step: reload it (unused)
         mm8_xload(r.a, o0, rx, xplane, g.rows, k0);
         mm8_wload<FMT>(r.a, o0, rw, nb, k0);
-        mm8_wload<FMT>(r.b, o1, rw, nb, k0);
+        mm8_wload<FMT>(r.b, o1, rw1, nb, k0);
     };
     auto stage = [&](const R2& r, uint32_t st, __bf16* buf) __attribute__((always_inline)) {
         __bf16* xh = buf;
@@ -2321,6 +2327,37 @@ QP_DEV void gemm_mfma256w_body(const QpGemmArgs& g) {
         step(s, r0, r1);
         step(s + 1, r1, r0);
     }
+    if constexpr (GLU) {
+        // the up sums (wavefronts wn = 2, 3) to LDS, read by the gate wavefronts wn - 2 at the same index
+        __syncthreads();  // every wavefront has read the last step's LDS buffer
+        float* ex = reinterpret_cast<float*>(smem4);  // [wm][2][4][2][16][64] floats: 128 KB
+        if (wn >= 2) {
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 2; b++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++)
+                        ex[((((wm * 2 + (wn - 2)) * 4 + a) * 2 + b) * 16 + v) * 64 + lane] = acc[a][b][v];
+        }
+        __syncthreads();
+        if (wn >= 2) return;
+        float* Y = mptr<float>(g.y);
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const uint32_t n = n0 + wn * 64 + b * 32 + (lane & 31);
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const uint32_t t = t0 + wm * 128 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                    const float gv = acc[a][b][v];
+                    const float uv = ex[((((wm * 2 + wn) * 4 + a) * 2 + b) * 16 + v) * 64 + lane];
+                    if (t < T && n < N) Y[(uint64_t)t * N + n] = (gv / (1.0f + expf(-gv))) * uv;
+                }
+            }
+        return;
+    }
     float* Y = g.ws ? mptr<float>(g.ws) + (uint64_t)zs * g.rows * N : mptr<float>(g.y);
     const bool add = g.acc && !g.ws;
 #pragma unroll
@@ -2344,6 +2381,11 @@ KERNEL __launch_bounds__(512) void qp_gemm_mfma256w_q5k(QpGemmArgs a) { gemm_mfm
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256w_q6k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q6_K>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256w_q3k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q3_K>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256w_q2k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q2_K>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_glu_q4k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q4_K, true>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_glu_q5k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q5_K, true>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_glu_q6k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q6_K, true>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_glu_q3k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q3_K, true>(a); }
+KERNEL __launch_bounds__(512) void qp_gemm_glu_q2k(QpGemmArgs a) { gemm_mfma256w_body<QP_Q2_K, true>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q4k(QpGemmArgs a) { gemm_mfma256_body<QP_Q4_K>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q5k(QpGemmArgs a) { gemm_mfma256_body<QP_Q5_K>(a); }
 KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q3k(QpGemmArgs a) { gemm_mfma256_body<QP_Q3_K>(a); }

@@ -102,6 +102,7 @@ typedef struct {
     // rows e * n .. of the stacked tensor.  xrows, yrows, nlst: rows of x, y and entries of lst that exist.
     uint64_t lst, off;
     uint32_t n_exp, tpe, tfijo, xrows, yrows, nlst;
+    uint64_t w2;  // matmul_<fmt>_t_swiglu: the up tensor (w is the gate tensor); y = silu(x w) * (x w2)
 } QpGemmArgs;
 
 // moe_group: lst[off[e] .. off[e + 1]) = the jobs i < T * n (in increasing order) with sel[i] == e, e < n_exp;

@@ -465,6 +465,40 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
     return launch(K_gemm_mt, cdiv(N, 64), cdiv(tmax ? tmax : 1, 64), 1, 256, 0, a);
 }
 
+// matmul_<fmt>_t_swiglu: P{N, K}; [paso, w_gate, w_up, x, y]; y[t][n] = silu(x[t] . gate[n]) * (x[t] . up[n]) for
+// the T tokens of paso (K-quants).  No counterpart in the reference, whose prompt pass runs matmul_<fmt>_t on the
+// gate and up tensors and then swiglu (transformer.js:311-313): the same three results in one matrix-core launch
+// (256-token tiles of 128 gate and 128 up rows), for prompt chunks of at least 256 tokens.  Same accumulation as
+// matmul_<fmt>_t with 256 x 256 tiles.  Not while capturing a graph (the input planes may need a larger workspace).
+int op_matmul_glu(const Ctx& c, int fmt, const char* name) {
+    if (int e = need_bufs(c, 5, name)) return e;
+    const uint32_t N = c.U(0), K = c.U(1);
+    if (!is_kq(fmt)) return fail(QP_E_ARG, "%s: K-quant weights only", name);
+    if (int e = check_k(fmt, K, name)) return e;
+    if (N == 0) return fail(QP_E_ARG, "%s: N is 0", name);
+    const uint32_t tmax = c.gz * 32;
+    if (tmax < 256) return fail(QP_E_ARG, "%s: for prompt chunks of 256 tokens or more (grid z %u)", name, c.gz);
+    if (g_capturing && !g_noalloc) return fail(QP_E_CAPTURE, "%s: not while capturing a graph", name);
+    QpGemmArgs a = {};
+    a.w = c.B(1);
+    a.w2 = c.B(2);
+    a.x = c.B(3);
+    a.y = c.B(4);
+    a.paso = c.B(0);
+    a.fmt = fmt;
+    a.n = N;
+    a.k = K;
+    const uint32_t mt = cdiv(tmax, 256), nt = cdiv(N, 128);
+    a.rows = mt * 256;
+    uint64_t ws = 0;
+    if (int e = workspace(4ull * a.rows * K, &ws)) return e;
+    a.xs = ws;
+    QpSplitArgs sa = {a.x, a.xs, a.paso, K, a.rows};
+    if (int e = launch(K_split_bf16, grid_cap((uint64_t)tmax * K / 8), 1, 1, 256, 0, sa)) return e;
+    static const Kid kg_of[5] = {K_gemm_glu_q4k, K_gemm_glu_q5k, K_gemm_glu_q6k, K_gemm_glu_q3k, K_gemm_glu_q2k};
+    return launch(kg_of[kq_index(fmt)], nt, mt, 1, 512, 2 * (256 + 256 + 256 + 256) * 40 * 2, a);
+}
+
 // matmul_<fmt>_e (kquants.js:256-304, kds.js:110-186): P{N,K,acc,tfijo,E}; [paso, w, x, y, sel]
 // (q8: [paso, qs, ds, x, y, sel]); jobs = gz.  E (the 5th word) sizes the planar formats' sub-arrays.
 int op_matmul_e(const Ctx& c, int fmt, const char* name, bool swiglu) {
@@ -1100,6 +1134,10 @@ void register_ops() {
         v.push_back({n1, [fmt, n1](const Ctx& c) { return op_matmul_1(c, fmt, n1.c_str()); }});
         v.push_back({n4, [fmt, n4](const Ctx& c) { return op_matmul_mt(c, fmt, n4.c_str(), 4); }});
         v.push_back({nt, [fmt, nt](const Ctx& c) { return op_matmul_mt(c, fmt, nt.c_str(), 32); }});
+        if (is_kq(fmt)) {
+            const std::string ng = nt + "_swiglu";
+            v.push_back({ng, [fmt, ng](const Ctx& c) { return op_matmul_glu(c, fmt, ng.c_str()); }});
+        }
         v.push_back({ne, [fmt, ne](const Ctx& c) { return op_matmul_e(c, fmt, ne.c_str(), false); }});
         v.push_back({nes, [fmt, nes](const Ctx& c) { return op_matmul_e(c, fmt, nes.c_str(), true); }});
         v.push_back({nem, [fmt, nem](const Ctx& c) { return op_embed(c, fmt, nem.c_str()); }});

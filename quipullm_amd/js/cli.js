@@ -2,18 +2,18 @@
 // Command-line driver of the engine, for tests and the benchmark.
 //
 //   node cli.js generate --model M.gguf --prompt-file ids.json --n 128 [--mode fast|ref|engine|sample] [--kv f16|f32]
-//                        [--ctx N] [--batch N] [--no-tiled] [--logits-out file.f32] [--kv-out file]
+//                        [--ctx N] [--batch N] [--no-tiled] [--no-fused-ffn] [--logits-out file.f32] [--kv-out file]
 //                        [--repeat-penalty R] [--frequency-penalty F] [--presence-penalty P] [--host-loop]
 //                        [--temperature T] [--top-k K] [--top-p P] [--min-p M] [--seed S]
 //   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
 //                        [--warmup W] [--prefill P1,P2] [--eager] [--sample] [--keys-per-split N]
-//                        [--no-moe-grouped]
+//                        [--no-moe-grouped] [--no-fused-ffn]
 //   node cli.js motor    --servidor http://127.0.0.1:PORT [--id ID] [--kv f16] [--batch N]   (the server's engine)
 //                        [--check-prompt-file ids.json --check-n N --check-logits file.f32]
 //
 // generate prints one JSON line {ids, prompt_ms, decode_ms, tps}; with --logits-out the logits each token was
 // chosen from are appended to the file as float32 (vocab floats per token).  mode "ref" runs the reference op
-// sequence with a host argmax per token; "fast" runs the captured one-token graph with the device argmax;
+// sequence (prompt pass included: no fused gate/up/SwiGLU) with a host argmax per token; "fast" runs the captured one-token graph with the device argmax;
 // "engine" runs engine.generar with the given sampler parameters (no logits file); "sample" the sampled
 // continuation with the host cross-check of every token (result field `control`).
 // bench prefills the prompt, then times n decode steps (device events around the graph replays, and the wall
@@ -43,6 +43,8 @@ async function cargar(o) {
   if (o.eager) options.eager_decode = true;
   if (o['keys-per-split']) options.attn_keys_per_split = parseInt(o['keys-per-split'], 10);
   if (o['no-moe-grouped']) options.moe_grouped = false;
+  // the reference's op sequence keeps gate, up and SwiGLU as three ops in the prompt pass too
+  if (o['no-fused-ffn'] || o.mode === 'ref') options.fused_ffn = false;
   return engine.cargarModelo(o.model, { ctx: o.ctx ? parseInt(o.ctx, 10) : undefined, options: options });
 }
 

@@ -91,6 +91,10 @@ class ModeloTransformer {
     // MoE prompt batches of 8 or more tokens grouped by expert on the matrix cores (moe_group + matmul_*_eg, the
     // reference's deepseek2.js:353-378); false: one job per (token, expert) on the expert GEMV
     this.agrupado = op.moe_grouped !== false;
+    // dense FFN of prompt chunks of 256 tokens or more: gate, up and SwiGLU as one matrix-core launch
+    // (matmul_<fmt>_t_swiglu, the same results as the reference's matmul_<fmt>_t, matmul_<fmt>_t, swiglu of
+    // transformer.js:311-313); false: those three ops
+    this.ffnFusionada = op.fused_ffn !== false;
     this.bufs = [];
     this.pos = 0;
     this.grafo = null;
@@ -315,6 +319,10 @@ class ModeloTransformer {
       } else {
         gc.gate = this._mm(c.gate, this.xn, this.g, 0);
         gc.up = this._mm(c.up, this.xn, this.u, 0);
+        if (this.ffnFusionada && this.fusion && this.baldosa && KQ.has(c.gate.tipo) && c.up.tipo === c.gate.tipo &&
+            c.up.N === c.gate.N && c.up.K === c.gate.K)
+          gc.glu = gpu.grupo('matmul_' + c.gate.tipo + '_t_swiglu', [gpu.uniforme([['u', c.gate.N], ['u', c.gate.K]]),
+            P, c.gate.w, c.up.w, this.xn, this.g]);
         gc.swiglu = gpu.grupo(this.gemma ? 'geglu' : 'swiglu', [gpu.uniforme([['u', c.gate.N]]), P, this.g, this.u]);
         gc.F = c.gate.N;
         gc.down = directo(c.down, this.g, c.postFfn);
@@ -393,8 +401,11 @@ class ModeloTransformer {
         e(gc.ed);
         despachar(null, gc.comb, filas(this.D));
       } else {
-        mm(gc.gate); mm(gc.up);
-        despachar(null, gc.swiglu, filas(gc.F));
+        if (gc.glu && T >= 256) despachar(null, gc.glu, Math.ceil(gc.F / 64), 1, Math.ceil(T / 32));
+        else {
+          mm(gc.gate); mm(gc.up);
+          despachar(null, gc.swiglu, filas(gc.F));
+        }
         salida(gc.down);
       }
     }

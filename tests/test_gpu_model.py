@@ -39,7 +39,7 @@ def rel(a, b):
     return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
 
 
-def generate(path, prompt, n, mode, kv, tmp, extra=(), kv_out=None):
+def generate(path, prompt, n, mode, kv, tmp, extra=(), kv_out=None, ctx=256):
     pf = os.path.join(tmp, "prompt.json")
     lf = os.path.join(tmp, "logits.f32")
     with open(pf, "w") as f:
@@ -47,7 +47,7 @@ def generate(path, prompt, n, mode, kv, tmp, extra=(), kv_out=None):
     if os.path.exists(lf):
         os.remove(lf)
     cmd = ["timeout", "-k", "5", "110", "node", CLI, "generate", "--model", path, "--prompt-file", pf, "--n", str(n),
-           "--mode", mode, "--kv", kv, "--ctx", "256"] + (["--logits-out", lf] if mode in ("fast", "ref") else []) + \
+           "--mode", mode, "--kv", kv, "--ctx", str(ctx)] + (["--logits-out", lf] if mode in ("fast", "ref") else []) + \
         (["--kv-out", kv_out] if kv_out else []) + list(extra)
     print("node generate", os.path.basename(path), mode, kv, flush=True)
     rc, out, err = run(cmd, timeout=120)
@@ -57,8 +57,8 @@ def generate(path, prompt, n, mode, kv, tmp, extra=(), kv_out=None):
     return r, lg
 
 
-def oracle_run(oracle, path, prompt, n, kv_f16, kv_ref=None):
-    m = oracle.Model(path, ctx=256, kv_f16=kv_f16)
+def oracle_run(oracle, path, prompt, n, kv_f16, kv_ref=None, ctx=256):
+    m = oracle.Model(path, ctx=ctx, kv_f16=kv_f16)
     if kv_ref is not None:
         m.set_kv_reference(*kv_ref)
     ids, lgs = m.generate(prompt, n)
@@ -91,15 +91,18 @@ def read_kv_f16(path, n_layers, ctx, kvd, npos):
                                   "mini_llama_q8_c", "mini_qwen3_q4km_c",
                                   "mini_qwen3moe_q4k_c", "mini_qwen3moe_q5k_c", "mini_llama_iq4nl_c",
                                   "mini_qwen3moe_iq4nl_c", "mini_gemma3_q4km_c"])
-def test_long_prefill_on_matrix_cores_matches_oracle(oracle, models_dir, tmp_path, name):
-    """A 150-token prompt in one chunk runs the prefill matmuls on MFMA (bf16 hi/lo products); the logits of the
-    prompt's last token and the greedy continuation must still match the oracle."""
+@pytest.mark.parametrize("plen", [150, 300])
+def test_long_prefill_on_matrix_cores_matches_oracle(oracle, models_dir, tmp_path, name, plen):
+    """A 150- or 300-token prompt in one chunk runs the prefill matmuls on MFMA (bf16 hi/lo products; from 256
+    tokens on the 256-token tiles and, for the dense K-quant models, gate, up and SwiGLU fused into one launch);
+    the logits of the prompt's last token and the greedy continuation must still match the oracle."""
     path = synth.ensure_model(name, models_dir)
     vocab = oracle.GGUF(path).tensors["token_embd.weight"]["dims"][1]
-    prompt = synth.random_prompt(vocab, 150, 2)
+    prompt = synth.random_prompt(vocab, plen, 2)
     n = 8
-    want_ids, want_lg = oracle_run(oracle, path, prompt, n, False)
-    r, lg = generate(path, prompt, n, "fast", "f32", str(tmp_path), ["--batch", "160"])
+    ctx = 256 if plen + n <= 256 else 320
+    want_ids, want_lg = oracle_run(oracle, path, prompt, n, False, ctx=ctx)
+    r, lg = generate(path, prompt, n, "fast", "f32", str(tmp_path), ["--batch", str(plen + 10)], ctx=ctx)
     lg = lg.reshape(-1, vocab)
     errs = [rel(a, b) for a, b in zip(lg, want_lg)]
     assert r["ids"] == want_ids, (r["ids"], want_ids, errs)

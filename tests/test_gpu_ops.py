@@ -319,6 +319,60 @@ def test_matmul_prefill_tile_kinds(quipu, dev, oracle, monkeypatch, fmt, tiles, 
     assert np.all(np.abs(got - want) <= bound)
 
 
+@pytest.mark.parametrize("fmt", KQ_FMTS)
+@pytest.mark.parametrize("T,N,K", [(256, 300, 2048), (300, 520, 1024), (513, 130, 4864)])
+def test_matmul_swiglu_fused(quipu, dev, oracle, fmt, T, N, K):
+    """matmul_<fmt>_t_swiglu: silu(x . gate) * (x . up) in one launch (tiles of 128 gate and 128 up rows), against
+    float64: the gate and up sums within the float32 dot bound, propagated through silu and the product."""
+    rg, ru = raw_matrix(fmt, N, K, 71), raw_matrix(fmt, N, K, 72)
+    Wg = oracle.dequant(fmt, rg, N * K).reshape(N, K).astype(np.float64)
+    Wu = oracle.dequant(fmt, ru, N * K).reshape(N, K).astype(np.float64)
+    x = (np.random.default_rng(16).standard_normal((T, K)) * 0.5).astype(np.float32)
+    y = dev.buf(np.full((T, N), np.nan, np.float32))
+    quipu.dispatch("matmul_%s_t_swiglu" % capi.FMT_NAME[fmt], [("u", N), ("u", K)],
+                   [dev.paso(T, 0), dev.matrix(fmt, rg, N, K), dev.matrix(fmt, ru, N, K), dev.buf(x), y],
+                   ((N + 63) // 64, 1, (T + 31) // 32))
+    got = dev.get(y, (T, N)).astype(np.float64)
+    x64 = x.astype(np.float64)
+    g, u = x64 @ Wg.T, x64 @ Wu.T
+    dg, du = 2e-5 * (np.abs(x64) @ np.abs(Wg).T), 2e-5 * (np.abs(x64) @ np.abs(Wu).T)
+    sg = g / (1.0 + np.exp(np.minimum(-g, 700.0)))
+    want = sg * u
+    bound = 1.1 * dg * (np.abs(u) + du) + np.abs(sg) * du + 1e-6 * np.abs(want) + 1e-30
+    assert np.all(np.isfinite(got)) and np.all(np.abs(got - want) <= bound)
+
+
+@pytest.mark.parametrize("fmt", [capi.Q4_K, capi.Q6_K])
+def test_matmul_swiglu_fused_equals_the_three_ops(quipu, dev, monkeypatch, fmt):
+    """At 2048 tokens x 4352 rows (136 tiles of 256 x 256: no K split) the fused op gives exactly what
+    matmul_<fmt>_t on gate and on up followed by swiglu give: the same sums in the same order."""
+    monkeypatch.setenv("QP_GEMM_TILES", "wide")
+    T, N, K = 2048, 4352, 1024
+    rg, ru = raw_matrix(fmt, N, K, 73), raw_matrix(fmt, N, K, 74)
+    wg, wu = dev.matrix(fmt, rg, N, K), dev.matrix(fmt, ru, N, K)
+    x = dev.buf((np.random.default_rng(17).standard_normal((T, K))).astype(np.float32))
+    paso = dev.paso(T, 0)
+    grid = ((N + 63) // 64, 1, (T + 31) // 32)
+    y = dev.buf(np.zeros((T, N), np.float32))
+    quipu.dispatch("matmul_%s_t_swiglu" % capi.FMT_NAME[fmt], [("u", N), ("u", K)], [paso, wg, wu, x, y], grid)
+    g, u = dev.buf(np.zeros((T, N), np.float32)), dev.buf(np.zeros((T, N), np.float32))
+    name = "matmul_%s_t" % capi.FMT_NAME[fmt]
+    quipu.dispatch(name, [("u", N), ("u", K), ("u", 0), ("u", 0)], [paso, wg, x, g], grid)
+    quipu.dispatch(name, [("u", N), ("u", K), ("u", 0), ("u", 0)], [paso, wu, x, u], grid)
+    quipu.dispatch("swiglu", [("u", N)], [paso, g, u], (-(-T * N // 256), 1, 1))
+    assert np.array_equal(dev.get(y, (T, N)), dev.get(g, (T, N)))
+
+
+def test_matmul_swiglu_fused_rejections(quipu, dev):
+    """Prompt chunks under 256 tokens (grid z < 8) and non-K-quant formats are refused with a message."""
+    N, K = 256, 256
+    raw = raw_matrix(capi.Q4_K, N, K, 75)
+    w = dev.matrix(capi.Q4_K, raw, N, K)
+    bufs = [dev.paso(100, 0), w, w, dev.buf(np.zeros((100, K), np.float32)), dev.buf(np.zeros((100, N), np.float32))]
+    with pytest.raises(capi.QuipuError, match="256 tokens"):
+        quipu.dispatch("matmul_q4k_t_swiglu", [("u", N), ("u", K)], bufs, (4, 1, 4))
+
+
 @pytest.mark.parametrize("T,N,K", [(256, 300, 4096), (700, 130, 1024)])
 def test_matmul_q4k_prefill_row_magnitudes(quipu, dev, oracle, T, N, K):
     """Q4_K prefill from 256 tokens on (the 256-token tiles, inputs as bf16 high + low planes): token rows of

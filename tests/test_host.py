@@ -54,7 +54,8 @@ OPS = ["matmul_%s_%s" % (f, s) for f in FORMATS for s in ("1", "4", "t", "e", "e
       ["rmsnorm", "norm_rope", "kv_write", "atencion", "swiglu", "geglu", "escalar", "suma_esc", "moe_topk", "moe_comb", "gemv", "dec_attn",
        "dec_attn_comb", "argmax", "argmax_fin", "repack_q2k", "repack_q3k", "repack_q4k", "repack_q5k", "repack_q6k", "repack_q8", "repack_iq4nl", "fill_u32", "dequant",
        "copy_f4", "read_f4", "moe_gate_up_q4k", "moe_gate_up_q6k", "moe_down_q4k", "moe_down_q6k", "penalizar",
-       "topk_cand", "moe_group"] + ["matmul_%s_eg" % f for f in FORMATS]
+       "topk_cand", "moe_group"] + ["matmul_%s_eg" % f for f in FORMATS] + \
+      ["matmul_%s_t_swiglu" % f for f in ("q2k", "q3k", "q4k", "q5k", "q6k")]
 
 
 def test_op_table(built):
@@ -62,6 +63,7 @@ def test_op_table(built):
     ids = [lib.qp_op_id(n.encode()) for n in OPS]
     assert min(ids) >= 0 and len(set(ids)) == len(ids)
     assert lib.qp_op_id(b"matmul_iq2xs_1") == -1 and lib.qp_op_id(b"") == -1 and lib.qp_op_id(None) == -1
+    assert lib.qp_op_id(b"matmul_q8_t_swiglu") == -1  # the fused gate/up/SwiGLU matmul is for K-quants only
 
 
 def test_ops_used_by_the_js_host_exist(built):
