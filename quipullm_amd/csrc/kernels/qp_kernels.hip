@@ -2819,6 +2819,41 @@ QP_DEV void wave_norm_rope_f(float* v, const float* w, uint32_t hd, bool use_nor
     __builtin_amdgcn_wave_barrier();
 }
 
+// The same with the angles' sines and cosines from tables in LDS (sn[p], cs[p] for pair p: the values
+// wave_norm_rope_f computes per pair, computed once for every head of a workgroup).
+QP_DEV void wave_norm_rope_t(float* v, const float* w, uint32_t hd, bool use_norm, float eps, const float* snt,
+                             const float* cst, uint32_t nrot, bool neox, int lane) {
+    if (use_norm) {
+        float vals[4], ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t i = lane + 64 * c;
+            vals[c] = i < hd ? v[i] : 0.0f;
+            ss += vals[c] * vals[c];
+        }
+        ss = wave_sum_v(ss, (uint32_t)lane);
+        const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t i = lane + 64 * c;
+            if (i < hd) v[i] = (vals[c] * inv) * w[i];
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    const uint32_t mitad = nrot / 2;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const uint32_t pr = lane + 64 * c;
+        if (pr < mitad) {
+            const uint32_t i0 = neox ? pr : 2 * pr, i1 = neox ? pr + mitad : 2 * pr + 1;
+            const float a = v[i0], b = v[i1], sn = snt[pr], cs = cst[pr];
+            v[i0] = a * cs - b * sn;
+            v[i1] = a * sn + b * cs;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
 template <int HD, bool F16>
 struct DecCfg {
     static constexpr int E = F16 ? 8 : 4;   // cache elements per 16-byte chunk
@@ -3110,8 +3145,9 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
     extern __shared__ float4 smem4[];
     float* kn = reinterpret_cast<float*>(smem4);
     float* vn = kn + HD;
-    float* freq = vn + HD;
-    float* qw = freq + HD / 2;
+    float* snt = vn + HD;   // sine and cosine of this position's RoPE angles, one per rotated pair
+    float* cst = snt + HD / 2;
+    float* qw = cst + HD / 2;
     float* kw = qw + HD;
     float* R = kw + HD;
     float* qs = R;
@@ -3157,9 +3193,15 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
         dec_load<HD, F16>(A, rk, rv, a.nkv, kvh, kw0, kw1, kq, dsub);
         dec_load<HD, F16>(B, rk, rv, a.nkv, kvh, kw0 + KS, kw1, kq, dsub);
     }
-    // 2. the preparation (waits for the loads of 1 only)
-    if (tid < a.nrot / 2)
-        freq[tid] = a.freq ? ft : (float)pow((double)a.base, (double)((-2.0f * (float)tid) / (float)a.nrot));
+    // 2. the preparation (waits for the loads of 1 only); the angles' sines and cosines once for all the heads
+    const float pos_esc = (float)pos0 * a.esc;
+    if (tid < a.nrot / 2) {
+        const float fr = a.freq ? ft : (float)pow((double)a.base, (double)((-2.0f * (float)tid) / (float)a.nrot));
+        float sn, cs;
+        sincos2(pos_esc * fr, sn, cs);
+        snt[tid] = sn;
+        cst[tid] = cs;
+    }
 #pragma unroll
     for (int c = 0; c < QN; c++) {
         const uint32_t i = tid + 256 * c;
@@ -3175,13 +3217,11 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
     }
     __syncthreads();
     tl_ph(6, 1);  // q, k, v loaded
-    const float pos_esc = (float)pos0 * a.esc;
     for (uint32_t g = wave; g < G + (wg_new ? 1u : 0u); g += 4) {
         if (g < G)
-            wave_norm_rope_f(qs + g * HD, qw, HD, a.qnorm != 0, a.eps, pos_esc, freq, a.nrot, a.neox != 0,
-                             (int)lane);
+            wave_norm_rope_t(qs + g * HD, qw, HD, a.qnorm != 0, a.eps, snt, cst, a.nrot, a.neox != 0, (int)lane);
         else
-            wave_norm_rope_f(kn, kw, HD, a.knorm != 0, a.eps, pos_esc, freq, a.nrot, a.neox != 0, (int)lane);
+            wave_norm_rope_t(kn, kw, HD, a.knorm != 0, a.eps, snt, cst, a.nrot, a.neox != 0, (int)lane);
     }
     __syncthreads();
     if (F16 && wg_new && tid < HD) {
@@ -3291,21 +3331,27 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
     }
     __syncthreads();
     tl_ph(6, 5);
-    // 5. this workgroup's partial per head: merge of its 4 wavefronts (those with no key have l = 0)
-    for (uint32_t t = tid; t < G * HD; t += 256) {
-        const uint32_t g = t / HD, d = t % HD;
+    // 5. this workgroup's partial per head: merge of its 4 wavefronts (those with no key have l = 0), four
+    // consecutive dimensions of one head per thread
+    for (uint32_t t = tid; t < G * (HD / 4); t += 256) {
+        const uint32_t g = t / (HD / 4), d = (t % (HD / 4)) * 4;
         float M = -3.0e38f;
         for (int w = 0; w < 4; w++)
             if (wl[w * 8 + g] > 0.0f) M = fmaxf(M, wm[w * 8 + g]);
-        float o = 0.0f, L = 0.0f;
+        float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+        float L = 0.0f;
         for (int w = 0; w < 4; w++)
             if (wl[w * 8 + g] > 0.0f) {
                 const float f = __builtin_amdgcn_exp2f((wm[w * 8 + g] - M) * QP_LOG2E);
-                o = fmaf(f, wacc[(w * G + g) * HD + d], o);
+                const float4 c = *reinterpret_cast<const float4*>(wacc + (w * G + g) * HD + d);
+                o.x = fmaf(f, c.x, o.x);
+                o.y = fmaf(f, c.y, o.y);
+                o.z = fmaf(f, c.z, o.z);
+                o.w = fmaf(f, c.w, o.w);
                 L = fmaf(f, wl[w * 8 + g], L);
             }
         const uint64_t i = (uint64_t)(h0 + g) * a.nsplit + wg;
-        gstore<float>(a.part_o + 4 * (i * HD + d), o);
+        gstore<float4>(a.part_o + 4 * (i * HD + d), o);
         if (d == 0) gstore<float2>(a.part_ml + 8 * i, make_float2(M, L));
     }
     if (wg_new && tid < HD) {

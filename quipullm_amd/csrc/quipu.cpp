@@ -955,9 +955,9 @@ int op_dec_attn(const Ctx& c) {
         {{K_dec_attn_h128_f32_g1, K_dec_attn_h128_f32_g2, K_dec_attn_h128_f32_g4, K_dec_attn_h128_f32_g8},
          {K_dec_attn_h128_f16_g1, K_dec_attn_h128_f16_g2, K_dec_attn_h128_f16_g4, K_dec_attn_h128_f16_g8}}};
     const Kid k = kt[a.hd == 128][a.f16 ? 1 : 0][gi];
-    // LDS floats: kn, vn [hd] | freq [hd/2] | q/k norm weights [hd] each | wavefront partials 4*G*hd + 64 (also
-    // holds q [G][hd] before)
-    const uint32_t lds = 4 * (a.hd * 9 / 2 + 4 * G * a.hd + 64);
+    // LDS floats: kn, vn [hd] | RoPE sines, cosines [hd/2] each | q/k norm weights [hd] each | wavefront partials
+    // 4*G*hd + 64 (also holds q [G][hd] before)
+    const uint32_t lds = 4 * (a.hd * 5 + 4 * G * a.hd + 64);
     return launch(k, a.nkv, a.nsplit, 1, 256, lds, a);
 }
 

@@ -500,7 +500,8 @@ class ModeloTransformer {
           return gpu.uniforme([['u', n], ['u', k], ['u', E], ['u', K], ['f', self.eps], ['f', self.escExp],
             ['u', self.normExp ? 1 : 0]]);
         };
-        plan.push([this._gemv([{ W: c.router, mode: STORE, y: this.rl }], this.x, c.ffnNorm, D), 1]);
+        // the router (E rows): one row per wavefront, so that the short tensor spreads over more workgroups
+        plan.push([this._gemv([{ W: c.router, mode: STORE, y: this.rl }], this.x, c.ffnNorm, D, { R: 1 }), 1]);
         plan.push([gpu.grupo('moe_gate_up_' + c.eg.tipo, [u(this.ffe, D), P, c.eg.w, c.eu.w, this.x, c.ffnNorm, this.rl,
           this.g, this.sel, this.wts]), 1]);
         plan.push([gpu.grupo('moe_down_' + c.ed.tipo, [u(D, this.ffe), P, c.ed.w, this.g, this.x, this.sel, this.wts]), 1]);
