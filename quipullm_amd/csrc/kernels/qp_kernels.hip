@@ -3127,6 +3127,9 @@ QP_DEV void mt_consume(const MTile<HD>& b, uint32_t t, uint32_t kend, uint32_t p
 
 // LDS (floats): kn [HD] | vn [HD] | freq [HD/2] | q-norm, k-norm weights [HD] each | region R: q [G][HD]
 // during the preparation, then the wavefront partials wacc [4][G][HD], wm [4][8], wl [4][8].
+template <bool COH>
+QP_DEV void comb_head(uint64_t part_o, uint64_t part_ml, uint64_t out, uint32_t hd, uint32_t ns, uint32_t h, float* ws,
+                      float* red, float* part);
 template <int HD, bool F16, int G>
 QP_DEV void attn_dec_body_(const QpDecAttnArgs& a);
 template <int HD, bool F16, int G>
@@ -3156,6 +3159,7 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
     float* wl = wm + 32;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kvh = blockIdx.x, wg = blockIdx.y, h0 = kvh * G;
+    if (kvh >= a.nkv) return;  // the padding of a merged launch's grid (x = 8)
     const uint32_t kq = lane / LPK, dsub = lane % LPK;
     const uint32_t pos0 = paso_pos(a.paso);
     const uint32_t nk = pos0 < a.rows ? pos0 + 1 : 0;  // a position past the cache reads and writes nothing
@@ -3365,6 +3369,69 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
             gstore<float>(a.vc + 4 * o, vn[tid]);
         }
     }
+    if (a.att) {
+        // 6. the last of the head's workgroups to finish merges its G heads (the dec_attn_comb computation).  With
+        // the grid's x = 8, workgroup (x, y) has linear id x + 8y, and workgroups are handed to the 8 XCDs round
+        // robin by that id: all workgroups of KV head x run on one XCD and share its L2, where the counter's atomic
+        // add executes and the partial stores land once they are complete (workgroup-scope release: the stores
+        // have been acknowledged).  The merge reads them past this CU's L1.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __syncthreads();
+        __shared__ uint32_t last;
+        if (tid == 0) {
+            QP_GLOBAL uint32_t* c = reinterpret_cast<QP_GLOBAL uint32_t*>(a.cnt + 128ull * kvh);
+            const uint32_t n = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            last = n + 1 == gridDim.y;
+            if (n + 1 == gridDim.y) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        __syncthreads();
+        if (last) {
+            // the G heads at once: wavefront w finds the weights e[g][s] = exp(m_s - M) (0 for a split without
+            // keys) and the denominator L = sum l_s e_s of heads g = w, w + 4; then each thread sums four
+            // dimensions of one head over the splits.  The partials are read past this CU's L1 (sc0).
+            const uint32_t ns = a.nsplit;
+            float* eb = R;           // [G][ns]
+            float* lb = R + G * ns;  // [G]
+            const __amdgpu_buffer_rsrc_t rml = kq_rsrc(a.part_ml, 8ull * a.nh * ns);
+            const __amdgpu_buffer_rsrc_t rpo = kq_rsrc(a.part_o, 4ull * a.nh * ns * HD);
+            for (uint32_t g = wave; g < (uint32_t)G; g += 4) {
+                const uint32_t h = h0 + g;
+                float mx = -3.0e38f;
+                for (uint32_t sp = lane; sp < ns; sp += 64) {
+                    const u32x2 r = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * (h * ns + sp), 0, 1);
+                    if (__uint_as_float(r.y) > 0.0f) mx = fmaxf(mx, __uint_as_float(r.x));
+                }
+                mx = wave_max(mx);
+                float ls = 0.0f;
+                for (uint32_t sp = lane; sp < ns; sp += 64) {
+                    const u32x2 r = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * (h * ns + sp), 0, 1);
+                    const float l = __uint_as_float(r.y);
+                    const float e = l > 0.0f ? expf(__uint_as_float(r.x) - mx) : 0.0f;
+                    eb[g * ns + sp] = e;
+                    ls += l * e;
+                }
+                ls = wave_sum(ls);
+                if (lane == 0) lb[g] = ls;
+            }
+            __syncthreads();
+            for (uint32_t t = tid; t < G * (HD / 4); t += 256) {
+                const uint32_t g = t / (HD / 4), d = (t % (HD / 4)) * 4, h = h0 + g;
+                float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+                for (uint32_t sp = 0; sp < ns; sp++) {
+                    const float e = eb[g * ns + sp];
+                    const u32x4 c = __builtin_amdgcn_raw_buffer_load_b128(rpo, 4 * ((h * ns + sp) * HD + d), 0, 1);
+                    o.x = fmaf(e, __uint_as_float(c.x), o.x);
+                    o.y = fmaf(e, __uint_as_float(c.y), o.y);
+                    o.z = fmaf(e, __uint_as_float(c.z), o.z);
+                    o.w = fmaf(e, __uint_as_float(c.w), o.w);
+                }
+                const float L = lb[g];
+                const float4 r = L > 0.0f ? make_float4(o.x / L, o.y / L, o.z / L, o.w / L) : make_float4(0, 0, 0, 0);
+                gstore<float4>(a.att + 4ull * (h * HD + d), r);  // no key: zeros
+            }
+        }
+    }
 }
 
 // (two workgroups per CU: at most 256 registers per lane)
@@ -3448,32 +3515,42 @@ ATTN_MFMA_KERNEL(128, 1) ATTN_MFMA_KERNEL(128, 2) ATTN_MFMA_KERNEL(128, 4) ATTN_
 // (all of them empty, for a position past the cache: o = 0).
 // grid nh; every load of the first batch of splits (up to 16 per thread) and of the (m, l) pairs is issued
 // before any of them is used, so the kernel waits for one memory round trip.
-QP_DEV void qp_dec_attn_comb_impl(QpDecCombArgs a);
-KERNEL __launch_bounds__(256) void qp_dec_attn_comb(QpDecCombArgs a) {
-    const uint64_t t0 = tl_now();
-    qp_dec_attn_comb_impl(a);
-    tl_rec(a.tseq, t0);
-}
-QP_DEV void qp_dec_attn_comb_impl(QpDecCombArgs a) {
+// Merge of one head's split partials (log-sum-exp weights; empty splits skipped; no keys gives zeros), by a whole
+// workgroup of 256 threads: ws [1024], red [4] and part [256] in LDS.  COH: read the partials past the CU's L1 (they
+// were written by other workgroups of the same launch).
+template <bool COH>
+QP_DEV void comb_head(uint64_t part_o, uint64_t part_ml, uint64_t out, uint32_t hd, uint32_t ns, uint32_t h, float* ws,
+                      float* red, float* part) {
     constexpr int CB = 16;
-    __shared__ float ws[1024];
-    __shared__ float red[4];
-    __shared__ float part[256];
-    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t ns = a.nsplit, P = 256 / a.hd, d = tid % a.hd, pt = tid / a.hd;
-    const uint64_t ml = a.part_ml + 8ull * h * ns;
-    const uint64_t po = a.part_o + 4ull * h * ns * a.hd;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t P = 256 / hd, d = tid % hd, pt = tid / hd;
+    const uint64_t ml = part_ml + 8ull * h * ns;
+    const uint64_t po = part_o + 4ull * h * ns * hd;
+    const __amdgpu_buffer_rsrc_t rml = kq_rsrc(ml, 8ull * ns), rpo = kq_rsrc(po, 4ull * ns * hd);
+    auto ldo = [&](uint32_t sp) __attribute__((always_inline)) {
+        const uint32_t off = 4 * (sp * hd + d);
+        return COH ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rpo, off, 0, 1)) : gload<float>(po + off);
+    };
     float pv[CB];
 #pragma unroll
     for (int i = 0; i < CB; i++) {
         const uint32_t sp = pt + P * i;
-        pv[i] = pt < P && sp < ns ? gload<float>(po + 4ull * ((uint64_t)sp * a.hd + d)) : 0.0f;
+        pv[i] = pt < P && sp < ns ? ldo(sp) : 0.0f;
     }
     float2 mv[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const uint32_t sp = tid + 256 * i;
-        mv[i] = sp < ns ? gload<float2>(ml + 8ull * sp) : make_float2(-3.0e38f, 0.0f);
+        if (sp < ns) {
+            if (COH) {
+                const u32x2 r = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * sp, 0, 1);
+                mv[i] = make_float2(__uint_as_float(r.x), __uint_as_float(r.y));
+            } else {
+                mv[i] = gload<float2>(ml + 8ull * sp);
+            }
+        } else {
+            mv[i] = make_float2(-3.0e38f, 0.0f);
+        }
     }
     float mx = -3.0e38f;
 #pragma unroll
@@ -3504,15 +3581,29 @@ QP_DEV void qp_dec_attn_comb_impl(QpDecCombArgs a) {
             if (sp < ns) o = fmaf(ws[sp], pv[i], o);
         }
         for (uint32_t sp = pt + P * CB; sp < ns; sp += P)  // more than CB splits per thread: the rest in turn
-            o = fmaf(ws[sp], gload<float>(po + 4ull * ((uint64_t)sp * a.hd + d)), o);
+            o = fmaf(ws[sp], ldo(sp), o);
     }
     part[tid] = o;
     __syncthreads();
-    if (tid < a.hd) {
+    if (tid < hd) {
         float t = 0.0f;
-        for (uint32_t i = 0; i < P; i++) t += part[i * a.hd + tid];
-        gstore<float>(a.o + 4ull * ((uint64_t)h * a.hd + tid), L > 0.0f ? t / L : 0.0f);  // no key: zeros
+        for (uint32_t i = 0; i < P; i++) t += part[i * hd + tid];
+        gstore<float>(out + 4ull * ((uint64_t)h * hd + tid), L > 0.0f ? t / L : 0.0f);  // no key: zeros
     }
+    __syncthreads();  // ws, red and part may be reused by the caller
+}
+
+QP_DEV void qp_dec_attn_comb_impl(QpDecCombArgs a);
+KERNEL __launch_bounds__(256) void qp_dec_attn_comb(QpDecCombArgs a) {
+    const uint64_t t0 = tl_now();
+    qp_dec_attn_comb_impl(a);
+    tl_rec(a.tseq, t0);
+}
+QP_DEV void qp_dec_attn_comb_impl(QpDecCombArgs a) {
+    __shared__ float ws[1024];
+    __shared__ float red[4];
+    __shared__ float part[256];
+    comb_head<false>(a.part_o, a.part_ml, a.o, a.hd, a.nsplit, blockIdx.x, ws, red, part);
 }
 
 // ====================================================================================== argmax

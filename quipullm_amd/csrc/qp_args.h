@@ -152,6 +152,9 @@ typedef struct {
     float scale, eps, base, esc;
     uint32_t nrot, neox, f16, rows;  // rows: slots of the cache; a position at or past it writes an empty result
     uint32_t tseq, pad[3];
+    // merged output: 0, or o [nh][hd] written by the last workgroup of each KV head to finish (the grid's x is then
+    // 8: workgroups x >= nkv exit); cnt: arrival counters, one per KV head 128 bytes apart, zero between launches
+    uint64_t att, cnt;
 } QpDecAttnArgs;
 
 typedef struct {

@@ -948,6 +948,18 @@ int op_dec_attn(const Ctx& c) {
     a.part_o = c.B(8);
     a.part_ml = c.B(9);
     a.freq = c.B(10);
+    // P[12] = 1: the merge of the splits in the same launch (bindings 11: o [nh][hd], 12: the counters, 8 x 128
+    // bytes, zero before the first launch; the kernel leaves them zero), for nkv <= 8
+    const bool merged = c.U(12) != 0;
+    if (merged) {
+        if (a.nkv > 8) return fail(QP_E_ARG, "dec_attn: the merged form takes at most 8 KV heads (nkv=%u)", a.nkv);
+        a.att = c.nb > 11 ? c.B(11) : 0;
+        a.cnt = c.nb > 12 ? c.B(12) : 0;
+        if (!a.att || !a.cnt) return fail(QP_E_ARG, "dec_attn: the merged form needs bindings 11 (o) and 12 (counters)");
+        if (!buf_room(a.cnt) || buf_room(a.cnt) < 8 * 128)
+            return fail(QP_E_ARG, "dec_attn: the counters must be a library buffer of at least 1024 bytes");
+        if (int e = need_room(a.att, 4ull * a.nh * a.hd, "dec_attn", "the merged output")) return e;
+    }
     const uint32_t gi = G == 1 ? 0 : G == 2 ? 1 : G == 4 ? 2 : 3;
     static const Kid kt[2][2][4] = {
         {{K_dec_attn_h64_f32_g1, K_dec_attn_h64_f32_g2, K_dec_attn_h64_f32_g4, K_dec_attn_h64_f32_g8},
@@ -956,9 +968,10 @@ int op_dec_attn(const Ctx& c) {
          {K_dec_attn_h128_f16_g1, K_dec_attn_h128_f16_g2, K_dec_attn_h128_f16_g4, K_dec_attn_h128_f16_g8}}};
     const Kid k = kt[a.hd == 128][a.f16 ? 1 : 0][gi];
     // LDS floats: kn, vn [hd] | RoPE sines, cosines [hd/2] each | q/k norm weights [hd] each | wavefront partials
-    // 4*G*hd + 64 (also holds q [G][hd] before)
-    const uint32_t lds = 4 * (a.hd * 5 + 4 * G * a.hd + 64);
-    return launch(k, a.nkv, a.nsplit, 1, 256, lds, a);
+    // 4*G*hd + 64 (also holds q [G][hd] before, and the merge's weights G*(nsplit + 1) after)
+    const uint32_t region = 4 * G * a.hd + 64, mreg = G * (a.nsplit + 1);
+    const uint32_t lds = 4 * (a.hd * 5 + (merged && region < mreg ? mreg : region));
+    return launch(k, merged ? 8 : a.nkv, a.nsplit, 1, 256, lds, a);
 }
 
 // dec_attn_comb: P{hd, nh, nsplit}; [paso, part_o, part_ml, o].

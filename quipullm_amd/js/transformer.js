@@ -95,6 +95,11 @@ class ModeloTransformer {
     // (matmul_<fmt>_t_swiglu, the same results as the reference's matmul_<fmt>_t, matmul_<fmt>_t, swiglu of
     // transformer.js:311-313); false: those three ops
     this.ffnFusionada = op.fused_ffn !== false;
+    // one-token step: the split-K attention's partials merged by the last workgroup of each KV head in the same
+    // launch (dec_attn P[12] = 1) instead of a dec_attn_comb launch, for groups of up to 4 query heads (measured:
+    // 8B decode 449 -> 455 tok/s; with 8 heads per group the merge on one workgroup costs more than the launch it
+    // saves, MoE 400 -> 396); false: the separate merge
+    this.atencionUnida = op.merged_attention !== false && this.nkv <= 8 && this.nh / this.nkv <= 4;
     this.bufs = [];
     this.pos = 0;
     this.grafo = null;
@@ -217,6 +222,8 @@ class ModeloTransformer {
     this.nsplit = Math.max(1, Math.min(256, Math.ceil(this.ctx / this.attnPorSplit)));
     this.partO = B(4 * this.nh * this.nsplit * this.hd, 'attn_part_o');
     this.partML = B(8 * this.nh * this.nsplit, 'attn_part_ml');
+    this.attCnt = B(8 * 128, 'attn_counters');   // the merged attention's arrival counters (kept at zero by it)
+    gpu.escribir(this.attCnt, 0, new Uint8Array(8 * 128));
     this.ropeFreq = B(4 * Math.max(1, this.nrot / 2), 'rope_freq');
     gpu.escribir(this.ropeFreq, 0, tablaRope(this.base, this.nrot));
     this.amax = B(8 * AMAX_WG, 'argmax_partials');
@@ -484,13 +491,21 @@ class ModeloTransformer {
     const uAtt = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', this.nsplit], ['f', this.escAtt],
       ['f', this.eps], ['f', this.base], ['u', 0], ['u', this.nrot], ['u', this.neox], ['u', this.kvF16 ? 1 : 0], ['u', this.ctx]]);
     const uComb = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nsplit]]);
+    const uAttM = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', this.nsplit], ['f', this.escAtt],
+      ['f', this.eps], ['f', this.base], ['u', 0], ['u', this.nrot], ['u', this.neox], ['u', this.kvF16 ? 1 : 0], ['u', this.ctx],
+      ['u', 1]]);
     for (let i = 0; i < this.capas.length; i++) {
       const c = this.capas[i], gc = this.G.capas[i];
       for (const g of this._gemvPorFormato([{ W: c.wq, mode: STORE, y: this.q }, { W: c.wk, mode: STORE, y: this.k },
         { W: c.wv, mode: STORE, y: this.v }], this.x, c.attnNorm, D)) plan.push([g, 1]);
-      plan.push([gpu.grupo('dec_attn', [uAtt, P, this.q, this.k, this.v, c.kc, c.vc, c.qNorm, c.kNorm, this.partO, this.partML,
-        this.ropeFreq]), 1]);
-      plan.push([gpu.grupo('dec_attn_comb', [uComb, P, this.partO, this.partML, this.att]), 1]);
+      if (this.atencionUnida) {
+        plan.push([gpu.grupo('dec_attn', [uAttM, P, this.q, this.k, this.v, c.kc, c.vc, c.qNorm, c.kNorm, this.partO,
+          this.partML, this.ropeFreq, this.att, this.attCnt]), 1]);
+      } else {
+        plan.push([gpu.grupo('dec_attn', [uAtt, P, this.q, this.k, this.v, c.kc, c.vc, c.qNorm, c.kNorm, this.partO, this.partML,
+          this.ropeFreq]), 1]);
+        plan.push([gpu.grupo('dec_attn_comb', [uComb, P, this.partO, this.partML, this.att]), 1]);
+      }
       plan.push([this._gemv([{ W: c.wo, mode: ACC, y: this.x }], this.att, null, qd), 1]);
       if (this.nExp && this._moeFusionable(c)) {
         // routing, gate/up with SwiGLU, down and the weighted combine in two launches (the norm is fused in both

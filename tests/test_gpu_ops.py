@@ -910,6 +910,74 @@ def test_dec_attn_fused(quipu, dev, oracle, hd, nh, nkv, pos0, nsplit, f16, neox
     np.testing.assert_array_equal(gv[pos0 + 1:].astype(np.float32), vc[pos0 + 1:])
 
 
+@pytest.mark.parametrize("hd,nh,nkv,pos0,nsplit,f16,neox,qk_norm",
+                         [(128, 32, 8, 4095, 17, 1, 0, 0), (128, 32, 4, 2047, 18, 1, 1, 1), (128, 32, 8, 777, 7, 0, 1, 1),
+                          (64, 8, 1, 31, 1, 0, 0, 1), (128, 16, 8, 33, 200, 0, 0, 0), (64, 32, 4, 2000, 16, 1, 0, 1),
+                          (128, 8, 1, 64, 5, 1, 1, 1), (64, 8, 2, 95, 300, 1, 0, 0), (128, 16, 2, 3000, 1024, 1, 0, 0)])
+def test_dec_attn_merged(quipu, dev, hd, nh, nkv, pos0, nsplit, f16, neox, qk_norm):
+    """dec_attn with P[12] = 1: the last workgroup of each KV head to finish merges its heads' partials in the same
+    launch (grid x = 8, so a head's workgroups share one XCD).  The same as dec_attn + dec_attn_comb up to the
+    order of the merge's sums (within 1e-5), the same cache row appended, and bit-identical over three launches in a
+    row whichever workgroup finishes last (the arrival counters return to zero after each), including splits
+    without keys (nsplit 200 .. 1024 over a short cache)."""
+    rows = 4100
+    kvd = nkv * hd
+    rng = np.random.default_rng(22)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(kvd).astype(np.float32)
+    v = rng.standard_normal(kvd).astype(np.float32)
+    kc = rng.standard_normal((rows, kvd)).astype(np.float32)
+    vc = rng.standard_normal((rows, kvd)).astype(np.float32)
+    if f16:
+        kc, vc = f16r(kc), f16r(vc)
+    qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    dt = np.float16 if f16 else np.float32
+    u = [("u", hd), ("u", nh), ("u", nkv), ("u", nsplit), ("f", float(np.float32(1 / np.sqrt(hd)))), ("f", 1e-6),
+         ("f", 1e6), ("u", 0), ("u", hd), ("u", neox), ("u", f16), ("u", rows)]
+
+    def run(merged):
+        kcb, vcb = dev.buf(kc.astype(dt)), dev.buf(refs.v_tiled(vc.astype(dt), kvd) if f16 else vc)
+        po, pml, o = dev.zeros(nh * nsplit * hd * 4), dev.zeros(nh * nsplit * 8), dev.zeros(nh * hd * 4)
+        paso = dev.paso(1, pos0)
+        b = [paso, dev.buf(q), dev.buf(k), dev.buf(v), kcb, vcb, dev.buf(qn) if qk_norm else 0,
+             dev.buf(kn) if qk_norm else 0, po, pml, dev.buf(rope_table(1e6, hd))]
+        outs = []
+        if merged:
+            cnt = dev.zeros(8 * 128)
+            for _ in range(3):
+                quipu.upload(o, np.full(nh * hd, np.nan, np.float32))
+                quipu.dispatch("dec_attn", u + [("u", 1)], b + [o, cnt], (1, 1, 1))
+                outs.append(dev.get(o, (nh * hd,)))
+            assert np.all(dev.get(cnt, (8 * 32,), np.uint32) == 0)
+        else:
+            quipu.dispatch("dec_attn", u, b)
+            quipu.dispatch("dec_attn_comb", [("u", hd), ("u", nh), ("u", nsplit)], [paso, po, pml, o])
+            outs.append(dev.get(o, (nh * hd,)))
+        return outs, dev.get(kcb, (rows, kvd), dt)
+
+    want, kw = run(False)
+    got, kg = run(True)
+    np.testing.assert_allclose(got[0], want[0], rtol=1e-5, atol=1e-6)
+    for g in got[1:]:
+        np.testing.assert_array_equal(g, got[0])
+    np.testing.assert_array_equal(kg, kw)
+
+
+def test_dec_attn_merged_rejections(quipu, dev):
+    """The merged form needs at most 8 KV heads, the output and a counter buffer of this library."""
+    hd, nh, nkv, rows = 64, 16, 16, 64
+    b = [dev.paso(1, 3)] + [dev.zeros(4 * nh * hd)] * 3 + [dev.zeros(4 * rows * nkv * hd)] * 2 + [0, 0] + \
+        [dev.zeros(4 * nh * hd), dev.zeros(8 * nh), 0, dev.zeros(4 * nh * hd), dev.zeros(1024)]
+    u = [("u", hd), ("u", nh), ("u", nkv), ("u", 1), ("f", 0.125), ("f", 1e-6), ("f", 1e4), ("u", 0), ("u", hd),
+         ("u", 0), ("u", 0), ("u", rows), ("u", 1)]
+    with pytest.raises(capi.QuipuError, match="at most 8 KV heads"):
+        quipu.dispatch("dec_attn", u, b)
+    u[2] = ("u", 8)
+    with pytest.raises(capi.QuipuError, match="at least 1024 bytes"):
+        quipu.dispatch("dec_attn", u, b[:12] + [dev.zeros(512)])
+
+
 @pytest.mark.parametrize("pos0", [4, 40, 700])
 def test_attention_large_scores_stay_finite(quipu, dev, oracle, pos0):
     """Scores of order 1e8 (q and k of order 1e4) through the matrix-core decode and prefill attention: the softmax
