@@ -476,6 +476,8 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
 // gate and up tensors and then swiglu (transformer.js:311-313): the same three results in one matrix-core launch
 // (256-token tiles of 128 gate and 128 up rows), for prompt chunks of at least 256 tokens.  Same accumulation as
 // matmul_<fmt>_t with 256 x 256 tiles.  Not while capturing a graph (the input planes may need a larger workspace).
+uint64_t tensor_bytes(int fmt, uint64_t rows, uint32_t K);
+int need_room(uint64_t p, uint64_t bytes, const char* op, const char* what);
 int op_matmul_glu(const Ctx& c, int fmt, const char* name) {
     if (int e = need_bufs(c, 5, name)) return e;
     const uint32_t N = c.U(0), K = c.U(1);
@@ -485,6 +487,9 @@ int op_matmul_glu(const Ctx& c, int fmt, const char* name) {
     const uint32_t tmax = c.gz * 32;
     if (tmax < 256) return fail(QP_E_ARG, "%s: for prompt chunks of 256 tokens or more (grid z %u)", name, c.gz);
     if (g_capturing && !g_noalloc) return fail(QP_E_CAPTURE, "%s: not while capturing a graph", name);
+    const uint64_t tb = tensor_bytes(fmt, N, K);
+    if (int e = need_room(c.B(1), tb, name, "the gate tensor's buffer")) return e;
+    if (int e = need_room(c.B(2), tb, name, "the up tensor's buffer")) return e;
     QpGemmArgs a = {};
     a.w = c.B(1);
     a.w2 = c.B(2);

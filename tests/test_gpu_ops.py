@@ -364,13 +364,17 @@ def test_matmul_swiglu_fused_equals_the_three_ops(quipu, dev, monkeypatch, fmt):
 
 
 def test_matmul_swiglu_fused_rejections(quipu, dev):
-    """Prompt chunks under 256 tokens (grid z < 8) and non-K-quant formats are refused with a message."""
+    """Prompt chunks under 256 tokens (grid z < 8) and weight buffers smaller than their tensors are refused with a
+    message (the op is registered for K-quants only: see the host test of the op table)."""
     N, K = 256, 256
     raw = raw_matrix(capi.Q4_K, N, K, 75)
     w = dev.matrix(capi.Q4_K, raw, N, K)
     bufs = [dev.paso(100, 0), w, w, dev.buf(np.zeros((100, K), np.float32)), dev.buf(np.zeros((100, N), np.float32))]
     with pytest.raises(capi.QuipuError, match="256 tokens"):
         quipu.dispatch("matmul_q4k_t_swiglu", [("u", N), ("u", K)], bufs, (4, 1, 4))
+    bufs[2] = dev.zeros(N * K // 256 * 144 - 16)  # an up tensor one chunk short
+    with pytest.raises(capi.QuipuError, match="up tensor"):
+        quipu.dispatch("matmul_q4k_t_swiglu", [("u", N), ("u", K)], bufs, (4, 1, 8))
 
 
 @pytest.mark.parametrize("T,N,K", [(256, 300, 4096), (700, 130, 1024)])
