@@ -367,6 +367,7 @@ int op_matmul_1(const Ctx& c, int fmt, const char* name) {
 // The library's scratch buffer for the prefill matmul (split input planes, split-K partials): grown on demand
 // (the stream is drained before the old one is freed) and kept until the process ends.  Not while capturing.
 uint64_t g_ws = 0, g_ws_bytes = 0;
+uint32_t g_ws_gen = 0;  // counts the workspace's reallocations
 int workspace(uint64_t bytes, uint64_t* out) {
     if (g_noalloc) {
         if (bytes > QP_SCRATCH_BYTES)
@@ -387,8 +388,29 @@ int workspace(uint64_t bytes, uint64_t* out) {
         HIPCHK(hipMalloc(&p, bytes), "hipMalloc (prefill workspace)");
         g_ws = (uint64_t)p;
         g_ws_bytes = bytes;
+        g_ws_gen++;
     }
     *out = g_ws;
+    return 0;
+}
+
+// The input split into bf16 planes for the matrix-core matmuls.  reuse (the caller's word: x and paso hold what the
+// previous prefill matmul in stream order read): the planes that matmul split are used again when they are still
+// there (the same x, paso, K, planes and workspace allocation), else x is split.
+struct SplitMemo {
+    uint64_t x, xs, paso;
+    uint32_t k, rows, gen;
+    bool valid;
+} g_split_memo = {};
+int split_input(uint64_t x, uint64_t xs, uint64_t paso, uint32_t K, uint32_t rows, uint32_t tmax, bool reuse) {
+    const SplitMemo& m = g_split_memo;
+    if (reuse && m.valid && m.x == x && m.xs == xs && m.paso == paso && m.k == K && m.rows == rows &&
+        m.gen == g_ws_gen)
+        return 0;
+    QpSplitArgs sa = {x, xs, paso, K, rows};
+    g_split_memo = {x, xs, paso, K, rows, g_ws_gen, false};
+    if (int e = launch(K_split_bf16, grid_cap((uint64_t)tmax * K / 8), 1, 1, 256, 0, sa)) return e;
+    g_split_memo.valid = true;
     return 0;
 }
 
@@ -445,8 +467,8 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
             if (int e = workspace(xs_bytes + ws_bytes, &ws)) return e;
             a.xs = ws;
             a.ws = ns > 1 ? ws + xs_bytes : 0;
-            QpSplitArgs sa = {a.x, a.xs, a.paso, K, a.rows};
-            if (int e = launch(K_split_bf16, grid_cap((uint64_t)tmax * K / 8), 1, 1, 256, 0, sa)) return e;
+            // P[4] = 1: reuse the previous matmul's input planes (see split_input)
+            if (int e = split_input(a.x, a.xs, a.paso, K, a.rows, tmax, c.U(4) == 1)) return e;
             if (wide) {
                 static const Kid kw_of[5] = {K_gemm_mfma256w_q4k, K_gemm_mfma256w_q5k, K_gemm_mfma256w_q6k,
                                              K_gemm_mfma256w_q3k, K_gemm_mfma256w_q2k};
@@ -504,8 +526,7 @@ int op_matmul_glu(const Ctx& c, int fmt, const char* name) {
     uint64_t ws = 0;
     if (int e = workspace(4ull * a.rows * K, &ws)) return e;
     a.xs = ws;
-    QpSplitArgs sa = {a.x, a.xs, a.paso, K, a.rows};
-    if (int e = launch(K_split_bf16, grid_cap((uint64_t)tmax * K / 8), 1, 1, 256, 0, sa)) return e;
+    if (int e = split_input(a.x, a.xs, a.paso, K, a.rows, tmax, false)) return e;
     static const Kid kg_of[5] = {K_gemm_glu_q4k, K_gemm_glu_q5k, K_gemm_glu_q6k, K_gemm_glu_q3k, K_gemm_glu_q2k};
     return launch(kg_of[kq_index(fmt)], nt, mt, 1, 512, 2 * (256 + 256 + 256 + 256) * 40 * 2, a);
 }

@@ -246,14 +246,18 @@ class ModeloTransformer {
   // ---------------------------------------------------------------- reference op sequence
   // matmul of the reference facade: one token -> matmul_<t>_1; T >= 8 with a K-quant and tiling -> _t; else _4
   // (transformer.js:268-284).
-  _mm(W, x, y, acc) {
+  // reusa: x is the input of the matmul dispatched just before (Q, K, V): the tiled form may reuse the bf16 planes
+  // that matmul split it into (P[4] = 1, an addition of this backend's; the reference's P has four words)
+  _mm(W, x, y, acc, reusa) {
     const gpu = this.gpu;
     const u = gpu.uniforme([['u', W.N], ['u', W.K], ['u', acc ? 1 : 0], ['u', 0]]);
     const wb = plano(W) ? [W.qs, W.ds] : [W.w];
     const b = [u, this.bPaso].concat(wb, [x, y]);
+    const bt = reusa && this.fusion ? [gpu.uniforme([['u', W.N], ['u', W.K], ['u', acc ? 1 : 0], ['u', 0], ['u', 1]]),
+      this.bPaso].concat(wb, [x, y]) : b;
     return {
       uno: gpu.grupo('matmul_' + W.tipo + '_1', b), lote: gpu.grupo('matmul_' + W.tipo + '_4', b),
-      baldosa: this.baldosa && KQ.has(W.tipo) ? gpu.grupo('matmul_' + W.tipo + '_t', b) : null, filas: W.N,
+      baldosa: this.baldosa && KQ.has(W.tipo) ? gpu.grupo('matmul_' + W.tipo + '_t', bt) : null, filas: W.N,
     };
   }
 
@@ -302,7 +306,8 @@ class ModeloTransformer {
       const gc = {
         attnNorm: gpu.grupo('rmsnorm', [uNorm, P, this.x, c.attnNorm, this.xn]),
         ffnNorm: gpu.grupo('rmsnorm', [uNorm, P, this.x, c.ffnNorm, this.xn]),
-        wq: this._mm(c.wq, this.xn, this.q, 0), wk: this._mm(c.wk, this.xn, this.k, 0), wv: this._mm(c.wv, this.xn, this.v, 0),
+        wq: this._mm(c.wq, this.xn, this.q, 0), wk: this._mm(c.wk, this.xn, this.k, 0, true),
+        wv: this._mm(c.wv, this.xn, this.v, 0, true),
         ropeQ: gpu.grupo('norm_rope', [ur(this.nh, !!c.qNorm), P, this.q, c.qNorm || dummy]),
         ropeK: gpu.grupo('norm_rope', [ur(this.nkv, !!c.kNorm), P, this.k, c.kNorm || dummy]),
         kvw: gpu.grupo('kv_write', [gpu.uniforme([['u', kvd], ['u', c.anillo], ['u', f16], ['u', c.slots]]), P, this.k, this.v,

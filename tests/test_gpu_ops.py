@@ -363,6 +363,37 @@ def test_matmul_swiglu_fused_equals_the_three_ops(quipu, dev, monkeypatch, fmt):
     assert np.array_equal(dev.get(y, (T, N)), dev.get(g, (T, N)))
 
 
+def test_matmul_reuses_the_split_input(quipu, dev):
+    """P[4] = 1 (Q, then K and V of the same input): the bf16 planes the previous matrix-core matmul split are used
+    again; results equal those of a fresh split.  With another input (x2), or after the workspace grew (a larger
+    call in between), the flag still splits, so the results stay right."""
+    T, K = 300, 1024
+    fm = capi.Q4_K
+    raws = [raw_matrix(fm, N, K, 80 + N) for N in (512, 256, 768)]
+    ws = [dev.matrix(fm, r, r.size * 256 // 144 // K, K) for r in raws]
+    x1, x2 = (dev.buf(np.random.default_rng(s).standard_normal((T, K)).astype(np.float32)) for s in (30, 31))
+    paso = dev.paso(T, 0)
+    grid = lambda N: ((N + 63) // 64, 1, (T + 31) // 32)
+
+    def mm(i, x, reuse):
+        N = (512, 256, 768)[i]
+        y = dev.zeros(T * N * 4)
+        u = [("u", N), ("u", K), ("u", 0), ("u", 0)] + ([("u", 1)] if reuse else [])
+        quipu.dispatch("matmul_q4k_t", u, [paso, ws[i], x, y], grid(N))
+        return dev.get(y, (T, N))
+
+    fresh = [mm(i, x1, False) for i in range(3)]
+    mm(0, x1, False)
+    assert np.array_equal(mm(1, x1, True), fresh[1]) and np.array_equal(mm(2, x1, True), fresh[2])
+    mm(0, x2, False)
+    assert np.array_equal(mm(1, x1, True), fresh[1])  # the planes hold x2: x1 is split again
+    big = dev.buf(np.zeros((2048, 4096), np.float32))  # a larger call reallocates the workspace
+    quipu.dispatch("matmul_q4k_t", [("u", 256), ("u", 4096), ("u", 0), ("u", 0)],
+                   [dev.paso(2048, 0), dev.matrix(fm, raw_matrix(fm, 256, 4096, 90), 256, 4096), big,
+                    dev.zeros(2048 * 256 * 4)], (4, 1, 64))
+    assert np.array_equal(mm(2, x1, True), fresh[2])
+
+
 def test_matmul_swiglu_fused_rejections(quipu, dev):
     """Prompt chunks under 256 tokens (grid z < 8) and weight buffers smaller than their tensors are refused with a
     message (the op is registered for K-quants only: see the host test of the op table)."""
