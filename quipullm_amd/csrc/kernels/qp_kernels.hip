@@ -3446,68 +3446,97 @@ DEC_ATTN_KERNELS(128, f16, true)
 DEC_ATTN_KERNELS(128, f32, false)
 
 // Causal attention of a prefill chunk on the matrix cores (f16 cache; no sliding window, no ring cap), the
-// reference atencion (gpu.js:467-539).  Wavefront w of workgroup (kvh, y) takes 16 rows: TPW = 16 / G tokens x the
-// G heads of KV head kvh (row r: token t0 + r / G, head r % G), and streams keys 0 .. pos0 + its last token in
-// tiles of 32 with the decode tile step (two tiles in flight), each row masked at its own causal limit.
-template <int HD, int G>
+// reference atencion (gpu.js:467-539).  Wavefront w of workgroup (kvh, y) takes RG groups of 16 rows: TPW = 16 RG / G
+// tokens x the G heads of KV head kvh (row r of group g: token t0 + (16 g + r) / G, head r % G), and streams keys
+// 0 .. pos0 + its last token in tiles of 32 with the decode tile step, each row masked at its own causal limit.
+// RG = 2: every tile loaded feeds both row groups (half the key and value loads per row; one tile in flight
+// instead of two, for the registers of the second group's query and accumulators).
+template <int HD, int G, int RG>
 QP_DEV void attn_mfma_body(const QpAttnArgs& a) {
-    constexpr uint32_t TPW = 16 / G;
+    constexpr uint32_t TPW = 16 * RG / G;
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t T = paso_T(a.paso), pos0 = paso_pos(a.paso);
     const uint32_t kvh = blockIdx.x, t0 = (blockIdx.y * 4 + wave) * TPW;
     if (t0 >= T) return;  // the whole wavefront (no barriers below)
     const uint32_t kvd = a.nkv * HD, r = lane & 15, qg = lane >> 4;
-    const uint32_t tr = t0 + r / G, hr = kvh * G + r % G;  // this lane's row
-    const bool row_ok = tr < T;
     const uint32_t tlast = min(t0 + TPW, T) - 1;
-    const uint32_t kend = min(pos0 + tlast + 1, a.rows);                      // keys this wavefront reads
-    const uint32_t kend_row = row_ok ? min(pos0 + tr + 1, a.rows) : 0u;       // keys this row attends to
+    const uint32_t kend = min(pos0 + tlast + 1, a.rows);  // keys this wavefront reads
     const __amdgpu_buffer_rsrc_t rk = kq_rsrc(a.kc, (uint64_t)a.rows * kvd * 2);
     const __amdgpu_buffer_rsrc_t rv = kq_rsrc(a.vc, (uint64_t)((a.rows + 31) / 32) * 32 * kvd * 2);
     MTile<HD> A, B;
     mt_load<HD>(A, rk, rv, kvd, kvh, 0, kend, lane);
-    mt_load<HD>(B, rk, rv, kvd, kvh, 32, kend, lane);
-    h8v qh[HD / 32], ql[HD / 32];
-    float qv[HD / 32][8];
-    const uint64_t qrow = a.q + 4ull * (((uint64_t)(row_ok ? tr : 0) * a.nh + hr) * HD);
+    if constexpr (RG == 1) mt_load<HD>(B, rk, rv, kvd, kvh, 32, kend, lane);
+    h8v qh[RG][HD / 32], ql[RG][HD / 32];
+    float qsc[RG], m[RG], l[RG];
+    uint32_t tr[RG], hr[RG], kend_row[RG], kend_grp[RG];
+    bool row_ok[RG];
+    f4v acc[RG][HD / 16];
 #pragma unroll
-    for (int c = 0; c < HD / 32; c++) {
-        const float4 x0 = gload<float4>(qrow + 4 * (32 * c + 8 * qg));
-        const float4 x1 = gload<float4>(qrow + 4 * (32 * c + 8 * qg + 4));
-        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    for (int g = 0; g < RG; g++) {
+        tr[g] = t0 + (16 * g + r) / G;  // this lane's row in group g
+        hr[g] = kvh * G + r % G;
+        row_ok[g] = tr[g] < T;
+        kend_row[g] = row_ok[g] ? min(pos0 + tr[g] + 1, a.rows) : 0u;  // keys this row attends to
+        // keys the group's last row attends to (uniform: a group past T reads none)
+        const uint32_t tg = t0 + (16 * g + 15) / G;
+        kend_grp[g] = t0 + (16 * g) / G < T ? min(pos0 + min(tg, T - 1) + 1, a.rows) : 0u;
+        float qv[HD / 32][8];
+        const uint64_t qrow = a.q + 4ull * (((uint64_t)(row_ok[g] ? tr[g] : 0) * a.nh + hr[g]) * HD);
 #pragma unroll
-        for (int j = 0; j < 8; j++) qv[c][j] = row_ok ? xv[j] : 0.0f;
+        for (int c = 0; c < HD / 32; c++) {
+            const float4 x0 = gload<float4>(qrow + 4 * (32 * c + 8 * qg));
+            const float4 x1 = gload<float4>(qrow + 4 * (32 * c + 8 * qg + 4));
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++) qv[c][jj] = row_ok[g] ? xv[jj] : 0.0f;
+        }
+        qsc[g] = a.scale * mt_split_q<HD>(qv, qh[g], ql[g], lane);
+        m[g] = -3.0e38f;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int mm = 0; mm < HD / 16; mm++) acc[g][mm] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    const float qsc = a.scale * mt_split_q<HD>(qv, qh, ql, lane);
-    float m = -3.0e38f, l = 0.0f;
-    f4v acc[HD / 16];
+    if constexpr (RG == 1) {
+        for (uint32_t t = 0; t < kend; t += 64) {
+            mt_consume<HD>(A, t, kend_row[0], 0xffffffffu, qh[0], ql[0], qsc[0], m[0], l[0], acc[0], lane);
+            mt_load<HD>(A, rk, rv, kvd, kvh, t + 64, kend, lane);
+            if (t + 32 < kend)
+                mt_consume<HD>(B, t + 32, kend_row[0], 0xffffffffu, qh[0], ql[0], qsc[0], m[0], l[0], acc[0], lane);
+            mt_load<HD>(B, rk, rv, kvd, kvh, t + 96, kend, lane);
+        }
+    } else {
+        for (uint32_t t = 0; t < kend; t += 32) {
 #pragma unroll
-    for (int mm = 0; mm < HD / 16; mm++) acc[mm] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t t = 0; t < kend; t += 64) {
-        mt_consume<HD>(A, t, kend_row, 0xffffffffu, qh, ql, qsc, m, l, acc, lane);
-        mt_load<HD>(A, rk, rv, kvd, kvh, t + 64, kend, lane);
-        if (t + 32 < kend) mt_consume<HD>(B, t + 32, kend_row, 0xffffffffu, qh, ql, qsc, m, l, acc, lane);
-        mt_load<HD>(B, rk, rv, kvd, kvh, t + 96, kend, lane);
+            for (int g = 0; g < RG; g++)
+                if (t < kend_grp[g])  // a group whose rows all stop before this tile skips it
+                    mt_consume<HD>(A, t, kend_row[g], 0xffffffffu, qh[g], ql[g], qsc[g], m[g], l[g], acc[g], lane);
+            mt_load<HD>(A, rk, rv, kvd, kvh, t + 32, kend, lane);
+        }
     }
-    float lt = l + bfly_f<4>(l, lane);
-    lt += bfly_f<5>(lt, lane);
-    if (row_ok) {
-        const uint64_t orow = a.o + 4ull * (((uint64_t)tr * a.nh + hr) * HD);
 #pragma unroll
-        for (int mm = 0; mm < HD / 16; mm++) {
-            float4 v;
-            v.x = lt > 0.0f ? acc[mm][0] / lt : 0.0f;
-            v.y = lt > 0.0f ? acc[mm][1] / lt : 0.0f;
-            v.z = lt > 0.0f ? acc[mm][2] / lt : 0.0f;
-            v.w = lt > 0.0f ? acc[mm][3] / lt : 0.0f;
-            gstore<float4>(orow + 4 * (16 * mm + 4 * qg), v);
+    for (int g = 0; g < RG; g++) {
+        float lt = l[g] + bfly_f<4>(l[g], lane);
+        lt += bfly_f<5>(lt, lane);
+        if (row_ok[g]) {
+            const uint64_t orow = a.o + 4ull * (((uint64_t)tr[g] * a.nh + hr[g]) * HD);
+#pragma unroll
+            for (int mm = 0; mm < HD / 16; mm++) {
+                float4 v;
+                v.x = lt > 0.0f ? acc[g][mm][0] / lt : 0.0f;
+                v.y = lt > 0.0f ? acc[g][mm][1] / lt : 0.0f;
+                v.z = lt > 0.0f ? acc[g][mm][2] / lt : 0.0f;
+                v.w = lt > 0.0f ? acc[g][mm][3] / lt : 0.0f;
+                gstore<float4>(orow + 4 * (16 * mm + 4 * qg), v);
+            }
         }
     }
 }
 
 #define ATTN_MFMA_KERNEL(HD, G)                                                                                   \
     KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qp_attn_mfma_h##HD##_g##G(        \
-        QpAttnArgs a) { attn_mfma_body<HD, G>(a); }
+        QpAttnArgs a) { attn_mfma_body<HD, G, 1>(a); }                                                            \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qp_attn_mfma2_h##HD##_g##G(       \
+        QpAttnArgs a) { attn_mfma_body<HD, G, 2>(a); }
 ATTN_MFMA_KERNEL(64, 1) ATTN_MFMA_KERNEL(64, 2) ATTN_MFMA_KERNEL(64, 4) ATTN_MFMA_KERNEL(64, 8)
 ATTN_MFMA_KERNEL(128, 1) ATTN_MFMA_KERNEL(128, 2) ATTN_MFMA_KERNEL(128, 4) ATTN_MFMA_KERNEL(128, 8)
 

@@ -671,12 +671,20 @@ int op_atencion(const Ctx& c) {
     a.o = c.B(4);
     const uint32_t G = a.nh / a.nkv;
     if (a.f16 && !a.swa && !a.cap && (G == 1 || G == 2 || G == 4 || G == 8) && !getenv_flag("QP_NO_MFMA")) {
-        // matrix-core path: a wavefront takes 16 / G tokens x G heads, a workgroup four wavefronts
+        // matrix-core path: a wavefront takes 16 rg / G tokens x G heads, a workgroup four wavefronts
         static const Kid km[2][4] = {{K_attn_mfma_h64_g1, K_attn_mfma_h64_g2, K_attn_mfma_h64_g4, K_attn_mfma_h64_g8},
                                      {K_attn_mfma_h128_g1, K_attn_mfma_h128_g2, K_attn_mfma_h128_g4,
                                       K_attn_mfma_h128_g8}};
+        static const Kid km2[2][4] = {{K_attn_mfma2_h64_g1, K_attn_mfma2_h64_g2, K_attn_mfma2_h64_g4,
+                                       K_attn_mfma2_h64_g8},
+                                      {K_attn_mfma2_h128_g1, K_attn_mfma2_h128_g2, K_attn_mfma2_h128_g4,
+                                       K_attn_mfma2_h128_g8}};
         const uint32_t gi = G == 1 ? 0 : G == 2 ? 1 : G == 4 ? 2 : 3;
-        return launch(km[a.hd == 128][gi], a.nkv, cdiv(c.gy ? c.gy : 1, 4 * (16 / G)), 1, 256, 0, a);
+        // two 16-row groups per wavefront sharing each key tile (measured: 8B prefill of 4096 tokens 201 -> 192 ms,
+        // MoE 176 -> 160 ms); QP_ATTN_RG1 keeps one group and two tiles in flight, for comparisons
+        const bool two = !getenv_flag("QP_ATTN_RG1");
+        const uint32_t rg = two ? 2 : 1;
+        return launch((two ? km2 : km)[a.hd == 128][gi], a.nkv, cdiv(c.gy ? c.gy : 1, 4 * (16 * rg / G)), 1, 256, 0, a);
     }
     const uint32_t qb = 32 / G;
     a.qb = qb;
