@@ -201,10 +201,11 @@ def side_configs(steps, warmup, eager):
     return out
 
 
-def parity_fixture(case="c3_ctx512"):
+def parity_fixture(case="c3_ctx512", eager=False):
     """The fused path against the CPU oracle's fixture of `case` (tests/golden/make_e2e.py): the same 8B model,
     prompt and greedy length, the reference's f32 KV cache.  Reports the ids, the largest relative logit error over
-    the fixture's per-step top-16 logits and its whole rows, and the smallest oracle top-1 / top-2 margin."""
+    the fixture's per-step top-16 logits and its whole rows, and the smallest oracle top-1 / top-2 margin.  eager:
+    the one-token step dispatched op by op (for profilers) instead of replaying its graph."""
     fp = os.path.join(ROOT, "tests", "golden", f"e2e_{case}.npz")
     if not os.path.exists(fp):
         return {"case": case, "error": "fixture missing"}
@@ -218,7 +219,7 @@ def parity_fixture(case="c3_ctx512"):
         json.dump(synth.random_prompt(c.vocab, P, int(fx["prompt_seed"])), f)
     cmd = ["node", os.path.join(ROOT, "quipullm_amd", "js", "cli.js"), "generate", "--model", path, "--prompt-file",
            pf, "--n", str(n), "--mode", "fast", "--kv", "f32", "--ctx", str(P + n + 8), "--batch", str(batch),
-           "--logits-out", lf]
+           "--logits-out", lf] + (["--eager"] if eager else [])
     log("bench: " + " ".join(cmd))
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     if r.returncode != 0:
@@ -282,7 +283,7 @@ def main():
     log("bench: cpu side baselines " + json.dumps(cpu_side))
     prefills = [4096, 2048, 512]
     dec = run_decode(MODEL, path, a.steps, a.warmup, prefills, a.decode_launch == "eager", sample=True)
-    check = parity_fixture()
+    check = parity_fixture(eager=a.decode_launch == "eager")
     runs = {r["prompt_tokens"]: r for r in dec["runs"]}
     log("bench: decode " + json.dumps(dec))
     log("bench: parity " + json.dumps(check))
