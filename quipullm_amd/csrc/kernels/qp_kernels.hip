@@ -932,9 +932,12 @@ struct KNoPro {
 };
 // NT: threads per workgroup (256, or 512 for the no-norm variant of long rows: one input staging shared by eight
 // wavefronts).  NORM: the fused RMSNorm prologue is compiled in.
-template <int FMT, int R, int XS, class SegAt, class Lay = KDense, class Pro = KNoPro, int NT = 256, bool NORM = true>
+// EXTRA: vector-memory loads pro() issues (counted in the wait for the input).  wgi / wgn: this workgroup's index
+// among the wgn that share the units (wgn = 0: the grid's x dimension).
+template <int FMT, int R, int XS, class SegAt, class Lay = KDense, class Pro = KNoPro, int NT = 256, bool NORM = true,
+          int EXTRA = 0>
 QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t x, uint64_t norm_w, float eps,
-                    uint32_t K, uint64_t amax, Lay lay = Lay(), Pro pro = Pro()) {
+                    uint32_t K, uint64_t amax, Lay lay = Lay(), Pro pro = Pro(), uint32_t wgi = 0, uint32_t wgn = 0) {
     extern __shared__ float4 xs[];
     float* xsum = reinterpret_cast<float*>(xs + (K >> 8) * 65);
     constexpr uint32_t nwv = NT / 64;
@@ -952,7 +955,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     while (nbp < nb) nbp <<= 1;
     const uint32_t S = 64 / nbp, s = lane / nbp, b = lane % nbp;
     const bool lane_on = b < nb;
-    const uint32_t W = gridDim.x * nwv, w = blockIdx.x * nwv + wave;
+    const uint32_t W = (wgn ? wgn : gridDim.x) * nwv, w = (wgn ? wgi : blockIdx.x) * nwv + wave;
     const uint32_t nmine = w < total_units ? (total_units - 1 - w) / W + 1 : 0;
     const uint32_t ngrp = K / KQ<FMT>::GROUP;
 
@@ -1022,7 +1025,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     __builtin_amdgcn_sched_barrier(0);
     {
         // the x loads are the oldest in flight: wait for them alone
-        constexpr int n = R * KQ<FMT>::LOADS > 63 ? 63 : R * KQ<FMT>::LOADS;
+        constexpr int n = R * KQ<FMT>::LOADS + EXTRA > 63 ? 63 : R * KQ<FMT>::LOADS + EXTRA;
         __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8));
     }
     tl_ph(TLK, 1);  // input arrived
@@ -3444,6 +3447,331 @@ DEC_ATTN_KERNELS(64, f16, true)
 DEC_ATTN_KERNELS(64, f32, false)
 DEC_ATTN_KERNELS(128, f16, true)
 DEC_ATTN_KERNELS(128, f32, false)
+
+// ------------------------------------------------------------------------ attention block of one decode token
+// dec_attn_block (QpDecBlockArgs documents the three phases).  Head group c = blockIdx.x runs on one XCD: the
+// workgroups of a launch are handed to the 8 XCDs round robin by linear id x + 8y, so the ns workgroups of column c
+// share one L2.  The group's barrier counter lives there (its adds and polls are atomics, executed in the L2), and
+// the stores a workgroup makes before a barrier are there once acknowledged; after the barrier they are read past
+// the CU's L1 (sc0 loads).  A group found on more than one XCD sets err (checked by the host), so the assumption
+// cannot fail silently.
+
+// this wavefront's vector-memory operations complete (stores acknowledged by the L2)
+QP_DEV void vm_drain() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xf << 8)); }
+
+QP_DEV uint32_t ld_sc0(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 1);
+}
+
+// Barrier of the ns workgroups of a group (ns a power of two).  Every barrier adds ns to the counter, so arrival
+// number n belongs to the barrier that completes when the counter reaches (n rounded down to ns) + ns, compared
+// modulo 2^32.  The polls are atomic adds of a zero the compiler cannot see (it would turn an add of a known 0
+// into a plain load, which may be served by a cache level the increments do not update): they execute where the
+// increments do.  Past spin_max polls the wait sets err bit 0 and stops, so every workgroup always ends.
+QP_DEV void group_barrier(uint64_t cnt, uint32_t ns, uint32_t spin_max, uint64_t err) {
+    vm_drain();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        QP_GLOBAL uint32_t* c = reinterpret_cast<QP_GLOBAL uint32_t*>(cnt);
+        const uint32_t n = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const uint32_t target = (n & ~(ns - 1)) + ns;
+        uint32_t zero;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+        for (uint32_t it = 0;; it++) {
+            const uint32_t v = __hip_atomic_fetch_add(c, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if ((int32_t)(v - target) >= 0) break;
+            if (it >= spin_max) {
+                __hip_atomic_fetch_or(reinterpret_cast<QP_GLOBAL uint32_t*>(err), 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __syncthreads();
+}
+
+template <int FQ, int HD, int GP>
+QP_DEV void dec_block_body_(const QpDecBlockArgs& a);
+template <int FQ, int HD, int GP>
+QP_DEV void dec_block_body(const QpDecBlockArgs& a) {
+    const uint64_t t0 = tl_now();
+    dec_block_body_<FQ, HD, GP>(a);
+    tl_rec(a.tseq, t0);
+}
+template <int FQ, int HD, int GP>
+QP_DEV void dec_block_body_(const QpDecBlockArgs& a) {
+    extern __shared__ float4 smem4[];
+    tl_ph(7, 0);
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t c = blockIdx.x, y = blockIdx.y, ns = a.ns;
+    const uint32_t r8 = 8 / a.nkv, kvh = c / r8, h0 = c * GP;
+    const bool app = c % r8 == 0;  // this group appends its KV head's new key and value
+    const uint64_t cnt = a.cnt + 256ull * c;
+    // the XCD of this workgroup; workgroup (c, 0) stores its XCD + 1 before the first barrier, and the others compare
+    // after it (the XCD a group lands on can change from launch to launch, the sharing within a launch cannot)
+    const uint32_t xid = (__builtin_amdgcn_s_getreg(20 | (15 << 11)) & 15u) + 1u;  // HW_REG_XCC_ID
+    if (tid == 0 && y == 0) gstore<uint32_t>(a.xcc + 4ull * c, xid);
+    const uint32_t pos0 = paso_pos(a.paso);
+    const uint32_t nk = pos0 < a.rows ? pos0 + 1 : 0;  // a position past the cache reads and writes nothing
+    // keys in whole tiles of 32: wavefront i of the group's W = 4 ns takes tiles [i nt / W, (i + 1) nt / W)
+    const uint32_t W = 4 * ns, nt = (nk + 31) / 32, wi = 4 * y + wave;
+    const uint32_t kw0 = min(nk, 32 * (wi * nt / W)), kw1 = min(nk, 32 * ((wi + 1) * nt / W));
+    const uint32_t g0 = min(nk, 32 * (4 * y * nt / W)), g1 = min(nk, 32 * ((4 * y + 4) * nt / W));
+    const bool wg_new = g0 <= pos0 && pos0 < g1;  // this workgroup's keys hold the new one
+    const uint32_t kvd = a.nkv * HD;
+    const uint64_t cbytes = (uint64_t)a.rows * kvd * 2;
+    const uint64_t vbytes = (uint64_t)((a.rows + 31) / 32) * 32 * kvd * 2;  // whole tiles
+    const __amdgpu_buffer_rsrc_t rk = kq_rsrc(a.kc, cbytes), rv = kq_rsrc(a.vc, vbytes);
+
+    // 1. the group's q rows and its KV head's k and v rows; each wavefront's first key/value tile loads meanwhile
+    MTile<HD> MA;
+    {
+        uint32_t nbp = 1;
+        while (nbp < (a.dm >> 8)) nbp <<= 1;
+        const uint32_t S = 64 / nbp, nq = GP * HD, uq = (nq + S - 1) / S, uk = (HD + S - 1) / S;
+        // segments q, k, v (field by field: selects, not a table in private memory)
+        auto seg_at = [&](uint32_t i) __attribute__((always_inline)) {
+            const bool s1 = i >= 1, s2 = i >= 2;
+            KSeg sg;
+            sg.w = s2 ? a.wv : s1 ? a.wk : a.wq;
+            sg.w2 = sg.w;
+            sg.y = s2 ? a.v + 4ull * kvh * HD : s1 ? a.k + 4ull * kvh * HD : a.q + 4ull * h0 * HD;
+            sg.n = s1 ? HD : nq;
+            sg.row_base = s1 ? kvh * HD : h0 * HD;
+            sg.rows_total = s1 ? kvd : a.nh * HD;
+            sg.mode = QP_GEMV_STORE;
+            sg.u0 = (s1 ? uq : 0u) + (s2 ? uk : 0u);
+            sg.fmt = s2 ? a.fv : s1 ? a.fk : a.fq;
+            return sg;
+        };
+        auto pro = [&]() __attribute__((always_inline)) { mt_load<HD>(MA, rk, rv, kvd, kvh, kw0, kw1, lane); };
+        kq_gemv<FQ, 1, 1, decltype(seg_at), KDense, decltype(pro), 256, true, HD / 8>(
+            seg_at, 3, uq + 2 * uk, a.x, a.norm_w, a.eps, a.dm, 0, KDense(), pro, y, ns);
+    }
+    tl_ph(7, 1);
+    group_barrier(cnt, ns, a.spin_max, a.err);
+    tl_ph(7, 2);
+    // (read past the L1, which has never held the line in this launch: the L1 is invalidated at each launch)
+    const uint32_t xseen = tid == 0 ? ld_sc0(kq_rsrc(a.xcc, 32), 4 * c) : xid;
+
+    // 2. attention of the group's GP query heads over keys [kw0, kw1) of this wavefront.  LDS (floats): kn [HD] |
+    // vn [HD] | RoPE sines, cosines [HD/2] each | q/k norm weights [HD] each | region R: q [GP][HD], then the
+    // wavefront partials wacc [4][GP][HD], wm [4][8], wl [4][8]
+    constexpr int QN = (GP * HD + 255) / 256;
+    float* kn = reinterpret_cast<float*>(smem4);
+    float* vn = kn + HD;
+    float* snt = vn + HD;
+    float* cst = snt + HD / 2;
+    float* qw = cst + HD / 2;
+    float* kw = qw + HD;
+    float* R = kw + HD;
+    float* qs = R;
+    float* wacc = R;
+    float* wm = R + 4 * GP * HD;
+    float* wl = wm + 32;
+    const __amdgpu_buffer_rsrc_t rq = kq_rsrc(a.q, 4ull * a.nh * HD);
+    const __amdgpu_buffer_rsrc_t rkn = kq_rsrc(a.k, 4ull * kvd), rvn = kq_rsrc(a.v, 4ull * kvd);
+    float qt[QN], knt = 0.0f, vnt = 0.0f, ft = 0.0f, qwt = 0.0f, kwt = 0.0f;
+#pragma unroll
+    for (int j = 0; j < QN; j++) {
+        const uint32_t i = tid + 256 * j;
+        qt[j] = i < GP * HD ? __uint_as_float(ld_sc0(rq, 4 * (h0 * HD + i))) : 0.0f;
+    }
+    if (wg_new && tid < HD) {
+        knt = __uint_as_float(ld_sc0(rkn, 4 * (kvh * HD + tid)));
+        vnt = __uint_as_float(ld_sc0(rvn, 4 * (kvh * HD + tid)));
+    }
+    if (a.freq && tid < a.nrot / 2) ft = gload<float>(a.freq + 4ull * tid);
+    if (a.qnorm && tid < HD) qwt = gload<float>(a.qnorm + 4ull * tid);
+    if (a.knorm && wg_new && tid < HD) kwt = gload<float>(a.knorm + 4ull * tid);
+    const float pos_esc = (float)pos0 * a.esc;
+    if (tid < a.nrot / 2) {
+        const float fr = a.freq ? ft : (float)pow((double)a.base, (double)((-2.0f * (float)tid) / (float)a.nrot));
+        float sn, cs;
+        sincos2(pos_esc * fr, sn, cs);
+        snt[tid] = sn;
+        cst[tid] = cs;
+    }
+#pragma unroll
+    for (int j = 0; j < QN; j++) {
+        const uint32_t i = tid + 256 * j;
+        if (i < GP * HD) qs[i] = qt[j];
+    }
+    if (wg_new && tid < HD) {
+        kn[tid] = knt;
+        vn[tid] = vnt;
+    }
+    if (tid < HD) {
+        qw[tid] = qwt;
+        kw[tid] = kwt;
+    }
+    __syncthreads();
+    for (uint32_t g = wave; g < GP + (wg_new ? 1u : 0u); g += 4) {
+        if (g < GP)
+            wave_norm_rope_t(qs + g * HD, qw, HD, a.qnorm != 0, a.eps, snt, cst, a.nrot, a.neox != 0, (int)lane);
+        else
+            wave_norm_rope_t(kn, kw, HD, a.knorm != 0, a.eps, snt, cst, a.nrot, a.neox != 0, (int)lane);
+    }
+    __syncthreads();
+    if (wg_new && tid < HD) {
+        // the new key and value as the f16 cache will hold them
+        kn[tid] = h2f(f2h(kn[tid]));
+        vn[tid] = h2f(f2h(vn[tid]));
+    }
+    __syncthreads();
+    {
+        const uint32_t hr = lane & 15, qg = lane >> 4;
+        h8v qh[HD / 32], ql[HD / 32];
+        float qv[HD / 32][8];
+#pragma unroll
+        for (int j = 0; j < HD / 32; j++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) qv[j][e] = hr < GP ? qs[hr * HD + 32 * j + 8 * qg + e] : 0.0f;
+        const float qsc = a.scale * mt_split_q<HD>(qv, qh, ql, lane);
+        __syncthreads();  // every wavefront holds its q before region R is reused
+        tl_ph(7, 3);
+        float m = -3.0e38f, l = 0.0f;
+        f4v acc[HD / 16];
+#pragma unroll
+        for (int mm = 0; mm < HD / 16; mm++) acc[mm] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t t = kw0; t < kw1; t += 32) {
+            mt_consume<HD>(MA, t, kw1, pos0, qh, ql, qsc, m, l, acc, lane);
+            if (t + 32 < kw1) mt_load<HD>(MA, rk, rv, kvd, kvh, t + 32, kw1, lane);
+        }
+        if (kw0 <= pos0 && pos0 < kw1) {
+            // the new key, from kn / vn (the cache slot is written at the end)
+#pragma clang fp contract(off)
+            float d = 0.0f;
+#pragma unroll
+            for (int j = 0; j < HD / 32; j++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) d = fmaf((float)qh[j][e] + (float)ql[j][e], kn[32 * j + 8 * qg + e], d);
+            d += bfly_f<4>(d, lane);
+            d += bfly_f<5>(d, lane);
+            const float sn = d * qsc;
+            const float mn = fmaxf(m, sn);
+            const float cf = __builtin_amdgcn_exp2f((m - mn) * QP_LOG2E);
+            const float p = __builtin_amdgcn_exp2f(fminf(sn - mn, 0.0f) * QP_LOG2E) * QP_PSCALE;
+            m = mn;
+            l = l * cf + (qg == 0 ? p : 0.0f);
+#pragma unroll
+            for (int mm = 0; mm < HD / 16; mm++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[mm][i] = fmaf(p, vn[16 * mm + 4 * qg + i], acc[mm][i] * cf);
+        }
+        float lt = l + bfly_f<4>(l, lane);
+        lt += bfly_f<5>(lt, lane);
+        if (hr < GP) {
+#pragma unroll
+            for (int mm = 0; mm < HD / 16; mm++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) wacc[(wave * GP + hr) * HD + 16 * mm + 4 * qg + i] = acc[mm][i];
+            if (qg == 0) {
+                wm[wave * 8 + hr] = m;
+                wl[wave * 8 + hr] = lt;
+            }
+        }
+    }
+    __syncthreads();
+    // this workgroup's partial per head: merge of its 4 wavefronts, four dimensions per thread
+    for (uint32_t t = tid; t < GP * (HD / 4); t += 256) {
+        const uint32_t g = t / (HD / 4), d = (t % (HD / 4)) * 4;
+        float M = -3.0e38f;
+        for (int w = 0; w < 4; w++)
+            if (wl[w * 8 + g] > 0.0f) M = fmaxf(M, wm[w * 8 + g]);
+        float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+        float L = 0.0f;
+        for (int w = 0; w < 4; w++)
+            if (wl[w * 8 + g] > 0.0f) {
+                const float f = __builtin_amdgcn_exp2f((wm[w * 8 + g] - M) * QP_LOG2E);
+                const float4 cc = *reinterpret_cast<const float4*>(wacc + (w * GP + g) * HD + d);
+                o.x = fmaf(f, cc.x, o.x);
+                o.y = fmaf(f, cc.y, o.y);
+                o.z = fmaf(f, cc.z, o.z);
+                o.w = fmaf(f, cc.w, o.w);
+                L = fmaf(f, wl[w * 8 + g], L);
+            }
+        const uint64_t i = (uint64_t)(h0 + g) * ns + y;
+        gstore<float4>(a.part_o + 4 * (i * HD + d), o);
+        if (d == 0) gstore<float2>(a.part_ml + 8 * i, make_float2(M, L));
+    }
+    if (app && wg_new && tid < HD) {
+        // append the new key and value at slot pos0 (f16-rounded in kn / vn)
+        const uint64_t o = (uint64_t)pos0 * kvd + (uint64_t)kvh * HD + tid;
+        gstore<uint16_t>(a.kc + 2 * o, f2h(kn[tid]));
+        gstore<uint16_t>(a.vc + 2 * vt_index(pos0, kvd, kvh * HD + tid), f2h(vn[tid]));
+    }
+    tl_ph(7, 4);
+    group_barrier(cnt, ns, a.spin_max, a.err);
+    tl_ph(7, 5);
+
+    // 3. the split merge (log-sum-exp weights; a split without keys has l = 0 and weight 0; no key at all gives 0):
+    // workgroup y writes outputs [y cs, (y + 1) cs) of the group's GP * HD (the host keeps ns <= GP * HD).  The
+    // partials of those outputs are loaded with the (m, l) pairs, one (split, output) pair per thread, so the merge
+    // waits for one round of loads; the products go through LDS and are summed in split order.
+    {
+        const uint32_t cs = GP * HD / ns;
+        float* eb = R;                       // [GP][ns] weights
+        float* lb = R + GP * ns;             // [GP] denominators
+        float* pb = R + GP * ns + 8;         // [ns][cs] weighted partials
+        const __amdgpu_buffer_rsrc_t rml = kq_rsrc(a.part_ml, 8ull * a.nh * ns);
+        const __amdgpu_buffer_rsrc_t rpo = kq_rsrc(a.part_o, 4ull * a.nh * ns * HD);
+        constexpr uint32_t NPV = (GP * HD + 255) / 256;  // (split, output) pairs per thread
+        float pv[NPV];
+#pragma unroll
+        for (uint32_t j = 0; j < NPV; j++) {
+            const uint32_t t = tid + 256 * j, sp = t / cs, i = y * cs + t % cs;
+            pv[j] = t < GP * HD ? __uint_as_float(ld_sc0(rpo, 4 * (((h0 + i / HD) * ns + sp) * HD + i % HD))) : 0.0f;
+        }
+        for (uint32_t g = wave; g < (uint32_t)GP; g += 4) {
+            const uint32_t h = h0 + g;
+            float mv = -3.0e38f, lv = 0.0f;
+            if (lane < ns) {
+                const u32x2 r = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * (h * ns + lane), 0, 1);
+                mv = __uint_as_float(r.x);
+                lv = __uint_as_float(r.y);
+            }
+            const float mx = wave_max(lv > 0.0f ? mv : -3.0e38f);
+            const float e = lv > 0.0f ? expf(mv - mx) : 0.0f;
+            if (lane < ns) eb[g * ns + lane] = e;
+            const float ls = wave_sum(lv * e);
+            if (lane == 0) lb[g] = ls;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t j = 0; j < NPV; j++) {
+            const uint32_t t = tid + 256 * j, sp = t / cs, i = y * cs + t % cs;
+            if (t < GP * HD) pb[t] = eb[(i / HD) * ns + sp] * pv[j];
+        }
+        __syncthreads();
+        for (uint32_t t = tid; t < cs; t += 256) {
+            const uint32_t i = y * cs + t, g = i / HD, h = h0 + g;
+            float o = 0.0f;
+            for (uint32_t sp = 0; sp < ns; sp++) o += pb[sp * cs + t];
+            const float L = lb[g];
+            gstore<float>(a.att + 4ull * (h * HD + i % HD), L > 0.0f ? o / L : 0.0f);
+        }
+    }
+    tl_ph(7, 6);
+    if (tid == 0 && xseen != xid)
+        __hip_atomic_fetch_or(reinterpret_cast<QP_GLOBAL uint32_t*>(a.err), 2u, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+}
+
+#define DEC_BLOCK_KERNEL(NAME, FQ, HD, GP)                                                                        \
+    KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qp_dec_block_##NAME##_h##HD##_g##GP( \
+        QpDecBlockArgs a) { dec_block_body<FQ, HD, GP>(a); }
+DEC_BLOCK_KERNEL(q4k, QP_Q4_K, 128, 1)
+DEC_BLOCK_KERNEL(q4k, QP_Q4_K, 128, 2)
+DEC_BLOCK_KERNEL(q4k, QP_Q4_K, 128, 4)
+DEC_BLOCK_KERNEL(mix, QP_KQ_MIX, 128, 1)
+DEC_BLOCK_KERNEL(mix, QP_KQ_MIX, 128, 2)
+DEC_BLOCK_KERNEL(mix, QP_KQ_MIX, 128, 4)
+DEC_BLOCK_KERNEL(q4k, QP_Q4_K, 64, 1)
+DEC_BLOCK_KERNEL(q4k, QP_Q4_K, 64, 4)
+DEC_BLOCK_KERNEL(mix, QP_KQ_MIX, 64, 1)
+DEC_BLOCK_KERNEL(mix, QP_KQ_MIX, 64, 4)
 
 // Causal attention of a prefill chunk on the matrix cores (f16 cache; no sliding window, no ring cap), the
 // reference atencion (gpu.js:467-539).  Wavefront w of workgroup (kvh, y) takes RG groups of 16 rows: TPW = 16 RG / G

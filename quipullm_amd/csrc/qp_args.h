@@ -162,6 +162,34 @@ typedef struct {
     uint32_t hd, nh, nsplit, tseq;
 } QpDecCombArgs;
 
+// The attention block of one decode token in one launch (dec_attn_block; no reference counterpart: the reference
+// dispatches rmsnorm, matmul q/k/v, norm_rope, kv_write, atencion and matmul wo): grid (8, ns).  The 8 columns
+// are head groups, one per XCD: group c takes KV head c / (8 / nkv) and its gq = nh / 8 query heads starting at
+// c * gq.  Its ns workgroups
+//   1. compute the group's q rows and its KV head's k and v rows of W . (rmsnorm(x) * norm_w) (K = dm; the K/V
+//      rows are computed by every group of the KV head), while the first key/value tile of each wavefront loads;
+//   2. meet at a barrier of the group (a counter in the XCD's L2), then run the split-K attention of the group's
+//      query heads over the cache with the fused q/k norm, RoPE and KV append (groups with c % (8 / nkv) == 0
+//      append), storing the split partials;
+//   3. meet again, then either (wo == 0) merge the partials into att [nh][hd], a slice per workgroup, or (wo != 0)
+//      each merges the group's gq * hd outputs in LDS and computes rows [y * dm / ns, ...) of the group's column
+//      slice of wo: xpart[c][r] = sum over the group's columns of wo[r][col] * att[col] (Q4_K wo; the consumer
+//      adds x + xpart[0] + ... + xpart[7], in that order).
+// cnt: 8 counters 256 bytes apart that only this op touches, zero at allocation (each barrier adds ns to its
+// group's counter; ns is a power of two).  err: a word set non-zero when a barrier's wait runs past spin_max
+// polls (bit 0) or a workgroup found itself on another XCD than its group's first (bit 1; xcc: 8 words, the XCD
+// + 1 of workgroup (c, 0) in the last launch).
+typedef struct {
+    uint64_t x, norm_w, wq, wk, wv, q, k, v;
+    uint64_t kc, vc, paso, qnorm, knorm, part_o, part_ml, freq, att;
+    uint64_t wo, xpart, cnt, xcc, err;
+    uint32_t fq, fk, fv, dm;     // formats of wq, wk, wv (QP_Q4_K / QP_Q6_K); model width
+    uint32_t hd, nh, nkv, ns;    // ns: workgroups per group (power of two, <= 64)
+    float scale, eps, base, esc;
+    uint32_t nrot, neox, rows, tseq;
+    uint32_t spin_max, fo, pad[2];
+} QpDecBlockArgs;
+
 // Greedy argmax finish: reads the packed max, writes ids[0] and tokens[step], clears the max, advances
 // paso.pos0 by T and the step counter.
 // cap: entries of `tokens`; steps at or past it are not recorded

@@ -99,6 +99,7 @@ template <class A> void tl_tag(A&, uint32_t) {}
 void tl_tag(QpGemvArgs& a, uint32_t v) { a.tseq = v; }
 void tl_tag(QpDecAttnArgs& a, uint32_t v) { a.tseq = v; }
 void tl_tag(QpDecCombArgs& a, uint32_t v) { a.tseq = v; }
+void tl_tag(QpDecBlockArgs& a, uint32_t v) { a.tseq = v; }
 void tl_tag(QpArgmaxFinArgs& a, uint32_t v) { a.tseq = v; }
 void tl_tag(QpEmbedArgs& a, uint32_t v) { a.tseq = v; }
 void tl_tag(QpMoeArgs& a, uint32_t v) { a.tseq = v; }
@@ -1014,6 +1015,105 @@ int op_dec_attn(const Ctx& c) {
     return launch(k, merged ? 8 : a.nkv, a.nsplit, 1, 256, lds, a);
 }
 
+// dec_attn_block: the attention block of one decode token in one launch (QpDecBlockArgs): Q/K/V GEMV with the
+// fused RMSNorm, split-K attention with q/k norm, RoPE and the KV append, and the split merge into att.
+// P{hd, nh, nkv, ns, scale, eps, base, esc, nrot, neox, rows, dm, fq, fk, fv, spin_max};
+// [paso, x, norm_w, wq, wk, wv, q, k, v, kc, vc (f16 cache), qnorm|0, knorm|0, part_o, part_ml, freq|0, att, sync].
+// sync: a library buffer of at least 2116 bytes, zero at allocation, used by this op only (group counters 256
+// bytes apart, then the 8 groups' XCD words at 2048, the error word at 2112).  ns: workgroups per head group (a power of two,
+// at most 64, at most nh / 8 * hd and two per CU of an XCD); spin_max 0: the default bound on a barrier's polls.
+int op_dec_attn_block(const Ctx& c) {
+    if (int e = need_bufs(c, 18, "dec_attn_block")) return e;
+    QpDecBlockArgs a = {};
+    a.hd = c.U(0);
+    a.nh = c.U(1);
+    a.nkv = c.U(2);
+    a.ns = c.U(3);
+    a.scale = c.F(4);
+    a.eps = c.F(5);
+    a.base = c.F(6);
+    a.esc = c.U(7) ? c.F(7) : 1.0f;
+    a.nrot = c.U(8);
+    a.neox = c.U(9);
+    a.rows = c.U(10);
+    a.dm = c.U(11);
+    a.fq = c.U(12);
+    a.fk = c.U(13);
+    a.fv = c.U(14);
+    a.spin_max = c.U(15) ? c.U(15) : (1u << 18);
+    const char* op = "dec_attn_block";
+    if (!a.rows) return fail(QP_E_ARG, "%s: P.rows (cache slots) is 0", op);
+    if (a.hd != 64 && a.hd != 128) return fail(QP_E_ARG, "%s: head_dim %u (64 or 128)", op, a.hd);
+    if (a.nrot > a.hd || a.nrot % 2) return fail(QP_E_ARG, "%s: nrot=%u", op, a.nrot);
+    if (!(a.nkv == 1 || a.nkv == 2 || a.nkv == 4 || a.nkv == 8) || a.nh % 8 || a.nh % a.nkv)
+        return fail(QP_E_ARG, "%s: nh=%u nkv=%u (nkv 1, 2, 4 or 8; nh a multiple of 8)", op, a.nh, a.nkv);
+    const uint32_t GP = a.nh / 8;
+    if (!(GP == 1 || GP == 4 || (GP == 2 && a.hd == 128)))
+        return fail(QP_E_ARG, "%s: %u query heads per group of head_dim %u (1, 2 or 4; 1 or 4 at 64)", op, GP, a.hd);
+    const uint32_t per_xcd = g_cus >= 8 ? (uint32_t)g_cus / 8 : 1;
+    if (a.ns == 0 || (a.ns & (a.ns - 1)) || a.ns > 64 || a.ns > GP * a.hd || a.ns > 2 * per_xcd)
+        return fail(QP_E_ARG, "%s: ns=%u (a power of two, at most 64, %u and two per CU of an XCD)", op, a.ns,
+                    GP * a.hd);
+    if (a.dm == 0 || a.dm % 256 || a.dm > 8192) return fail(QP_E_ARG, "%s: model width %u (a multiple of 256, at most 8192)", op, a.dm);
+    for (uint32_t f : {a.fq, a.fk, a.fv})
+        if (f != QP_Q4_K && f != QP_Q6_K) return fail(QP_E_ARG, "%s: Q/K/V format %u (Q4_K 12 or Q6_K 14)", op, f);
+    a.paso = c.B(0);
+    a.x = c.B(1);
+    a.norm_w = c.B(2);
+    a.wq = c.B(3);
+    a.wk = c.B(4);
+    a.wv = c.B(5);
+    a.q = c.B(6);
+    a.k = c.B(7);
+    a.v = c.B(8);
+    a.kc = c.B(9);
+    a.vc = c.B(10);
+    a.qnorm = c.B(11);
+    a.knorm = c.B(12);
+    a.part_o = c.B(13);
+    a.part_ml = c.B(14);
+    a.freq = c.B(15);
+    a.att = c.B(16);
+    const uint64_t sync = c.B(17);
+    if (!a.x || !a.norm_w || !a.wq || !a.wk || !a.wv || !a.q || !a.k || !a.v || !a.kc || !a.vc || !a.part_o ||
+        !a.part_ml || !a.att || !sync)
+        return fail(QP_E_ARG, "%s: a required binding is missing", op);
+    if (buf_room(sync) < 2116) return fail(QP_E_ARG, "%s: sync must be a library buffer of at least 2116 bytes", op);
+    a.cnt = sync;
+    a.xcc = sync + 2048;
+    a.err = sync + 2112;
+    const uint32_t kvd = a.nkv * a.hd;
+    struct Need { uint64_t p, n; const char* what; } need[] = {
+        {a.wq, kq_tensor_bytes((int)a.fq, (uint64_t)a.nh * a.hd, a.dm), "wq"},
+        {a.wk, kq_tensor_bytes((int)a.fk, kvd, a.dm), "wk"},
+        {a.wv, kq_tensor_bytes((int)a.fv, kvd, a.dm), "wv"},
+        {a.x, 4ull * a.dm, "x"}, {a.norm_w, 4ull * a.dm, "norm_w"},
+        {a.q, 4ull * a.nh * a.hd, "q"}, {a.k, 4ull * kvd, "k"}, {a.v, 4ull * kvd, "v"},
+        {a.kc, 2ull * a.rows * kvd, "the K cache"}, {a.vc, 2ull * ((a.rows + 31) / 32) * 32 * kvd, "the V cache"},
+        {a.part_o, 4ull * a.nh * a.ns * a.hd, "part_o"}, {a.part_ml, 8ull * a.nh * a.ns, "part_ml"},
+        {a.att, 4ull * a.nh * a.hd, "att"}};
+    for (const Need& n : need)
+        if (int e = need_room(n.p, n.n, op, n.what)) return e;
+    const bool mix = a.fq != QP_Q4_K || a.fk != QP_Q4_K || a.fv != QP_Q4_K;
+    Kid k;
+    if (a.hd == 128) {
+        static const Kid t[2][3] = {{K_dec_block_q4k_h128_g1, K_dec_block_q4k_h128_g2, K_dec_block_q4k_h128_g4},
+                                    {K_dec_block_mix_h128_g1, K_dec_block_mix_h128_g2, K_dec_block_mix_h128_g4}};
+        k = t[mix][GP == 1 ? 0 : GP == 2 ? 1 : 2];
+    } else {
+        static const Kid t[2][2] = {{K_dec_block_q4k_h64_g1, K_dec_block_q4k_h64_g4},
+                                    {K_dec_block_mix_h64_g1, K_dec_block_mix_h64_g4}};
+        k = t[mix][GP == 1 ? 0 : 1];
+    }
+    // LDS: the GEMV's input staging; the attention's floats (5 hd + the wavefront partials 4 GP hd + 64); the
+    // merge's weights, denominators and weighted partials (GP ns + 8 + GP hd)
+    const uint32_t att_lds = 4 * (a.hd * 5 + 4 * GP * a.hd + 64), mrg_lds = 4 * (a.hd * 5 + GP * a.ns + 8 + GP * a.hd);
+    uint32_t lds = kq_lds(a.dm);
+    if (att_lds > lds) lds = att_lds;
+    if (mrg_lds > lds) lds = mrg_lds;
+    return launch(k, 8, a.ns, 1, 256, lds, a);
+}
+
 // dec_attn_comb: P{hd, nh, nsplit}; [paso, part_o, part_ml, o].
 int op_dec_attn_comb(const Ctx& c) {
     if (int e = need_bufs(c, 4, "dec_attn_comb")) return e;
@@ -1218,6 +1318,7 @@ void register_ops() {
     v.push_back({"gemv", op_gemv});
     v.push_back({"dec_attn", op_dec_attn});
     v.push_back({"dec_attn_comb", op_dec_attn_comb});
+    v.push_back({"dec_attn_block", op_dec_attn_block});
     v.push_back({"argmax", op_argmax});
     v.push_back({"argmax_fin", op_argmax_fin});
     v.push_back({"penalizar", op_penalizar});

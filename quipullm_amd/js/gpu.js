@@ -52,7 +52,7 @@ class GPU {
     const i = JSON.parse(this.n.info());
     this.info = {
       summary: 'AMD ' + i.arch + ' (' + i.cus + ' CUs, ' + (i.hbm_bytes / 1e9).toFixed(0) + ' GB)',
-      maxBuffer: i.max_buffer, maxBufferSize: i.max_buffer, vendor: 'amd', arquitectura: i.arch,
+      maxBuffer: i.max_buffer, maxBufferSize: i.max_buffer, vendor: 'amd', arquitectura: i.arch, cus: i.cus,
     };
     this.pipelines = {};
     this.perdido = false;

@@ -100,6 +100,12 @@ class ModeloTransformer {
     // 8B decode 449 -> 455 tok/s; with 8 heads per group the merge on one workgroup costs more than the launch it
     // saves, MoE 400 -> 396); false: the separate merge
     this.atencionUnida = op.merged_attention !== false && this.nkv <= 8 && this.nh / this.nkv <= 4;
+    // one-token step: each layer's Q/K/V GEMV, attention, KV append and split merge as one launch (dec_attn_block,
+    // eight head groups on the eight XCDs meeting at barriers in their L2) where the layer fits it (_bloqueAtt).
+    // Off unless asked: measured no faster than the separate launches (8B at ctx 4096 450 against 455 tok/s, MoE
+    // at ctx 2048 398 against 397): the chain of dependent memory round trips is as long with barriers as with
+    // launch boundaries.
+    this.bloqueAtt = op.attn_block === true;
     this.bufs = [];
     this.pos = 0;
     this.grafo = null;
@@ -224,6 +230,16 @@ class ModeloTransformer {
     this.partML = B(8 * this.nh * this.nsplit, 'attn_part_ml');
     this.attCnt = B(8 * 128, 'attn_counters');   // the merged attention's arrival counters (kept at zero by it)
     gpu.escribir(this.attCnt, 0, new Uint8Array(8 * 128));
+    // dec_attn_block: 64 workgroups per head group (two per CU of an XCD: every wavefront then has at most one
+    // unit of the Q/K/V GEMV), their partials, and the op's sync words (barrier counters, XCD words, error word),
+    // zero at allocation and touched by that op only
+    const cusXcd = Math.max(1, Math.floor((gpu.info.cus || 256) / 8));
+    this.nsBloque = 1;
+    while (this.nsBloque * 2 <= Math.min(64, 2 * cusXcd, (this.nh / 8) * this.hd)) this.nsBloque *= 2;
+    this.partOB = B(4 * this.nh * this.nsBloque * this.hd, 'block_part_o');
+    this.partMLB = B(8 * this.nh * this.nsBloque, 'block_part_ml');
+    this.syncBloque = B(2304, 'block_sync');
+    gpu.escribir(this.syncBloque, 0, new Uint8Array(2304));
     this.ropeFreq = B(4 * Math.max(1, this.nrot / 2), 'rope_freq');
     gpu.escribir(this.ropeFreq, 0, tablaRope(this.base, this.nrot));
     this.amax = B(8 * AMAX_WG, 'argmax_partials');
@@ -489,6 +505,29 @@ class ModeloTransformer {
       this.D <= 16384 && this.nUsados * this.ffe <= 16384 && this.ffe % 256 === 0 && this.D % 256 === 0;
   }
 
+  // Whether dec_attn_block takes layer c: f16 cache, Q4_K q and k with Q4_K or Q6_K v, head_dim 64 or 128, 1, 2,
+  // 4 or 8 KV heads and a multiple of 8 query heads (1, 2 or 4 per head group; 1 or 4 at head_dim 64), a model
+  // width the GEMV stages whole (a multiple of 256, at most 8192).
+  _bloqueAtt(c) {
+    const gp = this.nh / 8;
+    return this.bloqueAtt && this.kvF16 && c.wq.tipo === 'q4k' && c.wk.tipo === 'q4k' &&
+      (c.wv.tipo === 'q4k' || c.wv.tipo === 'q6k') && (this.hd === 64 || this.hd === 128) &&
+      [1, 2, 4, 8].indexOf(this.nkv) >= 0 && this.nh % 8 === 0 &&
+      (gp === 1 || gp === 4 || (gp === 2 && this.hd === 128)) && this.D % 256 === 0 && this.D <= 8192;
+  }
+
+  // The error word of dec_attn_block (a barrier wait past its bound, or a head group seen on two XCDs): the
+  // decode results are then invalid.
+  _comprobarBloque() {
+    if (!this.usaBloque) return;
+    const e = new Uint32Array(1);
+    this.gpu.leer(this.syncBloque, 2112, e);
+    if (e[0]) {
+      throw new Error('dec_attn_block: ' + ((e[0] & 1) ? 'a barrier wait ran past its bound; ' : '') +
+        ((e[0] & 2) ? 'a head group ran on more than one XCD; ' : '') + 'the decode results are invalid');
+    }
+  }
+
   _armarDecode() {
     const gpu = this.gpu, P = this.bPaso, D = this.D, qd = this.nh * this.hd, self = this;
     const plan = [];
@@ -499,8 +538,17 @@ class ModeloTransformer {
     const uAttM = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', this.nsplit], ['f', this.escAtt],
       ['f', this.eps], ['f', this.base], ['u', 0], ['u', this.nrot], ['u', this.neox], ['u', this.kvF16 ? 1 : 0], ['u', this.ctx],
       ['u', 1]]);
+    this.usaBloque = false;
     for (let i = 0; i < this.capas.length; i++) {
       const c = this.capas[i], gc = this.G.capas[i];
+      if (this._bloqueAtt(c)) {
+        this.usaBloque = true;
+        const uB = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', this.nsBloque], ['f', this.escAtt],
+          ['f', this.eps], ['f', this.base], ['u', 0], ['u', this.nrot], ['u', this.neox], ['u', this.ctx], ['u', D],
+          ['u', FMT_ID[c.wq.tipo]], ['u', FMT_ID[c.wk.tipo]], ['u', FMT_ID[c.wv.tipo]], ['u', 0]]);
+        plan.push([gpu.grupo('dec_attn_block', [uB, P, this.x, c.attnNorm, c.wq.w, c.wk.w, c.wv.w, this.q, this.k, this.v,
+          c.kc, c.vc, c.qNorm, c.kNorm, this.partOB, this.partMLB, this.ropeFreq, this.att, this.syncBloque]), 1]);
+      } else {
       for (const g of this._gemvPorFormato([{ W: c.wq, mode: STORE, y: this.q }, { W: c.wk, mode: STORE, y: this.k },
         { W: c.wv, mode: STORE, y: this.v }], this.x, c.attnNorm, D)) plan.push([g, 1]);
       if (this.atencionUnida) {
@@ -510,6 +558,7 @@ class ModeloTransformer {
         plan.push([gpu.grupo('dec_attn', [uAtt, P, this.q, this.k, this.v, c.kc, c.vc, c.qNorm, c.kNorm, this.partO, this.partML,
           this.ropeFreq]), 1]);
         plan.push([gpu.grupo('dec_attn_comb', [uComb, P, this.partO, this.partML, this.att]), 1]);
+      }
       }
       plan.push([this._gemv([{ W: c.wo, mode: ACC, y: this.x }], this.att, null, qd), 1]);
       if (this.nExp && this._moeFusionable(c)) {
@@ -622,6 +671,7 @@ class ModeloTransformer {
     }
     const out = new Uint32Array(n);
     gpu.leer(this.tokens, 0, out);
+    this._comprobarBloque();
     this.pos += n;
     this.hist.push(primero);                                    // the n processed ids: primero and out[0..n-2]
     for (let i = 0; i + 1 < n; i++) this.hist.push(out[i]);
@@ -644,6 +694,7 @@ class ModeloTransformer {
     gpu.escribir(this.bPaso, 0, new Uint32Array([1, this.pos, 0, 0]));
     gpu.escribir(this.bIds, 0, new Uint32Array([id]));
     this._pasos(1);
+    this._comprobarBloque();
     this.pos += 1;
     this.hist.push(id);
     const lg = new Float32Array(this.vocab);

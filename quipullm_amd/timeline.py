@@ -33,6 +33,7 @@ PHASE_KINDS = {
     4: ("gemv, Q6_K", ["input arrived", "input staged", "first unit's weights", "all units"]),
     5: ("gemv, other formats", ["input arrived", "input staged", "first unit's weights", "all units"]),
     6: ("decode attention", ["q,k,v loaded", "norm+RoPE", "q split", "key stream", "wave merge", "end"]),
+    7: ("attention block", ["Q/K/V GEMV", "barrier 1", "q split", "partials stored", "barrier 2", "merged"]),
 }
 
 

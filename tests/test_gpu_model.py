@@ -139,6 +139,26 @@ def test_greedy_matches_oracle(oracle, models_dir, tmp_path, name, kv):
         assert r["pos"] == len(prompt) + n - 1
 
 
+@pytest.mark.parametrize("name", ["mini_llama_q4km_c", "mini_qwen3_q4km_c", "mini_qwen3moe_q4k_c"])
+def test_attention_block_matches_oracle(oracle, models_dir, tmp_path, name):
+    """The fused one-token step with dec_attn_block (--attn-block: Q/K/V, attention and the split merge of each
+    layer in one launch) against the oracle as above (f16 cache, the oracle given the GPU's cache rows): ids
+    identical, logits within 1e-3 relative at every step."""
+    path = synth.ensure_model(name, models_dir)
+    vocab = oracle.GGUF(path).tensors["token_embd.weight"]["dims"][1]
+    prompt = synth.random_prompt(vocab, 40, 1)
+    n = 24
+    kvf = os.path.join(str(tmp_path), "kv.bin")
+    r, lg = generate(path, prompt, n, "fast", "f16", str(tmp_path), extra=("--attn-block",), kv_out=kvf)
+    lg = lg.reshape(-1, vocab)
+    c = synth.CONFIGS[name]
+    ref = read_kv_f16(kvf, c.n_layers, 256, c.nkv * c.hd, len(prompt) + n - 1)
+    want_ids, want_lg = oracle_run(oracle, path, prompt, n, True, ref)
+    errs = [rel(a, b) for a, b in zip(lg, want_lg)]
+    assert r["ids"] == want_ids, (r["ids"], want_ids, errs)
+    assert max(errs) < 1e-3, errs
+
+
 def test_f16_cache_rows_are_the_rounded_values(oracle, models_dir, tmp_path):
     """The GPU's f16 cache rows of layer 0 (computed from the embeddings only, before any f16 cache value is
     used) are the f16 roundings of the oracle's float32 K and V of that layer: every element within one f16 step

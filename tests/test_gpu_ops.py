@@ -999,6 +999,105 @@ def test_dec_attn_merged(quipu, dev, hd, nh, nkv, pos0, nsplit, f16, neox, qk_no
     np.testing.assert_array_equal(kg, kw)
 
 
+@pytest.mark.parametrize("hd,nh,nkv,D,fv,pos0,ns,neox,qk_norm",
+                         [(128, 32, 8, 4096, capi.Q6_K, 4095, 64, 0, 0), (128, 32, 4, 2048, capi.Q4_K, 2047, 64, 1, 1),
+                          (128, 32, 8, 4096, capi.Q6_K, 2000, 32, 0, 0),
+                          (128, 8, 2, 512, capi.Q6_K, 300, 16, 1, 1), (64, 8, 2, 512, capi.Q6_K, 100, 8, 0, 0),
+                          (128, 16, 8, 1024, capi.Q4_K, 31, 4, 0, 1), (64, 32, 8, 1024, capi.Q6_K, 5, 64, 1, 0),
+                          (128, 32, 8, 4096, capi.Q6_K, 0, 32, 0, 0), (64, 8, 1, 256, capi.Q4_K, 700, 2, 0, 0)])
+def test_dec_attn_block(quipu, dev, hd, nh, nkv, D, fv, pos0, ns, neox, qk_norm):
+    """dec_attn_block (Q/K/V GEMV with the fused norm, attention, KV append and the split merge in one launch, the
+    8 head groups on the 8 XCDs meeting at barriers in their L2) against the three launches it replaces: gemv (Q,
+    K Q4_K and V in one launch) + dec_attn + dec_attn_comb on the same inputs.  q, k, v and the appended cache row
+    are bit-identical; the merged output (other split boundaries) within 5e-5.  Three launches in a row (the
+    barrier counters only grow) give identical outputs, and no barrier timeout or group spread over two XCDs is
+    recorded."""
+    rows = 4100
+    kvd = nkv * hd
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal(D).astype(np.float32)
+    nw = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32)
+    kc = f16r(rng.standard_normal((rows, kvd)).astype(np.float32))
+    vc = f16r(rng.standard_normal((rows, kvd)).astype(np.float32))
+    qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    eps, base = 1e-6, 1e6
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    mats = [(capi.Q4_K, nh * hd, 90), (capi.Q4_K, kvd, 91), (fv, kvd, 92)]
+    W = [dev.matrix(f, raw_matrix(f, n, D, sd), n, D) for f, n, sd in mats]
+    xb, nwb, paso = dev.buf(x), dev.buf(nw), dev.paso(1, pos0)
+    qnb, knb = (dev.buf(qn), dev.buf(kn)) if qk_norm else (0, 0)
+    freq = dev.buf(rope_table(base, hd))
+
+    def fresh():
+        return (dev.buf(kc.astype(np.float16)), dev.buf(refs.v_tiled(vc.astype(np.float16), kvd)),
+                dev.zeros(nh * hd * 4), dev.zeros(kvd * 4), dev.zeros(kvd * 4), dev.zeros(nh * hd * 4))
+
+    # the three launches
+    kcb, vcb, q, k, v, o = fresh()
+    segs = [(capi.STORE, nh * hd, 0, nh * hd, capi.Q4_K), (capi.STORE, kvd, 0, kvd, capi.Q4_K),
+            (capi.STORE, kvd, 0, kvd, fv)]
+    quipu.dispatch("gemv", capi.gemv_uniform(3, D, eps=eps, fmt=capi.Q4_K, segs=segs),
+                   [paso, xb, nwb, 0, W[0], 0, q, W[1], 0, k, W[2], 0, v])
+    nsp = 17
+    po, pml = dev.zeros(nh * nsp * hd * 4), dev.zeros(nh * nsp * 8)
+    ua = [("u", hd), ("u", nh), ("u", nkv), ("u", nsp), ("f", scale), ("f", eps), ("f", base), ("u", 0),
+          ("u", hd), ("u", neox), ("u", 1), ("u", rows)]
+    quipu.dispatch("dec_attn", ua, [paso, q, k, v, kcb, vcb, qnb, knb, po, pml, freq])
+    quipu.dispatch("dec_attn_comb", [("u", hd), ("u", nh), ("u", nsp)], [paso, po, pml, o])
+    want = [dev.get(t, (n,)) for t, n in ((q, nh * hd), (k, kvd), (v, kvd), (o, nh * hd))]
+    want_k = dev.get(kcb, (rows, kvd), np.float16)
+    want_v = dev.get(vcb, ((rows + 31) // 32 * 32, kvd), np.float16)
+
+    # the one launch
+    kcb, vcb, q, k, v, o = fresh()
+    po, pml, sync = dev.zeros(nh * ns * hd * 4), dev.zeros(nh * ns * 8), dev.zeros(2304)
+    ub = [("u", hd), ("u", nh), ("u", nkv), ("u", ns), ("f", scale), ("f", eps), ("f", base), ("u", 0), ("u", hd),
+          ("u", neox), ("u", rows), ("u", D), ("u", capi.Q4_K), ("u", capi.Q4_K), ("u", fv), ("u", 0)]
+    outs = []
+    for it in range(3):
+        if it:  # the same token again: restore the cache row the launch appended
+            quipu.upload(kcb, kc.astype(np.float16))
+            quipu.upload(vcb, refs.v_tiled(vc.astype(np.float16), kvd))
+        quipu.upload(o, np.full(nh * hd, np.nan, np.float32))
+        quipu.dispatch("dec_attn_block", ub, [paso, xb, nwb, W[0], W[1], W[2], q, k, v, kcb, vcb, qnb, knb, po, pml,
+                                              freq, o, sync], (8, ns, 1))
+        outs.append(dev.get(o, (nh * hd,)))
+        if it == 0:
+            for t, n, w_ in zip((q, k, v), (nh * hd, kvd, kvd), want):
+                np.testing.assert_array_equal(dev.get(t, (n,)), w_)
+            np.testing.assert_array_equal(dev.get(kcb, (rows, kvd), np.float16), want_k)
+            np.testing.assert_array_equal(dev.get(vcb, ((rows + 31) // 32 * 32, kvd), np.float16), want_v)
+    sw = dev.get(sync, (576,), np.uint32)
+    bad = np.abs(outs[0] - want[3]) > 5e-5 + 5e-5 * np.abs(want[3])
+    print("error word %#x, XCD words %s, counters %s, mismatches per head %s, per launch %s" % (
+        sw[528], [hex(m) for m in sw[512:520]], sw[0:512:64].tolist(),
+        bad.reshape(nh, hd).sum(axis=1).tolist(), [int((np.abs(o_ - want[3]) > 1e-3).sum()) for o_ in outs]))
+    np.testing.assert_allclose(outs[0], want[3], rtol=5e-5, atol=5e-5)
+    for o_ in outs[1:]:
+        np.testing.assert_array_equal(o_, outs[0])
+    assert sw[528] == 0, "barrier timeout or a group on two XCDs (error word %#x)" % sw[528]
+    xw = sw[512:520]
+    assert len(set(xw.tolist())) == 8 and all(1 <= w <= 16 for w in xw)  # each group on an XCD of its own
+    # each group's counter: 2 barriers x ns arrivals per launch
+    assert np.all(sw[0:512:64] == 3 * 2 * ns)
+
+
+def test_dec_attn_block_rejections(quipu, dev):
+    """Shapes the kernel cannot take are refused on the host before any launch."""
+    base = [("u", 128), ("u", 32), ("u", 8), ("u", 32), ("f", 0.1), ("f", 1e-5), ("f", 1e4), ("u", 0), ("u", 128),
+            ("u", 0), ("u", 64), ("u", 4096), ("u", capi.Q4_K), ("u", capi.Q4_K), ("u", capi.Q6_K), ("u", 0)]
+    bufs = [dev.zeros(64) for _ in range(18)]
+    for i, v, msg in [(3, 24, "ns=24"), (3, 128, "ns=128"), (2, 16, "nkv 1, 2, 4 or 8"), (0, 96, "head_dim 96"),
+                      (11, 4000, "model width 4000"), (14, capi.Q8_0, "Q/K/V format"), (1, 64, "query heads per group")]:
+        u = list(base)
+        u[i] = ("u", v)
+        with pytest.raises(capi.QuipuError, match=msg):
+            quipu.dispatch("dec_attn_block", u, bufs, (8, 32, 1))
+    with pytest.raises(capi.QuipuError, match="sync must be"):
+        quipu.dispatch("dec_attn_block", base, bufs, (8, 32, 1))
+
+
 def test_dec_attn_merged_rejections(quipu, dev):
     """The merged form needs at most 8 KV heads, the output and a counter buffer of this library."""
     hd, nh, nkv, rows = 64, 16, 16, 64
