@@ -88,6 +88,10 @@ QP_DEV float wave_sum_v(float v, uint32_t lane) {
     return v + bfly_f<5>(v, lane);
 }
 
+// This wavefront's vector-memory operations complete: loads returned, stores acknowledged by the L2 (what another
+// CU of the XCD reads after a barrier needs; a workgroup-scope release fence does not wait for it).
+QP_DEV void vm_drain() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xf << 8)); }
+
 // Paso in device memory: {T, pos0, a, b}
 QP_DEV uint32_t paso_T(uint64_t p) { return cptr<uint32_t>(p)[0]; }
 QP_DEV uint32_t paso_pos(uint64_t p) { return cptr<uint32_t>(p)[1]; }

@@ -608,6 +608,11 @@ QP_DEV __amdgpu_buffer_rsrc_t kq_rsrc(uint64_t base, uint64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
 }
 
+// A 32-bit load past the CU's L1 (sc0): data another CU of the XCD stored before a barrier, never read here before.
+QP_DEV uint32_t ld_sc0(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 1);
+}
+
 // Bytes of LDS the K-quant GEMV uses for a K-wide input (staged x + group sums + reduction slots).
 QP_DEV uint32_t kq_lds_offset_sum(uint32_t K) { return (K >> 8) * 65 * 16; }
 
@@ -1229,25 +1234,28 @@ QP_DEV void kq_gemv_exp(const QpGemvExpArgs& a) {
 // router logits, kused rounds of strict maximum over the probabilities (ties to the lower expert index), weights =
 // chosen probabilities times scale, divided by their running sum (at least 2^-14) when norm.  Lane i < kused
 // returns slot i's expert and weight.
-QP_DEV void moe_route(const QpMoeArgs& a, uint32_t lane, uint32_t& sel, float& wt) {
+// ld(e) returns logit e.
+template <class Ld>
+QP_DEV void moe_route_(uint32_t E, uint32_t kused, float scale, uint32_t norm, Ld ld, uint32_t lane, uint32_t& sel,
+                       float& wt) {
     float p[4];
     float m = -3.0e38f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const uint32_t e = lane + 64 * j;
-        p[j] = e < a.e ? gload<float>(a.logits + 4ull * e) : -3.0e38f;
+        p[j] = e < E ? ld(e) : -3.0e38f;
         m = fmaxf(m, p[j]);
     }
     m = wave_max_v(m, lane);
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        p[j] = lane + 64 * j < a.e ? expf(p[j] - m) : 0.0f;
+        p[j] = lane + 64 * j < E ? expf(p[j] - m) : 0.0f;
         s += p[j];
     }
     s = wave_sum_v(s, lane);
 #pragma unroll
-    for (int j = 0; j < 4; j++) p[j] = lane + 64 * j < a.e ? p[j] / s : -3.0f;  // -3: below every candidate
+    for (int j = 0; j < 4; j++) p[j] = lane + 64 * j < E ? p[j] / s : -3.0f;  // -3: below every candidate
     float tot = 0.0f;
     sel = 0;
     wt = 0.0f;
@@ -1259,7 +1267,7 @@ QP_DEV void moe_route(const QpMoeArgs& a, uint32_t lane, uint32_t& sel, float& w
         bv = take ? ov : bv;
         bi = take ? oi : bi;
     };
-    for (uint32_t i = 0; i < a.kused; i++) {
+    for (uint32_t i = 0; i < kused; i++) {
         float bv = -1.0f;
         uint32_t bi = 0xffffffffu;
 #pragma unroll
@@ -1284,9 +1292,14 @@ QP_DEV void moe_route(const QpMoeArgs& a, uint32_t lane, uint32_t& sel, float& w
         }
         tot = tot + bv;
     }
-    float f = a.scale;
-    if (a.norm) f = f / fmaxf(tot, 6.103515625e-5f);
+    float f = scale;
+    if (norm) f = f / fmaxf(tot, 6.103515625e-5f);
     wt = wt * f;
+}
+
+QP_DEV void moe_route(const QpMoeArgs& a, uint32_t lane, uint32_t& sel, float& wt) {
+    moe_route_(a.e, a.kused, a.scale, a.norm, [&](uint32_t e) { return gload<float>(a.logits + 4ull * e); }, lane, sel,
+               wt);
 }
 
 template <int FMT, int XS>
@@ -1302,9 +1315,11 @@ QP_DEV void moe_gate_up_body_(const QpMoeArgs& a) {
     const uint32_t lane = threadIdx.x & 63, job = blockIdx.y;
     uint32_t sel = 0, ex = 0;
     float wt = 0.0f;
-    // the routing runs while the input loads are in flight; the job's expert decides its weight rows
+    // the routing runs (or, with presel, the chosen experts load) while the input loads are in flight; the job's
+    // expert decides its weight rows
     auto route = [&]() __attribute__((always_inline)) {
-        moe_route(a, lane, sel, wt);
+        if (a.presel) sel = lane < a.kused ? gload<uint32_t>(a.sel + 4ull * lane) : 0u;
+        else moe_route(a, lane, sel, wt);
         ex = (uint32_t)__builtin_amdgcn_readlane((int)sel, (int)job);
         if (ex >= a.e) ex = a.e - 1;
     };
@@ -1317,11 +1332,97 @@ QP_DEV void moe_gate_up_body_(const QpMoeArgs& a) {
                         (uint32_t)FMT};
         },
         1, units, a.x, a.norm_w, a.eps, a.k, 0, KDense(), route);
-    if (blockIdx.x == 0 && job == 0 && threadIdx.x < a.kused) {
+    if (!a.presel && blockIdx.x == 0 && job == 0 && threadIdx.x < a.kused) {
         gstore<uint32_t>(a.sel + 4ull * lane, sel);
         gstore<float>(a.wts + 4ull * lane, wt);
     }
 }
+
+// ------------------------------------------------------------------------ router logits + routing (moe_router)
+// Column 0 of the grid works: its nw workgroups share one XCD (workgroups go to the 8 XCDs round robin by linear id
+// x + 8y), so the arrival counter and the logits live in one L2.  Wavefront i of the column takes rows i, i + 4 nw,
+// ...: its first row's weights load before the input is staged.  The last workgroup to arrive reads the logits back
+// past its L1 and routes.
+QP_DEV void moe_router_body_(const QpRouterArgs& a);
+QP_DEV void moe_router_body(const QpRouterArgs& a) {
+    const uint64_t t0 = tl_now();
+    moe_router_body_(a);
+    tl_rec(a.tseq, t0);
+}
+QP_DEV void moe_router_body_(const QpRouterArgs& a) {
+    if (blockIdx.x != 0) return;
+    extern __shared__ float4 xs4[];  // k floats: x * norm_w
+    __shared__ float red[4];
+    __shared__ uint32_t last;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t nf4 = a.k >> 2, W = 4 * a.nw, r0 = blockIdx.y * 4 + wave;
+    constexpr int NP = 8;  // float4 of a row per lane held in flight (k <= 2048; longer rows loop)
+    const __amdgpu_buffer_rsrc_t rw = kq_rsrc(a.w, 4ull * a.e * a.k);
+    float4 wv[NP];
+    auto issue = [&](uint32_t r, uint32_t q0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const uint32_t q = q0 + lane + 64 * i;
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+                rw, r < a.e && q < nf4 ? (r * nf4 + q) * 16 : 0x80000000u, 0, 0);
+            wv[i] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                                __uint_as_float(v[3]));
+        }
+    };
+    issue(r0, 0);
+    float ss = 0.0f;
+    for (uint32_t q = tid; q < nf4; q += 256) {
+        float4 v = gload<float4>(a.x + 16ull * q);
+        if (a.norm_w) {
+            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+            const float4 nw = gload<float4>(a.norm_w + 16ull * q);
+            v.x *= nw.x;
+            v.y *= nw.y;
+            v.z *= nw.z;
+            v.w *= nw.w;
+        }
+        xs4[q] = v;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    const float inv = a.norm_w ? 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)a.k + a.eps) : 1.0f;
+    for (uint32_t r = r0; r < a.e; r += W) {
+        float s = 0.0f;
+        for (uint32_t q0 = 0; q0 < nf4; q0 += 64 * NP) {
+            if (r != r0 || q0 != 0) issue(r, q0);
+#pragma unroll
+            for (int i = 0; i < NP; i++) {
+                const uint32_t q = q0 + lane + 64 * i;
+                if (q < nf4) {
+                    const float4 xv = xs4[q];
+                    s += (wv[i].x * xv.x + wv[i].y * xv.y) + (wv[i].z * xv.z + wv[i].w * xv.w);
+                }
+            }
+        }
+        s = wave_sum(s) * inv;
+        if (lane == 0) gstore<float>(a.logits + 4ull * r, s);
+    }
+    vm_drain();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t n = __hip_atomic_fetch_add(reinterpret_cast<QP_GLOBAL uint32_t*>(a.cnt), 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
+        last = ((n + 1) & (a.nw - 1)) == 0;
+    }
+    __syncthreads();
+    if (!last || wave != 0) return;
+    const __amdgpu_buffer_rsrc_t rl = kq_rsrc(a.logits, 4ull * a.e);
+    uint32_t sel = 0;
+    float wt = 0.0f;
+    moe_route_(a.e, a.kused, a.scale, a.norm, [&](uint32_t e) { return __uint_as_float(ld_sc0(rl, 4 * e)); }, lane,
+               sel, wt);
+    if (lane < a.kused) {
+        gstore<uint32_t>(a.sel + 4ull * lane, sel);
+        gstore<float>(a.wts + 4ull * lane, wt);
+    }
+}
+KERNEL __launch_bounds__(256) void qp_moe_router(QpRouterArgs a) { moe_router_body(a); }
 
 // moe_down's gathered layout: x block b (of kused * nbwv) is block b % nbwv of row r of expert sel[b / nbwv], and
 // the input sub-blocks of slot j are scaled by wts[j].  Lane j < kused of every wavefront holds sel[j], wts[j].
@@ -3376,9 +3477,10 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
         // 6. the last of the head's workgroups to finish merges its G heads (the dec_attn_comb computation).  With
         // the grid's x = 8, workgroup (x, y) has linear id x + 8y, and workgroups are handed to the 8 XCDs round
         // robin by that id: all workgroups of KV head x run on one XCD and share its L2, where the counter's atomic
-        // add executes and the partial stores land once they are complete (workgroup-scope release: the stores
-        // have been acknowledged).  The merge reads them past this CU's L1.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        // add executes and the partial stores land once acknowledged: every wavefront waits for that (a
+        // workgroup-scope release fence does not) before the barrier that precedes the add.  The merge reads them
+        // past this CU's L1.
+        vm_drain();
         __syncthreads();
         __shared__ uint32_t last;
         if (tid == 0) {
@@ -3455,13 +3557,6 @@ DEC_ATTN_KERNELS(128, f32, false)
 // the stores a workgroup makes before a barrier are there once acknowledged; after the barrier they are read past
 // the CU's L1 (sc0 loads).  A group found on more than one XCD sets err (checked by the host), so the assumption
 // cannot fail silently.
-
-// this wavefront's vector-memory operations complete (stores acknowledged by the L2)
-QP_DEV void vm_drain() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xf << 8)); }
-
-QP_DEV uint32_t ld_sc0(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 1);
-}
 
 // Barrier of the ns workgroups of a group (ns a power of two).  Every barrier adds ns to the counter, so arrival
 // number n belongs to the barrier that completes when the counter reaches (n rounded down to ns) + ns, compared

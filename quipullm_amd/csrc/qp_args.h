@@ -85,7 +85,21 @@ typedef struct {
     uint32_t n, k, e, kused;
     float eps, scale;
     uint32_t norm, tseq;
+    uint32_t presel, pad[3];  // gate/up: 1 = the routing is read from sel (written by moe_router), not computed
 } QpMoeArgs;
+
+// moe_router (no reference counterpart; the reference runs rmsnorm, matmul_f32 and moe_topk): the router logits
+// logits[e] = W[e] . (rmsnorm(x) * norm_w) of one token (W f32 [e][k]) and, in the last of its workgroups to
+// finish, the routing of moe_topk (kds.js:191-221) into sel[kused], wts[kused].  Grid (8, nw): only column 0
+// works (its nw workgroups share one XCD, whose L2 holds the arrival counter cnt and the logits they store); the
+// other columns exit at once.  cnt: a word only this op touches, zero at allocation (grows by nw per launch; nw is
+// a power of two).
+typedef struct {
+    uint64_t w, x, norm_w, logits, sel, wts, cnt;
+    uint32_t e, k, kused, nw;
+    float eps, scale;
+    uint32_t norm, tseq;
+} QpRouterArgs;
 
 // Multi-token GEMV for prefill (reference matmul_*_4 / matmul_*_t semantics): y[t][r] (+)= W[r].x[t].
 typedef struct {

@@ -103,6 +103,7 @@ void tl_tag(QpDecBlockArgs& a, uint32_t v) { a.tseq = v; }
 void tl_tag(QpArgmaxFinArgs& a, uint32_t v) { a.tseq = v; }
 void tl_tag(QpEmbedArgs& a, uint32_t v) { a.tseq = v; }
 void tl_tag(QpMoeArgs& a, uint32_t v) { a.tseq = v; }
+void tl_tag(QpRouterArgs& a, uint32_t v) { a.tseq = v; }
 #endif
 
 template <class A>
@@ -791,7 +792,48 @@ int op_moe(const Ctx& c, int fmt, bool down, const char* name) {
     a.y = c.B(6);
     a.sel = c.B(7);
     a.wts = c.B(8);
+    a.presel = c.U(7);  // P[7] = 1: sel holds the routing (moe_router), the logits are not read
     return launch(kg[q6][x2], cdiv(units, 4), a.kused, 1, 256, kq_lds(K), a);
+}
+
+// moe_router: P{e, k, kused, nw, eps, scale, norm}; [paso, w (f32 [e][k]), x, norm_w|0, logits, sel, wts, cnt].
+// The router GEMV of one token with the fused RMSNorm and the routing in one launch (QpRouterArgs); cnt: a library
+// buffer of at least 4 bytes, zero at allocation, used by this op only.
+uint64_t buf_room(uint64_t p);
+int op_moe_router(const Ctx& c) {
+    if (int e = need_bufs(c, 8, "moe_router")) return e;
+    QpRouterArgs a = {};
+    a.e = c.U(0);
+    a.k = c.U(1);
+    a.kused = c.U(2);
+    a.nw = c.U(3);
+    a.eps = c.F(4);
+    a.scale = c.F(5);
+    a.norm = c.U(6);
+    if (a.e == 0 || a.e > 256) return fail(QP_E_ARG, "moe_router: %u experts (1..256)", a.e);
+    if (a.kused == 0 || a.kused > a.e || a.kused > 64)
+        return fail(QP_E_ARG, "moe_router: %u experts used of %u", a.kused, a.e);
+    if (a.k == 0 || a.k % 4 || a.k > 16384) return fail(QP_E_ARG, "moe_router: k=%u (a multiple of 4, at most 16384)", a.k);
+    const uint32_t per_xcd = g_cus >= 8 ? (uint32_t)g_cus / 8 : 1;
+    if (a.nw == 0 || (a.nw & (a.nw - 1)) || a.nw > 2 * per_xcd)
+        return fail(QP_E_ARG, "moe_router: nw=%u (a power of two, at most two per CU of an XCD)", a.nw);
+    a.w = c.B(1);
+    a.x = c.B(2);
+    a.norm_w = c.B(3);
+    a.logits = c.B(4);
+    a.sel = c.B(5);
+    a.wts = c.B(6);
+    a.cnt = c.B(7);
+    if (!a.w || !a.x || !a.logits || !a.sel || !a.wts || !a.cnt)
+        return fail(QP_E_ARG, "moe_router: a required binding is missing");
+    if (buf_room(a.cnt) < 4) return fail(QP_E_ARG, "moe_router: cnt must be a library buffer");
+    struct Need { uint64_t p, n; const char* what; } need[] = {
+        {a.w, 4ull * a.e * a.k, "the router weights"}, {a.x, 4ull * a.k, "x"}, {a.norm_w, 4ull * a.k, "norm_w"},
+        {a.logits, 4ull * a.e, "logits"}, {a.sel, 4ull * a.kused, "sel"}, {a.wts, 4ull * a.kused, "wts"}};
+    for (const Need& n : need)
+        if (n.p)
+            if (int e = need_room(n.p, n.n, "moe_router", n.what)) return e;
+    return launch(K_moe_router, 8, a.nw, 1, 256, 4 * a.k, a);
 }
 
 // moe_comb (kds.js:224-240): P{D, k}; [paso, x, de, wts].
@@ -1319,6 +1361,7 @@ void register_ops() {
     v.push_back({"dec_attn", op_dec_attn});
     v.push_back({"dec_attn_comb", op_dec_attn_comb});
     v.push_back({"dec_attn_block", op_dec_attn_block});
+    v.push_back({"moe_router", op_moe_router});
     v.push_back({"argmax", op_argmax});
     v.push_back({"argmax_fin", op_argmax_fin});
     v.push_back({"penalizar", op_penalizar});

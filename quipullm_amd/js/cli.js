@@ -7,7 +7,7 @@
 //                        [--temperature T] [--top-k K] [--top-p P] [--min-p M] [--seed S]
 //   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
 //                        [--warmup W] [--prefill P1,P2] [--eager] [--sample] [--keys-per-split N]
-//                        [--no-moe-grouped] [--no-fused-ffn] [--no-merged-attention] [--attn-block]
+//                        [--no-moe-grouped] [--no-fused-ffn] [--no-merged-attention] [--attn-block] [--no-moe-router]
 //   node cli.js motor    --servidor http://127.0.0.1:PORT [--id ID] [--kv f16] [--batch N]   (the server's engine)
 //                        [--check-prompt-file ids.json --check-n N --check-logits file.f32]
 //
@@ -47,6 +47,7 @@ async function cargar(o) {
   if (o['no-fused-ffn'] || o.mode === 'ref') options.fused_ffn = false;
   if (o['no-merged-attention']) options.merged_attention = false;
   if (o['attn-block']) options.attn_block = true;
+  if (o['no-moe-router']) options.moe_router = false;
   return engine.cargarModelo(o.model, { ctx: o.ctx ? parseInt(o.ctx, 10) : undefined, options: options });
 }
 

@@ -106,6 +106,9 @@ class ModeloTransformer {
     // at ctx 2048 398 against 397): the chain of dependent memory round trips is as long with barriers as with
     // launch boundaries.
     this.bloqueAtt = op.attn_block === true;
+    // one-token MoE step: the router GEMV and the routing in one launch (moe_router; f32 routers); false: the router
+    // GEMV, with the routing computed by every workgroup of the gate/up kernel
+    this.enrutador = op.moe_router !== false;
     this.bufs = [];
     this.pos = 0;
     this.grafo = null;
@@ -240,6 +243,14 @@ class ModeloTransformer {
     this.partMLB = B(8 * this.nh * this.nsBloque, 'block_part_ml');
     this.syncBloque = B(2304, 'block_sync');
     gpu.escribir(this.syncBloque, 0, new Uint8Array(2304));
+    if (this.nExp) {
+      // moe_router: workgroups (a power of two, four router rows each, at most two per CU of an XCD) and their
+      // arrival counter, zero at allocation and touched by that op only
+      this.nwRouter = 1;
+      while (this.nwRouter * 4 < this.nExp && this.nwRouter * 2 <= 2 * cusXcd) this.nwRouter *= 2;
+      this.routerCnt = B(4, 'router_counter');
+      gpu.escribir(this.routerCnt, 0, new Uint8Array(4));
+    }
     this.ropeFreq = B(4 * Math.max(1, this.nrot / 2), 'rope_freq');
     gpu.escribir(this.ropeFreq, 0, tablaRope(this.base, this.nrot));
     this.amax = B(8 * AMAX_WG, 'argmax_partials');
@@ -569,10 +580,21 @@ class ModeloTransformer {
           return gpu.uniforme([['u', n], ['u', k], ['u', E], ['u', K], ['f', self.eps], ['f', self.escExp],
             ['u', self.normExp ? 1 : 0]]);
         };
-        // the router (E rows): one row per wavefront, so that the short tensor spreads over more workgroups
-        plan.push([this._gemv([{ W: c.router, mode: STORE, y: this.rl }], this.x, c.ffnNorm, D, { R: 1 }), 1]);
-        plan.push([gpu.grupo('moe_gate_up_' + c.eg.tipo, [u(this.ffe, D), P, c.eg.w, c.eu.w, this.x, c.ffnNorm, this.rl,
-          this.g, this.sel, this.wts]), 1]);
+        if (this.enrutador && c.router.tipo === 'f32') {
+          // the router GEMV and the routing in one launch (moe_router), so that the gate/up kernel reads the chosen
+          // experts instead of routing in every workgroup
+          plan.push([gpu.grupo('moe_router', [gpu.uniforme([['u', E], ['u', D], ['u', K], ['u', this.nwRouter], ['f', self.eps],
+            ['f', self.escExp], ['u', self.normExp ? 1 : 0]]), P, c.router.w, this.x, c.ffnNorm, this.rl, this.sel, this.wts,
+            this.routerCnt]), 1]);
+          plan.push([gpu.grupo('moe_gate_up_' + c.eg.tipo, [gpu.uniforme([['u', this.ffe], ['u', D], ['u', E], ['u', K],
+            ['f', self.eps], ['f', self.escExp], ['u', self.normExp ? 1 : 0], ['u', 1]]), P, c.eg.w, c.eu.w, this.x,
+            c.ffnNorm, this.rl, this.g, this.sel, this.wts]), 1]);
+        } else {
+          // the router (E rows): one row per wavefront, so that the short tensor spreads over more workgroups
+          plan.push([this._gemv([{ W: c.router, mode: STORE, y: this.rl }], this.x, c.ffnNorm, D, { R: 1 }), 1]);
+          plan.push([gpu.grupo('moe_gate_up_' + c.eg.tipo, [u(this.ffe, D), P, c.eg.w, c.eu.w, this.x, c.ffnNorm, this.rl,
+            this.g, this.sel, this.wts]), 1]);
+        }
         plan.push([gpu.grupo('moe_down_' + c.ed.tipo, [u(D, this.ffe), P, c.ed.w, this.g, this.x, this.sel, this.wts]), 1]);
       } else if (this.nExp) {
         plan.push([gc.ffnNorm, 1]);

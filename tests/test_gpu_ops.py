@@ -604,6 +604,73 @@ def test_moe_fused_decode(quipu, dev, oracle, fmt, E, k, D, Fe, norm):
         assert np.all(np.abs(got - want) <= bound), np.abs(got - want).max()
 
 
+@pytest.mark.parametrize("E,k,D,nw,norm", [(128, 8, 2048, 32, 1), (16, 4, 512, 4, 0), (256, 8, 4096, 64, 1),
+                                           (60, 4, 6144, 16, 1)])
+def test_moe_router(quipu, dev, oracle, E, k, D, nw, norm):
+    """moe_router: the f32 router GEMV of the normalized token (column 0's nw workgroups on one XCD) and the routing
+    by the last of them to finish.  Logits within 2e-5 sum |w x| of the oracle's rmsnorm + matmul; sel and wts
+    the oracle's moe_topk of those logits (sel exact, an exact tie at the top to the lower expert; wts within
+    2e-6), over three
+    launches in a row (the arrival counter only grows); then moe_gate_up with the routing read from sel (P[7] = 1)
+    and moe_down give bit-identical results to moe_gate_up routing from the same logits itself."""
+    rng = np.random.default_rng([E, k, D])
+    W = (0.02 * rng.standard_normal((E, D))).astype(np.float32)
+    W[E - 3] = W[5]  # rows 5 and E - 3 equal: an exact tie of their logits
+    nw_ = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    eps, scale = 1e-6, 1.0 if norm else 2.5
+    hw, hn, lg, sel, wts, cnt = dev.buf(W), dev.buf(nw_), dev.zeros(E * 4), dev.zeros(k * 4), dev.zeros(k * 4), dev.zeros(4)
+    u = [("u", E), ("u", D), ("u", k), ("u", nw), ("f", eps), ("f", scale), ("u", norm)]
+    for call in range(3):
+        x = rng.standard_normal(D).astype(np.float32)
+        x *= np.float32(1 + call)
+        xb = dev.buf(x)
+        if call == 1:
+            # make rows 5 / E - 3 the largest logits: x along their row
+            x = (W[5] * 50).astype(np.float32)
+            quipu.upload(xb, x)
+        quipu.dispatch("moe_router", u, [dev.paso(1, 0), hw, xb, hn, lg, sel, wts, cnt], (8, nw, 1))
+        got = dev.get(lg, (E,))
+        xn = oracle.rmsnorm(x[None, :], nw_, eps)[0]
+        want = W.astype(np.float64) @ xn.astype(np.float64)
+        assert np.all(np.abs(got - want) <= dot_bound(W, xn)), np.abs(got - want).max()
+        s_want, w_want = oracle.moe_topk(got[None, :], E, k, norm, scale)
+        np.testing.assert_array_equal(dev.get(sel, (k,), np.uint32), s_want)
+        np.testing.assert_allclose(dev.get(wts, (k,)), w_want, rtol=2e-6, atol=1e-7)
+        if call == 1:
+            assert list(s_want[:2]) == [5, E - 3]
+    assert dev.get(cnt, (1,), np.uint32)[0] == 3 * nw
+    if D % 256 or E * 64 * D * 0.5625 > 2 ** 30:
+        return
+    # the expert FFN from the router's routing: presel against routing in moe_gate_up, bit for bit
+    Fe = 256
+    rg, ru, rd = raw_matrix(capi.Q4_K, E * Fe, D, 84), raw_matrix(capi.Q4_K, E * Fe, D, 85), raw_matrix(capi.Q4_K, E * D, Fe, 86)
+    hg, hu, hd = (dev.matrix(capi.Q4_K, rg, E * Fe, D), dev.matrix(capi.Q4_K, ru, E * Fe, D),
+                  dev.matrix(capi.Q4_K, rd, E * D, Fe))
+    outs = []
+    for presel in (1, 0):
+        xb, h, s2, w2 = dev.buf(x), dev.zeros(k * Fe * 4), dev.zeros(k * 4), dev.zeros(k * 4)
+        if presel:
+            quipu.upload(s2, dev.get(sel, (k,), np.uint32))
+            quipu.upload(w2, dev.get(wts, (k,)))
+        ug = [("u", Fe), ("u", D), ("u", E), ("u", k), ("f", eps), ("f", scale), ("u", norm), ("u", presel)]
+        ud = [("u", D), ("u", Fe), ("u", E), ("u", k), ("f", eps), ("f", scale), ("u", norm)]
+        quipu.dispatch("moe_gate_up_q4k", ug, [dev.paso(1, 0), hg, hu, xb, hn, lg, h, s2, w2])
+        quipu.dispatch("moe_down_q4k", ud, [dev.paso(1, 0), hd, h, xb, s2, w2])
+        outs.append((dev.get(h, (k, Fe)), dev.get(xb, (D,)), dev.get(s2, (k,), np.uint32)))
+    for a_, b_ in zip(outs[0], outs[1]):
+        np.testing.assert_array_equal(a_, b_)
+
+
+def test_moe_router_rejections(quipu, dev):
+    """Shapes and bindings the kernel cannot take are refused on the host."""
+    b = [dev.zeros(16 * 512 * 4), dev.zeros(2048), dev.zeros(2048), dev.zeros(64), dev.zeros(64), dev.zeros(64), dev.zeros(4)]
+    for u3, msg in [((16, 512, 4, 3), "nw=3"), ((300, 512, 4, 4), "300 experts"), ((16, 512, 20, 4), "20 experts used"),
+                    ((16, 510, 4, 4), "k=510"), ((16, 512, 4, 256), "nw=256")]:
+        u = [("u", v) for v in u3] + [("f", 1e-6), ("f", 1.0), ("u", 1)]
+        with pytest.raises(capi.QuipuError, match=msg):
+            quipu.dispatch("moe_router", u, [0] + b, (8, 4, 1))
+
+
 # ------------------------------------------------------------------------------------------------ elementwise
 def test_rmsnorm(quipu, dev, oracle):
     T, D = 5, 4096
