@@ -3262,8 +3262,11 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
     float* wm = R + 4 * G * HD;
     float* wl = wm + 32;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t kvh = blockIdx.x, wg = blockIdx.y, h0 = kvh * G;
-    if (kvh >= a.nkv) return;  // the padding of a merged launch's grid (x = 8)
+    // column c: KV head c / gsplit, query heads c * G ..; the padding of a merged launch's grid (x = 8) exits
+    const uint32_t gs = a.gsplit ? a.gsplit : 1u;
+    const uint32_t col = blockIdx.x, kvh = col / gs, wg = blockIdx.y, h0 = col * G;
+    const bool app = col % gs == 0;  // this column appends its KV head's new key and value
+    if (kvh >= a.nkv) return;
     const uint32_t kq = lane / LPK, dsub = lane % LPK;
     const uint32_t pos0 = paso_pos(a.paso);
     const uint32_t nk = pos0 < a.rows ? pos0 + 1 : 0;  // a position past the cache reads and writes nothing
@@ -3462,7 +3465,7 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
         gstore<float4>(a.part_o + 4 * (i * HD + d), o);
         if (d == 0) gstore<float2>(a.part_ml + 8 * i, make_float2(M, L));
     }
-    if (wg_new && tid < HD) {
+    if (app && wg_new && tid < HD) {
         // append the new key and value to the cache at slot pos0 (kn / vn hold them, f16-rounded in f16 mode)
         const uint64_t o = (uint64_t)pos0 * kvd + (uint64_t)kvh * HD + tid;
         if (F16) {
@@ -3484,7 +3487,7 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
         __syncthreads();
         __shared__ uint32_t last;
         if (tid == 0) {
-            QP_GLOBAL uint32_t* c = reinterpret_cast<QP_GLOBAL uint32_t*>(a.cnt + 128ull * kvh);
+            QP_GLOBAL uint32_t* c = reinterpret_cast<QP_GLOBAL uint32_t*>(a.cnt + 128ull * col);
             const uint32_t n = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             last = n + 1 == gridDim.y;
             if (n + 1 == gridDim.y) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);

@@ -165,9 +165,13 @@ typedef struct {
     uint32_t hd, nh, nkv, nsplit;
     float scale, eps, base, esc;
     uint32_t nrot, neox, f16, rows;  // rows: slots of the cache; a position at or past it writes an empty result
-    uint32_t tseq, pad[3];
-    // merged output: 0, or o [nh][hd] written by the last workgroup of each KV head to finish (the grid's x is then
-    // 8: workgroups x >= nkv exit); cnt: arrival counters, one per KV head 128 bytes apart, zero between launches
+    uint32_t tseq;
+    // columns per KV head of a merged launch (1, or 2, 4, 8): column c of the grid takes KV head c / gsplit and its
+    // G query heads from c * G (G = the kernel's group, nh / nkv / gsplit); only column c % gsplit == 0 appends
+    uint32_t gsplit, pad[2];
+    // merged output: 0, or o [nh][hd] written by the last workgroup of each column to finish (the grid's x is then
+    // 8: columns past nkv * gsplit exit); cnt: arrival counters, one per column 128 bytes apart, zero between
+    // launches
     uint64_t att, cnt;
 } QpDecAttnArgs;
 

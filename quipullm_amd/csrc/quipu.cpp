@@ -1032,10 +1032,17 @@ int op_dec_attn(const Ctx& c) {
     a.part_ml = c.B(9);
     a.freq = c.B(10);
     // P[12] = 1: the merge of the splits in the same launch (bindings 11: o [nh][hd], 12: the counters, 8 x 128
-    // bytes, zero before the first launch; the kernel leaves them zero), for nkv <= 8
+    // bytes, zero before the first launch; the kernel leaves them zero), for nkv * gsplit <= 8
     const bool merged = c.U(12) != 0;
+    // P[13]: columns per KV head of the merged form (1, 2, 4 or 8; each takes G / gsplit query heads)
+    a.gsplit = merged && c.U(13) ? c.U(13) : 1;
+    if (a.gsplit != 1 && a.gsplit != 2 && a.gsplit != 4 && a.gsplit != 8)
+        return fail(QP_E_ARG, "dec_attn: gsplit=%u (1, 2, 4 or 8)", a.gsplit);
+    if (G % a.gsplit) return fail(QP_E_ARG, "dec_attn: gsplit=%u does not divide the group of %u query heads", a.gsplit, G);
     if (merged) {
-        if (a.nkv > 8) return fail(QP_E_ARG, "dec_attn: the merged form takes at most 8 KV heads (nkv=%u)", a.nkv);
+        if (a.nkv * a.gsplit > 8)
+            return fail(QP_E_ARG, "dec_attn: the merged form takes at most 8 columns (nkv=%u x gsplit=%u)", a.nkv,
+                        a.gsplit);
         a.att = c.nb > 11 ? c.B(11) : 0;
         a.cnt = c.nb > 12 ? c.B(12) : 0;
         if (!a.att || !a.cnt) return fail(QP_E_ARG, "dec_attn: the merged form needs bindings 11 (o) and 12 (counters)");
@@ -1043,7 +1050,8 @@ int op_dec_attn(const Ctx& c) {
             return fail(QP_E_ARG, "dec_attn: the counters must be a library buffer of at least 1024 bytes");
         if (int e = need_room(a.att, 4ull * a.nh * a.hd, "dec_attn", "the merged output")) return e;
     }
-    const uint32_t gi = G == 1 ? 0 : G == 2 ? 1 : G == 4 ? 2 : 3;
+    const uint32_t Gc = G / a.gsplit;  // query heads per column
+    const uint32_t gi = Gc == 1 ? 0 : Gc == 2 ? 1 : Gc == 4 ? 2 : 3;
     static const Kid kt[2][2][4] = {
         {{K_dec_attn_h64_f32_g1, K_dec_attn_h64_f32_g2, K_dec_attn_h64_f32_g4, K_dec_attn_h64_f32_g8},
          {K_dec_attn_h64_f16_g1, K_dec_attn_h64_f16_g2, K_dec_attn_h64_f16_g4, K_dec_attn_h64_f16_g8}},
@@ -1052,7 +1060,7 @@ int op_dec_attn(const Ctx& c) {
     const Kid k = kt[a.hd == 128][a.f16 ? 1 : 0][gi];
     // LDS floats: kn, vn [hd] | RoPE sines, cosines [hd/2] each | q/k norm weights [hd] each | wavefront partials
     // 4*G*hd + 64 (also holds q [G][hd] before, and the merge's weights G*(nsplit + 1) after)
-    const uint32_t region = 4 * G * a.hd + 64, mreg = G * (a.nsplit + 1);
+    const uint32_t region = 4 * Gc * a.hd + 64, mreg = Gc * (a.nsplit + 1);
     const uint32_t lds = 4 * (a.hd * 5 + (merged && region < mreg ? mreg : region));
     return launch(k, merged ? 8 : a.nkv, a.nsplit, 1, 256, lds, a);
 }

@@ -95,11 +95,17 @@ class ModeloTransformer {
     // (matmul_<fmt>_t_swiglu, the same results as the reference's matmul_<fmt>_t, matmul_<fmt>_t, swiglu of
     // transformer.js:311-313); false: those three ops
     this.ffnFusionada = op.fused_ffn !== false;
-    // one-token step: the split-K attention's partials merged by the last workgroup of each KV head in the same
-    // launch (dec_attn P[12] = 1) instead of a dec_attn_comb launch, for groups of up to 4 query heads (measured:
-    // 8B decode 449 -> 455 tok/s; with 8 heads per group the merge on one workgroup costs more than the launch it
-    // saves, MoE 400 -> 396); false: the separate merge
-    this.atencionUnida = op.merged_attention !== false && this.nkv <= 8 && this.nh / this.nkv <= 4;
+    // one-token step: the split-K attention's partials merged by the last workgroup of each grid column in the same
+    // launch (dec_attn P[12] = 1) instead of a dec_attn_comb launch.  A column takes at most 4 query heads: groups of
+    // 8 or more query heads are split over gsplit columns per KV head (P[13]; each column streams its KV head's keys
+    // and merges its own heads), as long as the columns fit the 8 XCDs.  Measured: 8B decode 449 -> 455 tok/s; MoE
+    // (8 query heads per KV head): one workgroup merging all 8 cost more than the launch it saved (400 -> 396),
+    // two columns of 4 heads each 403 -> see DESIGN; false: the separate merge
+    const grupoQ = this.nh / this.nkv;
+    this.gsplitAtt = 1;
+    while (grupoQ / this.gsplitAtt > 4 && this.gsplitAtt < 8) this.gsplitAtt *= 2;
+    this.atencionUnida = op.merged_attention !== false && this.nkv * this.gsplitAtt <= 8 &&
+      grupoQ % this.gsplitAtt === 0 && grupoQ / this.gsplitAtt <= 4;
     // one-token step: each layer's Q/K/V GEMV, attention, KV append and split merge as one launch (dec_attn_block,
     // eight head groups on the eight XCDs meeting at barriers in their L2) where the layer fits it (_bloqueAtt).
     // Off unless asked: measured no faster than the separate launches (8B at ctx 4096 450 against 455 tok/s, MoE
@@ -548,7 +554,7 @@ class ModeloTransformer {
     const uComb = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nsplit]]);
     const uAttM = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', this.nsplit], ['f', this.escAtt],
       ['f', this.eps], ['f', this.base], ['u', 0], ['u', this.nrot], ['u', this.neox], ['u', this.kvF16 ? 1 : 0], ['u', this.ctx],
-      ['u', 1]]);
+      ['u', 1], ['u', this.gsplitAtt]]);
     this.usaBloque = false;
     for (let i = 0; i < this.capas.length; i++) {
       const c = this.capas[i], gc = this.G.capas[i];

@@ -1012,16 +1012,22 @@ def test_dec_attn_fused(quipu, dev, oracle, hd, nh, nkv, pos0, nsplit, f16, neox
     np.testing.assert_array_equal(gv[pos0 + 1:].astype(np.float32), vc[pos0 + 1:])
 
 
-@pytest.mark.parametrize("hd,nh,nkv,pos0,nsplit,f16,neox,qk_norm",
-                         [(128, 32, 8, 4095, 17, 1, 0, 0), (128, 32, 4, 2047, 18, 1, 1, 1), (128, 32, 8, 777, 7, 0, 1, 1),
-                          (64, 8, 1, 31, 1, 0, 0, 1), (128, 16, 8, 33, 200, 0, 0, 0), (64, 32, 4, 2000, 16, 1, 0, 1),
-                          (128, 8, 1, 64, 5, 1, 1, 1), (64, 8, 2, 95, 300, 1, 0, 0), (128, 16, 2, 3000, 1024, 1, 0, 0)])
-def test_dec_attn_merged(quipu, dev, hd, nh, nkv, pos0, nsplit, f16, neox, qk_norm):
-    """dec_attn with P[12] = 1: the last workgroup of each KV head to finish merges its heads' partials in the same
-    launch (grid x = 8, so a head's workgroups share one XCD).  The same as dec_attn + dec_attn_comb up to the
-    order of the merge's sums (within 1e-5), the same cache row appended, and bit-identical over three launches in a
-    row whichever workgroup finishes last (the arrival counters return to zero after each), including splits
-    without keys (nsplit 200 .. 1024 over a short cache)."""
+MERGED_CASES = [(128, 32, 8, 4095, 17, 1, 0, 0), (128, 32, 4, 2047, 18, 1, 1, 1), (128, 32, 8, 777, 7, 0, 1, 1),
+                (64, 8, 1, 31, 1, 0, 0, 1), (128, 16, 8, 33, 200, 0, 0, 0), (64, 32, 4, 2000, 16, 1, 0, 1),
+                (128, 8, 1, 64, 5, 1, 1, 1), (64, 8, 2, 95, 300, 1, 0, 0), (128, 16, 2, 3000, 1024, 1, 0, 0)]
+
+
+@pytest.mark.parametrize("hd,nh,nkv,pos0,nsplit,f16,neox,qk_norm,gsplit",
+                         [c + (1,) for c in MERGED_CASES] +
+                         [c + (g,) for c in MERGED_CASES for g in (2, 4)
+                          if c[2] * g <= 8 and (c[1] // c[2]) % g == 0])
+def test_dec_attn_merged(quipu, dev, hd, nh, nkv, pos0, nsplit, f16, neox, qk_norm, gsplit):
+    """dec_attn with P[12] = 1: the last workgroup of each grid column to finish merges its heads' partials in the
+    same launch (grid x = 8, so a column's workgroups share one XCD); with P[13] = gsplit > 1 a KV head's query
+    heads are split over gsplit columns (each streams the head's keys, one appends).  The same as dec_attn +
+    dec_attn_comb up to the order of the merge's sums (within 1e-5), the same cache row appended, and bit-identical
+    over three launches in a row whichever workgroup finishes last (the arrival counters return to zero after
+    each), including splits without keys (nsplit 200 .. 1024 over a short cache)."""
     rows = 4100
     kvd = nkv * hd
     rng = np.random.default_rng(22)
@@ -1049,7 +1055,7 @@ def test_dec_attn_merged(quipu, dev, hd, nh, nkv, pos0, nsplit, f16, neox, qk_no
             cnt = dev.zeros(8 * 128)
             for _ in range(3):
                 quipu.upload(o, np.full(nh * hd, np.nan, np.float32))
-                quipu.dispatch("dec_attn", u + [("u", 1)], b + [o, cnt], (1, 1, 1))
+                quipu.dispatch("dec_attn", u + [("u", 1), ("u", gsplit)], b + [o, cnt], (1, 1, 1))
                 outs.append(dev.get(o, (nh * hd,)))
             assert np.all(dev.get(cnt, (8 * 32,), np.uint32) == 0)
         else:
@@ -1166,15 +1172,19 @@ def test_dec_attn_block_rejections(quipu, dev):
 
 
 def test_dec_attn_merged_rejections(quipu, dev):
-    """The merged form needs at most 8 KV heads, the output and a counter buffer of this library."""
+    """The merged form needs at most 8 columns (KV heads x gsplit), a gsplit of 1, 2, 4 or 8 dividing the query
+    group, the output and a counter buffer of this library."""
     hd, nh, nkv, rows = 64, 16, 16, 64
     b = [dev.paso(1, 3)] + [dev.zeros(4 * nh * hd)] * 3 + [dev.zeros(4 * rows * nkv * hd)] * 2 + [0, 0] + \
         [dev.zeros(4 * nh * hd), dev.zeros(8 * nh), 0, dev.zeros(4 * nh * hd), dev.zeros(1024)]
     u = [("u", hd), ("u", nh), ("u", nkv), ("u", 1), ("f", 0.125), ("f", 1e-6), ("f", 1e4), ("u", 0), ("u", hd),
          ("u", 0), ("u", 0), ("u", rows), ("u", 1)]
-    with pytest.raises(capi.QuipuError, match="at most 8 KV heads"):
+    with pytest.raises(capi.QuipuError, match="at most 8 columns"):
         quipu.dispatch("dec_attn", u, b)
-    u[2] = ("u", 8)
+    u[2] = ("u", 8)  # groups of 2 query heads
+    for g, msg in ((2, "at most 8 columns"), (3, "gsplit=3"), (4, "does not divide")):
+        with pytest.raises(capi.QuipuError, match=msg):
+            quipu.dispatch("dec_attn", u + [("u", g)], b)
     with pytest.raises(capi.QuipuError, match="at least 1024 bytes"):
         quipu.dispatch("dec_attn", u, b[:12] + [dev.zeros(512)])
 
