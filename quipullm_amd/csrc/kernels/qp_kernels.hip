@@ -3494,49 +3494,84 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
         }
         __syncthreads();
         if (last) {
-            // the G heads at once: wavefront w finds the weights e[g][s] = exp(m_s - M) (0 for a split without
-            // keys) and the denominator L = sum l_s e_s of heads g = w, w + 4; then each thread sums four
-            // dimensions of one head over the splits.  The partials are read past this CU's L1 (sc0).
+            // the column's G heads at once.  Thread t takes the float4 q = t % NQ of the outputs (four dimensions
+            // of one head; NQ = G HD / 4 divides 256) and share r = t / NQ of the splits (RS = 256 / NQ shares of
+            // consecutive splits).  Its partials' loads are issued PB at a time, the first batch before the
+            // weights are known, so the merge waits for about one round of loads; they are read past this CU's L1
+            // (sc0).  Wavefront w finds the weights e[g][s] = exp(m_s - M) (0 for a split without keys) and the
+            // denominator L = sum l_s e_s of heads g = w, w + 4.  Each share sums its splits in order, and the
+            // shares are added in order.
             const uint32_t ns = a.nsplit;
-            float* eb = R;           // [G][ns]
-            float* lb = R + G * ns;  // [G]
+            constexpr uint32_t NQ = G * HD / 4, RS = 256 / NQ;
+            constexpr int PB = 8;
+            float* eb = R;                                             // [G][ns]
+            float* lb = R + G * ns;                                    // [G]
+            float4* pb = reinterpret_cast<float4*>(R + ((G * ns + 8 + 3) & ~3u));  // [RS][NQ]
             const __amdgpu_buffer_rsrc_t rml = kq_rsrc(a.part_ml, 8ull * a.nh * ns);
             const __amdgpu_buffer_rsrc_t rpo = kq_rsrc(a.part_o, 4ull * a.nh * ns * HD);
-            for (uint32_t g = wave; g < (uint32_t)G; g += 4) {
-                const uint32_t h = h0 + g;
+            const uint32_t q = tid % NQ, r = tid / NQ, g = q / (HD / 4), d = (q % (HD / 4)) * 4, h = h0 + g;
+            const uint32_t per = (ns + RS - 1) / RS, s0 = min(ns, r * per), s1 = min(ns, s0 + per);
+            u32x4 pv[PB];
+            auto issue = [&](uint32_t base) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < PB; i++) {
+                    const uint32_t sp = base + i;
+                    pv[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rpo, sp < s1 ? 4 * ((h * ns + sp) * HD + d) : 0x80000000u, 0, 1);
+                }
+            };
+            issue(s0);
+            for (uint32_t gg = wave; gg < (uint32_t)G; gg += 4) {
+                const uint32_t hh = h0 + gg;
                 float mx = -3.0e38f;
                 for (uint32_t sp = lane; sp < ns; sp += 64) {
-                    const u32x2 r = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * (h * ns + sp), 0, 1);
-                    if (__uint_as_float(r.y) > 0.0f) mx = fmaxf(mx, __uint_as_float(r.x));
+                    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * (hh * ns + sp), 0, 1);
+                    if (__uint_as_float(v.y) > 0.0f) mx = fmaxf(mx, __uint_as_float(v.x));
                 }
                 mx = wave_max(mx);
                 float ls = 0.0f;
                 for (uint32_t sp = lane; sp < ns; sp += 64) {
-                    const u32x2 r = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * (h * ns + sp), 0, 1);
-                    const float l = __uint_as_float(r.y);
-                    const float e = l > 0.0f ? expf(__uint_as_float(r.x) - mx) : 0.0f;
-                    eb[g * ns + sp] = e;
+                    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * (hh * ns + sp), 0, 1);
+                    const float l = __uint_as_float(v.y);
+                    const float e = l > 0.0f ? expf(__uint_as_float(v.x) - mx) : 0.0f;
+                    eb[gg * ns + sp] = e;
                     ls += l * e;
                 }
                 ls = wave_sum(ls);
-                if (lane == 0) lb[g] = ls;
+                if (lane == 0) lb[gg] = ls;
             }
             __syncthreads();
-            for (uint32_t t = tid; t < G * (HD / 4); t += 256) {
-                const uint32_t g = t / (HD / 4), d = (t % (HD / 4)) * 4, h = h0 + g;
-                float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-                for (uint32_t sp = 0; sp < ns; sp++) {
-                    const float e = eb[g * ns + sp];
-                    const u32x4 c = __builtin_amdgcn_raw_buffer_load_b128(rpo, 4 * ((h * ns + sp) * HD + d), 0, 1);
-                    o.x = fmaf(e, __uint_as_float(c.x), o.x);
-                    o.y = fmaf(e, __uint_as_float(c.y), o.y);
-                    o.z = fmaf(e, __uint_as_float(c.z), o.z);
-                    o.w = fmaf(e, __uint_as_float(c.w), o.w);
+            float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (uint32_t base = s0; base < s1; base += PB) {
+                if (base != s0) issue(base);
+#pragma unroll
+                for (int i = 0; i < PB; i++) {
+                    const uint32_t sp = base + i;
+                    if (sp < s1) {
+                        const float e = eb[g * ns + sp];
+                        o.x = fmaf(e, __uint_as_float(pv[i][0]), o.x);
+                        o.y = fmaf(e, __uint_as_float(pv[i][1]), o.y);
+                        o.z = fmaf(e, __uint_as_float(pv[i][2]), o.z);
+                        o.w = fmaf(e, __uint_as_float(pv[i][3]), o.w);
+                    }
                 }
-                const float L = lb[g];
-                const float4 r = L > 0.0f ? make_float4(o.x / L, o.y / L, o.z / L, o.w / L) : make_float4(0, 0, 0, 0);
-                gstore<float4>(a.att + 4ull * (h * HD + d), r);  // no key: zeros
+            }
+            pb[r * NQ + q] = o;
+            __syncthreads();
+            for (uint32_t t = tid; t < NQ; t += 256) {
+                float4 sum = pb[t];
+                for (uint32_t rr = 1; rr < RS; rr++) {
+                    const float4 v = pb[rr * NQ + t];
+                    sum.x += v.x;
+                    sum.y += v.y;
+                    sum.z += v.z;
+                    sum.w += v.w;
+                }
+                const uint32_t tg = t / (HD / 4), td = (t % (HD / 4)) * 4, th = h0 + tg;
+                const float L = lb[tg];
+                const float4 res =
+                    L > 0.0f ? make_float4(sum.x / L, sum.y / L, sum.z / L, sum.w / L) : make_float4(0, 0, 0, 0);
+                gstore<float4>(a.att + 4ull * (th * HD + td), res);  // no key: zeros
             }
         }
     }

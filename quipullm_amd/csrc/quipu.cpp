@@ -1059,8 +1059,9 @@ int op_dec_attn(const Ctx& c) {
          {K_dec_attn_h128_f16_g1, K_dec_attn_h128_f16_g2, K_dec_attn_h128_f16_g4, K_dec_attn_h128_f16_g8}}};
     const Kid k = kt[a.hd == 128][a.f16 ? 1 : 0][gi];
     // LDS floats: kn, vn [hd] | RoPE sines, cosines [hd/2] each | q/k norm weights [hd] each | wavefront partials
-    // 4*G*hd + 64 (also holds q [G][hd] before, and the merge's weights G*(nsplit + 1) after)
-    const uint32_t region = 4 * Gc * a.hd + 64, mreg = Gc * (a.nsplit + 1);
+    // 4*G*hd + 64 (also holds q [G][hd] before, and the merge's weights and share sums after)
+    // the merge: weights G*nsplit, denominators, then 256 float4 of share sums (aligned to 16 bytes)
+    const uint32_t region = 4 * Gc * a.hd + 64, mreg = ((Gc * a.nsplit + 8 + 3) & ~3u) + 4 * 256;
     const uint32_t lds = 4 * (a.hd * 5 + (merged && region < mreg ? mreg : region));
     return launch(k, merged ? 8 : a.nkv, a.nsplit, 1, 256, lds, a);
 }
