@@ -106,7 +106,7 @@ QP_DEV uint32_t paso_pos(uint64_t p) { return cptr<uint32_t>(p)[1]; }
 #define QP_TL_SLOTS 4096
 #define QP_TL_MAXSEQ 420
 __device__ uint4 qp_tl[QP_TL_MAXSEQ * QP_TL_SLOTS];
-__device__ uint32_t qp_tl_ph[8 * QP_TL_SLOTS * 8];
+__device__ uint32_t qp_tl_ph[16 * QP_TL_SLOTS * 8];
 QP_DEV uint64_t tl_now() { return __builtin_amdgcn_s_memrealtime(); }
 QP_DEV void tl_rec(uint32_t tseq, uint64_t t0) {
     if (tseq == 0 || tseq > QP_TL_MAXSEQ || threadIdx.x != 0) return;

@@ -1234,11 +1234,9 @@ QP_DEV void kq_gemv_exp(const QpGemvExpArgs& a) {
 // router logits, kused rounds of strict maximum over the probabilities (ties to the lower expert index), weights =
 // chosen probabilities times scale, divided by their running sum (at least 2^-14) when norm.  Lane i < kused
 // returns slot i's expert and weight.
-// ld(e) returns logit e.
+// ld(e) returns logit e.  The probabilities of experts lane + 64 j (p[j]; -3, below every candidate, past E).
 template <class Ld>
-QP_DEV void moe_route_(uint32_t E, uint32_t kused, float scale, uint32_t norm, Ld ld, uint32_t lane, uint32_t& sel,
-                       float& wt) {
-    float p[4];
+QP_DEV void moe_probs(uint32_t E, Ld ld, uint32_t lane, float (&p)[4]) {
     float m = -3.0e38f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -1255,7 +1253,14 @@ QP_DEV void moe_route_(uint32_t E, uint32_t kused, float scale, uint32_t norm, L
     }
     s = wave_sum_v(s, lane);
 #pragma unroll
-    for (int j = 0; j < 4; j++) p[j] = lane + 64 * j < E ? p[j] / s : -3.0f;  // -3: below every candidate
+    for (int j = 0; j < 4; j++) p[j] = lane + 64 * j < E ? p[j] / s : -3.0f;
+}
+
+template <class Ld>
+QP_DEV void moe_route_(uint32_t E, uint32_t kused, float scale, uint32_t norm, Ld ld, uint32_t lane, uint32_t& sel,
+                       float& wt) {
+    float p[4];
+    moe_probs(E, ld, lane, p);
     float tot = 0.0f;
     sel = 0;
     wt = 0.0f;
@@ -1295,6 +1300,59 @@ QP_DEV void moe_route_(uint32_t E, uint32_t kused, float scale, uint32_t norm, L
     float f = scale;
     if (norm) f = f / fmaxf(tot, 6.103515625e-5f);
     wt = wt * f;
+}
+
+// The same routing by a whole workgroup (256 threads, E <= 256), with the k rounds replaced by ranks: wavefront 0
+// computes the probabilities as above; thread t < E counts the experts that come before its own (a higher
+// probability, or an equal one at a lower index; a NaN probability never counts and is never chosen), the kused
+// first go to their slots in rank order (unfilled slots keep expert 0 with -1, as the rounds leave them), and the
+// weights follow from the running sum in rank order: the same experts and the same weights as moe_route_, with no
+// chain of dependent rounds.  lds: 384 floats.
+template <class Ld>
+QP_DEV void moe_route_wg(uint32_t E, uint32_t kused, float scale, uint32_t norm, Ld ld, float* lds, uint64_t sel_out,
+                         uint64_t wts_out) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float* lp = lds;                                               // [256] probabilities
+    uint32_t* slot_e = reinterpret_cast<uint32_t*>(lds + 256);     // [64]
+    float* slot_p = lds + 320;                                     // [64]
+    if (wave == 0) {
+        float p[4];
+        moe_probs(E, ld, lane, p);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (lane + 64 * j < E) lp[lane + 64 * j] = p[j];
+    }
+    if (tid < kused) {
+        slot_e[tid] = 0u;
+        slot_p[tid] = -1.0f;
+    }
+    __syncthreads();
+    if (tid < E) {
+        const float pt = lp[tid];
+        uint32_t rank = E;  // NaN: never chosen
+        if (pt == pt) {
+            rank = 0;
+            for (uint32_t e = 0; e < E; e++) {
+                const float pe = lp[e];
+                rank += (pe > pt || (pe == pt && e < tid)) ? 1u : 0u;
+            }
+        }
+        if (rank < kused) {
+            slot_e[rank] = tid;
+            slot_p[rank] = pt;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float tot = 0.0f;
+        for (uint32_t i = 0; i < kused; i++) tot = tot + slot_p[i];
+        float f = scale;
+        if (norm) f = f / fmaxf(tot, 6.103515625e-5f);
+        if (lane < kused) {
+            gstore<uint32_t>(sel_out + 4ull * lane, slot_e[lane]);
+            gstore<float>(wts_out + 4ull * lane, slot_p[lane] * f);
+        }
+    }
 }
 
 QP_DEV void moe_route(const QpMoeArgs& a, uint32_t lane, uint32_t& sel, float& wt) {
@@ -1351,6 +1409,7 @@ QP_DEV void moe_router_body(const QpRouterArgs& a) {
 }
 QP_DEV void moe_router_body_(const QpRouterArgs& a) {
     if (blockIdx.x != 0) return;
+    tl_ph(8, 0);
     extern __shared__ float4 xs4[];  // k floats: x * norm_w
     __shared__ float red[4];
     __shared__ uint32_t last;
@@ -1387,6 +1446,7 @@ QP_DEV void moe_router_body_(const QpRouterArgs& a) {
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     const float inv = a.norm_w ? 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)a.k + a.eps) : 1.0f;
+    tl_ph(8, 1);  // input staged
     for (uint32_t r = r0; r < a.e; r += W) {
         float s = 0.0f;
         for (uint32_t q0 = 0; q0 < nf4; q0 += 64 * NP) {
@@ -1403,6 +1463,7 @@ QP_DEV void moe_router_body_(const QpRouterArgs& a) {
         s = wave_sum(s) * inv;
         if (lane == 0) gstore<float>(a.logits + 4ull * r, s);
     }
+    tl_ph(8, 2);  // rows done
     vm_drain();
     __syncthreads();
     if (tid == 0) {
@@ -1411,16 +1472,12 @@ QP_DEV void moe_router_body_(const QpRouterArgs& a) {
         last = ((n + 1) & (a.nw - 1)) == 0;
     }
     __syncthreads();
-    if (!last || wave != 0) return;
+    tl_ph(8, 3);  // arrival counted
+    if (!last) return;
     const __amdgpu_buffer_rsrc_t rl = kq_rsrc(a.logits, 4ull * a.e);
-    uint32_t sel = 0;
-    float wt = 0.0f;
-    moe_route_(a.e, a.kused, a.scale, a.norm, [&](uint32_t e) { return __uint_as_float(ld_sc0(rl, 4 * e)); }, lane,
-               sel, wt);
-    if (lane < a.kused) {
-        gstore<uint32_t>(a.sel + 4ull * lane, sel);
-        gstore<float>(a.wts + 4ull * lane, wt);
-    }
+    moe_route_wg(a.e, a.kused, a.scale, a.norm, [&](uint32_t e) { return __uint_as_float(ld_sc0(rl, 4 * e)); },
+                 reinterpret_cast<float*>(xs4), a.sel, a.wts);
+    tl_ph(8, 4);  // routed (the last workgroup)
 }
 KERNEL __launch_bounds__(256) void qp_moe_router(QpRouterArgs a) { moe_router_body(a); }
 

@@ -34,6 +34,7 @@ PHASE_KINDS = {
     5: ("gemv, other formats", ["input arrived", "input staged", "first unit's weights", "all units"]),
     6: ("decode attention", ["q,k,v loaded", "norm+RoPE", "q split", "key stream", "wave merge", "end"]),
     7: ("attention block", ["Q/K/V GEMV", "barrier 1", "q split", "partials stored", "barrier 2", "merged"]),
+    8: ("MoE router (working column)", ["input staged", "rows done", "arrival counted", "routed (last workgroup)"]),
 }
 
 
@@ -43,7 +44,7 @@ def load(path):
     raw = raw[: len(raw) // (SLOTS * 4) * SLOTS * 4].reshape(-1, SLOTS, 4)
     ph = None
     if os.path.exists(path + ".ph"):
-        ph = np.fromfile(path + ".ph", np.uint32).reshape(8, SLOTS, 8)
+        ph = np.fromfile(path + ".ph", np.uint32).reshape(-1, SLOTS, 8)
     return meta, raw, ph
 
 
@@ -115,8 +116,10 @@ def report(path, n_first=12):
                 continue
             P = P[ok]
             rel = ((P - P[:, :1]) % (1 << 32)) * TICK_US
-            cols = "; ".join(f"{lab} {np.median(rel[:, j + 1]):.2f}/{np.percentile(rel[:, j + 1], 90):.2f}"
-                             for j, lab in enumerate(labels))
+            # a stamp only some workgroups write (0 in the others) is summarized over those that wrote it
+            cols = "; ".join(f"{lab} {np.median(rel[P[:, j + 1] != 0, j + 1]):.2f}/"
+                             f"{np.percentile(rel[P[:, j + 1] != 0, j + 1], 90):.2f}"
+                             for j, lab in enumerate(labels) if (P[:, j + 1] != 0).any())
             lines.append(f"  {name} ({int(ok.sum())} WGs): {cols}")
     return "\n".join(lines)
 
