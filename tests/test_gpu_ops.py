@@ -1156,6 +1156,47 @@ def test_dec_attn_block(quipu, dev, hd, nh, nkv, D, fv, pos0, ns, neox, qk_norm)
     assert np.all(sw[0:512:64] == 3 * 2 * ns)
 
 
+def test_dec_attn_block_wait_bound(quipu, dev):
+    """The barriers' bounded wait, forced from the host: with spin_max = 1 a workgroup that arrives early gives up
+    after two polls, sets bit 0 of the error word and goes on, so the launch still ends (its results are not
+    meaningful).  Every workgroup still arrives at both barriers, so the counters stay consistent: after the error
+    word is cleared, a launch with the default bound gives the three-launch result again with no error."""
+    hd, nh, nkv, D, rows, pos0, ns = 128, 32, 8, 4096, 4100, 3000, 32
+    kvd = nkv * hd
+    rng = np.random.default_rng(24)
+    x = rng.standard_normal(D).astype(np.float32)
+    nw = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32)
+    kc = f16r(rng.standard_normal((rows, kvd)).astype(np.float32))
+    vc = f16r(rng.standard_normal((rows, kvd)).astype(np.float32))
+    mats = [(capi.Q4_K, nh * hd, 90), (capi.Q4_K, kvd, 91), (capi.Q6_K, kvd, 92)]
+    W = [dev.matrix(f, raw_matrix(f, n, D, sd), n, D) for f, n, sd in mats]
+    xb, nwb, paso, freq = dev.buf(x), dev.buf(nw), dev.paso(1, pos0), dev.buf(rope_table(1e6, hd))
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    kcb, vcb = dev.buf(kc.astype(np.float16)), dev.buf(refs.v_tiled(vc.astype(np.float16), kvd))
+    q, k, v, o = dev.zeros(nh * hd * 4), dev.zeros(kvd * 4), dev.zeros(kvd * 4), dev.zeros(nh * hd * 4)
+    po, pml, sync = dev.zeros(nh * ns * hd * 4), dev.zeros(nh * ns * 8), dev.zeros(2304)
+    b = [paso, xb, nwb, W[0], W[1], W[2], q, k, v, kcb, vcb, 0, 0, po, pml, freq, o, sync]
+
+    def launch(spin):
+        u = [("u", hd), ("u", nh), ("u", nkv), ("u", ns), ("f", scale), ("f", 1e-6), ("f", 1e6), ("u", 0),
+             ("u", hd), ("u", 0), ("u", rows), ("u", D), ("u", capi.Q4_K), ("u", capi.Q4_K), ("u", capi.Q6_K),
+             ("u", spin)]
+        quipu.upload(kcb, kc.astype(np.float16))
+        quipu.upload(vcb, refs.v_tiled(vc.astype(np.float16), kvd))
+        quipu.dispatch("dec_attn_block", u, b, (8, ns, 1))
+        return dev.get(o, (nh * hd,)), dev.get(sync, (576,), np.uint32)
+
+    want, sw = launch(0)
+    assert sw[528] == 0
+    _, sw = launch(1)
+    assert sw[528] & 1, "no barrier wait ran past a bound of one poll"
+    assert np.all(sw[0:512:64] == 2 * 2 * ns)
+    quipu.upload(sync, np.concatenate([sw[:528], np.zeros(576 - 528, np.uint32)]))
+    got, sw = launch(0)
+    assert sw[528] == 0
+    np.testing.assert_array_equal(got, want)
+
+
 def test_dec_attn_block_rejections(quipu, dev):
     """Shapes the kernel cannot take are refused on the host before any launch."""
     base = [("u", 128), ("u", 32), ("u", 8), ("u", 32), ("f", 0.1), ("f", 1e-5), ("f", 1e4), ("u", 0), ("u", 128),
