@@ -1307,42 +1307,65 @@ QP_DEV void moe_route_(uint32_t E, uint32_t kused, float scale, uint32_t norm, L
 // probability, or an equal one at a lower index; a NaN probability never counts and is never chosen), the kused
 // first go to their slots in rank order (unfilled slots keep expert 0 with -1, as the rounds leave them), and the
 // weights follow from the running sum in rank order: the same experts and the same weights as moe_route_, with no
-// chain of dependent rounds.  lds: 384 floats.
+// chain of dependent rounds.  lds: 896 floats.
 template <class Ld>
 QP_DEV void moe_route_wg(uint32_t E, uint32_t kused, float scale, uint32_t norm, Ld ld, float* lds, uint64_t sel_out,
                          uint64_t wts_out) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float* lp = lds;                                               // [256] probabilities
-    uint32_t* slot_e = reinterpret_cast<uint32_t*>(lds + 256);     // [64]
-    float* slot_p = lds + 320;                                     // [64]
+    // one 64-bit key per expert: the probability's bits above, 0xffffffff - index below.  The probabilities are
+    // non-negative (never -0), so their bits order as the values do and equal bits are equal values: key_e > key_t
+    // exactly when p_e > p_t, or p_e == p_t and e < t.  A NaN probability keys to 0, which outranks nothing; the
+    // entries past E are 0 too.
+    uint64_t* lk = reinterpret_cast<uint64_t*>(lds);                 // [256] keys
+    uint32_t* part = reinterpret_cast<uint32_t*>(lds + 512);         // [256] partial ranks
+    uint32_t* slot_e = reinterpret_cast<uint32_t*>(lds + 768);       // [64]
+    float* slot_p = lds + 832;                                       // [64]
+    tl_ph(9, 0);
     if (wave == 0) {
         float p[4];
         moe_probs(E, ld, lane, p);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (lane + 64 * j < E) lp[lane + 64 * j] = p[j];
+        for (int j = 0; j < 4; j++) {
+            const uint32_t e = lane + 64 * j;
+            lk[e] = e < E && p[j] == p[j]
+                        ? ((uint64_t)__float_as_uint(p[j]) << 32) | (uint64_t)(0xffffffffu - e)
+                        : 0ull;
+        }
     }
+    tl_ph(9, 1);
     if (tid < kused) {
         slot_e[tid] = 0u;
         slot_p[tid] = -1.0f;
     }
     __syncthreads();
-    if (tid < E) {
-        const float pt = lp[tid];
-        uint32_t rank = E;  // NaN: never chosen
-        if (pt == pt) {
-            rank = 0;
-            for (uint32_t e = 0; e < E; e++) {
-                const float pe = lp[e];
-                rank += (pe > pt || (pe == pt && e < tid)) ? 1u : 0u;
-            }
-        }
-        if (rank < kused) {
-            slot_e[rank] = tid;
-            slot_p[rank] = pt;
+    tl_ph(9, 2);
+    // up to 128 experts two threads count each expert's rank, over alternate pairs of keys
+    const uint32_t two = E <= 128, t = two ? tid & 127 : tid, h = two ? tid >> 7 : 0u, step = two ? 2u : 1u;
+    uint32_t r = 0;
+    if (t < E) {
+        const uint64_t kt = lk[t];
+        const ulonglong2* lk2 = reinterpret_cast<const ulonglong2*>(lk);
+        const uint32_t n2 = (E + 1) >> 1;
+#pragma unroll 8
+        for (uint32_t i = h; i < n2; i += step) {
+            const ulonglong2 q = lk2[i];
+            r += q.x > kt ? 1u : 0u;
+            r += q.y > kt ? 1u : 0u;
         }
     }
+    part[tid] = r;
     __syncthreads();
+    if (tid < E && (!two || tid < 128)) {
+        const uint64_t kt = lk[tid];
+        const uint32_t rank = kt == 0ull ? E : part[tid] + (two ? part[tid + 128] : 0u);  // NaN: never chosen
+        if (rank < kused) {
+            slot_e[rank] = tid;
+            slot_p[rank] = __uint_as_float((uint32_t)(kt >> 32));
+        }
+    }
+    tl_ph(9, 3);
+    __syncthreads();
+    tl_ph(9, 4);
     if (wave == 0) {
         float tot = 0.0f;
         for (uint32_t i = 0; i < kused; i++) tot = tot + slot_p[i];
@@ -1352,6 +1375,7 @@ QP_DEV void moe_route_wg(uint32_t E, uint32_t kused, float scale, uint32_t norm,
             gstore<uint32_t>(sel_out + 4ull * lane, slot_e[lane]);
             gstore<float>(wts_out + 4ull * lane, slot_p[lane] * f);
         }
+        tl_ph(9, 5);
     }
 }
 

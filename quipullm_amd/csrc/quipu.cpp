@@ -833,8 +833,8 @@ int op_moe_router(const Ctx& c) {
     for (const Need& n : need)
         if (n.p)
             if (int e = need_room(n.p, n.n, "moe_router", n.what)) return e;
-    // LDS: the staged input (k floats), then the routing's probabilities and slots (384 floats)
-    return launch(K_moe_router, 8, a.nw, 1, 256, 4 * (a.k > 384 ? a.k : 384), a);
+    // LDS: the staged input (k floats), then the routing's keys, partial ranks and slots (896 floats)
+    return launch(K_moe_router, 8, a.nw, 1, 256, 4 * (a.k > 896 ? a.k : 896), a);
 }
 
 // moe_comb (kds.js:224-240): P{D, k}; [paso, x, de, wts].
