@@ -3566,6 +3566,7 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
         // past this CU's L1.
         vm_drain();
         __syncthreads();
+        tl_ph(10, 0);
         __shared__ uint32_t last;
         if (tid == 0) {
             QP_GLOBAL uint32_t* c = reinterpret_cast<QP_GLOBAL uint32_t*>(a.cnt + 128ull * col);
@@ -3574,17 +3575,18 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
             if (n + 1 == gridDim.y) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         __syncthreads();
+        tl_ph(10, 1);
         if (last) {
             // the column's G heads at once.  Thread t takes the float4 q = t % NQ of the outputs (four dimensions
             // of one head; NQ = G HD / 4 divides 256) and share r = t / NQ of the splits (RS = 256 / NQ shares of
-            // consecutive splits).  Its partials' loads are issued PB at a time, the first batch before the
-            // weights are known, so the merge waits for about one round of loads; they are read past this CU's L1
-            // (sc0).  Wavefront w finds the weights e[g][s] = exp(m_s - M) (0 for a split without keys) and the
+            // consecutive splits).  Its partials' loads are issued PB at a time (one batch up to RS PB splits),
+            // the first batch before the weights are known, so the merge waits for about one round of loads; they
+            // are read past this CU's L1 (sc0).  Wavefront w finds the weights e[g][s] = exp(m_s - M) (0 for a split without keys) and the
             // denominator L = sum l_s e_s of heads g = w, w + 4.  Each share sums its splits in order, and the
             // shares are added in order.
             const uint32_t ns = a.nsplit;
             constexpr uint32_t NQ = G * HD / 4, RS = 256 / NQ;
-            constexpr int PB = 8;
+            constexpr int PB = 16;
             float* eb = R;                                             // [G][ns]
             float* lb = R + G * ns;                                    // [G]
             float4* pb = reinterpret_cast<float4*>(R + ((G * ns + 8 + 3) & ~3u));  // [RS][NQ]
@@ -3601,17 +3603,42 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
                         rpo, sp < s1 ? 4 * ((h * ns + sp) * HD + d) : 0x80000000u, 0, 1);
                 }
             };
+            // the first 128 splits' (m, l) stay in registers from the maximum to the weights (one round of
+            // loads); splits past 128 are read twice.  A load past ns reads l = 0 (the buffer's bound).  The first
+            // head's (m, l) loads go out before the partials', which return after them.
+            u32x2 v2[2];
+            auto load_ml = [&](uint32_t hh) __attribute__((always_inline)) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t sp = lane + 64 * j;
+                    v2[j] = __builtin_amdgcn_raw_buffer_load_b64(rml, sp < ns ? 8 * (hh * ns + sp) : 0x80000000u, 0,
+                                                                 1);
+                }
+            };
+            if (wave < (uint32_t)G) load_ml(h0 + wave);
             issue(s0);
             for (uint32_t gg = wave; gg < (uint32_t)G; gg += 4) {
                 const uint32_t hh = h0 + gg;
+                if (gg != wave) load_ml(hh);
                 float mx = -3.0e38f;
-                for (uint32_t sp = lane; sp < ns; sp += 64) {
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    if (__uint_as_float(v2[j].y) > 0.0f) mx = fmaxf(mx, __uint_as_float(v2[j].x));
+                for (uint32_t sp = lane + 128; sp < ns; sp += 64) {
                     const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * (hh * ns + sp), 0, 1);
                     if (__uint_as_float(v.y) > 0.0f) mx = fmaxf(mx, __uint_as_float(v.x));
                 }
                 mx = wave_max(mx);
                 float ls = 0.0f;
-                for (uint32_t sp = lane; sp < ns; sp += 64) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t sp = lane + 64 * j;
+                    const float l = __uint_as_float(v2[j].y);
+                    const float e = l > 0.0f ? expf(__uint_as_float(v2[j].x) - mx) : 0.0f;
+                    if (sp < ns) eb[gg * ns + sp] = e;
+                    ls += l * e;
+                }
+                for (uint32_t sp = lane + 128; sp < ns; sp += 64) {
                     const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * (hh * ns + sp), 0, 1);
                     const float l = __uint_as_float(v.y);
                     const float e = l > 0.0f ? expf(__uint_as_float(v.x) - mx) : 0.0f;
@@ -3621,7 +3648,9 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
                 ls = wave_sum(ls);
                 if (lane == 0) lb[gg] = ls;
             }
+            tl_ph(10, 2);
             __syncthreads();
+            tl_ph(10, 3);
             float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
             for (uint32_t base = s0; base < s1; base += PB) {
                 if (base != s0) issue(base);
@@ -3638,7 +3667,9 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
                 }
             }
             pb[r * NQ + q] = o;
+            tl_ph(10, 4);
             __syncthreads();
+            tl_ph(10, 5);
             for (uint32_t t = tid; t < NQ; t += 256) {
                 float4 sum = pb[t];
                 for (uint32_t rr = 1; rr < RS; rr++) {

@@ -35,6 +35,9 @@ PHASE_KINDS = {
     6: ("decode attention", ["q,k,v loaded", "norm+RoPE", "q split", "key stream", "wave merge", "end"]),
     7: ("attention block", ["Q/K/V GEMV", "barrier 1", "q split", "partials stored", "barrier 2", "merged"]),
     8: ("MoE router (working column)", ["input staged", "rows done", "arrival counted", "routed (last workgroup)"]),
+    10: ("decode attention, merge (last workgroups of the columns)", ["partials stored", "arrival counted",
+                                                                    "weights", "weights barrier", "sums",
+                                                                    "sums barrier"]),
     9: ("MoE router, routing (last workgroups)", ["probabilities", "first barrier", "ranks", "second barrier",
                                                 "weights stored"]),
 }
