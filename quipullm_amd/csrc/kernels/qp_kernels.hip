@@ -967,14 +967,29 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     // 1. this thread's share of x (and of the norm weight): float4 f = tid + NT i of the K / 4, so that each load
     // instruction of a wave reads 1 KB contiguous (8 lanes per cache line; one lane per line costs the address
     // unit 8x more work, and the weight loads queue behind it).  K % 256 == 0 keeps the bound wave-uniform.
+    // Buffer loads (a float4 past K reads 0) keep the input loads out of branches, and they come last: the
+    // compiler then counts at least NF loads after any earlier one (pro()'s, or the caller's), which is waited for
+    // alone.  The norm weight's loads go first, under one uniform branch.
     constexpr int NF = 8 * XS;
     const uint32_t nf4 = K >> 2;
     float4 xr[NF], nr[NF];
+    const __amdgpu_buffer_rsrc_t rxs = kq_rsrc(x, 16ull * nf4);
+    if (norm_w) {
+        const __amdgpu_buffer_rsrc_t rns = kq_rsrc(norm_w, 16ull * nf4);
+#pragma unroll
+        for (int i = 0; i < NF; i++) {
+            const uint32_t f = tid + NT * i;
+            const u32x4 n = __builtin_amdgcn_raw_buffer_load_b128(rns, f < nf4 ? 16 * f : 0x80000000u, 0, 0);
+            nr[i] = make_float4(__uint_as_float(n[0]), __uint_as_float(n[1]), __uint_as_float(n[2]),
+                                __uint_as_float(n[3]));
+        }
+    }
 #pragma unroll
     for (int i = 0; i < NF; i++) {
         const uint32_t f = tid + NT * i;
-        xr[i] = f < nf4 ? gload<float4>(x + 16ull * f) : float4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (norm_w) nr[i] = f < nf4 ? gload<float4>(norm_w + 16ull * f) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rxs, f < nf4 ? 16 * f : 0x80000000u, 0, 0);
+        xr[i] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                            __uint_as_float(v[3]));
     }
     float xsc[NF];
 #pragma unroll
@@ -1397,11 +1412,12 @@ QP_DEV void moe_gate_up_body_(const QpMoeArgs& a) {
     const uint32_t lane = threadIdx.x & 63, job = blockIdx.y;
     uint32_t sel = 0, ex = 0;
     float wt = 0.0f;
-    // the routing runs (or, with presel, the chosen experts load) while the input loads are in flight; the job's
-    // expert decides its weight rows
+    // with presel the chosen experts load before the input (loads return in order, so the weight loads wait for
+    // them alone); else the routing runs while the input loads are in flight.  The job's expert decides its
+    // weight rows.
+    if (a.presel) sel = lane < a.kused ? gload<uint32_t>(a.sel + 4ull * lane) : 0u;
     auto route = [&]() __attribute__((always_inline)) {
-        if (a.presel) sel = lane < a.kused ? gload<uint32_t>(a.sel + 4ull * lane) : 0u;
-        else moe_route(a, lane, sel, wt);
+        if (!a.presel) moe_route(a, lane, sel, wt);
         ex = (uint32_t)__builtin_amdgcn_readlane((int)sel, (int)job);
         if (ex >= a.e) ex = a.e - 1;
     };
