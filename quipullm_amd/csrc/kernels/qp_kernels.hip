@@ -3365,7 +3365,23 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
     const bool app = col % gs == 0;  // this column appends its KV head's new key and value
     if (kvh >= a.nkv) return;
     const uint32_t kq = lane / LPK, dsub = lane % LPK;
-    const uint32_t pos0 = paso_pos(a.paso);
+    // 1. the position first, then q, the frequency table and the q norm weight (none of them depends on it) as
+    // buffer loads out of branches (past the end: 0), so the wait for the position leaves them in flight
+    const uint32_t pos_w = __builtin_amdgcn_raw_buffer_load_b32(kq_rsrc(a.paso, 8), 4, 0, 0);
+    float qt[QN], knt = 0.0f, vnt = 0.0f, ft, qwt, kwt = 0.0f;
+    {
+        const __amdgpu_buffer_rsrc_t rq = kq_rsrc(a.q + 4ull * h0 * HD, 4ull * G * HD);
+#pragma unroll
+        for (int c = 0; c < QN; c++) {
+            const uint32_t i = tid + 256 * c;
+            qt[c] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, i < G * HD ? 4 * i : 0x80000000u, 0, 0));
+        }
+        const __amdgpu_buffer_rsrc_t rf = kq_rsrc(a.freq ? a.freq : a.q, a.freq ? 4ull * (a.nrot / 2) : 0ull);
+        ft = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rf, 4 * tid, 0, 0));
+        const __amdgpu_buffer_rsrc_t rqn = kq_rsrc(a.qnorm ? a.qnorm : a.q, a.qnorm ? 4ull * HD : 0ull);
+        qwt = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rqn, 4 * tid, 0, 0));
+    }
+    const uint32_t pos0 = pos_w;
     const uint32_t nk = pos0 < a.rows ? pos0 + 1 : 0;  // a position past the cache reads and writes nothing
     const uint32_t W = 4 * a.nsplit;
     // keys per wavefront (whole tiles of 32 for the matrix-core stream)
@@ -3373,19 +3389,11 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
     const uint32_t kw0 = min(nk, (wg * 4 + wave) * per), kw1 = min(nk, kw0 + per);
     const uint32_t g0 = min(nk, wg * 4 * per), g1 = min(nk, g0 + 4 * per);
     const bool wg_new = g0 <= pos0 && pos0 < g1;  // this workgroup holds the new key: it appends it
-    // 1. q (and the new k, v, and the frequency table) into registers, then the first K/V step
-    float qt[QN], knt = 0.0f, vnt = 0.0f, ft = 0.0f, qwt = 0.0f, kwt = 0.0f;
-#pragma unroll
-    for (int c = 0; c < QN; c++) {
-        const uint32_t i = tid + 256 * c;
-        qt[c] = i < G * HD ? gload<float>(a.q + 4ull * ((uint64_t)h0 * HD + i)) : 0.0f;
-    }
+    // the new k and v (and the k norm weight) where this workgroup appends them, then the first K/V step
     if (wg_new && tid < HD) {
         knt = gload<float>(a.k + 4ull * ((uint64_t)kvh * HD + tid));
         vnt = gload<float>(a.v + 4ull * ((uint64_t)kvh * HD + tid));
     }
-    if (a.freq && tid < a.nrot / 2) ft = gload<float>(a.freq + 4ull * tid);
-    if (a.qnorm && tid < HD) qwt = gload<float>(a.qnorm + 4ull * tid);
     if (a.knorm && wg_new && tid < HD) kwt = gload<float>(a.knorm + 4ull * tid);
     // issued by every wavefront (one without keys loads nothing: its offsets are past the end), so the waits below
     // can count these loads as still in flight
