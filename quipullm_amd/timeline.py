@@ -35,9 +35,8 @@ PHASE_KINDS = {
     6: ("decode attention", ["q,k,v loaded", "norm+RoPE", "q split", "key stream", "wave merge", "end"]),
     7: ("attention block", ["Q/K/V GEMV", "barrier 1", "q split", "partials stored", "barrier 2", "merged"]),
     8: ("MoE router (working column)", ["input staged", "rows done", "arrival counted", "routed (last workgroup)"]),
-    10: ("decode attention, merge (last workgroups of the columns)", ["partials stored", "arrival counted",
-                                                                    "weights", "weights barrier", "sums",
-                                                                    "sums barrier"]),
+    10: ("decode attention, merge (from the partials' drain; the last workgroups of the columns)",
+         ["arrival counted", "weights", "weights barrier", "sums", "sums barrier"]),
     9: ("MoE router, routing (last workgroups)", ["probabilities", "first barrier", "ranks", "second barrier",
                                                 "weights stored"]),
 }
@@ -120,12 +119,17 @@ def report(path, n_first=12):
             if not ok.any():
                 continue
             P = P[ok]
+            # the last launch of the kind: first stamps within 20 us of the latest (launches of one kind are a
+            # layer, 40 us or more, apart); workgroup slots that only earlier launches wrote drop out
+            P = P[(P[:, 0].max() - P[:, 0]) < int(20.0 / TICK_US)]
             rel = ((P - P[:, :1]) % (1 << 32)) * TICK_US
-            # a stamp only some workgroups write (0 in the others) is summarized over those that wrote it
-            cols = "; ".join(f"{lab} {np.median(rel[P[:, j + 1] != 0, j + 1]):.2f}/"
-                             f"{np.percentile(rel[P[:, j + 1] != 0, j + 1], 90):.2f}"
-                             for j, lab in enumerate(labels) if (P[:, j + 1] != 0).any())
-            lines.append(f"  {name} ({int(ok.sum())} WGs): {cols}")
+            # a stamp only some workgroups write is summarized over those that wrote it in this launch (0, or a
+            # stale stamp of an earlier launch, in the others: more than 1 ms from the workgroup's first)
+            mine = (P != 0) & (rel < 1000.0)
+            cols = "; ".join(f"{lab} {np.median(rel[mine[:, j + 1], j + 1]):.2f}/"
+                             f"{np.percentile(rel[mine[:, j + 1], j + 1], 90):.2f}"
+                             for j, lab in enumerate(labels) if mine[:, j + 1].any())
+            lines.append(f"  {name} ({len(P)} WGs): {cols}")
     return "\n".join(lines)
 
 
