@@ -967,29 +967,40 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     // 1. this thread's share of x (and of the norm weight): float4 f = tid + NT i of the K / 4, so that each load
     // instruction of a wave reads 1 KB contiguous (8 lanes per cache line; one lane per line costs the address
     // unit 8x more work, and the weight loads queue behind it).  K % 256 == 0 keeps the bound wave-uniform.
-    // Buffer loads (a float4 past K reads 0) keep the input loads out of branches, and they come last: the
-    // compiler then counts at least NF loads after any earlier one (pro()'s, or the caller's), which is waited for
-    // alone.  The norm weight's loads go first, under one uniform branch.
+    // Where an earlier load has to be waited for alone (pro()'s, or the caller's ahead of a gathered layout), the
+    // input loads are buffer loads out of branches (a float4 past K reads 0) and come last: the compiler then
+    // counts at least NF loads after the earlier one.  The norm weight's loads go first, under one uniform branch.
+    // Elsewhere a float4 past K is skipped by a wave-uniform branch (K % 256 == 0), which issues fewer loads.
     constexpr int NF = 8 * XS;
     const uint32_t nf4 = K >> 2;
     float4 xr[NF], nr[NF];
-    const __amdgpu_buffer_rsrc_t rxs = kq_rsrc(x, 16ull * nf4);
-    if (norm_w) {
-        const __amdgpu_buffer_rsrc_t rns = kq_rsrc(norm_w, 16ull * nf4);
+    constexpr bool BF = !__is_same(Pro, KNoPro) || !__is_same(Lay, KDense);
+    if constexpr (!BF) {
 #pragma unroll
         for (int i = 0; i < NF; i++) {
             const uint32_t f = tid + NT * i;
-            const u32x4 n = __builtin_amdgcn_raw_buffer_load_b128(rns, f < nf4 ? 16 * f : 0x80000000u, 0, 0);
-            nr[i] = make_float4(__uint_as_float(n[0]), __uint_as_float(n[1]), __uint_as_float(n[2]),
-                                __uint_as_float(n[3]));
+            xr[i] = f < nf4 ? gload<float4>(x + 16ull * f) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (norm_w) nr[i] = f < nf4 ? gload<float4>(norm_w + 16ull * f) : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-    }
+    } else {
+        const __amdgpu_buffer_rsrc_t rxs = kq_rsrc(x, 16ull * nf4);
+        if (norm_w) {
+            const __amdgpu_buffer_rsrc_t rns = kq_rsrc(norm_w, 16ull * nf4);
 #pragma unroll
-    for (int i = 0; i < NF; i++) {
-        const uint32_t f = tid + NT * i;
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rxs, f < nf4 ? 16 * f : 0x80000000u, 0, 0);
-        xr[i] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
-                            __uint_as_float(v[3]));
+            for (int i = 0; i < NF; i++) {
+                const uint32_t f = tid + NT * i;
+                const u32x4 n = __builtin_amdgcn_raw_buffer_load_b128(rns, f < nf4 ? 16 * f : 0x80000000u, 0, 0);
+                nr[i] = make_float4(__uint_as_float(n[0]), __uint_as_float(n[1]), __uint_as_float(n[2]),
+                                    __uint_as_float(n[3]));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NF; i++) {
+            const uint32_t f = tid + NT * i;
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rxs, f < nf4 ? 16 * f : 0x80000000u, 0, 0);
+            xr[i] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                                __uint_as_float(v[3]));
+        }
     }
     float xsc[NF];
 #pragma unroll
