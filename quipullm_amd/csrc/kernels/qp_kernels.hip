@@ -3663,7 +3663,7 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
                     const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rml, 8 * (hh * ns + sp), 0, 1);
                     if (__uint_as_float(v.y) > 0.0f) mx = fmaxf(mx, __uint_as_float(v.x));
                 }
-                mx = wave_max(mx);
+                mx = wave_max_v(mx, lane);  // lane exchanges, no LDS round trips
                 float ls = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
@@ -3680,7 +3680,7 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
                     eb[gg * ns + sp] = e;
                     ls += l * e;
                 }
-                ls = wave_sum(ls);
+                ls = wave_sum_v(ls, lane);
                 if (lane == 0) lb[gg] = ls;
             }
             tl_ph(10, 2);
