@@ -1099,7 +1099,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         }
     }
     if (norm_w) {
-        ss = wave_sum(ss);
+        ss = wave_sum_v(ss, lane);  // lane exchanges, no LDS round trips
         if (lane == 0) red[wave] = ss;
     }
     __syncthreads();
@@ -1171,8 +1171,15 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         float v[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
+            // the butterfly of lane exchanges over the slot's nbp lanes (aligned, a power of two; wave-uniform
+            // branches): quad steps, then the mirror within 8 and 16 lanes, the row pair, the halves
             float t = lane_on ? tot[r] : 0.0f;
-            for (uint32_t m = nbp >> 1; m >= 1; m >>= 1) t += __shfl_xor(t, m, 64);
+            if (nbp > 1) t += bfly_f<0>(t, lane);
+            if (nbp > 2) t += bfly_f<1>(t, lane);
+            if (nbp > 4) t += bfly_f<2>(t, lane);
+            if (nbp > 8) t += bfly_f<3>(t, lane);
+            if (nbp > 16) t += bfly_f<4>(t, lane);
+            if (nbp > 32) t += bfly_f<5>(t, lane);
             v[r] = t * inv;
         }
         const uint32_t nper = pair ? 1 : R;
