@@ -1500,7 +1500,7 @@ QP_DEV void moe_router_body_(const QpRouterArgs& a) {
         }
         xs4[q] = v;
     }
-    ss = wave_sum(ss);
+    ss = wave_sum_v(ss, lane);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     const float inv = a.norm_w ? 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)a.k + a.eps) : 1.0f;
@@ -1518,7 +1518,7 @@ QP_DEV void moe_router_body_(const QpRouterArgs& a) {
                 }
             }
         }
-        s = wave_sum(s) * inv;
+        s = wave_sum_v(s, lane) * inv;  // lane exchanges: no LDS round trips on the way to the arrival
         if (lane == 0) gstore<float>(a.logits + 4ull * r, s);
     }
     tl_ph(8, 2);  // rows done
