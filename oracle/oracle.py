@@ -21,6 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL = 0, 8, 10, 11, 12, 13, 14, 20
+F16, BF16 = 1, 30  # matrices the reference widens to f32 when it uploads them (weights.js:127-133)
 _BLOCKS = {0: (1, 4), 1: (1, 2), 8: (32, 34), 20: (32, 18), 10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176),
            14: (256, 210), 30: (1, 2)}
 _NAMES = {0: "F32", 1: "F16", 8: "Q8_0", 20: "IQ4_NL", 10: "Q2_K", 11: "Q3_K", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 30: "BF16"}
@@ -328,6 +329,7 @@ class Model:
         self.ctx = ctx or get("context_length", 4096)
         self.n_exp = get("expert_count", 0)
         self.vocab = g.tensors["token_embd.weight"]["dims"][1]
+        self._kvref = None
         self.ptr = L.or_model_new()
         m = _Model.from_address(self.ptr)
         m.n_layers, m.D, m.nh, m.nkv, m.hd = self.n_layers, self.D, self.nh, self.nkv, self.hd
@@ -363,10 +365,16 @@ class Model:
         m.moe_scale = get("expert_weights_scale", 1.0) or 1.0
         m.F = get("feed_forward_length", 0) or 0
         t = g.tensors
-        ptr = lambda n: g.raw(n).ctypes.data if n in t else None
-        m.tok_embd, m.f_embd = ptr("token_embd.weight"), t["token_embd.weight"]["tipo"]
+        # F16 / BF16 tensors widened to f32 once, as the reference's loader does at upload (weights.js:127-133)
+        self._wide = {}
+        for n, ti in t.items():
+            if ti["tipo"] in (F16, BF16):
+                self._wide[n] = dequant(ti["tipo"], g.raw(n), int(np.prod(ti["dims"])))
+        ptr = lambda n: (self._wide[n].ctypes.data if n in self._wide else g.raw(n).ctypes.data) if n in t else None
+        tipo = lambda n: F32 if n in self._wide else t[n]["tipo"]
+        m.tok_embd, m.f_embd = ptr("token_embd.weight"), tipo("token_embd.weight")
         out = "output.weight" if "output.weight" in t else "token_embd.weight"
-        m.output, m.f_output = ptr(out), t[out]["tipo"]
+        m.output, m.f_output = ptr(out), tipo(out)
         m.output_norm = ptr("output_norm.weight")
         layers = C.cast(L.or_model_layers(self.ptr, self.n_layers), C.POINTER(_Layer))
         for i in range(self.n_layers):
@@ -384,7 +392,7 @@ class Model:
                                 ("frouter", "ffn_gate_inp"), ("fgate_e", "ffn_gate_exps"),
                                 ("fup_e", "ffn_up_exps"), ("fdown_e", "ffn_down_exps")):
                 n = p + name + ".weight"
-                setattr(ly, field, t[n]["tipo"] if n in t else 0)
+                setattr(ly, field, tipo(n) if n in t else 0)
             if self.n_exp == 0 and m.F == 0:
                 m.F = t[p + "ffn_gate.weight"]["dims"][1]
             ly.post_att, ly.post_ffn = ptr(p + "post_attention_norm.weight"), ptr(p + "post_ffw_norm.weight")
@@ -406,6 +414,37 @@ class Model:
         assert k16.shape == v16.shape and k16.ndim == 3 and k16.shape[0] == self.n_layers and k16.shape[2] == kvd
         self._kvref = (k16, v16)
         m.kref, m.vref, m.nref = k16.ctypes.data, v16.ctypes.data, k16.shape[1]
+
+    def resume_from_reference(self, pos):
+        """f16 mode: continue from position `pos` of the run whose cache rows set_kv_reference gave, without
+        recomputing its first pos tokens: the cache rows of positions 0 .. pos-1 are those rows (f16, widened
+        exactly as the cache holds them) and the position moves to pos.  The next forward then computes what that
+        run computed at position pos, over the same keys and values (the reference rows also stand in for the
+        positions this model writes afterwards, up to their count)."""
+        m = _Model.from_address(self.ptr)
+        assert m.kv_f16 and self._kvref is not None, "resume_from_reference needs kv_f16 and set_kv_reference"
+        k16, v16 = self._kvref
+        assert 0 < pos <= k16.shape[1] and pos < self.ctx
+        kvd = self.nkv * self.hd
+        n = self.n_layers * self.ctx * kvd
+        for ptr, r in ((m.kc, k16), (m.vc, v16)):
+            a = np.ctypeslib.as_array((C.c_float * n).from_address(ptr)).reshape(self.n_layers, self.ctx, kvd)
+            for li in range(self.n_layers):
+                a[li, :pos] = dequant(F16, np.ascontiguousarray(r[li, :pos]).view(np.uint8), pos * kvd).reshape(pos, kvd)
+        m.pos = pos
+
+    def kv_cache_f16(self, npos):
+        """f16 mode: this model's own cache rows of positions 0 .. npos-1 as f16 bits, uint16 [n_layers][npos][kvd]
+        each for K and V (the layout set_kv_reference takes)."""
+        m = _Model.from_address(self.ptr)
+        assert m.kv_f16 and 0 < npos <= self.ctx
+        kvd = self.nkv * self.hd
+        n = self.n_layers * self.ctx * kvd
+        out = []
+        for ptr in (m.kc, m.vc):
+            a = np.ctypeslib.as_array((C.c_float * n).from_address(ptr)).reshape(self.n_layers, self.ctx, kvd)
+            out.append(a[:, :npos].astype(np.float16).view(np.uint16).copy())
+        return out[0], out[1]
 
     def fill_cache_to(self, npos):
         """For timing only: copies the cached rows of positions 0 .. pos-1 over positions pos .. npos-1 and moves the

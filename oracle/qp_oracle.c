@@ -29,6 +29,8 @@
 #define OR_Q5_K 13
 #define OR_Q6_K 14
 #define OR_IQ4_NL 20
+#define OR_F16 1   /* matrices widened to f32 at upload */
+#define OR_BF16 30
 
 /* ------------------------------------------------------------------ f16 -> f32 (exact)
  * web/js/gpu.js:939-948 (F16 table); unpack2x16float in kquants.js:67 is the same map. */
@@ -210,6 +212,15 @@ void or_dequant(int fmt, const uint8_t* raw, int64_t nelem, float* out) {
         for (i = 0; i < nelem; i++) out[i] = q8_deq(raw + (i >> 5) * 34, (int)(i & 31));
     } else if (fmt == OR_IQ4_NL) {
         for (i = 0; i < nelem; i++) out[i] = iq4nl_deq(raw + (i >> 5) * 18, (int)(i & 31));
+    } else if (fmt == OR_F16) {
+        /* F16 matrices are widened to f32 when uploaded (weights.js:128, f16af32 of gpu.js:939-948) */
+        for (i = 0; i < nelem; i++) out[i] = or_f16(rd16(raw + 2 * i));
+    } else if (fmt == OR_BF16) {
+        /* BF16: the 16 bits are the high half of the f32 (weights.js:129-133, v[i] = s[i] << 16) */
+        for (i = 0; i < nelem; i++) {
+            const uint32_t u = (uint32_t)rd16(raw + 2 * i) << 16;
+            memcpy(out + i, &u, 4);
+        }
     } else {
         memcpy(out, raw, (size_t)nelem * 4);
     }

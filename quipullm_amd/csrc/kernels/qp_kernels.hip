@@ -613,6 +613,28 @@ QP_DEV uint32_t ld_sc0(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 1);
 }
 
+// Arrival of one of the n workgroups that share a counter word in their XCD's L2 (a launch whose workgroups go to
+// the 8 XCDs round robin by linear id x + 8y puts every workgroup of grid column x on one XCD; the kernels that call
+// this rely on it).  Each arrival adds 1 + (its XCD id << 16): the low half counts the arrivals, the high half sums
+// their XCD ids.  The arrival that brings the count to n is the last (returns true) and resets the word; if the ids
+// it sums are not n times its own, or a count ever passes n (arrivals left over from a launch whose workgroups were
+// spread over XCDs, so that no add saw the full count), it sets bit 0 of *err (a device word the host checks) instead
+// of letting the placement fail silently.  The work after a last arrival runs either way, so every workgroup ends.
+// One thread per workgroup calls it; n <= 4096.
+QP_DEV bool xcd_arrive(uint64_t cnt, uint32_t n, uint64_t err) {
+    const uint32_t xid = __builtin_amdgcn_s_getreg(20 | (15 << 11)) & 15u;  // HW_REG_XCC_ID
+    const uint32_t add = 1u + (xid << 16);
+    QP_GLOBAL uint32_t* c = reinterpret_cast<QP_GLOBAL uint32_t*>(cnt);
+    const uint32_t t = __hip_atomic_fetch_add(c, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) + add;
+    const uint32_t got = t & 0xffffu;
+    const bool last = got == n;
+    if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if ((last && (t >> 16) != n * xid) || got > n)
+        __hip_atomic_fetch_or(reinterpret_cast<QP_GLOBAL uint32_t*>(err), 1u, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+    return last;
+}
+
 // Bytes of LDS the K-quant GEMV uses for a K-wide input (staged x + group sums + reduction slots).
 QP_DEV uint32_t kq_lds_offset_sum(uint32_t K) { return (K >> 8) * 65 * 16; }
 
@@ -1524,11 +1546,7 @@ QP_DEV void moe_router_body_(const QpRouterArgs& a) {
     tl_ph(8, 2);  // rows done
     vm_drain();
     __syncthreads();
-    if (tid == 0) {
-        const uint32_t n = __hip_atomic_fetch_add(reinterpret_cast<QP_GLOBAL uint32_t*>(a.cnt), 1u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
-        last = ((n + 1) & (a.nw - 1)) == 0;
-    }
+    if (tid == 0) last = xcd_arrive(a.cnt, a.nw, a.cnt + 4);
     __syncthreads();
     tl_ph(8, 3);  // arrival counted
     if (!last) return;
@@ -3605,17 +3623,12 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
         // robin by that id: all workgroups of KV head x run on one XCD and share its L2, where the counter's atomic
         // add executes and the partial stores land once acknowledged: every wavefront waits for that (a
         // workgroup-scope release fence does not) before the barrier that precedes the add.  The merge reads them
-        // past this CU's L1.
+        // past this CU's L1.  The placement is checked by the same add (xcd_arrive).
         vm_drain();
         __syncthreads();
         tl_ph(10, 0);
         __shared__ uint32_t last;
-        if (tid == 0) {
-            QP_GLOBAL uint32_t* c = reinterpret_cast<QP_GLOBAL uint32_t*>(a.cnt + 128ull * col);
-            const uint32_t n = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            last = n + 1 == gridDim.y;
-            if (n + 1 == gridDim.y) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
+        if (tid == 0) last = xcd_arrive(a.cnt + 128ull * col, gridDim.y, a.cnt + 1024);
         __syncthreads();
         tl_ph(10, 1);
         if (last) {

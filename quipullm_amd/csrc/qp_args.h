@@ -92,8 +92,9 @@ typedef struct {
 // logits[e] = W[e] . (rmsnorm(x) * norm_w) of one token (W f32 [e][k]) and, in the last of its workgroups to
 // finish, the routing of moe_topk (kds.js:191-221) into sel[kused], wts[kused].  Grid (8, nw): only column 0
 // works (its nw workgroups share one XCD, whose L2 holds the arrival counter cnt and the logits they store); the
-// other columns exit at once.  cnt: a word only this op touches, zero at allocation (grows by nw per launch; nw is
-// a power of two).
+// other columns exit at once.  cnt: two words only this op touches, zero at allocation: the arrival counter (the
+// last arrival resets it) and, at cnt + 4, an error word whose bit 0 is set when the workgroups were found on more
+// than one XCD (the host checks it).
 typedef struct {
     uint64_t w, x, norm_w, logits, sel, wts, cnt;
     uint32_t e, k, kused, nw;
@@ -171,7 +172,8 @@ typedef struct {
     uint32_t gsplit, pad[2];
     // merged output: 0, or o [nh][hd] written by the last workgroup of each column to finish (the grid's x is then
     // 8: columns past nkv * gsplit exit); cnt: arrival counters, one per column 128 bytes apart, zero between
-    // launches
+    // launches, and at cnt + 1024 an error word whose bit 0 is set when a column's workgroups were found on more
+    // than one XCD (the host checks it)
     uint64_t att, cnt;
 } QpDecAttnArgs;
 

@@ -16,6 +16,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -404,15 +405,18 @@ struct SplitMemo {
     uint32_t k, rows, gen;
     bool valid;
 } g_split_memo = {};
+// While a graph is captured nothing runs, so a split recorded then proves nothing about the planes' contents now,
+// and a replay may overwrite them (the noalloc scratch is shared): the memo is neither used nor set during capture,
+// and graph launches invalidate it.
 int split_input(uint64_t x, uint64_t xs, uint64_t paso, uint32_t K, uint32_t rows, uint32_t tmax, bool reuse) {
     const SplitMemo& m = g_split_memo;
-    if (reuse && m.valid && m.x == x && m.xs == xs && m.paso == paso && m.k == K && m.rows == rows &&
+    if (reuse && !g_capturing && m.valid && m.x == x && m.xs == xs && m.paso == paso && m.k == K && m.rows == rows &&
         m.gen == g_ws_gen)
         return 0;
     QpSplitArgs sa = {x, xs, paso, K, rows};
     g_split_memo = {x, xs, paso, K, rows, g_ws_gen, false};
     if (int e = launch(K_split_bf16, grid_cap((uint64_t)tmax * K / 8), 1, 1, 256, 0, sa)) return e;
-    g_split_memo.valid = true;
+    g_split_memo.valid = !g_capturing;
     return 0;
 }
 
@@ -458,13 +462,21 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
                                       : 4 * wt >= 3 * (uint32_t)g_cus || (2 * wt >= (uint32_t)g_cus && K >= 8192));
             if (wide) nt = cdiv(N, 256);
             const uint32_t steps = K / 64, slots = (big ? 1 : 2) * (uint32_t)g_cus;
-            uint32_t ns = 1;
-            while (mt * nt * ns * 2 <= slots && steps / (ns * 2) >= 4) ns *= 2;
-            a.kchunk = ns > 1 ? cdiv(steps, ns) * 64 : 0;  // whole 64-input steps (the 256-token tiles take 32)
-            if (ns > 1) ns = cdiv(K, a.kchunk);
+            uint32_t ns2 = 1;  // K splits, a power of two
+            while (mt * nt * ns2 * 2 <= slots && steps / (ns2 * 2) >= 4) ns2 *= 2;
             a.rows = mt * (big ? 256 : 128);
             // the bf16 planes: 2 x 2 bytes per token row and input, K rounded up to whole 32-input chunks
-            const uint64_t xs_bytes = 4ull * a.rows * ((K + 31) / 32 * 32), ws_bytes = ns > 1 ? 4ull * ns * a.rows * N : 0;
+            const uint64_t xs_bytes = 4ull * a.rows * ((K + 31) / 32 * 32);
+            uint32_t ns;
+            uint64_t ws_bytes;
+            for (;;) {
+                a.kchunk = ns2 > 1 ? cdiv(steps, ns2) * 64 : 0;  // whole 64-input steps (the 256-token tiles take 32)
+                ns = ns2 > 1 ? cdiv(K, a.kchunk) : 1;
+                ws_bytes = ns > 1 ? 4ull * ns * a.rows * N : 0;
+                // the fixed scratch of qp_dispatch_noalloc: fewer K splits (down to none) until the partials fit
+                if (!g_noalloc || ns2 == 1 || xs_bytes + ws_bytes <= QP_SCRATCH_BYTES) break;
+                ns2 /= 2;
+            }
             uint64_t ws = 0;
             if (int e = workspace(xs_bytes + ws_bytes, &ws)) return e;
             a.xs = ws;
@@ -798,7 +810,7 @@ int op_moe(const Ctx& c, int fmt, bool down, const char* name) {
 
 // moe_router: P{e, k, kused, nw, eps, scale, norm}; [paso, w (f32 [e][k]), x, norm_w|0, logits, sel, wts, cnt].
 // The router GEMV of one token with the fused RMSNorm and the routing in one launch (QpRouterArgs); cnt: a library
-// buffer of at least 4 bytes, zero at allocation, used by this op only.
+// buffer of at least 8 bytes (the arrival counter, then the error word), zero at allocation, used by this op only.
 uint64_t buf_room(uint64_t p);
 int op_moe_router(const Ctx& c) {
     if (int e = need_bufs(c, 8, "moe_router")) return e;
@@ -826,7 +838,7 @@ int op_moe_router(const Ctx& c) {
     a.cnt = c.B(7);
     if (!a.w || !a.x || !a.logits || !a.sel || !a.wts || !a.cnt)
         return fail(QP_E_ARG, "moe_router: a required binding is missing");
-    if (buf_room(a.cnt) < 4) return fail(QP_E_ARG, "moe_router: cnt must be a library buffer");
+    if (buf_room(a.cnt) < 8) return fail(QP_E_ARG, "moe_router: cnt must be a library buffer of at least 8 bytes");
     struct Need { uint64_t p, n; const char* what; } need[] = {
         {a.w, 4ull * a.e * a.k, "the router weights"}, {a.x, 4ull * a.k, "x"}, {a.norm_w, 4ull * a.k, "norm_w"},
         {a.logits, 4ull * a.e, "logits"}, {a.sel, 4ull * a.kused, "sel"}, {a.wts, 4ull * a.kused, "wts"}};
@@ -1033,7 +1045,8 @@ int op_dec_attn(const Ctx& c) {
     a.part_ml = c.B(9);
     a.freq = c.B(10);
     // P[12] = 1: the merge of the splits in the same launch (bindings 11: o [nh][hd], 12: the counters, 8 x 128
-    // bytes, zero before the first launch; the kernel leaves them zero), for nkv * gsplit <= 8
+    // bytes, then the error word: zero before the first launch; the kernel leaves the counters zero and sets the
+    // error word only when a column's workgroups ran on more than one XCD), for nkv * gsplit <= 8
     const bool merged = c.U(12) != 0;
     // P[13]: columns per KV head of the merged form (1, 2, 4 or 8; each takes G / gsplit query heads)
     a.gsplit = merged && c.U(13) ? c.U(13) : 1;
@@ -1047,8 +1060,8 @@ int op_dec_attn(const Ctx& c) {
         a.att = c.nb > 11 ? c.B(11) : 0;
         a.cnt = c.nb > 12 ? c.B(12) : 0;
         if (!a.att || !a.cnt) return fail(QP_E_ARG, "dec_attn: the merged form needs bindings 11 (o) and 12 (counters)");
-        if (!buf_room(a.cnt) || buf_room(a.cnt) < 8 * 128)
-            return fail(QP_E_ARG, "dec_attn: the counters must be a library buffer of at least 1024 bytes");
+        if (!buf_room(a.cnt) || buf_room(a.cnt) < 8 * 128 + 4)
+            return fail(QP_E_ARG, "dec_attn: the counters must be a library buffer of at least 1028 bytes");
         if (int e = need_room(a.att, 4ull * a.nh * a.hd, "dec_attn", "the merged output")) return e;
     }
     const uint32_t Gc = G / a.gsplit;  // query heads per column
@@ -1592,6 +1605,10 @@ int qp_graph_begin(void) {
     return 0;
 }
 
+// The captured graph of each instantiated one, kept until qp_graph_free destroys both: a tool that holds on to the
+// graph's nodes from instantiation (a tracer) finds them alive for every launch.
+std::map<uint64_t, hipGraph_t> g_graphs;
+
 int qp_graph_end(uint64_t* graph) {
     NEED_INIT();
     if (!g_capturing) return fail(QP_E_CAPTURE, "no capture open");
@@ -1600,14 +1617,19 @@ int qp_graph_end(uint64_t* graph) {
     HIPCHK(hipStreamEndCapture(g_stream, &g), "hipStreamEndCapture");
     hipGraphExec_t ex;
     hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(g);
-    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    g_graphs[(uint64_t)ex] = g;
     *graph = (uint64_t)ex;
     return 0;
 }
 
 int qp_graph_launch(uint64_t graph) {
     NEED_INIT();
+    if (!g_graphs.count(graph)) return fail(QP_E_ARG, "qp_graph_launch: not a graph of this library");
+    g_split_memo.valid = false;  // a replay may rewrite the input planes
     HIPCHK(hipGraphLaunch((hipGraphExec_t)graph, g_stream), "hipGraphLaunch");
     return 0;
 }
@@ -1648,7 +1670,12 @@ int qp_graph_free(uint64_t graph) {
 #ifdef QP_TIMELINE
     tl_dump();
 #endif
+    auto it = g_graphs.find(graph);
+    if (it == g_graphs.end()) return fail(QP_E_ARG, "qp_graph_free: not a graph of this library");
+    const hipGraph_t g = it->second;
+    g_graphs.erase(it);
     HIPCHK(hipGraphExecDestroy((hipGraphExec_t)graph), "hipGraphExecDestroy");
+    HIPCHK(hipGraphDestroy(g), "hipGraphDestroy");
     return 0;
 }
 

@@ -3,6 +3,7 @@
 //
 //   node cli.js generate --model M.gguf --prompt-file ids.json --n 128 [--mode fast|ref|engine|sample] [--kv f16|f32]
 //                        [--ctx N] [--batch N] [--no-tiled] [--no-fused-ffn] [--logits-out file.f32] [--kv-out file]
+//                        [--force-ids ids.json]
 //                        [--repeat-penalty R] [--frequency-penalty F] [--presence-penalty P] [--host-loop]
 //                        [--temperature T] [--top-k K] [--top-p P] [--min-p M] [--seed S]
 //   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
@@ -105,6 +106,20 @@ async function generate(o) {
       if (toks.length >= n) break;
       lg = await modelo.forward([t], true);
     }
+  } else if (o['force-ids']) {
+    // teacher forcing on the fused one-token plan: step i consumes forced[i - 1] (step 0 is the prompt's last
+    // token) and its logits and the device's argmax are recorded, so a checker that has the forced sequence can
+    // compare every step even after a near tie sent the free-running sequences apart
+    const forzados = JSON.parse(fs.readFileSync(o['force-ids'], 'utf8'));
+    if (forzados.length < n) throw new Error('--force-ids holds ' + forzados.length + ' ids, fewer than --n');
+    escribe(logits);
+    toks.push(argmax(logits));
+    if (n > 1) {
+      const nuevos = modelo.decodificarVoraz(forzados[0], n - 1,
+        { forzar: forzados.slice(1, n - 1), porPaso: function (i, t, lg) { escribe(lg); } });
+      for (const t of nuevos) toks.push(t);
+    }
+    extra.forced = true;
   } else {
     escribe(logits);
     toks.push(argmax(logits));

@@ -47,17 +47,26 @@ function rango(url, ini, n) {
       }
       const out = Buffer.allocUnsafe(n);
       let got = 0, salto = res.statusCode === 200 ? ini : 0;   // a server without ranges sends the whole file
+      let hecho = false;
       res.on('data', function (c) {
+        if (hecho) return;
         if (salto) { const s = Math.min(salto, c.length); c = c.subarray(s); salto -= s; }
         const k = Math.min(c.length, n - got);
         c.copy(out, got, 0, k);
         got += k;
+        if (got === n && res.statusCode === 200) {
+          // the n wanted bytes are in: stop the rest of a whole-file answer instead of streaming it to the end
+          hecho = true;
+          resolve(out);
+          req.destroy();
+        }
       });
       res.on('end', function () {
+        if (hecho) return;
         if (got !== n) reject(new Error('incomplete range of ' + url + ': ' + got + ' of ' + n + ' bytes'));
         else resolve(out);
       });
-      res.on('error', reject);
+      res.on('error', function (e) { if (!hecho) reject(e); });
     });
     req.on('error', reject);
     req.end();

@@ -237,8 +237,9 @@ class ModeloTransformer {
     this.nsplit = Math.max(1, Math.min(256, Math.ceil(this.ctx / this.attnPorSplit)));
     this.partO = B(4 * this.nh * this.nsplit * this.hd, 'attn_part_o');
     this.partML = B(8 * this.nh * this.nsplit, 'attn_part_ml');
-    this.attCnt = B(8 * 128, 'attn_counters');   // the merged attention's arrival counters (kept at zero by it)
-    gpu.escribir(this.attCnt, 0, new Uint8Array(8 * 128));
+    // the merged attention's arrival counters (kept at zero by it) and its error word at byte 1024
+    this.attCnt = B(8 * 128 + 128, 'attn_counters');
+    gpu.escribir(this.attCnt, 0, new Uint8Array(8 * 128 + 128));
     // dec_attn_block: 64 workgroups per head group (two per CU of an XCD: every wavefront then has at most one
     // unit of the Q/K/V GEMV), their partials, and the op's sync words (barrier counters, XCD words, error word),
     // zero at allocation and touched by that op only
@@ -254,8 +255,8 @@ class ModeloTransformer {
       // arrival counter, zero at allocation and touched by that op only
       this.nwRouter = 1;
       while (this.nwRouter * 4 < this.nExp && this.nwRouter * 2 <= 2 * cusXcd) this.nwRouter *= 2;
-      this.routerCnt = B(4, 'router_counter');
-      gpu.escribir(this.routerCnt, 0, new Uint8Array(4));
+      this.routerCnt = B(8, 'router_counter');   // arrival counter, then the error word
+      gpu.escribir(this.routerCnt, 0, new Uint8Array(8));
     }
     this.ropeFreq = B(4 * Math.max(1, this.nrot / 2), 'rope_freq');
     gpu.escribir(this.ropeFreq, 0, tablaRope(this.base, this.nrot));
@@ -533,15 +534,38 @@ class ModeloTransformer {
       (gp === 1 || gp === 4 || (gp === 2 && this.hd === 128)) && this.D % 256 === 0 && this.D <= 8192;
   }
 
-  // The error word of dec_attn_block (a barrier wait past its bound, or a head group seen on two XCDs): the
-  // decode results are then invalid.
+  // The sync words of the fused step's launches that share counters in one XCD's L2: the error word of
+  // dec_attn_block (a barrier wait past its bound, or a head group seen on two XCDs), the merged attention's
+  // counters and error word and the MoE router's (a grid column found on more than one XCD, or an arrival count
+  // left over).  The decode results are then invalid.
   _comprobarBloque() {
-    if (!this.usaBloque) return;
     const e = new Uint32Array(1);
-    this.gpu.leer(this.syncBloque, 2112, e);
-    if (e[0]) {
-      throw new Error('dec_attn_block: ' + ((e[0] & 1) ? 'a barrier wait ran past its bound; ' : '') +
-        ((e[0] & 2) ? 'a head group ran on more than one XCD; ' : '') + 'the decode results are invalid');
+    if (this.usaBloque) {
+      this.gpu.leer(this.syncBloque, 2112, e);
+      if (e[0]) {
+        throw new Error('dec_attn_block: ' + ((e[0] & 1) ? 'a barrier wait ran past its bound; ' : '') +
+          ((e[0] & 2) ? 'a head group ran on more than one XCD; ' : '') + 'the decode results are invalid');
+      }
+    }
+    if (this.usaMerged) {
+      const w = new Uint32Array(8 * 32 + 1);
+      this.gpu.leer(this.attCnt, 0, w);
+      let resto = 0;
+      for (let i = 0; i < 8; i++) resto |= w[32 * i];
+      if (w[256] || resto) {
+        this.gpu.escribir(this.attCnt, 0, new Uint8Array(8 * 128 + 128));   // the next launch starts clean
+        throw new Error('dec_attn (merged): ' + (w[256] ? 'a column of workgroups ran on more than one XCD; ' : '') +
+          (resto ? 'arrival counters left non-zero; ' : '') + 'the decode results are invalid');
+      }
+    }
+    if (this.usaRouter) {
+      const w = new Uint32Array(2);
+      this.gpu.leer(this.routerCnt, 0, w);
+      if (w[0] || w[1]) {
+        this.gpu.escribir(this.routerCnt, 0, new Uint8Array(8));
+        throw new Error('moe_router: ' + (w[1] ? 'its workgroups ran on more than one XCD; ' : '') +
+          (w[0] ? 'arrival counter left non-zero; ' : '') + 'the routing is invalid');
+      }
     }
   }
 
@@ -555,7 +579,7 @@ class ModeloTransformer {
     const uAttM = gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', this.nsplit], ['f', this.escAtt],
       ['f', this.eps], ['f', this.base], ['u', 0], ['u', this.nrot], ['u', this.neox], ['u', this.kvF16 ? 1 : 0], ['u', this.ctx],
       ['u', 1], ['u', this.gsplitAtt]]);
-    this.usaBloque = false;
+    this.usaBloque = this.usaMerged = this.usaRouter = false;
     for (let i = 0; i < this.capas.length; i++) {
       const c = this.capas[i], gc = this.G.capas[i];
       if (this._bloqueAtt(c)) {
@@ -569,6 +593,7 @@ class ModeloTransformer {
       for (const g of this._gemvPorFormato([{ W: c.wq, mode: STORE, y: this.q }, { W: c.wk, mode: STORE, y: this.k },
         { W: c.wv, mode: STORE, y: this.v }], this.x, c.attnNorm, D)) plan.push([g, 1]);
       if (this.atencionUnida) {
+        this.usaMerged = true;
         plan.push([gpu.grupo('dec_attn', [uAttM, P, this.q, this.k, this.v, c.kc, c.vc, c.qNorm, c.kNorm, this.partO,
           this.partML, this.ropeFreq, this.att, this.attCnt]), 1]);
       } else {
@@ -589,6 +614,7 @@ class ModeloTransformer {
         if (this.enrutador && c.router.tipo === 'f32') {
           // the router GEMV and the routing in one launch (moe_router), so that the gate/up kernel reads the chosen
           // experts instead of routing in every workgroup
+          this.usaRouter = true;
           plan.push([gpu.grupo('moe_router', [gpu.uniforme([['u', E], ['u', D], ['u', K], ['u', this.nwRouter], ['f', self.eps],
             ['f', self.escExp], ['u', self.normExp ? 1 : 0]]), P, c.router.w, this.x, c.ffnNorm, this.rl, this.sel, this.wts,
             this.routerCnt]), 1]);
@@ -667,7 +693,10 @@ class ModeloTransformer {
   // Greedy continuation on the device: `primero` is the token chosen from the last logits; runs `n` one-token
   // steps (each consumes the previous token and picks the next with the reference's argmax: strict '>', lowest
   // index on ties) and returns the n new token ids.  Positions advance by n.  With porPaso, each step's logits
-  // are passed to porPaso(i, token, logits) (one readback per step, for checks).
+  // are passed to porPaso(i, token, logits) (one readback per step, for checks).  With forzar (n - 1 ids, and
+  // porPaso), step i > 0 consumes forzar[i - 1] instead of the token chosen at step i - 1 (teacher forcing for
+  // checks): the same replays, with the step's input id written from the host; the returned ids are still the
+  // device's choices.
   decodificarVoraz(primero, n, opciones) {
     opciones = opciones || {};
     if (n < 1) return [];
@@ -679,9 +708,15 @@ class ModeloTransformer {
     gpu.escribir(this.bPaso, 0, new Uint32Array([1, this.pos, 0, 0]));
     gpu.escribir(this.bIds, 0, new Uint32Array([primero]));
     gpu.escribir(this.contador, 0, new Uint32Array([0, 0, 0, 0]));
+    const forzar = opciones.forzar || null;
+    if (forzar && (!opciones.porPaso || forzar.length < n - 1)) throw new Error('forzar needs porPaso and n - 1 ids');
     if (opciones.porPaso) {
       const lg = new Float32Array(this.vocab), t = new Uint32Array(1);
       for (let i = 0; i < n; i++) {
+        if (forzar && i > 0) {
+          if (!(forzar[i - 1] >= 0 && forzar[i - 1] < this.vocab)) throw new Error('forced id outside the vocabulary');
+          gpu.escribir(this.bIds, 0, new Uint32Array([forzar[i - 1]]));
+        }
         this._pasos(1);
         gpu.leer(this.logits, 0, lg);
         gpu.leer(this.bIds, 0, t);
@@ -702,7 +737,7 @@ class ModeloTransformer {
     this._comprobarBloque();
     this.pos += n;
     this.hist.push(primero);                                    // the n processed ids: primero and out[0..n-2]
-    for (let i = 0; i + 1 < n; i++) this.hist.push(out[i]);
+    for (let i = 0; i + 1 < n; i++) this.hist.push(forzar ? forzar[i] : out[i]);
     return Array.from(out);
   }
 

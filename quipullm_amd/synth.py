@@ -14,6 +14,8 @@ the configurations specify, so no quantizer is needed:
 * Q6_K (210 B): 6-bit quants uniform 0..63 (ql/qh bytes uniform); int8 sub-scales uniform in [-64, 63];
   d f16 |N(0, 0.01)|.
 * F32 vectors (norms, f32 embeddings): N(1, 0.02); the f32 MoE router: N(0, 0.02).
+* F16 / BF16 matrices: N(0, wstd) (0.02 when unset) rounded to the nearest half / bfloat16 (ties to even);
+  F16 embeddings of a centered model N(0, 1).
 
 Test variants marked `centered` make the weights zero-mean, so that greedy decoding does not collapse onto
 one token: Q4_K blocks get mins equal to their scales and dmin = f16(7.5 d) (the mean nibble is 7.5; Q5_K: 15.5), and
@@ -32,7 +34,8 @@ import numpy as np
 
 GGML_F32, GGML_Q8_0, GGML_Q2_K, GGML_Q3_K, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 0, 8, 10, 11, 12, 13, 14
 GGML_IQ4_NL = 20
-BLOCK = {GGML_F32: (1, 4), GGML_Q8_0: (32, 34), GGML_Q2_K: (256, 84), GGML_Q3_K: (256, 110), GGML_Q4_K: (256, 144),
+GGML_F16, GGML_BF16 = 1, 30
+BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_BF16: (1, 2), GGML_Q8_0: (32, 34), GGML_Q2_K: (256, 84), GGML_Q3_K: (256, 110), GGML_Q4_K: (256, 144),
          GGML_Q5_K: (256, 176), GGML_Q6_K: (256, 210), GGML_IQ4_NL: (32, 18)}
 ALIGN = 32
 
@@ -61,6 +64,7 @@ class ModelConfig:
     ctx: int = 4096
     centered: bool = False    # zero-mean weights (test variants; see gen_blocks)
     wstd: float = 0.0         # > 0: K-quant block scales drawn so the weights' standard deviation is about wstd
+    flat_d: bool = False      # centered Q4_K: one d for every block (rows of nearly equal norm; see gen_blocks)
     post_norms: bool = False  # post_attention_norm / post_ffw_norm per layer (gemma3)
     extra_kv: tuple = ()      # further (key after "<arch>.", gguf value type, value) entries
 
@@ -99,6 +103,15 @@ CONFIGS = {
     # shape in 4 layers
     "llama8b_q4km_c2": ModelConfig("llama8b_q4km_c2", "llama", 2, 4096, 32, 8, 128, 14336, 128256, 1e-5, 500000.0,
                                    _q4km(), ctx=4400, centered=True, wstd=0.02),
+    # the 8B shape at full depth, centered with weights of standard deviation 0.02: the timed decode path (f16 KV at
+    # ctx 4096) checked end to end with varied greedy ids, and the full-depth fixture at ctx 512
+    "llama8b_q4km_c": ModelConfig("llama8b_q4km_c", "llama", 32, 4096, 32, 8, 128, 14336, 128256, 1e-5, 500000.0,
+                                  _q4km(), ctx=4400, centered=True, wstd=0.02),
+    # the MoE shape at full depth, centered with weights of standard deviation 0.1 (full-depth fixture; at 0.02 the
+    # context-averaged attention outweighs the experts and greedy decoding cycles through a few tokens)
+    "qwen3moe_q4k_c": ModelConfig("qwen3moe_q4k_c", "qwen3moe", 48, 2048, 32, 4, 128, 0, 151936, 1e-6, 1000000.0,
+                                  {"default": GGML_Q4_K}, n_exp=128, n_used=8, ffe=768, qk_norm=True, ctx=2400,
+                                  centered=True, wstd=0.1),
     "qwen3moe_q4k_c4": ModelConfig("qwen3moe_q4k_c4", "qwen3moe", 4, 2048, 32, 4, 128, 0, 151936, 1e-6, 1000000.0,
                                    {"default": GGML_Q4_K}, n_exp=128, n_used=8, ffe=768, qk_norm=True, ctx=2400,
                                    centered=True, wstd=0.02),
@@ -142,6 +155,13 @@ CONFIGS = {
     "mini_llama_q3k_c": ModelConfig("mini_llama_q3k_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
                                     {"default": GGML_Q3_K, "attn_v": GGML_Q5_K, "output": GGML_Q6_K}, ctx=512,
                                     centered=True),
+    # F16 and BF16 matrices (the reference widens them to f32 at upload, weights.js:127-133): F16 embeddings, q, k
+    # and wo; BF16 v, ffn_down and output; Q4_K gate/up
+    "mini_llama_f16_c": ModelConfig("mini_llama_f16_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
+                                    {"default": GGML_Q4_K, "token_embd": GGML_F16, "attn_q": GGML_F16,
+                                     "attn_k": GGML_F16, "attn_output": GGML_F16, "attn_v": GGML_BF16,
+                                     "ffn_down": GGML_BF16, "output": GGML_BF16}, ctx=512, centered=True,
+                                    wstd=0.02),
     "mini_llama_q2k_c": ModelConfig("mini_llama_q2k_c", "llama", 2, 512, 8, 2, 64, 768, 1000, 1e-5, 500000.0,
                                     {"default": GGML_Q2_K, "ffn_down": GGML_Q3_K, "output": GGML_Q6_K}, ctx=512,
                                     centered=True),
@@ -213,10 +233,20 @@ def pack_q4k_scales(sc, mn):
 _STD_PER_SIGMA = {GGML_Q4_K: 36.4 * 4.61, GGML_Q5_K: 36.4 * 9.23, GGML_Q6_K: 36.9 * 18.5}
 
 
-def gen_blocks(rng, gtype, nelem, kind="w", centered=False, wstd=0.0):
+def gen_blocks(rng, gtype, nelem, kind="w", centered=False, wstd=0.0, flat_d=False):
     """Bytes of one tensor of `nelem` elements.  wstd > 0 (Q4_K, Q5_K centered and Q6_K): the d scales' sigma
-    is chosen so that the weights' standard deviation is about wstd, instead of the configs' 0.01."""
+    is chosen so that the weights' standard deviation is about wstd, instead of the configs' 0.01.  flat_d
+    (centered Q4_K): every block's d is that sigma instead of |N(0, sigma)|, so that the rows' norms vary little
+    and no row outweighs the others in every argmax (greedy sequences that wander instead of repeating a few
+    tokens)."""
     sig = np.float32(wstd / _STD_PER_SIGMA[gtype]) if wstd > 0 and gtype in _STD_PER_SIGMA else 0.01
+    if gtype in (GGML_F16, GGML_BF16):
+        sd = np.float32(1.0 if (kind == "embd" and centered) else (wstd or 0.02))
+        a = rng.standard_normal(nelem, dtype=np.float32) * sd
+        if gtype == GGML_F16:
+            return a.astype("<f2").tobytes()
+        u = a.view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype("<u2").tobytes()
     if gtype == GGML_F32:
         if kind == "embd" and centered:
             a = rng.standard_normal(nelem, dtype=np.float32)
@@ -244,6 +274,8 @@ def gen_blocks(rng, gtype, nelem, kind="w", centered=False, wstd=0.0):
     blk = np.frombuffer(rng.bytes(nb * bpb), np.uint8).reshape(nb, bpb).copy()
     if gtype in (GGML_Q4_K, GGML_Q5_K):
         d = _abs_normal_f16(rng, nb, sig)
+        if flat_d and centered:
+            d = np.full(nb, sig, np.float32).astype(np.float16)
         blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         if centered:
             mean = np.float32(7.5 if gtype == GGML_Q4_K else 15.5)
@@ -348,7 +380,7 @@ def write_gguf(path: str, c: ModelConfig, seed: int = 0) -> str:
                 f.write(b"\0" * (o - pos))
                 pos = o
             rng = np.random.default_rng([seed, i])
-            data = gen_blocks(rng, gtype, int(np.prod(dims)), kind, c.centered, c.wstd)
+            data = gen_blocks(rng, gtype, int(np.prod(dims)), kind, c.centered, c.wstd, c.flat_d)
             f.write(data)
             pos += len(data)
     os.replace(tmp, path)

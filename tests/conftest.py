@@ -23,6 +23,18 @@ def pytest_sessionstart(session):
                                 stdout=subprocess.PIPE, text=True)
 
 
+# One line per end-to-end parity case (steps compared, distinct ids, ties, errors), printed at the end of the run
+# so that the short summary of a quiet run shows how much each case checked.
+E2E_SUMMARY = []
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    if E2E_SUMMARY:
+        terminalreporter.section("end-to-end parity")
+        for line in E2E_SUMMARY:
+            terminalreporter.write_line(line)
+
+
 def pytest_sessionfinish(session, exitstatus):
     if _spawner is not None:
         _spawner.stdin.close()

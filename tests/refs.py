@@ -178,6 +178,10 @@ def dequant(fmt, raw):
         return dequant_q8_0(raw)
     if fmt == IQ4_NL:
         return dequant_iq4_nl(raw)
+    if fmt == 1:   # F16
+        return raw.view(np.float16).astype(np.float32)
+    if fmt == 30:  # BF16: the upper half of a float32
+        return (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
     return raw.view(np.float32).copy()
 
 
@@ -379,3 +383,19 @@ def v_rows(tiled, rows, kvd):
     """Inverse of v_tiled: rows [rows][kvd]."""
     t = np.asarray(tiled).reshape(-1, kvd, 32)[:, :, [vt_pos(k) for k in range(32)]]
     return t.transpose(0, 2, 1).reshape(-1, kvd)[:rows]
+
+
+def read_kv_f16(path, n_layers, ctx, kvd, npos):
+    """The f16 KV cache that `cli.js generate --kv-out` wrote (per layer: K rows [ctx][kvd], then the V cache in
+    32-slot tiles), as uint16 [n_layers][npos][kvd] arrays of K and V rows."""
+    raw = np.memmap(path, np.uint16, "r")
+    kn, vn = ctx * kvd, -(-ctx // 32) * 32 * kvd
+    assert raw.size == n_layers * (kn + vn), (raw.size, n_layers, kn, vn)
+    ks = np.empty((n_layers, npos, kvd), np.uint16)
+    vs = np.empty((n_layers, npos, kvd), np.uint16)
+    nt = -(-npos // 32)
+    for i in range(n_layers):
+        base = i * (kn + vn)
+        ks[i] = raw[base:base + kn].reshape(ctx, kvd)[:npos]
+        vs[i] = v_rows(raw[base + kn:base + kn + nt * 32 * kvd], npos, kvd)
+    return ks, vs

@@ -123,3 +123,52 @@ m.correr({ parar: function () { return Date.now() - t0 > 500; } }).then(function
     assert rc == 0, err
     r = json.loads(out.strip().splitlines()[-1])
     assert r["r"] == "parado" and r["logs"] == 1  # one message for a run of failures
+
+
+def test_range_read_stops_a_whole_file_answer(tmp_path):
+    """rango() against a server that ignores Range and answers 200 with the whole file: the wanted bytes come back
+    exact, and the transfer is stopped once they are in (the server gets to write only a small part of the 256 MB
+    body instead of streaming it to the end)."""
+    import http.server
+    import threading
+    size, chunk = 256 << 20, 1 << 16
+    pat = bytes(range(256)) * (chunk // 256)
+    sent = []
+
+    class H(http.server.BaseHTTPRequestHandler):
+        def log_message(self, *a):
+            pass
+
+        def do_GET(self):
+            self.send_response(200)
+            self.send_header("Content-Type", "application/octet-stream")
+            self.send_header("Content-Length", str(size))
+            self.end_headers()
+            n = 0
+            try:
+                while n < size:
+                    self.wfile.write(pat)
+                    n += chunk
+            except OSError:
+                pass
+            sent.append(n)
+
+    srv = http.server.ThreadingHTTPServer(("127.0.0.1", 0), H)
+    th = threading.Thread(target=srv.serve_forever, daemon=True)
+    th.start()
+    try:
+        url = "http://127.0.0.1:%d/file" % srv.server_address[1]
+        script = ("const { rango } = require(%r);\n"
+                  "rango(%r, 1000, 5000).then(function (b) { console.log(JSON.stringify(Array.from(b))); },\n"
+                  "  function (e) { console.error(e.stack); process.exit(1); });\n") % (os.path.join(JS, "http.js"), url)
+        rc, out, err = run(["node", "-e", script], timeout=60)
+        assert rc == 0, err[-2000:]
+        got = json.loads(out.strip().splitlines()[-1])
+        assert got == [(1000 + i) % 256 for i in range(5000)]
+        for _ in range(100):
+            if sent:
+                break
+            threading.Event().wait(0.05)
+        assert sent and sent[0] < size // 4, sent
+    finally:
+        srv.shutdown()

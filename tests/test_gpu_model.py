@@ -16,6 +16,7 @@ import os
 import numpy as np
 import pytest
 
+import refs
 from conftest import ROOT, run
 from quipullm_amd import build, synth
 
@@ -26,7 +27,7 @@ CLI = os.path.join(ROOT, "quipullm_amd", "js", "cli.js")
 MINI = ["mini_llama_q4km_c", "mini_llama_q5km_c", "mini_qwen3moe_q5k_c", "mini_llama_q3k_c", "mini_llama_q2k_c",
         "mini_llama_q8_c", "mini_qwen3_q4km_c", "mini_llama_iq4nl_c", "mini_qwen3moe_iq4nl_c",
         "mini_qwen3moe_q4k_c", "mini_llama_q4km",
-        "mini_qwen3moe_q4k"]
+        "mini_qwen3moe_q4k", "mini_llama_f16_c"]
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -66,31 +67,13 @@ def oracle_run(oracle, path, prompt, n, kv_f16, kv_ref=None, ctx=256):
     return ids, lgs
 
 
-def vt_pos(k):
-    """Position of slot k (0..31) in a 32-slot tile of the f16 value cache (quipullm_amd/csrc/kernels/qp_common.h)."""
-    return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3)
-
-
-def read_kv_f16(path, n_layers, ctx, kvd, npos):
-    """The f16 KV cache that `cli.js generate --kv-out` wrote (per layer: K rows [ctx][kvd], then the V cache in
-    32-slot tiles), as uint16 [n_layers][npos][kvd] arrays of K and V rows."""
-    raw = np.fromfile(path, np.uint16)
-    kn, vn = ctx * kvd, -(-ctx // 32) * 32 * kvd
-    assert raw.size == n_layers * (kn + vn), (raw.size, n_layers, kn, vn)
-    s = np.arange(npos)
-    vidx = ((s // 32)[:, None] * kvd + np.arange(kvd)[None, :]) * 32 + np.array([vt_pos(k) for k in s % 32])[:, None]
-    ks, vs = [], []
-    for i in range(n_layers):
-        base = i * (kn + vn)
-        ks.append(raw[base:base + kn].reshape(ctx, kvd)[:npos])
-        vs.append(raw[base + kn:base + kn + vn][vidx])
-    return np.stack(ks), np.stack(vs)
+read_kv_f16 = refs.read_kv_f16
 
 
 @pytest.mark.parametrize("name", ["mini_llama_q4km_c", "mini_llama_q5km_c", "mini_llama_q3k_c", "mini_llama_q2k_c",
                                   "mini_llama_q8_c", "mini_qwen3_q4km_c",
                                   "mini_qwen3moe_q4k_c", "mini_qwen3moe_q5k_c", "mini_llama_iq4nl_c",
-                                  "mini_qwen3moe_iq4nl_c", "mini_gemma3_q4km_c"])
+                                  "mini_qwen3moe_iq4nl_c", "mini_gemma3_q4km_c", "mini_llama_f16_c"])
 @pytest.mark.parametrize("plen", [150, 300])
 def test_long_prefill_on_matrix_cores_matches_oracle(oracle, models_dir, tmp_path, name, plen):
     """A 150- or 300-token prompt in one chunk runs the prefill matmuls on MFMA (bf16 hi/lo products; from 256

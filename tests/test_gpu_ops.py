@@ -611,14 +611,15 @@ def test_moe_router(quipu, dev, oracle, E, k, D, nw, norm):
     by the last of them to finish.  Logits within 2e-5 sum |w x| of the oracle's rmsnorm + matmul; sel and wts
     the oracle's moe_topk of those logits (sel exact, an exact tie at the top to the lower expert; wts within
     2e-6), over three
-    launches in a row (the arrival counter only grows); then moe_gate_up with the routing read from sel (P[7] = 1)
+    launches in a row (the last arrival resets the counter; the error word stays clear); then moe_gate_up with the
+    routing read from sel (P[7] = 1)
     and moe_down give bit-identical results to moe_gate_up routing from the same logits itself."""
     rng = np.random.default_rng([E, k, D])
     W = (0.02 * rng.standard_normal((E, D))).astype(np.float32)
     W[E - 3] = W[5]  # rows 5 and E - 3 equal: an exact tie of their logits
     nw_ = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
     eps, scale = 1e-6, 1.0 if norm else 2.5
-    hw, hn, lg, sel, wts, cnt = dev.buf(W), dev.buf(nw_), dev.zeros(E * 4), dev.zeros(k * 4), dev.zeros(k * 4), dev.zeros(4)
+    hw, hn, lg, sel, wts, cnt = dev.buf(W), dev.buf(nw_), dev.zeros(E * 4), dev.zeros(k * 4), dev.zeros(k * 4), dev.zeros(8)
     u = [("u", E), ("u", D), ("u", k), ("u", nw), ("f", eps), ("f", scale), ("u", norm)]
     for call in range(3):
         x = rng.standard_normal(D).astype(np.float32)
@@ -638,7 +639,7 @@ def test_moe_router(quipu, dev, oracle, E, k, D, nw, norm):
         np.testing.assert_allclose(dev.get(wts, (k,)), w_want, rtol=2e-6, atol=1e-7)
         if call == 1:
             assert list(s_want[:2]) == [5, E - 3]
-    assert dev.get(cnt, (1,), np.uint32)[0] == 3 * nw
+    assert list(dev.get(cnt, (2,), np.uint32)) == [0, 0]
     if D % 256 or E * 64 * D * 0.5625 > 2 ** 30:
         return
     # the expert FFN from the router's routing: presel against routing in moe_gate_up, bit for bit
@@ -663,7 +664,7 @@ def test_moe_router(quipu, dev, oracle, E, k, D, nw, norm):
 
 def test_moe_router_rejections(quipu, dev):
     """Shapes and bindings the kernel cannot take are refused on the host."""
-    b = [dev.zeros(16 * 512 * 4), dev.zeros(2048), dev.zeros(2048), dev.zeros(64), dev.zeros(64), dev.zeros(64), dev.zeros(4)]
+    b = [dev.zeros(16 * 512 * 4), dev.zeros(2048), dev.zeros(2048), dev.zeros(64), dev.zeros(64), dev.zeros(64), dev.zeros(8)]
     for u3, msg in [((16, 512, 4, 3), "nw=3"), ((300, 512, 4, 4), "300 experts"), ((16, 512, 20, 4), "20 experts used"),
                     ((16, 510, 4, 4), "k=510"), ((16, 512, 4, 256), "nw=256")]:
         u = [("u", v) for v in u3] + [("f", 1e-6), ("f", 1.0), ("u", 1)]
@@ -1052,12 +1053,12 @@ def test_dec_attn_merged(quipu, dev, hd, nh, nkv, pos0, nsplit, f16, neox, qk_no
              dev.buf(kn) if qk_norm else 0, po, pml, dev.buf(rope_table(1e6, hd))]
         outs = []
         if merged:
-            cnt = dev.zeros(8 * 128)
+            cnt = dev.zeros(8 * 128 + 128)
             for _ in range(3):
                 quipu.upload(o, np.full(nh * hd, np.nan, np.float32))
                 quipu.dispatch("dec_attn", u + [("u", 1), ("u", gsplit)], b + [o, cnt], (1, 1, 1))
                 outs.append(dev.get(o, (nh * hd,)))
-            assert np.all(dev.get(cnt, (8 * 32,), np.uint32) == 0)
+            assert np.all(dev.get(cnt, (8 * 32 + 1,), np.uint32) == 0)  # counters back at zero, error word clear
         else:
             quipu.dispatch("dec_attn", u, b)
             quipu.dispatch("dec_attn_comb", [("u", hd), ("u", nh), ("u", nsplit)], [paso, po, pml, o])
@@ -1217,7 +1218,7 @@ def test_dec_attn_merged_rejections(quipu, dev):
     group, the output and a counter buffer of this library."""
     hd, nh, nkv, rows = 64, 16, 16, 64
     b = [dev.paso(1, 3)] + [dev.zeros(4 * nh * hd)] * 3 + [dev.zeros(4 * rows * nkv * hd)] * 2 + [0, 0] + \
-        [dev.zeros(4 * nh * hd), dev.zeros(8 * nh), 0, dev.zeros(4 * nh * hd), dev.zeros(1024)]
+        [dev.zeros(4 * nh * hd), dev.zeros(8 * nh), 0, dev.zeros(4 * nh * hd), dev.zeros(1028)]
     u = [("u", hd), ("u", nh), ("u", nkv), ("u", 1), ("f", 0.125), ("f", 1e-6), ("f", 1e4), ("u", 0), ("u", hd),
          ("u", 0), ("u", 0), ("u", rows), ("u", 1)]
     with pytest.raises(capi.QuipuError, match="at most 8 columns"):
@@ -1226,8 +1227,85 @@ def test_dec_attn_merged_rejections(quipu, dev):
     for g, msg in ((2, "at most 8 columns"), (3, "gsplit=3"), (4, "does not divide")):
         with pytest.raises(capi.QuipuError, match=msg):
             quipu.dispatch("dec_attn", u + [("u", g)], b)
-    with pytest.raises(capi.QuipuError, match="at least 1024 bytes"):
-        quipu.dispatch("dec_attn", u, b[:12] + [dev.zeros(512)])
+    with pytest.raises(capi.QuipuError, match="at least 1028 bytes"):
+        quipu.dispatch("dec_attn", u, b[:12] + [dev.zeros(1024)])
+
+
+def test_xcd_placement_checks_fire_and_recover(quipu, dev):
+    """The merged attention and moe_router count arrivals in their XCD's L2 and rely on every workgroup of a grid
+    column running on one XCD.  Each arrival adds 1 + (XCD id << 16) to the column's counter and the last one checks
+    the sum, so a column spread over XCDs sets the op's error word instead of failing silently.  Forced from the host:
+    a counter seeded with an arrival from a foreign XCD (high half 1, count 0) makes the last arrival's check fire
+    while the results stay exact (the merge and the routing still run), and the counter is reset, so the next launch
+    is exact with the error word clear; a counter seeded with a full launch's arrivals left over (every later count
+    past the grid) fires too.  Every kernel ends normally in all cases."""
+    # merged attention: the 8B shapes at position 4095, 17 splits, f16 cache
+    hd, nh, nkv, pos0, nsplit, rows = 128, 32, 8, 4095, 17, 4100
+    kvd = nkv * hd
+    rng = np.random.default_rng(31)
+    kc = f16r(rng.standard_normal((rows, kvd)).astype(np.float32))
+    vc = f16r(rng.standard_normal((rows, kvd)).astype(np.float32))
+    u = [("u", hd), ("u", nh), ("u", nkv), ("u", nsplit), ("f", float(np.float32(1 / np.sqrt(hd)))), ("f", 1e-6),
+         ("f", 5e5), ("u", 0), ("u", hd), ("u", 0), ("u", 1), ("u", rows), ("u", 1), ("u", 1)]
+    q, k, v = (rng.standard_normal(n).astype(np.float32) for n in (nh * hd, kvd, kvd))
+    kcb, vcb = dev.buf(kc.astype(np.float16)), dev.buf(refs.v_tiled(vc.astype(np.float16), kvd))
+    po, pml, o, cnt = dev.zeros(nh * nsplit * hd * 4), dev.zeros(nh * nsplit * 8), dev.zeros(nh * hd * 4), \
+        dev.zeros(8 * 128 + 128)
+    b = [dev.paso(1, pos0), dev.buf(q), dev.buf(k), dev.buf(v), kcb, vcb, 0, 0, po, pml, dev.buf(rope_table(5e5, hd)),
+         o, cnt]
+
+    def attn(seed=None):
+        if seed is not None:
+            quipu.upload(cnt, np.array([seed if i % 32 == 0 and i < 256 else 0 for i in range(8 * 32 + 1)], np.uint32))
+        quipu.upload(o, np.full(nh * hd, np.nan, np.float32))
+        quipu.dispatch("dec_attn", u, b, (1, 1, 1))
+        w = dev.get(cnt, (8 * 32 + 1,), np.uint32)
+        return dev.get(o, (nh * hd,)), int(w[256]), [int(w[32 * i]) for i in range(8)]
+
+    want, err, c = attn()
+    assert err == 0 and c == [0] * 8 and np.isfinite(want).all()
+    got, err, c = attn(seed=1 << 16)          # a foreign XCD's arrival in every column
+    assert err == 1 and c == [0] * 8
+    np.testing.assert_array_equal(got, want)
+    got, err, c = attn(seed=0)                # error word cleared by the host: the next launch is exact and clean
+    assert err == 0 and c == [0] * 8
+    np.testing.assert_array_equal(got, want)
+    _, err, _ = attn(seed=nsplit)             # a full launch's arrivals left over: every count passes the grid
+    assert err == 1
+    got, err, c = attn(seed=0)
+    assert err == 0 and c == [0] * 8
+    np.testing.assert_array_equal(got, want)
+
+    # moe_router: 128 experts, 32 workgroups
+    E, kk, D, nw = 128, 8, 2048, 32
+    W = (0.02 * rng.standard_normal((E, D))).astype(np.float32)
+    x = rng.standard_normal(D).astype(np.float32)
+    lg, sel, wts, rc = dev.zeros(E * 4), dev.zeros(kk * 4), dev.zeros(kk * 4), dev.zeros(8)
+    ur = [("u", E), ("u", D), ("u", kk), ("u", nw), ("f", 1e-6), ("f", 1.0), ("u", 1)]
+    br = [dev.paso(1, 0), dev.buf(W), dev.buf(x), dev.buf(np.ones(D, np.float32)), lg, sel, wts, rc]
+
+    def route(seed):
+        quipu.upload(rc, np.array([seed, 0], np.uint32))
+        quipu.upload(sel, np.full(kk, 0xffffffff, np.uint32))
+        quipu.dispatch("moe_router", ur, br, (8, nw, 1))
+        w = dev.get(rc, (2,), np.uint32)
+        return dev.get(sel, (kk,), np.uint32), dev.get(wts, (kk,)), int(w[1]), int(w[0])
+
+    s0, w0, err, c = route(0)
+    assert err == 0 and c == 0 and np.all(s0 < E)
+    s1, w1, err, c = route(1 << 16)
+    assert err == 1 and c == 0
+    np.testing.assert_array_equal(s1, s0)
+    np.testing.assert_array_equal(w1, w0)
+    s1, w1, err, c = route(0)
+    assert err == 0 and c == 0
+    np.testing.assert_array_equal(s1, s0)
+    _, _, err, _ = route(nw)
+    assert err == 1
+    s1, w1, err, c = route(0)
+    assert err == 0 and c == 0
+    np.testing.assert_array_equal(s1, s0)
+    np.testing.assert_array_equal(w1, w0)
 
 
 @pytest.mark.parametrize("pos0", [4, 40, 700])

@@ -40,6 +40,31 @@ def test_f16_rounding_matches_numpy(oracle):
     assert oracle.f16_from(float("nan")) & 0x7c00 == 0x7c00 and oracle.f16_from(float("nan")) & 0x3ff
 
 
+def test_f16_bf16_matrix_widening(oracle):
+    """or_dequant of F16 / BF16 matrices (the reference widens them to f32 at upload, weights.js:127-133): every
+    one of the 65536 bit patterns of each.  F16 against numpy's float16; BF16 against the value its fields define,
+    computed in float64 (sign, 8-bit exponent with bias 127, 7-bit fraction, subnormals at 2^-126, all-ones
+    exponent inf / NaN), plus known answers."""
+    h = np.arange(65536, dtype=np.uint16)
+    got = oracle.dequant(oracle.F16, h.view(np.uint8), 65536)
+    ref = h.view(np.float16).astype(np.float32)
+    fin = ~np.isnan(ref)
+    np.testing.assert_array_equal(got.view(np.uint32)[fin], ref.view(np.uint32)[fin])
+    assert np.isnan(got[~fin]).all()
+    with np.errstate(invalid="ignore"):  # signalling NaN patterns
+        got = oracle.dequant(oracle.BF16, h.view(np.uint8), 65536).astype(np.float64)
+    s, e, f = (h >> 15).astype(np.float64), ((h >> 7) & 255).astype(np.int64), (h & 127).astype(np.float64)
+    mag = np.where(e == 0, np.ldexp(f / 128.0, -126), np.ldexp(1.0 + f / 128.0, (e - 127).clip(-200, 200)))
+    mag = np.where(e == 255, np.where(f == 0, np.inf, np.nan), mag)
+    want = np.where(s == 1, -mag, mag)
+    fin = ~np.isnan(want)
+    np.testing.assert_array_equal(got[fin], want[fin])
+    assert np.isnan(got[~fin]).all()
+    kat = np.array([0x3F80, 0xC000, 0x4049, 0x0001, 0x7F80, 0x8000], np.uint16)
+    np.testing.assert_array_equal(oracle.dequant(oracle.BF16, kat.view(np.uint8), 6),
+                                  np.array([1.0, -2.0, 3.140625, 2.0 ** -133, np.inf, -0.0], np.float32))
+
+
 @pytest.mark.parametrize("fmt,n", [(refs.Q2_K, 256 * 300), (refs.Q3_K, 256 * 300), (refs.Q4_K, 256 * 300),
                                    (refs.Q5_K, 256 * 300), (refs.Q6_K, 256 * 300), (refs.Q8_0, 32 * 500),
                                    (refs.IQ4_NL, 32 * 500)])
@@ -366,7 +391,8 @@ def test_argmax_ties_nan(oracle):
                                        ("mini_llama_q2k_c", 0), ("mini_qwen3_q4km_c", 1),
                                        ("mini_qwen3moe_q5k_c", 1), ("mini_qwen3moe_q4k_c", 1),
                                        ("mini_llama_q8_c", 0), ("mini_llama_iq4nl_c", 0),
-                                       ("mini_qwen3moe_iq4nl_c", 1), ("mini_gemma3_q4km_c", 1)])
+                                       ("mini_qwen3moe_iq4nl_c", 1), ("mini_gemma3_q4km_c", 1),
+                                       ("mini_llama_f16_c", 0)])
 def test_model_forward_vs_float64(oracle, models_dir, name, neox):
     # float32 rounding, amplified by near-ties of the large activations of the centered models, stays below these
     # bounds; a semantic slip (RoPE pairing, norm placement, GQA head map, missing residual) is O(0.1)
@@ -439,3 +465,49 @@ def test_gguf_roundtrip(oracle, models_dir):
     assert g.kv["general.architecture"] == "qwen3moe"
     assert g.kv["qwen3moe.expert_count"] == 16 and g.kv["qwen3moe.expert_weights_norm"] is True
     assert len(g.kv["tokenizer.ggml.tokens"]) == c.vocab
+
+
+def test_resume_from_reference_cache_is_bit_exact(oracle, models_dir):
+    """resume_from_reference (the entry the long-context GPU check uses): a run that prefills P - 1 tokens, then
+    takes token P - 1 and 8 greedy steps one token at a time (f16 cache), and a second model given the first run's
+    own cache rows and resumed at position P - 1, must produce the same logits bit for bit and the same ids.  The
+    resumed model really reads the rows it was given: the value rows of the positions before P - 1 scaled by 1.5
+    give other logits."""
+    path = synth.ensure_model("mini_llama_q4km_c", models_dir)
+    P, n = 40, 8
+    a = oracle.Model(path, ctx=64, kv_f16=True)
+    prompt = synth.random_prompt(a.vocab, P, 5)
+    a.forward(prompt[:-1], False)
+    lg = a.forward([prompt[-1]], True)
+    want_lg, want_ids = [lg], []
+    for i in range(n):
+        want_ids.append(oracle.argmax(lg))
+        if i + 1 < n:
+            lg = a.forward([want_ids[-1]], True)
+            want_lg.append(lg)
+    k16, v16 = a.kv_cache_f16(P + n - 1)
+    a.close()
+
+    def resumed(k, v):
+        b = oracle.Model(path, ctx=64, kv_f16=True)
+        b.set_kv_reference(k, v)
+        b.resume_from_reference(P - 1)
+        assert b.pos == P - 1
+        lg = b.forward([prompt[-1]], True)
+        lgs, ids = [lg], []
+        for i in range(n):
+            ids.append(oracle.argmax(lg))
+            if i + 1 < n:
+                lg = b.forward([ids[-1]], True)
+                lgs.append(lg)
+        b.close()
+        return lgs, ids
+
+    got_lg, got_ids = resumed(k16, v16)
+    assert got_ids == want_ids
+    for g, w in zip(got_lg, want_lg):
+        np.testing.assert_array_equal(g.view(np.uint32), w.view(np.uint32))
+    v2 = v16.copy()
+    v2[:, :P - 1] = (v2[:, :P - 1].view(np.float16) * np.float16(1.5)).view(np.uint16)
+    other, _ = resumed(k16, v2)
+    assert not np.array_equal(other[0], want_lg[0])
