@@ -1075,10 +1075,22 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
         }
     };
     issue(buf, 0);
+    // an accumulating segment: the y value each lane adds its first unit's output to is loaded now, behind the
+    // weights, so that the stores at the end do not wait for a load (lane L < R S holds output L of the unit: row
+    // u R S + L).  One load per lane always (past the rows: offset out of range, no traffic), so the wait below
+    // counts it.
+    float ypre;
+    {
+        const KSeg sg0 = seg_at(seg_of(w));
+        const uint32_t lr = (w - sg0.u0) * R * S + lane;
+        const bool on = nmine > 0 && sg0.mode == QP_GEMV_ACC && lane < R * S && lr < sg0.n;
+        ypre = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(kq_rsrc(sg0.y, 4ull * sg0.n), on ? 4 * lr : 0x80000000u, 0, 0));
+    }
     __builtin_amdgcn_sched_barrier(0);
     {
         // the x loads are the oldest in flight: wait for them alone
-        constexpr int n = R * KQ<FMT>::LOADS + EXTRA > 63 ? 63 : R * KQ<FMT>::LOADS + EXTRA;
+        constexpr int n = R * KQ<FMT>::LOADS + EXTRA + 1 > 63 ? 63 : R * KQ<FMT>::LOADS + EXTRA + 1;
         __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8));
     }
     tl_ph(TLK, 1);  // input arrived
@@ -1138,6 +1150,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
     constexpr int NO = 2;  // deferred outputs: lane L of register k holds output L + 64k of this wave
     float outv[NO];
     uint32_t outk[NO];     // segment << 28 | row within the segment
+    uint32_t pre = 0;      // bit k: outv[k] already holds y + the output (an accumulating first unit)
 #pragma unroll
     for (int k = 0; k < NO; k++) {
         outv[k] = 0.0f;
@@ -1152,7 +1165,7 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
             for (int k = 0; k < NO; k++) {
                 if (lane + 64 * k < nout && outk[k] != 0xffffffffu && (outk[k] >> 28) == si) {
                     QP_GLOBAL float* y = reinterpret_cast<QP_GLOBAL float*>(sg.y) + (outk[k] & 0x0fffffffu);
-                    *y = sg.mode == QP_GEMV_ACC ? *y + outv[k] : outv[k];
+                    *y = (sg.mode == QP_GEMV_ACC && !((pre >> k) & 1u)) ? *y + outv[k] : outv[k];
                 }
             }
         }
@@ -1219,7 +1232,10 @@ QP_DEV void kq_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_units, uint64_t 
                 const bool take = slot && lr0 + rel < sg.n;
                 const float vv = __shfl(val, (take ? rel : 0) * (int)nbp, 64);
                 if (take) {
-                    outv[k] = vv;
+                    // the first unit of an accumulating segment: y + output now, as the store would add them
+                    const bool ya = n == 0 && sg.mode == QP_GEMV_ACC;
+                    outv[k] = ya ? ypre + vv : vv;
+                    pre = ya ? (pre | (1u << k)) : (pre & ~(1u << k));
                     outk[k] = (si << 28) | (lr0 + rel);
                     if (sg.mode == QP_GEMV_ARGMAX) {
                         const uint64_t key = amax_key(vv, lr0 + rel);
@@ -3425,12 +3441,17 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
     const uint32_t kw0 = min(nk, (wg * 4 + wave) * per), kw1 = min(nk, kw0 + per);
     const uint32_t g0 = min(nk, wg * 4 * per), g1 = min(nk, g0 + 4 * per);
     const bool wg_new = g0 <= pos0 && pos0 < g1;  // this workgroup holds the new key: it appends it
-    // the new k and v (and the k norm weight) where this workgroup appends them, then the first K/V step
-    if (wg_new && tid < HD) {
-        knt = gload<float>(a.k + 4ull * ((uint64_t)kvh * HD + tid));
-        vnt = gload<float>(a.v + 4ull * ((uint64_t)kvh * HD + tid));
+    // the new k and v (and the k norm weight) where this workgroup appends them, then the first K/V step: buffer
+    // loads out of branches (elsewhere past the end: 0), so that the compiler counts them and the wait for q, k, v
+    // leaves the key/value tiles in flight
+    {
+        const bool on = wg_new && tid < HD;
+        const uint32_t o = on ? 4 * ((uint32_t)kvh * HD + tid) : 0x80000000u;
+        knt = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(kq_rsrc(a.k, 4ull * a.nkv * HD), o, 0, 0));
+        vnt = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(kq_rsrc(a.v, 4ull * a.nkv * HD), o, 0, 0));
+        const __amdgpu_buffer_rsrc_t rkn = kq_rsrc(a.knorm ? a.knorm : a.k, a.knorm ? 4ull * HD : 0ull);
+        kwt = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rkn, on ? 4 * tid : 0x80000000u, 0, 0));
     }
-    if (a.knorm && wg_new && tid < HD) kwt = gload<float>(a.knorm + 4ull * tid);
     // issued by every wavefront (one without keys loads nothing: its offsets are past the end), so the waits below
     // can count these loads as still in flight
     const uint32_t kvd = a.nkv * HD;
@@ -3438,7 +3459,7 @@ QP_DEV void attn_dec_body_(const QpDecAttnArgs& a) {
     const uint64_t vbytes = F16 ? (uint64_t)((a.rows + 31) / 32) * 32 * kvd * 2 : cbytes;  // whole tiles
     const __amdgpu_buffer_rsrc_t rk = kq_rsrc(a.kc, cbytes), rv = kq_rsrc(a.vc, vbytes);
     DecBuf A, B;
-    MTile<HD> MA;  // one tile in flight: a workgroup covers about 128 keys, one tile per wavefront
+    MTile<HD> MA;  // one tile in flight per wavefront
     if constexpr (F16) {
         mt_load<HD>(MA, rk, rv, kvd, kvh, kw0, kw1, lane);
     } else {
