@@ -44,9 +44,9 @@ CASES = {
     # the MoE shapes (4 centered layers): varied greedy ids after 2048 prompt ids
     "c5s_ctx2048": ("qwen3moe_q4k_c4", 2048, 25, 2048, 128, (0, 127)),
     # full depth with varied greedy ids: the 8B shape (32 centered layers, weights of standard deviation 0.02) at
-    # context 512, and the MoE shape (48 centered layers, 0.05) after a 512-token prompt
+    # context 512, and the MoE shape (48 centered layers, 0.1) after a 64-token prompt
     "c3c_ctx512": ("llama8b_q4km_c", 512, 27, 512, 128, (0, 64, 127)),
-    "c5c_ctx512": ("qwen3moe_q4k_c", 512, 28, 512, 128, (0, 64, 127)),
+    "c5c_ctx64": ("qwen3moe_q4k_c", 64, 28, 64, 128, (0, 64, 127)),
 }
 
 

@@ -11,7 +11,7 @@ regenerates with quipullm_amd.synth and identifies by a digest of sampled bytes)
 * the 8B shapes in 2 centered layers at context 4096;
 * C4: a 2048-token prompt in one prefill chunk, its last token's logits and 8 greedy tokens;
 * C5 (48-layer MoE, 128 experts, top-8) after a 2048-token prompt;
-* the MoE shape in 48 centered layers after a 512-token prompt (varied greedy ids), and in 4 centered layers after
+* the MoE shape in 48 centered layers after a 64-token prompt (varied greedy ids), and in 4 centered layers after
   2048.
 
 The GPU runs the product host (Node.js engine, fused one-token graph) with the reference's f32 KV cache, as the
@@ -46,7 +46,7 @@ pytestmark = pytest.mark.gpu
 CLI = os.path.join(ROOT, "quipullm_amd", "js", "cli.js")
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 TOL = 1e-3
-CASES = ["c3_ctx512", "c3c_ctx512", "c3s_ctx4096", "c4_prefill2048", "c5_ctx2048", "c5c_ctx512", "c5s_ctx2048"]
+CASES = ["c3_ctx512", "c3c_ctx512", "c3s_ctx4096", "c4_prefill2048", "c5_ctx2048", "c5c_ctx64", "c5s_ctx2048"]
 
 
 def fixture(case):
