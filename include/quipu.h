@@ -66,12 +66,14 @@ int qp_dispatch(int op, const void* uniform, uint32_t uniform_size, const uint64
                 uint32_t gx, uint32_t gy, uint32_t gz);
 
 /* qp_dispatch for callers that cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid
- * hipMalloc); no counterpart in the reference.  The same ops and results as qp_dispatch, and no allocation: the
- * prefill matmul (matmul_<fmt>_4 / _t), whose workspace qp_dispatch grows with hipMalloc, takes it from a fixed
- * device array of 32 MiB that each device holds from qp_init until the process ends (its split input planes, 4
- * bytes per input value, and split-K partials: up to 256 tokens at K = 14336); a call that would need more fails
- * with QP_E_ARG.  Every call on a device shares that array and finds the last call's contents; calls that overlap
- * on one device race. */
+ * hipMalloc); no counterpart in the reference.  The same ops as qp_dispatch, and no allocation: the prefill matmul
+ * (matmul_<fmt>_4 / _t / _t_swiglu), whose workspace qp_dispatch grows with hipMalloc, takes it from a fixed device
+ * array of 32 MiB that each device holds from qp_init until the process ends.  Its split input planes (4 bytes per
+ * input value, the tokens rounded up to whole tiles) must fit: up to 512 tokens at K = 14336, 2048 at K = 4096; a
+ * call that needs more fails with QP_E_ARG.  Where qp_dispatch's split-K partials would not fit beside them, the
+ * K range is split fewer times (the same results up to the order of the partial sums, within the matmul's error
+ * bound; bit-identical where nothing is lowered).  Every call on a device shares that array and finds the last
+ * call's contents; calls that overlap on one device race. */
 int qp_dispatch_noalloc(int op, const void* uniform, uint32_t uniform_size, const uint64_t* bufs, uint32_t nbuf,
                         uint32_t gx, uint32_t gy, uint32_t gz);
 /* ---------------------------------------------------------------- raw code objects (no reference counterpart) */

@@ -3,7 +3,8 @@
 #include <stdint.h>
 
 // Bytes of the scratch array each device holds from qp_init until the process ends: the prefill matmul's split
-// input planes (4 bytes per input value) and split-K partials of up to 256 tokens at K = 14336.
+// input planes (4 bytes per input value: up to 512 tokens at K = 14336) and as many split-K partials as fit beside
+// them.
 #define QP_SCRATCH_BYTES (32u << 20)
 
 namespace qp_scratch {
