@@ -104,17 +104,15 @@ def gguf_bytes(fmt, N, K):
     return N * K // epb * bpb
 
 
+def scale_plane(fmt, h, N, K):
+    """Address of the f16 scale plane of the planar device tensor h (Q8_0, IQ4_NL) of N x K weights: after the N*K/32
+    blocks' quants (32 bytes each for Q8_0, 16 for IQ4_NL), the second binding of the planar formats' ops."""
+    return h + N * K // 32 * (32 if fmt == Q8_0 else 16)
+
+
 def device_bytes(fmt, N, K):
-    """Bytes of the device tensor: the GGUF size, except Q3_K blocks padded to 112 bytes and IQ4_NL repacked into
-    the Q8_0 layout (34 bytes per 32 weights)."""
-    if fmt == IQ4_NL:
-        return N * K // 32 * 34
+    """Bytes of the device tensor: the GGUF size, except Q3_K blocks padded to 112 bytes."""
     return N * K // 256 * 112 if fmt == Q3_K else gguf_bytes(fmt, N, K)
-
-
-def layout_fmt(fmt):
-    """The format code of the device layout a tensor of GGUF type fmt is held in (IQ4_NL: Q8_0)."""
-    return Q8_0 if fmt == IQ4_NL else fmt
 
 
 class Quipu:
@@ -194,7 +192,7 @@ class Quipu:
     # -------------------------------------------------------------- weights (device layout)
     def upload_matrix(self, fmt, raw, N, K):
         """GGUF blocks of an N x K matrix -> device tensor in this backend's layout (repacked on the device: Q4_K,
-        Q5_K and Q6_K to row chunk planes, Q8_0 to planar qs | d, IQ4_NL to the Q8_0 layout).  Returns the handle."""
+        Q5_K and Q6_K to row chunk planes, Q8_0 and IQ4_NL to planar qs | d).  Returns the handle."""
         raw = np.ascontiguousarray(np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray)) else raw)
         assert raw.nbytes == gguf_bytes(fmt, N, K), (raw.nbytes, gguf_bytes(fmt, N, K))
         if fmt == F32:
@@ -212,7 +210,7 @@ class Quipu:
     def dequant(self, fmt, h, nelem, K):
         """The device tensor h (rows of K elements) dequantized to f32, in element order."""
         y = self.alloc(nelem * 4)
-        self.dispatch("dequant", [("u", layout_fmt(fmt)), ("u", nelem & 0xFFFFFFFF), ("u", nelem >> 32), ("u", K)], [0, h, y])
+        self.dispatch("dequant", [("u", fmt), ("u", nelem & 0xFFFFFFFF), ("u", nelem >> 32), ("u", K)], [0, h, y])
         out = self.download(y, (nelem,))
         self.free(y)
         return out
@@ -256,12 +254,10 @@ class Quipu:
 
 def gemv_uniform(nseg, K, eps=0.0, last_row=0, R=0, max_wg=0, fmt=Q4_K, segs=()):
     """P of the fused `gemv` op: segs = [(mode, n, row_base, rows_total[, seg_fmt]), ...]; a segment's own format
-    (Q4_K / Q6_K mixed in one launch) rides in bits 8..15 of its mode word.  Formats are GGUF types, written as
-    the code of their device layout (IQ4_NL: Q8_0)."""
-    u = [("u", nseg), ("u", K), ("f", eps), ("u", last_row), ("u", R), ("u", max_wg), ("u", layout_fmt(fmt)),
-         ("u", 0)]
+    (Q4_K / Q6_K mixed in one launch) rides in bits 8..15 of its mode word.  Formats are GGUF type ids."""
+    u = [("u", nseg), ("u", K), ("f", eps), ("u", last_row), ("u", R), ("u", max_wg), ("u", fmt), ("u", 0)]
     for sg in segs:
         mode, n, rb, rt = sg[:4]
-        sf = layout_fmt(sg[4]) if len(sg) > 4 else 0
+        sf = sg[4] if len(sg) > 4 else 0
         u += [("u", mode | (sf << 8)), ("u", n), ("u", rb), ("u", rt)]
     return u

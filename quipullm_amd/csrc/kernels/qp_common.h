@@ -28,6 +28,15 @@ QP_DEV void gstore(uint64_t addr, T v) {
     *(QP_GLOBAL T*)addr = v;
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// A buffer resource over `bytes` bytes from base (raw, no stride).  A load whose offset lies past them returns 0 and
+// moves no data: kernels pass QP_NOOFF for a lane or row without work, so that every path issues the same loads.
+QP_DEV __amdgpu_buffer_rsrc_t kq_rsrc(uint64_t base, uint64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+constexpr uint32_t QP_NOOFF = 0x80000000u;
+
 QP_DEV float wave_sum(float v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
@@ -189,6 +198,25 @@ QP_DEV float deq_q8_planar(const uint8_t* base, uint64_t NB, uint64_t gb, uint32
     return (float)q * h2f(dp[0] | (dp[1] << 8));
 }
 
+// IQ4_NL (ggml type 20, reference kds.js:36-39): weight = d * table[nibble] with the non-linear 16-entry int8 table
+// {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113}, held here in four dwords (entry 4j + i
+// in byte i of dword j).  iq4nl_lut4 looks up the four nibbles held one per byte of idx (each 0..15) and returns the
+// four table bytes with three byte permutes: entries 0..7 for every byte (a nibble of 8 or more selects a constant,
+// unused), entries 8..15 for every byte (by nibble ^ 8), then per byte the first or the second by bit 3.
+QP_DEV uint32_t iq4nl_lut4(uint32_t idx) {
+    constexpr uint32_t T0 = 0xbfad9881u, T1 = 0xf6eaddcfu, T2 = 0x26190d01u, T3 = 0x71594535u;
+    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, idx);
+    const uint32_t hi = __builtin_amdgcn_perm(T3, T2, idx ^ 0x08080808u);
+    return __builtin_amdgcn_perm(hi, lo, 0x03020100u | ((idx >> 1) & 0x04040404u));
+}
+QP_DEV float deq_iq4nl_planar(const uint8_t* base, uint64_t NB, uint64_t gb, uint32_t e) {
+#pragma clang fp contract(off)
+    const uint32_t byte = base[gb * 16 + (e & 15)];
+    const int8_t q = (int8_t)(iq4nl_lut4(e < 16 ? byte & 15u : byte >> 4) & 0xffu);
+    const uint8_t* dp = base + NB * 16 + gb * 2;
+    return h2f(dp[0] | (dp[1] << 8)) * (float)q;
+}
+
 // Q5_K (reference kquants.js:8, deq at 151-153): the Q4_K header and sub-block scales, qh[32] at bytes 16..47 and
 // qs[128] at 48..175; q = nibble (low for even sub-blocks, high for odd) + 16 * bit j of qh[l].
 QP_DEV float deq_q5k_dev(const uint8_t* base, uint32_t nb, uint64_t row, uint32_t b, uint32_t e) {
@@ -257,12 +285,13 @@ QP_DEV float deq_elem(uint32_t fmt, const uint8_t* base, uint64_t NB, uint64_t r
     if (fmt == QP_Q2_K) return deq_q2k_dev(base, K >> 8, NB, row, k >> 8, k & 255);
     if (fmt == QP_Q6_K) return deq_q6k_dev(base, K >> 8, NB, row, k >> 8, k & 255);
     if (fmt == QP_Q8_0) return deq_q8_planar(base, NB, row * (K >> 5) + (k >> 5), k & 31);
+    if (fmt == QP_IQ4_NL) return deq_iq4nl_planar(base, NB, row * (K >> 5) + (k >> 5), k & 31);
     return reinterpret_cast<const float*>(base)[row * K + k];
 }
 
 QP_DEV uint64_t total_blocks(uint32_t fmt, uint64_t nrows, uint32_t K) {
     if (fmt == QP_Q2_K || fmt == QP_Q3_K || fmt == QP_Q4_K || fmt == QP_Q5_K || fmt == QP_Q6_K) return nrows * (K >> 8);
-    if (fmt == QP_Q8_0) return nrows * (K >> 5);
+    if (fmt == QP_Q8_0 || fmt == QP_IQ4_NL) return nrows * (K >> 5);
     return nrows * K;
 }
 

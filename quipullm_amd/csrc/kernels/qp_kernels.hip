@@ -88,23 +88,16 @@ KERNEL __launch_bounds__(256) void qp_repack_q8(QpRepackArgs a) {
     }
 }
 
-// IQ4_NL (GGML type 20, reference weights.js:110-116 and kds.js:36-39): 18-byte blocks of 32 weights, d (f16)
-// then 16 bytes whose low nibbles index weights 0..15 and high nibbles weights 16..31 in the non-linear table
-// below; weight = d * table[nibble].  Repacked into the planar Q8_0 layout with q = table[nibble] (every entry
-// is an int8): the Q8_0 element q * d is the same single product, so every Q8_0 kernel computes IQ4_NL exactly.
+// IQ4_NL (GGML type 20, reference weights.js:110-116 and kds.js:36-39): GGUF 18-byte blocks (d f16, then 16 nibble
+// bytes) -> planar qs [NB][16] | d [NB] f16, the nibble bytes unchanged (18 bytes per 32 weights on the device).
 KERNEL __launch_bounds__(256) void qp_repack_iq4nl(QpRepackArgs a) {
-    constexpr int8_t kv[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
     const uint64_t NB = a.nblocks;
     for (uint64_t b = blockIdx.x * 256ull + threadIdx.x; b < NB; b += (uint64_t)gridDim.x * 256ull) {
         const uint8_t* s = cptr<uint8_t>(a.src) + b * 18;
         uint8_t* d = mptr<uint8_t>(a.dst);
-        for (int l = 0; l < 16; l++) {
-            const uint8_t q = s[2 + l];
-            d[b * 32 + l] = (uint8_t)kv[q & 15];
-            d[b * 32 + 16 + l] = (uint8_t)kv[q >> 4];
-        }
-        d[NB * 32 + b * 2] = s[0];
-        d[NB * 32 + b * 2 + 1] = s[1];
+        for (int l = 0; l < 16; l++) d[b * 16 + l] = s[2 + l];
+        d[NB * 16 + b * 2] = s[0];
+        d[NB * 16 + b * 2 + 1] = s[1];
     }
 }
 
@@ -145,32 +138,26 @@ QP_DEV void qp_embed_impl(QpEmbedArgs a) {
     }
 }
 
-// ====================================================================================== GEMV (one token)
-// A wavefront computes R weight rows at once.  Lanes stride over "pieces" of each row; the input vector is
-// staged once per workgroup in LDS (optionally RMS-normalized on the way in), with per-group sums of x, and each
-// piece's x values are read from LDS once for all R rows.  Q4_K piece: one 32-byte quant group = 64 weights
-// (low nibbles: sub-block 2g, high nibbles: sub-block 2g+1) plus the block header.  Q6_K piece: 64 weights
-// (ql 2x16 B, qh 16 B, 4 scales).  Q8_0 piece: one 32-weight block.  F32 piece: 16 floats.
-// Semantics: reference matmul_*_1 (kquants.js:188-251, gpu.js:123-198): y = W.x with the per-sub-block
-// factoring a += d*sc*sum(q x) - dmin*m*sum(x).
-
-// Dot of the 4 bytes of w (each a small unsigned integer) with x.  The empty asm makes w opaque to the
-// optimizer, so the byte selects stay (w >> 8k) & 0xff and become single v_cvt_f32_ubyte{k} instructions
-// instead of a bit-field extract plus a convert.
-QP_DEV float nib4_dot(uint32_t w, const float4 x) {
-    asm("" : "+v"(w));
-    return (float)(w & 0xffu) * x.x + (float)((w >> 8) & 0xffu) * x.y + (float)((w >> 16) & 0xffu) * x.z +
-           (float)(w >> 24) * x.w;
-}
-// acc + dot(bytes of w, x) as one chain of fused multiply-adds (one instruction per weight after the convert).
-QP_DEV float nib4_fma(uint32_t w, const float4 x, float acc) {
-    asm("" : "+v"(w));
-    acc = fmaf((float)(w & 0xffu), x.x, acc);
-    acc = fmaf((float)((w >> 8) & 0xffu), x.y, acc);
-    acc = fmaf((float)((w >> 16) & 0xffu), x.z, acc);
-    return fmaf((float)(w >> 24), x.w, acc);
-}
-QP_DEV float sum4(const float4 x) { return (x.x + x.y) + (x.z + x.w); }
+// ====================================================================================== GEMV (one token), planar
+// Q8_0, IQ4_NL and F32 y = W.x for one token: the fused `gemv` op, the reference's matmul_q8_1 / matmul_iq4nl_1 /
+// matmul_f32_1 (gpu.js:123-198, kds.js:41-107) and the gathered-expert matmul_*_e (kds.js:110-186).
+//
+// A wavefront computes R weight rows at once; its lanes stride over the rows' "pieces" (Q8_0, IQ4_NL: one 32-weight
+// block; F32: 16 floats), so one load instruction reads 64 consecutive pieces of a row (2 KB of Q8_0 quants, 1 KB of
+// IQ4_NL nibbles) and their 128 contiguous bytes of scales.  The work of a wavefront is one sequence of items (pass
+// k, piece slot j < ppl): pass k takes the R rows of row group blockIdx.x + k * gridDim.x (a persistent grid), slot j
+// the pieces lane + 64 j.  D register sets rotate, so the loads of the D - 1 items after item n are in flight while
+// item n is multiplied.  Every item issues the same loads through buffer resources of its rows: a lane past the
+// row's pieces passes an offset past the resource, and a row past its segment (or an item past the wave's last
+// pass) gets an empty resource; neither moves data.  As the number of loads never depends on the path taken, the
+// compiler's waits count exactly the loads in flight (a load issued on one path only would make it wait for all).
+// The input's loads are issued before the first items' weights and awaited alone; the input is staged once per
+// workgroup in LDS in piece-major order (float4 j of piece p at xs[j * npc + p]: the lanes of an LDS read touch
+// consecutive 16-byte words), optionally RMS-normalized on the way in.  Outputs are held in registers and written
+// after the item loop: a store in flight counts in the same counter as the loads, and every later wait would
+// include it.
+// Semantics: reference matmul_*_1 (kquants.js:188-251, gpu.js:123-198): y = W.x; Q8_0 and IQ4_NL take a += d * s
+// per block with s the block's dot product, as the reference does (kds.js:80-88).
 
 QP_DEV void q4k_sm(uint32_t s03, uint32_t s47, uint32_t s811, uint32_t j, uint32_t& sc, uint32_t& mn) {
     // 6-bit scale/min unpack of sub-block j (reference scmin, kquants.js:65-76)
@@ -185,49 +172,84 @@ QP_DEV void q4k_sm(uint32_t s03, uint32_t s47, uint32_t s811, uint32_t j, uint32
     }
 }
 
-struct RowRef {
-    uint64_t base;  // tensor base address (device layout)
-    uint64_t row;   // weight row index within the tensor
+// A value the compiler takes for a per-lane one (read from memory) that is the same in every lane.
+QP_DEV uint64_t uni64(uint64_t v) {
+    return ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
+           (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+}
+
+// A row of one pass: its quant (F32: float) bytes and its f16 scales.
+struct PlRow {
+    __amdgpu_buffer_rsrc_t q, d;
 };
 
-// Per-format piece registers for R rows: load() issues the global loads of piece p, compute() consumes them
-// with the piece's x values (xs, piece-major) and x-group sums (xsum[p*S + i]) from LDS.  Splitting the two
-// lets the row loop keep the next piece's loads in flight while the current piece is being multiplied.
+// Per-format piece registers for R rows: load() issues the loads of piece p (on: the lane has the piece),
+// compute() consumes them with the piece's x values from LDS.  J: float4s of x per piece; QB: quant bytes per
+// piece; LOADS: load instructions per row.
 template <int FMT, int R>
 struct Piece;
 
+QP_DEV float sdot4(uint32_t w, const float4 x) {  // the 4 signed bytes of w with x
+    return (float)(int8_t)(w & 0xffu) * x.x + (float)(int8_t)((w >> 8) & 0xffu) * x.y +
+           (float)(int8_t)((w >> 16) & 0xffu) * x.z + (float)(int8_t)(w >> 24) * x.w;
+}
+
 template <int R>
 struct Piece<QP_Q8_0, R> {
-    uint4 q0[R], q1[R];
-    uint32_t dd[R];
-    static constexpr uint32_t J = 8;
-    static constexpr uint32_t S = 0;
-    static QP_DEV uint32_t count(uint32_t K) { return K >> 5; }
-    static QP_DEV uint32_t x_src(uint32_t p, uint32_t j) { return p * 8 + j; }
-    QP_DEV void load(const RowRef (&rr)[R], uint64_t NB, uint32_t K, uint32_t p) {
-        const uint32_t nb = K >> 5;
+    static constexpr uint32_t J = 8, QB = 32, LOADS = 3;
+    u32x4 q0[R], q1[R];
+    uint16_t dd[R];  // 16-bit until used: a widening right after the load would wait for it
+    QP_DEV void load(const PlRow (&rw)[R], uint32_t p, bool on) {
+        const uint32_t o = on ? p * 32 : QP_NOOFF, od = on ? p * 2 : QP_NOOFF;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const uint64_t gb = rr[r].row * nb + p;
-            q0[r] = gload<uint4>(rr[r].base + gb * 32);
-            q1[r] = gload<uint4>(rr[r].base + gb * 32 + 16);
-            dd[r] = gload<uint16_t>(rr[r].base + NB * 32 + gb * 2);
+            q0[r] = __builtin_amdgcn_raw_buffer_load_b128(rw[r].q, o, 0, 0);
+            q1[r] = __builtin_amdgcn_raw_buffer_load_b128(rw[r].q, o, 16, 0);
+            dd[r] = __builtin_amdgcn_raw_buffer_load_b16(rw[r].d, od, 0, 0);
         }
     }
-    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, const float*, uint32_t p,
-                        float (&acc)[R]) const {
+    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, uint32_t p, float (&acc)[R]) const {
         float4 xv[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) xv[i] = xs[i * npc + p];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const uint32_t ws[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
             float s = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const uint32_t w = ws[i];
-                s += (float)(int8_t)(w & 0xffu) * xv[i].x + (float)(int8_t)((w >> 8) & 0xffu) * xv[i].y +
-                     (float)(int8_t)((w >> 16) & 0xffu) * xv[i].z + (float)(int8_t)(w >> 24) * xv[i].w;
+            for (int i = 0; i < 4; i++) s += sdot4(q0[r][i], xv[i]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) s += sdot4(q1[r][i], xv[4 + i]);
+            acc[r] += h2f(dd[r]) * s;
+        }
+    }
+};
+
+// IQ4_NL: word i of the block's 16 nibble bytes holds weights 4i..4i+3 in its low nibbles and 16+4i..16+4i+3 in
+// its high ones; s = sum over i of dot(lo_i, x_i) + dot(hi_i, x_(4+i)) (the reference's order, kds.js:80-88).
+template <int R>
+struct Piece<QP_IQ4_NL, R> {
+    static constexpr uint32_t J = 8, QB = 16, LOADS = 2;
+    u32x4 q[R];
+    uint16_t dd[R];  // 16-bit until used: a widening right after the load would wait for it
+    QP_DEV void load(const PlRow (&rw)[R], uint32_t p, bool on) {
+        const uint32_t o = on ? p * 16 : QP_NOOFF, od = on ? p * 2 : QP_NOOFF;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            q[r] = __builtin_amdgcn_raw_buffer_load_b128(rw[r].q, o, 0, 0);
+            dd[r] = __builtin_amdgcn_raw_buffer_load_b16(rw[r].d, od, 0, 0);
+        }
+    }
+    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, uint32_t p, float (&acc)[R]) const {
+        float4 xv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) xv[i] = xs[i * npc + p];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t lo = iq4nl_lut4(q[r][i] & 0x0f0f0f0fu), hi = iq4nl_lut4((q[r][i] >> 4) & 0x0f0f0f0fu);
+                s += sdot4(lo, xv[i]) + sdot4(hi, xv[4 + i]);
             }
             acc[r] += h2f(dd[r]) * s;
         }
@@ -236,21 +258,16 @@ struct Piece<QP_Q8_0, R> {
 
 template <int R>
 struct Piece<QP_F32, R> {
-    float4 w[R][4];
-    static constexpr uint32_t J = 4;
-    static constexpr uint32_t S = 0;
-    static QP_DEV uint32_t count(uint32_t K) { return K >> 4; }
-    static QP_DEV uint32_t x_src(uint32_t p, uint32_t j) { return p * 4 + j; }
-    QP_DEV void load(const RowRef (&rr)[R], uint64_t, uint32_t K, uint32_t p) {
+    static constexpr uint32_t J = 4, QB = 64, LOADS = 4;
+    u32x4 w[R][4];
+    QP_DEV void load(const PlRow (&rw)[R], uint32_t p, bool on) {
+        const uint32_t o = on ? p * 64 : QP_NOOFF;
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint64_t wp = rr[r].base + (rr[r].row * (K >> 2) + p * 4) * 16;
+        for (int r = 0; r < R; r++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) w[r][i] = gload<float4>(wp + 16 * i);
-        }
+            for (int i = 0; i < 4; i++) w[r][i] = __builtin_amdgcn_raw_buffer_load_b128(rw[r].q, o, 16 * i, 0);
     }
-    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, const float*, uint32_t p,
-                        float (&acc)[R]) const {
+    QP_DEV void compute(uint32_t npc, const float4* __restrict__ xs, uint32_t p, float (&acc)[R]) const {
         float4 xv[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) xv[i] = xs[i * npc + p];
@@ -259,74 +276,12 @@ struct Piece<QP_F32, R> {
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                s += w[r][i].x * xv[i].x + w[r][i].y * xv[i].y + w[r][i].z * xv[i].z + w[r][i].w * xv[i].w;
+                s += __uint_as_float(w[r][i][0]) * xv[i].x + __uint_as_float(w[r][i][1]) * xv[i].y +
+                     __uint_as_float(w[r][i][2]) * xv[i].z + __uint_as_float(w[r][i][3]) * xv[i].w;
             acc[r] += s;
         }
     }
 };
-
-// Software-pipelined row dot products: `cur` already holds piece `lane` (when lane < count); each step issues
-// the loads of the lane's next piece before multiplying the current one.
-template <int FMT, int R>
-QP_DEV void dot_rows_pipelined(Piece<FMT, R>& cur, const RowRef (&rr)[R], uint64_t NB, uint32_t K, const float4* xs,
-                               const float* xsum, uint32_t lane, float (&acc)[R]) {
-    const uint32_t npc = Piece<FMT, R>::count(K);
-    for (uint32_t p = lane; p < npc; p += 64) {
-        Piece<FMT, R> nxt;
-        const bool more = p + 64 < npc;
-        if (more) nxt.load(rr, NB, K, p + 64);
-        cur.compute(npc, xs, xsum, p, acc);
-        if (more) cur = nxt;
-    }
-}
-
-// Stage the input vector into LDS in the piece-major layout of FMT: float4 j of piece p at xs[j*npc + p], so that
-// in each LDS read the 64 lanes (consecutive pieces) touch consecutive 16-byte words (no bank conflicts).  With a
-// norm weight, x*w is stored and the RMSNorm scale 1/sqrt(mean(x^2)+eps) is returned (applied to the dot
-// products afterwards).
-template <int FMT>
-QP_DEV float stage_x(float4* xs, float* xsum, uint64_t x4, uint64_t nw, uint32_t K, float eps, float* red) {
-    const uint32_t tid = threadIdx.x;
-    const uint64_t w4 = nw;
-    const uint32_t npc = Piece<FMT, 1>::count(K);
-    float ss = 0.0f;
-    for (uint32_t q = tid; q < (K >> 2); q += blockDim.x) {
-        const uint32_t j = q / npc, p = q - j * npc;
-        const uint32_t src = Piece<FMT, 1>::x_src(p, j);
-        float4 v = gload<float4>(x4 + 16ull * src);
-        if (nw) {
-            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-            const float4 w = gload<float4>(w4 + 16ull * src);
-            v.x *= w.x; v.y *= w.y; v.z *= w.z; v.w *= w.w;
-        }
-        xs[q] = v;
-    }
-    float inv = 1.0f;
-    if (nw) {
-        ss = wave_sum(ss);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-    }
-    __syncthreads();
-    constexpr uint32_t S = Piece<FMT, 1>::S;
-    if constexpr (S > 0) {
-        constexpr uint32_t per = Piece<FMT, 1>::J / S;  // float4s per summed group
-        for (uint32_t p = tid; p < npc; p += blockDim.x)
-#pragma unroll
-            for (uint32_t i = 0; i < S; i++) {
-                float t = 0.0f;
-#pragma unroll
-                for (uint32_t j = 0; j < per; j++) t += sum4(xs[(i * per + j) * npc + p]);
-                xsum[p * S + i] = t;
-            }
-        __syncthreads();
-    }
-    if (nw) {
-        float t = 0.0f;
-        for (uint32_t i = 0; i < (blockDim.x >> 6); i++) t += red[i];
-        inv = 1.0f / sqrtf(t / (float)K + eps);
-    }
-    return inv;
-}
 
 QP_DEV uint64_t amax_key(float v, uint32_t idx) {
     if (v != v) return 0ull;  // NaN is never chosen (reference compares with '>')
@@ -335,205 +290,276 @@ QP_DEV uint64_t amax_key(float v, uint32_t idx) {
     return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - idx);
 }
 
-// Segment of workgroup wg: the last segment whose first workgroup is <= wg (segments are in order).
-QP_DEV uint32_t seg_of(const QpGemvArgs& a, uint32_t wg) {
-    uint32_t s = 0;
-    for (uint32_t i = 1; i < a.nseg; i++) s = wg >= a.seg[i].wg0 ? i : s;
-    return s;
-}
-
-// Rows of one pass (one row group of one segment) for this wavefront.
-template <int R>
-struct Pass {
-    uint32_t si, mode, n, r0;
-    bool pair;
-    uint64_t NB;
-    RowRef rr[R];
+// One segment as the item loop sees it (wave-uniform): rows row_base .. row_base + n - 1 of a tensor of rows_total
+// rows; its row groups are workgroups wg0 .. of the launch's total.
+struct PlSeg {
+    uint64_t w, w2, y;
+    uint32_t n, row_base, rows_total, mode, wg0;
 };
 
-template <int FMT, int R>
-QP_DEV void pass_setup(const QpGemvArgs& a, uint32_t wg, uint32_t wave, Pass<R>& P) {
-    P.si = seg_of(a, wg);
-    P.mode = a.seg[P.si].mode;
-    P.n = a.seg[P.si].n;
-    P.pair = P.mode == QP_GEMV_SWIGLU;
-    const uint32_t outs = P.pair ? R / 2 : R;  // output rows per wave
-    P.r0 = (wg - a.seg[P.si].wg0) * 4 * outs + wave * outs;
-    P.NB = total_blocks(FMT, (uint64_t)a.seg[P.si].rows_total, a.k);
-    const uint64_t w1 = a.seg[P.si].w;
-    const uint64_t w2 = a.seg[P.si].w2;
-    const uint32_t rb = a.seg[P.si].row_base;
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const uint32_t o = (P.pair && R > 1) ? (uint32_t)(r % (R / 2 > 0 ? R / 2 : 1)) : (uint32_t)r;
-        P.rr[r].base = (P.pair && r >= R / 2) ? w2 : w1;
-        P.rr[r].row = min(P.r0 + o, P.n - 1) + rb;
-    }
-}
+// The pass a wavefront is on: its segment, first output row, and the R rows' resources.
+template <int R>
+struct PlPass {
+    uint32_t si, mode, n, r0;
+    bool pair;
+};
 
-// All segments of one launch share the format FMT; a wavefront computes R weight rows per pass.  The grid is
-// sized to the resident capacity and each workgroup streams its passes (wg, wg + grid, ...).  The work of a
-// wavefront is one sequence of items (pass k, piece slot j < ppl); two register sets A and B alternate so that the
-// loads of item n+1 are in flight while item n is multiplied, across pass boundaries too.  Loads are issued for
-// every lane (the piece index is clamped), which keeps the wait counters exact; lanes past the row's last piece
-// skip the arithmetic.  The first item's loads are issued before the input vector is staged.
-template <int FMT, int R>
-QP_DEV void gemv_seg_body_(const QpGemvArgs& a);
-template <int FMT, int R>
-QP_DEV void gemv_seg_body(const QpGemvArgs& a) {
-    const uint64_t t0 = tl_now();
-    gemv_seg_body_<FMT, R>(a);
-    tl_rec(a.tseq, t0);
-}
-template <int FMT, int R>
-QP_DEV void gemv_seg_body_(const QpGemvArgs& a) {
+// seg_at(i): segment i < nseg (in order of wg0).  total_wg row groups of 4 waves x R rows (R / 2 output rows per wave
+// for a SwiGLU pair segment) over the grid.  x: the input row; norm_w: 0 or the fused RMSNorm weight.
+template <int FMT, int R, int D, class SegAt>
+QP_DEV void pl_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_wg, uint64_t x, uint64_t norm_w, float eps,
+                    uint32_t K, uint64_t amax) {
+    using P = Piece<FMT, R>;
     extern __shared__ float4 xs[];
-    float* xsum = reinterpret_cast<float*>(xs + (a.k >> 2));  // after the K floats of x
     __shared__ float red[4];
     __shared__ uint64_t wbest[4];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t K = a.k;
-    const uint32_t npc = Piece<FMT, R>::count(K);
-    const uint32_t ppl = (npc + 63) >> 6;  // piece slots per pass (wave-uniform)
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    x = uni64(x);  // the row read from the device step record: uniform, so its resource stays scalar
+    const uint32_t npc = K / (4 * P::J);   // pieces per row
+    const uint32_t ppl = (npc + 63) >> 6;  // piece slots per pass
     const uint32_t G = gridDim.x;
-    const uint32_t mine = blockIdx.x < a.total_wg ? (a.total_wg - 1 - blockIdx.x) / G + 1 : 0;
+    const uint32_t mine = blockIdx.x < total_wg ? (total_wg - 1 - blockIdx.x) / G + 1 : 0;
+    if (mine == 0) return;  // the whole workgroup
     const uint32_t n_total = mine * ppl;
-    Pass<R> PL, PC;
-    Piece<FMT, R> A, B;
-    auto load_item = [&](Piece<FMT, R>& X, uint32_t n) {
-        const uint32_t k = n / ppl, j = n - k * ppl;
-        if (j == 0) pass_setup<FMT, R>(a, blockIdx.x + k * G, wave, PL);
-        X.load(PL.rr, PL.NB, K, min(lane + 64 * j, npc - 1));
+    const uint64_t rowq = (uint64_t)npc * P::QB;
+
+    auto seg_of = [&](uint32_t wg) __attribute__((always_inline)) {
+        uint32_t s = 0;
+        for (uint32_t i = 1; i < nseg; i++) s = wg >= seg_at(i).wg0 ? i : s;
+        return s;
+    };
+    auto setup = [&](uint32_t k, PlPass<R>& ps) __attribute__((always_inline)) {
+        const uint32_t wg = blockIdx.x + (k < mine ? k : 0) * G;
+        ps.si = seg_of(wg);
+        const PlSeg sg = seg_at(ps.si);
+        ps.mode = sg.mode;
+        ps.n = sg.n;
+        ps.pair = sg.mode == QP_GEMV_SWIGLU;
+        const uint32_t outs = ps.pair ? R / 2 : R;
+        ps.r0 = (wg - sg.wg0) * 4 * outs + wave * outs;
+    };
+    // the resources of pass k's rows (empty past the wave's passes or the segment's rows)
+    auto rows = [&](uint32_t k, PlRow (&rw)[R]) __attribute__((always_inline)) {
+        PlPass<R> ps;
+        setup(k, ps);
+        const PlSeg sg = seg_at(ps.si);
+        const uint64_t NB = (uint64_t)sg.rows_total * npc;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t o = (ps.pair && R > 1) ? (uint32_t)(r % (R / 2 > 0 ? R / 2 : 1)) : (uint32_t)r;
+            const uint64_t base = (ps.pair && r >= R / 2) ? sg.w2 : sg.w;
+            const bool on = k < mine && ps.r0 + o < ps.n;
+            const uint64_t row = sg.row_base + (on ? ps.r0 + o : 0);
+            rw[r].q = kq_rsrc(base + row * rowq, on ? rowq : 0);
+            rw[r].d = kq_rsrc(base + NB * P::QB + row * npc * 2, (on && FMT != QP_F32) ? npc * 2 : 0);
+        }
+    };
+
+    // 1. the input: this thread's float4s f = tid + 256 i, i < 8 (K <= 8192), as buffer loads (past K: 0); the norm
+    // weight's first, under one uniform branch, then x, then the first items' weights, so that the wait for x counts
+    // only the weight loads
+    constexpr int NF = 8;
+    const uint32_t nf4 = K >> 2;
+    u32x4 xr[NF], nr[NF];
+    if (norm_w) {
+        const __amdgpu_buffer_rsrc_t rn = kq_rsrc(norm_w, 16ull * nf4);
+#pragma unroll
+        for (int i = 0; i < NF; i++) {
+            const uint32_t f = tid + 256 * i;
+            nr[i] = __builtin_amdgcn_raw_buffer_load_b128(rn, f < nf4 ? 16 * f : QP_NOOFF, 0, 0);
+        }
+    }
+    {
+        const __amdgpu_buffer_rsrc_t rx = kq_rsrc(x, 16ull * nf4);
+#pragma unroll
+        for (int i = 0; i < NF; i++) {
+            const uint32_t f = tid + 256 * i;
+            xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, f < nf4 ? 16 * f : QP_NOOFF, 0, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. the first D - 1 items' weights
+    P buf[D];
+    PlRow rwL[R];
+    uint32_t kL = 0, jL = 0;  // the next item to load
+    auto load_next = [&](P& X) __attribute__((always_inline)) {
+        if (jL == 0) rows(kL, rwL);
+        X.load(rwL, lane + 64 * jL, lane + 64 * jL < npc);
+        if (++jL == ppl) {
+            jL = 0;
+            kL++;
+        }
+    };
+#pragma unroll
+    for (int d = 0; d + 1 < D; d++) load_next(buf[d]);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. stage x (times the norm weight) in LDS, piece-major; the sum of squares for the norm
+    float ss = 0.0f;
+    auto put = [&](uint32_t f, float4 v, float4 w) __attribute__((always_inline)) {
+        if (norm_w) {
+            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+            v.x *= w.x;
+            v.y *= w.y;
+            v.z *= w.z;
+            v.w *= w.w;
+        }
+        const uint32_t p = f / P::J, j = f % P::J;
+        xs[j * npc + p] = v;
+    };
+    auto f4 = [](const u32x4 u) __attribute__((always_inline)) {
+        return make_float4(__uint_as_float(u[0]), __uint_as_float(u[1]), __uint_as_float(u[2]),
+                           __uint_as_float(u[3]));
+    };
+#pragma unroll
+    for (int i = 0; i < NF; i++) {
+        const uint32_t f = tid + 256 * i;
+        if (f < nf4) put(f, f4(xr[i]), norm_w ? f4(nr[i]) : float4{});
+    }
+    for (uint32_t f = tid + 256 * NF; f < nf4; f += 256)  // K > 8192: the rest (this wait includes the weights)
+        put(f, gload<float4>(x + 16ull * f), norm_w ? gload<float4>(norm_w + 16ull * f) : float4{});
+    if (norm_w) {
+        ss = wave_sum_v(ss, lane);
+        if (lane == 0) red[wave] = ss;
+    }
+    __syncthreads();
+    float inv = 1.0f;
+    if (norm_w) inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)K + eps);
+
+    // 4. items
+    constexpr int NO = 2;  // deferred outputs: lane L of register k holds output slot L + 64 k
+    float outv[NO];
+    uint32_t outk[NO];     // segment << 28 | row within the segment; all ones: nothing to write
+#pragma unroll
+    for (int k = 0; k < NO; k++) {
+        outv[k] = 0.0f;
+        outk[k] = 0xffffffffu;
+    }
+    uint32_t nout = 0;
+    uint64_t best = 0;
+    auto flush = [&](bool wait) __attribute__((always_inline)) {
+        for (uint32_t si = 0; si < nseg; si++) {
+            const PlSeg sg = seg_at(si);
+#pragma unroll
+            for (int k = 0; k < NO; k++) {
+                if (lane + 64 * k < nout && outk[k] != 0xffffffffu && (outk[k] >> 28) == si) {
+                    QP_GLOBAL float* y = reinterpret_cast<QP_GLOBAL float*>(sg.y) + (outk[k] & 0x0fffffffu);
+                    *y = sg.mode == QP_GEMV_ACC ? *y + outv[k] : outv[k];
+                }
+            }
+        }
+        nout = 0;
+        if (wait) __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xf << 8));  // drain the stores (rare)
     };
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
-    uint64_t best = 0;
-    float inv = 1.0f;
-    auto compute_item = [&](const Piece<FMT, R>& X, uint32_t n) {
-        const uint32_t k = n / ppl, j = n - k * ppl;
-        if (j == 0) pass_setup<FMT, R>(a, blockIdx.x + k * G, wave, PC);
-        const uint32_t p = lane + 64 * j;
-        if (p < npc) X.compute(npc, xs, xsum, p, acc);
-        if (j + 1 < ppl) return;
-        // end of pass: reduce across the wavefront and write the R rows
+    PlPass<R> PC;
+    uint32_t kC = 0, jC = 0;  // the item being computed
+    auto compute = [&](const P& X) __attribute__((always_inline)) {
+        if (jC == 0) setup(kC, PC);
+        // every lane: one past the row's pieces loaded zero weights (and scales), and reads a valid x; under a
+        // branch, the wait for this item's loads would not cover the path that skips it
+        const uint32_t p = lane + 64 * jC;
+        X.compute(npc, xs, p < npc ? p : npc - 1, acc);
+        if (++jC < ppl) return;
+        // end of the pass: reduce across the wavefront and defer the outputs (none for a padding pass)
+        jC = 0;
+        if (kC++ >= mine) return;
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]) * inv;
-        float* y = mptr<float>(a.seg[PC.si].y);
-        if (PC.pair) {
+        for (int r = 0; r < R; r++) acc[r] = wave_sum_v(acc[r], lane) * inv;
+        const uint32_t outs = PC.pair ? R / 2 : R;
+        if (nout + outs > 64 * NO) flush(true);
 #pragma unroll
-            for (int r = 0; r < R / 2; r++) {
-                const uint32_t row = PC.r0 + r;
-                if (lane == (uint32_t)r && row < PC.n) {
-                    const float g = acc[r], u = acc[r + R / 2];
-                    y[row] = (g / (1.0f + expf(-g))) * u;
-                }
+        for (int r = 0; r < R; r++) {
+            if (PC.pair && r >= R / 2) break;
+            const uint32_t row = PC.r0 + r;
+            const float val = PC.pair ? (acc[r] / (1.0f + expf(-acc[r]))) * acc[r + R / 2] : acc[r];
+            if (PC.mode == QP_GEMV_ARGMAX && row < PC.n) {
+                const uint64_t key = amax_key(val, row);
+                best = key > best ? key : best;
             }
-        } else {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint32_t row = PC.r0 + r;
-                if (lane == (uint32_t)r && row < PC.n) {
-                    if (PC.mode == QP_GEMV_ACC) y[row] = y[row] + acc[r];
-                    else y[row] = acc[r];
+            for (int k = 0; k < NO; k++)
+                if (lane + 64 * k == nout + r) {
+                    outv[k] = val;
+                    outk[k] = row < PC.n ? (PC.si << 28) | row : 0xffffffffu;
                 }
-                if (PC.mode == QP_GEMV_ARGMAX && row < PC.n) {
-                    const uint64_t key = amax_key(acc[r], row);
-                    best = key > best ? key : best;
-                }
-            }
         }
+        nout += outs;
 #pragma unroll
         for (int r = 0; r < R; r++) acc[r] = 0.0f;
     };
-    if (n_total) load_item(A, 0);
-    const uint32_t xrow = a.last_row ? paso_T(a.paso) - 1 : 0;
-    inv = stage_x<FMT>(xs, xsum, a.x + 4ull * xrow * K, a.norm_w, K, a.eps, red);
-    for (uint32_t n = 0; n < n_total; n += 2) {
-        if (n + 1 < n_total) load_item(B, n + 1);
-        compute_item(A, n);
-        if (n + 1 < n_total) {
-            if (n + 2 < n_total) load_item(A, n + 2);
-            compute_item(B, n + 1);
+    // the items run in whole rounds of D (the last round's items past n_total load nothing and write nothing), so
+    // that the loop body has no exit between its loads and the waits for them
+    for (uint32_t n0 = 0; n0 < n_total; n0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            load_next(buf[(d + D - 1) % D]);  // item n0 + d + D - 1 (an empty one past the wave's last)
+            compute(buf[d]);
         }
     }
-    if (a.amax) {
+    flush(false);
+    if (amax) {
         if (lane == 0) wbest[wave] = best;
         __syncthreads();
         if (tid == 0) {
             uint64_t b = wbest[0];
             for (int i = 1; i < 4; i++) b = wbest[i] > b ? wbest[i] : b;
-            mptr<uint64_t>(a.amax)[blockIdx.x] = b;
+            mptr<uint64_t>(amax)[blockIdx.x] = b;
         }
     }
+}
+
+// Register sets in rotation (items whose loads are in flight + the one being multiplied).  Measured on the 14336 x
+// 4096 and 4096 x 14336 GEMVs, 2 is faster than 3 or 4 for Q8_0, IQ4_NL and f32.
+#ifndef QP_PL_D
+#define QP_PL_D 2
+#endif
+template <int FMT, int R>
+QP_DEV void gemv_seg_body(const QpGemvArgs& a) {
+    const uint64_t t0 = tl_now();
+    auto seg_at = [&](uint32_t i) __attribute__((always_inline)) {
+        const QpGemvSeg& q = a.seg[i];
+        return PlSeg{q.w, q.w2, q.y, q.n, q.row_base, q.rows_total, q.mode, q.wg0};
+    };
+    const uint32_t xrow = a.last_row ? paso_T(a.paso) - 1 : 0;
+    constexpr int D = QP_PL_D;
+    pl_gemv<FMT, R, D>(seg_at, a.nseg, a.total_wg, a.x + 4ull * xrow * a.k, a.norm_w, a.eps, a.k, a.amax);
+    tl_rec(a.tseq, t0);
 }
 
 #define GEMV_KERNELS(NAME, FMT)                                                                          \
     KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r1(QpGemvArgs a) { gemv_seg_body<FMT, 1>(a); } \
     KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r2(QpGemvArgs a) { gemv_seg_body<FMT, 2>(a); } \
-    KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r4(QpGemvArgs a) { gemv_seg_body<FMT, 4>(a); }
-#define GEMV_KERNEL_R8(NAME, FMT) \
+    KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r4(QpGemvArgs a) { gemv_seg_body<FMT, 4>(a); } \
     KERNEL __launch_bounds__(256) void qp_gemv_##NAME##_r8(QpGemvArgs a) { gemv_seg_body<FMT, 8>(a); }
 GEMV_KERNELS(q8, QP_Q8_0)
+GEMV_KERNELS(iq4nl, QP_IQ4_NL)
 GEMV_KERNELS(f32, QP_F32)
-GEMV_KERNEL_R8(q8, QP_Q8_0)
-GEMV_KERNEL_R8(f32, QP_F32)
 
-// Gathered expert GEMV (reference matmul_*_e, kquants.js:256-304 and kds.js:110-186).
-// grid.x: row groups of 4*R rows (R/2 output rows per wave in SWIGLU mode), grid.y: job.
+// Gathered expert GEMV (reference matmul_*_e, kquants.js:256-304 and kds.js:110-186): grid.x row groups of 4 * R rows
+// (R / 2 output rows per wave in SWIGLU mode), grid.y the job; job z multiplies expert sel[z] by input row z / tfijo.
 template <int FMT, int R>
 QP_DEV void gemv_exp_body(const QpGemvExpArgs& a) {
-    extern __shared__ float4 xs[];
-    float* xsum = reinterpret_cast<float*>(xs + (a.k >> 2));  // after the K floats of x
-    __shared__ float red[4];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t njobs = a.njobs_fixed ? a.njobs_fixed : paso_T(a.paso) * a.kused;
     const uint32_t job = blockIdx.y;
     if (job >= njobs) return;
-    const uint32_t K = a.k;
-    uint32_t ex = cptr<uint32_t>(a.sel)[job];
+    uint32_t ex = __builtin_amdgcn_readfirstlane(cptr<uint32_t>(a.sel)[job]);
     if (ex >= a.n_exp) ex = a.n_exp - 1;  // routing only produces valid experts; never read outside the tensor
-    const bool pair = a.mode == QP_GEMV_SWIGLU;
-    const uint32_t outs = pair ? R / 2 : R;
-    const uint32_t r0 = blockIdx.x * 4 * outs + wave * outs;
-    RowRef rr[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const uint32_t o = (pair && R > 1) ? (uint32_t)(r % (R / 2 > 0 ? R / 2 : 1)) : (uint32_t)r;
-        rr[r].base = (pair && r >= R / 2) ? a.w2 : a.w;
-        rr[r].row = (uint64_t)ex * a.n + min(r0 + o, a.n - 1);
-    }
-    const uint64_t NB = total_blocks(FMT, (uint64_t)a.n_exp * a.n, K);
-    const uint32_t npc = Piece<FMT, R>::count(K);
-    Piece<FMT, R> cur;
-    if (lane < npc) cur.load(rr, NB, K, lane);
-    stage_x<FMT>(xs, xsum, a.x + 4ull * (job / a.tfijo) * K, 0, K, 0.0f, red);
-    if (r0 >= a.n) return;
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = 0.0f;
-    dot_rows_pipelined<FMT, R>(cur, rr, NB, K, xs, xsum, lane, acc);
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
-    float* y = mptr<float>(a.y) + (uint64_t)job * a.n;
-    if (pair) {
-#pragma unroll
-        for (int r = 0; r < R / 2; r++)
-            if (lane == (uint32_t)r && r0 + r < a.n) {
-                const float g = acc[r], u = acc[r + R / 2];
-                y[r0 + r] = (g / (1.0f + expf(-g))) * u;
-            }
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; r++)
-            if (lane == (uint32_t)r && r0 + r < a.n) y[r0 + r] = acc[r];
-    }
+    const PlSeg one{a.w, a.w2, a.y + 4ull * job * a.n, a.n, ex * a.n, a.n_exp * a.n,
+                    a.mode == QP_GEMV_SWIGLU ? (uint32_t)QP_GEMV_SWIGLU : (uint32_t)QP_GEMV_STORE, 0};
+    pl_gemv<FMT, R, 2>([&](uint32_t) __attribute__((always_inline)) { return one; }, 1, gridDim.x,
+                       a.x + 4ull * (job / a.tfijo) * a.k, 0, 0.0f, a.k, 0);
 }
 
 #define GEMV_EXP_KERNELS(NAME, FMT)                                                                              \
     KERNEL __launch_bounds__(256) void qp_gemv_exp_##NAME##_r2(QpGemvExpArgs a) { gemv_exp_body<FMT, 2>(a); } \
     KERNEL __launch_bounds__(256) void qp_gemv_exp_##NAME##_r4(QpGemvExpArgs a) { gemv_exp_body<FMT, 4>(a); }
 GEMV_EXP_KERNELS(q8, QP_Q8_0)
+GEMV_EXP_KERNELS(iq4nl, QP_IQ4_NL)
 GEMV_EXP_KERNELS(f32, QP_F32)
 
 // ====================================================================================== K-quant GEMV (one token)
@@ -555,7 +581,6 @@ GEMV_EXP_KERNELS(f32, QP_F32)
 // Semantics per row follow the reference's factoring: y = sum over sub-blocks of (d*sc)*sum(q*x) - (dmin*m)*sum(x)
 // (Q4_K) and (d*sc)*(sum(q*x) - 32*sum(x)) over 16-element groups (Q6_K); the summation order is this kernel's.
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <int FMT>
 struct KQ;
 template <>
@@ -603,10 +628,6 @@ QP_DEV float fmix(uint32_t m, float x, float acc) {
 // v is produced before this point and no memory access moves across it: keeps the compiler from hoisting every
 // LDS read of the input above the arithmetic that consumes the previous ones (the reads are loop-invariant).
 QP_DEV void kq_fence(float& v) { asm volatile("" : "+v"(v)::"memory"); }
-
-QP_DEV __amdgpu_buffer_rsrc_t kq_rsrc(uint64_t base, uint64_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
-}
 
 // A 32-bit load past the CU's L1 (sc0): data another CU of the XCD stored before a barrier, never read here before.
 QP_DEV uint32_t ld_sc0(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -1835,6 +1856,13 @@ QP_DEV void mm_wload(MmW& r, const QpGemmArgs& g, uint32_t row, bool on, uint32_
         r.a = gload<uint4>(g.w + bb * 32);
         r.b = gload<uint4>(g.w + bb * 32 + 16);
         r.f = gload<uint16_t>(g.w + NB * 32 + bb * 2);
+    } else if constexpr (FMT == QP_IQ4_NL) {
+        const uint64_t NB = (uint64_t)(g.wrows ? g.wrows : g.n) * (K >> 5);
+        const uint64_t blk = (uint64_t)row * (K >> 5) + (k0 >> 5) + part;
+        const bool in = k0 + 32 * part < K;
+        const uint64_t bb = in ? blk : (uint64_t)row * (K >> 5);
+        r.a = gload<uint4>(g.w + bb * 16);
+        r.f = gload<uint16_t>(g.w + NB * 16 + bb * 2);
     }
 }
 
@@ -1925,6 +1953,20 @@ QP_DEV void mm_wdeq(const MmW& r, const QpGemmArgs& g, uint32_t row, bool on, ui
 #pragma unroll
         for (int i = 0; i < 32; i++)
             w[i] = in ? (float)(int8_t)((q8[i >> 2] >> ((i & 3) * 8)) & 0xffu) * d : 0.0f;
+    } else if constexpr (FMT == QP_IQ4_NL) {
+        // w[4i..4i+3]: the low nibbles of word i; w[16+4i..]: its high nibbles (d * table[nibble])
+        const float d = h2f(r.f);
+        const uint32_t qw[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+        const bool in = k0 + 32 * part < g.k;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lo = iq4nl_lut4(qw[i] & 0x0f0f0f0fu), hi = iq4nl_lut4((qw[i] >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                w[4 * i + b] = in ? d * (float)(int8_t)((lo >> (8 * b)) & 0xffu) : 0.0f;
+                w[16 + 4 * i + b] = in ? d * (float)(int8_t)((hi >> (8 * b)) & 0xffu) : 0.0f;
+            }
+        }
     } else {
         const uint32_t kb = k0 + 32 * part;
 #pragma unroll
@@ -2648,6 +2690,7 @@ KERNEL __launch_bounds__(512) void qp_gemm_mfma256_q6k(QpGemmArgs a) { gemm_mfma
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q4k(QpGemmArgs a) { gemm_mfma_body<QP_Q4_K>(a); }
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q6k(QpGemmArgs a) { gemm_mfma_body<QP_Q6_K>(a); }
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q8(QpGemmArgs a) { gemm_mfma_body<QP_Q8_0>(a); }
+KERNEL __launch_bounds__(256) void qp_gemm_mfma_iq4nl(QpGemmArgs a) { gemm_mfma_body<QP_IQ4_NL>(a); }
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q5k(QpGemmArgs a) { gemm_mfma_body<QP_Q5_K>(a); }
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q3k(QpGemmArgs a) { gemm_mfma_body<QP_Q3_K>(a); }
 KERNEL __launch_bounds__(256) void qp_gemm_mfma_q2k(QpGemmArgs a) { gemm_mfma_body<QP_Q2_K>(a); }

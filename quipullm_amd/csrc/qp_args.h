@@ -12,6 +12,7 @@
 #define QP_Q4_K 12
 #define QP_Q5_K 13
 #define QP_Q6_K 14
+#define QP_IQ4_NL 20
 
 // Device layouts (private to the ops that read them; produced at load time by the repack ops):
 //  F32  : [N][K] floats.
@@ -20,6 +21,8 @@
 //  Q6_K : per row, 13 chunk planes (ql 0..7, qh 8..11, scales 12) at row*nb*208 + c*nb*16 + b*16, then after all
 //         rows a plane of the f16 d values [rows][nb].
 //  Q8_0 : planar over NB = N*K/32 blocks: qs [NB][32] int8 | d [NB] f16.
+//  IQ4_NL: planar over NB = N*K/32 blocks: qs [NB][16] bytes as in the GGUF block (byte l: weight l in the low
+//         nibble, weight 16 + l in the high one) | d [NB] f16 (the reference's qs / dh pair, kds.js:36-39).
 // Planar sub-arrays start at multiples of 16 bytes, so every lane load is a 16-byte vector load.
 
 // Paso (per-forward step record, reference gpu.js:9): {T, pos0, a, b}, in device memory.
@@ -36,7 +39,7 @@ typedef struct {
     uint64_t w;     // weights (device layout of fmt)
     uint64_t w2;    // second matrix (QP_GEMV_SWIGLU: the up projection; same fmt and shape)
     uint64_t y;     // output floats
-    uint32_t fmt;   // QP_F32 / QP_Q8_0 / QP_Q4_K / QP_Q5_K / QP_Q6_K
+    uint32_t fmt;   // QP_F32 / QP_Q8_0 / QP_IQ4_NL / the K-quants
     uint32_t n;     // output rows of this segment
     uint32_t wg0;   // first workgroup of this segment
     uint32_t mode;  // QP_GEMV_*
@@ -111,7 +114,7 @@ typedef struct {
     uint32_t tfix;    // 0: T from paso
     uint32_t kchunk;  // matrix-core path: inputs per K split (grid z = splits; a multiple of 64), or 0: all of k
     uint32_t rows;    // matrix-core path: token rows the xs planes and the ws partials are sized for (>= T)
-    uint32_t wrows;   // rows of the weight tensor (the Q6_K / Q8_0 scale arrays follow them), or 0: n
+    uint32_t wrows;   // rows of the weight tensor (the Q6_K / Q8_0 / IQ4_NL scale arrays follow them), or 0: n
     // grouped by expert (matmul_*_eg): lst != 0.  Grid y = n_exp * tpe slots; slot s takes tile s % tpe (128 jobs)
     // of expert s / tpe, jobs lst[off[e] ..off[e + 1]); job j reads x row j / tfijo and writes y row j, weights
     // rows e * n .. of the stacked tensor.  xrows, yrows, nlst: rows of x, y and entries of lst that exist.

@@ -168,7 +168,7 @@ int fmt_of(const char* s) {
     if (!strcmp(s, "q2k")) return QP_Q2_K;
     if (!strcmp(s, "q6k")) return QP_Q6_K;
     if (!strcmp(s, "q8")) return QP_Q8_0;
-    if (!strcmp(s, "iq4nl")) return QP_Q8_0;  // IQ4_NL matrices are repacked into the Q8_0 layout
+    if (!strcmp(s, "iq4nl")) return QP_IQ4_NL;
     if (!strcmp(s, "f32")) return QP_F32;
     return -1;
 }
@@ -176,21 +176,24 @@ int fmt_of(const char* s) {
 bool is_kq(int fmt) {
     return fmt == QP_Q2_K || fmt == QP_Q3_K || fmt == QP_Q4_K || fmt == QP_Q5_K || fmt == QP_Q6_K;
 }
+// The planar formats (bound as two buffers: quants, then the f16 scales after them) and their quant bytes per block.
+bool planar(int fmt) { return fmt == QP_Q8_0 || fmt == QP_IQ4_NL; }
+uint32_t planar_qbytes(int fmt) { return fmt == QP_Q8_0 ? 32 : 16; }
 // index of a K-quant format in the kernel tables: Q4_K, Q5_K, Q6_K, Q3_K, Q2_K
 int kq_index(int fmt) { return fmt == QP_Q5_K ? 1 : fmt == QP_Q6_K ? 2 : fmt == QP_Q3_K ? 3 : fmt == QP_Q2_K ? 4 : 0; }
 
 int check_k(int fmt, uint32_t K, const char* op) {
     if (is_kq(fmt) && K % 256)
         return fail(QP_E_ARG, "%s: K=%u is not a multiple of 256", op, K);
-    if (fmt == QP_Q8_0 && K % 32) return fail(QP_E_ARG, "%s: K=%u is not a multiple of 32", op, K);
+    if (planar(fmt) && K % 32) return fail(QP_E_ARG, "%s: K=%u is not a multiple of 32", op, K);
     if (fmt == QP_F32 && K % 16) return fail(QP_E_ARG, "%s: K=%u is not a multiple of 16", op, K);
     if (K == 0 || K > 15360) return fail(QP_E_ARG, "%s: K=%u outside 1..15360", op, K);
     return 0;
 }
 
-// Q8_0 bindings (qs, ds) must be the two planes of one device tensor: ds == qs + NB*32.
-int q8_planes(uint64_t qs, uint64_t ds, uint64_t nb, const char* op) {
-    if (ds != qs + nb * 32) return fail(QP_E_ARG, "%s: ds binding is not the scale plane of qs", op);
+// Planar bindings (qs, ds) must be the two planes of one device tensor: ds == qs + NB * (32 for Q8_0, 16 for IQ4_NL).
+int planes(int fmt, uint64_t qs, uint64_t ds, uint64_t nb, const char* op) {
+    if (ds != qs + nb * planar_qbytes(fmt)) return fail(QP_E_ARG, "%s: ds binding is not the scale plane of qs", op);
     return 0;
 }
 
@@ -209,10 +212,11 @@ int default_r(int fmt) {
     return 2;
 }
 
-Kid gemv_kid(int fmt, int R) {  // the generic kernels (Q8_0, F32)
-    int f = fmt == QP_Q8_0 ? 0 : 1;
+Kid gemv_kid(int fmt, int R) {  // the generic kernels (Q8_0, IQ4_NL, F32)
+    int f = fmt == QP_Q8_0 ? 0 : fmt == QP_IQ4_NL ? 1 : 2;
     int r = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : 3;
-    static const Kid t[2][4] = {{K_gemv_q8_r1, K_gemv_q8_r2, K_gemv_q8_r4, K_gemv_q8_r8},
+    static const Kid t[3][4] = {{K_gemv_q8_r1, K_gemv_q8_r2, K_gemv_q8_r4, K_gemv_q8_r8},
+                                {K_gemv_iq4nl_r1, K_gemv_iq4nl_r2, K_gemv_iq4nl_r4, K_gemv_iq4nl_r8},
                                 {K_gemv_f32_r1, K_gemv_f32_r2, K_gemv_f32_r4, K_gemv_f32_r8}};
     return t[f][r];
 }
@@ -345,13 +349,13 @@ int run_gemv(int fmt, QpGemvArgs& a, int R, uint32_t max_wg, uint32_t* grid_out)
 // ------------------------------------------------------------------------------------------------ reference ops
 // matmul_<fmt>_1 (kquants.js:188-251, gpu.js:123-198): P{N,K,acc,tfijo}; [paso, w, x, y] (q8: [paso,qs,ds,x,y]).
 int op_matmul_1(const Ctx& c, int fmt, const char* name) {
-    const bool q8 = fmt == QP_Q8_0;
+    const bool q8 = planar(fmt);
     if (int e = need_bufs(c, q8 ? 5 : 4, name)) return e;
     const uint32_t N = c.U(0), K = c.U(1), acc = c.U(2);
     if (int e = check_k(fmt, K, name)) return e;
     const uint64_t w = c.B(1);
     if (q8)
-        if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)N * K / 32, name)) return e;
+        if (int e = planes(fmt, c.B(1), c.B(2), (uint64_t)N * K / 32, name)) return e;
     QpGemvArgs a = {};
     a.nseg = 1;
     a.k = K;
@@ -421,12 +425,12 @@ int split_input(uint64_t x, uint64_t xs, uint64_t paso, uint32_t K, uint32_t row
 }
 
 int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z) {
-    const bool q8 = fmt == QP_Q8_0;
+    const bool q8 = planar(fmt);
     if (int e = need_bufs(c, q8 ? 5 : 4, name)) return e;
     const uint32_t N = c.U(0), K = c.U(1), acc = c.U(2);
     if (int e = check_k(fmt, K, name)) return e;
     if (q8)
-        if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)N * K / 32, name)) return e;
+        if (int e = planes(fmt, c.B(1), c.B(2), (uint64_t)N * K / 32, name)) return e;
     QpGemmArgs a = {};
     a.w = c.B(1);
     a.x = c.B(q8 ? 3 : 2);
@@ -440,7 +444,7 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
     if (tmax >= 64 && !getenv_flag("QP_NO_MFMA")) {
         // matrix cores: 128 x 128 tiles (the kernel reads T from paso; tiles past it exit)
         const Kid k = fmt == QP_Q4_K ? K_gemm_mfma_q4k : fmt == QP_Q6_K ? K_gemm_mfma_q6k
-                    : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
+                    : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : fmt == QP_IQ4_NL ? K_gemm_mfma_iq4nl : K_gemm_mfma_f32;
         uint32_t mt = cdiv(tmax, 128);
         uint32_t nt = cdiv(N, 128);
         if (!g_capturing || g_noalloc) {
@@ -548,15 +552,15 @@ int op_matmul_glu(const Ctx& c, int fmt, const char* name) {
 // matmul_<fmt>_e (kquants.js:256-304, kds.js:110-186): P{N,K,acc,tfijo,E}; [paso, w, x, y, sel]
 // (q8: [paso, qs, ds, x, y, sel]); jobs = gz.  E (the 5th word) sizes the planar formats' sub-arrays.
 int op_matmul_e(const Ctx& c, int fmt, const char* name, bool swiglu) {
-    const bool q8 = fmt == QP_Q8_0;
+    const bool q8 = planar(fmt);
     const uint32_t nb = (q8 ? 6 : 5) + (swiglu ? 1 : 0);
     if (int e = need_bufs(c, nb, name)) return e;
     const uint32_t N = c.U(0), K = c.U(1), tfijo = c.U(3), E = c.U(4);
     if (int e = check_k(fmt, K, name)) return e;
-    if (fmt == QP_Q8_0 && E == 0) return fail(QP_E_ARG, "%s: P.E (expert count) is 0", name);
+    if (q8 && E == 0) return fail(QP_E_ARG, "%s: P.E (expert count) is 0", name);
     if (tfijo == 0) return fail(QP_E_ARG, "%s: tfijo is 0", name);
     if (q8)
-        if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)E * N * K / 32, name)) return e;
+        if (int e = planes(fmt, c.B(1), c.B(2), (uint64_t)E * N * K / 32, name)) return e;
     QpGemvExpArgs a = {};
     uint32_t i = 1;
     a.w = c.B(i++);
@@ -583,21 +587,21 @@ int op_matmul_e(const Ctx& c, int fmt, const char* name, bool swiglu) {
     }
     const int R = 4;
     const uint32_t outs = (swiglu ? R / 2 : R) * 4;
-    const Kid k = fmt == QP_Q8_0 ? K_gemv_exp_q8_r4 : K_gemv_exp_f32_r4;
+    const Kid k = fmt == QP_Q8_0 ? K_gemv_exp_q8_r4 : fmt == QP_IQ4_NL ? K_gemv_exp_iq4nl_r4 : K_gemv_exp_f32_r4;
     return launch(k, cdiv(N, outs), c.gz, 1, 256, gemv_lds(K), a);
 }
 
 // embed_<fmt> (kquants.js:481-504, gpu.js:585-618): P{D, rows}; [paso, w, ids, y] (q8: [paso,qs,ds,ids,y]).
 int op_embed(const Ctx& c, int fmt, const char* name) {
-    const bool q8 = fmt == QP_Q8_0;
+    const bool q8 = planar(fmt);
     if (int e = need_bufs(c, q8 ? 5 : 4, name)) return e;
     QpEmbedArgs a = {};
     a.fmt = fmt;
     a.d = c.U(0);
     a.rows = c.U(1);
-    if ((fmt == QP_Q6_K || fmt == QP_Q8_0) && a.rows == 0) return fail(QP_E_ARG, "%s: P.rows is 0", name);
+    if ((fmt == QP_Q6_K || q8) && a.rows == 0) return fail(QP_E_ARG, "%s: P.rows is 0", name);
     if (q8)
-        if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)a.rows * a.d / 32, name)) return e;
+        if (int e = planes(fmt, c.B(1), c.B(2), (uint64_t)a.rows * a.d / 32, name)) return e;
     a.w = c.B(1);
     a.ids = c.B(q8 ? 3 : 2);
     a.y = c.B(q8 ? 4 : 3);
@@ -896,14 +900,14 @@ int op_moe_group(const Ctx& c) {
 // y[j][r] (+)= W[e*N + r] . x[j / tfijo] for every job j of expert e (lst / off from moe_group), on the matrix
 // cores: 128 jobs x 128 rows per workgroup, E * ceil(32*gz / 128) job tiles.
 int op_matmul_eg(const Ctx& c, int fmt, const char* name) {
-    const bool q8 = fmt == QP_Q8_0;
+    const bool q8 = planar(fmt);
     if (int e = need_bufs(c, q8 ? 7 : 6, name)) return e;
     const uint32_t N = c.U(0), K = c.U(1), acc = c.U(2), tfijo = c.U(3), E = c.gy, tz = c.gz;
     if (int e = check_k(fmt, K, name)) return e;
     if (N == 0 || tfijo == 0 || E == 0 || tz == 0)
         return fail(QP_E_ARG, "%s: N=%u tfijo=%u, dispatch y (experts)=%u z=%u", name, N, tfijo, E, tz);
     if (q8)
-        if (int e = q8_planes(c.B(1), c.B(2), (uint64_t)E * N * K / 32, name)) return e;
+        if (int e = planes(fmt, c.B(1), c.B(2), (uint64_t)E * N * K / 32, name)) return e;
     if (is_kq(fmt) && kq_tensor_bytes(fmt, (uint64_t)E * N, K) >= (1ull << 31))
         return fail(QP_E_ARG, "%s: expert tensor is 2 GiB or larger", name);
     QpGemmArgs a = {};
@@ -933,18 +937,19 @@ int op_matmul_eg(const Ctx& c, int fmt, const char* name) {
     if ((uint64_t)E * a.tpe > 65535) return fail(QP_E_ARG, "%s: %u experts x %u job tiles", name, E, a.tpe);
     const Kid k = fmt == QP_Q4_K ? K_gemm_mfma_q4k : fmt == QP_Q6_K ? K_gemm_mfma_q6k
                 : fmt == QP_Q5_K ? K_gemm_mfma_q5k : fmt == QP_Q3_K ? K_gemm_mfma_q3k
-                : fmt == QP_Q2_K ? K_gemm_mfma_q2k : fmt == QP_Q8_0 ? K_gemm_mfma_q8 : K_gemm_mfma_f32;
+                : fmt == QP_Q2_K ? K_gemm_mfma_q2k : fmt == QP_Q8_0 ? K_gemm_mfma_q8
+                : fmt == QP_IQ4_NL ? K_gemm_mfma_iq4nl : K_gemm_mfma_f32;
     return launch(k, cdiv(N, 128), E * a.tpe, 1, 256, 0, a);
 }
 
 // ------------------------------------------------------------------------------------------------ backend ops
-// Formats a format word may name: f32, Q8_0 (planar) and the K-quants (row chunk planes).
-bool known_fmt(int f) { return f == QP_F32 || f == QP_Q8_0 || is_kq(f); }
+// Formats a format word may name: f32, Q8_0 and IQ4_NL (planar) and the K-quants (row chunk planes).
+bool known_fmt(int f) { return f == QP_F32 || planar(f) || is_kq(f); }
 
 // Bytes of a device tensor of `rows` rows of K elements in the layout of fmt.
 uint64_t tensor_bytes(int fmt, uint64_t rows, uint32_t K) {
     if (is_kq(fmt)) return kq_tensor_bytes(fmt, rows, K);
-    if (fmt == QP_Q8_0) return rows * K + rows * (K / 32) * 2;
+    if (planar(fmt)) return rows * (K / 32) * (planar_qbytes(fmt) + 2);
     return rows * K * 4ull;
 }
 
@@ -975,7 +980,7 @@ int op_gemv(const Ctx& c) {
     if (R != 1 && R != 2 && R != 4 && R != 8) return fail(QP_E_ARG, "gemv: R=%d", R);
     const uint32_t max_wg = c.U(5);
     const int fmt = (int)c.U(6);
-    if (!known_fmt(fmt)) return fail(QP_E_ARG, "gemv: format %d is not a device layout (f32 0, Q8_0 8, K-quants 10..14)", fmt);
+    if (!known_fmt(fmt)) return fail(QP_E_ARG, "gemv: format %d is not a device layout (f32 0, Q8_0 8, K-quants 10..14, IQ4_NL 20)", fmt);
     a.paso = c.B(0);
     a.x = c.B(1);
     a.norm_w = c.B(2);
@@ -1274,11 +1279,11 @@ int op_repack(const Ctx& c, Kid k, const char* name) {
     a.dst = c.B(2);
     uint64_t threads = a.nblocks;
     if (k == K_repack_q8 || k == K_repack_iq4nl) {
-        // raw blocks of 34 (Q8_0) or 18 (IQ4_NL) bytes -> 34 bytes each in the planar layout
+        // raw blocks of 34 (Q8_0) or 18 (IQ4_NL) bytes -> as many bytes each in the planar layout
         const uint64_t rs = buf_room(a.src), rd = buf_room(a.dst), in = a.nblocks * (k == K_repack_q8 ? 34 : 18);
-        if ((rs && rs < in) || (rd && rd < a.nblocks * 34))
-            return fail(QP_E_ARG, "%s: %llu blocks need %llu source and %llu destination bytes", name,
-                        (unsigned long long)a.nblocks, (unsigned long long)in, (unsigned long long)(a.nblocks * 34));
+        if ((rs && rs < in) || (rd && rd < in))
+            return fail(QP_E_ARG, "%s: %llu blocks need %llu source and destination bytes", name,
+                        (unsigned long long)a.nblocks, (unsigned long long)in);
     }
     if (k == K_repack_q4k || k == K_repack_q5k || k == K_repack_q6k || k == K_repack_q3k || k == K_repack_q2k) {
         if (a.k == 0 || a.k % 256 || a.k > 15360) return fail(QP_E_ARG, "%s: K=%u must be a multiple of 256 <= 15360", name, a.k);
@@ -1321,7 +1326,7 @@ int op_dequant(const Ctx& c) {
     a.w = c.B(1);
     a.y = c.B(2);
     if (!known_fmt((int)a.fmt)) return fail(QP_E_ARG, "dequant: format %u is not a device layout", a.fmt);
-    if (a.k == 0) a.k = (a.fmt == QP_Q8_0) ? 32 : (a.fmt == QP_F32 ? 1 : 256);  // one row per block
+    if (a.k == 0) a.k = planar((int)a.fmt) ? 32 : (a.fmt == QP_F32 ? 1 : 256);  // one row per block
     if (int e = check_k((int)a.fmt, a.k, "dequant")) return e;
     if (a.nelem % a.k) return fail(QP_E_ARG, "dequant: %llu elements are not whole rows of K=%u",
                                    (unsigned long long)a.nelem, a.k);

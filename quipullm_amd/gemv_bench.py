@@ -32,8 +32,9 @@ def parse_shape(s):
     return FMT_BY_NAME[f], int(n), int(k)
 
 
-def time_gemv(q, fmt, N, K, iters=200, rotate_bytes=640 << 20, R=0):
-    """Average launch duration of the fused GEMV on one shape; returns a dict."""
+def time_gemv(q, fmt, N, K, iters=200, rotate_bytes=640 << 20, R=0, max_wg=0):
+    """Average launch duration of the fused GEMV on one shape; returns a dict.  R, max_wg: the op's rows per
+    wavefront and grid cap (0: the backend's defaults)."""
     paso = q.paso(1, 0)
     nbytes = capi.gguf_bytes(fmt, N, K)
     ncopy = max(2, rotate_bytes // nbytes + 1)
@@ -41,7 +42,7 @@ def time_gemv(q, fmt, N, K, iters=200, rotate_bytes=640 << 20, R=0):
     hs = [q.upload_matrix(fmt, raw, N, K) for _ in range(ncopy)]
     xb = q.buffer_from(np.random.default_rng(4).standard_normal(K).astype(np.float32))
     yb = q.alloc(N * 4)
-    u = capi.gemv_uniform(1, K, R=R, fmt=fmt, segs=[(capi.STORE, N, 0, N)])
+    u = capi.gemv_uniform(1, K, R=R, max_wg=max_wg, fmt=fmt, segs=[(capi.STORE, N, 0, N)])
     for i in range(10):
         q.dispatch("gemv", u, [paso, xb, 0, 0, hs[i % ncopy], 0, yb])
     q.sync()
@@ -58,8 +59,8 @@ def time_gemv(q, fmt, N, K, iters=200, rotate_bytes=640 << 20, R=0):
         q.free(h)
     q.event_free(e0)
     q.event_free(e1)
-    return {"kernel": "qp_gemv_%s" % capi.FMT_NAME[fmt], "format": capi.FMT_NAME[fmt], "N": N, "K": K,
-            "bytes": alg, "launches": iters, "us_per_launch": us, "GBs": alg / (us * 1e-6) / 1e9}
+    return {"kernel": "qp_gemv_%s" % capi.FMT_NAME[fmt], "format": capi.FMT_NAME[fmt], "N": N, "K": K, "R": R,
+            "max_wg": max_wg, "bytes": alg, "launches": iters, "us_per_launch": us, "GBs": alg / (us * 1e-6) / 1e9}
 
 
 def time_copy(q, nbytes, iters=20):
@@ -88,10 +89,11 @@ def time_copy(q, nbytes, iters=20):
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--shape", action="append", help="fmt:NxK with fmt in q4k, q6k, q8, f32")
+    ap.add_argument("--shape", action="append", help="fmt:NxK with fmt in q2k, q3k, q4k, q5k, q6k, q8, iq4nl, f32")
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--rotate-mb", type=int, default=640)
     ap.add_argument("--R", type=int, default=0, help="rows per wavefront (0: the backend default)")
+    ap.add_argument("--max-wg", type=int, default=0, help="grid cap (0: the backend default)")
     ap.add_argument("--copy-bytes", type=int, default=0)
     a = ap.parse_args()
     q = capi.Quipu(0)
@@ -100,7 +102,7 @@ def main():
     shapes = a.shape or ([] if a.copy_bytes else ["q4k:14336x4096"])
     for s in shapes:
         fmt, N, K = parse_shape(s)
-        print(json.dumps(time_gemv(q, fmt, N, K, a.iters, a.rotate_mb << 20, a.R)), flush=True)
+        print(json.dumps(time_gemv(q, fmt, N, K, a.iters, a.rotate_mb << 20, a.R, a.max_wg)), flush=True)
 
 
 if __name__ == "__main__":

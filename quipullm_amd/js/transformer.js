@@ -17,7 +17,7 @@ const ROPE_NEOX = new Set(['qwen2', 'qwen3', 'qwen3moe', 'phi3', 'gemma', 'gemma
 const KQ = new Set(['q2k', 'q3k', 'q4k', 'q5k', 'q6k']);
 const MEZCLA = new Set(['q4k', 'q6k']);    // formats whose GEMV segments may share one launch
 const EG = new Set(['q2k', 'q3k', 'q4k', 'q5k', 'q6k', 'q8', 'f32', 'iq4nl']);   // grouped expert matmul (matmul_<fmt>_eg)
-// handles bound as two buffers (quants, scales): Q8_0 and IQ4_NL (held in the Q8_0 layout)
+// handles bound as two buffers (quants, scales): Q8_0 and IQ4_NL
 function plano(W) { return W.tipo === 'q8' || W.tipo === 'iq4nl'; }
 // moe_group lists at most 65535 jobs (16-bit counts) of at most 256 experts: a batch whose jobs (tokens x
 // experts used) exceed that takes the ungrouped per-job expert path instead of failing.
@@ -25,7 +25,7 @@ const MOE_GROUP_JOBS = 65535, MOE_GROUP_EXPERTS = 256;
 function agrupable(formatos, batch, nUsados, nExp) {
   return formatos && batch * nUsados <= MOE_GROUP_JOBS && nExp <= MOE_GROUP_EXPERTS;
 }
-const FMT_ID = { f32: 0, q8: 8, q2k: 10, q3k: 11, q4k: 12, q5k: 13, q6k: 14, iq4nl: 8 };  // iq4nl: the Q8_0 layout
+const FMT_ID = { f32: 0, q8: 8, q2k: 10, q3k: 11, q4k: 12, q5k: 13, q6k: 14, iq4nl: 20 };
 // gemv segment modes (qp_args.h)
 const STORE = 0, ACC = 1, SWIGLU = 2, ARGMAX = 3;
 const AMAX_WG = 512;   // workgroups of the fused output GEMV = partial maxima for the device argmax

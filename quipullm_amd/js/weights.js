@@ -2,9 +2,10 @@
 // Loading of GGUF tensors into device buffers, from a local file or from the server's file URL by ranges.
 //
 // Same interface as quipullm's CargadorPesos (web/js/weights.js:15-139): existe(name), info(name),
-// f32(name) -> buffer, matriz(name) -> {tipo, N, K, w} ({tipo:'q8' | 'iq4nl', N, K, qs, ds} for Q8_0, IQ4_NL).  The device
-// layout behind a handle is this backend's own: K-quant blocks and Q8_0 repacked on the device
-// into planar arrays (quants | scales) so every lane load is a 16-byte vector load.
+// f32(name) -> buffer, matriz(name) -> {tipo, N, K, w} ({tipo:'q8' | 'iq4nl', N, K, qs, ds} for Q8_0, IQ4_NL: qs and
+// ds are the quant and scale planes of one buffer).  The device layout behind a handle is this backend's own:
+// K-quant blocks, Q8_0 and IQ4_NL repacked on the device into planar arrays (quants | scales) so every lane load is
+// a 16-byte vector load.
 // Source: a path (read synchronously), or {url} (the reference engine's /engine/file/<id>, web/js/weights.js:51):
 // then the caller awaits precargar(names) before the synchronous calls that use those tensors.
 const fs = require('fs');
@@ -142,13 +143,13 @@ class CargadorPesos {
       return { tipo: 'q8', N: N, K: K, w: w, qs: w, ds: vista(w, N * K) };
     }
     if (t.tipo === 20) {
-      // IQ4_NL (reference weights.js:110-116): repacked on the device into the Q8_0 layout (q = table[nibble],
-      // the same d), which every Q8_0 kernel reads; the ops are dispatched under the matmul_iq4nl_* names
+      // IQ4_NL (reference weights.js:110-116): the nibble bytes as they are (16 per block) then the f16 scales,
+      // 18 bytes per 32 weights as in the file; the reference's qs / dh pair is the two planes of one buffer
       if (K % 32) throw new Error(nombre + ': K=' + K + ' is not a multiple of 32');
       const u8 = this.bytes(t);
-      const w = this._subirRepack(u8, 'repack_iq4nl', N * K / 32, K, nombre, N * K / 32 * 34);
+      const w = this._subirRepack(u8, 'repack_iq4nl', N * K / 32, K, nombre);
       this.buffers.push(w);
-      return { tipo: 'iq4nl', N: N, K: K, w: w, qs: w, ds: vista(w, N * K) };
+      return { tipo: 'iq4nl', N: N, K: K, w: w, qs: w, ds: vista(w, N * K / 2) };
     }
     if (t.tipo === 0 || t.tipo === 1 || t.tipo === 30) {
       const w = this.f32(nombre);

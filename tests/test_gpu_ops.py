@@ -97,7 +97,7 @@ def test_embed_rows_bit_exact(quipu, dev, oracle, fmt):
     T = len(ids)
     y = dev.zeros(T * D * 4)
     nm = "embed_" + capi.FMT_NAME[fmt]
-    wb = [w, w + V * D] if fmt in PLANAR else [w]
+    wb = [w, capi.scale_plane(fmt, w, V, D)] if fmt in PLANAR else [w]
     quipu.dispatch(nm, [("u", D), ("u", V)], [dev.paso(T, 0)] + wb + [dev.buf(ids), y], ((T * D + 255) // 256,))
     got = dev.get(y, (T, D))
     np.testing.assert_array_equal(got.view(np.uint32), oracle.embed(fmt, raw, D, ids).view(np.uint32))
@@ -114,7 +114,7 @@ def test_matmul_1_reference_op(quipu, dev, oracle, fmt, N, K):
     x = np.random.default_rng(1).standard_normal(K).astype(np.float32)
     y0 = np.random.default_rng(2).standard_normal(N).astype(np.float32)
     W = oracle.dequant(fmt, raw, N * K).reshape(N, K) if fmt != capi.F32 else raw.view(np.float32).reshape(N, K)
-    wb = [w, w + N * K] if fmt in PLANAR else [w]
+    wb = [w, capi.scale_plane(fmt, w, N, K)] if fmt in PLANAR else [w]
     for acc in (0, 1):
         y = dev.buf(y0)
         quipu.dispatch("matmul_%s_1" % capi.FMT_NAME[fmt], [("u", N), ("u", K), ("u", acc), ("u", 0)],
@@ -257,7 +257,7 @@ def test_matmul_multi_token(quipu, dev, oracle, fmt, T, op):
     y = dev.buf(y0)
     wb = [dev.matrix(fmt, raw, N, K)]
     if fmt in PLANAR:
-        wb.append(wb[0] + N * K)
+        wb.append(capi.scale_plane(fmt, wb[0], N, K))
     grid = ((N + 63) // 64, 1, (T + 31) // 32) if op == "t" else capi.dim2((N + 7) // 8) + ((T + 3) // 4,)
     quipu.dispatch("matmul_%s_%s" % (capi.FMT_NAME[fmt], op), [("u", N), ("u", K), ("u", 1), ("u", 0)],
                    [dev.paso(T, 0)] + wb + [dev.buf(x), y], grid)
@@ -285,7 +285,7 @@ def test_matmul_prefill_mfma(quipu, dev, oracle, fmt, T, N, K, acc):
     y = dev.buf(y0)
     wb = [dev.matrix(fmt, raw, N, K)]
     if fmt in PLANAR:
-        wb.append(wb[0] + N * K)
+        wb.append(capi.scale_plane(fmt, wb[0], N, K))
     quipu.dispatch("matmul_%s_t" % capi.FMT_NAME[fmt], [("u", N), ("u", K), ("u", acc), ("u", 0)],
                    [dev.paso(T, 0)] + wb + [dev.buf(x), y], ((N + 63) // 64, 1, (T + 31) // 32))
     got = dev.get(y, (T, N))
@@ -448,7 +448,7 @@ def test_matmul_prefill_mfma_ragged_k(quipu, dev, oracle, fmt, T, N, K):
     W = (oracle.dequant(fmt, raw, N * K) if fmt != capi.F32 else raw.view(np.float32)).reshape(N, K)
     wb = [dev.matrix(fmt, raw, N, K)]
     if fmt in PLANAR:
-        wb.append(wb[0] + N * K)
+        wb.append(capi.scale_plane(fmt, wb[0], N, K))
     name = "matmul_%s_t" % capi.FMT_NAME[fmt]
     uni = [("u", N), ("u", K), ("u", 0), ("u", 0)]
     Tp = T + 200
@@ -511,7 +511,7 @@ def test_matmul_grouped_by_expert(quipu, dev, oracle, fmt, tfijo, acc):
     sb, lb, ob = dev.buf(sel), dev.zeros(4 * njob), dev.zeros(4 * (E + 1))
     quipu.dispatch("moe_group", [("u", E), ("u", k)], [dev.paso(T, 0), sb, lb, ob])
     hw = dev.matrix(fmt, raw, E * N, K)
-    wb = [hw, hw + E * N * K] if fmt in PLANAR else [hw]
+    wb = [hw, capi.scale_plane(fmt, hw, E * N, K)] if fmt in PLANAR else [hw]
     yb = dev.buf(y0)
     u = [("u", N), ("u", K), ("u", acc), ("u", tfijo)]
     quipu.dispatch("matmul_%s_eg" % capi.FMT_NAME[fmt], u, [dev.paso(T, 0)] + wb + [dev.buf(x), yb, lb, ob],
@@ -539,7 +539,7 @@ def test_matmul_expert_jobs(quipu, dev, oracle, fmt):
     hg, hu = dev.matrix(fmt, rg, E * N, K), dev.matrix(fmt, ru, E * N, K)
     y = dev.zeros(T * k * N * 4)
     u = [("u", N), ("u", K), ("u", 0), ("u", k), ("u", E)]
-    wb = [hg, hg + E * N * K] if fmt in PLANAR else [hg]
+    wb = [hg, capi.scale_plane(fmt, hg, E * N, K)] if fmt in PLANAR else [hg]
     xb, sb, pb = dev.buf(x), dev.buf(sel), dev.paso(T, 0)
     quipu.dispatch("matmul_%s_e" % capi.FMT_NAME[fmt], u, [pb] + wb + [xb, y, sb], (1, 1, T * k))
     got = dev.get(y, (T * k, N))
@@ -1435,7 +1435,7 @@ def test_graph_replay_matches_eager(quipu, dev, oracle):
 
 # ------------------------------------------------------------------------------------------------ errors
 def raw_fmt_word(u, fmt):
-    """A gemv uniform with its format word replaced by fmt as given (no mapping to a device layout)."""
+    """A gemv uniform with its format word replaced by fmt."""
     u = list(u)
     u[6] = ("u", fmt)
     return u
@@ -1462,13 +1462,13 @@ def test_host_checks_reject_bad_dispatches(quipu, dev):
                       ("u", 0), ("u", 0), ("u", 8)], [p, x, x, x, y, y, 0, 0, y, y]),
         ("moe_topk", [("u", 2000), ("u", 8), ("u", 1), ("f", 1)], [p, x, y, y]),
         ("matmul_q8_1", [("u", 16), ("u", 256), ("u", 0), ("u", 0)], [p, w, w + 8, x, y]),
-        # a format word that is not a device layout (the GGUF type of IQ4_NL), and weights smaller than their
-        # format and rows need (16 f32 rows of 256 in 2304 bytes; 32 Q4_K rows)
-        ("gemv", raw_fmt_word(capi.gemv_uniform(1, 256, segs=[(capi.STORE, 16, 0, 16)]), capi.IQ4_NL),
+        # a format word that is not a device layout (the GGUF type of F16, converted to f32 at load), and weights
+        # smaller than their format and rows need (16 f32 rows of 256 in 2304 bytes; 32 Q4_K rows)
+        ("gemv", raw_fmt_word(capi.gemv_uniform(1, 256, segs=[(capi.STORE, 16, 0, 16)]), 1),
          [p, x, 0, 0, w, 0, y]),
         ("gemv", capi.gemv_uniform(1, 256, fmt=capi.F32, R=1, segs=[(capi.STORE, 16, 0, 16)]), [p, x, 0, 0, w, 0, y]),
         ("gemv", capi.gemv_uniform(1, 256, segs=[(capi.STORE, 16, 0, 32)]), [p, x, 0, 0, w, 0, y]),
-        ("dequant", [("u", capi.IQ4_NL), ("u", 512), ("u", 0), ("u", 256)], [0, w, y]),
+        ("dequant", [("u", 1), ("u", 512), ("u", 0), ("u", 256)], [0, w, y]),
         ("dequant", [("u", capi.Q4_K), ("u", 32 * 256), ("u", 0), ("u", 256)], [0, w, y]),
     ]
     for name, u, b in bad:

@@ -116,6 +116,7 @@ def test_device_layout_sizes():
     assert capi.device_bytes(capi.Q4_K, 14336, 4096) == 14336 * 16 * 144
     assert capi.device_bytes(capi.Q6_K, 4096, 4096) == 4096 * 16 * 210
     assert capi.device_bytes(capi.Q8_0, 64, 2048) == 64 * 64 * 34
+    assert capi.device_bytes(capi.IQ4_NL, 64, 2048) == capi.gguf_bytes(capi.IQ4_NL, 64, 2048) == 64 * 64 * 18
     assert capi.device_bytes(capi.F32, 3, 5) == 60
     assert capi.gguf_bytes(capi.Q3_K, 8, 512) == 8 * 2 * 110 and capi.device_bytes(capi.Q3_K, 8, 512) == 8 * 2 * 112
     assert capi.device_bytes(capi.Q2_K, 8, 512) == capi.gguf_bytes(capi.Q2_K, 8, 512) == 8 * 2 * 84

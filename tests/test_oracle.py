@@ -36,7 +36,9 @@ def test_f16_rounding_matches_numpy(oracle):
                          np.array([65504, 65519.99, 65520, 1e6, -1e9, 2.0 ** -25, 2.0 ** -24 * 1.5, 0.0, -0.0])]
                         ).astype(np.float32)
     got = np.array([oracle.f16_from(float(x)) for x in xs], np.uint16)
-    np.testing.assert_array_equal(got, xs.astype(np.float16).view(np.uint16))
+    with np.errstate(over="ignore"):  # the values past 65520 round to infinity on purpose
+        want = xs.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(got, want)
     assert oracle.f16_from(float("nan")) & 0x7c00 == 0x7c00 and oracle.f16_from(float("nan")) & 0x3ff
 
 
