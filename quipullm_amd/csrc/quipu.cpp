@@ -273,6 +273,15 @@ Kid kq_kid(int fmt, int R, bool x2, bool expert) {
     return t[expert ? 1 : 0][kq_index(fmt)][R == 2 ? 1 : 0][x2 ? 1 : 0];
 }
 
+int need_room(uint64_t p, uint64_t bytes, const char* op, const char* what);
+// An argmax segment's partial maxima: one 8-byte entry per workgroup of the launch.
+int amax_room(const QpGemvArgs& a, uint32_t grid) {
+    for (uint32_t i = 0; i < a.nseg; i++)
+        if (a.seg[i].mode == QP_GEMV_ARGMAX)
+            return need_room(a.amax, 8ull * grid, "gemv", "the argmax partials (one entry per workgroup)");
+    return 0;
+}
+
 // Units per segment, then the grid: one unit per wavefront, at most two workgroups per CU (the kernel strides
 // over further units); max_wg caps it (the ARGMAX partials hold one entry per workgroup).
 int run_gemv_kq(int fmt, QpGemvArgs& a, uint32_t max_wg, uint32_t* grid_out) {
@@ -302,6 +311,7 @@ int run_gemv_kq(int fmt, QpGemvArgs& a, uint32_t max_wg, uint32_t* grid_out) {
     const bool wide = a.k > 8192 && R == 1 && !mixed && !a.norm_w;
     const uint32_t waves = wide ? 8 : 4;
     uint32_t grid = cdiv(total, waves);
+    // (3, 4, 6 or 8 workgroups per CU measured slower: each workgroup stages the input once more)
     if (grid > 2 * (uint32_t)g_cus) grid = 2 * (uint32_t)g_cus;
     if (max_wg && grid > max_wg) grid = max_wg;
     if (grid) {
@@ -311,6 +321,7 @@ int run_gemv_kq(int fmt, QpGemvArgs& a, uint32_t max_wg, uint32_t* grid_out) {
         grid = cdiv(total, waves * k);
     }
     if (grid == 0) grid = 1;
+    if (int e = amax_room(a, grid)) return e;
     if (grid_out) *grid_out = grid;
     if (wide) {
         static const Kid wide_kid[5] = {K_gemv_q4k_r1k2, K_gemv_q5k_r1k2, K_gemv_q6k_r1k2, K_gemv_q3k_r1k2,
@@ -342,6 +353,7 @@ int run_gemv(int fmt, QpGemvArgs& a, int R, uint32_t max_wg, uint32_t* grid_out)
     const uint32_t lds = gemv_lds(a.k);
     if (!max_wg) max_wg = resident_wgs(kid, 256, lds);  // persistent: one wave of resident workgroups
     uint32_t grid = max_wg && max_wg < total ? max_wg : total;
+    if (int e = amax_room(a, grid)) return e;
     if (grid_out) *grid_out = grid;
     return launch(kid, grid, 1, 1, 256, lds, a);
 }

@@ -1447,6 +1447,7 @@ def test_host_checks_reject_bad_dispatches(quipu, dev):
     y = dev.zeros(4096 * 4)
     w = dev.zeros(144 * 16)
     p = dev.paso(1, 0)
+    wbig, am1 = dev.zeros(144 * 4096), dev.zeros(8)
     bad = [
         ("gemv", capi.gemv_uniform(0, 256, segs=[]), [p, x, 0, 0]),
         ("gemv", capi.gemv_uniform(1, 256, R=3, segs=[(capi.STORE, 16, 0, 16)]), [p, x, 0, 0, w, 0, y]),
@@ -1470,6 +1471,9 @@ def test_host_checks_reject_bad_dispatches(quipu, dev):
         ("gemv", capi.gemv_uniform(1, 256, segs=[(capi.STORE, 16, 0, 32)]), [p, x, 0, 0, w, 0, y]),
         ("dequant", [("u", 1), ("u", 512), ("u", 0), ("u", 256)], [0, w, y]),
         ("dequant", [("u", capi.Q4_K), ("u", 32 * 256), ("u", 0), ("u", 256)], [0, w, y]),
+        # an argmax segment whose partials buffer holds fewer entries than the launch has workgroups (4096 Q4_K
+        # rows of 256: 64 units, 16 workgroups, one 8-byte entry each)
+        ("gemv", capi.gemv_uniform(1, 256, segs=[(capi.ARGMAX, 4096, 0, 4096)]), [p, x, 0, am1, wbig, 0, y]),
     ]
     for name, u, b in bad:
         with pytest.raises(capi.QuipuError):
