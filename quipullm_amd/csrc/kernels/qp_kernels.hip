@@ -465,9 +465,9 @@ QP_DEV void pl_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_wg, uint64_t x, 
         const uint32_t p = lane + 64 * jC;
         X.compute(npc, xs, p < npc ? p : npc - 1, acc);
         if (++jC < ppl) return;
-        // end of the pass: reduce across the wavefront and defer the outputs (none for a padding pass)
+        // end of the pass: reduce across the wavefront and defer the outputs
         jC = 0;
-        if (kC++ >= mine) return;
+        kC++;
 #pragma unroll
         for (int r = 0; r < R; r++) acc[r] = wave_sum_v(acc[r], lane) * inv;
         const uint32_t outs = PC.pair ? R / 2 : R;
@@ -492,15 +492,19 @@ QP_DEV void pl_gemv(SegAt seg_at, uint32_t nseg, uint32_t total_wg, uint64_t x, 
 #pragma unroll
         for (int r = 0; r < R; r++) acc[r] = 0.0f;
     };
-    // the items run in whole rounds of D (the last round's items past n_total load nothing and write nothing), so
-    // that the loop body has no exit between its loads and the waits for them
-    for (uint32_t n0 = 0; n0 < n_total; n0 += D) {
+    // whole rounds of D items (the loop body has no exit between its loads and the waits for them; loads past the
+    // wave's last item are empty), then the remaining items, whose loads are already in flight
+    uint32_t n0 = 0;
+    for (; n0 + D <= n_total; n0 += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
-            load_next(buf[(d + D - 1) % D]);  // item n0 + d + D - 1 (an empty one past the wave's last)
+            load_next(buf[(d + D - 1) % D]);  // item n0 + d + D - 1
             compute(buf[d]);
         }
     }
+#pragma unroll
+    for (int d = 0; d + 1 < D; d++)
+        if (n0 + d < n_total) compute(buf[d]);
     flush(false);
     if (amax) {
         if (lane == 0) wbest[wave] = best;
