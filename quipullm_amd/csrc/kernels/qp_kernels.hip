@@ -2501,15 +2501,34 @@ QP_DEV void gemm_mfma256w_body(const QpGemmArgs& g) {
     __bf16* lds = reinterpret_cast<__bf16*>(smem4);
     const uint32_t T = g.tfix ? g.tfix : paso_T(g.paso);
     const uint32_t N = g.n, K = g.k;
-    const uint32_t mt = (uint32_t)gridDim.y, ntl = (uint32_t)gridDim.x, nz = (uint32_t)gridDim.z;
-    const uint32_t total = mt * ntl * nz, id = (blockIdx.z * mt + blockIdx.y) * ntl + blockIdx.x;
-    const uint32_t base = total >> 3, rem = total & 7, xcd = id & 7, j = id >> 3;
-    const uint32_t L = xcd * base + (xcd < rem ? xcd : rem) + j;
+    const bool split_tail = GLU && g.tail != 0;
+    const uint32_t mt = split_tail ? g.mtiles : (uint32_t)gridDim.y, ntl = split_tail ? g.ntiles : (uint32_t)gridDim.x;
+    const uint32_t nz = split_tail ? 1u : (uint32_t)gridDim.z;
+    uint32_t L, half = 0, stile = 0;  // stile: the split tile's index among the tail tiles
+    bool split = false;
+    if (split_tail) {
+        // per XCD x (item % 8): whole tiles x * F .. x * F + F - 1, then K halves of tail tiles full + x * H ..
+        const uint32_t full = mt * ntl - g.tail, F = full >> 3, H = g.tail >> 3;
+        const uint32_t xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+        if (j < F) {
+            L = xcd * F + j;
+        } else {
+            const uint32_t jj = j - F;
+            stile = xcd * H + (jj >> 1);
+            L = full + stile;
+            half = jj & 1;
+            split = true;
+        }
+    } else {
+        const uint32_t total = mt * ntl * nz, id = (blockIdx.z * mt + blockIdx.y) * ntl + blockIdx.x;
+        const uint32_t base = total >> 3, rem = total & 7, xcd = id & 7, j = id >> 3;
+        L = xcd * base + (xcd < rem ? xcd : rem) + j;
+    }
     const uint32_t m_tile = L % mt, rest = L / mt, zs = rest % nz, n_tile = rest / nz;
     const uint32_t t0 = m_tile * TM, n0 = n_tile * (GLU ? TN / 2 : TN);
-    if (t0 >= T) return;
-    const uint32_t kbeg = g.kchunk ? zs * g.kchunk : 0;
-    const uint32_t kend = g.kchunk ? min(K, kbeg + g.kchunk) : K;
+    if (t0 >= T) return;  // (both halves of a split tile: neither counts, nothing is stored)
+    const uint32_t kbeg = split ? half * (K >> 1) : g.kchunk ? zs * g.kchunk : 0;
+    const uint32_t kend = split ? kbeg + (K >> 1) : g.kchunk ? min(K, kbeg + g.kchunk) : K;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t wm = wave >> 2, wn = wave & 3;
     const uint32_t lr = tid & 255, xq = tid >> 8, wq = wave * 16 + (lane & 15), sub = lane >> 4;
@@ -2627,6 +2646,38 @@ QP_DEV void gemm_mfma256w_body(const QpGemmArgs& g) {
         step(s + 1, r1, r0);
     }
     if constexpr (GLU) {
+        if (split) {
+            // this half's sums to its slot, [wave][a][b][v][lane]; drained, then one agent-scope arrival (its
+            // release writes the L2 back); the second arrival adds the other slot (the sum of the two halves does
+            // not depend on which arrives last) and goes on with the whole tile
+            float* mine = mptr<float>(g.part) + ((uint64_t)stile * 2 + half) * (512u * 128u);
+            const float* other = cptr<float>(g.part) + ((uint64_t)stile * 2 + (half ^ 1u)) * (512u * 128u);
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 2; b++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) mine[(((wave * 4 + a) * 2 + b) * 16 + v) * 64 + lane] = acc[a][b][v];
+            vm_drain();
+            uint32_t* second = reinterpret_cast<uint32_t*>(smem4);  // the K loop's LDS is free after this barrier
+            __syncthreads();
+            if (tid == 0) {
+                QP_GLOBAL uint32_t* c = reinterpret_cast<QP_GLOBAL uint32_t*>(g.cnt) + stile;
+                const uint32_t old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+                *second = old == 1u;
+                if (old == 1u) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+            if (!*second) return;
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 2; b++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++)
+                        acc[a][b][v] = acc[a][b][v] + other[(((wave * 4 + a) * 2 + b) * 16 + v) * 64 + lane];
+        }
         // the up sums (wavefronts wn = 2, 3) to LDS, read by the gate wavefronts wn - 2 at the same index
         __syncthreads();  // every wavefront has read the last step's LDS buffer
         float* ex = reinterpret_cast<float*>(smem4);  // [wm][2][4][2][16][64] floats: 128 KB

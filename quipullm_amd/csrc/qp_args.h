@@ -121,6 +121,12 @@ typedef struct {
     uint64_t lst, off;
     uint32_t n_exp, tpe, tfijo, xrows, yrows, nlst;
     uint64_t w2;  // matmul_<fmt>_t_swiglu: the up tensor (w is the gate tensor); y = silu(x w) * (x w2)
+    // matmul_<fmt>_t_swiglu with a split tail (tail != 0): a 1-D grid of items over mtiles x ntiles tiles; per XCD
+    // (item % 8), whole tiles first, then its share of the last `tail` tiles as K halves.  Each half stores its
+    // sums to part (two 256 KB slots per split tile) and counts its arrival in cnt[tile]; the second adds the
+    // other's sums and finishes the tile (and resets the word).
+    uint32_t tail, mtiles, ntiles, pad_t;
+    uint64_t part, cnt;
 } QpGemmArgs;
 
 // moe_group: lst[off[e] .. off[e + 1]) = the jobs i < T * n (in increasing order) with sel[i] == e, e < n_exp;

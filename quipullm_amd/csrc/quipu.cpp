@@ -530,6 +530,8 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
 // matmul_<fmt>_t with 256 x 256 tiles.  Not while capturing a graph (the input planes may need a larger workspace).
 uint64_t tensor_bytes(int fmt, uint64_t rows, uint32_t K);
 int need_room(uint64_t p, uint64_t bytes, const char* op, const char* what);
+constexpr uint32_t kGluCntWords = 1024;  // split tiles of one launch at most (one arrival word each)
+uint64_t g_glu_cnt = 0;                  // the arrival words, allocated on first use, kept until the process ends
 int op_matmul_glu(const Ctx& c, int fmt, const char* name) {
     if (int e = need_bufs(c, 5, name)) return e;
     const uint32_t N = c.U(0), K = c.U(1);
@@ -553,12 +555,36 @@ int op_matmul_glu(const Ctx& c, int fmt, const char* name) {
     a.k = K;
     const uint32_t mt = cdiv(tmax, 256), nt = cdiv(N, 128);
     a.rows = mt * 256;
+    // One workgroup per CU (the kernel takes the whole LDS), so the tiles run in rounds of g_cus.  When the last
+    // round would leave at least half the CUs idle, its tiles run as K halves instead (two items each, the second to
+    // finish adds the other's sums): 896 tiles of the 8B gate/up at 2048 tokens take 3.5 rounds' time, not 4.
+    // Needs every XCD to get the same numbers of whole and split tiles and K halves of whole 64-input steps; not
+    // under qp_dispatch_noalloc (the partials need workspace); QP_GLU_SPLIT=0 turns it off.
+    const uint32_t tiles = mt * nt, C = g_cus > 0 ? (uint32_t)g_cus : 1u, rem = tiles % C;
+    const char* sp = getenv("QP_GLU_SPLIT");
+    const bool split = !g_noalloc && !(sp && !strcmp(sp, "0")) && tiles > C && rem > 0 && 2 * rem <= C &&
+                       rem % 8 == 0 && (tiles - rem) % 8 == 0 && K % 128 == 0 && rem <= kGluCntWords;
+    const uint64_t planes = 4ull * a.rows * K, part = split ? (uint64_t)rem * 2 * 512 * 128 * 4 : 0;
     uint64_t ws = 0;
-    if (int e = workspace(4ull * a.rows * K, &ws)) return e;
+    if (int e = workspace(planes + part, &ws)) return e;
     a.xs = ws;
     if (int e = split_input(a.x, a.xs, a.paso, K, a.rows, tmax, false)) return e;
     static const Kid kg_of[5] = {K_gemm_glu_q4k, K_gemm_glu_q5k, K_gemm_glu_q6k, K_gemm_glu_q3k, K_gemm_glu_q2k};
-    return launch(kg_of[kq_index(fmt)], nt, mt, 1, 512, 2 * (256 + 256 + 256 + 256) * 40 * 2, a);
+    const uint32_t lds = 2 * (256 + 256 + 256 + 256) * 40 * 2;
+    if (!split) return launch(kg_of[kq_index(fmt)], nt, mt, 1, 512, lds, a);
+    if (!g_glu_cnt) {
+        // the arrival words: zero once, and every split tile's second arrival sets its word back to zero
+        void* p = nullptr;
+        HIPCHK(hipMalloc(&p, 4ull * kGluCntWords), "hipMalloc (split-tile counters)");
+        HIPCHK(hipMemsetAsync(p, 0, 4ull * kGluCntWords, g_stream), "hipMemsetAsync");
+        g_glu_cnt = (uint64_t)p;
+    }
+    a.tail = rem;
+    a.mtiles = mt;
+    a.ntiles = nt;
+    a.part = ws + planes;
+    a.cnt = g_glu_cnt;
+    return launch(kg_of[kq_index(fmt)], tiles + rem, 1, 1, 512, lds, a);
 }
 
 // matmul_<fmt>_e (kquants.js:256-304, kds.js:110-186): P{N,K,acc,tfijo,E}; [paso, w, x, y, sel]

@@ -347,6 +347,7 @@ def test_matmul_swiglu_fused_equals_the_three_ops(quipu, dev, monkeypatch, fmt):
     """At 2048 tokens x 4352 rows (136 tiles of 256 x 256: no K split) the fused op gives exactly what
     matmul_<fmt>_t on gate and on up followed by swiglu give: the same sums in the same order."""
     monkeypatch.setenv("QP_GEMM_TILES", "wide")
+    monkeypatch.setenv("QP_GLU_SPLIT", "0")  # 272 tiles: on 256 CUs the last 16 would run as K halves
     T, N, K = 2048, 4352, 1024
     rg, ru = raw_matrix(fmt, N, K, 73), raw_matrix(fmt, N, K, 74)
     wg, wu = dev.matrix(fmt, rg, N, K), dev.matrix(fmt, ru, N, K)
@@ -361,6 +362,39 @@ def test_matmul_swiglu_fused_equals_the_three_ops(quipu, dev, monkeypatch, fmt):
     quipu.dispatch(name, [("u", N), ("u", K), ("u", 0), ("u", 0)], [paso, wu, x, u], grid)
     quipu.dispatch("swiglu", [("u", N)], [paso, g, u], (-(-T * N // 256), 1, 1))
     assert np.array_equal(dev.get(y, (T, N)), dev.get(g, (T, N)))
+
+
+def test_matmul_swiglu_split_tail(quipu, dev, oracle, monkeypatch):
+    """matmul_q4k_t_swiglu at 256 tokens x 33792 rows (264 tiles): on 256 CUs the last 8 tiles run as K halves,
+    the second half to finish adding the first's sums.  Within the float64 bound; the same bits on a second call
+    (the arrival words are back at zero, and the sum of the two halves does not depend on their order); close to
+    the unsplit launch (QP_GLU_SPLIT=0), whose sums are accumulated in another order."""
+    fmt, T, N, K = capi.Q4_K, 256, 33792, 256
+    rg, ru = raw_matrix(fmt, N, K, 75), raw_matrix(fmt, N, K, 76)
+    Wg = oracle.dequant(fmt, rg, N * K).reshape(N, K).astype(np.float64)
+    Wu = oracle.dequant(fmt, ru, N * K).reshape(N, K).astype(np.float64)
+    x = (np.random.default_rng(18).standard_normal((T, K)) * 0.5).astype(np.float32)
+    wg, wu, xb, paso = dev.matrix(fmt, rg, N, K), dev.matrix(fmt, ru, N, K), dev.buf(x), dev.paso(T, 0)
+
+    def run():
+        y = dev.buf(np.full((T, N), np.nan, np.float32))
+        quipu.dispatch("matmul_q4k_t_swiglu", [("u", N), ("u", K)], [paso, wg, wu, xb, y],
+                       ((N + 63) // 64, 1, (T + 31) // 32))
+        return dev.get(y, (T, N))
+
+    a, b = run(), run()
+    assert np.array_equal(a, b)
+    monkeypatch.setenv("QP_GLU_SPLIT", "0")
+    c = run()
+    x64 = x.astype(np.float64)
+    g, u = x64 @ Wg.T, x64 @ Wu.T
+    dg, du = 2e-5 * (np.abs(x64) @ np.abs(Wg).T), 2e-5 * (np.abs(x64) @ np.abs(Wu).T)
+    sg = g / (1.0 + np.exp(np.minimum(-g, 700.0)))
+    want = sg * u
+    bound = 1.1 * dg * (np.abs(u) + du) + np.abs(sg) * du + 1e-6 * np.abs(want) + 1e-30
+    for got in (a, c):
+        got = got.astype(np.float64)
+        assert np.all(np.isfinite(got)) and np.all(np.abs(got - want) <= bound)
 
 
 def test_matmul_reuses_the_split_input(quipu, dev):
