@@ -107,7 +107,13 @@ def test_embed_rows_bit_exact(quipu, dev, oracle, fmt):
 @pytest.mark.parametrize("fmt,N,K", [(capi.Q4_K, 1000, 4096), (capi.Q6_K, 513, 2048), (capi.Q8_0, 700, 1536),
                                      (capi.IQ4_NL, 700, 1536), (capi.F32, 130, 1024), (capi.Q4_K, 64, 14336),
                                      (capi.Q6_K, 40, 14336),
-                                     (capi.Q6_K, 700, 9216), (capi.Q4_K, 4100, 15360)])
+                                     (capi.Q6_K, 700, 9216), (capi.Q4_K, 4100, 15360),
+                                     # the planar formats' edges: an odd number of 32-weight blocks per row (a
+                                     # partial slot of 64), the input staged in a second round (K > 8192), and
+                                     # several passes per workgroup whose item count is not a multiple of two
+                                     (capi.Q8_0, 37, 288), (capi.F32, 33, 80), (capi.IQ4_NL, 130, 2080),
+                                     (capi.IQ4_NL, 300, 9248), (capi.Q8_0, 100, 12320), (capi.IQ4_NL, 40000, 256),
+                                     (capi.Q8_0, 40000, 96)])
 def test_matmul_1_reference_op(quipu, dev, oracle, fmt, N, K):
     raw = raw_matrix(fmt, N, K, 13)
     w = dev.matrix(fmt, raw, N, K)
