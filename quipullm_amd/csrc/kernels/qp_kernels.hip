@@ -4193,25 +4193,40 @@ DEC_BLOCK_KERNEL(mix, QP_KQ_MIX, 64, 1)
 DEC_BLOCK_KERNEL(mix, QP_KQ_MIX, 64, 4)
 
 // Causal attention of a prefill chunk on the matrix cores (f16 cache; no sliding window, no ring cap), the
-// reference atencion (gpu.js:467-539).  Wavefront w of workgroup (kvh, y) takes RG groups of 16 rows: TPW = 16 RG / G
-// tokens x the G heads of KV head kvh (row r of group g: token t0 + (16 g + r) / G, head r % G), and streams keys
-// 0 .. pos0 + its last token in tiles of 32 with the decode tile step, each row masked at its own causal limit.
-// RG = 2: every tile loaded feeds both row groups (half the key and value loads per row; one tile in flight
-// instead of two, for the registers of the second group's query and accumulators).
+// reference atencion (gpu.js:467-539).  A wavefront takes RG groups of 16 rows: TPW = 16 RG / G tokens x the G heads
+// of KV head kvh (row r of group g: token t0 + (16 g + r) / G, head r % G), and streams keys in tiles of 32 with the
+// decode tile step, each row masked at its own causal limit pos0 + its token.
+// RG = 1: wavefront w of workgroup (kvh, y) takes token block 4y + w and all its keys, two tiles in flight.
+// RG = 2: every tile loaded feeds both row groups (half the key and value loads per row; one tile in flight, for
+// the registers of the second group's query and accumulators).  Workgroup (kvh, y) takes one token block (the
+// longest first: y counts from the last block), its key tiles dealt to the four wavefronts in four ranges, and the
+// wavefronts' partial softmax states merged in LDS (weights e^(m_w - M), in wavefront order).  A token block's
+// serial chain of tiles is then a quarter of its keys: the longest rows of a prompt chunk no longer set the launch's
+// time alone (2048 tokens: 64 tiles in one wavefront before).
 template <int HD, int G, int RG>
 QP_DEV void attn_mfma_body(const QpAttnArgs& a) {
     constexpr uint32_t TPW = 16 * RG / G;
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t T = paso_T(a.paso), pos0 = paso_pos(a.paso);
-    const uint32_t kvh = blockIdx.x, t0 = (blockIdx.y * 4 + wave) * TPW;
-    if (t0 >= T) return;  // the whole wavefront (no barriers below)
+    const uint32_t kvh = blockIdx.x;
+    const uint32_t blk = RG == 2 ? gridDim.y - 1 - blockIdx.y : blockIdx.y * 4 + wave;
+    const uint32_t t0 = blk * TPW;
+    if (t0 >= T) return;  // RG = 1: the wavefront; RG = 2: the whole workgroup (t0 is the same in its wavefronts)
     const uint32_t kvd = a.nkv * HD, r = lane & 15, qg = lane >> 4;
     const uint32_t tlast = min(t0 + TPW, T) - 1;
-    const uint32_t kend = min(pos0 + tlast + 1, a.rows);  // keys this wavefront reads
+    const uint32_t kend = min(pos0 + tlast + 1, a.rows);  // keys the token block reads
+    // this wavefront's keys [kb, ke): RG = 2, a quarter of the block's tiles (whole tiles, so the ranges do not meet
+    // inside a tile); RG = 1, all of them
+    uint32_t kb = 0, ke = kend;
+    if constexpr (RG == 2) {
+        const uint32_t q = ((kend + 31) / 32 + 3) / 4 * 32;
+        kb = min(kend, wave * q);
+        ke = min(kend, kb + q);
+    }
     const __amdgpu_buffer_rsrc_t rk = kq_rsrc(a.kc, (uint64_t)a.rows * kvd * 2);
     const __amdgpu_buffer_rsrc_t rv = kq_rsrc(a.vc, (uint64_t)((a.rows + 31) / 32) * 32 * kvd * 2);
     MTile<HD> A, B;
-    mt_load<HD>(A, rk, rv, kvd, kvh, 0, kend, lane);
+    mt_load<HD>(A, rk, rv, kvd, kvh, kb, ke, lane);
     if constexpr (RG == 1) mt_load<HD>(B, rk, rv, kvd, kvh, 32, kend, lane);
     h8v qh[RG][HD / 32], ql[RG][HD / 32];
     float qsc[RG], m[RG], l[RG];
@@ -4252,13 +4267,57 @@ QP_DEV void attn_mfma_body(const QpAttnArgs& a) {
             mt_load<HD>(B, rk, rv, kvd, kvh, t + 96, kend, lane);
         }
     } else {
-        for (uint32_t t = 0; t < kend; t += 32) {
+        for (uint32_t t = kb; t < ke; t += 32) {
 #pragma unroll
             for (int g = 0; g < RG; g++)
                 if (t < kend_grp[g])  // a group whose rows all stop before this tile skips it
                     mt_consume<HD>(A, t, kend_row[g], 0xffffffffu, qh[g], ql[g], qsc[g], m[g], l[g], acc[g], lane);
-            mt_load<HD>(A, rk, rv, kvd, kvh, t + 32, kend, lane);
+            mt_load<HD>(A, rk, rv, kvd, kvh, t + 32, ke, lane);
         }
+        // the merge: each wavefront's row maxima, row sums (the lane groups' shares added) and O^T values to LDS;
+        // wavefront w then finishes dimensions 16 mm + 4 qg + i of both groups for mm = 2 w, 2 w + 1
+        __shared__ float pm[4][RG][64], pl[4][RG][64];
+        __shared__ f4v pa[4][RG][HD / 16][64];
+#pragma unroll
+        for (int g = 0; g < RG; g++) {
+            float lt = l[g] + bfly_f<4>(l[g], lane);
+            lt += bfly_f<5>(lt, lane);
+            pm[wave][g][lane] = m[g];
+            pl[wave][g][lane] = lt;
+#pragma unroll
+            for (int mm = 0; mm < HD / 16; mm++) pa[wave][g][mm][lane] = acc[g][mm];
+        }
+        __syncthreads();
+        constexpr int MW = HD / 64;  // dimensions blocks of 16 per wavefront
+#pragma unroll
+        for (int g = 0; g < RG; g++) {
+            float M = -3.0e38f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) M = fmaxf(M, pm[w][g][lane]);
+            float f[4], L = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                f[w] = __builtin_amdgcn_exp2f((pm[w][g][lane] - M) * QP_LOG2E);
+                L = fmaf(f[w], pl[w][g][lane], L);
+            }
+            if (row_ok[g]) {
+                const uint64_t orow = a.o + 4ull * (((uint64_t)tr[g] * a.nh + hr[g]) * HD);
+#pragma unroll
+                for (int j = 0; j < MW; j++) {
+                    const int mm = (int)wave * MW + j;
+                    f4v o = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int w = 0; w < 4; w++) o = o + pa[w][g][mm][lane] * f[w];
+                    float4 v;
+                    v.x = L > 0.0f ? o[0] / L : 0.0f;
+                    v.y = L > 0.0f ? o[1] / L : 0.0f;
+                    v.z = L > 0.0f ? o[2] / L : 0.0f;
+                    v.w = L > 0.0f ? o[3] / L : 0.0f;
+                    gstore<float4>(orow + 4 * (16 * mm + 4 * qg), v);
+                }
+            }
+        }
+        return;
     }
 #pragma unroll
     for (int g = 0; g < RG; g++) {

@@ -737,10 +737,12 @@ int op_atencion(const Ctx& c) {
                                        K_attn_mfma2_h128_g8}};
         const uint32_t gi = G == 1 ? 0 : G == 2 ? 1 : G == 4 ? 2 : 3;
         // two 16-row groups per wavefront sharing each key tile (measured: 8B prefill of 4096 tokens 201 -> 192 ms,
-        // MoE 176 -> 160 ms); QP_ATTN_RG1 keeps one group and two tiles in flight, for comparisons
+        // MoE 176 -> 160 ms), one token block per workgroup with its keys split over the four wavefronts;
+        // QP_ATTN_RG1 keeps one group, two tiles in flight and four token blocks per workgroup, for comparisons
         const bool two = !getenv_flag("QP_ATTN_RG1");
-        const uint32_t rg = two ? 2 : 1;
-        return launch((two ? km2 : km)[a.hd == 128][gi], a.nkv, cdiv(c.gy ? c.gy : 1, 4 * (16 * rg / G)), 1, 256, 0, a);
+        const uint32_t tpw = 16 * (two ? 2 : 1) / G;  // tokens per wavefront
+        return launch((two ? km2 : km)[a.hd == 128][gi], a.nkv, cdiv(c.gy ? c.gy : 1, (two ? 1 : 4) * tpw), 1, 256, 0,
+                      a);
     }
     const uint32_t qb = 32 / G;
     a.qb = qb;
