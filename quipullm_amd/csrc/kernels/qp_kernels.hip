@@ -2691,6 +2691,50 @@ QP_DEV void gemm_mfma256w_body(const QpGemmArgs& g) {
                         ex[((((wm * 2 + (wn - 2)) * 4 + a) * 2 + b) * 16 + v) * 64 + lane] = acc[a][b][v];
         }
         __syncthreads();
+        if (g.yplanes) {
+            // y as the next matmul's input planes (xs_off's layout, g.rows token rows, K = N): the gate wavefronts'
+            // outputs go to an LDS tile [256 tokens][128 outputs] (rows padded to 132 floats) once the up sums are
+            // read, then every thread splits eight consecutive outputs of one token with qp_split_bf16's formula
+            // (the same planes that kernel makes of the f32 outputs) and stores their 16-byte high and low parts;
+            // token rows past T are not written
+            if (wn < 2) {
+#pragma unroll
+                for (int a = 0; a < 4; a++)
+#pragma unroll
+                    for (int b = 0; b < 2; b++)
+#pragma unroll
+                        for (int v = 0; v < 16; v++) {
+                            const float gv = acc[a][b][v];
+                            const float uv = ex[((((wm * 2 + wn) * 4 + a) * 2 + b) * 16 + v) * 64 + lane];
+                            acc[a][b][v] = (gv / (1.0f + expf(-gv))) * uv;
+                        }
+            }
+            __syncthreads();
+            float* tile = reinterpret_cast<float*>(smem4);
+            if (wn < 2) {
+#pragma unroll
+                for (int a = 0; a < 4; a++)
+#pragma unroll
+                    for (int b = 0; b < 2; b++)
+#pragma unroll
+                        for (int v = 0; v < 16; v++) {
+                            const uint32_t t = wm * 128 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                            tile[t * 132 + wn * 64 + b * 32 + (lane & 31)] = acc[a][b][v];
+                        }
+            }
+            __syncthreads();
+            const uint64_t plane = 2ull * g.rows * N;  // bytes of the high plane (N % 32 == 0)
+            for (uint32_t i = tid; i < 256 * 16; i += 512) {
+                const uint32_t t = i & 255, c8 = i >> 8, n = n0 + 8 * c8;
+                if (t0 + t >= T || n >= N) continue;
+                const float4 v0 = *reinterpret_cast<const float4*>(tile + t * 132 + 8 * c8);
+                const float4 v1 = *reinterpret_cast<const float4*>(tile + t * 132 + 8 * c8 + 4);
+                const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                const uint64_t o = xs_off(t0 + t, n, g.rows);
+                split_store8(v, reinterpret_cast<__bf16*>(g.y + o), reinterpret_cast<__bf16*>(g.y + plane + o));
+            }
+            return;
+        }
         if (wn >= 2) return;
         float* Y = mptr<float>(g.y);
 #pragma unroll

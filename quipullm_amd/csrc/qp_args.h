@@ -125,7 +125,10 @@ typedef struct {
     // (item % 8), whole tiles first, then its share of the last `tail` tiles as K halves.  Each half stores its
     // sums to part (two 256 KB slots per split tile) and counts its arrival in cnt[tile]; the second adds the
     // other's sums and finishes the tile (and resets the word).
-    uint32_t tail, mtiles, ntiles, pad_t;
+    uint32_t tail, mtiles, ntiles;
+    // matmul_<fmt>_t_swiglu: 1 = y receives the outputs as the next matmul's input planes (the bf16 high and low
+    // planes of qp_split_bf16's layout for rows token rows and K = n), not as f32 rows
+    uint32_t yplanes;
     uint64_t part, cnt;
 } QpGemmArgs;
 

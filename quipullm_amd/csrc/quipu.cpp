@@ -453,6 +453,11 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
     a.k = K;
     a.acc = acc;
     const uint32_t tmax = c.gz * tokens_per_z;
+    // P[4] = 2 (x holds input planes) is read by the 256-token tiles only (below: K-quants, 256 tokens or more)
+    const bool xplanes = c.U(4) == 2;
+    if (xplanes && (!is_kq(fmt) || tmax < 256 || (g_capturing && !g_noalloc) || getenv_flag("QP_NO_MFMA")))
+        return fail(QP_E_ARG, "%s: P[4] = 2 (x holds input planes) needs K-quant weights and a chunk of 256 tokens "
+                              "or more on the matrix cores", name);
     if (tmax >= 64 && !getenv_flag("QP_NO_MFMA")) {
         // matrix cores: 128 x 128 tiles (the kernel reads T from paso; tiles past it exit)
         const Kid k = fmt == QP_Q4_K ? K_gemm_mfma_q4k : fmt == QP_Q6_K ? K_gemm_mfma_q6k
@@ -494,11 +499,23 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
                 ns2 /= 2;
             }
             uint64_t ws = 0;
-            if (int e = workspace(xs_bytes + ws_bytes, &ws)) return e;
-            a.xs = ws;
-            a.ws = ns > 1 ? ws + xs_bytes : 0;
-            // P[4] = 1: reuse the previous matmul's input planes (see split_input)
-            if (int e = split_input(a.x, a.xs, a.paso, K, a.rows, tmax, c.U(4) == 1)) return e;
+            const uint32_t xmode = c.U(4);
+            if (xmode == 2) {
+                // P[4] = 2: x holds the input planes already (matmul_<fmt>_t_swiglu with planes = 1 wrote them for
+                // the same T), sized for 256-token tiles (big holds: checked above)
+                if (K % 32) return fail(QP_E_ARG, "%s: input planes need K %% 32 == 0", name);
+                if (int e = need_room(a.x, xs_bytes, name, "the input planes' buffer")) return e;
+                if (ws_bytes)
+                    if (int e = workspace(ws_bytes, &ws)) return e;
+                a.xs = a.x;
+                a.ws = ns > 1 ? ws : 0;
+            } else {
+                if (int e = workspace(xs_bytes + ws_bytes, &ws)) return e;
+                a.xs = ws;
+                a.ws = ns > 1 ? ws + xs_bytes : 0;
+                // P[4] = 1: reuse the previous matmul's input planes (see split_input)
+                if (int e = split_input(a.x, a.xs, a.paso, K, a.rows, tmax, xmode == 1)) return e;
+            }
             if (wide) {
                 static const Kid kw_of[5] = {K_gemm_mfma256w_q4k, K_gemm_mfma256w_q5k, K_gemm_mfma256w_q6k,
                                              K_gemm_mfma256w_q3k, K_gemm_mfma256w_q2k};
@@ -523,11 +540,14 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
     return launch(K_gemm_mt, cdiv(N, 64), cdiv(tmax ? tmax : 1, 64), 1, 256, 0, a);
 }
 
-// matmul_<fmt>_t_swiglu: P{N, K}; [paso, w_gate, w_up, x, y]; y[t][n] = silu(x[t] . gate[n]) * (x[t] . up[n]) for
-// the T tokens of paso (K-quants).  No counterpart in the reference, whose prompt pass runs matmul_<fmt>_t on the
-// gate and up tensors and then swiglu (transformer.js:311-313): the same three results in one matrix-core launch
-// (256-token tiles of 128 gate and 128 up rows), for prompt chunks of at least 256 tokens.  Same accumulation as
-// matmul_<fmt>_t with 256 x 256 tiles.  Not while capturing a graph (the input planes may need a larger workspace).
+// matmul_<fmt>_t_swiglu: P{N, K, planes}; [paso, w_gate, w_up, x, y]; y[t][n] = silu(x[t] . gate[n]) *
+// (x[t] . up[n]) for the T tokens of paso (K-quants).  No counterpart in the reference, whose prompt pass runs
+// matmul_<fmt>_t on the gate and up tensors and then swiglu (transformer.js:311-313): the same three results in one
+// matrix-core launch (256-token tiles of 128 gate and 128 up rows), for prompt chunks of at least 256 tokens.  Same
+// accumulation as matmul_<fmt>_t with 256 x 256 tiles.  Not while capturing a graph (the input planes may need a
+// larger workspace).  planes = 1 (the third word; absent: 0): y receives the outputs as the input planes of the
+// matmul that reads them next (matmul_<fmt>_t with P[4] = 2), the values qp_split_bf16 would make of the f32 rows,
+// for R = 256 * ceil(T / 256) token rows and K = N: 4 R N bytes.
 uint64_t tensor_bytes(int fmt, uint64_t rows, uint32_t K);
 int need_room(uint64_t p, uint64_t bytes, const char* op, const char* what);
 constexpr uint32_t kGluCntWords = 1024;  // split tiles of one launch at most (one arrival word each)
@@ -555,6 +575,12 @@ int op_matmul_glu(const Ctx& c, int fmt, const char* name) {
     a.k = K;
     const uint32_t mt = cdiv(tmax, 256), nt = cdiv(N, 128);
     a.rows = mt * 256;
+    a.yplanes = c.U(2);
+    if (a.yplanes > 1) return fail(QP_E_ARG, "%s: P[2] = %u (0: f32 rows, 1: input planes)", name, a.yplanes);
+    if (a.yplanes) {
+        if (N % 32) return fail(QP_E_ARG, "%s: the input planes need N %% 32 == 0 (N = %u)", name, N);
+        if (int e = need_room(a.y, 4ull * a.rows * N, name, "the output planes' buffer")) return e;
+    }
     // One workgroup per CU (the kernel takes the whole LDS), so the tiles run in rounds of g_cus.  When the last
     // round would leave at least half the CUs idle, its tiles run as K halves instead (two items each, the second to
     // finish adds the other's sums): 896 tiles of the 8B gate/up at 2048 tokens take 3.5 rounds' time, not 4.

@@ -95,6 +95,10 @@ class ModeloTransformer {
     // (matmul_<fmt>_t_swiglu, the same results as the reference's matmul_<fmt>_t, matmul_<fmt>_t, swiglu of
     // transformer.js:311-313); false: those three ops
     this.ffnFusionada = op.fused_ffn !== false;
+    // with K-quant down weights that launch writes the down matmul's input planes itself (matmul_<fmt>_t_swiglu
+    // P[2] = 1, matmul_<fmt>_t P[4] = 2: the same planes qp_split_bf16 makes of its f32 outputs, without the f32 round
+    // trip and the split launch); false: f32 outputs, split by the down matmul
+    this.planosFfn = op.ffn_planes !== false;
     // one-token step: the split-K attention's partials merged by the last workgroup of each grid column in the same
     // launch (dec_attn P[12] = 1) instead of a dec_attn_comb launch.  A column takes at most 4 query heads: groups of
     // 8 or more query heads are split over gsplit columns per KV head (P[13]; each column streams its KV head's keys
@@ -219,7 +223,8 @@ class ModeloTransformer {
     this.k = B(4 * TB * kvd, 'k');
     this.v = B(4 * TB * kvd, 'v');
     this.att = B(4 * TB * qd, 'att');
-    this.g = B(4 * TB * FF, 'g');
+    // (dense FFN: room for the down matmul's input planes, 256-token rows, that the fused gate/up writes here)
+    this.g = B(4 * (this.nExp ? TB : Math.ceil(TB / 256) * 256) * FF, 'g');
     this.u = B(4 * TB * FF, 'u');
     if (this.nExp) {
       this.rl = B(4 * TB * this.nExp, 'router_logits');
@@ -281,13 +286,15 @@ class ModeloTransformer {
   // matmul of the reference facade: one token -> matmul_<t>_1; T >= 8 with a K-quant and tiling -> _t; else _4
   // (transformer.js:268-284).
   // reusa: x is the input of the matmul dispatched just before (Q, K, V): the tiled form may reuse the bf16 planes
-  // that matmul split it into (P[4] = 1, an addition of this backend's; the reference's P has four words)
-  _mm(W, x, y, acc, reusa) {
+  // that matmul split it into (P[4] = 1, an addition of this backend's; the reference's P has four words).
+  // planos: x holds those planes already, written by the fused gate/up (P[4] = 2; the tiled form only).
+  _mm(W, x, y, acc, reusa, planos) {
     const gpu = this.gpu;
     const u = gpu.uniforme([['u', W.N], ['u', W.K], ['u', acc ? 1 : 0], ['u', 0]]);
     const wb = plano(W) ? [W.qs, W.ds] : [W.w];
     const b = [u, this.bPaso].concat(wb, [x, y]);
-    const bt = reusa && this.fusion ? [gpu.uniforme([['u', W.N], ['u', W.K], ['u', acc ? 1 : 0], ['u', 0], ['u', 1]]),
+    const modo = planos ? 2 : reusa && this.fusion ? 1 : 0;
+    const bt = modo ? [gpu.uniforme([['u', W.N], ['u', W.K], ['u', acc ? 1 : 0], ['u', 0], ['u', modo]]),
       this.bPaso].concat(wb, [x, y]) : b;
     return {
       uno: gpu.grupo('matmul_' + W.tipo + '_1', b), lote: gpu.grupo('matmul_' + W.tipo + '_4', b),
@@ -324,10 +331,10 @@ class ModeloTransformer {
     const resid = this.escRes || 1;
     // a block's output into the residual (transformer.js:218-233): added by the matmul itself (acc = 1), or, with
     // a post norm or a residual scale, written to tmp, normalized, then x += resid * it (suma_esc)
-    const directo = (W, x, post) => {
-      if (!post && resid === 1) return { mm: this._mm(W, x, this.x, 1) };
+    const directo = (W, x, post, planos) => {
+      if (!post && resid === 1) return { mm: this._mm(W, x, this.x, 1, false, planos) };
       return {
-        mm: this._mm(W, x, this.tmp, 0),
+        mm: this._mm(W, x, this.tmp, 0, false, planos),
         norma: post ? gpu.grupo('rmsnorm', [uNorm, P, this.tmp, post, this.xn]) : null,
         suma: gpu.grupo('suma_esc', [gpu.uniforme([['u', D], ['f', resid]]), P, this.x, post ? this.xn : this.tmp]),
       };
@@ -366,9 +373,13 @@ class ModeloTransformer {
         gc.gate = this._mm(c.gate, this.xn, this.g, 0);
         gc.up = this._mm(c.up, this.xn, this.u, 0);
         if (this.ffnFusionada && this.fusion && this.baldosa && KQ.has(c.gate.tipo) && c.up.tipo === c.gate.tipo &&
-            c.up.N === c.gate.N && c.up.K === c.gate.K)
-          gc.glu = gpu.grupo('matmul_' + c.gate.tipo + '_t_swiglu', [gpu.uniforme([['u', c.gate.N], ['u', c.gate.K]]),
-            P, c.gate.w, c.up.w, this.xn, this.g]);
+            c.up.N === c.gate.N && c.up.K === c.gate.K) {
+          // with K-quant down weights the fused gate/up writes the down matmul's input planes (no split between them)
+          const pl = KQ.has(c.down.tipo) && c.down.K === c.gate.N && this.planosFfn;
+          gc.glu = gpu.grupo('matmul_' + c.gate.tipo + '_t_swiglu', [gpu.uniforme([['u', c.gate.N], ['u', c.gate.K],
+            ['u', pl ? 1 : 0]]), P, c.gate.w, c.up.w, this.xn, this.g]);
+          if (pl) gc.downPl = directo(c.down, this.g, c.postFfn, true);
+        }
         gc.swiglu = gpu.grupo(this.gemma ? 'geglu' : 'swiglu', [gpu.uniforme([['u', c.gate.N]]), P, this.g, this.u]);
         gc.F = c.gate.N;
         gc.down = directo(c.down, this.g, c.postFfn);
@@ -447,12 +458,14 @@ class ModeloTransformer {
         e(gc.ed);
         despachar(null, gc.comb, filas(this.D));
       } else {
-        if (gc.glu && T >= 256) despachar(null, gc.glu, Math.ceil(gc.F / 64), 1, Math.ceil(T / 32));
-        else {
+        if (gc.glu && T >= 256) {
+          despachar(null, gc.glu, Math.ceil(gc.F / 64), 1, Math.ceil(T / 32));
+          salida(gc.downPl || gc.down);
+        } else {
           mm(gc.gate); mm(gc.up);
           despachar(null, gc.swiglu, filas(gc.F));
+          salida(gc.down);
         }
-        salida(gc.down);
       }
     }
     return mm;

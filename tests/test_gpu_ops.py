@@ -403,6 +403,54 @@ def test_matmul_swiglu_split_tail(quipu, dev, oracle, monkeypatch):
         assert np.all(np.isfinite(got)) and np.all(np.abs(got - want) <= bound)
 
 
+@pytest.mark.parametrize("fg,fd,T,F,D", [(capi.Q4_K, capi.Q6_K, 300, 512, 256), (capi.Q5_K, capi.Q4_K, 2048, 1536, 512),
+                                          (capi.Q4_K, capi.Q6_K, 2304, 15360, 256)])
+@pytest.mark.parametrize("acc", [0, 1])
+def test_matmul_swiglu_planes_feed_down(quipu, dev, fg, fd, T, F, D, acc):
+    """matmul_<fmt>_t_swiglu with P[2] = 1 writes the down matmul's input planes itself, and matmul_<fmt>_t with
+    P[4] = 2 reads them: the down matmul's output equals, bit for bit, the f32 path (the fused op's f32 outputs
+    split by the down matmul).  T = 300: token rows 300 .. 511 of the planes are not written; 2304 tokens x 15360
+    rows (1080 tiles): on 256 CUs the fused op's last 56 tiles run as K halves."""
+    rg, ru, rd = raw_matrix(fg, F, D, 91), raw_matrix(fg, F, D, 92), raw_matrix(fd, D, F, 93)
+    wg, wu, wd = dev.matrix(fg, rg, F, D), dev.matrix(fg, ru, F, D), dev.matrix(fd, rd, D, F)
+    x = dev.buf((np.random.default_rng(19).standard_normal((T, D)) * 0.5).astype(np.float32))
+    y0 = (np.random.default_rng(20).standard_normal((T, D))).astype(np.float32)
+    paso = dev.paso(T, 0)
+    rows = -(-T // 256) * 256
+    glu = "matmul_%s_t_swiglu" % capi.FMT_NAME[fg]
+    down = "matmul_%s_t" % capi.FMT_NAME[fd]
+    gz = (T + 31) // 32
+    h = dev.buf(np.full((T, F), np.nan, np.float32))
+    quipu.dispatch(glu, [("u", F), ("u", D)], [paso, wg, wu, x, h], ((F + 63) // 64, 1, gz))
+    ya = dev.buf(y0)
+    quipu.dispatch(down, [("u", D), ("u", F), ("u", acc), ("u", 0)], [paso, wd, h, ya], ((D + 63) // 64, 1, gz))
+    pl = dev.zeros(4 * rows * F)
+    quipu.dispatch(glu, [("u", F), ("u", D), ("u", 1)], [paso, wg, wu, x, pl], ((F + 63) // 64, 1, gz))
+    yb = dev.buf(y0)
+    quipu.dispatch(down, [("u", D), ("u", F), ("u", acc), ("u", 0), ("u", 2)], [paso, wd, pl, yb],
+                   ((D + 63) // 64, 1, gz))
+    a, b = dev.get(ya, (T, D)), dev.get(yb, (T, D))
+    assert np.all(np.isfinite(a)) and a.view(np.uint32).tolist() == b.view(np.uint32).tolist()
+
+
+def test_matmul_planes_rejections(quipu, dev):
+    """P[4] = 2 needs the 256-token tiles (under 256 tokens the matmul refuses it), and the planes' buffers must hold
+    4 * rows * K bytes (256-token rows)."""
+    T, F, D = 300, 256, 256
+    raw = raw_matrix(capi.Q4_K, F, D, 94)
+    w = dev.matrix(capi.Q4_K, raw, F, D)
+    x = dev.buf(np.zeros((T, D), np.float32))
+    with pytest.raises(capi.QuipuError, match="output planes"):
+        quipu.dispatch("matmul_q4k_t_swiglu", [("u", F), ("u", D), ("u", 1)],
+                       [dev.paso(T, 0), w, w, x, dev.zeros(4 * T * F)], (4, 1, 10))
+    with pytest.raises(capi.QuipuError, match="input planes"):
+        quipu.dispatch("matmul_q4k_t", [("u", D), ("u", F), ("u", 0), ("u", 0), ("u", 2)],
+                       [dev.paso(T, 0), w, dev.zeros(4 * T * F), dev.zeros(4 * T * D)], (4, 1, 10))
+    with pytest.raises(capi.QuipuError, match="256 tokens or more"):
+        quipu.dispatch("matmul_q4k_t", [("u", D), ("u", F), ("u", 0), ("u", 0), ("u", 2)],
+                       [dev.paso(100, 0), w, dev.zeros(4 * 256 * F), dev.zeros(4 * 100 * D)], (4, 1, 4))
+
+
 def test_matmul_reuses_the_split_input(quipu, dev):
     """P[4] = 1 (Q, then K and V of the same input): the bf16 planes the previous matrix-core matmul split are used
     again; results equal those of a fresh split.  With another input (x2), or after the workspace grew (a larger
