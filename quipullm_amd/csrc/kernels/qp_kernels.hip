@@ -2820,6 +2820,58 @@ KERNEL __launch_bounds__(256) void qp_rmsnorm(QpRmsArgs a) {
     for (uint32_t i = li; i < D; i += 256) y[i] = (x[i] * inv) * w[i];
 }
 
+// The rmsnorm of R = 8 token rows per workgroup written as the next matmul's input planes (xs_off's layout, a.rows
+// rows; rows past T are not written): qp_rmsnorm's sums in its order (256 threads stride each row, the LDS tree
+// 128 .. 1, the eight trees side by side) and its y = (x * inv) * w, split with qp_split_bf16's formula, so the
+// planes are those qp_split_bf16 makes of qp_rmsnorm's rows.  The second pass reads x again (from the caches),
+// eight consecutive inputs per thread, consecutive threads on consecutive rows.
+KERNEL __launch_bounds__(256) void qp_rmsnorm_planes(QpRmsPlanesArgs a) {
+    constexpr uint32_t R = 8;
+    __shared__ float red[R][256];
+    __shared__ float inv_s[R];
+    const uint32_t T = paso_T(a.paso), li = threadIdx.x, D = a.d, t0 = blockIdx.x * R;
+    if (t0 >= T) return;
+    const uint32_t nr = min(R, T - t0);
+    // the eight rows' loads of one stride step issued together (each row's sum still in qp_rmsnorm's order)
+    float s[R];
+#pragma unroll
+    for (uint32_t r = 0; r < R; r++) s[r] = 0.0f;
+    const float* xb = cptr<float>(a.x) + (uint64_t)t0 * D;
+    for (uint32_t i = li; i < D; i += 256) {
+        float v[R];
+#pragma unroll
+        for (uint32_t r = 0; r < R; r++) v[r] = r < nr ? xb[(uint64_t)r * D + i] : 0.0f;
+#pragma unroll
+        for (uint32_t r = 0; r < R; r++) s[r] = s[r] + v[r] * v[r];
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < R; r++) red[r][li] = s[r];
+    __syncthreads();
+    for (uint32_t k = 128; k > 0; k >>= 1) {
+        if (li < k)
+            for (uint32_t r = 0; r < R; r++) red[r][li] = red[r][li] + red[r][li + k];
+        __syncthreads();
+    }
+    if (li < R) inv_s[li] = 1.0f / sqrtf(red[li][0] / (float)D + a.eps);
+    __syncthreads();
+    const uint64_t plane = 2ull * a.rows * D;  // bytes of the high plane (D % 32 == 0)
+    const float* w = cptr<float>(a.w);
+    for (uint32_t i = li; i < R * (D / 8); i += 256) {
+        // no contraction: the product must be rounded to y before the split subtracts its high part (an FMA of
+        // (x * inv) * w - hi would give another low part than qp_split_bf16 gives of the rounded y)
+#pragma clang fp contract(off)
+        const uint32_t r = i % R, k8 = (i / R) * 8, t = t0 + r;
+        if (r >= nr) continue;
+        const float* x = cptr<float>(a.x) + (uint64_t)t * D + k8;
+        const float inv = inv_s[r];
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = (x[j] * inv) * w[k8 + j];
+        const uint64_t o = xs_off(t, k8, a.rows);
+        split_store8(v, reinterpret_cast<__bf16*>(a.xs + o), reinterpret_cast<__bf16*>(a.xs + plane + o));
+    }
+}
+
 // ====================================================================================== norm + RoPE
 // Reference norm_rope (gpu.js:394-444), one wavefront per head vector.
 QP_DEV void wave_norm_rope_f(float* v, const float* w, uint32_t hd, bool use_norm, float eps, float pos_esc,

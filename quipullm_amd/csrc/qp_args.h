@@ -146,6 +146,8 @@ typedef struct { uint64_t ws, y, paso; uint32_t n, rows, splits, acc; } QpReduce
 // ---------------------------------------------------------------- elementwise / small ops
 typedef struct { uint64_t w, ids, y, paso; uint32_t fmt, d, rows, tseq; } QpEmbedArgs;  // rows: tensor rows
 typedef struct { uint64_t x, w, y, paso; uint32_t d, ultima; float eps; uint32_t rows_fixed; } QpRmsArgs;
+// rmsnorm_planes: the rmsnorm of each token row written as the next matmul's bf16 input planes (xs, rows token rows)
+typedef struct { uint64_t x, w, xs, paso; uint32_t d, rows; float eps; uint32_t pad; } QpRmsPlanesArgs;
 typedef struct {
     uint64_t v, w, paso;
     uint32_t hd, nh, use_norm, neox;

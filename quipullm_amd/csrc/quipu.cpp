@@ -540,14 +540,15 @@ int op_matmul_mt(const Ctx& c, int fmt, const char* name, uint32_t tokens_per_z)
     return launch(K_gemm_mt, cdiv(N, 64), cdiv(tmax ? tmax : 1, 64), 1, 256, 0, a);
 }
 
-// matmul_<fmt>_t_swiglu: P{N, K, planes}; [paso, w_gate, w_up, x, y]; y[t][n] = silu(x[t] . gate[n]) *
+// matmul_<fmt>_t_swiglu: P{N, K, planes, xplanes}; [paso, w_gate, w_up, x, y]; y[t][n] = silu(x[t] . gate[n]) *
 // (x[t] . up[n]) for the T tokens of paso (K-quants).  No counterpart in the reference, whose prompt pass runs
 // matmul_<fmt>_t on the gate and up tensors and then swiglu (transformer.js:311-313): the same three results in one
 // matrix-core launch (256-token tiles of 128 gate and 128 up rows), for prompt chunks of at least 256 tokens.  Same
 // accumulation as matmul_<fmt>_t with 256 x 256 tiles.  Not while capturing a graph (the input planes may need a
 // larger workspace).  planes = 1 (the third word; absent: 0): y receives the outputs as the input planes of the
 // matmul that reads them next (matmul_<fmt>_t with P[4] = 2), the values qp_split_bf16 would make of the f32 rows,
-// for R = 256 * ceil(T / 256) token rows and K = N: 4 R N bytes.
+// for R = 256 * ceil(T / 256) token rows and K = N: 4 R N bytes.  P[3] = 1: x holds its input as such planes
+// (rmsnorm_planes), 4 R K bytes.
 uint64_t tensor_bytes(int fmt, uint64_t rows, uint32_t K);
 int need_room(uint64_t p, uint64_t bytes, const char* op, const char* what);
 constexpr uint32_t kGluCntWords = 1024;  // split tiles of one launch at most (one arrival word each)
@@ -590,11 +591,17 @@ int op_matmul_glu(const Ctx& c, int fmt, const char* name) {
     const char* sp = getenv("QP_GLU_SPLIT");
     const bool split = !g_noalloc && !(sp && !strcmp(sp, "0")) && tiles > C && rem > 0 && 2 * rem <= C &&
                        rem % 8 == 0 && (tiles - rem) % 8 == 0 && K % 128 == 0 && rem <= kGluCntWords;
-    const uint64_t planes = 4ull * a.rows * K, part = split ? (uint64_t)rem * 2 * 512 * 128 * 4 : 0;
+    // P[3] = 1: x holds the input planes already (rmsnorm_planes wrote them for the same T)
+    const bool xpl = c.U(3) == 1;
+    const uint64_t planes = xpl ? 0 : 4ull * a.rows * K, part = split ? (uint64_t)rem * 2 * 512 * 128 * 4 : 0;
+    if (xpl)
+        if (int e = need_room(a.x, 4ull * a.rows * K, name, "the input planes' buffer")) return e;
     uint64_t ws = 0;
-    if (int e = workspace(planes + part, &ws)) return e;
-    a.xs = ws;
-    if (int e = split_input(a.x, a.xs, a.paso, K, a.rows, tmax, false)) return e;
+    if (planes + part)
+        if (int e = workspace(planes + part, &ws)) return e;
+    a.xs = xpl ? a.x : ws;
+    if (!xpl)
+        if (int e = split_input(a.x, a.xs, a.paso, K, a.rows, tmax, false)) return e;
     static const Kid kg_of[5] = {K_gemm_glu_q4k, K_gemm_glu_q5k, K_gemm_glu_q6k, K_gemm_glu_q3k, K_gemm_glu_q2k};
     const uint32_t lds = 2 * (256 + 256 + 256 + 256) * 40 * 2;
     if (!split) return launch(kg_of[kq_index(fmt)], nt, mt, 1, 512, lds, a);
@@ -685,6 +692,26 @@ int op_rmsnorm(const Ctx& c) {
     a.w = c.B(2);
     a.y = c.B(3);
     return launch(K_rmsnorm, a.ultima ? 1 : c.gx, 1, 1, 256, 0, a);
+}
+
+// rmsnorm_planes: P{D, eps}; [paso, x, w, xs]; grid ceil(T / 8).  No counterpart in the reference: its rmsnorm
+// (gpu.js:332-356) of the T rows written as the bf16 input planes of the matmul that reads them next (matmul_<fmt>_t
+// with P[4] = 2, matmul_<fmt>_t_swiglu with P[3] = 1; K-quants, T >= 256), for R = 256 ceil(T / 256) token rows:
+// 4 R D bytes, D % 32 == 0.  The planes are those the matmul's own split makes of rmsnorm's rows.
+int op_rmsnorm_planes(const Ctx& c) {
+    if (int e = need_bufs(c, 4, "rmsnorm_planes")) return e;
+    QpRmsPlanesArgs a = {};
+    a.d = c.U(0);
+    a.eps = c.F(1);
+    a.paso = c.B(0);
+    a.x = c.B(1);
+    a.w = c.B(2);
+    a.xs = c.B(3);
+    if (!a.d || a.d % 32) return fail(QP_E_ARG, "rmsnorm_planes: D=%u (a multiple of 32)", a.d);
+    const uint32_t gx = c.gx ? c.gx : 1;
+    a.rows = cdiv(gx * 8, 256) * 256;
+    if (int e = need_room(a.xs, 4ull * a.rows * a.d, "rmsnorm_planes", "the planes' buffer")) return e;
+    return launch(K_rmsnorm_planes, gx, 1, 1, 256, 0, a);
 }
 
 // norm_rope (gpu.js:394-444): P{hd, nh, usaNorm, neox, eps, base, nrot, z=esc bits}; [paso, v, w]; (nh, T).
@@ -1432,6 +1459,7 @@ void register_ops() {
         v.push_back({nem, [fmt, nem](const Ctx& c) { return op_embed(c, fmt, nem.c_str()); }});
     }
     v.push_back({"rmsnorm", op_rmsnorm});
+    v.push_back({"rmsnorm_planes", op_rmsnorm_planes});
     v.push_back({"norm_rope", op_norm_rope});
     v.push_back({"kv_write", op_kv_write});
     v.push_back({"atencion", op_atencion});

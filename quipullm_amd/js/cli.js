@@ -2,13 +2,13 @@
 // Command-line driver of the engine, for tests and the benchmark.
 //
 //   node cli.js generate --model M.gguf --prompt-file ids.json --n 128 [--mode fast|ref|engine|sample] [--kv f16|f32]
-//                        [--ctx N] [--batch N] [--no-tiled] [--no-fused-ffn] [--no-ffn-planes] [--logits-out file.f32] [--kv-out file]
+//                        [--ctx N] [--batch N] [--no-tiled] [--no-fused-ffn] [--no-ffn-planes] [--no-norm-planes] [--logits-out file.f32] [--kv-out file]
 //                        [--force-ids ids.json]
 //                        [--repeat-penalty R] [--frequency-penalty F] [--presence-penalty P] [--host-loop]
 //                        [--temperature T] [--top-k K] [--top-p P] [--min-p M] [--seed S]
 //   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
 //                        [--warmup W] [--prefill P1,P2] [--eager] [--sample] [--keys-per-split N]
-//                        [--no-moe-grouped] [--no-fused-ffn] [--no-ffn-planes] [--no-merged-attention] [--attn-block] [--no-moe-router]
+//                        [--no-moe-grouped] [--no-fused-ffn] [--no-ffn-planes] [--no-norm-planes] [--no-merged-attention] [--attn-block] [--no-moe-router]
 //   node cli.js motor    --servidor http://127.0.0.1:PORT [--id ID] [--kv f16] [--batch N]   (the server's engine)
 //                        [--check-prompt-file ids.json --check-n N --check-logits file.f32]
 //
@@ -47,6 +47,7 @@ async function cargar(o) {
   // the reference's op sequence keeps gate, up and SwiGLU as three ops in the prompt pass too
   if (o['no-fused-ffn'] || o.mode === 'ref') options.fused_ffn = false;
   if (o['no-ffn-planes']) options.ffn_planes = false;
+  if (o['no-norm-planes']) options.norm_planes = false;
   if (o['no-merged-attention']) options.merged_attention = false;
   if (o['attn-block']) options.attn_block = true;
   if (o['no-moe-router']) options.moe_router = false;

@@ -99,6 +99,10 @@ class ModeloTransformer {
     // P[2] = 1, matmul_<fmt>_t P[4] = 2: the same planes qp_split_bf16 makes of its f32 outputs, without the f32 round
     // trip and the split launch); false: f32 outputs, split by the down matmul
     this.planosFfn = op.ffn_planes !== false;
+    // prompt chunks of 256 tokens or more: the attention (and dense FFN) norm writes the bf16 input planes of the
+    // K-quant matmuls that read it (rmsnorm_planes; Q, K, V with P[4] = 2, the fused gate/up with P[3] = 1) instead
+    // of f32 rows that each matmul splits; false: rmsnorm
+    this.planosNorma = op.norm_planes !== false;
     // one-token step: the split-K attention's partials merged by the last workgroup of each grid column in the same
     // launch (dec_attn P[12] = 1) instead of a dec_attn_comb launch.  A column takes at most 4 query heads: groups of
     // 8 or more query heads are split over gsplit columns per KV head (P[13]; each column streams its KV head's keys
@@ -213,6 +217,8 @@ class ModeloTransformer {
     }
     const B = (n, l) => { const b = gpu.buffer(n, undefined, l); this.bufs.push(b); return b; };
     const TB = this.batch, D = this.D, qd = this.nh * this.hd, kvd = this.nkv * this.hd;
+    // the norms' bf16 input planes for prompt chunks of 256 tokens or more (256-token rows)
+    this.xsPl = TB >= 256 ? B(4 * Math.ceil(TB / 256) * 256 * D, 'x_planes') : null;
     const FF = this.nExp ? this.nUsados * this.ffe : this.F;
     this.bPaso = B(16, 'paso');
     this.bIds = B(4 * TB, 'ids');
@@ -357,6 +363,15 @@ class ModeloTransformer {
           ['f', this.escAtt], ['u', c.anillo], ['u', 0], ['u', 0], ['u', f16], ['u', c.slots]]), P, this.q, c.kc, c.vc, this.att]),
         wo: directo(c.wo, this.att, c.postAtt),
       };
+      // the attention norm as input planes of Q, K and V (all K-quant, tiled)
+      const uPl = gpu.uniforme([['u', D], ['f', this.eps]]);
+      const pl = this.planosNorma && this.fusion && this.baldosa && this.xsPl && D % 32 === 0;
+      if (pl && KQ.has(c.wq.tipo) && KQ.has(c.wk.tipo) && KQ.has(c.wv.tipo)) {
+        gc.attnNormPl = gpu.grupo('rmsnorm_planes', [uPl, P, this.x, c.attnNorm, this.xsPl]);
+        gc.wqPl = this._mm(c.wq, this.xsPl, this.q, 0, false, true);
+        gc.wkPl = this._mm(c.wk, this.xsPl, this.k, 0, false, true);
+        gc.wvPl = this._mm(c.wv, this.xsPl, this.v, 0, false, true);
+      }
       if (this.nExp) {
         const K = this.nUsados;
         gc.router = this._mm(c.router, this.xn, this.rl, 0);
@@ -375,10 +390,16 @@ class ModeloTransformer {
         if (this.ffnFusionada && this.fusion && this.baldosa && KQ.has(c.gate.tipo) && c.up.tipo === c.gate.tipo &&
             c.up.N === c.gate.N && c.up.K === c.gate.K) {
           // with K-quant down weights the fused gate/up writes the down matmul's input planes (no split between them)
-          const pl = KQ.has(c.down.tipo) && c.down.K === c.gate.N && this.planosFfn;
+          const yp = KQ.has(c.down.tipo) && c.down.K === c.gate.N && this.planosFfn;
           gc.glu = gpu.grupo('matmul_' + c.gate.tipo + '_t_swiglu', [gpu.uniforme([['u', c.gate.N], ['u', c.gate.K],
-            ['u', pl ? 1 : 0]]), P, c.gate.w, c.up.w, this.xn, this.g]);
-          if (pl) gc.downPl = directo(c.down, this.g, c.postFfn, true);
+            ['u', yp ? 1 : 0]]), P, c.gate.w, c.up.w, this.xn, this.g]);
+          if (yp) gc.downPl = directo(c.down, this.g, c.postFfn, true);
+          // the FFN norm as the fused launch's input planes
+          if (pl) {
+            gc.ffnNormPl = gpu.grupo('rmsnorm_planes', [uPl, P, this.x, c.ffnNorm, this.xsPl]);
+            gc.gluPl = gpu.grupo('matmul_' + c.gate.tipo + '_t_swiglu', [gpu.uniforme([['u', c.gate.N],
+              ['u', c.gate.K], ['u', yp ? 1 : 0], ['u', 1]]), P, c.gate.w, c.up.w, this.xsPl, this.g]);
+          }
         }
         gc.swiglu = gpu.grupo(this.gemma ? 'geglu' : 'swiglu', [gpu.uniforme([['u', c.gate.N]]), P, this.g, this.u]);
         gc.F = c.gate.N;
@@ -435,14 +456,21 @@ class ModeloTransformer {
       despachar(null, d.suma, filas(self.D));
     };
     for (const gc of G.capas) {
-      despachar(null, gc.attnNorm, T);
-      mm(gc.wq); mm(gc.wk); mm(gc.wv);
+      if (gc.attnNormPl && T >= 256) {
+        despachar(null, gc.attnNormPl, Math.ceil(T / 8));
+        mm(gc.wqPl); mm(gc.wkPl); mm(gc.wvPl);
+      } else {
+        despachar(null, gc.attnNorm, T);
+        mm(gc.wq); mm(gc.wk); mm(gc.wv);
+      }
       despachar(null, gc.ropeQ, this.nh, T);
       despachar(null, gc.ropeK, this.nkv, T);
       despachar(null, gc.kvw, Math.ceil(T * this.nkv * this.hd / 256));
       despachar(null, gc.att, this.nh, T);
       salida(gc.wo);
-      despachar(null, gc.ffnNorm, T);
+      const gluPl = !this.nExp && gc.gluPl && T >= 256;
+      if (gluPl) despachar(null, gc.ffnNormPl, Math.ceil(T / 8));
+      else despachar(null, gc.ffnNorm, T);
       if (this.nExp) {
         mm(gc.router);
         despachar(null, gc.topk, Math.ceil(T / 64));
@@ -459,7 +487,7 @@ class ModeloTransformer {
         despachar(null, gc.comb, filas(this.D));
       } else {
         if (gc.glu && T >= 256) {
-          despachar(null, gc.glu, Math.ceil(gc.F / 64), 1, Math.ceil(T / 32));
+          despachar(null, gluPl ? gc.gluPl : gc.glu, Math.ceil(gc.F / 64), 1, Math.ceil(T / 32));
           salida(gc.downPl || gc.down);
         } else {
           mm(gc.gate); mm(gc.up);

@@ -433,6 +433,36 @@ def test_matmul_swiglu_planes_feed_down(quipu, dev, fg, fd, T, F, D, acc):
     assert np.all(np.isfinite(a)) and a.view(np.uint32).tolist() == b.view(np.uint32).tolist()
 
 
+@pytest.mark.parametrize("T,D,N", [(300, 1024, 512), (2048, 4096, 1024), (256, 2048, 768)])
+def test_rmsnorm_planes_feed_the_matmuls(quipu, dev, T, D, N):
+    """rmsnorm_planes writes the rmsnorm of each row as the matmuls' bf16 input planes: matmul_q4k_t with P[4] = 2
+    and matmul_q4k_t_swiglu with P[3] = 1 reading them give, bit for bit, what they give from rmsnorm's f32 rows
+    (which they split themselves)."""
+    x = dev.buf((np.random.default_rng(23).standard_normal((T, D)) * 3.0).astype(np.float32))
+    wn = dev.buf((1.0 + 0.1 * np.random.default_rng(24).standard_normal(D)).astype(np.float32))
+    paso = dev.paso(T, 0)
+    eps = 1e-5
+    xn = dev.buf(np.zeros((T, D), np.float32))
+    quipu.dispatch("rmsnorm", [("u", D), ("u", 0), ("f", eps), ("u", 0)], [paso, x, wn, xn], (T, 1, 1))
+    rows = -(-T // 256) * 256
+    xs = dev.zeros(4 * rows * D)
+    quipu.dispatch("rmsnorm_planes", [("u", D), ("f", eps)], [paso, x, wn, xs], (-(-T // 8), 1, 1))
+    raw = raw_matrix(capi.Q4_K, N, D, 96)
+    w = dev.matrix(capi.Q4_K, raw, N, D)
+    grid = ((N + 63) // 64, 1, (T + 31) // 32)
+    ya, yb = dev.buf(np.zeros((T, N), np.float32)), dev.buf(np.zeros((T, N), np.float32))
+    quipu.dispatch("matmul_q4k_t", [("u", N), ("u", D), ("u", 0), ("u", 0)], [paso, w, xn, ya], grid)
+    quipu.dispatch("matmul_q4k_t", [("u", N), ("u", D), ("u", 0), ("u", 0), ("u", 2)], [paso, w, xs, yb], grid)
+    a, b = dev.get(ya, (T, N)), dev.get(yb, (T, N))
+    assert np.all(np.isfinite(a)) and a.view(np.uint32).tolist() == b.view(np.uint32).tolist()
+    w2 = dev.matrix(capi.Q4_K, raw_matrix(capi.Q4_K, N, D, 97), N, D)
+    ga, gb = dev.buf(np.zeros((T, N), np.float32)), dev.buf(np.zeros((T, N), np.float32))
+    quipu.dispatch("matmul_q4k_t_swiglu", [("u", N), ("u", D)], [paso, w, w2, xn, ga], grid)
+    quipu.dispatch("matmul_q4k_t_swiglu", [("u", N), ("u", D), ("u", 0), ("u", 1)], [paso, w, w2, xs, gb], grid)
+    a, b = dev.get(ga, (T, N)), dev.get(gb, (T, N))
+    assert np.all(np.isfinite(a)) and a.view(np.uint32).tolist() == b.view(np.uint32).tolist()
+
+
 def test_matmul_planes_rejections(quipu, dev):
     """P[4] = 2 needs the 256-token tiles (under 256 tokens the matmul refuses it), and the planes' buffers must hold
     4 * rows * K bytes (256-token rows)."""
@@ -449,6 +479,12 @@ def test_matmul_planes_rejections(quipu, dev):
     with pytest.raises(capi.QuipuError, match="256 tokens or more"):
         quipu.dispatch("matmul_q4k_t", [("u", D), ("u", F), ("u", 0), ("u", 0), ("u", 2)],
                        [dev.paso(100, 0), w, dev.zeros(4 * 256 * F), dev.zeros(4 * 100 * D)], (4, 1, 4))
+    with pytest.raises(capi.QuipuError, match="planes' buffer"):
+        quipu.dispatch("rmsnorm_planes", [("u", D), ("f", 1e-5)],
+                       [dev.paso(T, 0), x, dev.buf(np.ones(D, np.float32)), dev.zeros(4 * T * D)], (-(-T // 8), 1, 1))
+    with pytest.raises(capi.QuipuError, match="input planes' buffer"):
+        quipu.dispatch("matmul_q4k_t_swiglu", [("u", F), ("u", D), ("u", 0), ("u", 1)],
+                       [dev.paso(T, 0), w, w, dev.zeros(4 * T * D), dev.zeros(4 * T * F)], (4, 1, 10))
 
 
 def test_matmul_reuses_the_split_input(quipu, dev):

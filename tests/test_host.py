@@ -51,7 +51,7 @@ def test_header_declares_the_facade():
 FORMATS = ("q2k", "q3k", "q4k", "q5k", "q6k", "q8", "f32", "iq4nl")
 OPS = ["matmul_%s_%s" % (f, s) for f in FORMATS for s in ("1", "4", "t", "e", "e_swiglu")] + \
       ["embed_%s" % f for f in FORMATS] + \
-      ["rmsnorm", "norm_rope", "kv_write", "atencion", "swiglu", "geglu", "escalar", "suma_esc", "moe_topk", "moe_comb", "gemv", "dec_attn",
+      ["rmsnorm", "rmsnorm_planes", "norm_rope", "kv_write", "atencion", "swiglu", "geglu", "escalar", "suma_esc", "moe_topk", "moe_comb", "gemv", "dec_attn",
        "dec_attn_comb", "argmax", "argmax_fin", "repack_q2k", "repack_q3k", "repack_q4k", "repack_q5k", "repack_q6k", "repack_q8", "repack_iq4nl", "fill_u32", "dequant",
        "copy_f4", "read_f4", "moe_gate_up_q4k", "moe_gate_up_q6k", "moe_down_q4k", "moe_down_q6k", "penalizar",
        "topk_cand", "moe_group"] + ["matmul_%s_eg" % f for f in FORMATS] + \
@@ -71,7 +71,7 @@ def test_ops_used_by_the_js_host_exist(built):
     used = set()
     for f in ("transformer.js", "weights.js"):
         src = open(os.path.join(JS, f)).read()
-        used |= set(re.findall(r"['\"]((?:matmul|embed)_[a-z0-9_]+|rmsnorm|norm_rope|kv_write|atencion|swiglu|"
+        used |= set(re.findall(r"['\"]((?:matmul|embed)_[a-z0-9_]+|rmsnorm(?:_planes)?|norm_rope|kv_write|atencion|swiglu|"
                                r"moe_topk|moe_comb|moe_group|moe_(?:gate_up|down)_|gemv|dec_attn(?:_comb)?|argmax(?:_fin)?|"
                                r"repack_q[2-68]k?|fill_u32)['\"]", src))
     # names built by concatenation in the host: matmul_<fmt>_<suffix> and embed_<fmt>
