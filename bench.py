@@ -56,7 +56,7 @@ def log(*a):
 
 
 def model_dir():
-    d = os.environ.get("QP_MODEL_DIR") or os.path.join(os.environ.get("TMPDIR", "/tmp"), "quipu_models")
+    d = os.environ.get("QP_MODEL_DIR") or os.path.join((os.environ.get("TMPDIR") or "/tmp"), "quipu_models")
     os.makedirs(d, exist_ok=True)
     return d
 

@@ -51,7 +51,10 @@ def run(cmd, timeout=300, env=None):
 
 @pytest.fixture(scope="session")
 def models_dir():
-    d = os.environ.get("QP_TEST_MODEL_DIR") or os.path.join(os.environ.get("TMPDIR", "/tmp"), "quipu_test_models")
+    """The synthetic models' directory: bench.py's by default (QP_MODEL_DIR, else $TMPDIR/quipu_models), so that a
+    test run and a benchmark on one machine write the models they share (the 8B and MoE shapes, ~22 GB) once."""
+    d = (os.environ.get("QP_TEST_MODEL_DIR") or os.environ.get("QP_MODEL_DIR")
+         or os.path.join(os.environ.get("TMPDIR") or "/tmp", "quipu_models"))
     os.makedirs(d, exist_ok=True)
     return d
 
