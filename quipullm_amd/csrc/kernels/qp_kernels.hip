@@ -2820,29 +2820,46 @@ KERNEL __launch_bounds__(256) void qp_rmsnorm(QpRmsArgs a) {
     for (uint32_t i = li; i < D; i += 256) y[i] = (x[i] * inv) * w[i];
 }
 
-// The rmsnorm of R = 8 token rows per workgroup written as the next matmul's input planes (xs_off's layout, a.rows
+// The rmsnorm of R token rows per workgroup written as the next matmul's input planes (xs_off's layout, a.rows
 // rows; rows past T are not written): qp_rmsnorm's sums in its order (256 threads stride each row, the LDS tree
-// 128 .. 1, the eight trees side by side) and its y = (x * inv) * w, split with qp_split_bf16's formula, so the
-// planes are those qp_split_bf16 makes of qp_rmsnorm's rows.  The second pass reads x again (from the caches),
-// eight consecutive inputs per thread, consecutive threads on consecutive rows.
-KERNEL __launch_bounds__(256) void qp_rmsnorm_planes(QpRmsPlanesArgs a) {
-    constexpr uint32_t R = 8;
+// 128 .. 1, the R trees side by side) and its y = (x * inv) * w, split with qp_split_bf16's formula, so the planes
+// are those qp_split_bf16 makes of qp_rmsnorm's rows.  The rows are kept in LDS from the first pass (row stride
+// D + 4 floats: the R rows' reads of one chunk fall in different banks); the second takes eight consecutive inputs
+// per thread, consecutive threads on consecutive rows (R threads store 16 R contiguous bytes of a plane).  R = 8 up
+// to D = 4096, 4 up to 8192, 2 up to 16384 (the rows fill up to 128 KB of dynamic LDS).
+template <uint32_t R>
+QP_DEV void rmsnorm_planes_body(const QpRmsPlanesArgs& a) {
+    extern __shared__ float4 smem4[];
+    float* xr = reinterpret_cast<float*>(smem4);  // [R][D + 4]
     __shared__ float red[R][256];
     __shared__ float inv_s[R];
-    const uint32_t T = paso_T(a.paso), li = threadIdx.x, D = a.d, t0 = blockIdx.x * R;
+    const uint32_t T = paso_T(a.paso), li = threadIdx.x, D = a.d, t0 = blockIdx.x * R, ld = D + 4;
     if (t0 >= T) return;
     const uint32_t nr = min(R, T - t0);
-    // the eight rows' loads of one stride step issued together (each row's sum still in qp_rmsnorm's order)
+    // the R rows' loads of U stride steps issued together (each row's sum still in qp_rmsnorm's order)
     float s[R];
 #pragma unroll
     for (uint32_t r = 0; r < R; r++) s[r] = 0.0f;
+    // four stride steps' loads in flight at once (a step past D loads 0, which adds nothing to a sum)
     const float* xb = cptr<float>(a.x) + (uint64_t)t0 * D;
-    for (uint32_t i = li; i < D; i += 256) {
-        float v[R];
+    constexpr uint32_t U = 32 / R;
+    for (uint32_t i0 = li; i0 < D; i0 += 256 * U) {
+        float v[U][R];
 #pragma unroll
-        for (uint32_t r = 0; r < R; r++) v[r] = r < nr ? xb[(uint64_t)r * D + i] : 0.0f;
+        for (uint32_t u = 0; u < U; u++)
 #pragma unroll
-        for (uint32_t r = 0; r < R; r++) s[r] = s[r] + v[r] * v[r];
+            for (uint32_t r = 0; r < R; r++) {
+                const uint32_t i = i0 + 256 * u;
+                v[u][r] = r < nr && i < D ? xb[(uint64_t)r * D + i] : 0.0f;
+            }
+#pragma unroll
+        for (uint32_t u = 0; u < U; u++)
+#pragma unroll
+            for (uint32_t r = 0; r < R; r++) {
+                const uint32_t i = i0 + 256 * u;
+                s[r] = s[r] + v[u][r] * v[u][r];
+                if (i < D) xr[r * ld + i] = v[u][r];
+            }
     }
 #pragma unroll
     for (uint32_t r = 0; r < R; r++) red[r][li] = s[r];
@@ -2855,22 +2872,43 @@ KERNEL __launch_bounds__(256) void qp_rmsnorm_planes(QpRmsPlanesArgs a) {
     if (li < R) inv_s[li] = 1.0f / sqrtf(red[li][0] / (float)D + a.eps);
     __syncthreads();
     const uint64_t plane = 2ull * a.rows * D;  // bytes of the high plane (D % 32 == 0)
-    const float* w = cptr<float>(a.w);
-    for (uint32_t i = li; i < R * (D / 8); i += 256) {
-        // no contraction: the product must be rounded to y before the split subtracts its high part (an FMA of
-        // (x * inv) * w - hi would give another low part than qp_split_bf16 gives of the rounded y)
-#pragma clang fp contract(off)
-        const uint32_t r = i % R, k8 = (i / R) * 8, t = t0 + r;
-        if (r >= nr) continue;
-        const float* x = cptr<float>(a.x) + (uint64_t)t * D + k8;
-        const float inv = inv_s[r];
-        float v[8];
+    // four chunks per round, their norm weight loads issued first (r and the chunk's first input: the thread's
+    // row stays r = li % R since 256 is a multiple of R)
+    const uint32_t r = li % R, t = t0 + r;
+    const float inv = inv_s[r];
+    const bool on = r < nr;
+    for (uint32_t i0 = li; i0 < R * (D / 8); i0 += 4 * 256) {
+        float4 wv[4][2];
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = (x[j] * inv) * w[k8 + j];
-        const uint64_t o = xs_off(t, k8, a.rows);
-        split_store8(v, reinterpret_cast<__bf16*>(a.xs + o), reinterpret_cast<__bf16*>(a.xs + plane + o));
+        for (int u = 0; u < 4; u++) {
+            const uint32_t k8 = ((i0 + 256 * u) / R) * 8;
+            const bool in = i0 + 256 * u < R * (D / 8);
+            wv[u][0] = in ? gload<float4>(a.w + 4ull * k8) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            wv[u][1] = in ? gload<float4>(a.w + 4ull * k8 + 16) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            // no contraction: the product must be rounded to y before the split subtracts its high part (an FMA of
+            // (x * inv) * w - hi would give another low part than qp_split_bf16 gives of the rounded y)
+#pragma clang fp contract(off)
+            const uint32_t i = i0 + 256 * u, k8 = (i / R) * 8;
+            if (!on || i >= R * (D / 8)) continue;
+            const float4 x0 = *reinterpret_cast<const float4*>(xr + r * ld + k8);
+            const float4 x1 = *reinterpret_cast<const float4*>(xr + r * ld + k8 + 4);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const float ww[8] = {wv[u][0].x, wv[u][0].y, wv[u][0].z, wv[u][0].w,
+                                 wv[u][1].x, wv[u][1].y, wv[u][1].z, wv[u][1].w};
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = (xv[j] * inv) * ww[j];
+            const uint64_t o = xs_off(t, k8, a.rows);
+            split_store8(v, reinterpret_cast<__bf16*>(a.xs + o), reinterpret_cast<__bf16*>(a.xs + plane + o));
+        }
     }
 }
+KERNEL __launch_bounds__(256) void qp_rmsnorm_planes(QpRmsPlanesArgs a) { rmsnorm_planes_body<8>(a); }
+KERNEL __launch_bounds__(256) void qp_rmsnorm_planes4(QpRmsPlanesArgs a) { rmsnorm_planes_body<4>(a); }
+KERNEL __launch_bounds__(256) void qp_rmsnorm_planes2(QpRmsPlanesArgs a) { rmsnorm_planes_body<2>(a); }
 
 // ====================================================================================== norm + RoPE
 // Reference norm_rope (gpu.js:394-444), one wavefront per head vector.

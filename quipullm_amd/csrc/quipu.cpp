@@ -697,7 +697,8 @@ int op_rmsnorm(const Ctx& c) {
 // rmsnorm_planes: P{D, eps}; [paso, x, w, xs]; grid ceil(T / 8).  No counterpart in the reference: its rmsnorm
 // (gpu.js:332-356) of the T rows written as the bf16 input planes of the matmul that reads them next (matmul_<fmt>_t
 // with P[4] = 2, matmul_<fmt>_t_swiglu with P[3] = 1; K-quants, T >= 256), for R = 256 ceil(T / 256) token rows:
-// 4 R D bytes, D % 32 == 0.  The planes are those the matmul's own split makes of rmsnorm's rows.
+// 4 R D bytes, D % 32 == 0, D <= 16384.  The planes are those the matmul's own split makes of rmsnorm's rows.  A
+// workgroup takes 8 rows (4 above D = 4096, 2 above 8192), kept in LDS between its two passes.
 int op_rmsnorm_planes(const Ctx& c) {
     if (int e = need_bufs(c, 4, "rmsnorm_planes")) return e;
     QpRmsPlanesArgs a = {};
@@ -707,11 +708,14 @@ int op_rmsnorm_planes(const Ctx& c) {
     a.x = c.B(1);
     a.w = c.B(2);
     a.xs = c.B(3);
-    if (!a.d || a.d % 32) return fail(QP_E_ARG, "rmsnorm_planes: D=%u (a multiple of 32)", a.d);
-    const uint32_t gx = c.gx ? c.gx : 1;
+    if (!a.d || a.d % 32 || a.d > 16384)
+        return fail(QP_E_ARG, "rmsnorm_planes: D=%u (a multiple of 32, at most 16384)", a.d);
+    const uint32_t gx = c.gx ? c.gx : 1;  // ceil(T / 8)
     a.rows = cdiv(gx * 8, 256) * 256;
     if (int e = need_room(a.xs, 4ull * a.rows * a.d, "rmsnorm_planes", "the planes' buffer")) return e;
-    return launch(K_rmsnorm_planes, gx, 1, 1, 256, 0, a);
+    const uint32_t rw = a.d <= 4096 ? 8 : a.d <= 8192 ? 4 : 2;  // rows per workgroup
+    const Kid k = rw == 8 ? K_rmsnorm_planes : rw == 4 ? K_rmsnorm_planes4 : K_rmsnorm_planes2;
+    return launch(k, gx * (8 / rw), 1, 1, 256, 4 * rw * (a.d + 4), a);
 }
 
 // norm_rope (gpu.js:394-444): P{hd, nh, usaNorm, neox, eps, base, nrot, z=esc bits}; [paso, v, w]; (nh, T).

@@ -433,11 +433,12 @@ def test_matmul_swiglu_planes_feed_down(quipu, dev, fg, fd, T, F, D, acc):
     assert np.all(np.isfinite(a)) and a.view(np.uint32).tolist() == b.view(np.uint32).tolist()
 
 
-@pytest.mark.parametrize("T,D,N", [(300, 1024, 512), (2048, 4096, 1024), (256, 2048, 768)])
+@pytest.mark.parametrize("T,D,N", [(300, 1024, 512), (2048, 4096, 1024), (256, 2048, 768), (300, 5120, 256),
+                                   (260, 9216, 256)])
 def test_rmsnorm_planes_feed_the_matmuls(quipu, dev, T, D, N):
     """rmsnorm_planes writes the rmsnorm of each row as the matmuls' bf16 input planes: matmul_q4k_t with P[4] = 2
     and matmul_q4k_t_swiglu with P[3] = 1 reading them give, bit for bit, what they give from rmsnorm's f32 rows
-    (which they split themselves)."""
+    (which they split themselves).  D = 5120 and 9216: 4 and 2 rows per workgroup."""
     x = dev.buf((np.random.default_rng(23).standard_normal((T, D)) * 3.0).astype(np.float32))
     wn = dev.buf((1.0 + 0.1 * np.random.default_rng(24).standard_normal(D)).astype(np.float32))
     paso = dev.paso(T, 0)
