@@ -4434,20 +4434,31 @@ QP_DEV void attn_mfma_body(const QpAttnArgs& a) {
                 f[w] = __builtin_amdgcn_exp2f((pm[w][g][lane] - M) * QP_LOG2E);
                 L = fmaf(f[w], pl[w][g][lane], L);
             }
-            if (row_ok[g]) {
-                const uint64_t orow = a.o + 4ull * (((uint64_t)tr[g] * a.nh + hr[g]) * HD);
+            const uint64_t orow = a.o + 4ull * (((uint64_t)tr[g] * a.nh + hr[g]) * HD);
 #pragma unroll
-                for (int j = 0; j < MW; j++) {
-                    const int mm = (int)wave * MW + j;
-                    f4v o = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < MW; j++) {
+                const int mm = (int)wave * MW + j;
+                f4v o = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                    for (int w = 0; w < 4; w++) o = o + pa[w][g][mm][lane] * f[w];
-                    float4 v;
-                    v.x = L > 0.0f ? o[0] / L : 0.0f;
-                    v.y = L > 0.0f ? o[1] / L : 0.0f;
-                    v.z = L > 0.0f ? o[2] / L : 0.0f;
-                    v.w = L > 0.0f ? o[3] / L : 0.0f;
-                    gstore<float4>(orow + 4 * (16 * mm + 4 * qg), v);
+                for (int w = 0; w < 4; w++) o = o + pa[w][g][mm][lane] * f[w];
+                float4 v;
+                v.x = L > 0.0f ? o[0] / L : 0.0f;
+                v.y = L > 0.0f ? o[1] / L : 0.0f;
+                v.z = L > 0.0f ? o[2] / L : 0.0f;
+                v.w = L > 0.0f ? o[3] / L : 0.0f;
+                if (!a.orows) {
+                    if (row_ok[g]) gstore<float4>(orow + 4 * (16 * mm + 4 * qg), v);
+                    continue;
+                }
+                // as the next matmul's input planes: lanes qg and qg + 1 (lane ^ 16, the same row) hold the two
+                // halves of eight consecutive outputs; the even one splits them with qp_split_bf16's formula
+                const float p0 = bfly_f<4>(v.x, lane), p1 = bfly_f<4>(v.y, lane), p2 = bfly_f<4>(v.z, lane),
+                            p3 = bfly_f<4>(v.w, lane);
+                if (row_ok[g] && !(qg & 1)) {
+                    const float e[8] = {v.x, v.y, v.z, v.w, p0, p1, p2, p3};
+                    const uint32_t K = a.nh * HD, k = hr[g] * HD + 16 * mm + 4 * qg;
+                    const uint64_t off = xs_off(tr[g], k, a.orows), plane = 2ull * a.orows * K;
+                    split_store8(e, reinterpret_cast<__bf16*>(a.o + off), reinterpret_cast<__bf16*>(a.o + plane + off));
                 }
             }
         }

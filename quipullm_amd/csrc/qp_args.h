@@ -168,7 +168,10 @@ typedef struct {
     uint32_t hd, nh, nkv, swa;
     float scale;
     uint32_t cap, f16, qb;   // qb: queries per workgroup
-    uint32_t rows, pad[3];   // rows: slots of the cache; keys at or past it are not read
+    uint32_t rows;           // slots of the cache; keys at or past it are not read
+    uint32_t orows;          // 0: o holds f32 rows; else o receives them as the next matmul's bf16 input planes
+                             // (qp_split_bf16's layout, orows token rows, K = nh hd)
+    uint32_t pad[2];
 } QpAttnArgs;
 
 // Split-K decode attention with fused q/k norm + RoPE + KV append (one token).

@@ -783,7 +783,19 @@ int op_atencion(const Ctx& c) {
     a.vc = c.B(3);
     a.o = c.B(4);
     const uint32_t G = a.nh / a.nkv;
-    if (a.f16 && !a.swa && !a.cap && (G == 1 || G == 2 || G == 4 || G == 8) && !getenv_flag("QP_NO_MFMA")) {
+    // P[10] = 1 (an addition of this backend's): o receives the output as the bf16 input planes of the matmul that
+    // reads it next (matmul_<fmt>_t with P[4] = 2: the same T, 256 ceil(T / 256) token rows, K = nh hd), the values
+    // its own split would make of the f32 rows.  The two-group matrix-core path only.
+    const bool oplanes = c.U(10) == 1;
+    const bool mfma = a.f16 && !a.swa && !a.cap && (G == 1 || G == 2 || G == 4 || G == 8) && !getenv_flag("QP_NO_MFMA");
+    if (oplanes) {
+        if (!mfma || getenv_flag("QP_ATTN_RG1"))
+            return fail(QP_E_ARG, "atencion: P[10] = 1 (output planes) needs the matrix-core path (f16 cache, no "
+                                  "window or ring, groups of 1, 2, 4 or 8 query heads)");
+        a.orows = cdiv(c.gy ? c.gy : 1, 256) * 256;
+        if (int e = need_room(a.o, 4ull * a.orows * a.nh * a.hd, "atencion", "the output planes' buffer")) return e;
+    }
+    if (mfma) {
         // matrix-core path: a wavefront takes 16 rg / G tokens x G heads, a workgroup four wavefronts
         static const Kid km[2][4] = {{K_attn_mfma_h64_g1, K_attn_mfma_h64_g2, K_attn_mfma_h64_g4, K_attn_mfma_h64_g8},
                                      {K_attn_mfma_h128_g1, K_attn_mfma_h128_g2, K_attn_mfma_h128_g4,

@@ -217,8 +217,9 @@ class ModeloTransformer {
     }
     const B = (n, l) => { const b = gpu.buffer(n, undefined, l); this.bufs.push(b); return b; };
     const TB = this.batch, D = this.D, qd = this.nh * this.hd, kvd = this.nkv * this.hd;
-    // the norms' bf16 input planes for prompt chunks of 256 tokens or more (256-token rows)
-    this.xsPl = TB >= 256 ? B(4 * Math.ceil(TB / 256) * 256 * D, 'x_planes') : null;
+    // the bf16 input planes the norms and the attention write for prompt chunks of 256 tokens or more (256-token
+    // rows of the wider of the model and attention widths)
+    this.xsPl = TB >= 256 ? B(4 * Math.ceil(TB / 256) * 256 * Math.max(D, qd), 'x_planes') : null;
     const FF = this.nExp ? this.nUsados * this.ffe : this.F;
     this.bPaso = B(16, 'paso');
     this.bIds = B(4 * TB, 'ids');
@@ -372,6 +373,14 @@ class ModeloTransformer {
         gc.wkPl = this._mm(c.wk, this.xsPl, this.k, 0, false, true);
         gc.wvPl = this._mm(c.wv, this.xsPl, this.v, 0, false, true);
       }
+      // the attention's output as wo's input planes (the matrix-core attention: f16 cache, no window or ring)
+      const grupoQ = this.nh / this.nkv, qd = this.nh * this.hd;
+      if (pl && KQ.has(c.wo.tipo) && f16 && !c.swa && !c.anillo && [1, 2, 4, 8].includes(grupoQ) && qd % 32 === 0) {
+        gc.attPl = gpu.grupo('atencion', [gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', c.swa],
+          ['f', this.escAtt], ['u', c.anillo], ['u', 0], ['u', 0], ['u', f16], ['u', c.slots], ['u', 1]]), P, this.q,
+          c.kc, c.vc, this.xsPl]);
+        gc.woPl = directo(c.wo, this.xsPl, c.postAtt, true);
+      }
       if (this.nExp) {
         const K = this.nUsados;
         gc.router = this._mm(c.router, this.xn, this.rl, 0);
@@ -466,8 +475,13 @@ class ModeloTransformer {
       despachar(null, gc.ropeQ, this.nh, T);
       despachar(null, gc.ropeK, this.nkv, T);
       despachar(null, gc.kvw, Math.ceil(T * this.nkv * this.hd / 256));
-      despachar(null, gc.att, this.nh, T);
-      salida(gc.wo);
+      if (gc.attPl && T >= 256) {
+        despachar(null, gc.attPl, this.nh, T);
+        salida(gc.woPl);
+      } else {
+        despachar(null, gc.att, this.nh, T);
+        salida(gc.wo);
+      }
       const gluPl = !this.nExp && gc.gluPl && T >= 256;
       if (gluPl) despachar(null, gc.ffnNormPl, Math.ceil(T / 8));
       else despachar(null, gc.ffnNorm, T);

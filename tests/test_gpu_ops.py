@@ -464,6 +464,37 @@ def test_rmsnorm_planes_feed_the_matmuls(quipu, dev, T, D, N):
     assert np.all(np.isfinite(a)) and a.view(np.uint32).tolist() == b.view(np.uint32).tolist()
 
 
+@pytest.mark.parametrize("hd,nh,nkv,T,pos0", [(128, 32, 8, 300, 0), (128, 32, 4, 256, 100), (64, 16, 2, 520, 7)])
+def test_atencion_output_planes_feed_wo(quipu, dev, hd, nh, nkv, T, pos0):
+    """atencion with P[10] = 1 writes its output as wo's bf16 input planes: matmul_q4k_t with P[4] = 2 reading them
+    gives, bit for bit, what it gives from the f32 output rows (which it splits itself)."""
+    rows = pos0 + T + 40
+    kvd, qd = nkv * hd, nh * hd
+    rng = np.random.default_rng(27)
+    q = rng.standard_normal((T, qd)).astype(np.float32)
+    kc = f16r(rng.standard_normal((rows, kvd)))
+    vc = f16r(rng.standard_normal((rows, kvd)))
+    paso = dev.paso(T, pos0)
+    kb, vb, qb = dev.buf(kc.astype(np.float16)), dev.buf(refs.v_tiled(vc.astype(np.float16), kvd)), dev.buf(q)
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    P = [("u", hd), ("u", nh), ("u", nkv), ("u", 0), ("f", scale), ("u", 0), ("u", 0), ("u", 0), ("u", 1), ("u", rows)]
+    o = dev.zeros(T * qd * 4)
+    quipu.dispatch("atencion", P, [paso, qb, kb, vb, o], (nh, T))
+    orows = -(-T // 256) * 256
+    ob = dev.zeros(4 * orows * qd)
+    quipu.dispatch("atencion", P + [("u", 1)], [paso, qb, kb, vb, ob], (nh, T))
+    N = 512
+    w = dev.matrix(capi.Q4_K, raw_matrix(capi.Q4_K, N, qd, 98), N, qd)
+    grid = ((N + 63) // 64, 1, (T + 31) // 32)
+    ya, yb = dev.buf(np.zeros((T, N), np.float32)), dev.buf(np.zeros((T, N), np.float32))
+    quipu.dispatch("matmul_q4k_t", [("u", N), ("u", qd), ("u", 0), ("u", 0)], [paso, w, o, ya], grid)
+    quipu.dispatch("matmul_q4k_t", [("u", N), ("u", qd), ("u", 0), ("u", 0), ("u", 2)], [paso, w, ob, yb], grid)
+    a, b = dev.get(ya, (T, N)), dev.get(yb, (T, N))
+    assert np.all(np.isfinite(a)) and a.view(np.uint32).tolist() == b.view(np.uint32).tolist()
+    with pytest.raises(capi.QuipuError, match="output planes"):
+        quipu.dispatch("atencion", P + [("u", 1)], [paso, qb, kb, vb, dev.zeros(4 * orows * qd - 64)], (nh, T))
+
+
 def test_matmul_planes_rejections(quipu, dev):
     """P[4] = 2 needs the 256-token tiles (under 256 tokens the matmul refuses it), and the planes' buffers must hold
     4 * rows * K bytes (256-token rows)."""
