@@ -2057,7 +2057,9 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const bool in = kb + 8 * i < K;
-                const uint64_t o = g.xs + xs_off(xst, kb + 8 * i, g.rows);
+                // grouped by expert: row-major planes (a tile gathers rows; each lane reads 64 bytes of one)
+                const uint64_t o = g.xs + (grp ? 2ull * ((uint64_t)xst * (((K + 31) >> 5) << 5) + kb + 8 * i)
+                                               : xs_off(xst, kb + 8 * i, g.rows));
                 xp[i] = in ? gload<uint4>(o) : uint4{0, 0, 0, 0};
                 xp[4 + i] = in ? gload<uint4>(o + xplane) : uint4{0, 0, 0, 0};
             }
@@ -2166,12 +2168,21 @@ QP_DEV void gemm_mfma_body(const QpGemmArgs& g) {
 // x [T][k] -> its bf16 high / low planes for the matrix-core matmul, in the layout of xs_off: one K step's quarter
 // q of 256 consecutive tokens is 4 KB contiguous (a wavefront's load covers 1 KB), and a chunk's inputs past K
 // are zeros.  Token rows T .. rows - 1 are not written: their products reach only outputs that are not
-// stored.  One 16-byte group per thread and step, consecutive threads on consecutive tokens.
+// stored.  One 16-byte group per thread and step, consecutive threads on consecutive tokens.  With mul (the grouped
+// expert matmul's rows): row-major planes, consecutive threads on consecutive groups of one row.
 KERNEL __launch_bounds__(256) void qp_split_bf16(QpSplitArgs a) {
-    const uint32_t T = paso_T(a.paso), nq = ((a.k + 31) >> 5) * 4;
+    const uint32_t T = a.mul ? min(paso_T(a.paso) * a.mul, a.cap) : paso_T(a.paso), nq = ((a.k + 31) >> 5) * 4;
     const uint64_t n = (uint64_t)nq * T, plane = 2ull * a.rows * (((a.k + 31) >> 5) << 5);
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull) {
-        const uint32_t cq = (uint32_t)(i / T), t = (uint32_t)(i - (uint64_t)cq * T), k8 = cq * 8;
+        uint32_t cq, t;
+        if (a.mul) {
+            t = (uint32_t)(i / nq);
+            cq = (uint32_t)(i - (uint64_t)t * nq);
+        } else {
+            cq = (uint32_t)(i / T);
+            t = (uint32_t)(i - (uint64_t)cq * T);
+        }
+        const uint32_t k8 = cq * 8;
         float v[8];
         if (k8 < a.k) {  // K is a multiple of 8 (16 for f32, 32 for Q8_0): a group is wholly inside or past the row
             const float4 v0 = gload<float4>(a.x + 4ull * ((uint64_t)t * a.k + k8));
@@ -2182,7 +2193,7 @@ KERNEL __launch_bounds__(256) void qp_split_bf16(QpSplitArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; j++) v[j] = 0.0f;
         }
-        const uint64_t o = xs_off(t, k8, a.rows);
+        const uint64_t o = a.mul ? 2ull * ((uint64_t)t * (nq * 8) + k8) : xs_off(t, k8, a.rows);
         split_store8(v, reinterpret_cast<__bf16*>(a.xs + o), reinterpret_cast<__bf16*>(a.xs + plane + o));
     }
 }

@@ -138,8 +138,10 @@ typedef struct {
     uint64_t sel, lst, off, paso;
     uint32_t n_exp, n, nsel, pad;
 } QpMoeGroupArgs;
-// x [T][k] -> bf16 high / low planes (hi = bf16(v), lo = bf16(v - hi)) at xs and xs + 2*rows*k.
-typedef struct { uint64_t x, xs, paso; uint32_t k, rows; } QpSplitArgs;
+// x [T][k] -> bf16 high / low planes (hi = bf16(v), lo = bf16(v - hi)) at xs and xs + 2*rows*k.  mul != 0: the
+// first min(T * mul, cap) rows of x instead of T, in row-major planes ([rows][k rounded up to 32]: the grouped
+// expert matmul, whose tiles gather rows), not the chunk-quarter layout of the 256-token tiles.
+typedef struct { uint64_t x, xs, paso; uint32_t k, rows, mul, cap; } QpSplitArgs;
 // y[t][n] = (acc ? y : 0) + sum over s (in order) of ws[s][t][n].
 typedef struct { uint64_t ws, y, paso; uint32_t n, rows, splits, acc; } QpReduceArgs;
 

@@ -418,19 +418,21 @@ int workspace(uint64_t bytes, uint64_t* out) {
 // there (the same x, paso, K, planes and workspace allocation), else x is split.
 struct SplitMemo {
     uint64_t x, xs, paso;
-    uint32_t k, rows, gen;
+    uint32_t k, rows, mul, cap, gen;
     bool valid;
 } g_split_memo = {};
 // While a graph is captured nothing runs, so a split recorded then proves nothing about the planes' contents now,
 // and a replay may overwrite them (the noalloc scratch is shared): the memo is neither used nor set during capture,
 // and graph launches invalidate it.
-int split_input(uint64_t x, uint64_t xs, uint64_t paso, uint32_t K, uint32_t rows, uint32_t tmax, bool reuse) {
+// mul, cap: rows T * mul of x, at most cap (QpSplitArgs); 0: T rows.
+int split_input(uint64_t x, uint64_t xs, uint64_t paso, uint32_t K, uint32_t rows, uint32_t tmax, bool reuse,
+                uint32_t mul = 0, uint32_t cap = 0) {
     const SplitMemo& m = g_split_memo;
     if (reuse && !g_capturing && m.valid && m.x == x && m.xs == xs && m.paso == paso && m.k == K && m.rows == rows &&
-        m.gen == g_ws_gen)
+        m.mul == mul && m.cap == cap && m.gen == g_ws_gen)
         return 0;
-    QpSplitArgs sa = {x, xs, paso, K, rows};
-    g_split_memo = {x, xs, paso, K, rows, g_ws_gen, false};
+    QpSplitArgs sa = {x, xs, paso, K, rows, mul, cap};
+    g_split_memo = {x, xs, paso, K, rows, mul, cap, g_ws_gen, false};
     if (int e = launch(K_split_bf16, grid_cap((uint64_t)tmax * K / 8), 1, 1, 256, 0, sa)) return e;
     g_split_memo.valid = !g_capturing;
     return 0;
@@ -1044,6 +1046,22 @@ int op_matmul_eg(const Ctx& c, int fmt, const char* name) {
     a.nlst = cap(rl / 4);
     a.tpe = cdiv(32 * tz, 128);
     if ((uint64_t)E * a.tpe > 65535) return fail(QP_E_ARG, "%s: %u experts x %u job tiles", name, E, a.tpe);
+    // P[4] = m (not a reference word; absent: 0): x holds m rows per token (1: gate/up, whose job j reads token
+    // row j / tfijo; the top-k count: down, job rows), and its first T * m rows are split into bf16 planes once
+    // (row-major: a tile gathers rows), which every tile then copies instead of loading and splitting f32 rows (the
+    // same planes: the sums are bit-equal).  P[5] = 1: the previous matmul split the same x (see split_input).  Not while capturing a graph or
+    // under qp_dispatch_noalloc (the planes need the workspace): there x is split in the tiles as without P[4].
+    const uint32_t m = c.U(4);
+    if (m && !g_capturing && !g_noalloc) {
+        if (K % 8) return fail(QP_E_ARG, "%s: input planes need K %% 8 == 0", name);
+        const uint64_t r64 = (uint64_t)32 * tz * m;
+        a.rows = (uint32_t)(r64 < a.xrows ? r64 : a.xrows);
+        uint64_t ws = 0;
+        if (int e = workspace(4ull * a.rows * ((K + 31) / 32 * 32), &ws)) return e;
+        a.xs = ws;
+        if (int e = split_input(a.x, a.xs, a.paso, K, a.rows, a.rows, c.U(5) == 1, m, a.xrows)) return e;
+        a.xrows = a.rows;  // a job whose row the planes do not hold stores nothing (an m too small for tfijo)
+    }
     const Kid k = fmt == QP_Q4_K ? K_gemm_mfma_q4k : fmt == QP_Q6_K ? K_gemm_mfma_q6k
                 : fmt == QP_Q5_K ? K_gemm_mfma_q5k : fmt == QP_Q3_K ? K_gemm_mfma_q3k
                 : fmt == QP_Q2_K ? K_gemm_mfma_q2k : fmt == QP_Q8_0 ? K_gemm_mfma_q8

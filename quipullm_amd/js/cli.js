@@ -8,7 +8,7 @@
 //                        [--temperature T] [--top-k K] [--top-p P] [--min-p M] [--seed S]
 //   node cli.js bench    --model M.gguf --prompt-file ids.json --n 256 [--kv f16] [--ctx N] [--batch N]
 //                        [--warmup W] [--prefill P1,P2] [--eager] [--sample] [--keys-per-split N]
-//                        [--no-moe-grouped] [--no-fused-ffn] [--no-ffn-planes] [--no-norm-planes] [--no-merged-attention] [--attn-block] [--no-moe-router]
+//                        [--no-moe-grouped] [--no-moe-planes] [--no-fused-ffn] [--no-ffn-planes] [--no-norm-planes] [--no-merged-attention] [--attn-block] [--no-moe-router]
 //   node cli.js motor    --servidor http://127.0.0.1:PORT [--id ID] [--kv f16] [--batch N]   (the server's engine)
 //                        [--check-prompt-file ids.json --check-n N --check-logits file.f32]
 //
@@ -48,6 +48,7 @@ async function cargar(o) {
   if (o['no-fused-ffn'] || o.mode === 'ref') options.fused_ffn = false;
   if (o['no-ffn-planes']) options.ffn_planes = false;
   if (o['no-norm-planes']) options.norm_planes = false;
+  if (o['no-moe-planes']) options.moe_planes = false;
   if (o['no-merged-attention']) options.merged_attention = false;
   if (o['attn-block']) options.attn_block = true;
   if (o['no-moe-router']) options.moe_router = false;

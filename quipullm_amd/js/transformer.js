@@ -103,6 +103,10 @@ class ModeloTransformer {
     // K-quant matmuls that read it (rmsnorm_planes; Q, K, V with P[4] = 2, the fused gate/up with P[3] = 1) instead
     // of f32 rows that each matmul splits; false: rmsnorm
     this.planosNorma = op.norm_planes !== false;
+    // MoE prompt batches grouped by expert: each expert matmul's input split into bf16 planes once (matmul_<fmt>_eg
+    // P[4] = rows per token: 1 for gate and up, the top-k count for down; up reuses gate's planes, P[5] = 1) instead
+    // of in every tile that reads a row; the same sums bit for bit.  false: f32 rows split in the tiles
+    this.planosMoe = op.moe_planes !== false;
     // one-token step: the split-K attention's partials merged by the last workgroup of each grid column in the same
     // launch (dec_attn P[12] = 1) instead of a dec_attn_comb launch.  A column takes at most 4 query heads: groups of
     // 8 or more query heads are split over gsplit columns per KV head (P[13]; each column streams its KV head's keys
@@ -309,12 +313,13 @@ class ModeloTransformer {
     };
   }
 
-  _mmE(W, x, y, tfijo) {
+  _mmE(W, x, y, tfijo, filasTok, reusa) {
     const gpu = this.gpu;
     const u = gpu.uniforme([['u', W.N / this.nExp], ['u', W.K], ['u', 0], ['u', tfijo], ['u', this.nExp]]);
     const wb = plano(W) ? [W.qs, W.ds] : [W.w];
     // grouped by expert (the reference's matmul_<fmt>_eg: P{N, K, acc, tfijo}; [paso, w, x, y, lst, off])
-    const ug = gpu.uniforme([['u', W.N / this.nExp], ['u', W.K], ['u', 0], ['u', tfijo]]);
+    const ug = gpu.uniforme([['u', W.N / this.nExp], ['u', W.K], ['u', 0], ['u', tfijo]].concat(
+      this.planosMoe ? [['u', filasTok], ['u', reusa ? 1 : 0]] : []));
     const gg = EG.has(W.tipo) ? gpu.grupo('matmul_' + W.tipo + '_eg', [ug, this.bPaso].concat(wb, [x, y, this.lst, this.off])) : null;
     return { g: gpu.grupo('matmul_' + W.tipo + '_e', [u, this.bPaso].concat(wb, [x, y, this.sel])), gg: gg, filas: W.N / this.nExp };
   }
@@ -386,10 +391,10 @@ class ModeloTransformer {
         gc.router = this._mm(c.router, this.xn, this.rl, 0);
         gc.topk = gpu.grupo('moe_topk', [gpu.uniforme([['u', this.nExp], ['u', K], ['u', this.normExp ? 1 : 0],
           ['f', this.escExp]]), P, this.rl, this.sel, this.wts]);
-        gc.eg = this._mmE(c.eg, this.xn, this.g, K);
-        gc.eu = this._mmE(c.eu, this.xn, this.u, K);
+        gc.eg = this._mmE(c.eg, this.xn, this.g, K, 1, false);
+        gc.eu = this._mmE(c.eu, this.xn, this.u, K, 1, true);
         gc.eact = gpu.grupo('swiglu', [gpu.uniforme([['u', K * this.ffe]]), P, this.g, this.u]);
-        gc.ed = this._mmE(c.ed, this.g, this.de, 1);
+        gc.ed = this._mmE(c.ed, this.g, this.de, 1, K, false);
         gc.comb = gpu.grupo('moe_comb', [gpu.uniforme([['u', D], ['u', K]]), P, this.x, this.de, this.wts]);
         gc.grupar = gpu.grupo('moe_group', [gpu.uniforme([['u', this.nExp], ['u', K]]), P, this.sel, this.lst, this.off]);
         gc.agrupado = agrupable(!!(gc.eg.gg && gc.eu.gg && gc.ed.gg), this.batch, K, this.nExp);

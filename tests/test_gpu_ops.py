@@ -651,7 +651,8 @@ def test_moe_group(quipu, dev, E, k, T):
 def test_matmul_grouped_by_expert(quipu, dev, oracle, fmt, tfijo, acc):
     """matmul_<fmt>_eg (kquants.js:386-460): the expert matmul over the job lists of moe_group, on the matrix cores.
     Expert 2 has 150 jobs (two job tiles), several experts none; rows N = 200 (a partial row tile).  tfijo = 4:
-    job j reads input row j / 4 (gate/up); tfijo = 1 with acc: row j, added to y (down)."""
+    job j reads input row j / 4 (gate/up); tfijo = 1 with acc: row j, added to y (down).  The same bits with the
+    input split into planes first (P[4]), and with that split reused (P[5])."""
     E, N, K, k = 8, 200, 512, 4
     T = 160 if tfijo > 1 else 40
     rng = np.random.default_rng(9)
@@ -668,11 +669,17 @@ def test_matmul_grouped_by_expert(quipu, dev, oracle, fmt, tfijo, acc):
     quipu.dispatch("moe_group", [("u", E), ("u", k)], [dev.paso(T, 0), sb, lb, ob])
     hw = dev.matrix(fmt, raw, E * N, K)
     wb = [hw, capi.scale_plane(fmt, hw, E * N, K)] if fmt in PLANAR else [hw]
-    yb = dev.buf(y0)
+    yb, xb, pb = dev.buf(y0), dev.buf(x), dev.paso(T, 0)
     u = [("u", N), ("u", K), ("u", acc), ("u", tfijo)]
-    quipu.dispatch("matmul_%s_eg" % capi.FMT_NAME[fmt], u, [dev.paso(T, 0)] + wb + [dev.buf(x), yb, lb, ob],
-                   ((N + 63) // 64, E, (T + 31) // 32))
+    name, grid = "matmul_%s_eg" % capi.FMT_NAME[fmt], ((N + 63) // 64, E, (T + 31) // 32)
+    quipu.dispatch(name, u, [pb] + wb + [xb, yb, lb, ob], grid)
     got = dev.get(yb, (njob, N))
+    # x split into bf16 planes once (P[4] = its rows per token: 1 for token rows, k for job rows) gives the same
+    # bits; then P[5] = 1 reuses that split
+    for reuse in (0, 1):
+        y2 = dev.buf(y0)
+        quipu.dispatch(name, u + [("u", 1 if tfijo > 1 else k), ("u", reuse)], [pb] + wb + [xb, y2, lb, ob], grid)
+        assert np.array_equal(dev.get(y2, (njob, N)), got), reuse
     for j in range(njob):
         e = int(sel[j])
         if e >= E:
