@@ -3068,6 +3068,38 @@ KERNEL __launch_bounds__(256) void qp_moe_topk(QpTopkArgs a) {
 // Reference moe_comb (kds.js:224-240): x[t][i] += sum_s wts[t*k+s] * de[(t*k+s)*D + i].
 KERNEL __launch_bounds__(256) void qp_moe_comb(QpCombArgs a) {
     const uint64_t n = (uint64_t)paso_T(a.paso) * a.d;
+    if ((a.d & 3) == 0 && a.k <= 8) {
+        // four consecutive outputs per thread, the k expert rows' loads issued together; per output the same sum
+        // as below (acc = acc + w * de over s in order, then x + acc)
+        const uint32_t d4 = a.d >> 2;
+        const uint64_t n4 = n >> 2;
+        for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n4; i += (uint64_t)gridDim.x * 256ull) {
+            const uint32_t t = (uint32_t)(i / d4), c = (uint32_t)(i - (uint64_t)t * d4) * 4;
+            float4 r[8];
+            float w[8];
+#pragma unroll
+            for (uint32_t s = 0; s < 8; s++) {
+                if (s < a.k) {
+                    r[s] = gload<float4>(a.de + 4ull * (((uint64_t)t * a.k + s) * a.d + c));
+                    w[s] = cptr<float>(a.wts)[t * a.k + s];
+                }
+            }
+            float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t s = 0; s < 8; s++) {
+                if (s < a.k) {
+                    acc.x = acc.x + w[s] * r[s].x;
+                    acc.y = acc.y + w[s] * r[s].y;
+                    acc.z = acc.z + w[s] * r[s].z;
+                    acc.w = acc.w + w[s] * r[s].w;
+                }
+            }
+            float4* xo = reinterpret_cast<float4*>(mptr<float>(a.x)) + i;
+            const float4 xv = *xo;
+            *xo = float4{xv.x + acc.x, xv.y + acc.y, xv.z + acc.z, xv.w + acc.w};
+        }
+        return;
+    }
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256ull) {
         const uint32_t t = (uint32_t)(i / a.d), c = (uint32_t)(i % a.d);
         float acc = 0.0f;

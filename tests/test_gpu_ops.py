@@ -628,7 +628,7 @@ def group_jobs(sel, E):
     return np.array(lst, np.uint32), np.concatenate([[0], np.cumsum(cnt)]).astype(np.uint32)
 
 
-@pytest.mark.parametrize("E,k,T", [(16, 4, 70), (128, 8, 300), (7, 1, 1)])
+@pytest.mark.parametrize("E,k,T", [(16, 4, 70), (128, 8, 300), (7, 1, 1), (128, 8, 2048), (256, 8, 4000), (5, 3, 21800)])
 def test_moe_group(quipu, dev, E, k, T):
     """moe_group (kds.js:491-516): jobs listed per expert in increasing order, off the running counts; one expert
     takes more than half of the tokens, several none; an id >= E (not a valid expert) is not listed."""
@@ -993,15 +993,16 @@ def test_swiglu_moe_ops(quipu, dev, oracle):
         np.testing.assert_array_equal(dev.get(sel, (3 * k,), np.uint32), s_want)
         np.testing.assert_allclose(dev.get(wts, (3 * k,)), w_want, rtol=2e-6, atol=1e-7)
         assert list(s_want[k:k + 2]) == [9, 100]
-    D = 1000
-    x = rng.standard_normal((T, D)).astype(np.float32)
-    de = rng.standard_normal((T * k, D)).astype(np.float32)
-    wts = rng.random(T * k).astype(np.float32)
-    xb = dev.buf(x)
-    quipu.dispatch("moe_comb", [("u", D), ("u", k)], [dev.paso(T, 0), xb, dev.buf(de), dev.buf(wts)],
-                   ((T * D + 255) // 256,))
-    np.testing.assert_allclose(dev.get(xb, (T, D)), oracle.moe_comb(x, de, wts, D, k).reshape(T, D),
-                               rtol=1e-6, atol=1e-6)
+    # moe_comb: four outputs per thread when D % 4 == 0 and k <= 8, else one
+    for D, kc in ((1000, k), (1002, k), (1000, 10)):
+        x = rng.standard_normal((T, D)).astype(np.float32)
+        de = rng.standard_normal((T * kc, D)).astype(np.float32)
+        wts = rng.random(T * kc).astype(np.float32)
+        xb = dev.buf(x)
+        quipu.dispatch("moe_comb", [("u", D), ("u", kc)], [dev.paso(T, 0), xb, dev.buf(de), dev.buf(wts)],
+                       ((T * D + 255) // 256,))
+        np.testing.assert_allclose(dev.get(xb, (T, D)), oracle.moe_comb(x, de, wts, D, kc).reshape(T, D),
+                                   rtol=1e-6, atol=1e-6)
 
 
 def test_argmax_ties_nan_negative(quipu, dev, oracle):
