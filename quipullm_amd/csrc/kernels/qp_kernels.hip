@@ -2926,25 +2926,46 @@ KERNEL __launch_bounds__(256) void qp_rmsnorm_planes2(QpRmsPlanesArgs a) { rmsno
 QP_DEV void wave_norm_rope_f(float* v, const float* w, uint32_t hd, bool use_norm, float eps, float pos_esc,
                              const float* freq, uint32_t nrot, bool neox, int lane);
 
-// grid (ceil(nh / 4), T): wavefront i of a workgroup takes head 4*blockIdx.x + i of token blockIdx.y.  The
-// frequency table base^(-2j/nrot) (each value rounded once to float from double, as rope_elem computes it per
-// element) is built once per workgroup.
+// grid (ceil(nh / 4), ceil(T / 4)): wavefront i of a workgroup takes head 4*blockIdx.x + i of the four tokens
+// from 4*blockIdx.y.  The frequency table base^(-2j/nrot) (each value rounded once to float from double, as
+// rope_elem computes it per element) is read from a.freq (the host's table of the same values), or built once per
+// workgroup.
 KERNEL __launch_bounds__(256) void qp_norm_rope(QpRopeArgs a) {
     __shared__ float v[4][256];
     __shared__ float freq[128];
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = blockIdx.x * 4 + wave, t = blockIdx.y;
-    if (t >= paso_T(a.paso)) return;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = blockIdx.x * 4 + wave;
+    const uint32_t T = paso_T(a.paso), t0 = blockIdx.y * 4;
+    if (t0 >= T) return;
     if (threadIdx.x < a.nrot / 2)
-        freq[threadIdx.x] = (float)pow((double)a.base, (double)((-2.0f * (float)threadIdx.x) / (float)a.nrot));
+        freq[threadIdx.x] = a.freq ? cptr<float>(a.freq)[threadIdx.x]
+                                   : (float)pow((double)a.base, (double)((-2.0f * (float)threadIdx.x) / (float)a.nrot));
     __syncthreads();
     if (h >= a.nh) return;
-    float* row = mptr<float>(a.v) + ((uint64_t)t * a.nh + h) * a.hd;
-    for (uint32_t i = lane; i < a.hd; i += 64) v[wave][i] = row[i];
-    __builtin_amdgcn_wave_barrier();
-    const float pos = (float)(paso_pos(a.paso) + t);
-    wave_norm_rope_f(v[wave], a.w ? cptr<float>(a.w) : nullptr, a.hd, a.use_norm != 0, a.eps, pos * a.esc, freq,
-                     a.nrot, a.neox != 0, (int)lane);
-    for (uint32_t i = lane; i < a.hd; i += 64) row[i] = v[wave][i];
+    // the four rows' loads issued together (hd <= 256: at most 4 values per lane and row)
+    const uint32_t nt = min(T, t0 + 4) - t0;
+    float pre[4][4];
+#pragma unroll
+    for (uint32_t r = 0; r < 4; r++)
+#pragma unroll
+        for (uint32_t c = 0; c < 4; c++) {
+            const uint32_t i = lane + 64 * c;
+            pre[r][c] = r < nt && i < a.hd ? cptr<float>(a.v)[((uint64_t)(t0 + r) * a.nh + h) * a.hd + i] : 0.0f;
+        }
+#pragma unroll
+    for (uint32_t r = 0; r < 4; r++) {
+        if (r >= nt) break;
+        const uint32_t t = t0 + r;
+        float* row = mptr<float>(a.v) + ((uint64_t)t * a.nh + h) * a.hd;
+#pragma unroll
+        for (uint32_t c = 0; c < 4; c++)
+            if (lane + 64 * c < a.hd) v[wave][lane + 64 * c] = pre[r][c];
+        __builtin_amdgcn_wave_barrier();
+        const float pos = (float)(paso_pos(a.paso) + t);
+        wave_norm_rope_f(v[wave], a.w ? cptr<float>(a.w) : nullptr, a.hd, a.use_norm != 0, a.eps, pos * a.esc, freq,
+                         a.nrot, a.neox != 0, (int)lane);
+        for (uint32_t i = lane; i < a.hd; i += 64) row[i] = v[wave][i];
+        __builtin_amdgcn_wave_barrier();  // the row's reads of v are done before the next row is loaded into it
+    }
 }
 
 // ====================================================================================== KV write

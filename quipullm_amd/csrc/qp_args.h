@@ -156,6 +156,7 @@ typedef struct {
     float eps, base;
     uint32_t nrot;
     float esc;
+    uint64_t freq;  // RoPE frequencies base^(-2j/nrot) as floats [nrot/2], or 0: computed in every workgroup
 } QpRopeArgs;
 // rows: slots of the cache (writes at or past it are dropped, never out of bounds)
 typedef struct { uint64_t k, v, kc, vc, paso; uint32_t kvd, cap, f16, rows; } QpKvArgs;

@@ -736,7 +736,12 @@ int op_norm_rope(const Ctx& c) {
     a.paso = c.B(0);
     a.v = c.B(1);
     a.w = c.B(2);
-    return launch(K_norm_rope, cdiv(a.nh, 4), c.gy, 1, 256, 0, a);
+    // a fourth binding (not the reference's): the frequency table for this base and nrot, base^(-2j/nrot) rounded
+    // once to float for j < nrot/2, so that no workgroup evaluates the powers
+    a.freq = c.nb > 3 ? c.B(3) : 0;
+    if (a.freq)
+        if (int e = need_room(a.freq, 4ull * (a.nrot / 2), "norm_rope", "the frequency table")) return e;
+    return launch(K_norm_rope, cdiv(a.nh, 4), cdiv(c.gy, 4), 1, 256, 0, a);  // four tokens per workgroup
 }
 
 // kv_write (gpu.js:447-466): P{kvd, cap, f16, rows}; [paso, k, v, kc, vc].  rows = cache slots (required).

@@ -353,6 +353,7 @@ class ModeloTransformer {
     };
     G.capas = this.capas.map((c) => {
       const baseCapa = this.gemma && c.swa ? this.baseSwa : this.base;
+      const tablaCapa = baseCapa === this.base ? [this.ropeFreq] : [];
       const escRope = this.gemma && !c.swa ? this.escalaGlobal : 1;
       const ur = (nh, norm) => gpu.uniforme([['u', this.hd], ['u', nh], ['u', norm ? 1 : 0], ['u', this.neox],
         ['f', this.eps], ['f', baseCapa], ['u', this.nrot], ['f', escRope === 1 ? 0 : escRope]]);
@@ -361,8 +362,9 @@ class ModeloTransformer {
         ffnNorm: gpu.grupo('rmsnorm', [uNorm, P, this.x, c.ffnNorm, this.xn]),
         wq: this._mm(c.wq, this.xn, this.q, 0), wk: this._mm(c.wk, this.xn, this.k, 0, true),
         wv: this._mm(c.wv, this.xn, this.v, 0, true),
-        ropeQ: gpu.grupo('norm_rope', [ur(this.nh, !!c.qNorm), P, this.q, c.qNorm || dummy]),
-        ropeK: gpu.grupo('norm_rope', [ur(this.nkv, !!c.kNorm), P, this.k, c.kNorm || dummy]),
+        // (the layer's frequency table when it has the model's base: no power evaluated in the kernel)
+        ropeQ: gpu.grupo('norm_rope', [ur(this.nh, !!c.qNorm), P, this.q, c.qNorm || dummy].concat(tablaCapa)),
+        ropeK: gpu.grupo('norm_rope', [ur(this.nkv, !!c.kNorm), P, this.k, c.kNorm || dummy].concat(tablaCapa)),
         kvw: gpu.grupo('kv_write', [gpu.uniforme([['u', kvd], ['u', c.anillo], ['u', f16], ['u', c.slots]]), P, this.k, this.v,
           c.kc, c.vc]),
         att: gpu.grupo('atencion', [gpu.uniforme([['u', this.hd], ['u', this.nh], ['u', this.nkv], ['u', c.swa],

@@ -859,6 +859,12 @@ def test_norm_rope(quipu, dev, oracle, hd, neox, use_norm):
     got = dev.get(vb, (T * nh * hd,))
     want = oracle.norm_rope(v, w, nh, hd, use_norm, neox, 1e-6, 5e5, hd, pos0).reshape(-1)
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+    # with the host's frequency table as a fourth binding: the same bits
+    vb2 = dev.buf(v)
+    quipu.dispatch("norm_rope", [("u", hd), ("u", nh), ("u", use_norm), ("u", neox), ("f", 1e-6), ("f", 5e5),
+                                 ("u", hd), ("u", 0)], [dev.paso(T, pos0), vb2, dev.buf(w), dev.buf(rope_table(5e5, hd))],
+                   (nh, T))
+    assert np.array_equal(dev.get(vb2, (T * nh * hd,)), got)
 
 
 @pytest.mark.parametrize("f16", [0, 1])
