@@ -3016,6 +3016,48 @@ KERNEL __launch_bounds__(256) void qp_kv_write(QpKvArgs a) {
     }
 }
 
+// The f16 cache for prompt chunks (kvd % 4 == 0): a workgroup takes 64 tokens x 64 channels.  K and V rows are read
+// four channels per thread; K goes out as four f16 per thread ([slot][kvd], rows contiguous); V goes through LDS so
+// that each thread writes 16 consecutive slots of one channel, which sit in that channel's 64-byte tile rows
+// (vt_index).  The same values and slots as qp_kv_write.  Grid (ceil(kvd / 64), ceil(T / 64)).
+KERNEL __launch_bounds__(256) void qp_kv_write16(QpKvArgs a) {
+    __shared__ float vt[64][65];  // [channel][token]
+    const uint32_t T = paso_T(a.paso), pos0 = paso_pos(a.paso);
+    const uint32_t c0 = blockIdx.x * 64, t0 = blockIdx.y * 64, tid = threadIdx.x;
+    if (t0 >= T) return;
+    const uint32_t cq = tid & 15, r0 = tid >> 4;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+        const uint32_t lt = r0 + 16 * i, t = t0 + lt, c = c0 + 4 * cq;
+        if (t < T && c < a.kvd) {
+            const uint64_t src = 4ull * ((uint64_t)t * a.kvd + c);
+            const float4 kv = gload<float4>(a.k + src), vv = gload<float4>(a.v + src);
+            uint32_t slot = pos0 + t;
+            if (a.cap) slot %= a.cap;
+            if (slot < a.rows) {
+                const uint32_t lo = (uint32_t)f2h(kv.x) | ((uint32_t)f2h(kv.y) << 16);
+                const uint32_t hi = (uint32_t)f2h(kv.z) | ((uint32_t)f2h(kv.w) << 16);
+                *reinterpret_cast<uint2*>(mptr<uint16_t>(a.kc) + (uint64_t)slot * a.kvd + c) = uint2{lo, hi};
+            }
+            vt[4 * cq][lt] = vv.x;
+            vt[4 * cq + 1][lt] = vv.y;
+            vt[4 * cq + 2][lt] = vv.z;
+            vt[4 * cq + 3][lt] = vv.w;
+        }
+    }
+    __syncthreads();
+    const uint32_t lc = tid >> 2, lt0 = (tid & 3) * 16, c = c0 + lc;
+    if (c >= a.kvd) return;
+    for (uint32_t j = 0; j < 16; j++) {
+        const uint32_t t = t0 + lt0 + j;
+        if (t >= T) break;
+        uint32_t slot = pos0 + t;
+        if (a.cap) slot %= a.cap;
+        if (slot >= a.rows) continue;
+        mptr<uint16_t>(a.vc)[vt_index(slot, a.kvd, c)] = f2h(vt[lc][lt0 + j]);
+    }
+}
+
 // ====================================================================================== SwiGLU
 // Reference swiglu (gpu.js:570-582): g = g / (1 + exp(-g)) * u over T*F.
 // GeGLU, the tanh form (reference geglu, gpu.js:318-330): g = 0.5 a (1 + tanh(z)) u with

@@ -760,6 +760,11 @@ int op_kv_write(const Ctx& c) {
     a.v = c.B(2);
     a.kc = c.B(3);
     a.vc = c.B(4);
+    // f16 cache, prompt chunks (the dispatch covers 64 tokens or more): tiles of 64 tokens x 64 channels, the tokens
+    // the dispatch covers (x = ceil(T * kvd / 256))
+    const uint64_t tcap = c.gx ? ((uint64_t)c.gx * 256 + a.kvd - 1) / a.kvd : 0;
+    if (a.f16 && a.kvd % 4 == 0 && tcap >= 64)
+        return launch(K_kv_write16, cdiv(a.kvd, 64), (uint32_t)((tcap + 63) / 64), 1, 256, 0, a);
     return launch(K_kv_write, c.gx ? (c.gx > 4096 ? 4096 : c.gx) : 1, 1, 1, 256, 0, a);
 }
 

@@ -868,8 +868,10 @@ def test_norm_rope(quipu, dev, oracle, hd, neox, use_norm):
 
 
 @pytest.mark.parametrize("f16", [0, 1])
-def test_kv_write(quipu, dev, oracle, f16):
-    kvd, rows, T, pos0 = 256, 20, 4, 15
+@pytest.mark.parametrize("kvd,rows,T,pos0", [(256, 20, 4, 15), (1024, 200, 100, 37), (132, 300, 130, 101)])
+def test_kv_write(quipu, dev, oracle, f16, kvd, rows, T, pos0):
+    """kv_write at positions pos0..pos0+T-1; from 64 tokens on the f16 cache takes the 64 x 64 tiles (K four
+    channels per thread, V through LDS), here with partial token and channel tiles and slots past a 32-slot tile."""
     k = np.random.default_rng(16).standard_normal((T, kvd)).astype(np.float32)
     v = np.random.default_rng(17).standard_normal((T, kvd)).astype(np.float32)
     es = 2 if f16 else 4
@@ -881,18 +883,22 @@ def test_kv_write(quipu, dev, oracle, f16):
     gk, gv = dev.get(kc, (rows, kvd), dt), dev.get(vc, (vrows, kvd), dt)
     if f16:
         gv = refs.v_rows(gv, rows, kvd)
-    # rows 15..18 written (f16: round to nearest even), everything else untouched
+    # rows pos0..pos0+T-1 written (f16: round to nearest even), everything else untouched
     np.testing.assert_array_equal(gk[pos0:pos0 + T], k.astype(dt))
     np.testing.assert_array_equal(gv[pos0:pos0 + T], v.astype(dt))
     assert not gk[:pos0].any() and not gk[pos0 + T:].any()
+    assert not gv[:pos0].any() and not gv[pos0 + T:].any()
 
 
 @pytest.mark.parametrize("f16", [0, 1])
-def test_kv_write_ring(quipu, dev, f16):
+@pytest.mark.parametrize("big", [False, True])
+def test_kv_write_ring(quipu, dev, f16, big):
     """kv_write into a ring of cap slots (the reference's sliding-window cache, transformer.js:106-111 and
     gpu.js:461-462): position p goes to slot p % cap; 8 tokens from position 20 of a 24-slot ring wrap to slots
     20..23 and 0..3, and the other slots keep their contents."""
     kvd, cap, T, pos0 = 128, 24, 8, 20
+    if big:  # 90 tokens from position 150 of a 96-slot ring: the 64 x 64 tiles of the f16 cache, wrapping once
+        cap, T, pos0 = 96, 90, 150
     rng = np.random.default_rng(26)
     k = rng.standard_normal((T, kvd)).astype(np.float32)
     v = rng.standard_normal((T, kvd)).astype(np.float32)
